@@ -1,0 +1,113 @@
+/*
+ * r9vx_expf.h -- f32 exp that reproduces the host glibc expf bit for bit.
+ *
+ * R9V's T0 router (crates/r9v-t0/src/moe_route.rs:331-346) evaluates the
+ * softmax numerators with Rust f32::exp, which lowers to the platform libm
+ * expf: on x86-64 Linux that is glibc's expf, whose algorithm (glibc >= 2.27)
+ * is the published ARM optimized-routines method: reduce x*N/ln2 = k + r with
+ * N = 32 by the 0x1.8p52 shift trick, look up 2^(k/N) in a 32-entry table,
+ * evaluate a cubic in r in double precision and round once to float.  glibc
+ * selects its FMA build on CPUs with FMA, in which the compiler fuses every
+ * multiply that feeds an add; this restatement spells those fusions out with
+ * fma() so the same double operations happen on the GPU.
+ *
+ * The table is 2^(i/32) correctly rounded to double, minus (i << 47) (so that
+ * adding k << 47 yields 2^(k/32)); it is regenerated from that definition by
+ * the CPU test.  Agreement with the host expf is checked exhaustively over
+ * every float in the router's domain [-104, 0] by the CPU test suite.
+ */
+#ifndef R9VX_EXPF_H
+#define R9VX_EXPF_H
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define R9VX_HD __host__ __device__ inline
+#else
+#define R9VX_HD static inline
+#include <math.h>
+#include <string.h>
+#endif
+
+#define R9VX_EXP2F_N 32
+
+#if defined(__HIPCC__)
+__host__ __device__ inline
+#else
+static inline
+#endif
+uint64_t r9vx_exp2_tab(uint32_t i) {
+    /* A switch keeps the table in instruction immediates on the GPU (no
+     * constant-memory global needed) and is a plain lookup on the host. */
+    switch (i & 31u) {
+    case 0: return 0x3ff0000000000000ull;  case 1: return 0x3fefd9b0d3158574ull;
+    case 2: return 0x3fefb5586cf9890full;  case 3: return 0x3fef9301d0125b51ull;
+    case 4: return 0x3fef72b83c7d517bull;  case 5: return 0x3fef54873168b9aaull;
+    case 6: return 0x3fef387a6e756238ull;  case 7: return 0x3fef1e9df51fdee1ull;
+    case 8: return 0x3fef06fe0a31b715ull;  case 9: return 0x3feef1a7373aa9cbull;
+    case 10: return 0x3feedea64c123422ull; case 11: return 0x3feece086061892dull;
+    case 12: return 0x3feebfdad5362a27ull; case 13: return 0x3feeb42b569d4f82ull;
+    case 14: return 0x3feeab07dd485429ull; case 15: return 0x3feea47eb03a5585ull;
+    case 16: return 0x3feea09e667f3bcdull; case 17: return 0x3fee9f75e8ec5f74ull;
+    case 18: return 0x3feea11473eb0187ull; case 19: return 0x3feea589994cce13ull;
+    case 20: return 0x3feeace5422aa0dbull; case 21: return 0x3feeb737b0cdc5e5ull;
+    case 22: return 0x3feec49182a3f090ull; case 23: return 0x3feed503b23e255dull;
+    case 24: return 0x3feee89f995ad3adull; case 25: return 0x3feeff76f2fb5e47ull;
+    case 26: return 0x3fef199bdd85529cull; case 27: return 0x3fef3720dcef9069ull;
+    case 28: return 0x3fef5818dcfba487ull; case 29: return 0x3fef7c97337b9b5full;
+    case 30: return 0x3fefa4afa2a490daull; default: return 0x3fefd0765b6e4540ull;
+    }
+}
+
+#if defined(__HIPCC__)
+__host__ __device__ inline
+#else
+static inline
+#endif
+float r9vx_expf(float x) {
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * R9VX_EXP2F_N;
+    const double shift = 0x1.8p+52;
+    /* Cubic for 2^(r/N), coefficients pre-divided by N^3, N^2, N. */
+    const double c0 = 0x1.c6af84b912394p-5 / R9VX_EXP2F_N / R9VX_EXP2F_N / R9VX_EXP2F_N;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / R9VX_EXP2F_N / R9VX_EXP2F_N;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / R9VX_EXP2F_N;
+    uint32_t ux;
+#if defined(__HIPCC__)
+    ux = __builtin_bit_cast(uint32_t, x);
+#else
+    memcpy(&ux, &x, 4);
+#endif
+    uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) { /* |x| >= 88, inf or nan (top12(88.0f) = 0x42b) */
+        if (ux == 0xff800000u) return 0.0f;
+        if (abstop >= 0x7f8u) return x + x;
+        if (x > 0x1.62e42ep6f) return __builtin_huge_valf();
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    double xd = (double)x;
+    double kd = fma(inv_ln2_n, xd, shift);
+    uint64_t ki;
+#if defined(__HIPCC__)
+    ki = __builtin_bit_cast(uint64_t, kd);
+#else
+    memcpy(&ki, &kd, 8);
+#endif
+    kd -= shift;
+    double r = fma(inv_ln2_n, xd, -kd);
+    uint64_t t = r9vx_exp2_tab((uint32_t)(ki % R9VX_EXP2F_N));
+    t += ki << (52 - 5);
+    double s;
+#if defined(__HIPCC__)
+    s = __builtin_bit_cast(double, t);
+#else
+    memcpy(&s, &t, 8);
+#endif
+    double z = fma(c0, r, c1);
+    double r2 = r * r;
+    double y = fma(c2, r, 1.0);
+    y = fma(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+#endif

@@ -1,0 +1,41 @@
+"""Copies the reference's own golden decode vectors for this path into tests/golden.
+
+Data only (inputs and expected outputs); run once in the build container where
+/root/reference exists.  Sources:
+  crates/r9v-format/tests/fixtures/r9v-format/q4k_reference.txt  (all 6 Q4_K cases,
+      consumed by crates/r9v-format/tests/schemes.rs:482-516)
+  crates/r9v-format/tests/fixtures/r9v-format/iq_a24_reference.txt (the IQ4_XS and
+      IQ4_NL cases, consumed by crates/r9v-format/tests/iq.rs:159-197)
+The reference is Apache-2.0; the fixture data derives from llama.cpp / gguf-py (MIT).
+"""
+import pathlib
+import sys
+
+SRC = pathlib.Path("/root/reference/crates/r9v-format/tests/fixtures/r9v-format")
+DST = pathlib.Path(__file__).resolve().parent
+
+HEADER = ("# Copied verbatim (data lines) from R9V {src} -- reference golden vectors.\n"
+          "# License: Apache-2.0 (R9V); data derived from llama.cpp / gguf-py (MIT).\n")
+
+
+def main() -> int:
+    q4k = (SRC / "q4k_reference.txt").read_text()
+    (DST / "q4k_reference.txt").write_text(
+        HEADER.format(src="crates/r9v-format/tests/fixtures/r9v-format/q4k_reference.txt") + q4k)
+    keep, out = False, []
+    for line in (SRC / "iq_a24_reference.txt").read_text().splitlines():
+        if line.startswith("#"):
+            out.append(line)
+            continue
+        if line.startswith("case "):
+            keep = line.split()[1] in ("IQ4_XS", "IQ4_NL")
+        if keep:
+            out.append(line)
+    (DST / "iq4_reference.txt").write_text(
+        HEADER.format(src="crates/r9v-format/tests/fixtures/r9v-format/iq_a24_reference.txt")
+        + "\n".join(out) + "\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,146 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so) -- the checker.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load this.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import subprocess
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+LIB_PATH = ROOT / "oracle" / "liboracle.so"
+
+Q4_K, IQ4_XS = 12, 23
+F32, BF16 = 0, 2
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        P = ctypes.c_void_p
+        U = ctypes.c_uint32
+        I = ctypes.c_int
+        L.rxo_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.rxo_f16_to_f32.restype = ctypes.c_float
+        L.rxo_f32_to_bf16.argtypes = [ctypes.c_float]
+        L.rxo_f32_to_bf16.restype = ctypes.c_uint16
+        L.rxo_expf.argtypes = [ctypes.c_float]
+        L.rxo_expf.restype = ctypes.c_float
+        L.rxo_q4k_unpack_scales.argtypes = [P, P, P]
+        L.rxo_dequantize.argtypes = [I, P, U, U, P]
+        L.rxo_matmul.argtypes = [I, P, U, U, I, P, U, P, P, I, P]
+        L.rxo_matmul_mt.argtypes = [I, P, U, U, I, P, U, I, P, I]
+        L.rxo_moe_route.argtypes = [P, P, U, U, U, ctypes.c_float, I, I, P, P]
+        L.rxo_moe_sort.argtypes = [P, U, U, U, P, P, P]
+        L.rxo_moe_ffn.argtypes = [I, P, U, U, U, U, U, U, P, P, I, P, I, P, I, P]
+        L.rxo_moe_ffn_full.argtypes = [I, P, U, U, U, U, U, P, P, I, P, I, P, P]
+        L.rxo_expert_ffn.argtypes = [I, P, U, U, U, I, P, I, P, I, P]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+class OracleError(RuntimeError):
+    def __init__(self, code: int, what: str):
+        super().__init__(f"{what}: oracle refused with code {code}")
+        self.code = code
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise OracleError(rc, what)
+
+
+def dequantize(scheme, wire, n, k):
+    out = np.empty((n, k), dtype=np.float32)
+    _check(lib().rxo_dequantize(scheme, _p(np.ascontiguousarray(wire)), n, k, _p(out)), "dequantize")
+    return out
+
+
+def matmul(scheme, w, n, k, x, x_dtype, y_dtype=F32, bias=None, residual=None, threads=0):
+    x = np.ascontiguousarray(x)
+    m = x.shape[0]
+    y = np.empty((m, n), dtype=np.float32 if y_dtype == F32 else np.uint16)
+    w = np.ascontiguousarray(w)
+    if threads:
+        rc = lib().rxo_matmul_mt(scheme, _p(w), n, k, x_dtype, _p(x), m, y_dtype, _p(y), threads)
+    else:
+        rc = lib().rxo_matmul(scheme, _p(w), n, k, x_dtype, _p(x), m, _p(bias), _p(residual),
+                              y_dtype, _p(y))
+    _check(rc, "matmul")
+    return y
+
+
+def moe_route(logits, k, bias=None, scale=1.0, renormalize=True, scoring=0):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    t, e = logits.shape
+    ids = np.zeros((t, k), dtype=np.uint32)
+    w = np.zeros((t, k), dtype=np.float32)
+    _check(lib().rxo_moe_route(_p(logits), _p(bias), t, e, k, scale, int(renormalize), scoring,
+                               _p(ids), _p(w)), "moe_route")
+    return ids, w
+
+
+def moe_sort(ids, e):
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    t, k = ids.shape
+    counts = np.zeros(e, dtype=np.uint32)
+    offsets = np.zeros(e + 1, dtype=np.uint32)
+    sorted_ = np.zeros(t * k, dtype=np.uint32)
+    _check(lib().rxo_moe_sort(_p(ids), t, k, e, _p(counts), _p(offsets), _p(sorted_)), "moe_sort")
+    return counts, offsets, sorted_
+
+
+def moe_ffn(x, x_dtype, ids, weights, e, dff, w_gate_up, w_down, scheme_gu=IQ4_XS,
+            scheme_dn=Q4_K, shared=0, h_bf16=False):
+    x = np.ascontiguousarray(x)
+    t, dm = x.shape
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    k = ids.shape[1]
+    y = np.empty((t, dm), dtype=np.float32)
+    _check(lib().rxo_moe_ffn(x_dtype, _p(x), t, dm, dff, e, shared, k, _p(ids), _p(weights),
+                             scheme_gu, _p(np.ascontiguousarray(w_gate_up)), scheme_dn,
+                             _p(np.ascontiguousarray(w_down)), int(h_bf16), _p(y)), "moe_ffn")
+    return y
+
+
+def moe_ffn_full(x, x_dtype, ids, weights, e, dff, w_gate_up, w_down, scheme_gu=IQ4_XS,
+                 scheme_dn=Q4_K):
+    x = np.ascontiguousarray(x)
+    t, dm = x.shape
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    k = ids.shape[1]
+    y = np.empty((t, dm), dtype=np.float32)
+    _check(lib().rxo_moe_ffn_full(x_dtype, _p(x), t, dm, dff, e, k, _p(ids), _p(weights),
+                                  scheme_gu, _p(np.ascontiguousarray(w_gate_up)), scheme_dn,
+                                  _p(np.ascontiguousarray(w_down)), _p(y)), "moe_ffn_full")
+    return y
+
+
+def expert_ffn(x, x_dtype, dff, w_gate_up, w_down, scheme_gu=IQ4_XS, scheme_dn=Q4_K,
+               h_bf16=False):
+    x = np.ascontiguousarray(x)
+    rows, dm = x.shape
+    out = np.empty((rows, dm), dtype=np.float32)
+    _check(lib().rxo_expert_ffn(x_dtype, _p(x), rows, dm, dff, scheme_gu,
+                                _p(np.ascontiguousarray(w_gate_up)), scheme_dn,
+                                _p(np.ascontiguousarray(w_down)), int(h_bf16), _p(out)),
+           "expert_ffn")
+    return out
