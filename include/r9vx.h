@@ -1,0 +1,235 @@
+/*
+ * r9vx.h -- C ABI of the MI355X (gfx950) quantized-weight matrix path.
+ *
+ * Drop-in for R9V's device tier of three ops: `matmul` with GGUF Q4_K /
+ * IQ4_XS weights, `moe_route` and `moe_ffn`.  The argument structs are
+ * byte-for-byte the kgen ABI structs of those ops
+ * (crates/r9v-kgen/src/abi/per_op.rs:794-968): pointer fields first in
+ * declaration order, then the u32 dynamic scalar, tail-padded to 8
+ * (crates/r9v-kgen/src/abi/layout.rs:102-180).  A caller that already packs
+ * `LaunchEntry.args_blob` (crates/r9v-registry/src/launch.rs:27) can pass that
+ * blob's address as `args`.  The static structs carry the variant keys of
+ * crates/r9v-registry/src/types.rs:727-860 that this path reads.
+ *
+ * Conventions (crates/r9v-kgen/src/abi/types.rs:14-19; spec-04 sec. 7):
+ *  - the caller owns every buffer; workspaces are caller-allocated with the
+ *    size the *_workspace_bytes query returns; nothing here allocates device
+ *    memory during a launch;
+ *  - device pointers should be 256-byte aligned (16-byte alignment is
+ *    required and checked);
+ *  - launches are stream-ordered on `stream` (NULL = the default stream);
+ *  - status: 0 = launched; > 0 = a HIP error code from the runtime; < 0 = a
+ *    host-side refusal (R9VX_ERR_*) before anything was enqueued.  The text of
+ *    the last error on the calling thread is r9vx_last_error().
+ *  - data-dependent refusals that only the device can see (non-finite router
+ *    logits, expert ids >= E) follow T0's refuse-before-mutation rule: a
+ *    check pass sets a status word and the compute kernels then write
+ *    nothing.  The word is read back with r9vx_moe_route_status /
+ *    r9vx_moe_ffn_status.
+ */
+#ifndef R9VX_H
+#define R9VX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in HIP headers. */
+typedef struct ihipStream_t *r9vx_stream_t;
+
+/* Element dtypes: discriminants of r9v-ir DType (crates/r9v-ir/src/dtype.rs:15-35). */
+enum r9vx_dtype {
+    R9VX_DTYPE_F32 = 0,
+    R9VX_DTYPE_F16 = 1,
+    R9VX_DTYPE_BF16 = 2,
+    R9VX_DTYPE_U32 = 8
+};
+
+/* Weight schemes: GGUF ggml type codes (crates/r9v-format/src/ggml.rs:38;
+ * codes checked by crates/r9v-format/tests/iq.rs:131-141). */
+enum r9vx_scheme {
+    R9VX_SCHEME_Q4_K = 12,  /* 144-B super-block per 256 weights */
+    R9VX_SCHEME_IQ4_XS = 23 /* 136-B super-block per 256 weights */
+};
+
+/* Matmul epilogues (crates/r9v-t0/src/matmul.rs:2421-2446). */
+enum r9vx_epilogue { R9VX_EPILOGUE_NONE = 0, R9VX_EPILOGUE_BIAS = 1, R9VX_EPILOGUE_RESIDUAL = 2 };
+
+/* Router scoring (crates/r9v-t0/src/moe_route.rs:329-351). */
+enum r9vx_scoring { R9VX_SCORING_SOFTMAX = 0, R9VX_SCORING_SIGMOID = 1 };
+
+/* Expert activation (crates/r9v-t0/src/activation.rs:133-138). */
+enum r9vx_act { R9VX_ACT_SILU = 0 };
+
+/* Host-side refusals. */
+#define R9VX_OK 0
+#define R9VX_ERR_INVALID -1     /* shape / static / argument mismatch */
+#define R9VX_ERR_UNSUPPORTED -2 /* a variant key this path does not implement */
+#define R9VX_ERR_NULL -3        /* a required pointer is NULL */
+#define R9VX_ERR_ALIGN -4       /* a device pointer is not 16-byte aligned */
+#define R9VX_ERR_WORKSPACE -5   /* workspace missing or too small */
+
+/* Device status bits (read back by the *_status calls). */
+#define R9VX_STATUS_NONFINITE 1u   /* non-finite logits / bias / scores */
+#define R9VX_STATUS_DEGENERATE 2u  /* renormalise over a zero selected sum */
+#define R9VX_STATUS_BAD_EXPERT 4u  /* an expert id >= E */
+
+/* ------------------------------------------------------------------ matmul */
+
+/* Variant key subset of MatmulStatic (crates/r9v-registry/src/types.rs:727-770). */
+typedef struct r9vx_matmul_static {
+    uint32_t m_bucket;       /* M bucket; the launch's dynamic m <= m_bucket */
+    uint32_t n;              /* output columns N */
+    uint32_t k;              /* reduction length K, a multiple of 256 */
+    uint32_t w_scheme;       /* enum r9vx_scheme; weights are GGUF wire blocks [N, K/256] */
+    uint32_t in_dtype;       /* F32 (m <= 8 GEMV only) or BF16 */
+    uint32_t out_dtype;      /* F32 or BF16 (RNE) */
+    uint32_t epilogue;       /* enum r9vx_epilogue */
+    uint32_t residual_dtype; /* F32 when epilogue == RESIDUAL */
+} r9vx_matmul_static;
+
+/* matmul ABI struct (crates/r9v-kgen/src/abi/per_op.rs:794-868). */
+typedef struct r9vx_matmul_args {
+    const uint8_t *w;         /* GGUF blocks, row n at n * (K/256) * block_bytes */
+    const void *w_scales;     /* must be NULL: GGUF scales are inline */
+    const uint8_t *w_indices; /* must be NULL: no sparsity on this path */
+    const void *x;            /* [m, K] in_dtype */
+    const float *x_scale;     /* must be NULL: activations are not quantized */
+    const float *bias;        /* [N] f32 when epilogue == BIAS */
+    const void *residual;     /* [m, N] f32 when epilogue == RESIDUAL */
+    void *y;                  /* [m, N] out_dtype */
+    float *workspace;         /* split-K partials; may be NULL when 0 bytes are required */
+    uint32_t m;               /* dynamic row count */
+    uint32_t _tail_pad;
+} r9vx_matmul_args;
+
+/* Replaces: Registry::resolve + dispatch_launch for Op::Matmul
+ * (crates/r9v-registry/src/resolution.rs:232, launch.rs:97) whose T0 meaning
+ * is matmul_with_scales Branch D (crates/r9v-t0/src/matmul.rs:1940-2414). */
+int r9vx_matmul_launch(const r9vx_matmul_static *st, const r9vx_matmul_args *args,
+                       r9vx_stream_t stream);
+/* Workspace slot SplitKPartials size (crates/r9v-kgen/src/abi/workspace.rs:13-40). */
+size_t r9vx_matmul_workspace_bytes(const r9vx_matmul_static *st);
+/* LaunchEntry.static_bytes / static_flops (crates/r9v-registry/src/launch.rs:22-25):
+ * algorithmic HBM bytes (weights + x + y) and 2*m*N*K. */
+uint64_t r9vx_matmul_static_bytes(const r9vx_matmul_static *st, uint32_t m);
+uint64_t r9vx_matmul_static_flops(const r9vx_matmul_static *st, uint32_t m);
+
+/* --------------------------------------------------------------- moe_route */
+
+/* MoeRouteStatic (crates/r9v-registry/src/types.rs:774-800); grouped routing
+ * (n_group > 0) is not implemented and refused. */
+typedef struct r9vx_moe_route_static {
+    uint32_t t_bucket;
+    uint32_t e_total;     /* E <= 1024 */
+    uint32_t top_k;       /* K <= 32, K <= E */
+    uint32_t scoring;     /* enum r9vx_scoring */
+    uint32_t renormalize; /* 0 / 1 */
+    uint32_t scale_bits;  /* IEEE-754 bits of the f32 route scale */
+    uint32_t has_bias;    /* 0 / 1 */
+    uint32_t n_group;     /* must be 0 */
+} r9vx_moe_route_static;
+
+/* moe_route ABI struct (crates/r9v-kgen/src/abi/per_op.rs:870-901). */
+typedef struct r9vx_moe_route_args {
+    const float *logits;  /* [t, E] f32 */
+    const float *bias;    /* [E] f32 or NULL */
+    uint32_t *expert_ids; /* [t, K] u32 */
+    float *weights;       /* [t, K] f32 */
+    uint32_t t;
+    uint32_t _tail_pad;
+} r9vx_moe_route_args;
+
+/* Replaces: dispatch of Op::MoeRoute; T0 meaning moe_route
+ * (crates/r9v-t0/src/moe_route.rs:89-419).  Ids are bit-exact with T0. */
+int r9vx_moe_route_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_args *args,
+                          r9vx_stream_t stream);
+/* Synchronises `stream`, returns the device status bits of the last
+ * moe_route launch on this device in *status and clears them. */
+int r9vx_moe_route_status(uint32_t *status, r9vx_stream_t stream);
+uint64_t r9vx_moe_route_static_bytes(const r9vx_moe_route_static *st, uint32_t t);
+
+/* ----------------------------------------------------------------- moe_ffn */
+
+/* MoeFfnStatic (crates/r9v-registry/src/types.rs:828-860). */
+typedef struct r9vx_moe_ffn_static {
+    uint32_t t_bucket;
+    uint32_t e_local;        /* routed experts E */
+    uint32_t k_topk;         /* K */
+    uint32_t dm;             /* hidden size, multiple of 256 */
+    uint32_t dff;            /* expert intermediate size, multiple of 256 */
+    uint32_t gate_up_scheme; /* enum r9vx_scheme of w_gate_up [E+S, 2Dff, Dm] */
+    uint32_t down_scheme;    /* enum r9vx_scheme of w_down [E+S, Dm, Dff] */
+    uint32_t in_dtype;       /* BF16 */
+    uint32_t out_dtype;      /* F32 */
+    uint32_t act;            /* enum r9vx_act */
+    uint32_t shared_experts; /* S shared experts stored after the E routed ones */
+    uint32_t _reserved;
+} r9vx_moe_ffn_static;
+
+/* moe_ffn ABI struct (crates/r9v-kgen/src/abi/per_op.rs:903-968). */
+typedef struct r9vx_moe_ffn_args {
+    const void *x;                /* [t, Dm] in_dtype */
+    const uint32_t *expert_ids;   /* [t, K] */
+    const float *weights;         /* [t, K] */
+    const void *w_gate_up;        /* GGUF blocks, gate rows [0,Dff) then up rows [Dff,2Dff) */
+    const void *w_gate_up_scales; /* must be NULL (inline GGUF scales) */
+    const void *w_down;           /* GGUF blocks */
+    const void *w_down_scales;    /* must be NULL */
+    void *y;                      /* [t, Dm] out_dtype */
+    uint8_t *sort_workspace;      /* MoeSortBuffers, r9vx_moe_ffn_workspace_bytes */
+    uint32_t t;
+    uint32_t _tail_pad;
+} r9vx_moe_ffn_args;
+
+/* Replaces: dispatch of Op::MoeFfn; T0 meaning moe_ffn
+ * (crates/r9v-t0/src/moe_ffn.rs:75-660) plus, when shared_experts > 0, the
+ * shared-expert matmul/act_mul/residual_add graph of
+ * crates/r9v-models/src/generic.rs:1458-1495, fused. */
+int r9vx_moe_ffn_launch(const r9vx_moe_ffn_static *st, const r9vx_moe_ffn_args *args,
+                        r9vx_stream_t stream);
+size_t r9vx_moe_ffn_workspace_bytes(const r9vx_moe_ffn_static *st);
+/* Synchronises `stream` and returns the status bits the last launch with
+ * this workspace left in it (R9VX_STATUS_BAD_EXPERT). */
+int r9vx_moe_ffn_status(const r9vx_moe_ffn_static *st, const uint8_t *sort_workspace,
+                        uint32_t *status, r9vx_stream_t stream);
+uint64_t r9vx_moe_ffn_static_flops(const r9vx_moe_ffn_static *st, uint32_t t);
+
+/* Permute pre-pass of moe_ffn on its own: counts [E], offsets [E+1] and
+ * sorted [t*K] (= token*K + slot in stable (expert, token, slot) order), the
+ * counting-sort restatement of crates/r9v-t0/src/moe_ffn.rs:477-493 and the
+ * MoeSortBuffers contents (crates/r9v-kgen/src/abi/workspace.rs:13-40).  Uses
+ * the moe_ffn workspace for its scratch. */
+int r9vx_moe_sort_launch(const r9vx_moe_ffn_static *st, const uint32_t *expert_ids, uint32_t t,
+                         uint8_t *sort_workspace, uint32_t *counts, uint32_t *offsets,
+                         uint32_t *sorted, r9vx_stream_t stream);
+
+/* ------------------------------------------------------------ weights / decode */
+
+/* Bit-exact decode of GGUF wire blocks to f32 [n_rows, k]: the
+ * ggml_dequantize of crates/r9v-format/src/ggml.rs:1025-1150 (Q4_K) and
+ * crates/r9v-format/src/iq.rs:578-598 (IQ4_XS). */
+int r9vx_dequantize_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k,
+                           float *out, r9vx_stream_t stream);
+/* Load-time scale validation (check_wire_f16, crates/r9v-format/src/ggml.rs:421):
+ * counts blocks with a non-finite d (or dmin) into *bad_blocks (device u32,
+ * caller-zeroed). */
+int r9vx_validate_weights_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows,
+                                 uint32_t k, uint32_t *bad_blocks, r9vx_stream_t stream);
+
+/* ------------------------------------------------------------------ misc */
+
+/* Text of the last refusal / HIP error on the calling thread. */
+const char *r9vx_last_error(void);
+/* ABI version of this header (bumped on any struct change). */
+uint32_t r9vx_abi_version(void);
+
+#define R9VX_ABI_VERSION 1u
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,176 @@
+/*
+ * gemv.hip -- decode-time dequant-fused GEMV, y[m, n] = sum_k x[m, k] * w[n, k],
+ * for GGUF Q4_K / IQ4_XS weights and m <= 8 activation rows.
+ *
+ * T0 meaning: crates/r9v-t0/src/matmul.rs:1940-2414 (Branch D, f32
+ * accumulate); weight decode crates/r9v-format/src/ggml.rs:1131-1150 (Q4_K)
+ * and crates/r9v-format/src/iq.rs:578-598 (IQ4_XS).
+ *
+ * Bandwidth-bound design for CDNA4 wave64 (no MFMA):
+ *  - A lane owns a fixed set of 16-byte payload chunks (32 weights each) at the
+ *    same K positions in every row, so its activation slice is loaded and
+ *    re-arranged into registers once and reused for all R rows it visits.
+ *  - A row's chunks are spread over LPR consecutive lanes, so one 128-bit load
+ *    instruction of a wave reads whole contiguous row segments (coalesced).
+ *    All of a lane's weight loads for its R rows are issued before any math.
+ *  - bf16 activations use v_dot2_f32_bf16 (two MACs per lane-op, f32
+ *    accumulate).  Q4_K nibbles become bf16 with one AND-OR: 0x4300|q is the
+ *    bf16 of 128+q, and the 128*sum(x) offset is folded into the min term.
+ *    IQ4_XS nibble pairs index a 256-entry LDS table of bf16 codebook pairs.
+ *  - f32 activations (config 0) use exact nibble->f32 conversion and f32 FMA.
+ *  - Per-row partials are summed across the LPR lanes with a butterfly.
+ */
+#include "r9vx_gemv_core.h"
+
+namespace {
+
+struct GemvArgs {
+    const uint8_t *w;
+    const void *x;
+    const float *bias;
+    const float *residual;
+    void *y;
+    uint64_t w_row_stride;
+    uint64_t x_row_stride;
+    uint32_t n;
+    uint32_t k;
+    uint32_t lpr_log2; /* lanes per row = 1 << lpr_log2 */
+    uint32_t nseg;     /* K segments of LPR*SPL chunks */
+    uint32_t y_bf16;
+    uint32_t epilogue;
+};
+
+constexpr int kRows = 4; /* rows per lane group per wave */
+
+using namespace r9vx;
+
+template <int SCHEME, int M, bool XF32, int SPL>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+    __shared__ uint32_t lut[256];
+    if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
+        init_iq4_lut(lut, threadIdx.x, blockDim.x);
+        __syncthreads();
+    }
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t lpr = 1u << a.lpr_log2;
+    const uint32_t rpi = 64u >> a.lpr_log2; /* row slots per wave */
+    const uint32_t lir = lane & (lpr - 1);
+    const uint32_t slot = lane >> a.lpr_log2;
+    const uint32_t row0 = wave * rpi * kRows + slot;
+
+    float acc[kRows][M];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r)
+#pragma unroll
+        for (int t = 0; t < M; ++t) acc[r][t] = 0.f;
+
+    for (uint32_t seg = 0; seg < a.nseg; ++seg) {
+        XChunk<SCHEME, XF32> xc[SPL][M];
+        uint32_t cis[SPL];
+#pragma unroll
+        for (int s = 0; s < SPL; ++s) {
+            cis[s] = seg * lpr * SPL + s * lpr + lir;
+            uint32_t klo, khi;
+            chunk_k<SCHEME>(cis[s], klo, khi);
+#pragma unroll
+            for (int t = 0; t < M; ++t) {
+                const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.x) +
+                                    (uint64_t)t * a.x_row_stride * (XF32 ? 4 : 2);
+                load_x<SCHEME, XF32>(xb, klo, khi, xc[s][t]);
+            }
+        }
+        r9vx_u32x4 qs[kRows][SPL];
+        Hdr hd[kRows][SPL];
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            uint32_t row = row0 + r * rpi;
+            uint32_t rr = row < a.n ? row : a.n - 1; /* clamp: loads stay in bounds */
+            const uint8_t *wrow = a.w + (uint64_t)rr * a.w_row_stride;
+#pragma unroll
+            for (int s = 0; s < SPL; ++s) load_chunk<SCHEME>(wrow, cis[s], qs[r][s], hd[r][s]);
+        }
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int s = 0; s < SPL; ++s)
+                chunk_dot<SCHEME, XF32, M>(qs[r][s], hd[r][s], cis[s] & 7, xc[s], acc[r], lut);
+    }
+
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+#pragma unroll
+        for (int t = 0; t < M; ++t) acc[r][t] = r9vx_group_sum(acc[r][t], (int)lpr);
+        uint32_t row = row0 + r * rpi;
+        if (lir == 0 && row < a.n) {
+#pragma unroll
+            for (int t = 0; t < M; ++t) {
+                float v = acc[r][t];
+                if (a.epilogue == R9VX_EPILOGUE_BIAS) v += a.bias[row];
+                if (a.epilogue == R9VX_EPILOGUE_RESIDUAL) v += a.residual[(uint64_t)t * a.n + row];
+                uint64_t o = (uint64_t)t * a.n + row;
+                if (a.y_bf16)
+                    reinterpret_cast<uint16_t *>(a.y)[o] = r9vx_f32_to_bf16(v);
+                else
+                    reinterpret_cast<float *>(a.y)[o] = v;
+            }
+        }
+    }
+}
+
+template <int SCHEME, bool XF32, int SPL>
+int launch_m(const GemvArgs &a, uint32_t m, dim3 grid, hipStream_t s) {
+    switch (m) {
+#define R9VX_CASE(MM)                                                                          \
+    case MM:                                                                                   \
+        hipLaunchKernelGGL((gemv_kernel<SCHEME, MM, XF32, SPL>), grid, dim3(256), 0, s, a); \
+        break;
+        R9VX_CASE(1) R9VX_CASE(2) R9VX_CASE(3) R9VX_CASE(4)
+        R9VX_CASE(5) R9VX_CASE(6) R9VX_CASE(7) R9VX_CASE(8)
+#undef R9VX_CASE
+    default:
+        return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
+
+template <int SCHEME>
+int launch_scheme(const GemvArgs &a, uint32_t m, bool xf32, int spl, dim3 grid, hipStream_t s) {
+    if (xf32) return spl == 2 ? launch_m<SCHEME, true, 2>(a, m, grid, s) : launch_m<SCHEME, true, 1>(a, m, grid, s);
+    return spl == 2 ? launch_m<SCHEME, false, 2>(a, m, grid, s) : launch_m<SCHEME, false, 1>(a, m, grid, s);
+}
+
+}  // namespace
+
+/* m <= 8 rows, K % 256 == 0.  Rows of x are x_row_stride elements apart. */
+int r9vx_launch_gemv(const r9vx_gemv_problem &p, hipStream_t stream) {
+    const uint32_t cpr = p.k / 32; /* 16-byte chunks per row, a multiple of 8 */
+    /* Two chunks per lane when a row has >= 128 chunks and the activation
+     * registers fit (M rows x 2 chunks). */
+    int spl = (cpr % 128 == 0 && p.m <= (p.x_dtype == R9VX_DTYPE_F32 ? 2u : 4u)) ? 2 : 1;
+    uint32_t lpr = 64;
+    while (lpr > 8 && (cpr / spl) % lpr) lpr >>= 1;
+    if ((cpr / spl) < lpr) lpr = cpr / spl;
+    uint32_t lpr_log2 = 0;
+    while ((1u << lpr_log2) < lpr) ++lpr_log2;
+    GemvArgs a;
+    a.w = p.w;
+    a.x = p.x;
+    a.bias = p.bias;
+    a.residual = p.residual;
+    a.y = p.y;
+    a.w_row_stride = p.w_row_stride;
+    a.x_row_stride = p.x_row_stride;
+    a.n = p.n;
+    a.k = p.k;
+    a.lpr_log2 = lpr_log2;
+    a.nseg = cpr / (lpr * spl);
+    a.y_bf16 = p.y_dtype == R9VX_DTYPE_BF16;
+    a.epilogue = p.epilogue;
+    const uint32_t rows_per_wave = (64 / lpr) * kRows;
+    const uint32_t waves = (p.n + rows_per_wave - 1) / rows_per_wave;
+    dim3 grid((waves + 3) / 4);
+    const bool xf32 = p.x_dtype == R9VX_DTYPE_F32;
+    if (p.scheme == R9VX_SCHEME_Q4_K) return launch_scheme<R9VX_SCHEME_Q4_K>(a, p.m, xf32, spl, grid, stream);
+    return launch_scheme<R9VX_SCHEME_IQ4_XS>(a, p.m, xf32, spl, grid, stream);
+}

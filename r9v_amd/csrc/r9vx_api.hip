@@ -1,0 +1,387 @@
+/*
+ * r9vx_api.hip -- the C ABI of include/r9vx.h: host-side validation that
+ * mirrors T0's collect-all refusal (every problem is reported, nothing is
+ * enqueued when any is found), variant selection by shape, and launch.
+ *
+ * Validation mirrors crates/r9v-t0/src/matmul.rs:60-411 (rank/dtype/scheme/
+ * epilogue checks), moe_route.rs:96-311 and moe_ffn.rs:95-465, restricted to
+ * what a host can see without reading device memory.
+ */
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "r9vx_internal.h"
+#include "r9vx_moe.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Problems {
+    std::string text;
+    int code = R9VX_OK;
+    void add(int c, const char *fmt, ...) {
+        char buf[256];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        if (!text.empty()) text += "; ";
+        text += buf;
+        if (code == R9VX_OK) code = c;
+    }
+    int finish(const char *op) {
+        if (code != R9VX_OK) g_last_error = std::string(op) + ": " + text;
+        return code;
+    }
+};
+
+int hip_status(const char *op, int rc) {
+    if (rc != 0) {
+        g_last_error = std::string(op) + ": HIP error " + std::to_string(rc) + " (" +
+                       hipGetErrorString((hipError_t)rc) + ")";
+    }
+    return rc;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool known_scheme(uint32_t s) { return s == R9VX_SCHEME_Q4_K || s == R9VX_SCHEME_IQ4_XS; }
+
+uint32_t block_bytes(uint32_t s) {
+    return s == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : (s == R9VX_SCHEME_IQ4_XS ? R9VX_IQ4XS_BYTES : 0);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *r9vx_last_error(void) { return g_last_error.c_str(); }
+
+uint32_t r9vx_abi_version(void) { return R9VX_ABI_VERSION; }
+
+/* ------------------------------------------------------------------ matmul */
+
+static void check_matmul_static(const r9vx_matmul_static *st, Problems &pr) {
+    if (!known_scheme(st->w_scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u is not Q4_K (12) or IQ4_XS (23)", st->w_scheme);
+    if (st->k == 0 || st->k % 256)
+        pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of the 256-weight super-block", st->k);
+    if (st->n == 0) pr.add(R9VX_ERR_INVALID, "n must be positive");
+    if (st->in_dtype != R9VX_DTYPE_F32 && st->in_dtype != R9VX_DTYPE_BF16)
+        pr.add(R9VX_ERR_UNSUPPORTED, "in_dtype %u: only f32 and bf16 activations", st->in_dtype);
+    if (st->out_dtype != R9VX_DTYPE_F32 && st->out_dtype != R9VX_DTYPE_BF16)
+        pr.add(R9VX_ERR_UNSUPPORTED, "out_dtype %u: only f32 and bf16 outputs", st->out_dtype);
+    if (st->epilogue > R9VX_EPILOGUE_RESIDUAL)
+        pr.add(R9VX_ERR_UNSUPPORTED, "epilogue %u: only none/bias/residual", st->epilogue);
+    if (st->epilogue == R9VX_EPILOGUE_RESIDUAL && st->residual_dtype != R9VX_DTYPE_F32)
+        pr.add(R9VX_ERR_UNSUPPORTED, "residual_dtype %u: only f32 residuals", st->residual_dtype);
+}
+
+/* The MFMA path (bf16 activations, m > 8) stages x as fp16 rows plus per-row
+ * scales in the workspace; the GEMV path needs none. */
+size_t r9vx_matmul_workspace_bytes(const r9vx_matmul_static *st) {
+    if (!st || st->in_dtype != R9VX_DTYPE_BF16 || st->m_bucket <= 8) return 0;
+    return r9vx_gemm_workspace_bytes(st->m_bucket, st->k);
+}
+
+uint64_t r9vx_matmul_static_bytes(const r9vx_matmul_static *st, uint32_t m) {
+    if (!st || !known_scheme(st->w_scheme)) return 0;
+    uint64_t w = (uint64_t)st->n * (st->k / 256) * block_bytes(st->w_scheme);
+    uint64_t xe = st->in_dtype == R9VX_DTYPE_F32 ? 4 : 2;
+    uint64_t ye = st->out_dtype == R9VX_DTYPE_F32 ? 4 : 2;
+    return w + (uint64_t)m * st->k * xe + (uint64_t)m * st->n * ye;
+}
+
+uint64_t r9vx_matmul_static_flops(const r9vx_matmul_static *st, uint32_t m) {
+    if (!st) return 0;
+    return 2ull * m * st->n * st->k;
+}
+
+int r9vx_matmul_launch(const r9vx_matmul_static *st, const r9vx_matmul_args *a,
+                       r9vx_stream_t stream) {
+    Problems pr;
+    if (!st || !a) {
+        pr.add(R9VX_ERR_NULL, "static and args must be non-NULL");
+        return pr.finish("matmul");
+    }
+    check_matmul_static(st, pr);
+    if (a->m > st->m_bucket)
+        pr.add(R9VX_ERR_INVALID, "m=%u exceeds m_bucket=%u", a->m, st->m_bucket);
+    if (a->m > 0) {
+        if (!a->w) pr.add(R9VX_ERR_NULL, "w is NULL");
+        if (!a->x) pr.add(R9VX_ERR_NULL, "x is NULL");
+        if (!a->y) pr.add(R9VX_ERR_NULL, "y is NULL");
+    }
+    if (a->w_scales) pr.add(R9VX_ERR_UNSUPPORTED, "w_scales must be NULL: GGUF blocks carry inline scales");
+    if (a->w_indices) pr.add(R9VX_ERR_UNSUPPORTED, "w_indices must be NULL: no sparse weights");
+    if (a->x_scale) pr.add(R9VX_ERR_UNSUPPORTED, "x_scale must be NULL: activations are not quantized");
+    if (st->epilogue == R9VX_EPILOGUE_BIAS && !a->bias) pr.add(R9VX_ERR_NULL, "bias epilogue without bias");
+    if (st->epilogue != R9VX_EPILOGUE_BIAS && a->bias) pr.add(R9VX_ERR_INVALID, "bias given without bias epilogue");
+    if (st->epilogue == R9VX_EPILOGUE_RESIDUAL && !a->residual)
+        pr.add(R9VX_ERR_NULL, "residual epilogue without residual");
+    if (st->epilogue != R9VX_EPILOGUE_RESIDUAL && a->residual)
+        pr.add(R9VX_ERR_INVALID, "residual given without residual epilogue");
+    if ((a->w && !aligned16(a->w)) || (a->x && !aligned16(a->x)) || (a->y && !aligned16(a->y)))
+        pr.add(R9VX_ERR_ALIGN, "w, x and y must be 16-byte aligned");
+    if (st->in_dtype == R9VX_DTYPE_BF16 && a->m > 8) {
+        if (!a->workspace)
+            pr.add(R9VX_ERR_WORKSPACE, "m=%u > 8 runs the MFMA path: workspace of r9vx_matmul_workspace_bytes required", a->m);
+        else if ((uintptr_t)a->workspace & 255u)
+            pr.add(R9VX_ERR_ALIGN, "workspace must be 256-byte aligned");
+    }
+    int rc = pr.finish("matmul");
+    if (rc || a->m == 0) return rc;
+
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const uint64_t w_row = (uint64_t)(st->k / 256) * block_bytes(st->w_scheme);
+    const bool mfma = st->in_dtype == R9VX_DTYPE_BF16 && a->m > 8;
+    if (mfma) {
+        r9vx_gemm_problem g{};
+        g.w = a->w;
+        g.x = reinterpret_cast<const uint16_t *>(a->x);
+        g.bias = a->bias;
+        g.residual = reinterpret_cast<const float *>(a->residual);
+        g.y = a->y;
+        g.workspace = a->workspace;
+        g.n = st->n;
+        g.k = st->k;
+        g.m = a->m;
+        g.scheme = st->w_scheme;
+        g.y_dtype = st->out_dtype;
+        g.epilogue = st->epilogue;
+        return hip_status("matmul", r9vx_launch_gemm(g, s));
+    }
+    /* GEMV, eight activation rows per launch. */
+    const uint32_t xe = st->in_dtype == R9VX_DTYPE_F32 ? 4 : 2;
+    const uint32_t ye = st->out_dtype == R9VX_DTYPE_F32 ? 4 : 2;
+    for (uint32_t m0 = 0; m0 < a->m; m0 += 8) {
+        r9vx_gemv_problem p{};
+        p.w = a->w;
+        p.x = reinterpret_cast<const uint8_t *>(a->x) + (uint64_t)m0 * st->k * xe;
+        p.bias = a->bias;
+        p.residual = a->residual ? reinterpret_cast<const float *>(a->residual) + (uint64_t)m0 * st->n : nullptr;
+        p.y = reinterpret_cast<uint8_t *>(a->y) + (uint64_t)m0 * st->n * ye;
+        p.n = st->n;
+        p.k = st->k;
+        p.m = a->m - m0 < 8 ? a->m - m0 : 8;
+        p.scheme = st->w_scheme;
+        p.x_dtype = st->in_dtype;
+        p.y_dtype = st->out_dtype;
+        p.epilogue = st->epilogue;
+        p.w_row_stride = w_row;
+        p.x_row_stride = st->k;
+        int e = r9vx_launch_gemv(p, s);
+        if (e) return hip_status("matmul", e);
+    }
+    return R9VX_OK;
+}
+
+/* ----------------------------------------------------------- weights/decode */
+
+int r9vx_dequantize_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k,
+                           float *out, r9vx_stream_t stream) {
+    Problems pr;
+    if (!known_scheme(scheme)) pr.add(R9VX_ERR_UNSUPPORTED, "scheme %u", scheme);
+    if (k == 0 || k % 256) pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of 256", k);
+    if (n_rows && (!wire || !out)) pr.add(R9VX_ERR_NULL, "wire and out must be non-NULL");
+    if ((wire && !aligned16(wire)) || (out && !aligned16(out))) pr.add(R9VX_ERR_ALIGN, "16-byte alignment");
+    int rc = pr.finish("dequantize");
+    if (rc || n_rows == 0) return rc;
+    return hip_status("dequantize", r9vx_launch_dequant(scheme, wire, n_rows, k, out,
+                                                        reinterpret_cast<hipStream_t>(stream)));
+}
+
+int r9vx_validate_weights_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k,
+                                 uint32_t *bad_blocks, r9vx_stream_t stream) {
+    Problems pr;
+    if (!known_scheme(scheme)) pr.add(R9VX_ERR_UNSUPPORTED, "scheme %u", scheme);
+    if (k == 0 || k % 256) pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of 256", k);
+    if (n_rows && (!wire || !bad_blocks)) pr.add(R9VX_ERR_NULL, "wire and bad_blocks must be non-NULL");
+    int rc = pr.finish("validate_weights");
+    if (rc || n_rows == 0) return rc;
+    return hip_status("validate_weights", r9vx_launch_validate(scheme, wire, n_rows, k, bad_blocks,
+                                                               reinterpret_cast<hipStream_t>(stream)));
+}
+
+/* --------------------------------------------------------------- moe_route */
+
+uint64_t r9vx_moe_route_static_bytes(const r9vx_moe_route_static *st, uint32_t t) {
+    if (!st) return 0;
+    return (uint64_t)t * st->e_total * 4 + (st->has_bias ? 4ull * st->e_total : 0) + (uint64_t)t * st->top_k * 8;
+}
+
+int r9vx_moe_route_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_args *a,
+                          r9vx_stream_t stream) {
+    Problems pr;
+    if (!st || !a) {
+        pr.add(R9VX_ERR_NULL, "static and args must be non-NULL");
+        return pr.finish("moe_route");
+    }
+    float scale;
+    memcpy(&scale, &st->scale_bits, 4);
+    if (st->top_k == 0) pr.add(R9VX_ERR_INVALID, "top_k must be > 0");
+    if (!(scale > 0.0f) || !(scale < __builtin_huge_valf()))
+        pr.add(R9VX_ERR_INVALID, "scale must be finite and > 0, got %g", (double)scale);
+    if (st->n_group != 0) pr.add(R9VX_ERR_UNSUPPORTED, "grouped expert routing is not implemented");
+    if (a->t == 0 || st->e_total == 0) pr.add(R9VX_ERR_INVALID, "T=%u and E=%u must be > 0", a->t, st->e_total);
+    if (st->top_k > st->e_total) pr.add(R9VX_ERR_INVALID, "top_k %u cannot exceed number of experts E=%u", st->top_k, st->e_total);
+    if (st->e_total > 1024) pr.add(R9VX_ERR_UNSUPPORTED, "E=%u exceeds 1024", st->e_total);
+    if (st->top_k > 32) pr.add(R9VX_ERR_UNSUPPORTED, "top_k=%u exceeds 32", st->top_k);
+    if (st->scoring > R9VX_SCORING_SIGMOID) pr.add(R9VX_ERR_UNSUPPORTED, "scoring %u", st->scoring);
+    if (a->t > st->t_bucket) pr.add(R9VX_ERR_INVALID, "t=%u exceeds t_bucket=%u", a->t, st->t_bucket);
+    if (!a->logits || !a->expert_ids || !a->weights) pr.add(R9VX_ERR_NULL, "logits, expert_ids and weights are required");
+    if (st->has_bias && !a->bias) pr.add(R9VX_ERR_NULL, "has_bias set but bias is NULL");
+    if (!st->has_bias && a->bias) pr.add(R9VX_ERR_INVALID, "bias given but has_bias is 0");
+    int rc = pr.finish("moe_route");
+    if (rc) return rc;
+    r9vx_route_problem p{a->logits, a->bias, a->expert_ids, a->weights, a->t, st->e_total, st->top_k,
+                         st->scoring, st->renormalize ? 1u : 0u, scale};
+    return hip_status("moe_route", r9vx_launch_route(p, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int r9vx_moe_route_status(uint32_t *status, r9vx_stream_t stream) {
+    if (!status) {
+        g_last_error = "moe_route_status: status is NULL";
+        return R9VX_ERR_NULL;
+    }
+    return hip_status("moe_route_status", r9vx_read_route_status(status, reinterpret_cast<hipStream_t>(stream)));
+}
+
+/* ----------------------------------------------------------------- moe_ffn */
+
+static void check_ffn_static(const r9vx_moe_ffn_static *st, Problems &pr) {
+    if (st->e_local == 0 || st->e_local > kMoeMaxE) pr.add(R9VX_ERR_INVALID, "E=%u must be in 1..1024", st->e_local);
+    if (st->k_topk == 0 || st->k_topk > kMoeMaxK) pr.add(R9VX_ERR_INVALID, "K=%u must be in 1..32", st->k_topk);
+    if (st->dm == 0 || st->dm % 256) pr.add(R9VX_ERR_INVALID, "Dm=%u must be a positive multiple of 256", st->dm);
+    if (st->dff == 0 || st->dff % 256) pr.add(R9VX_ERR_INVALID, "Dff=%u must be a positive multiple of 256", st->dff);
+    if (!known_scheme(st->gate_up_scheme)) pr.add(R9VX_ERR_UNSUPPORTED, "gate_up_scheme %u", st->gate_up_scheme);
+    if (!known_scheme(st->down_scheme)) pr.add(R9VX_ERR_UNSUPPORTED, "down_scheme %u", st->down_scheme);
+    if (st->in_dtype != R9VX_DTYPE_BF16) pr.add(R9VX_ERR_UNSUPPORTED, "in_dtype %u: bf16 activations only", st->in_dtype);
+    if (st->out_dtype != R9VX_DTYPE_F32) pr.add(R9VX_ERR_UNSUPPORTED, "out_dtype %u: f32 output only", st->out_dtype);
+    if (st->act != R9VX_ACT_SILU) pr.add(R9VX_ERR_UNSUPPORTED, "act %u: SiLU only", st->act);
+    if (st->shared_experts > 8) pr.add(R9VX_ERR_UNSUPPORTED, "shared_experts=%u exceeds 8", st->shared_experts);
+    if (st->t_bucket == 0) pr.add(R9VX_ERR_INVALID, "t_bucket must be > 0");
+}
+
+size_t r9vx_moe_ffn_workspace_bytes(const r9vx_moe_ffn_static *st) {
+    if (!st) return 0;
+    return (size_t)r9vx_moe_layout(st->t_bucket, st->e_local, st->k_topk, st->dm, st->dff, st->shared_experts).total;
+}
+
+uint64_t r9vx_moe_ffn_static_flops(const r9vx_moe_ffn_static *st, uint32_t t) {
+    if (!st) return 0;
+    uint64_t per_row = 2ull * (2ull * st->dff * st->dm) + 2ull * st->dm * st->dff;
+    return per_row * ((uint64_t)t * st->k_topk + (uint64_t)t * st->shared_experts);
+}
+
+static int ffn_common(const char *op, const r9vx_moe_ffn_static *st, const uint32_t *ids, uint32_t t,
+                      const uint8_t *ws, Problems &pr) {
+    check_ffn_static(st, pr);
+    if (t == 0) pr.add(R9VX_ERR_INVALID, "t must be > 0");
+    if (t > st->t_bucket) pr.add(R9VX_ERR_INVALID, "t=%u exceeds t_bucket=%u", t, st->t_bucket);
+    if (!ids) pr.add(R9VX_ERR_NULL, "expert_ids is NULL");
+    if (!ws) pr.add(R9VX_ERR_WORKSPACE, "sort_workspace is NULL (size r9vx_moe_ffn_workspace_bytes)");
+    if (ws && ((uintptr_t)ws & 255u)) pr.add(R9VX_ERR_ALIGN, "sort_workspace must be 256-byte aligned");
+    return pr.finish(op);
+}
+
+static r9vx_moe_problem ffn_problem(const r9vx_moe_ffn_static *st, const r9vx_moe_ffn_args *a) {
+    r9vx_moe_problem p{};
+    p.x = reinterpret_cast<const uint16_t *>(a->x);
+    p.ids = a->expert_ids;
+    p.weights = a->weights;
+    p.w_gu = reinterpret_cast<const uint8_t *>(a->w_gate_up);
+    p.w_dn = reinterpret_cast<const uint8_t *>(a->w_down);
+    p.y = reinterpret_cast<float *>(a->y);
+    p.ws = a->sort_workspace;
+    p.t = a->t;
+    p.e = st->e_local;
+    p.k = st->k_topk;
+    p.dm = st->dm;
+    p.dff = st->dff;
+    p.shared = st->shared_experts;
+    p.t_bucket = st->t_bucket;
+    p.scheme_gu = st->gate_up_scheme;
+    p.scheme_dn = st->down_scheme;
+    return p;
+}
+
+int r9vx_moe_ffn_launch(const r9vx_moe_ffn_static *st, const r9vx_moe_ffn_args *a,
+                        r9vx_stream_t stream) {
+    Problems pr;
+    if (!st || !a) {
+        pr.add(R9VX_ERR_NULL, "static and args must be non-NULL");
+        return pr.finish("moe_ffn");
+    }
+    if (!a->x || !a->weights || !a->w_gate_up || !a->w_down || !a->y)
+        pr.add(R9VX_ERR_NULL, "x, weights, w_gate_up, w_down and y are required");
+    if (a->w_gate_up_scales || a->w_down_scales)
+        pr.add(R9VX_ERR_UNSUPPORTED, "separate scale carriers must be NULL: GGUF blocks carry inline scales");
+    if ((a->x && !aligned16(a->x)) || (a->y && !aligned16(a->y)) || (a->w_gate_up && !aligned16(a->w_gate_up)) ||
+        (a->w_down && !aligned16(a->w_down)))
+        pr.add(R9VX_ERR_ALIGN, "x, y and weights must be 16-byte aligned");
+    int rc = ffn_common("moe_ffn", st, a->expert_ids, a->t, a->sort_workspace, pr);
+    if (rc) return rc;
+    r9vx_moe_problem p = ffn_problem(st, a);
+    return hip_status("moe_ffn", r9vx_launch_moe(p, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int r9vx_moe_ffn_status(const r9vx_moe_ffn_static *st, const uint8_t *ws, uint32_t *status,
+                        r9vx_stream_t stream) {
+    if (!st || !ws || !status) {
+        g_last_error = "moe_ffn_status: static, workspace and status are required";
+        return R9VX_ERR_NULL;
+    }
+    MoeLayout L = r9vx_moe_layout(st->t_bucket, st->e_local, st->k_topk, st->dm, st->dff, st->shared_experts);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    int rc = (int)hipMemcpyAsync(status, ws + L.status, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
+    if (!rc) rc = (int)hipStreamSynchronize(s);
+    return hip_status("moe_ffn_status", rc);
+}
+
+int r9vx_moe_sort_launch(const r9vx_moe_ffn_static *st, const uint32_t *ids, uint32_t t, uint8_t *ws,
+                         uint32_t *counts, uint32_t *offsets, uint32_t *sorted, r9vx_stream_t stream) {
+    Problems pr;
+    if (!st) {
+        pr.add(R9VX_ERR_NULL, "static is NULL");
+        return pr.finish("moe_sort");
+    }
+    if (!counts || !offsets || !sorted) pr.add(R9VX_ERR_NULL, "counts, offsets and sorted are required");
+    int rc = ffn_common("moe_sort", st, ids, t, ws, pr);
+    if (rc) return rc;
+    r9vx_moe_ffn_args a{};
+    a.expert_ids = ids;
+    a.sort_workspace = ws;
+    a.t = t;
+    r9vx_moe_problem p = ffn_problem(st, &a);
+    return hip_status("moe_sort", r9vx_launch_moe_sort(p, counts, offsets, sorted, reinterpret_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"
+
+/* ------------------------------------------------------------------ dispatch */
+
+int r9vx_launch_moe(const r9vx_moe_problem &p, hipStream_t s) {
+    MoeLayout L = r9vx_moe_layout(p.t_bucket, p.e, p.k, p.dm, p.dff, p.shared);
+    int rc = r9vx_moe_sort_stage(p, L, s);
+    if (rc) return rc;
+    rc = r9vx_moe_decode_stage(p, L, s);
+    if (rc) return rc;
+    return r9vx_moe_combine_stage(p, L, s);
+}
+
+int r9vx_launch_moe_sort(const r9vx_moe_problem &p, uint32_t *counts, uint32_t *offsets, uint32_t *sorted,
+                         hipStream_t s) {
+    MoeLayout L = r9vx_moe_layout(p.t_bucket, p.e, p.k, p.dm, p.dff, p.shared);
+    int rc = r9vx_moe_sort_stage(p, L, s);
+    if (rc) return rc;
+    uint64_t pp = (uint64_t)p.t * p.k;
+    rc = (int)hipMemcpyAsync(counts, p.ws + L.counts, 4ull * p.e, hipMemcpyDeviceToDevice, s);
+    if (!rc) rc = (int)hipMemcpyAsync(offsets, p.ws + L.offsets, 4ull * (p.e + 1), hipMemcpyDeviceToDevice, s);
+    if (!rc) rc = (int)hipMemcpyAsync(sorted, p.ws + L.sorted, 4 * pp, hipMemcpyDeviceToDevice, s);
+    return rc;
+}

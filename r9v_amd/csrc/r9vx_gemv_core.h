@@ -1,0 +1,221 @@
+/*
+ * r9vx_gemv_core.h -- the per-lane pieces of the dequant-fused GEMV shared by
+ * the dense GEMV (gemv.hip) and the MoE decode kernels (moe.hip).
+ *
+ * A lane owns 16-byte payload chunks (32 weights); chunk ci of a row covers
+ * K positions klo..klo+15 (low nibbles of its 16 bytes) and khi..khi+15
+ * (high nibbles).  Q4_K: byte (j/2)*32+p holds sub-blocks 2g/2g+1
+ * (crates/r9v-format/src/ggml.rs:744-790); IQ4_XS: byte 8+16g+(j%16) holds
+ * positions j and j+16 of sub-block g (crates/r9v-format/src/iq.rs:274-293).
+ */
+#ifndef R9VX_GEMV_CORE_H
+#define R9VX_GEMV_CORE_H
+
+#include "r9vx_device.h"
+#include "r9vx_internal.h"
+
+namespace r9vx {
+
+/* Activation registers of one chunk for one token. */
+template <int SCHEME, bool XF32>
+struct XChunk;
+
+template <int SCHEME>
+struct XChunk<SCHEME, false> {
+    uint32_t p[16]; /* bf16 pairs arranged to match the weight decode */
+    float slo, shi; /* sum of the 16 low-/high-nibble activations (Q4_K) */
+};
+
+template <int SCHEME>
+struct XChunk<SCHEME, true> {
+    float lo[16], hi[16];
+    float slo, shi;
+};
+
+/* K offset of byte 0 low nibble / high nibble of chunk ci. */
+template <int SCHEME>
+__device__ __forceinline__ void chunk_k(uint32_t ci, uint32_t &klo, uint32_t &khi) {
+    uint32_t b = ci >> 3, c = ci & 7;
+    if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
+        klo = 256 * b + 64 * (c >> 1) + 16 * (c & 1);
+        khi = klo + 32;
+    } else {
+        klo = 256 * b + 32 * c;
+        khi = klo + 16;
+    }
+}
+
+template <int SCHEME, bool XF32>
+__device__ __forceinline__ void load_x(const void *xbase, uint32_t klo, uint32_t khi,
+                                       XChunk<SCHEME, XF32> &xc) {
+    if constexpr (XF32) {
+        const float *x = reinterpret_cast<const float *>(xbase);
+        const r9vx_f32x4 *l4 = reinterpret_cast<const r9vx_f32x4 *>(x + klo);
+        const r9vx_f32x4 *h4 = reinterpret_cast<const r9vx_f32x4 *>(x + khi);
+        float slo = 0.f, shi = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r9vx_f32x4 a = l4[i], b = h4[i];
+            xc.lo[4 * i] = a.x; xc.lo[4 * i + 1] = a.y; xc.lo[4 * i + 2] = a.z; xc.lo[4 * i + 3] = a.w;
+            xc.hi[4 * i] = b.x; xc.hi[4 * i + 1] = b.y; xc.hi[4 * i + 2] = b.z; xc.hi[4 * i + 3] = b.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            slo += xc.lo[i];
+            shi += xc.hi[i];
+        }
+        xc.slo = slo;
+        xc.shi = shi;
+    } else {
+        const uint16_t *x = reinterpret_cast<const uint16_t *>(xbase);
+        const r9vx_u32x4 *l4 = reinterpret_cast<const r9vx_u32x4 *>(x + klo);
+        const r9vx_u32x4 *h4 = reinterpret_cast<const r9vx_u32x4 *>(x + khi);
+        uint32_t L[8], H[8];
+        r9vx_u32x4 a0 = l4[0], a1 = l4[1], b0 = h4[0], b1 = h4[1];
+        L[0] = a0.x; L[1] = a0.y; L[2] = a0.z; L[3] = a0.w;
+        L[4] = a1.x; L[5] = a1.y; L[6] = a1.z; L[7] = a1.w;
+        H[0] = b0.x; H[1] = b0.y; H[2] = b0.z; H[3] = b0.w;
+        H[4] = b1.x; H[5] = b1.y; H[6] = b1.z; H[7] = b1.w;
+        float slo = 0.f, shi = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            slo += __builtin_bit_cast(float, L[j] << 16) + __builtin_bit_cast(float, L[j] & 0xFFFF0000u);
+            shi += __builtin_bit_cast(float, H[j] << 16) + __builtin_bit_cast(float, H[j] & 0xFFFF0000u);
+        }
+        xc.slo = slo;
+        xc.shi = shi;
+        if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
+            /* pair i = {x_lo(i), x_hi(i)}: byte i's two nibbles */
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                xc.p[2 * j] = (L[j] & 0xFFFFu) | (H[j] << 16);
+                xc.p[2 * j + 1] = (L[j] >> 16) | (H[j] & 0xFFFF0000u);
+            }
+        } else {
+            /* dword d of the payload holds positions 4d..4d+3:
+             * p[4d+0] = {lo(4d), lo(4d+2)}, p[4d+1] = {lo(4d+1), lo(4d+3)},
+             * p[4d+2] = {hi(4d), hi(4d+2)}, p[4d+3] = {hi(4d+1), hi(4d+3)} */
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                xc.p[4 * d + 0] = (L[2 * d] & 0xFFFFu) | (L[2 * d + 1] << 16);
+                xc.p[4 * d + 1] = (L[2 * d] >> 16) | (L[2 * d + 1] & 0xFFFF0000u);
+                xc.p[4 * d + 2] = (H[2 * d] & 0xFFFFu) | (H[2 * d + 1] << 16);
+                xc.p[4 * d + 3] = (H[2 * d] >> 16) | (H[2 * d + 1] & 0xFFFF0000u);
+            }
+        }
+    }
+}
+
+/* Block header of the chunk's super-block. */
+struct Hdr {
+    r9vx_u32x4 v;
+};
+
+template <int SCHEME>
+__device__ __forceinline__ void load_chunk(const uint8_t *row, uint32_t ci, r9vx_u32x4 &qs, Hdr &h) {
+    uint32_t b = ci >> 3, c = ci & 7;
+    if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
+        const uint8_t *blk = row + (uint64_t)b * R9VX_Q4K_BYTES;
+        h.v = r9vx_ld128(blk);
+        qs = r9vx_ld128_nt(blk + 16 + 16 * c);
+    } else {
+        const uint8_t *blk = row + (uint64_t)b * R9VX_IQ4XS_BYTES;
+        r9vx_u32x2 hh = *reinterpret_cast<const r9vx_u32x2 *>(blk);
+        h.v = r9vx_u32x4{hh.x, hh.y, 0u, 0u};
+        qs = r9vx_ld128_nt(blk + 8 + 16 * c);
+    }
+}
+
+/* One chunk of one row against M activation rows: acc[t] += chunk dot. */
+/* `m` (<= M, wave-uniform) limits the activation rows that are live. */
+template <int SCHEME, bool XF32, int M>
+__device__ __forceinline__ void chunk_dot(const r9vx_u32x4 &qs, const Hdr &h, uint32_t c,
+                                          const XChunk<SCHEME, XF32> (&xc)[M], float (&acc)[M],
+                                          const uint32_t *lut, int m = M) {
+    uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
+    if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
+        float d = r9vx_f16_to_f32((uint16_t)(h.v.x & 0xFFFF));
+        float dmin = r9vx_f16_to_f32((uint16_t)(h.v.x >> 16));
+        uint32_t sc[2], mn[2];
+        r9vx_q4k_scale_pair(h.v, c >> 1, sc, mn);
+        float dl0 = d * (float)sc[0], dl1 = d * (float)sc[1];
+        float ml0 = dmin * (float)mn[0], ml1 = dmin * (float)mn[1];
+        if constexpr (XF32) {
+#pragma unroll
+            for (int t = 0; t < M; ++t) {
+                if (t >= m) break;
+                float dlo = 0.f, dhi = 0.f;
+#pragma unroll
+                for (int dw = 0; dw < 4; ++dw) {
+                    uint32_t lo4 = q[dw] & 0x0F0F0F0Fu, hi4 = (q[dw] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        dlo = fmaf((float)((lo4 >> (8 * i)) & 0xFF), xc[t].lo[4 * dw + i], dlo);
+                        dhi = fmaf((float)((hi4 >> (8 * i)) & 0xFF), xc[t].hi[4 * dw + i], dhi);
+                    }
+                }
+                acc[t] += dl0 * dlo + dl1 * dhi - (ml0 * xc[t].slo + ml1 * xc[t].shi);
+            }
+        } else {
+            uint32_t v[16];
+#pragma unroll
+            for (int dw = 0; dw < 4; ++dw) {
+                v[4 * dw + 0] = (q[dw] & 0x000F000Fu) | 0x43004300u;
+                v[4 * dw + 1] = ((q[dw] >> 8) & 0x000F000Fu) | 0x43004300u;
+                v[4 * dw + 2] = ((q[dw] >> 4) & 0x000F000Fu) | 0x43004300u;
+                v[4 * dw + 3] = ((q[dw] >> 12) & 0x000F000Fu) | 0x43004300u;
+            }
+            /* sum (128+q)x = sum qx + 128 sum x; fold the offset into the min. */
+            float off0 = fmaf(128.f, dl0, ml0), off1 = fmaf(128.f, dl1, ml1);
+#pragma unroll
+            for (int t = 0; t < M; ++t) {
+                if (t >= m) break;
+                float dlo = 0.f, dhi = 0.f;
+#pragma unroll
+                for (int dw = 0; dw < 4; ++dw) {
+                    dlo = r9vx_dot2_bf16(v[4 * dw + 0], xc[t].p[4 * dw + 0], dlo);
+                    dlo = r9vx_dot2_bf16(v[4 * dw + 1], xc[t].p[4 * dw + 1], dlo);
+                    dhi = r9vx_dot2_bf16(v[4 * dw + 2], xc[t].p[4 * dw + 2], dhi);
+                    dhi = r9vx_dot2_bf16(v[4 * dw + 3], xc[t].p[4 * dw + 3], dhi);
+                }
+                acc[t] += dl0 * dlo + dl1 * dhi - (off0 * xc[t].slo + off1 * xc[t].shi);
+            }
+        }
+    } else {
+        float d = r9vx_f16_to_f32((uint16_t)(h.v.x & 0xFFFF));
+        float dl = d * r9vx_iq4xs_scale(r9vx_u32x2{h.v.x, h.v.y}, c);
+        uint32_t lv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) lv[i] = lut[(q[i >> 2] >> (8 * (i & 3))) & 0xFF];
+#pragma unroll
+        for (int t = 0; t < M; ++t) {
+            if (t >= m) break;
+            float s = 0.f;
+            if constexpr (XF32) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    s = fmaf(__builtin_bit_cast(float, lv[i] << 16), xc[t].lo[i], s);
+                    s = fmaf(__builtin_bit_cast(float, lv[i] & 0xFFFF0000u), xc[t].hi[i], s);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) s = r9vx_dot2_bf16(lv[i], xc[t].p[i], s);
+            }
+            acc[t] = fmaf(dl, s, acc[t]);
+        }
+    }
+}
+
+
+/* IQ4_XS bf16 codebook-pair table: entry b = {kv[b & 15], kv[b >> 4]}. */
+__device__ __forceinline__ void init_iq4_lut(uint32_t *lut, uint32_t tid, uint32_t nthreads) {
+    for (uint32_t i = tid; i < 256; i += nthreads) {
+        uint32_t lo = __builtin_bit_cast(uint32_t, (float)r9vx_iq4_kvalue(i & 15)) >> 16;
+        uint32_t hi = __builtin_bit_cast(uint32_t, (float)r9vx_iq4_kvalue(i >> 4)) >> 16;
+        lut[i] = lo | (hi << 16);
+    }
+}
+
+}  // namespace r9vx
+
+#endif

@@ -1,0 +1,110 @@
+/*
+ * r9vx_internal.h -- block-header decoding shared by the kernels, and the
+ * internal launchers the C-ABI layer (r9vx_api.cpp) dispatches to.
+ */
+#ifndef R9VX_INTERNAL_H
+#define R9VX_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "r9vx.h"
+
+#ifdef __HIPCC__
+#include "r9vx_device.h"
+/* Q4_K 6-bit scale/min of sub-blocks 2g and 2g+1 from the 16-byte block
+ * header read as four dwords (bytes 4..15 are the packed payload):
+ * crates/r9v-format/src/ggml.rs:973-995 (unpack_k4_scales). */
+__device__ __forceinline__ uint32_t r9vx_q4k_payload_byte(r9vx_u32x4 h, uint32_t i) {
+    uint32_t w = i < 4 ? h.y : (i < 8 ? h.z : h.w);
+    return (w >> ((i & 3) * 8)) & 0xFFu;
+}
+
+__device__ __forceinline__ void r9vx_q4k_scale_pair(r9vx_u32x4 h, uint32_t g, uint32_t sc[2],
+                                                    uint32_t mn[2]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        uint32_t j = 2 * g + t;
+        if (j < 4) {
+            sc[t] = r9vx_q4k_payload_byte(h, j) & 63u;
+            mn[t] = r9vx_q4k_payload_byte(h, j + 4) & 63u;
+        } else {
+            uint32_t bj4 = r9vx_q4k_payload_byte(h, j + 4);
+            sc[t] = (bj4 & 0xFu) | ((r9vx_q4k_payload_byte(h, j - 4) >> 2) & 0x30u);
+            mn[t] = (bj4 >> 4) | ((r9vx_q4k_payload_byte(h, j) >> 2) & 0x30u);
+        }
+    }
+}
+
+/* IQ4_XS sub-block scale s - 32 as f32 from the 8-byte header
+ * (crates/r9v-format/src/iq.rs:587-590): low nibble from scales_l, high two
+ * bits from scales_h. */
+__device__ __forceinline__ float r9vx_iq4xs_scale(r9vx_u32x2 h, uint32_t c) {
+    uint32_t lo = (h.y >> (4 * c)) & 0xFu;
+    uint32_t hi = (h.x >> (16 + 2 * c)) & 0x3u;
+    return (float)(int)(lo | (hi << 4)) - 32.0f;
+}
+#endif
+
+/* Internal launchers (return hipError_t as int). */
+int r9vx_launch_dequant(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k,
+                        float *out, hipStream_t stream);
+int r9vx_launch_validate(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k,
+                         uint32_t *bad, hipStream_t stream);
+
+struct r9vx_gemv_problem {
+    const uint8_t *w;
+    const void *x;
+    const float *bias;
+    const float *residual;
+    void *y;
+    uint32_t n, k, m;
+    uint32_t scheme, x_dtype, y_dtype, epilogue;
+    uint64_t w_row_stride; /* bytes between weight rows */
+    uint64_t x_row_stride; /* elements between activation rows */
+};
+int r9vx_launch_gemv(const r9vx_gemv_problem &p, hipStream_t stream);
+
+struct r9vx_gemm_problem {
+    const uint8_t *w;
+    const uint16_t *x; /* bf16 [m, k] */
+    const float *bias;
+    const float *residual;
+    void *y;
+    void *workspace; /* r9vx_gemm_workspace_bytes(m, k): fp16 x rows + row scales */
+    uint32_t n, k, m;
+    uint32_t scheme, y_dtype, epilogue;
+};
+size_t r9vx_gemm_workspace_bytes(uint32_t m_bucket, uint32_t k);
+int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream);
+
+struct r9vx_route_problem {
+    const float *logits;
+    const float *bias;
+    uint32_t *ids;
+    float *weights;
+    uint32_t t, e, k, scoring, renormalize;
+    float scale;
+};
+int r9vx_launch_route(const r9vx_route_problem &p, hipStream_t stream);
+int r9vx_read_route_status(uint32_t *status, hipStream_t stream);
+
+struct r9vx_moe_problem {
+    const uint16_t *x; /* bf16 [t, dm] */
+    const uint32_t *ids;
+    const float *weights;
+    const uint8_t *w_gu;
+    const uint8_t *w_dn;
+    float *y;
+    uint8_t *ws;
+    uint32_t t, e, k, dm, dff, shared, t_bucket;
+    uint32_t scheme_gu, scheme_dn;
+};
+size_t r9vx_moe_workspace_bytes(uint32_t t_bucket, uint32_t e, uint32_t k, uint32_t dm,
+                                uint32_t dff, uint32_t shared);
+int r9vx_launch_moe(const r9vx_moe_problem &p, hipStream_t stream);
+int r9vx_launch_moe_sort(const r9vx_moe_problem &p, uint32_t *counts, uint32_t *offsets,
+                         uint32_t *sorted, hipStream_t stream);
+int r9vx_read_moe_status(const r9vx_moe_problem &p, uint32_t *status, hipStream_t stream);
+
+#endif

@@ -1,0 +1,78 @@
+/*
+ * r9vx_moe.h -- the moe_ffn workspace layout (the kgen MoeSortBuffers slot,
+ * crates/r9v-kgen/src/abi/workspace.rs:13-40) and the stage launchers.
+ *
+ * Workspace regions (each 256-byte aligned), sized for t_bucket tokens:
+ *   status  u32[16]  [0] status bits, [1] scan counter, [2] work items
+ *   counts  u32[E]   pairs per expert
+ *   offsets u32[E+1] exclusive scan of counts
+ *   sorted  u32[P]   pair index (token*K + slot) at each sorted position
+ *   inv     u32[P]   sorted position of each pair
+ *   rank    u32[P]   rank of a pair among its expert's pairs in its chunk
+ *   ccount  u32[E*C] per-expert counts of each 256-pair chunk
+ *   cbase   u32[E*C] exclusive scan of ccount over chunks
+ *   work    u32x4[E+S] (expert, first position, pair count, 0) of active experts
+ *   tiles   u32x4[...] grouped-GEMM tile schedule
+ *   h       f32[(P + S*T) * Dff]  SwiGLU rows in sorted order, shared rows after
+ *   o       f32[(P + S*T) * Dm]   expert output rows in the same order
+ */
+#ifndef R9VX_MOE_H
+#define R9VX_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "r9vx_internal.h"
+
+constexpr uint32_t kMoeMaxE = 1024;
+constexpr uint32_t kMoeMaxK = 32;
+constexpr uint32_t kMoeTileM = 128; /* grouped-GEMM rows per tile */
+
+struct MoeLayout {
+    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, work, tiles, h, o, total;
+    uint32_t max_tiles;
+};
+
+inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint32_t dm, uint32_t dff,
+                                 uint32_t shared) {
+    MoeLayout L{};
+    uint64_t p = (uint64_t)t_bucket * k;
+    uint64_t nchunk = (p + 255) / 256;
+    uint64_t rows = p + (uint64_t)shared * t_bucket;
+    uint64_t off = 0;
+    auto take = [&](uint64_t bytes) {
+        uint64_t at = off;
+        off += (bytes + 255) & ~255ull;
+        return at;
+    };
+    L.max_tiles = (uint32_t)(p / kMoeTileM + e + shared + 1);
+    L.status = take(64);
+    L.counts = take(4ull * e);
+    L.offsets = take(4ull * (e + 1));
+    L.sorted = take(4 * p);
+    L.inv = take(4 * p);
+    L.rank = take(4 * p);
+    L.ccount = take(4ull * e * nchunk);
+    L.cbase = take(4ull * e * nchunk);
+    L.work = take(16ull * (e + shared));
+    L.tiles = take(16ull * L.max_tiles + 16);
+    L.h = take(4ull * rows * dff);
+    L.o = take(4ull * rows * dm);
+    L.total = off;
+    return L;
+}
+
+struct MoeCombineArgs {
+    const float *weights;
+    float *y;
+    uint8_t *ws;
+    MoeLayout L;
+    uint32_t t, k, dm, shared, p;
+};
+
+int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
+int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
+int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
+int r9vx_moe_combine_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
+
+#endif

@@ -1,0 +1,275 @@
+"""ctypes binding of libr9vx.so (include/r9vx.h) with torch device-memory plumbing.
+
+This is the host-side mirror of R9V's op surface for this path: `matmul`,
+`moe_route` and `moe_ffn` take the same operands with the same meaning as the
+T0 executors (crates/r9v-t0/src/lib.rs:280-348 execute_matmul_op,
+crates/r9v-t0/src/moe_route.rs:89 moe_route, crates/r9v-t0/src/moe_ffn.rs:75
+moe_ffn) and raise R9vxError where those return a T0Error.  All compute runs in
+the HIP library; there is no CPU or PyTorch fallback: a missing library or GPU
+raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import struct
+
+PKG = pathlib.Path(__file__).resolve().parent
+LIB_PATH = PKG / "libr9vx.so"
+
+# enums (include/r9vx.h)
+F32, F16, BF16, U32 = 0, 1, 2, 8
+Q4_K, IQ4_XS = 12, 23
+EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_RESIDUAL = 0, 1, 2
+SCORING_SOFTMAX, SCORING_SIGMOID = 0, 1
+ACT_SILU = 0
+STATUS_NONFINITE, STATUS_DEGENERATE, STATUS_BAD_EXPERT = 1, 2, 4
+BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136}
+
+_P = ctypes.c_void_p
+_U32 = ctypes.c_uint32
+
+
+class MatmulStatic(ctypes.Structure):
+    _fields_ = [("m_bucket", _U32), ("n", _U32), ("k", _U32), ("w_scheme", _U32),
+                ("in_dtype", _U32), ("out_dtype", _U32), ("epilogue", _U32),
+                ("residual_dtype", _U32)]
+
+
+class MatmulArgs(ctypes.Structure):
+    _fields_ = [("w", _P), ("w_scales", _P), ("w_indices", _P), ("x", _P), ("x_scale", _P),
+                ("bias", _P), ("residual", _P), ("y", _P), ("workspace", _P), ("m", _U32),
+                ("_tail_pad", _U32)]
+
+
+class MoeRouteStatic(ctypes.Structure):
+    _fields_ = [("t_bucket", _U32), ("e_total", _U32), ("top_k", _U32), ("scoring", _U32),
+                ("renormalize", _U32), ("scale_bits", _U32), ("has_bias", _U32),
+                ("n_group", _U32)]
+
+
+class MoeRouteArgs(ctypes.Structure):
+    _fields_ = [("logits", _P), ("bias", _P), ("expert_ids", _P), ("weights", _P), ("t", _U32),
+                ("_tail_pad", _U32)]
+
+
+class MoeFfnStatic(ctypes.Structure):
+    _fields_ = [("t_bucket", _U32), ("e_local", _U32), ("k_topk", _U32), ("dm", _U32),
+                ("dff", _U32), ("gate_up_scheme", _U32), ("down_scheme", _U32),
+                ("in_dtype", _U32), ("out_dtype", _U32), ("act", _U32),
+                ("shared_experts", _U32), ("_reserved", _U32)]
+
+
+class MoeFfnArgs(ctypes.Structure):
+    _fields_ = [("x", _P), ("expert_ids", _P), ("weights", _P), ("w_gate_up", _P),
+                ("w_gate_up_scales", _P), ("w_down", _P), ("w_down_scales", _P), ("y", _P),
+                ("sort_workspace", _P), ("t", _U32), ("_tail_pad", _U32)]
+
+
+# Every function include/r9vx.h declares: (name, argtypes, restype).
+EXPORTS = [
+    ("r9vx_matmul_launch", [_P, _P, _P], ctypes.c_int),
+    ("r9vx_matmul_workspace_bytes", [_P], ctypes.c_size_t),
+    ("r9vx_matmul_static_bytes", [_P, _U32], ctypes.c_uint64),
+    ("r9vx_matmul_static_flops", [_P, _U32], ctypes.c_uint64),
+    ("r9vx_moe_route_launch", [_P, _P, _P], ctypes.c_int),
+    ("r9vx_moe_route_status", [_P, _P], ctypes.c_int),
+    ("r9vx_moe_route_static_bytes", [_P, _U32], ctypes.c_uint64),
+    ("r9vx_moe_ffn_launch", [_P, _P, _P], ctypes.c_int),
+    ("r9vx_moe_ffn_workspace_bytes", [_P], ctypes.c_size_t),
+    ("r9vx_moe_ffn_status", [_P, _P, _P, _P], ctypes.c_int),
+    ("r9vx_moe_ffn_static_flops", [_P, _U32], ctypes.c_uint64),
+    ("r9vx_moe_sort_launch", [_P, _P, _U32, _P, _P, _P, _P, _P], ctypes.c_int),
+    ("r9vx_dequantize_launch", [_U32, _P, _U32, _U32, _P, _P], ctypes.c_int),
+    ("r9vx_validate_weights_launch", [_U32, _P, _U32, _U32, _P, _P], ctypes.c_int),
+    ("r9vx_last_error", [], ctypes.c_char_p),
+    ("r9vx_abi_version", [], _U32),
+]
+
+_lib = None
+
+
+class R9vxError(RuntimeError):
+    """A refusal (code < 0) or HIP error (code > 0) from libr9vx."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+
+
+def load():
+    """Loads libr9vx.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise R9vxError(-100, f"{LIB_PATH} is missing: run `python -m r9v_amd.build`")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, argtypes, restype in EXPORTS:
+            fn = getattr(L, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        _lib = L
+    return _lib
+
+
+def _check(rc: int):
+    if rc != 0:
+        raise R9vxError(rc, load().r9vx_last_error().decode(errors="replace"))
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(torch, stream):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _need_gpu(*tensors):
+    import torch
+
+    if not torch.cuda.is_available():
+        raise R9vxError(-101, "no HIP device: libr9vx has no CPU path")
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise R9vxError(-102, "operands must be device tensors")
+    return torch
+
+
+def _dtype_code(t):
+    import torch
+
+    return {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}[t.dtype]
+
+
+# ---------------------------------------------------------------- matmul
+
+def matmul_static(n, k, w_scheme, in_dtype, out_dtype, m_bucket=8, epilogue=EPILOGUE_NONE,
+                  residual_dtype=F32):
+    return MatmulStatic(m_bucket, n, k, w_scheme, in_dtype, out_dtype, epilogue, residual_dtype)
+
+
+def matmul(w, w_scheme, n, k, x, out_dtype=F32, bias=None, residual=None, y=None, workspace=None,
+           stream=None):
+    """y[m, n] = x[m, :] . w[n, :] (+ bias | + residual): T0 execute_matmul_op meaning."""
+    torch = _need_gpu(w, x, bias, residual, y)
+    m = x.shape[0]
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32 if out_dtype == F32 else torch.bfloat16,
+                        device=x.device)
+    epi = EPILOGUE_BIAS if bias is not None else (EPILOGUE_RESIDUAL if residual is not None else EPILOGUE_NONE)
+    st = matmul_static(n, k, w_scheme, _dtype_code(x), out_dtype, m_bucket=max(m, 1), epilogue=epi)
+    if workspace is None:
+        nbytes = matmul_workspace_bytes(st)
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes else None
+    args = MatmulArgs(_ptr(w), None, None, _ptr(x), None, _ptr(bias), _ptr(residual), _ptr(y),
+                      _ptr(workspace), m, 0)
+    _check(load().r9vx_matmul_launch(ctypes.byref(st), ctypes.byref(args), _stream(torch, stream)))
+    return y
+
+
+def matmul_workspace_bytes(st: MatmulStatic) -> int:
+    return int(load().r9vx_matmul_workspace_bytes(ctypes.byref(st)))
+
+
+def matmul_static_bytes(st: MatmulStatic, m: int) -> int:
+    return int(load().r9vx_matmul_static_bytes(ctypes.byref(st), m))
+
+
+# ---------------------------------------------------------------- decode
+
+def dequantize(wire, scheme, n_rows, k, out=None, stream=None):
+    torch = _need_gpu(wire, out)
+    if out is None:
+        out = torch.empty((n_rows, k), dtype=torch.float32, device=wire.device)
+    _check(load().r9vx_dequantize_launch(scheme, _ptr(wire), n_rows, k, _ptr(out), _stream(torch, stream)))
+    return out
+
+
+def validate_weights(wire, scheme, n_rows, k, stream=None) -> int:
+    torch = _need_gpu(wire)
+    bad = torch.zeros(1, dtype=torch.int32, device=wire.device)
+    _check(load().r9vx_validate_weights_launch(scheme, _ptr(wire), n_rows, k, _ptr(bad),
+                                               _stream(torch, stream)))
+    return int(bad.item())
+
+
+# ---------------------------------------------------------------- moe_route
+
+def route_static(e, k, t_bucket, scoring=SCORING_SOFTMAX, renormalize=True, scale=1.0,
+                 has_bias=False):
+    scale_bits = struct.unpack("<I", struct.pack("<f", scale))[0]
+    return MoeRouteStatic(t_bucket, e, k, scoring, int(renormalize), scale_bits, int(has_bias), 0)
+
+
+def moe_route(logits, k, bias=None, scoring=SCORING_SOFTMAX, renormalize=True, scale=1.0,
+              ids=None, weights=None, stream=None):
+    torch = _need_gpu(logits, bias)
+    t, e = logits.shape
+    if ids is None:
+        ids = torch.empty((t, k), dtype=torch.int32, device=logits.device)
+    if weights is None:
+        weights = torch.empty((t, k), dtype=torch.float32, device=logits.device)
+    st = route_static(e, k, max(t, 1), scoring, renormalize, scale, bias is not None)
+    args = MoeRouteArgs(_ptr(logits), _ptr(bias), _ptr(ids), _ptr(weights), t, 0)
+    _check(load().r9vx_moe_route_launch(ctypes.byref(st), ctypes.byref(args), _stream(torch, stream)))
+    return ids, weights
+
+
+def moe_route_status(stream=None) -> int:
+    import torch
+
+    s = ctypes.c_uint32(0)
+    _check(load().r9vx_moe_route_status(ctypes.byref(s), _stream(torch, stream)))
+    return s.value
+
+
+# ---------------------------------------------------------------- moe_ffn
+
+def ffn_static(t_bucket, e, k, dm, dff, shared=0, gate_up_scheme=IQ4_XS, down_scheme=Q4_K):
+    return MoeFfnStatic(t_bucket, e, k, dm, dff, gate_up_scheme, down_scheme, BF16, F32,
+                        ACT_SILU, shared, 0)
+
+
+def ffn_workspace_bytes(st: MoeFfnStatic) -> int:
+    return int(load().r9vx_moe_ffn_workspace_bytes(ctypes.byref(st)))
+
+
+def moe_ffn(x, ids, weights, w_gate_up, w_down, e, dff, shared=0, gate_up_scheme=IQ4_XS,
+            down_scheme=Q4_K, y=None, workspace=None, t_bucket=None, stream=None):
+    torch = _need_gpu(x, ids, weights, w_gate_up, w_down, y, workspace)
+    t, dm = x.shape
+    k = ids.shape[1]
+    st = ffn_static(t_bucket or max(t, 1), e, k, dm, dff, shared, gate_up_scheme, down_scheme)
+    if workspace is None:
+        workspace = torch.empty(ffn_workspace_bytes(st), dtype=torch.uint8, device=x.device)
+    if y is None:
+        y = torch.empty((t, dm), dtype=torch.float32, device=x.device)
+    args = MoeFfnArgs(_ptr(x), _ptr(ids), _ptr(weights), _ptr(w_gate_up), None, _ptr(w_down), None,
+                      _ptr(y), _ptr(workspace), t, 0)
+    _check(load().r9vx_moe_ffn_launch(ctypes.byref(st), ctypes.byref(args), _stream(torch, stream)))
+    return y, workspace, st
+
+
+def moe_ffn_status(st, workspace, stream=None) -> int:
+    import torch
+
+    s = ctypes.c_uint32(0)
+    _check(load().r9vx_moe_ffn_status(ctypes.byref(st), _ptr(workspace), ctypes.byref(s),
+                                      _stream(torch, stream)))
+    return s.value
+
+
+def moe_sort(ids, e, dm=256, dff=256, workspace=None, stream=None):
+    torch = _need_gpu(ids, workspace)
+    t, k = ids.shape
+    st = ffn_static(max(t, 1), e, k, dm, dff)
+    if workspace is None:
+        workspace = torch.empty(ffn_workspace_bytes(st), dtype=torch.uint8, device=ids.device)
+    counts = torch.empty(e, dtype=torch.int32, device=ids.device)
+    offsets = torch.empty(e + 1, dtype=torch.int32, device=ids.device)
+    order = torch.empty(t * k, dtype=torch.int32, device=ids.device)
+    _check(load().r9vx_moe_sort_launch(ctypes.byref(st), _ptr(ids), t, _ptr(workspace), _ptr(counts),
+                                       _ptr(offsets), _ptr(order), _stream(torch, stream)))
+    return counts, offsets, order

@@ -1,0 +1,126 @@
+"""CPU checks of the C-ABI boundary: the library loads, exports every function
+include/r9vx.h declares, the argument structs follow the kgen layout rule, and
+host-side refusals happen before any device call."""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+from r9v_amd import ffi
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "r9vx.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^[a-z_0-9 *]*?\b(r9vx_[a-z_0-9]+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ffi.load()
+    names = declared_functions()
+    assert len(names) >= 16
+    for n in names:
+        assert hasattr(lib, n), n
+    assert sorted(n for n, _, _ in ffi.EXPORTS) == names
+    assert lib.r9vx_abi_version() == 1
+
+
+def kgen_layout(fields):
+    """crates/r9v-kgen/src/abi/layout.rs:102-180: stable sort by descending
+    alignment, natural padding, total rounded to the max alignment."""
+    order = sorted(range(len(fields)), key=lambda i: (-fields[i][1], i))
+    off, offs, maxal = 0, {}, 1
+    for i in order:
+        name, al = fields[i]
+        off = (off + al - 1) // al * al
+        offs[name] = off
+        off += al
+        maxal = max(maxal, al)
+    return offs, (off + maxal - 1) // maxal * maxal
+
+
+# Field declaration order of crates/r9v-kgen/src/abi/per_op.rs:794-968
+# (pointer = 8 bytes, u32 = 4 bytes); the workspace slot is appended where
+# add_workspace_slot is called.
+KGEN = {
+    "r9vx_matmul_args": [("w", 8), ("w_scales", 8), ("w_indices", 8), ("x", 8), ("x_scale", 8), ("bias", 8),
+                         ("residual", 8), ("y", 8), ("workspace", 8), ("m", 4)],
+    "r9vx_moe_route_args": [("logits", 8), ("bias", 8), ("expert_ids", 8), ("weights", 8), ("t", 4)],
+    "r9vx_moe_ffn_args": [("x", 8), ("expert_ids", 8), ("weights", 8), ("w_gate_up", 8),
+                          ("w_gate_up_scales", 8), ("w_down", 8), ("w_down_scales", 8), ("y", 8),
+                          ("sort_workspace", 8), ("t", 4)],
+}
+
+
+def test_arg_structs_match_kgen_layout(tmp_path):
+    src = tmp_path / "layout.c"
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "r9vx.h"', "int main(void){"]
+    for st, fields in KGEN.items():
+        lines.append(f'printf("{st} size %zu\\n", sizeof({st}));')
+        for name, _ in fields:
+            lines.append(f'printf("{st} {name} %zu\\n", offsetof({st}, {name}));')
+    lines.append("return 0;}")
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        st, field, val = line.split()
+        got[(st, field)] = int(val)
+    for st, fields in KGEN.items():
+        offs, size = kgen_layout(fields)
+        assert got[(st, "size")] == size, st
+        for name, _ in fields:
+            assert got[(st, name)] == offs[name], (st, name)
+    # the ctypes mirror agrees with the C header
+    assert ctypes.sizeof(ffi.MatmulArgs) == got[("r9vx_matmul_args", "size")]
+    assert ctypes.sizeof(ffi.MoeRouteArgs) == got[("r9vx_moe_route_args", "size")]
+    assert ctypes.sizeof(ffi.MoeFfnArgs) == got[("r9vx_moe_ffn_args", "size")]
+
+
+def _call(fn, st, args):
+    return fn(ctypes.byref(st) if st is not None else None, ctypes.byref(args) if args is not None else None, None)
+
+
+def test_host_refusals_collect_all_problems():
+    lib = ffi.load()
+    assert _call(lib.r9vx_matmul_launch, None, None) == -3
+    st = ffi.matmul_static(n=0, k=300, w_scheme=99, in_dtype=5, out_dtype=ffi.F32)
+    args = ffi.MatmulArgs()
+    args.m = 1
+    rc = _call(lib.r9vx_matmul_launch, st, args)
+    msg = lib.r9vx_last_error().decode()
+    assert rc < 0
+    for part in ("w_scheme 99", "k=300", "n must be positive", "in_dtype 5", "w is NULL"):
+        assert part in msg, msg
+    rst = ffi.route_static(e=4, k=5, t_bucket=1, scale=-1.0)
+    rargs = ffi.MoeRouteArgs()
+    rargs.t = 2
+    assert _call(lib.r9vx_moe_route_launch, rst, rargs) < 0
+    msg = lib.r9vx_last_error().decode()
+    for part in ("scale must be finite", "top_k 5 cannot exceed", "t=2 exceeds t_bucket=1", "logits"):
+        assert part in msg, msg
+    fst = ffi.ffn_static(t_bucket=4, e=4, k=2, dm=300, dff=256)
+    fargs = ffi.MoeFfnArgs()
+    fargs.t = 2
+    assert _call(lib.r9vx_moe_ffn_launch, fst, fargs) < 0
+    msg = lib.r9vx_last_error().decode()
+    assert "Dm=300" in msg and "sort_workspace is NULL" in msg
+
+
+def test_workspace_and_static_figures():
+    st = ffi.matmul_static(n=5120, k=2048, w_scheme=ffi.IQ4_XS, in_dtype=ffi.BF16, out_dtype=ffi.F32, m_bucket=5)
+    assert ffi.matmul_static_bytes(st, 1) == 5_595_136  # BASELINE.md config 1, M=1
+    assert ffi.matmul_static_bytes(st, 5) == 5_693_440  # M=5
+    st0 = ffi.matmul_static(n=4096, k=4096, w_scheme=ffi.Q4_K, in_dtype=ffi.F32, out_dtype=ffi.F32)
+    assert ffi.matmul_static_bytes(st0, 1) == 9_469_952  # config 0
+    fst = ffi.ffn_static(t_bucket=8192, e=512, k=10, dm=2048, dff=512)
+    lib = ffi.load()
+    assert lib.r9vx_moe_ffn_static_flops(ctypes.byref(fst), 8192) == 515_396_075_520  # config 4
+    assert ffi.ffn_workspace_bytes(fst) > 81920 * 2048 * 4

@@ -1,0 +1,207 @@
+"""GPU parity of the decode (bit-exact) and of the dequant-fused GEMV / GEMM
+against the CPU oracle, through the C ABI."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle_ffi as O
+from golden_io import iq4_cases, q4k_cases
+from r9v_amd import ffi, synth
+from tol import check_bf16_out, check_close
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def bf16_dev(bits):
+    return dev(bits.view(np.int16)).view(torch.bfloat16)
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+# ---------------------------------------------------------------- decode
+
+@pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])
+def test_dequantize_bit_exact_random(scheme):
+    n, k = 61, 1024
+    w = synth.quant_weights(scheme, 101, n, k)
+    got = host(ffi.dequantize(dev(w), scheme, n, k))
+    want = O.dequantize(scheme, w, n, k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequantize_golden_vectors():
+    for c in q4k_cases():
+        got = host(ffi.dequantize(dev(c["block"]), O.Q4_K, 1, 256))[0]
+        assert np.array_equal(got.view(np.uint32), c["y_bits"]), c["name"]
+    c = iq4_cases()["IQ4_XS"]
+    got = host(ffi.dequantize(dev(c["wire"]), O.IQ4_XS, c["n"], c["k"]))
+    assert np.array_equal(got.reshape(-1).view(np.uint32), c["y_bits"])
+
+
+def test_validate_weights_counts_nonfinite_blocks():
+    w = synth.quant_weights(O.Q4_K, 5, 8, 512).copy()
+    w[3, 2:4] = [0x00, 0x7C]  # dmin of block 6 = +inf
+    w[5, 144:146] = [0x01, 0x7E]  # d of block 11 = nan
+    assert ffi.validate_weights(dev(w), O.Q4_K, 8, 512) == 2
+    assert ffi.validate_weights(dev(synth.quant_weights(O.IQ4_XS, 6, 8, 512)), O.IQ4_XS, 8, 512) == 0
+
+
+# ---------------------------------------------------------------- GEMV
+
+def _gemv_case(scheme, n, k, m, x_dtype, out_dtype=O.F32, seed=0, bias=False, residual=False):
+    w = synth.quant_weights(scheme, seed + 1, n, k)
+    if x_dtype == O.BF16:
+        x = synth.normal_bf16(seed + 2, (m, k))
+        xd = bf16_dev(x)
+    else:
+        x = synth.normal_f32(seed + 2, (m, k))
+        xd = dev(x)
+    b = synth.normal_f32(seed + 3, (n,)) if bias else None
+    r = synth.normal_f32(seed + 4, (m, n)) if residual else None
+    ref = O.matmul(scheme, w, n, k, x, x_dtype, bias=b, residual=r)
+    y = ffi.matmul(dev(w), scheme, n, k, xd, out_dtype=out_dtype,
+                   bias=None if b is None else dev(b), residual=None if r is None else dev(r))
+    torch.cuda.synchronize()
+    got = host(y.float()) if out_dtype == O.BF16 else host(y)
+    return got, ref
+
+
+def test_gemv_config0_q4k_f32():
+    """Q4_K 4096x4096, x fp32 [1x4096], y fp32."""
+    got, ref = _gemv_case(O.Q4_K, 4096, 4096, 1, O.F32, seed=1000)
+    check_close(got, ref, "config0")
+
+
+@pytest.mark.parametrize("m", [1, 5])
+def test_gemv_config1_iq4xs_bf16(m):
+    """IQ4_XS K=2048 N=5120, x bf16 [M x 2048], M in {1, 5}."""
+    got, ref = _gemv_case(O.IQ4_XS, 5120, 2048, m, O.BF16, seed=2000 + m)
+    check_close(got, ref, f"config1 m={m}")
+
+
+@pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])
+@pytest.mark.parametrize("x_dtype", [O.F32, O.BF16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_gemv_all_m(scheme, x_dtype, m):
+    got, ref = _gemv_case(scheme, 77, 1024, m, x_dtype, seed=3000 + m)
+    check_close(got, ref, f"m={m}")
+
+
+@pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])
+@pytest.mark.parametrize("n,k", [(1, 256), (3, 512), (17, 768), (130, 2048), (33, 4096), (9, 8192)])
+def test_gemv_ragged_shapes(scheme, n, k):
+    got, ref = _gemv_case(scheme, n, k, 3, O.BF16, seed=4000 + n + k)
+    check_close(got, ref, f"n={n} k={k}")
+    got, ref = _gemv_case(scheme, n, k, 1, O.F32, seed=4100 + n + k)
+    check_close(got, ref, f"f32 n={n} k={k}")
+
+
+def test_gemv_epilogues_and_bf16_out():
+    got, ref = _gemv_case(O.IQ4_XS, 96, 512, 4, O.BF16, seed=5000, bias=True)
+    check_close(got, ref, "bias")
+    got, ref = _gemv_case(O.Q4_K, 96, 512, 4, O.BF16, seed=5001, residual=True)
+    check_close(got, ref, "residual")
+    got, ref = _gemv_case(O.Q4_K, 96, 512, 2, O.BF16, out_dtype=O.BF16, seed=5002)
+    check_bf16_out(got, ref, "bf16 out")
+
+
+def test_gemv_batch_invariance():
+    """Row m of a batched launch equals the same row launched alone (bit-equal),
+    the T0 batch-invariance gate (crates/r9v-t0/src/harness.rs:910-950)."""
+    n, k = 300, 2048
+    w = dev(synth.quant_weights(O.IQ4_XS, 6001, n, k))
+    x = bf16_dev(synth.normal_bf16(6002, (5, k)))
+    yb = host(ffi.matmul(w, O.IQ4_XS, n, k, x))
+    for r in range(5):
+        y1 = host(ffi.matmul(w, O.IQ4_XS, n, k, x[r:r + 1].contiguous()))
+        assert np.array_equal(y1[0], yb[r])
+    y2 = host(ffi.matmul(w, O.IQ4_XS, n, k, x))
+    assert np.array_equal(y2, yb)  # run-twice determinism
+
+
+def test_matmul_refusals():
+    w = dev(synth.quant_weights(O.Q4_K, 7, 4, 256))
+    x = dev(np.zeros((1, 300), np.float32))
+    with pytest.raises(ffi.R9vxError) as e:
+        ffi.matmul(w, O.Q4_K, 4, 300, x)
+    assert e.value.code == -1 and "k=300" in str(e.value)
+    with pytest.raises(ffi.R9vxError):
+        ffi.matmul(w, 99, 4, 256, dev(np.zeros((1, 256), np.float32)))
+
+
+# ---------------------------------------------------------------- MFMA GEMM
+
+def _gemm_case(scheme, n, k, m, seed, out_dtype=O.F32, bias=False, residual=False, rows=None, cols=None):
+    """Full GPU GEMM; oracle on the sampled rows/cols (all when None)."""
+    w = synth.quant_weights(scheme, seed + 1, n, k)
+    x = synth.normal_bf16(seed + 2, (m, k))
+    b = synth.normal_f32(seed + 3, (n,)) if bias else None
+    r = synth.normal_f32(seed + 4, (m, n)) if residual else None
+    y = ffi.matmul(dev(w), scheme, n, k, bf16_dev(x), out_dtype=out_dtype,
+                   bias=None if b is None else dev(b), residual=None if r is None else dev(r))
+    got = host(y.float())
+    rows = np.arange(m) if rows is None else np.asarray(rows)
+    cols = np.arange(n) if cols is None else np.asarray(cols)
+    ref = O.matmul(scheme, np.ascontiguousarray(w[cols]), len(cols), k, np.ascontiguousarray(x[rows]), O.BF16,
+                   bias=None if b is None else np.ascontiguousarray(b[cols]),
+                   residual=None if r is None else np.ascontiguousarray(r[np.ix_(rows, cols)]))
+    return got[np.ix_(rows, cols)], ref
+
+
+def test_gemm_config2_sampled():
+    """x bf16 [2048 x 4096] . Q4_K [14336 x 4096]^T -> bf16, full
+    launch; 48 rows (every M tile, tile edges) x 1536 columns checked."""
+    m, n, k = 2048, 14336, 4096
+    rows = np.unique(np.concatenate([np.arange(0, m, 97), [0, 1, 255, 256, 1023, 2047]]))
+    cols = np.unique(np.concatenate([np.arange(0, n, 11)[:1500], [0, 255, 256, 14335, 7000]]))
+    got, ref = _gemm_case(O.Q4_K, n, k, m, 7000, out_dtype=O.BF16, rows=rows, cols=cols)
+    check_bf16_out(got, ref, "config2 sampled")
+
+
+@pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])
+@pytest.mark.parametrize("m,n,k", [(9, 33, 256), (100, 300, 768), (257, 256, 512), (512, 513, 1024)])
+def test_gemm_shapes(scheme, m, n, k):
+    got, ref = _gemm_case(scheme, n, k, m, 7100 + m + n + k)
+    check_close(got, ref, f"m={m} n={n} k={k}")
+
+
+def test_gemm_epilogues_bf16_out():
+    got, ref = _gemm_case(O.IQ4_XS, 200, 512, 40, 7200, bias=True)
+    check_close(got, ref, "bias")
+    got, ref = _gemm_case(O.Q4_K, 200, 512, 40, 7201, residual=True)
+    check_close(got, ref, "residual")
+    got, ref = _gemm_case(O.Q4_K, 300, 1024, 70, 7202, out_dtype=O.BF16)
+    check_bf16_out(got, ref, "bf16 out")
+
+
+def test_gemm_row_permutation_invariance_full_size():
+    """Each output row depends only on its own x row: permuting the 2048 rows
+    of configs[2] permutes y bit for bit (size-independent check)."""
+    m, n, k = 2048, 14336, 4096
+    w = dev(synth.quant_weights(O.Q4_K, 7301, n, k))
+    x = synth.normal_bf16(7302, (m, k))
+    perm = np.random.default_rng(5).permutation(m)
+    y = host(ffi.matmul(w, O.Q4_K, n, k, bf16_dev(x), out_dtype=O.BF16).view(torch.int16))
+    yp = host(ffi.matmul(w, O.Q4_K, n, k, bf16_dev(x[perm]), out_dtype=O.BF16).view(torch.int16))
+    assert np.array_equal(yp, y[perm])
+
+
+def test_gemm_large_activation_rows_scaled_exactly():
+    """Rows with |x| >= 2^15 go through the power-of-two row scale."""
+    m, n, k = 16, 64, 512
+    w = synth.quant_weights(O.Q4_K, 7401, n, k)
+    xf = synth.normal_f32(7402, (m, k))
+    xf[3] *= 1e6
+    xf[7, 5] = 3e9
+    x = synth.to_bf16_bits(xf)
+    y = host(ffi.matmul(dev(w), O.Q4_K, n, k, bf16_dev(x)))
+    ref = O.matmul(O.Q4_K, w, n, k, x, O.BF16)
+    check_close(y, ref, "large rows")

@@ -1,0 +1,188 @@
+"""GPU parity of moe_route (bit-exact ids and weights), the permute
+(bit-exact counts/offsets/order) and moe_ffn against
+the CPU oracle, through the C ABI."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle_ffi as O
+from r9v_amd import ffi, synth
+from tol import check_close
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def bf16_dev(bits):
+    return dev(bits.view(np.int16)).view(torch.bfloat16)
+
+
+# ---------------------------------------------------------------- routing
+
+def _route_both(logits, k, **kw):
+    ids_o, w_o = O.moe_route(logits, k, **{kk: v for kk, v in kw.items()})
+    bias = kw.get("bias")
+    ids_g, w_g = ffi.moe_route(dev(logits), k, bias=None if bias is None else dev(bias),
+                               scoring=kw.get("scoring", 0), renormalize=kw.get("renormalize", True),
+                               scale=kw.get("scale", 1.0))
+    torch.cuda.synchronize()
+    return (ids_o, w_o), (host(ids_g).view(np.uint32), host(w_g))
+
+
+def _assert_bit_exact(o, g):
+    assert np.array_equal(o[0], g[0]), "expert ids differ"
+    assert np.array_equal(o[1].view(np.uint32), g[1].view(np.uint32)), "weights differ"
+
+
+def test_route_config3_bit_exact():
+    """T=5, E=512, top-10 from N(0,1) logits, renormalised softmax."""
+    logits = synth.normal_f32(synth.seed_for("c3", "logits"), (5, 512))
+    _assert_bit_exact(*_route_both(logits, 10))
+
+
+def test_route_config4_zipf_bit_exact():
+    """T=8192, E=512, top-10, Zipf(1.1)-skewed logits."""
+    logits = synth.zipf_logits(synth.seed_for("c4", "logits"), 8192, 512)
+    _assert_bit_exact(*_route_both(logits, 10))
+
+
+@pytest.mark.parametrize("t,e,k", [(1, 8, 1), (3, 64, 8), (65, 128, 4), (200, 1024, 32), (7, 100, 7)])
+def test_route_shapes_bit_exact(t, e, k):
+    logits = synth.normal_f32(700 + t + e + k, (t, e), sigma=3.0)
+    _assert_bit_exact(*_route_both(logits, k))
+
+
+def test_route_ties_bias_sigmoid_scale():
+    logits = np.ones((2, 6), dtype=np.float32)
+    for scoring in (0, 1):
+        o, g = _route_both(logits, 3, scoring=scoring)
+        assert g[0].reshape(-1).tolist() == [0, 1, 2, 0, 1, 2]
+        _assert_bit_exact(o, g)
+    logits = synth.normal_f32(801, (100, 256))
+    bias = synth.normal_f32(802, (256,))
+    _assert_bit_exact(*_route_both(logits, 6, bias=bias))
+    _assert_bit_exact(*_route_both(logits, 6, scoring=1))
+    _assert_bit_exact(*_route_both(logits, 6, scale=2.5, renormalize=False))
+    _assert_bit_exact(*_route_both(logits, 6, scoring=1, renormalize=False, scale=0.75))
+    # quantised logits produce many exact score ties: lowest id must win
+    tied = (np.round(synth.normal_f32(803, (300, 512)) * 2) / 2).astype(np.float32)
+    _assert_bit_exact(*_route_both(tied, 10))
+
+
+@pytest.mark.parametrize("t", [4, 300])
+def test_route_refuses_nonfinite_before_writing(t):
+    logits = synth.normal_f32(901, (t, 64))
+    logits[t // 2, 5] = np.nan
+    ids = torch.full((t, 4), 77, dtype=torch.int32, device="cuda")
+    w = torch.full((t, 4), -1.0, dtype=torch.float32, device="cuda")
+    ffi.moe_route(dev(logits), 4, ids=ids, weights=w)
+    assert ffi.moe_route_status() & ffi.STATUS_NONFINITE
+    assert (host(ids) == 77).all() and (host(w) == -1.0).all()
+    # the next valid call clears the status and writes
+    ffi.moe_route(dev(np.zeros((t, 64), np.float32)), 4, ids=ids, weights=w)
+    assert ffi.moe_route_status() == 0
+    assert (host(ids)[:, 0] == 0).all()
+
+
+def test_route_host_refusals():
+    with pytest.raises(ffi.R9vxError) as e:
+        ffi.moe_route(dev(np.zeros((2, 4), np.float32)), 5)
+    assert "top_k 5 cannot exceed" in str(e.value)
+    with pytest.raises(ffi.R9vxError):
+        ffi.moe_route(dev(np.zeros((2, 4), np.float32)), 2, scale=0.0)
+
+
+# ---------------------------------------------------------------- permute
+
+@pytest.mark.parametrize("t,e,k", [(5, 512, 10), (8192, 512, 10), (1, 4, 2), (103, 1024, 32), (3000, 7, 3)])
+def test_sort_bit_exact(t, e, k):
+    if e >= 64:
+        logits = synth.zipf_logits(1000 + t + e, t, e)
+        ids, _ = O.moe_route(logits, k)
+    else:
+        ids = (synth.splitmix64(1001 + t, t * k) % np.uint64(e)).astype(np.uint32).reshape(t, k)
+    c_o, off_o, srt_o = O.moe_sort(ids, e)
+    c_g, off_g, srt_g = ffi.moe_sort(dev(ids.view(np.int32)), e)
+    assert np.array_equal(host(c_g).view(np.uint32), c_o)
+    assert np.array_equal(host(off_g).view(np.uint32), off_o)
+    assert np.array_equal(host(srt_g).view(np.uint32), srt_o)
+
+
+# ---------------------------------------------------------------- moe_ffn
+
+def _experts(seed, e, s, dm, dff, active):
+    """Stacked expert weights with the `active` experts (and the shared ones)
+    filled from the seeded generator and the rest zero blocks."""
+    bb_gu, bb_dn = synth.BLOCK_BYTES[synth.IQ4_XS], synth.BLOCK_BYTES[synth.Q4_K]
+    gu = np.zeros(((e + s) * 2 * dff, dm // 256 * bb_gu), dtype=np.uint8)
+    dn = np.zeros(((e + s) * dm, dff // 256 * bb_dn), dtype=np.uint8)
+    for ex in sorted(set(int(v) for v in active)) + list(range(e, e + s)):
+        gu[ex * 2 * dff:(ex + 1) * 2 * dff] = synth.quant_weights(synth.IQ4_XS, seed + 2 * ex, 2 * dff, dm)
+        dn[ex * dm:(ex + 1) * dm] = synth.quant_weights(synth.Q4_K, seed + 2 * ex + 1, dm, dff)
+    return gu, dn
+
+
+def _moe_case(t, e, k, dm, dff, shared, seed, zipf=False):
+    logits = synth.zipf_logits(seed, t, e) if zipf else synth.normal_f32(seed, (t, e))
+    ids, w = O.moe_route(logits, k)
+    gu, dn = _experts(seed + 10, e, shared, dm, dff, ids.reshape(-1))
+    x = synth.normal_bf16(seed + 3, (t, dm))
+    ref = O.moe_ffn(x, O.BF16, ids, w, e, dff, gu, dn, shared=shared)
+    y, ws, st = ffi.moe_ffn(bf16_dev(x), dev(ids.view(np.int32)), dev(w), dev(gu), dev(dn), e, dff,
+                            shared=shared)
+    torch.cuda.synchronize()
+    assert ffi.moe_ffn_status(st, ws) == 0
+    return host(y), ref
+
+
+def test_moe_ffn_config3_decode():
+    """T=5 (MTP4 verify), hidden 2048, 512 experts, top-10, IQ4_XS
+    gate/up [2048 -> 2x512] + Q4_K down [512 -> 2048], plus one shared expert."""
+    got, ref = _moe_case(5, 512, 10, 2048, 512, 1, synth.seed_for("c3", "moe") % (1 << 32))
+    check_close(got, ref, "config3")
+
+
+@pytest.mark.parametrize("t,e,k,dm,dff,shared", [(1, 8, 2, 256, 256, 0), (3, 16, 4, 512, 256, 1),
+                                                  (8, 32, 3, 256, 512, 2), (2, 4, 4, 768, 256, 0)])
+def test_moe_ffn_decode_shapes(t, e, k, dm, dff, shared):
+    got, ref = _moe_case(t, e, k, dm, dff, shared, 1100 + t + e)
+    check_close(got, ref, f"t={t} e={e}")
+
+
+def test_moe_ffn_duplicate_slots_and_refusal():
+    t, e, k, dm, dff = 4, 8, 3, 256, 256
+    ids = np.array([[1, 1, 5], [0, 7, 7], [2, 3, 4], [6, 6, 6]], dtype=np.uint32)
+    w = synth.normal_f32(1201, (t, k))
+    gu, dn = _experts(1202, e, 0, dm, dff, range(e))
+    x = synth.normal_bf16(1203, (t, dm))
+    ref = O.moe_ffn(x, O.BF16, ids, w, e, dff, gu, dn)
+    y, ws, st = ffi.moe_ffn(bf16_dev(x), dev(ids.view(np.int32)), dev(w), dev(gu), dev(dn), e, dff)
+    check_close(host(y), ref, "duplicates")
+    bad = ids.copy()
+    bad[2, 1] = e  # out of range
+    y2 = torch.full((t, dm), 3.0, dtype=torch.float32, device="cuda")
+    ffi.moe_ffn(bf16_dev(x), dev(bad.view(np.int32)), dev(w), dev(gu), dev(dn), e, dff, y=y2, workspace=ws)
+    assert ffi.moe_ffn_status(st, ws) & ffi.STATUS_BAD_EXPERT
+    assert (host(y2) == 3.0).all()
+
+
+def test_moe_ffn_token_permutation_invariance():
+    """Permuting tokens permutes outputs bit for bit (moe_ffn_tests.rs:278)."""
+    t, e, k, dm, dff = 6, 16, 4, 512, 256
+    logits = synth.normal_f32(1301, (t, e))
+    ids, w = O.moe_route(logits, k)
+    gu, dn = _experts(1302, e, 0, dm, dff, range(e))
+    x = synth.normal_bf16(1303, (t, dm))
+    perm = np.array([4, 2, 0, 5, 1, 3])
+    y, _, _ = ffi.moe_ffn(bf16_dev(x), dev(ids.view(np.int32)), dev(w), dev(gu), dev(dn), e, dff)
+    yp, _, _ = ffi.moe_ffn(bf16_dev(x[perm]), dev(ids[perm].view(np.int32)), dev(w[perm]), dev(gu), dev(dn), e, dff)
+    assert np.array_equal(host(yp), host(y)[perm])
