@@ -1,17 +1,22 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X quantized-weight matrix path (one GPU).
 
-Headline: IQ4_XS dequant-fused GEMV, K=2048,
-N=5120, M=5 (1 + 4 MTP draft tokens), bf16 x, f32 y.  A step is one GEMV over
-one batch; weights rotate through enough distinct copies (>= 2x the 256 MB
-Infinity Cache) that every step reads them from HBM.  value = algorithmic
-bytes / wall time of the K timed steps, inputs resident in HBM.
+Headline: the IQ4_XS dequant-fused GEMV at
+K=2048, N=5120, M=5 (1 + 4 MTP draft tokens), bf16 x, f32 y.  A step is one
+GEMV launch over one batch; the weights rotate through enough distinct copies
+(>= 2x the 256 MB Infinity Cache) that every step reads them from HBM.
+`value` = algorithmic bytes / time of the K timed steps with every input
+resident in HBM.  `roofline` is the GEMV kernel's per-launch figure from
+back-to-back launches replayed from a HIP graph.
 
-The other configs are reported in `extras` with their own roofline figures.
-The CPU baseline times the oracle (a scalar restatement of R9V's T0 path) on
-a bounded sample of the same workload on this host.
+`extras` carries the other configs with their own roofline figures:
+configs[0] Q4_K GEMV (HBM), configs[2] dense dequant-GEMM (MFMA),
+configs[3] MoE decode (HBM), configs[4] MoE prefill grouped GEMM (MFMA),
+plus the router on its own.  `cpu_baseline` times the oracle (a scalar C
+restatement of R9V's T0 Branch-D path) on a bounded sample of the headline
+workload on this host.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c0,c2,...]
 """
 from __future__ import annotations
 
@@ -23,8 +28,9 @@ import time
 
 import numpy as np
 
+ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
-BF16_PEAK_TFLOPS = 2500.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16/fp16 MFMA, MI355X
 IC_BYTES = 256 << 20
 METRIC = "quant GEMV/MoE HBM GB/s (% of peak); prefill grouped-GEMM TFLOP/s (% MFMA)"
 
@@ -35,7 +41,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of extras to run (c0,c1m1)")
+    ap.add_argument("--only", default="", help="comma list of extras: c0,c1m1,c2,c3,c4,ceilings")
     return ap.parse_args()
 
 
@@ -43,102 +49,230 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-class GemvBench:
-    """One dense GEMV workload with rotated weight copies."""
+def copies_for(nbytes):
+    return max(2, -(-2 * IC_BYTES // max(nbytes, 1)))
 
-    def __init__(self, torch, ffi, synth, scheme, n, k, m, x_dtype, seed):
+
+def event_time(torch, fn, steps, warmup):
+    """ms per call over `steps` calls, events on the launch stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(steps):
+        fn()
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def graph_time(torch, fn, launches, reps=20):
+    """ms per launch of `launches` back-to-back calls captured in a HIP graph."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            for i in range(launches):
+                fn(i, s)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(launches):
+                fn(i, s)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(cur)
+    for _ in range(reps):
+        g.replay()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (reps * launches)
+
+
+def hbm(bytes_, ms):
+    gbs = bytes_ / (ms * 1e-3) / 1e9
+    return {"GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def mfma(flops, ms):
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"TFLOP/s": round(tf, 1), "frac_mfma": round(tf / MFMA_PEAK_TFLOPS, 4)}
+
+
+class Gemv:
+    def __init__(self, torch, ffi, synth, gsynth, scheme, n, k, m, x_dtype, tag):
         self.torch, self.ffi = torch, ffi
         self.scheme, self.n, self.k, self.m, self.x_dtype = scheme, n, k, m, x_dtype
-        w = synth.quant_weights(scheme, synth.seed_for(seed, "w"), n, k)
-        self.w_host = w
-        self.w_bytes = w.nbytes
-        copies = max(2, -(-2 * IC_BYTES // w.nbytes))
-        wd = torch.from_numpy(w).cuda()
-        self.ws = [wd] + [wd.clone() for _ in range(copies - 1)]
+        self.w_host = synth.quant_weights(scheme, synth.seed_for(tag, "w"), n, k)
+        wd = torch.from_numpy(self.w_host).cuda()
+        self.ws = [wd] + [wd.clone() for _ in range(copies_for(self.w_host.nbytes) - 1)]
         if x_dtype == ffi.BF16:
-            self.x_host = synth.normal_bf16(synth.seed_for(seed, "x"), (m, k))
+            self.x_host = synth.normal_bf16(synth.seed_for(tag, "x"), (m, k))
             self.x = torch.from_numpy(self.x_host.view(np.int16)).cuda().view(torch.bfloat16)
         else:
-            self.x_host = synth.normal_f32(synth.seed_for(seed, "x"), (m, k))
+            self.x_host = synth.normal_f32(synth.seed_for(tag, "x"), (m, k))
             self.x = torch.from_numpy(self.x_host).cuda()
         self.y = torch.empty((m, n), dtype=torch.float32, device="cuda")
-        self.st = ffi.matmul_static(n, k, scheme, x_dtype, ffi.F32, m_bucket=m)
-        self.bytes = ffi.matmul_static_bytes(self.st, m)
-        self.flops = 2 * m * n * k
+        self.bytes = ffi.matmul_static_bytes(ffi.matmul_static(n, k, scheme, x_dtype, ffi.F32, m_bucket=m), m)
         self.i = 0
 
-    def step(self):
-        w = self.ws[self.i % len(self.ws)]
-        self.i += 1
-        self.ffi.matmul(w, self.scheme, self.n, self.k, self.x, y=self.y)
+    def launch(self, i=None, stream=None):
+        if i is None:
+            i, self.i = self.i, self.i + 1
+        self.ffi.matmul(self.ws[i % len(self.ws)], self.scheme, self.n, self.k, self.x, y=self.y, stream=stream)
 
-    def timed(self, steps, warmup):
-        torch = self.torch
-        for _ in range(warmup):
-            self.step()
-        torch.cuda.synchronize()
-        stream = torch.cuda.current_stream()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        e0.record(stream)
-        for _ in range(steps):
-            self.step()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        ms = e0.elapsed_time(e1)
-        return ms / steps, wall
-
-    def graph_timed(self, reps):
-        """Per-launch time of back-to-back launches replayed from a HIP graph
-        (one launch per rotated weight copy), measured with events on the
-        launch stream."""
-        torch = self.torch
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(s):
-            for _ in range(3):
-                for w in self.ws:
-                    self.ffi.matmul(w, self.scheme, self.n, self.k, self.x, y=self.y, stream=s)
-            s.synchronize()
-            with torch.cuda.graph(g, stream=s):
-                for w in self.ws:
-                    self.ffi.matmul(w, self.scheme, self.n, self.k, self.x, y=self.y, stream=s)
-        torch.cuda.synchronize()
-        g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        cur = torch.cuda.current_stream()
-        e0.record(cur)
-        for _ in range(reps):
-            g.replay()
-        e1.record(cur)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / (reps * len(self.ws))
+    def graph_ms(self):
+        return graph_time(self.torch, lambda i, s: self.launch(i, s), len(self.ws))
 
     def cpu_baseline(self, budget_s=12.0):
-        """Scalar oracle (1 thread) on whole GEMVs until ~budget_s of CPU time."""
-        sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
         import oracle_ffi as O
 
-        n_calls, t0 = 0, time.perf_counter()
+        calls, t0 = 0, time.perf_counter()
         while True:
             O.matmul(self.scheme, self.w_host, self.n, self.k, self.x_host, self.x_dtype)
-            n_calls += 1
+            calls += 1
             el = time.perf_counter() - t0
             if el >= budget_s:
                 break
-        return self.bytes * n_calls / el / 1e9, n_calls, el
+        return self.bytes * calls / el / 1e9, calls, el
+
+
+def bench_c2(torch, ffi, synth, gsynth, steps):
+    m, n, k = 2048, 14336, 4096
+    w0 = gsynth.quant_weights_gpu(torch, ffi.Q4_K, 201, n, k)
+    ws = [w0] + [w0.clone() for _ in range(copies_for(w0.numel()) - 1)]
+    x = torch.from_numpy(synth.normal_bf16(synth.seed_for("c2", "x"), (m, k)).view(np.int16)).cuda().view(torch.bfloat16)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    st = ffi.matmul_static(n, k, ffi.Q4_K, ffi.BF16, ffi.BF16, m_bucket=m)
+    wsp = torch.empty(ffi.matmul_workspace_bytes(st), dtype=torch.uint8, device="cuda")
+    it = [0]
+
+    def step():
+        ffi.matmul(ws[it[0] % len(ws)], ffi.Q4_K, n, k, x, out_dtype=ffi.BF16, y=y, workspace=wsp)
+        it[0] += 1
+
+    ms = event_time(torch, step, steps, 3)
+    flops = 2 * m * n * k
+    out = {"workload": "configs[2]: x bf16 [2048x4096] . Q4_K [14336x4096]^T -> bf16, fp16 MFMA",
+           "ms_per_step": round(ms, 4), "tokens/s": round(m / (ms * 1e-3), 1), "flops": flops,
+           "weight_copies": len(ws)}
+    out.update(mfma(flops, ms))
+    return out
+
+
+def moe_weights(torch, gsynth, ffi, e, dm, dff, seed, copies):
+    gu = gsynth.quant_weights_gpu(torch, ffi.IQ4_XS, seed, e * 2 * dff, dm)
+    dn = gsynth.quant_weights_gpu(torch, ffi.Q4_K, seed + 1, e * dm, dff)
+    return [(gu, dn)] + [(gu.clone(), dn.clone()) for _ in range(copies - 1)]
+
+
+def bench_c3(torch, ffi, synth, gsynth, steps):
+    """MoE decode: T=5, E=512 routed + 1 shared, top-10; per step the router
+    and the FFN over freshly routed tokens (8 routing patterns rotate)."""
+    t, e, k, dm, dff, shared = 5, 512, 10, 2048, 512, 1
+    per_expert = 2 * dff * dm // 256 * 136 + dm * dff // 256 * 144
+    pats = [torch.from_numpy(synth.normal_f32(synth.seed_for("c3", f"logits{i}"), (t, e))).cuda() for i in range(8)]
+    # working set per step ~ (U+1) experts; rotate copies so it misses the Infinity Cache
+    wsets = moe_weights(torch, gsynth, ffi, e + shared, dm, dff, 301, 7)
+    x = torch.from_numpy(synth.normal_bf16(synth.seed_for("c3", "x"), (t, dm)).view(np.int16)).cuda().view(torch.bfloat16)
+    ids = torch.empty((t, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((t, k), dtype=torch.float32, device="cuda")
+    y = torch.empty((t, dm), dtype=torch.float32, device="cuda")
+    st = ffi.ffn_static(t, e, k, dm, dff, shared)
+    wsp = torch.empty(ffi.ffn_workspace_bytes(st), dtype=torch.uint8, device="cuda")
+    uniq = []
+    for p in pats:
+        ffi.moe_route(p, k, ids=ids, weights=w)
+        uniq.append(len(set(ids.cpu().numpy().reshape(-1).tolist())))
+    it = [0]
+
+    def ffn_step():
+        i = it[0]
+        it[0] += 1
+        ffi.moe_route(pats[i % len(pats)], k, ids=ids, weights=w)
+        gu, dn = wsets[i % len(wsets)]
+        ffi.moe_ffn(x, ids, w, gu, dn, e, dff, shared=shared, y=y, workspace=wsp, t_bucket=t)
+
+    ms = event_time(torch, ffn_step, steps, 10)
+    u = float(np.mean(uniq))
+    bytes_ = (u + shared) * per_expert + t * dm * 2 + t * dm * 4 + t * e * 4
+    flops = (t * k + t * shared) * (2 * 2 * dff * dm + 2 * dm * dff)
+    out = {"workload": "configs[3]: MoE decode T=5, E=512+1 shared, top-10, IQ4_XS gate/up + Q4_K down "
+                       "(route + permute + expert GEMVs + combine per step)",
+           "ms_per_step": round(ms, 4), "distinct_experts_mean": u, "bytes_per_step": int(bytes_),
+           "tokens/s": round(t / (ms * 1e-3), 1), "flops": flops, "weight_copies": len(wsets)}
+    out.update(hbm(bytes_, ms))
+    return out
+
+
+def bench_c4(torch, ffi, synth, gsynth, steps):
+    """MoE prefill: T=8192, E=512, top-10, Zipf(1.1) routing."""
+    t, e, k, dm, dff = 8192, 512, 10, 2048, 512
+    logits = torch.from_numpy(synth.zipf_logits(synth.seed_for("c4", "logits"), t, e)).cuda()
+    wsets = moe_weights(torch, gsynth, ffi, e, dm, dff, 401, 2)
+    x = torch.from_numpy(synth.normal_bf16(synth.seed_for("c4", "x"), (t, dm)).view(np.int16)).cuda().view(torch.bfloat16)
+    ids = torch.empty((t, k), dtype=torch.int32, device="cuda")
+    w = torch.empty((t, k), dtype=torch.float32, device="cuda")
+    y = torch.empty((t, dm), dtype=torch.float32, device="cuda")
+    st = ffi.ffn_static(t, e, k, dm, dff)
+    wsp = torch.empty(ffi.ffn_workspace_bytes(st), dtype=torch.uint8, device="cuda")
+    ffi.moe_route(logits, k, ids=ids, weights=w)
+    it = [0]
+
+    def ffn_step():
+        gu, dn = wsets[it[0] % len(wsets)]
+        it[0] += 1
+        ffi.moe_ffn(x, ids, w, gu, dn, e, dff, y=y, workspace=wsp)
+
+    def route_step():
+        ffi.moe_route(logits, k, ids=ids, weights=w)
+
+    ms = event_time(torch, ffn_step, steps, 2)
+    rms = event_time(torch, route_step, steps, 2)
+    flops = t * k * (2 * 2 * dff * dm + 2 * dm * dff)
+    out = {"workload": "configs[4]: MoE prefill T=8192, E=512, top-10 Zipf(1.1); permute + grouped fp16-MFMA "
+                       "gate/up+SwiGLU and down + weighted unpermute-sum to f32",
+           "ms_per_step": round(ms, 4), "tokens/s": round(t / (ms * 1e-3), 1), "flops": flops,
+           "route_ms": round(rms, 4), "route_GB/s": round(t * e * 4 / (rms * 1e-3) / 1e9, 1)}
+    out.update(mfma(flops, ms))
+    return out
+
+
+def bench_ceilings(torch, ffi):
+    """Measured ceilings of this device: 128-bit streaming reads at the
+    configs' working-set sizes (rotated copies, graph-replayed launches) and
+    an MFMA-only loop (fp16 32x32x16)."""
+    out = {}
+    for label, nbytes in (("5.6MB", 5_693_440), ("9.5MB", 9_469_952), ("84MB", 84 << 20), ("1GB", 1 << 30)):
+        nbytes -= nbytes % 16
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1) for _ in range(copies_for(nbytes))]
+        ms = graph_time(torch, lambda i, s: ffi.probe_stream(bufs[i % len(bufs)], stream=s), len(bufs), reps=10)
+        out[f"stream_{label}"] = {"us": round(ms * 1e3, 2), **hbm(nbytes, ms)}
+        del bufs
+    blocks, iters = 256 * 8, 256
+    sink = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+    ms = event_time(torch, lambda: ffi.probe_mfma(blocks, iters, sink=sink), 5, 2)
+    flops = blocks * 4 * iters * 16 * 32768
+    out["mfma_f16_32x32x16"] = {"us": round(ms * 1e3, 1), **mfma(flops, ms)}
+    return out
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU figures are out of scope "
-                                   "(--gpus must be 1)"}))
+        print(json.dumps({"error": "this build runs on one GPU only: multi-GPU figures are out of scope, "
+                                   "run with --gpus 1"}))
         return 2
     import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import gpu_synth as gsynth
 
     from r9v_amd import ffi, synth
 
@@ -146,44 +280,46 @@ def main():
         print(json.dumps({"error": "no GPU"}))
         return 1
     ffi.load()
-
-    # headline: configs[1], IQ4_XS GEMV, M = 5
-    log("setup c1 (IQ4_XS GEMV K=2048 N=5120 M=5)")
-    head = GemvBench(torch, ffi, synth, ffi.IQ4_XS, 5120, 2048, 5, ffi.BF16, "c1m5")
-    ms, wall = head.timed(args.steps, args.warmup)
-    value = head.bytes / (ms * 1e-3) / 1e9
-    g_ms = head.graph_timed(20)
-    achieved = head.bytes / (g_ms * 1e-3) / 1e9
-    log(f"c1 m5: {ms*1e3:.2f} us/step stream, {g_ms*1e3:.2f} us/launch graph -> {achieved:.0f} GB/s")
-
-    extras = {}
     only = set(filter(None, args.only.split(",")))
 
     def want(name):
         return not only or name in only
 
+    log("c1 m5: IQ4_XS GEMV K=2048 N=5120 M=5")
+    head = Gemv(torch, ffi, synth, gsynth, ffi.IQ4_XS, 5120, 2048, 5, ffi.BF16, "c1m5")
+    ms = event_time(torch, head.launch, args.steps, args.warmup)
+    value = head.bytes / (ms * 1e-3) / 1e9
+    g_ms = head.graph_ms()
+    achieved = head.bytes / (g_ms * 1e-3) / 1e9
+    log(f"  {ms * 1e3:.2f} us/step stream, {g_ms * 1e3:.2f} us/launch graph -> {achieved:.0f} GB/s")
+
+    extras = {}
     if want("c1m1"):
-        b = GemvBench(torch, ffi, synth, ffi.IQ4_XS, 5120, 2048, 1, ffi.BF16, "c1m1")
-        gm = b.graph_timed(20)
-        extras["c1_iq4xs_gemv_m1"] = {"us_per_launch": round(gm * 1e3, 3),
-                                      "GB/s": round(b.bytes / (gm * 1e-3) / 1e9, 1),
-                                      "frac_hbm": round(b.bytes / (gm * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                      "bytes": b.bytes}
+        b = Gemv(torch, ffi, synth, gsynth, ffi.IQ4_XS, 5120, 2048, 1, ffi.BF16, "c1m1")
+        gm = b.graph_ms()
+        extras["c1_iq4xs_gemv_m1"] = {"us_per_launch": round(gm * 1e3, 3), "bytes": b.bytes, **hbm(b.bytes, gm)}
         del b
     if want("c0"):
-        b = GemvBench(torch, ffi, synth, ffi.Q4_K, 4096, 4096, 1, ffi.F32, "c0")
-        gm = b.graph_timed(20)
-        extras["c0_q4k_gemv_f32"] = {"us_per_launch": round(gm * 1e3, 3),
-                                     "GB/s": round(b.bytes / (gm * 1e-3) / 1e9, 1),
-                                     "frac_hbm": round(b.bytes / (gm * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                     "bytes": b.bytes}
+        b = Gemv(torch, ffi, synth, gsynth, ffi.Q4_K, 4096, 4096, 1, ffi.F32, "c0")
+        gm = b.graph_ms()
+        extras["c0_q4k_gemv_f32"] = {"us_per_launch": round(gm * 1e3, 3), "bytes": b.bytes, **hbm(b.bytes, gm)}
         del b
+    if want("ceilings"):
+        extras["measured_ceilings"] = bench_ceilings(torch, ffi)
+        log(f"  ceilings {extras['measured_ceilings']}")
+    for name, fn, st in (("c2", bench_c2, 20), ("c3", bench_c3, 200), ("c4", bench_c4, 10)):
+        if want(name):
+            log(f"{name} ...")
+            extras[name] = fn(torch, ffi, synth, gsynth, st)
+            log(f"  {extras[name]}")
+            torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
         v, calls, el = head.cpu_baseline()
         cpu = {"value": round(v, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"{calls} full c1 M=5 GEMVs (oracle, scalar T0 Branch-D restatement) in {el:.1f} s"}
+               "sample": f"{calls} full configs[1] M=5 GEMVs by the oracle (scalar C restatement of T0 "
+                         f"Branch D, 1 thread) in {el:.1f} s"}
 
     out = {
         "metric": METRIC,
@@ -197,13 +333,14 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded SplitMix64; GGUF IQ4_XS blocks, x ~ N(0,1) bf16)",
+        "data": "synthetic: seeded GGUF IQ4_XS blocks (uniform 4-bit indices / 6-bit scales, "
+                "d = f16|N(0,0.02)|), x ~ N(0,1) bf16",
         "config": {"workload": "configs[1]: IQ4_XS dequant GEMV K=2048 N=5120 M=5, x bf16, y f32",
                    "weight_copies": len(head.ws), "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_kernel<IQ4_XS, M=5, bf16>",
-                     "bytes_per_launch": head.bytes, "us_per_launch": round(g_ms * 1e3, 3)},
+                     "kernel": "gemv_kernel<IQ4_XS, M=5, bf16>", "bytes_per_launch": head.bytes,
+                     "us_per_launch": round(g_ms * 1e3, 3)},
         "cpu_baseline": cpu,
         "extras": extras,
     }

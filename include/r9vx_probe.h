@@ -1,0 +1,31 @@
+/*
+ * r9vx_probe.h -- measured-ceiling probes of libr9vx (diagnostics; no
+ * counterpart in the reference's op surface -- the reference measured its
+ * ceilings with stand-alone spikes, spikes/dot4-gemv and spikes/wmma-l1).
+ */
+#ifndef R9VX_PROBE_H
+#define R9VX_PROBE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "r9vx.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Streams `bytes` (a multiple of 16) from `src` with 128-bit loads and writes
+ * one u32 checksum per workgroup to `sink` (>= r9vx_probe_stream_blocks()
+ * u32).  Duration / bytes is the measured HBM read ceiling. */
+int r9vx_probe_stream_launch(const void *src, uint64_t bytes, uint32_t *sink, r9vx_stream_t stream);
+uint32_t r9vx_probe_stream_blocks(uint64_t bytes);
+/* Runs `iters` dependent rounds of 16 independent v_mfma_f32_32x32x16_f16
+ * per wave on every CU (256 threads x `blocks` workgroups); writes one f32
+ * per thread to `sink`.  FLOPs = blocks * 4 waves * iters * 16 * 32768. */
+int r9vx_probe_mfma_launch(uint32_t blocks, uint32_t iters, float *sink, r9vx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

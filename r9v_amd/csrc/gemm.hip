@@ -186,6 +186,12 @@ size_t r9vx_gemm_workspace_bytes(uint32_t m_bucket, uint32_t k) {
     return (((size_t)m_bucket * k * 2 + 255) & ~(size_t)255) + (size_t)m_bucket * 4;
 }
 
+int r9vx_launch_x_to_f16(const uint16_t *x, uint32_t m, uint32_t k, _Float16 *x16, float *scale,
+                         hipStream_t stream) {
+    hipLaunchKernelGGL(x_to_f16_kernel, dim3(m), dim3(256), 0, stream, x, k, x16, scale);
+    return (int)hipGetLastError();
+}
+
 int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     _Float16 *x16 = reinterpret_cast<_Float16 *>(p.workspace);
     float *scale = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(p.workspace) +

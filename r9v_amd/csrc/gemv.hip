@@ -47,10 +47,6 @@ using namespace r9vx;
 template <int SCHEME, int M, bool XF32, int SPL>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     __shared__ uint32_t lut[256];
-    if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
-        init_iq4_lut(lut, threadIdx.x, blockDim.x);
-        __syncthreads();
-    }
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     const uint32_t lpr = 1u << a.lpr_log2;
@@ -66,20 +62,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         for (int t = 0; t < M; ++t) acc[r][t] = 0.f;
 
     for (uint32_t seg = 0; seg < a.nseg; ++seg) {
-        XChunk<SCHEME, XF32> xc[SPL][M];
         uint32_t cis[SPL];
 #pragma unroll
-        for (int s = 0; s < SPL; ++s) {
-            cis[s] = seg * lpr * SPL + s * lpr + lir;
-            uint32_t klo, khi;
-            chunk_k<SCHEME>(cis[s], klo, khi);
-#pragma unroll
-            for (int t = 0; t < M; ++t) {
-                const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.x) +
-                                    (uint64_t)t * a.x_row_stride * (XF32 ? 4 : 2);
-                load_x<SCHEME, XF32>(xb, klo, khi, xc[s][t]);
-            }
-        }
+        for (int s = 0; s < SPL; ++s) cis[s] = seg * lpr * SPL + s * lpr + lir;
+        /* 1. every weight load of this wave, first: they carry the HBM latency */
         r9vx_u32x4 qs[kRows][SPL];
         Hdr hd[kRows][SPL];
 #pragma unroll
@@ -90,6 +76,31 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int s = 0; s < SPL; ++s) load_chunk<SCHEME>(wrow, cis[s], qs[r][s], hd[r][s]);
         }
+        /* 2. every activation load, still before any wait */
+        XRaw<XF32> xr[SPL][M];
+#pragma unroll
+        for (int s = 0; s < SPL; ++s) {
+            uint32_t klo, khi;
+            chunk_k<SCHEME>(cis[s], klo, khi);
+#pragma unroll
+            for (int t = 0; t < M; ++t) {
+                const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.x) +
+                                    (uint64_t)t * a.x_row_stride * (XF32 ? 4 : 2);
+                load_x_raw<XF32>(xb, klo, khi, xr[s][t]);
+            }
+        }
+        /* 3. the codebook table is built while the loads are in flight */
+        if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
+            if (seg == 0) {
+                init_iq4_lut(lut, threadIdx.x, blockDim.x);
+                __syncthreads();
+            }
+        }
+        XChunk<SCHEME, XF32> xc[SPL][M];
+#pragma unroll
+        for (int s = 0; s < SPL; ++s)
+#pragma unroll
+            for (int t = 0; t < M; ++t) arrange_x<SCHEME, XF32>(xr[s][t], xc[s][t]);
 #pragma unroll
         for (int r = 0; r < kRows; ++r)
 #pragma unroll

@@ -266,8 +266,10 @@ struct FfnArgs {
     uint32_t dn_lpr_log2, dn_nseg;
 };
 
-constexpr int kPairs = 2; /* gate/up row pairs per lane group per wave */
-constexpr int kDnRows = 4;
+/* Rows per lane group per wave: fewer when more activation rows are live,
+ * so that the activation registers of MT rows fit without spilling. */
+constexpr int pairs_for(int mt) { return mt <= 2 ? 2 : 1; }
+constexpr int dn_rows_for(int mt) { return mt <= 2 ? 4 : 2; }
 
 __device__ __forceinline__ bool refused(const FfnArgs &a) {
     return reinterpret_cast<const uint32_t *>(a.ws + a.L.status)[0] != 0u;
@@ -281,11 +283,8 @@ __device__ __forceinline__ uint32_t token_of(const FfnArgs &a, uint32_t expert, 
 /* gate/up GEMV + SwiGLU for one work item; block = 4 waves over Dff rows. */
 template <int GU, int MT>
 __global__ __launch_bounds__(256) void moe_gu_kernel(FfnArgs a) {
+    constexpr int kPairs = pairs_for(MT);
     __shared__ uint32_t lut[256];
-    if constexpr (GU == R9VX_SCHEME_IQ4_XS) {
-        init_iq4_lut(lut, threadIdx.x, blockDim.x);
-        __syncthreads();
-    }
     const uint32_t *status = reinterpret_cast<const uint32_t *>(a.ws + a.L.status);
     if (status[0] != 0u || blockIdx.x >= status[2]) return;
     r9vx_u32x4 wk = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.work)[blockIdx.x];
@@ -297,6 +296,7 @@ __global__ __launch_bounds__(256) void moe_gu_kernel(FfnArgs a) {
     const uint32_t r0 = wave * rpi * kPairs + slot;
     const uint8_t *wexp = a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes;
     float *h = reinterpret_cast<float *>(a.ws + a.L.h);
+    bool lut_ready = false;
 
     for (uint32_t t0 = 0; t0 < cnt; t0 += MT) {
         const int m = (int)(cnt - t0 < (uint32_t)MT ? cnt - t0 : (uint32_t)MT);
@@ -312,12 +312,9 @@ __global__ __launch_bounds__(256) void moe_gu_kernel(FfnArgs a) {
 #pragma unroll
             for (int t = 0; t < MT; ++t) ag[r][t] = au[r][t] = 0.f;
         for (uint32_t seg = 0; seg < a.gu_nseg; ++seg) {
-            XChunk<GU, false> xc[MT];
             uint32_t ci = seg * lpr + lir, klo, khi;
             chunk_k<GU>(ci, klo, khi);
-#pragma unroll
-            for (int t = 0; t < MT; ++t)
-                if (t < m) load_x<GU, false>(xrow[t], klo, khi, xc[t]);
+            /* weights first, then activations, then the table: one latency */
             r9vx_u32x4 qg[kPairs], qu[kPairs];
             Hdr hg[kPairs], hu[kPairs];
 #pragma unroll
@@ -327,6 +324,21 @@ __global__ __launch_bounds__(256) void moe_gu_kernel(FfnArgs a) {
                 load_chunk<GU>(wexp + (uint64_t)rr * a.gu_row_bytes, ci, qg[r], hg[r]);
                 load_chunk<GU>(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes, ci, qu[r], hu[r]);
             }
+            XRaw<false> xr[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                if (t < m) load_x_raw<false>(xrow[t], klo, khi, xr[t]);
+            if constexpr (GU == R9VX_SCHEME_IQ4_XS) {
+                if (!lut_ready) {
+                    init_iq4_lut(lut, threadIdx.x, blockDim.x);
+                    __syncthreads();
+                    lut_ready = true;
+                }
+            }
+            XChunk<GU, false> xc[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                if (t < m) arrange_x<GU, false>(xr[t], xc[t]);
 #pragma unroll
             for (int r = 0; r < kPairs; ++r) {
                 chunk_dot<GU, false, MT>(qg[r], hg[r], ci & 7, xc, ag[r], lut, m);
@@ -353,11 +365,8 @@ __global__ __launch_bounds__(256) void moe_gu_kernel(FfnArgs a) {
 /* down GEMV for one work item: o[pos, d] = h[pos, :] . Wd[d, :]. */
 template <int DN, int MT>
 __global__ __launch_bounds__(256) void moe_down_kernel(FfnArgs a) {
+    constexpr int kDnRows = dn_rows_for(MT);
     __shared__ uint32_t lut[256];
-    if constexpr (DN == R9VX_SCHEME_IQ4_XS) {
-        init_iq4_lut(lut, threadIdx.x, blockDim.x);
-        __syncthreads();
-    }
     const uint32_t *status = reinterpret_cast<const uint32_t *>(a.ws + a.L.status);
     if (status[0] != 0u || blockIdx.x >= status[2]) return;
     r9vx_u32x4 wk = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.work)[blockIdx.x];
@@ -370,6 +379,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(FfnArgs a) {
     const uint8_t *wexp = a.w_dn + (uint64_t)expert * a.dm * a.dn_row_bytes;
     const float *h = reinterpret_cast<const float *>(a.ws + a.L.h);
     float *o = reinterpret_cast<float *>(a.ws + a.L.o);
+    bool lut_ready = false;
 
     for (uint32_t t0 = 0; t0 < cnt; t0 += MT) {
         const int m = (int)(cnt - t0 < (uint32_t)MT ? cnt - t0 : (uint32_t)MT);
@@ -379,12 +389,8 @@ __global__ __launch_bounds__(256) void moe_down_kernel(FfnArgs a) {
 #pragma unroll
             for (int t = 0; t < MT; ++t) acc[r][t] = 0.f;
         for (uint32_t seg = 0; seg < a.dn_nseg; ++seg) {
-            XChunk<DN, true> xc[MT];
             uint32_t ci = seg * lpr + lir, klo, khi;
             chunk_k<DN>(ci, klo, khi);
-#pragma unroll
-            for (int t = 0; t < MT; ++t)
-                if (t < m) load_x<DN, true>(h + (uint64_t)(beg + t0 + t) * a.dff, klo, khi, xc[t]);
             r9vx_u32x4 q[kDnRows];
             Hdr hd[kDnRows];
 #pragma unroll
@@ -393,6 +399,21 @@ __global__ __launch_bounds__(256) void moe_down_kernel(FfnArgs a) {
                 uint32_t rr = row < a.dm ? row : a.dm - 1;
                 load_chunk<DN>(wexp + (uint64_t)rr * a.dn_row_bytes, ci, q[r], hd[r]);
             }
+            XRaw<true> xr[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                if (t < m) load_x_raw<true>(h + (uint64_t)(beg + t0 + t) * a.dff, klo, khi, xr[t]);
+            if constexpr (DN == R9VX_SCHEME_IQ4_XS) {
+                if (!lut_ready) {
+                    init_iq4_lut(lut, threadIdx.x, blockDim.x);
+                    __syncthreads();
+                    lut_ready = true;
+                }
+            }
+            XChunk<DN, true> xc[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                if (t < m) arrange_x<DN, true>(xr[t], xc[t]);
 #pragma unroll
             for (int r = 0; r < kDnRows; ++r) chunk_dot<DN, true, MT>(q[r], hd[r], ci & 7, xc, acc[r], lut, m);
         }
@@ -482,8 +503,12 @@ int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream
 }
 
 template <int MT>
-static void launch_decode_mt(const FfnArgs &f, uint32_t gu_scheme, uint32_t dn_scheme, dim3 ggu, dim3 gdn,
+static void launch_decode_mt(const FfnArgs &f, uint32_t gu_scheme, uint32_t dn_scheme, uint32_t max_work,
                              hipStream_t s) {
+    const uint32_t gu_rows_per_block = 4 * (64u >> f.gu_lpr_log2) * pairs_for(MT);
+    const uint32_t dn_rows_per_block = 4 * (64u >> f.dn_lpr_log2) * dn_rows_for(MT);
+    dim3 ggu(max_work, (f.dff + gu_rows_per_block - 1) / gu_rows_per_block);
+    dim3 gdn(max_work, (f.dm + dn_rows_per_block - 1) / dn_rows_per_block);
     if (gu_scheme == R9VX_SCHEME_IQ4_XS)
         hipLaunchKernelGGL((moe_gu_kernel<R9VX_SCHEME_IQ4_XS, MT>), ggu, dim3(256), 0, s, f);
     else
@@ -515,20 +540,16 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
     f.gu_lpr_log2 = lpr_for(p.dm, f.gu_nseg);
     f.dn_lpr_log2 = lpr_for(p.dff, f.dn_nseg);
     uint32_t max_work = (f.p < p.e ? f.p : p.e) + p.shared;
-    uint32_t gu_rows_per_block = 4 * (64u >> f.gu_lpr_log2) * kPairs;
-    uint32_t dn_rows_per_block = 4 * (64u >> f.dn_lpr_log2) * kDnRows;
-    dim3 ggu(max_work, (p.dff + gu_rows_per_block - 1) / gu_rows_per_block);
-    dim3 gdn(max_work, (p.dm + dn_rows_per_block - 1) / dn_rows_per_block);
-    uint32_t mt = p.t < 8 ? p.t : 8;
+    uint32_t mt = p.t < 4 ? p.t : 4; /* larger t runs in groups of 4 rows */
     switch (mt) {
-    case 1: launch_decode_mt<1>(f, p.scheme_gu, p.scheme_dn, ggu, gdn, s); break;
-    case 2: launch_decode_mt<2>(f, p.scheme_gu, p.scheme_dn, ggu, gdn, s); break;
-    case 3: launch_decode_mt<3>(f, p.scheme_gu, p.scheme_dn, ggu, gdn, s); break;
-    case 4: launch_decode_mt<4>(f, p.scheme_gu, p.scheme_dn, ggu, gdn, s); break;
-    case 5: launch_decode_mt<5>(f, p.scheme_gu, p.scheme_dn, ggu, gdn, s); break;
-    case 6: launch_decode_mt<6>(f, p.scheme_gu, p.scheme_dn, ggu, gdn, s); break;
-    case 7: launch_decode_mt<7>(f, p.scheme_gu, p.scheme_dn, ggu, gdn, s); break;
-    default: launch_decode_mt<8>(f, p.scheme_gu, p.scheme_dn, ggu, gdn, s); break;
+    case 1: launch_decode_mt<1>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
+    case 2: launch_decode_mt<2>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
+    case 3: launch_decode_mt<3>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
+    case 4: launch_decode_mt<4>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
+    case 5: launch_decode_mt<5>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
+    case 6: launch_decode_mt<6>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
+    case 7: launch_decode_mt<7>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
+    default: launch_decode_mt<8>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
     }
     return (int)hipGetLastError();
 }

@@ -1,0 +1,78 @@
+/*
+ * probe.hip -- ceilings measured on the device itself: a 128-bit streaming
+ * read over a buffer and an MFMA-only loop (the MI355X counterpart of the
+ * reference's spikes/dot4-gemv and spikes/wmma-l1 measurements).
+ */
+#include "r9vx_device.h"
+#include "r9vx_probe.h"
+
+namespace {
+
+constexpr uint32_t kStreamThreads = 256;
+constexpr uint32_t kStreamPerThread = 8; /* 16-byte loads per thread, all issued before use */
+
+__global__ __launch_bounds__(256) void stream_kernel(const r9vx_u32x4 *__restrict__ src, uint64_t n16,
+                                                     uint32_t *__restrict__ sink) {
+    const uint64_t base = (uint64_t)blockIdx.x * kStreamThreads * kStreamPerThread + threadIdx.x;
+    r9vx_u32x4 v[kStreamPerThread];
+#pragma unroll
+    for (uint32_t i = 0; i < kStreamPerThread; ++i) {
+        uint64_t j = base + (uint64_t)i * kStreamThreads;
+        v[i] = j < n16 ? __builtin_nontemporal_load(src + j) : r9vx_u32x4{0u, 0u, 0u, 0u};
+    }
+    uint32_t x = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < kStreamPerThread; ++i) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    for (int off = 32; off > 0; off >>= 1) x ^= __shfl_xor(x, off, 64);
+    if (threadIdx.x == 0) sink[blockIdx.x] = x;
+}
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+
+__global__ __launch_bounds__(256) void mfma_kernel(uint32_t iters, float *sink) {
+    half8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (_Float16)(0.001f * (threadIdx.x + i));
+        b[i] = (_Float16)(0.002f * (blockIdx.x + i));
+    }
+    r9vx_f32x16 acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+    for (uint32_t it = 0; it < iters; ++it)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[j], 0, 0, 0);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += acc[j][r];
+    sink[(uint64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t r9vx_probe_stream_blocks(uint64_t bytes) {
+    uint64_t n16 = bytes / 16;
+    return (uint32_t)((n16 + kStreamThreads * kStreamPerThread - 1) / (kStreamThreads * kStreamPerThread));
+}
+
+int r9vx_probe_stream_launch(const void *src, uint64_t bytes, uint32_t *sink, r9vx_stream_t stream) {
+    if (!src || !sink || bytes % 16 || ((uintptr_t)src & 15)) return R9VX_ERR_INVALID;
+    hipLaunchKernelGGL(stream_kernel, dim3(r9vx_probe_stream_blocks(bytes)), dim3(kStreamThreads), 0,
+                       reinterpret_cast<hipStream_t>(stream), reinterpret_cast<const r9vx_u32x4 *>(src), bytes / 16,
+                       sink);
+    return (int)hipGetLastError();
+}
+
+int r9vx_probe_mfma_launch(uint32_t blocks, uint32_t iters, float *sink, r9vx_stream_t stream) {
+    if (!sink || blocks == 0) return R9VX_ERR_INVALID;
+    hipLaunchKernelGGL(mfma_kernel, dim3(blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), iters, sink);
+    return (int)hipGetLastError();
+}
+
+}  // extern "C"

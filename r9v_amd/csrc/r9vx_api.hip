@@ -369,7 +369,7 @@ int r9vx_launch_moe(const r9vx_moe_problem &p, hipStream_t s) {
     MoeLayout L = r9vx_moe_layout(p.t_bucket, p.e, p.k, p.dm, p.dff, p.shared);
     int rc = r9vx_moe_sort_stage(p, L, s);
     if (rc) return rc;
-    rc = r9vx_moe_decode_stage(p, L, s);
+    rc = p.t <= 8 ? r9vx_moe_decode_stage(p, L, s) : r9vx_moe_grouped_stage(p, L, s);
     if (rc) return rc;
     return r9vx_moe_combine_stage(p, L, s);
 }

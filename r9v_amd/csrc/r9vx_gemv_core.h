@@ -28,8 +28,10 @@ struct XChunk<SCHEME, false> {
 
 template <int SCHEME>
 struct XChunk<SCHEME, true> {
-    float lo[16], hi[16];
+    r9vx_f32x4 v[8]; /* v[0..3]: low-nibble positions, v[4..7]: high */
     float slo, shi;
+    __device__ __forceinline__ float lo(int i) const { return v[i >> 2][i & 3]; }
+    __device__ __forceinline__ float hi(int i) const { return v[4 + (i >> 2)][i & 3]; }
 };
 
 /* K offset of byte 0 low nibble / high nibble of chunk ci. */
@@ -45,37 +47,58 @@ __device__ __forceinline__ void chunk_k(uint32_t ci, uint32_t &klo, uint32_t &kh
     }
 }
 
-template <int SCHEME, bool XF32>
-__device__ __forceinline__ void load_x(const void *xbase, uint32_t klo, uint32_t khi,
-                                       XChunk<SCHEME, XF32> &xc) {
+/* Raw activation bytes of one chunk for one row: the 16 low- and 16
+ * high-nibble K positions (bf16: 2 x 32 bytes, f32: 2 x 64 bytes). */
+template <bool XF32>
+struct XRaw;
+template <>
+struct XRaw<false> {
+    r9vx_u32x4 v[4];
+};
+template <>
+struct XRaw<true> {
+    r9vx_f32x4 v[8];
+};
+
+template <bool XF32>
+__device__ __forceinline__ void load_x_raw(const void *xbase, uint32_t klo, uint32_t khi, XRaw<XF32> &r) {
     if constexpr (XF32) {
-        const float *x = reinterpret_cast<const float *>(xbase);
-        const r9vx_f32x4 *l4 = reinterpret_cast<const r9vx_f32x4 *>(x + klo);
-        const r9vx_f32x4 *h4 = reinterpret_cast<const r9vx_f32x4 *>(x + khi);
+        const r9vx_f32x4 *l4 = reinterpret_cast<const r9vx_f32x4 *>(reinterpret_cast<const float *>(xbase) + klo);
+        const r9vx_f32x4 *h4 = reinterpret_cast<const r9vx_f32x4 *>(reinterpret_cast<const float *>(xbase) + khi);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r.v[i] = l4[i];
+            r.v[4 + i] = h4[i];
+        }
+    } else {
+        const r9vx_u32x4 *l4 = reinterpret_cast<const r9vx_u32x4 *>(reinterpret_cast<const uint16_t *>(xbase) + klo);
+        const r9vx_u32x4 *h4 = reinterpret_cast<const r9vx_u32x4 *>(reinterpret_cast<const uint16_t *>(xbase) + khi);
+        r.v[0] = l4[0];
+        r.v[1] = l4[1];
+        r.v[2] = h4[0];
+        r.v[3] = h4[1];
+    }
+}
+
+template <int SCHEME, bool XF32>
+__device__ __forceinline__ void arrange_x(const XRaw<XF32> &r, XChunk<SCHEME, XF32> &xc) {
+    if constexpr (XF32) {
         float slo = 0.f, shi = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            r9vx_f32x4 a = l4[i], b = h4[i];
-            xc.lo[4 * i] = a.x; xc.lo[4 * i + 1] = a.y; xc.lo[4 * i + 2] = a.z; xc.lo[4 * i + 3] = a.w;
-            xc.hi[4 * i] = b.x; xc.hi[4 * i + 1] = b.y; xc.hi[4 * i + 2] = b.z; xc.hi[4 * i + 3] = b.w;
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            slo += xc.lo[i];
-            shi += xc.hi[i];
+            xc.v[i] = r.v[i];
+            xc.v[4 + i] = r.v[4 + i];
+            slo += (r.v[i].x + r.v[i].y) + (r.v[i].z + r.v[i].w);
+            shi += (r.v[4 + i].x + r.v[4 + i].y) + (r.v[4 + i].z + r.v[4 + i].w);
         }
         xc.slo = slo;
         xc.shi = shi;
     } else {
-        const uint16_t *x = reinterpret_cast<const uint16_t *>(xbase);
-        const r9vx_u32x4 *l4 = reinterpret_cast<const r9vx_u32x4 *>(x + klo);
-        const r9vx_u32x4 *h4 = reinterpret_cast<const r9vx_u32x4 *>(x + khi);
         uint32_t L[8], H[8];
-        r9vx_u32x4 a0 = l4[0], a1 = l4[1], b0 = h4[0], b1 = h4[1];
-        L[0] = a0.x; L[1] = a0.y; L[2] = a0.z; L[3] = a0.w;
-        L[4] = a1.x; L[5] = a1.y; L[6] = a1.z; L[7] = a1.w;
-        H[0] = b0.x; H[1] = b0.y; H[2] = b0.z; H[3] = b0.w;
-        H[4] = b1.x; H[5] = b1.y; H[6] = b1.z; H[7] = b1.w;
+        L[0] = r.v[0].x; L[1] = r.v[0].y; L[2] = r.v[0].z; L[3] = r.v[0].w;
+        L[4] = r.v[1].x; L[5] = r.v[1].y; L[6] = r.v[1].z; L[7] = r.v[1].w;
+        H[0] = r.v[2].x; H[1] = r.v[2].y; H[2] = r.v[2].z; H[3] = r.v[2].w;
+        H[4] = r.v[3].x; H[5] = r.v[3].y; H[6] = r.v[3].z; H[7] = r.v[3].w;
         float slo = 0.f, shi = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -104,6 +127,13 @@ __device__ __forceinline__ void load_x(const void *xbase, uint32_t klo, uint32_t
             }
         }
     }
+}
+
+template <int SCHEME, bool XF32>
+__device__ __forceinline__ void load_x(const void *xbase, uint32_t klo, uint32_t khi, XChunk<SCHEME, XF32> &xc) {
+    XRaw<XF32> r;
+    load_x_raw<XF32>(xbase, klo, khi, r);
+    arrange_x<SCHEME, XF32>(r, xc);
 }
 
 /* Block header of the chunk's super-block. */
@@ -150,8 +180,8 @@ __device__ __forceinline__ void chunk_dot(const r9vx_u32x4 &qs, const Hdr &h, ui
                     uint32_t lo4 = q[dw] & 0x0F0F0F0Fu, hi4 = (q[dw] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        dlo = fmaf((float)((lo4 >> (8 * i)) & 0xFF), xc[t].lo[4 * dw + i], dlo);
-                        dhi = fmaf((float)((hi4 >> (8 * i)) & 0xFF), xc[t].hi[4 * dw + i], dhi);
+                        dlo = fmaf((float)((lo4 >> (8 * i)) & 0xFF), xc[t].lo(4 * dw + i), dlo);
+                        dhi = fmaf((float)((hi4 >> (8 * i)) & 0xFF), xc[t].hi(4 * dw + i), dhi);
                     }
                 }
                 acc[t] += dl0 * dlo + dl1 * dhi - (ml0 * xc[t].slo + ml1 * xc[t].shi);
@@ -194,8 +224,8 @@ __device__ __forceinline__ void chunk_dot(const r9vx_u32x4 &qs, const Hdr &h, ui
             if constexpr (XF32) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    s = fmaf(__builtin_bit_cast(float, lv[i] << 16), xc[t].lo[i], s);
-                    s = fmaf(__builtin_bit_cast(float, lv[i] & 0xFFFF0000u), xc[t].hi[i], s);
+                    s = fmaf(__builtin_bit_cast(float, lv[i] << 16), xc[t].lo(i), s);
+                    s = fmaf(__builtin_bit_cast(float, lv[i] & 0xFFFF0000u), xc[t].hi(i), s);
                 }
             } else {
 #pragma unroll

@@ -140,4 +140,8 @@ __device__ __forceinline__ int row_shift(float maxabs) {
 
 }  // namespace r9vx
 
+/* bf16 rows -> fp16 rows with a per-row power-of-two scale (gemm.hip). */
+int r9vx_launch_x_to_f16(const uint16_t *x, uint32_t m, uint32_t k, _Float16 *x16, float *scale,
+                         hipStream_t stream);
+
 #endif

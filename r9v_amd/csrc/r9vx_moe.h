@@ -15,6 +15,8 @@
  *   tiles   u32x4[...] grouped-GEMM tile schedule
  *   h       f32[(P + S*T) * Dff]  SwiGLU rows in sorted order, shared rows after
  *   o       f32[(P + S*T) * Dm]   expert output rows in the same order
+ *   hmax    u32[P + S*T]          bits of max|h| per row (grouped GEMM)
+ *   x16     fp16[T * Dm], xscale f32[T]  scaled activations (grouped GEMM)
  */
 #ifndef R9VX_MOE_H
 #define R9VX_MOE_H
@@ -29,7 +31,8 @@ constexpr uint32_t kMoeMaxK = 32;
 constexpr uint32_t kMoeTileM = 128; /* grouped-GEMM rows per tile */
 
 struct MoeLayout {
-    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, work, tiles, h, o, total;
+    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, work, tiles, h, o, hmax, x16, xscale,
+        total;
     uint32_t max_tiles;
 };
 
@@ -45,7 +48,7 @@ inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint
         off += (bytes + 255) & ~255ull;
         return at;
     };
-    L.max_tiles = (uint32_t)(p / kMoeTileM + e + shared + 1);
+    L.max_tiles = (uint32_t)((p + (uint64_t)shared * t_bucket) / kMoeTileM + e + shared + 1);
     L.status = take(64);
     L.counts = take(4ull * e);
     L.offsets = take(4ull * (e + 1));
@@ -58,6 +61,9 @@ inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint
     L.tiles = take(16ull * L.max_tiles + 16);
     L.h = take(4ull * rows * dff);
     L.o = take(4ull * rows * dm);
+    L.hmax = take(4ull * rows);
+    L.x16 = take(2ull * t_bucket * dm);
+    L.xscale = take(4ull * t_bucket);
     L.total = off;
     return L;
 }

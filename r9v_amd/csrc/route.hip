@@ -17,7 +17,7 @@
  * Refusal before mutation (:313-418): a check pass flags non-finite logits,
  * bias or post-bias scores, and a zero selected sum under sigmoid
  * renormalisation, in a device status word; the compute pass writes nothing
- * when the word is set.  Small T runs both passes in one workgroup.
+ * when the word is set.  T <= 8 runs both passes in one workgroup, one wave per row.
  */
 #include "r9vx_device.h"
 #include "r9vx_expf.h"
@@ -84,8 +84,28 @@ __device__ uint32_t check_row(const RouteArgs &a, uint32_t row, uint32_t lane) {
     return bad;
 }
 
-/* Per-wave LDS: the E softmax numerators for the sequential sum. */
-__device__ void route_row(const RouteArgs &a, uint32_t row, uint32_t lane, float *vbuf) {
+/* sum_{c=0}^{E-1} v[c] in ascending c with one f32 accumulator, v[c] held by
+ * lane c % 64 in register c / 64.  Every lane runs the same chain: each term
+ * is broadcast with readlane, so the order and the roundings are exactly the
+ * reference's sequential loop. */
+__device__ __forceinline__ float ordered_sum(const float (&v)[kMaxPerLane], uint32_t e) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i) {
+        if ((uint32_t)(64 * i) >= e) break;
+        const int bits = __builtin_bit_cast(int, v[i]);
+        if ((uint32_t)(64 * i + 64) <= e) {
+#pragma unroll
+            for (int l = 0; l < 64; ++l) sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, l));
+        } else {
+            for (uint32_t l = 0; l < e - 64 * i; ++l)
+                sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, (int)l));
+        }
+    }
+    return sum;
+}
+
+__device__ void route_row(const RouteArgs &a, uint32_t row, uint32_t lane) {
     const uint32_t per = (a.e + 63) / 64;
     float sc[kMaxPerLane];
 #pragma unroll
@@ -106,20 +126,9 @@ __device__ void route_row(const RouteArgs &a, uint32_t row, uint32_t lane, float
 #pragma unroll
         for (int i = 0; i < kMaxPerLane; ++i) {
             uint32_t c = lane + 64 * i;
-            if (i < (int)per && c < a.e) {
-                float d = sc[i] - mx;
-                sc[i] = r9vx_expf(d);
-                vbuf[c] = sc[i];
-            }
+            sc[i] = (i < (int)per && c < a.e) ? r9vx_expf(sc[i] - mx) : 0.0f;
         }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        float sum = 0.0f;
-        if (lane == 0) {
-            for (uint32_t c = 0; c < a.e; ++c) sum = sum + vbuf[c];
-        }
-        sum = __shfl(sum, 0, 64);
+        const float sum = ordered_sum(sc, a.e);
 #pragma unroll
         for (int i = 0; i < kMaxPerLane; ++i) {
             uint32_t c = lane + 64 * i;
@@ -180,17 +189,15 @@ __global__ __launch_bounds__(256) void route_check_kernel(RouteArgs a) {
 
 /* Grid-wide form: runs after route_check_kernel. */
 __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
-    __shared__ float vbuf[4][1024];
     uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     uint32_t row = blockIdx.x * 4 + wv;
     if (row >= a.t) return;
     if (__atomic_load_n(&g_route_status, __ATOMIC_RELAXED) != 0u) return;
-    route_row(a, row, lane, vbuf[wv]);
+    route_row(a, row, lane);
 }
 
 /* Single-workgroup form for small T: check every row, then compute. */
 __global__ __launch_bounds__(512) void route_small_kernel(RouteArgs a) {
-    __shared__ float vbuf[8][1024];
     __shared__ uint32_t bad_all;
     uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
     if (threadIdx.x == 0) bad_all = 0;
@@ -203,15 +210,15 @@ __global__ __launch_bounds__(512) void route_small_kernel(RouteArgs a) {
     uint32_t bad = bad_all;
     if (threadIdx.x == 0) g_route_status = bad;
     if (bad) return;
-    for (uint32_t row = wv; row < a.t; row += nw) route_row(a, row, lane, vbuf[wv]);
+    for (uint32_t row = wv; row < a.t; row += nw) route_row(a, row, lane);
 }
 
 }  // namespace
 
 int r9vx_launch_route(const r9vx_route_problem &p, hipStream_t stream) {
     RouteArgs a{p.logits, p.bias, p.ids, p.weights, p.t, p.e, p.k, p.scoring, p.renormalize, p.scale};
-    if (p.t <= 64) {
-        uint32_t waves = p.t < 8 ? p.t : 8;
+    if (p.t <= 8) {
+        uint32_t waves = p.t;
         hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(64 * waves), 0, stream, a);
         return (int)hipGetLastError();
     }

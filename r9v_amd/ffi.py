@@ -84,6 +84,10 @@ EXPORTS = [
     ("r9vx_validate_weights_launch", [_U32, _P, _U32, _U32, _P, _P], ctypes.c_int),
     ("r9vx_last_error", [], ctypes.c_char_p),
     ("r9vx_abi_version", [], _U32),
+    # include/r9vx_probe.h
+    ("r9vx_probe_stream_launch", [_P, ctypes.c_uint64, _P, _P], ctypes.c_int),
+    ("r9vx_probe_stream_blocks", [ctypes.c_uint64], _U32),
+    ("r9vx_probe_mfma_launch", [_U32, _U32, _P, _P], ctypes.c_int),
 ]
 
 _lib = None
@@ -273,3 +277,22 @@ def moe_sort(ids, e, dm=256, dff=256, workspace=None, stream=None):
     _check(load().r9vx_moe_sort_launch(ctypes.byref(st), _ptr(ids), t, _ptr(workspace), _ptr(counts),
                                        _ptr(offsets), _ptr(order), _stream(torch, stream)))
     return counts, offsets, order
+
+
+# ---------------------------------------------------------------- ceilings
+
+def probe_stream(src, stream=None):
+    """Streams src (a device tensor) once; returns the sink tensor."""
+    torch = _need_gpu(src)
+    nbytes = src.numel() * src.element_size()
+    sink = torch.empty(load().r9vx_probe_stream_blocks(nbytes), dtype=torch.int32, device=src.device)
+    _check(load().r9vx_probe_stream_launch(_ptr(src), nbytes, _ptr(sink), _stream(torch, stream)))
+    return sink
+
+
+def probe_mfma(blocks, iters, sink=None, stream=None):
+    torch = _need_gpu(sink)
+    if sink is None:
+        sink = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+    _check(load().r9vx_probe_mfma_launch(blocks, iters, _ptr(sink), _stream(torch, stream)))
+    return sink

@@ -13,12 +13,14 @@ import pytest
 from r9v_amd import ffi
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
-HEADER = ROOT / "include" / "r9vx.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def declared_functions():
-    text = HEADER.read_text()
-    return sorted(set(re.findall(r"^[a-z_0-9 *]*?\b(r9vx_[a-z_0-9]+)\s*\(", text, flags=re.M)))
+    names = set()
+    for h in HEADERS:
+        names |= set(re.findall(r"^[a-z_0-9 *]*?\b(r9vx_[a-z_0-9]+)\s*\(", h.read_text(), flags=re.M))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():

@@ -110,7 +110,8 @@ def test_gemv_epilogues_and_bf16_out():
     got, ref = _gemv_case(O.Q4_K, 96, 512, 4, O.BF16, seed=5001, residual=True)
     check_close(got, ref, "residual")
     got, ref = _gemv_case(O.Q4_K, 96, 512, 2, O.BF16, out_dtype=O.BF16, seed=5002)
-    check_bf16_out(got, ref, "bf16 out")
+    got32, _ = _gemv_case(O.Q4_K, 96, 512, 2, O.BF16, out_dtype=O.F32, seed=5002)
+    check_bf16_out(got, got32, ref, "bf16 out")
 
 
 def test_gemv_batch_invariance():
@@ -139,7 +140,8 @@ def test_matmul_refusals():
 
 # ---------------------------------------------------------------- MFMA GEMM
 
-def _gemm_case(scheme, n, k, m, seed, out_dtype=O.F32, bias=False, residual=False, rows=None, cols=None):
+def _gemm_case(scheme, n, k, m, seed, out_dtype=O.F32, bias=False, residual=False, rows=None, cols=None,
+               oracle=True):
     """Full GPU GEMM; oracle on the sampled rows/cols (all when None)."""
     w = synth.quant_weights(scheme, seed + 1, n, k)
     x = synth.normal_bf16(seed + 2, (m, k))
@@ -150,6 +152,8 @@ def _gemm_case(scheme, n, k, m, seed, out_dtype=O.F32, bias=False, residual=Fals
     got = host(y.float())
     rows = np.arange(m) if rows is None else np.asarray(rows)
     cols = np.arange(n) if cols is None else np.asarray(cols)
+    if not oracle:
+        return got[np.ix_(rows, cols)], None
     ref = O.matmul(scheme, np.ascontiguousarray(w[cols]), len(cols), k, np.ascontiguousarray(x[rows]), O.BF16,
                    bias=None if b is None else np.ascontiguousarray(b[cols]),
                    residual=None if r is None else np.ascontiguousarray(r[np.ix_(rows, cols)]))
@@ -163,7 +167,8 @@ def test_gemm_config2_sampled():
     rows = np.unique(np.concatenate([np.arange(0, m, 97), [0, 1, 255, 256, 1023, 2047]]))
     cols = np.unique(np.concatenate([np.arange(0, n, 11)[:1500], [0, 255, 256, 14335, 7000]]))
     got, ref = _gemm_case(O.Q4_K, n, k, m, 7000, out_dtype=O.BF16, rows=rows, cols=cols)
-    check_bf16_out(got, ref, "config2 sampled")
+    got32, _ = _gemm_case(O.Q4_K, n, k, m, 7000, out_dtype=O.F32, rows=rows, cols=cols, oracle=False)
+    check_bf16_out(got, got32, ref, "config2 sampled")
 
 
 @pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])
@@ -179,7 +184,8 @@ def test_gemm_epilogues_bf16_out():
     got, ref = _gemm_case(O.Q4_K, 200, 512, 40, 7201, residual=True)
     check_close(got, ref, "residual")
     got, ref = _gemm_case(O.Q4_K, 300, 1024, 70, 7202, out_dtype=O.BF16)
-    check_bf16_out(got, ref, "bf16 out")
+    got32, _ = _gemm_case(O.Q4_K, 300, 1024, 70, 7202, out_dtype=O.F32, oracle=False)
+    check_bf16_out(got, got32, ref, "bf16 out")
 
 
 def test_gemm_row_permutation_invariance_full_size():

@@ -186,3 +186,87 @@ def test_moe_ffn_token_permutation_invariance():
     y, _, _ = ffi.moe_ffn(bf16_dev(x), dev(ids.view(np.int32)), dev(w), dev(gu), dev(dn), e, dff)
     yp, _, _ = ffi.moe_ffn(bf16_dev(x[perm]), dev(ids[perm].view(np.int32)), dev(w[perm]), dev(gu), dev(dn), e, dff)
     assert np.array_equal(host(yp), host(y)[perm])
+
+
+# ---------------------------------------------------------------- prefill (grouped MFMA)
+
+def _expert_slices(gu, dn, experts, e, dm, dff):
+    """Host copies of the given experts' blocks, re-stacked as experts 0..n-1."""
+    gu_r = gu.view(e, 2 * dff, -1)
+    dn_r = dn.view(e, dm, -1)
+    idx = torch.tensor(experts, dtype=torch.long, device=gu.device)
+    return host(gu_r.index_select(0, idx).reshape(len(experts) * 2 * dff, -1)), \
+        host(dn_r.index_select(0, idx).reshape(len(experts) * dm, -1))
+
+
+def _sampled_oracle(x, ids, w, gu, dn, e, dm, dff, tokens, shared=0):
+    """Oracle on a token subset: a token's output depends only on its own row
+    and routing, so the sub-batch reproduces the full batch's rows."""
+    sub_ids = ids[tokens]
+    experts = sorted(set(int(v) for v in sub_ids.reshape(-1)))
+    remap = {ex: i for i, ex in enumerate(experts)}
+    local = np.vectorize(remap.get)(sub_ids).astype(np.uint32)
+    all_experts = experts + list(range(e, e + shared))
+    gu_h, dn_h = _expert_slices(gu, dn, all_experts, e + shared, dm, dff)
+    return O.moe_ffn(np.ascontiguousarray(x[tokens]), O.BF16, local, np.ascontiguousarray(w[tokens]),
+                     len(experts), dff, gu_h, dn_h, shared=shared)
+
+
+def test_moe_ffn_config4_prefill_sampled():
+    """8192 tokens, hidden 2048, 512 experts, top-10 over
+    Zipf(1.1) logits; full GPU run (route -> permute -> grouped GEMMs ->
+    combine); oracle on 40 tokens spanning head and tail experts."""
+    import gpu_synth
+    t, e, k, dm, dff = 8192, 512, 10, 2048, 512
+    logits = synth.zipf_logits(synth.seed_for("c4", "logits"), t, e)
+    ids_d, w_d = ffi.moe_route(dev(logits), k)
+    ids, w = host(ids_d).view(np.uint32), host(w_d)
+    gu = gpu_synth.quant_weights_gpu(torch, O.IQ4_XS, 41, e * 2 * dff, dm)
+    dn = gpu_synth.quant_weights_gpu(torch, O.Q4_K, 42, e * dm, dff)
+    x = synth.normal_bf16(synth.seed_for("c4", "x"), (t, dm))
+    y, ws, st = ffi.moe_ffn(bf16_dev(x), ids_d, w_d, gu, dn, e, dff)
+    torch.cuda.synchronize()
+    assert ffi.moe_ffn_status(st, ws) == 0
+    counts = np.bincount(ids.reshape(-1), minlength=e)
+    tail = np.where((counts > 0) & (counts < 20))[0]
+    tok_tail = [int(np.where((ids == ex).any(1))[0][0]) for ex in tail[:12]]
+    tokens = sorted(set([0, 1, 127, 128, 4095, 8191] + list(range(300, 8192, 401)) + tok_tail))
+    ref = _sampled_oracle(x, ids, w, gu, dn, e, dm, dff, tokens)
+    check_close(host(y)[tokens], ref, "config4 sampled")
+
+
+@pytest.mark.parametrize("t,e,k,dm,dff,shared,gu_s,dn_s", [
+    (9, 8, 2, 256, 256, 0, O.IQ4_XS, O.Q4_K),
+    (130, 16, 4, 512, 256, 1, O.IQ4_XS, O.Q4_K),
+    (300, 64, 6, 256, 512, 2, O.Q4_K, O.IQ4_XS),
+    (257, 4, 3, 768, 256, 0, O.Q4_K, O.Q4_K),
+])
+def test_moe_ffn_prefill_shapes(t, e, k, dm, dff, shared, gu_s, dn_s):
+    logits = synth.zipf_logits(1400 + t, t, e)
+    ids, w = O.moe_route(logits, k)
+    gu = synth.quant_weights(gu_s, 1401 + t, (e + shared) * 2 * dff, dm)
+    dn = synth.quant_weights(dn_s, 1402 + t, (e + shared) * dm, dff)
+    x = synth.normal_bf16(1403 + t, (t, dm))
+    ref = O.moe_ffn(x, O.BF16, ids, w, e, dff, gu, dn, scheme_gu=gu_s, scheme_dn=dn_s, shared=shared)
+    y, ws, st = ffi.moe_ffn(bf16_dev(x), dev(ids.view(np.int32)), dev(w), dev(gu), dev(dn), e, dff,
+                            shared=shared, gate_up_scheme=gu_s, down_scheme=dn_s)
+    torch.cuda.synchronize()
+    assert ffi.moe_ffn_status(st, ws) == 0
+    check_close(host(y), ref, f"prefill t={t} e={e}")
+
+
+def test_moe_ffn_prefill_permutation_invariance_full_size():
+    """Permuting the 8192 tokens of configs[4] permutes y bit for bit (rows
+    keep their K order wherever they land in the expert tiles)."""
+    import gpu_synth
+    t, e, k, dm, dff = 8192, 512, 10, 2048, 512
+    logits = synth.zipf_logits(1501, t, e)
+    ids_d, w_d = ffi.moe_route(dev(logits), k)
+    gu = gpu_synth.quant_weights_gpu(torch, O.IQ4_XS, 51, e * 2 * dff, dm)
+    dn = gpu_synth.quant_weights_gpu(torch, O.Q4_K, 52, e * dm, dff)
+    x = bf16_dev(synth.normal_bf16(1502, (t, dm)))
+    y, ws, st = ffi.moe_ffn(x, ids_d, w_d, gu, dn, e, dff)
+    perm = torch.from_numpy(np.random.default_rng(9).permutation(t)).cuda()
+    yp, _, _ = ffi.moe_ffn(x[perm].contiguous(), ids_d[perm].contiguous(), w_d[perm].contiguous(), gu, dn, e,
+                           dff, workspace=ws)
+    assert torch.equal(yp, y[perm])

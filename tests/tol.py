@@ -18,17 +18,22 @@ def check_close(got, ref, what=""):
     return float((err / np.maximum(np.max(np.abs(ref)), 1e-30)).max())
 
 
-def check_bf16_out(got_bf16_as_f32, ref_f32, what=""):
-    """bf16 outputs: T0 writes bf16(acc) (dtype.rs:102-111).  Two f32 results
-    within tolerance can round to neighbouring bf16 values (one bf16 ulp is
-    2^-8 relative, above the 2e-3 relative term), so the GPU's bf16 output is
-    checked against the oracle's f32 accumulator: |bf16(g) - r| <= 2^-9 |g| +
-    |g - r| fits the same bound.  Most outputs must also be bit-identical to
-    the oracle's own bf16 rounding."""
+def check_bf16_out(got_bf16_as_f32, got_f32, ref_f32, what=""):
+    """bf16 outputs.  T0 writes bf16(acc) (crates/r9v-t0/src/dtype.rs:102-111)
+    and one bf16 ulp (2^-8 relative) is larger than the 2e-3 relative term,
+    so the tolerance is applied where it is meaningful: the kernel's f32
+    accumulator (the same launch with an f32 output) must be within tolerance
+    of the oracle's f32 accumulator, and the bf16 output must be exactly the
+    round-to-nearest-even of that accumulator.  The fraction of bf16 outputs
+    equal to the oracle's own bf16 is returned (only rounding-boundary
+    straddles differ)."""
     from r9v_amd import synth
 
-    check_close(got_bf16_as_f32, ref_f32, what)
+    check_close(got_f32, ref_f32, what)
+    want = synth.bf16_bits_to_f32(synth.to_bf16_bits(np.asarray(got_f32, dtype=np.float32)))
+    assert np.array_equal(np.asarray(got_bf16_as_f32, dtype=np.float32).view(np.uint32), want.view(np.uint32)), \
+        f"{what}: bf16 output is not the RNE of the f32 accumulator"
     ref16 = synth.bf16_bits_to_f32(synth.to_bf16_bits(ref_f32))
     same = float(np.mean(np.asarray(got_bf16_as_f32, dtype=np.float32) == ref16))
-    assert same >= 0.9, f"{what}: only {same:.3f} of bf16 outputs equal the oracle's bf16"
+    assert same >= 0.8, f"{what}: only {same:.3f} of bf16 outputs equal the oracle's bf16"
     return same
