@@ -18,7 +18,7 @@
  *     contiguous band of weight columns: the 8 M-tiles that reuse a weight
  *     tile run on the same XCD and hit its L2.
  */
-#include "r9vx_mfma.h"
+#include "r9vx_mma.h"
 
 using namespace r9vx;
 
@@ -72,100 +72,43 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t *__restric
     }
 }
 
-template <int SCHEME>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][kStageHalfs * 2];
+template <int SCHEME, int BM, int NBUF>
+__global__ __launch_bounds__(256, NBUF == 1 ? 2 : 1) void gemm_kernel(GemmArgs a) {
+    using S = MmaShape<BM, NBUF>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t wm = wave & 1, wn = wave >> 1;
 
-    /* XCD-aware tile order: workgroup b runs on XCD b % 8. */
+    /* XCD-aware tile order: workgroup b runs on XCD b % 8; each XCD takes a
+     * contiguous band of weight columns so the M tiles sharing a weight tile
+     * hit the same L2. */
     const uint32_t total = a.m_tiles * a.n_tiles;
     uint32_t t = blockIdx.x;
     if (total % 8 == 0) t = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
     const uint32_t n_tile = t / a.m_tiles, m_tile = t % a.m_tiles;
-    const uint32_t m0 = m_tile * kTileM, n0 = n_tile * kTileN;
-    const uint32_t kt_n = a.k / kTileK;
+    const uint32_t m0 = m_tile * BM, n0 = n_tile * 256;
 
-    /* global -> register assignment */
-    const uint32_t ac = tid & 7;      /* A: 16-byte chunk of the 128-byte row slice */
-    const uint32_t ar0 = tid >> 3;    /* A: rows ar0 + 32 i */
-    const uint32_t wr = tid;          /* B: one weight row per thread */
-    const uint32_t wrow = n0 + wr < a.n ? n0 + wr : a.n - 1;
-    const uint8_t *wptr = a.w + (uint64_t)wrow * a.w_row_stride;
-    const _Float16 *xrow[8];
+    AF16Rows<BM> as;
+    as.chunk = tid & 7;
+    as.row0 = tid >> 3;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        uint32_t r = m0 + ar0 + 32 * i;
-        xrow[i] = a.x16 + (uint64_t)(r < a.m ? r : a.m - 1) * a.k + 8 * ac;
+    for (int i = 0; i < BM / 32; ++i) {
+        uint32_t r = m0 + as.row0 + 32 * i;
+        as.row[i] = a.x16 + (uint64_t)(r < a.m ? r : a.m - 1) * a.k + 8 * as.chunk;
     }
+    const uint32_t wrow = n0 + tid < a.n ? n0 + tid : a.n - 1;
+    r9vx_f32x16 acc[BM / 32][2];
+    mma_mainloop<SCHEME, BM, NBUF>(lds, as, a.w + (uint64_t)wrow * a.w_row_stride, a.k / kTileK, acc);
 
-    r9vx_u32x4 ra[8], q0, q1, hdr;
-    auto gload = [&](uint32_t kt) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ra[i] = *reinterpret_cast<const r9vx_u32x4 *>(xrow[i] + kt * kTileK);
-        load_w64<SCHEME>(wptr, kt, q0, q1, hdr);
-    };
-    auto lstore = [&](uint32_t buf, uint32_t kt) {
-        uint8_t *A = lds[buf][0];
-        uint8_t *B = lds[buf][1];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) *reinterpret_cast<r9vx_u32x4 *>(A + lds_chunk(ar0 + 32 * i, ac)) = ra[i];
-        r9vx_u32x4 wq[8];
-        dequant_row64<SCHEME>(q0, q1, hdr, kt & 3, wq);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) *reinterpret_cast<r9vx_u32x4 *>(B + lds_chunk(wr, c)) = wq[c];
-    };
-
-    r9vx_f32x16 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    gload(0);
-    lstore(0, 0);
-    __syncthreads();
-
-    const uint32_t frow = lane & 31, fchk = lane >> 5;
-    for (uint32_t kt = 0; kt < kt_n; ++kt) {
-        const uint32_t cur = kt & 1;
-        const bool more = kt + 1 < kt_n;
-        if (more) gload(kt + 1);
-        const uint8_t *A = lds[cur][0];
-        const uint8_t *B = lds[cur][1];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            half8 af[4], bf[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                af[i] = *reinterpret_cast<const half8 *>(A + lds_chunk(wm * 128 + i * 32 + frow, 2 * s + fchk));
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                bf[j] = *reinterpret_cast<const half8 *>(B + lds_chunk(wn * 128 + j * 32 + frow, 2 * s + fchk));
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (more) lstore(cur ^ 1, kt + 1);
-        __syncthreads();
-    }
-
-    /* epilogue: D[i][j] of a 32x32 tile sits in lane l, register r at
-     * row 8*(r/4) + 4*(l/32) + r%4, column l%32. */
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < BM / 32; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const uint32_t row = m0 + acc_row(i, r, lane);
             if (row >= a.m) continue;
             const float sc = a.scale[row];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t col = n0 + wn * 128 + j * 32 + (lane & 31);
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t col = n0 + acc_col(wave, j, lane);
                 if (col >= a.n) continue;
                 float v = acc[i][j][r] * sc;
                 if (a.epilogue == R9VX_EPILOGUE_BIAS) v += a.bias[col];
@@ -208,14 +151,26 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     a.m = p.m;
     a.n = p.n;
     a.k = p.k;
-    a.m_tiles = (p.m + kTileM - 1) / kTileM;
-    a.n_tiles = (p.n + kTileN - 1) / kTileN;
+    /* 256-row tiles, double-buffered, one workgroup per CU when there are
+     * enough rows to fill the chip; 128-row single-buffered tiles (two
+     * workgroups per CU) otherwise. */
+    const bool big = (uint64_t)((p.m + 255) / 256) * ((p.n + 255) / 256) >= 256;
+    const uint32_t bm = big ? 256 : 128;
+    a.m_tiles = (p.m + bm - 1) / bm;
+    a.n_tiles = (p.n + 255) / 256;
     a.y_bf16 = p.y_dtype == R9VX_DTYPE_BF16;
     a.epilogue = p.epilogue;
     dim3 grid(a.m_tiles * a.n_tiles);
-    if (p.scheme == R9VX_SCHEME_Q4_K)
-        hipLaunchKernelGGL(gemm_kernel<R9VX_SCHEME_Q4_K>, grid, dim3(256), 0, stream, a);
-    else
-        hipLaunchKernelGGL(gemm_kernel<R9VX_SCHEME_IQ4_XS>, grid, dim3(256), 0, stream, a);
+    if (p.scheme == R9VX_SCHEME_Q4_K) {
+        if (big)
+            hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q4_K, 256, 2>), grid, dim3(256), 0, stream, a);
+        else
+            hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q4_K, 128, 1>), grid, dim3(256), 0, stream, a);
+    } else {
+        if (big)
+            hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_IQ4_XS, 256, 2>), grid, dim3(256), 0, stream, a);
+        else
+            hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_IQ4_XS, 128, 1>), grid, dim3(256), 0, stream, a);
+    }
     return (int)hipGetLastError();
 }

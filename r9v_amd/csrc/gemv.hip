@@ -108,24 +108,30 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
                 chunk_dot<SCHEME, XF32, M>(qs[r][s], hd[r][s], cis[s] & 7, xc[s], acc[r], lut);
     }
 
+    /* cross-lane sums of all kRows*M partials at once, then every lane
+     * writes the values it ended up owning */
+    constexpr int V = kRows * M;
+    float v[V];
+    int idx[V];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
+    for (int r = 0; r < kRows; ++r)
 #pragma unroll
-        for (int t = 0; t < M; ++t) acc[r][t] = r9vx_group_sum(acc[r][t], (int)lpr);
-        uint32_t row = row0 + r * rpi;
-        if (lir == 0 && row < a.n) {
+        for (int t = 0; t < M; ++t) v[r * M + t] = acc[r][t];
+    const int live = reduce_scatter<V>(v, idx, lane, (int)lpr);
 #pragma unroll
-            for (int t = 0; t < M; ++t) {
-                float v = acc[r][t];
-                if (a.epilogue == R9VX_EPILOGUE_BIAS) v += a.bias[row];
-                if (a.epilogue == R9VX_EPILOGUE_RESIDUAL) v += a.residual[(uint64_t)t * a.n + row];
-                uint64_t o = (uint64_t)t * a.n + row;
-                if (a.y_bf16)
-                    reinterpret_cast<uint16_t *>(a.y)[o] = r9vx_f32_to_bf16(v);
-                else
-                    reinterpret_cast<float *>(a.y)[o] = v;
-            }
-        }
+    for (int i = 0; i < V; ++i) {
+        if (i >= live) break;
+        const int r = idx[i] / M, t = idx[i] % M;
+        const uint32_t row = row0 + r * rpi;
+        if (row >= a.n) continue;
+        float val = v[i];
+        if (a.epilogue == R9VX_EPILOGUE_BIAS) val += a.bias[row];
+        if (a.epilogue == R9VX_EPILOGUE_RESIDUAL) val += a.residual[(uint64_t)t * a.n + row];
+        const uint64_t o = (uint64_t)t * a.n + row;
+        if (a.y_bf16)
+            reinterpret_cast<uint16_t *>(a.y)[o] = r9vx_f32_to_bf16(val);
+        else
+            reinterpret_cast<float *>(a.y)[o] = val;
     }
 }
 

@@ -268,8 +268,8 @@ struct FfnArgs {
 
 /* Rows per lane group per wave: fewer when more activation rows are live,
  * so that the activation registers of MT rows fit without spilling. */
-constexpr int pairs_for(int mt) { return mt <= 2 ? 2 : 1; }
-constexpr int dn_rows_for(int mt) { return mt <= 2 ? 4 : 2; }
+constexpr int pairs_for(int mt) { return mt <= 1 ? 4 : (mt <= 2 ? 4 : 2); }
+constexpr int dn_rows_for(int mt) { return mt <= 1 ? 8 : (mt <= 2 ? 4 : 2); }
 
 __device__ __forceinline__ bool refused(const FfnArgs &a) {
     return reinterpret_cast<const uint32_t *>(a.ws + a.L.status)[0] != 0u;
@@ -345,19 +345,29 @@ __global__ __launch_bounds__(256) void moe_gu_kernel(FfnArgs a) {
                 chunk_dot<GU, false, MT>(qu[r], hu[r], ci & 7, xc, au[r], lut, m);
             }
         }
+        /* g and u go through the same reduce-scatter, so slot i of both
+         * holds the same (row, token) */
+        constexpr int V = kPairs * MT;
+        float gv[V], uv[V];
+        int gi[V], ui[V];
 #pragma unroll
-        for (int r = 0; r < kPairs; ++r) {
-            uint32_t row = r0 + r * rpi;
+        for (int r = 0; r < kPairs; ++r)
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
-                if (t >= m) break;
-                float g = r9vx_group_sum(ag[r][t], (int)lpr);
-                float u = r9vx_group_sum(au[r][t], (int)lpr);
-                if (lir == 0 && row < a.dff) {
-                    float act = g / (1.0f + r9vx_expf(-g));
-                    h[(uint64_t)(beg + t0 + t) * a.dff + row] = act * u;
-                }
+                gv[r * MT + t] = ag[r][t];
+                uv[r * MT + t] = au[r][t];
             }
+        const int live = reduce_scatter<V>(gv, gi, lane, (int)lpr);
+        reduce_scatter<V>(uv, ui, lane, (int)lpr);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            if (i >= live) break;
+            const int r = gi[i] / MT, t = gi[i] % MT;
+            const uint32_t row = r0 + r * rpi;
+            if (t >= m || row >= a.dff) continue;
+            const float g = gv[i];
+            const float act = g / (1.0f + r9vx_expf(-g));
+            h[(uint64_t)(beg + t0 + t) * a.dff + row] = act * uv[i];
         }
     }
 }
@@ -417,15 +427,21 @@ __global__ __launch_bounds__(256) void moe_down_kernel(FfnArgs a) {
 #pragma unroll
             for (int r = 0; r < kDnRows; ++r) chunk_dot<DN, true, MT>(q[r], hd[r], ci & 7, xc, acc[r], lut, m);
         }
+        constexpr int V = kDnRows * MT;
+        float v[V];
+        int vi[V];
 #pragma unroll
-        for (int r = 0; r < kDnRows; ++r) {
-            uint32_t row = r0 + r * rpi;
+        for (int r = 0; r < kDnRows; ++r)
 #pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                if (t >= m) break;
-                float v = r9vx_group_sum(acc[r][t], (int)lpr);
-                if (lir == 0 && row < a.dm) o[(uint64_t)(beg + t0 + t) * a.dm + row] = v;
-            }
+            for (int t = 0; t < MT; ++t) v[r * MT + t] = acc[r][t];
+        const int live = reduce_scatter<V>(v, vi, lane, (int)lpr);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            if (i >= live) break;
+            const int r = vi[i] / MT, t = vi[i] % MT;
+            const uint32_t row = r0 + r * rpi;
+            if (t >= m || row >= a.dm) continue;
+            o[(uint64_t)(beg + t0 + t) * a.dm + row] = v[i];
         }
     }
 }
@@ -435,36 +451,49 @@ __global__ __launch_bounds__(256) void moe_down_kernel(FfnArgs a) {
 /* ---------------------------------------------------------------- combine */
 
 /* y[t, d] = sum over the token's pairs in ascending sorted position (=
- * ascending expert, then slot) of w * o, then + each shared expert's o. */
+ * ascending expert, then slot) of w * o, then + each shared expert's o.
+ * The first K threads rank the token's K positions in LDS (positions are
+ * distinct), so every thread then walks the same ordered list from LDS and
+ * issues its K row loads before the ordered f32 sum. */
 __global__ __launch_bounds__(256) void r9vx_moe_combine_kernel(MoeCombineArgs a) {
+    __shared__ uint32_t spos[kMoeMaxK], opos[kMoeMaxK];
+    __shared__ float sw[kMoeMaxK], ow[kMoeMaxK];
     const uint32_t *status = reinterpret_cast<const uint32_t *>(a.ws + a.L.status);
     if (status[0] != 0u) return;
-    uint32_t t = blockIdx.y;
-    uint32_t d0 = (blockIdx.x * 256 + threadIdx.x) * 4;
-    if (t >= a.t || d0 >= a.dm) return;
+    const uint32_t t = blockIdx.y;
+    const uint32_t kk = a.k;
     const uint32_t *inv = reinterpret_cast<const uint32_t *>(a.ws + a.L.inv);
-    const uint32_t *sorted = reinterpret_cast<const uint32_t *>(a.ws + a.L.sorted);
+    if (threadIdx.x < kk) {
+        spos[threadIdx.x] = inv[(uint64_t)t * kk + threadIdx.x];
+        sw[threadIdx.x] = a.weights[(uint64_t)t * kk + threadIdx.x];
+    }
+    __syncthreads();
+    if (threadIdx.x < kk) {
+        const uint32_t p = spos[threadIdx.x];
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < kk; ++j) rank += spos[j] < p ? 1u : 0u;
+        opos[rank] = p;
+        ow[rank] = sw[threadIdx.x];
+    }
+    __syncthreads();
+    const uint32_t d0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (d0 >= a.dm) return;
     const float *o = reinterpret_cast<const float *>(a.ws + a.L.o);
-    uint32_t pos[kMoeMaxK];
-    uint32_t kk = a.k;
-    for (uint32_t j = 0; j < kk; ++j) {
-        uint32_t v = inv[(uint64_t)t * kk + j];
-        uint32_t i = j;
-        while (i > 0 && pos[i - 1] > v) {
-            pos[i] = pos[i - 1];
-            --i;
-        }
-        pos[i] = v;
+    r9vx_f32x4 rows[kMoeMaxK];
+#pragma unroll
+    for (uint32_t j = 0; j < kMoeMaxK; ++j) {
+        if (j >= kk) break;
+        rows[j] = *reinterpret_cast<const r9vx_f32x4 *>(o + (uint64_t)opos[j] * a.dm + d0);
     }
     r9vx_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t j = 0; j < kk; ++j) {
-        uint32_t slot = sorted[pos[j]] - t * kk;
-        float w = a.weights[(uint64_t)t * kk + slot];
-        r9vx_f32x4 v = *reinterpret_cast<const r9vx_f32x4 *>(o + (uint64_t)pos[j] * a.dm + d0);
-        acc.x = acc.x + w * v.x;
-        acc.y = acc.y + w * v.y;
-        acc.z = acc.z + w * v.z;
-        acc.w = acc.w + w * v.w;
+#pragma unroll
+    for (uint32_t j = 0; j < kMoeMaxK; ++j) {
+        if (j >= kk) break;
+        const float w = ow[j];
+        acc.x = acc.x + w * rows[j].x;
+        acc.y = acc.y + w * rows[j].y;
+        acc.z = acc.z + w * rows[j].z;
+        acc.w = acc.w + w * rows[j].w;
     }
     for (uint32_t s = 0; s < a.shared; ++s) {
         r9vx_f32x4 v = *reinterpret_cast<const r9vx_f32x4 *>(o + (uint64_t)(a.p + s * a.t + t) * a.dm + d0);
@@ -540,17 +569,10 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
     f.gu_lpr_log2 = lpr_for(p.dm, f.gu_nseg);
     f.dn_lpr_log2 = lpr_for(p.dff, f.dn_nseg);
     uint32_t max_work = (f.p < p.e ? f.p : p.e) + p.shared;
-    uint32_t mt = p.t < 4 ? p.t : 4; /* larger t runs in groups of 4 rows */
-    switch (mt) {
-    case 1: launch_decode_mt<1>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
-    case 2: launch_decode_mt<2>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
-    case 3: launch_decode_mt<3>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
-    case 4: launch_decode_mt<4>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
-    case 5: launch_decode_mt<5>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
-    case 6: launch_decode_mt<6>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
-    case 7: launch_decode_mt<7>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
-    default: launch_decode_mt<8>(f, p.scheme_gu, p.scheme_dn, max_work, s); break;
-    }
+    /* Decode routes mostly one token to an expert: one activation row per
+     * pass keeps the registers for rows and loads in flight; an expert with
+     * more tokens re-reads its rows from L2 once per token. */
+    launch_decode_mt<1>(f, p.scheme_gu, p.scheme_dn, max_work, s);
     return (int)hipGetLastError();
 }
 

@@ -17,9 +17,10 @@
  *          by the power of two that brings max|h| below 2^15, rounded to fp16
  *          into LDS, and the scale is undone on the f32 accumulators.
  * Weight tiles are dequantized into LDS as fp16 exactly as in gemm.hip; LDS
- * is double-buffered (48 KiB per stage).  Tiles past the scanned count exit.
+ * is single-buffered (48 KiB) so two workgroups share a CU and one's MFMAs
+ * overlap the other's dequantization.  Tiles past the scanned count exit.
  */
-#include "r9vx_mfma.h"
+#include "r9vx_mma.h"
 #include "r9vx_moe.h"
 
 using namespace r9vx;
@@ -91,10 +92,12 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(GroupedArgs a) {
 
 /* ---------------------------------------------------------------- gate/up */
 
+constexpr int kNB = 1; /* single-buffered LDS: two workgroups share a CU */
+
 template <int GU>
-__global__ __launch_bounds__(256) void moe_gu_mfma_kernel(GroupedArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t ldsA[2][kBM * 128];
-    __shared__ __attribute__((aligned(16))) uint8_t ldsB[2][256 * 128];
+__global__ __launch_bounds__(256, 2) void moe_gu_mfma_kernel(GroupedArgs a) {
+    using S = MmaShape<kBM, kNB>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
     __shared__ uint32_t rowmax[kBM];
     const uint32_t *status = ws_u32(a, a.L.status);
     const uint32_t ntile_n = a.dff / 128;
@@ -104,95 +107,38 @@ __global__ __launch_bounds__(256) void moe_gu_mfma_kernel(GroupedArgs a) {
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
     const uint32_t j0 = nt * 128;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t wm = wave & 1, wn = wave >> 1;
     if (tid < kBM) rowmax[tid] = 0u;
 
-    /* A: 4 rows x one 16-byte chunk per thread; B: one weight row per thread */
-    const uint32_t ac = tid & 7, ar0 = tid >> 3;
-    const _Float16 *xrow[4];
+    AF16Rows<kBM> as;
+    as.chunk = tid & 7;
+    as.row0 = tid >> 3;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t r = ar0 + 32 * i;
+    for (int i = 0; i < kBM / 32; ++i) {
+        uint32_t r = as.row0 + 32 * i;
         uint32_t tok = row_token(a, expert, pos0 + (r < rows ? r : 0));
-        xrow[i] = a.x16 + (uint64_t)tok * a.dm + 8 * ac;
+        as.row[i] = a.x16 + (uint64_t)tok * a.dm + 8 * as.chunk;
     }
-    const uint32_t wr = tid < 128 ? (j0 + tid) : (a.dff + j0 + tid - 128);
+    /* B row t: wave w = t/64 takes gate rows j0+32w.. (t%64 < 32) and the
+     * matching up rows, so acc[i][0] is g and acc[i][1] is u of the same j. */
+    const uint32_t bw = tid >> 6, bh = (tid >> 5) & 1, bj = tid & 31;
+    const uint32_t wr = (bh ? a.dff : 0u) + j0 + 32 * bw + bj;
     const uint8_t *wptr = a.w_gu + ((uint64_t)expert * 2 * a.dff + wr) * a.gu_row_bytes;
-    const uint32_t kt_n = a.dm / kTileK;
-
-    r9vx_u32x4 ra[4], q0, q1, hdr;
-    auto gload = [&](uint32_t kt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const r9vx_u32x4 *>(xrow[i] + kt * kTileK);
-        load_w64<GU>(wptr, kt, q0, q1, hdr);
-    };
-    auto lstore = [&](uint32_t buf, uint32_t kt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<r9vx_u32x4 *>(ldsA[buf] + lds_chunk(ar0 + 32 * i, ac)) = ra[i];
-        r9vx_u32x4 wq[8];
-        dequant_row64<GU>(q0, q1, hdr, kt & 3, wq);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) *reinterpret_cast<r9vx_u32x4 *>(ldsB[buf] + lds_chunk(tid, c)) = wq[c];
-    };
-
-    r9vx_f32x16 ag[2][2], au[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) ag[i][j][r] = au[i][j][r] = 0.f;
-
-    gload(0);
-    lstore(0, 0);
-    __syncthreads();
-    const uint32_t frow = lane & 31, fchk = lane >> 5;
-    for (uint32_t kt = 0; kt < kt_n; ++kt) {
-        const uint32_t cur = kt & 1;
-        const bool more = kt + 1 < kt_n;
-        if (more) gload(kt + 1);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            half8 af[2], bg[2], bu[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                af[i] = *reinterpret_cast<const half8 *>(ldsA[cur] + lds_chunk(wm * 64 + i * 32 + frow, 2 * s + fchk));
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                bg[j] = *reinterpret_cast<const half8 *>(ldsB[cur] + lds_chunk(wn * 64 + j * 32 + frow, 2 * s + fchk));
-                bu[j] = *reinterpret_cast<const half8 *>(ldsB[cur] +
-                                                         lds_chunk(128 + wn * 64 + j * 32 + frow, 2 * s + fchk));
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    ag[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bg[j], ag[i][j], 0, 0, 0);
-                    au[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bu[j], au[i][j], 0, 0, 0);
-                }
-        }
-        if (more) lstore(cur ^ 1, kt + 1);
-        __syncthreads();
-    }
+    r9vx_f32x16 acc[kBM / 32][2];
+    mma_mainloop<GU, kBM, kNB>(lds, as, wptr, a.dm / kTileK, acc);
 
     float *h = reinterpret_cast<float *>(a.ws + a.L.h);
+    const uint32_t col = j0 + 32 * wave + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kBM / 32; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const uint32_t rl = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            const bool live = rl < rows;
-            const float sc = live ? a.xscale[row_token(a, expert, pos0 + rl)] : 0.f;
-            float m = 0.f;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint32_t col = j0 + wn * 64 + j * 32 + (lane & 31);
-                float g = ag[i][j][r] * sc, u = au[i][j][r] * sc;
-                float v = g / (1.0f + __expf(-g)) * u;
-                if (live) h[(uint64_t)(pos0 + rl) * a.dff + col] = v;
-                m = fmaxf(m, fabsf(v));
-            }
-            if (live) atomicMax(&rowmax[rl], __builtin_bit_cast(uint32_t, m));
+            const uint32_t rl = acc_row(i, r, lane);
+            if (rl >= rows) continue;
+            const float sc = a.xscale[row_token(a, expert, pos0 + rl)];
+            const float g = acc[i][0][r] * sc, u = acc[i][1][r] * sc;
+            const float v = g / (1.0f + __expf(-g)) * u;
+            h[(uint64_t)(pos0 + rl) * a.dff + col] = v;
+            atomicMax(&rowmax[rl], __builtin_bit_cast(uint32_t, fabsf(v)));
         }
     }
     __syncthreads();
@@ -202,9 +148,9 @@ __global__ __launch_bounds__(256) void moe_gu_mfma_kernel(GroupedArgs a) {
 /* ---------------------------------------------------------------- down */
 
 template <int DN>
-__global__ __launch_bounds__(256) void moe_dn_mfma_kernel(GroupedArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t ldsA[2][kBM * 128];
-    __shared__ __attribute__((aligned(16))) uint8_t ldsB[2][256 * 128];
+__global__ __launch_bounds__(256, 2) void moe_dn_mfma_kernel(GroupedArgs a) {
+    using S = MmaShape<kBM, kNB>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
     const uint32_t *status = ws_u32(a, a.L.status);
     const uint32_t ntile_n = a.dm / 256;
     const uint32_t tix = blockIdx.x / ntile_n, nt = blockIdx.x % ntile_n;
@@ -213,98 +159,34 @@ __global__ __launch_bounds__(256) void moe_dn_mfma_kernel(GroupedArgs a) {
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
     const uint32_t n0 = nt * 256;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t wm = wave & 1, wn = wave >> 1;
 
-    /* A: h rows (f32) -> fp16 with 2^-e(row); 4 rows x 8 columns per thread */
-    const uint32_t ac = tid & 7, ar0 = tid >> 3;
-    const float *hrow[4];
-    float inv[4];
+    AF32ScaledRows<kBM> as;
+    as.chunk = tid & 7;
+    as.row0 = tid >> 3;
     const float *hbase = reinterpret_cast<const float *>(a.ws + a.L.h);
     const uint32_t *hmax = ws_u32(a, a.L.hmax);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t r = ar0 + 32 * i;
+    for (int i = 0; i < kBM / 32; ++i) {
+        uint32_t r = as.row0 + 32 * i;
         uint32_t pos = pos0 + (r < rows ? r : 0);
-        hrow[i] = hbase + (uint64_t)pos * a.dff + 8 * ac;
-        inv[i] = ldexpf(1.0f, -row_shift(__builtin_bit_cast(float, hmax[pos])));
+        as.row[i] = hbase + (uint64_t)pos * a.dff + 8 * as.chunk;
+        as.inv[i] = ldexpf(1.0f, -row_shift(__builtin_bit_cast(float, hmax[pos])));
     }
     const uint8_t *wptr = a.w_dn + ((uint64_t)expert * a.dm + n0 + tid) * a.dn_row_bytes;
-    const uint32_t kt_n = a.dff / kTileK;
-
-    r9vx_f32x4 ra[4][2];
-    r9vx_u32x4 q0, q1, hdr;
-    auto gload = [&](uint32_t kt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const r9vx_f32x4 *p4 = reinterpret_cast<const r9vx_f32x4 *>(hrow[i] + kt * kTileK);
-            ra[i][0] = p4[0];
-            ra[i][1] = p4[1];
-        }
-        load_w64<DN>(wptr, kt, q0, q1, hdr);
-    };
-    auto lstore = [&](uint32_t buf, uint32_t kt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            r9vx_f32x4 v0 = ra[i][0], v1 = ra[i][1];
-            const float s = inv[i];
-            r9vx_u32x4 o{pack_h2(v0.x * s, v0.y * s), pack_h2(v0.z * s, v0.w * s), pack_h2(v1.x * s, v1.y * s),
-                         pack_h2(v1.z * s, v1.w * s)};
-            *reinterpret_cast<r9vx_u32x4 *>(ldsA[buf] + lds_chunk(ar0 + 32 * i, ac)) = o;
-        }
-        r9vx_u32x4 wq[8];
-        dequant_row64<DN>(q0, q1, hdr, kt & 3, wq);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) *reinterpret_cast<r9vx_u32x4 *>(ldsB[buf] + lds_chunk(tid, c)) = wq[c];
-    };
-
-    r9vx_f32x16 acc[2][4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    gload(0);
-    lstore(0, 0);
-    __syncthreads();
-    const uint32_t frow = lane & 31, fchk = lane >> 5;
-    for (uint32_t kt = 0; kt < kt_n; ++kt) {
-        const uint32_t cur = kt & 1;
-        const bool more = kt + 1 < kt_n;
-        if (more) gload(kt + 1);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            half8 af[2], bf[4];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                af[i] = *reinterpret_cast<const half8 *>(ldsA[cur] + lds_chunk(wm * 64 + i * 32 + frow, 2 * s + fchk));
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                bf[j] = *reinterpret_cast<const half8 *>(ldsB[cur] + lds_chunk(wn * 128 + j * 32 + frow, 2 * s + fchk));
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (more) lstore(cur ^ 1, kt + 1);
-        __syncthreads();
-    }
+    r9vx_f32x16 acc[kBM / 32][2];
+    mma_mainloop<DN, kBM, kNB>(lds, as, wptr, a.dff / kTileK, acc);
 
     float *o = reinterpret_cast<float *>(a.ws + a.L.o);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kBM / 32; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const uint32_t rl = wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const uint32_t rl = acc_row(i, r, lane);
             if (rl >= rows) continue;
             const float sc = ldexpf(1.0f, row_shift(__builtin_bit_cast(float, hmax[pos0 + rl])));
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t col = n0 + wn * 128 + j * 32 + (lane & 31);
-                o[(uint64_t)(pos0 + rl) * a.dm + col] = acc[i][j][r] * sc;
-            }
+            for (int j = 0; j < 2; ++j)
+                o[(uint64_t)(pos0 + rl) * a.dm + n0 + acc_col(wave, j, lane)] = acc[i][j][r] * sc;
         }
     }
 }

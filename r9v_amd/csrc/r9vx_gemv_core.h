@@ -83,30 +83,34 @@ __device__ __forceinline__ void load_x_raw(const void *xbase, uint32_t klo, uint
 template <int SCHEME, bool XF32>
 __device__ __forceinline__ void arrange_x(const XRaw<XF32> &r, XChunk<SCHEME, XF32> &xc) {
     if constexpr (XF32) {
-        float slo = 0.f, shi = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            xc.v[i] = r.v[i];
-            xc.v[4 + i] = r.v[4 + i];
-            slo += (r.v[i].x + r.v[i].y) + (r.v[i].z + r.v[i].w);
-            shi += (r.v[4 + i].x + r.v[4 + i].y) + (r.v[4 + i].z + r.v[4 + i].w);
+        for (int i = 0; i < 8; ++i) xc.v[i] = r.v[i];
+        if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
+            float slo = 0.f, shi = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                slo += (r.v[i].x + r.v[i].y) + (r.v[i].z + r.v[i].w);
+                shi += (r.v[4 + i].x + r.v[4 + i].y) + (r.v[4 + i].z + r.v[4 + i].w);
+            }
+            xc.slo = slo;
+            xc.shi = shi;
         }
-        xc.slo = slo;
-        xc.shi = shi;
     } else {
         uint32_t L[8], H[8];
         L[0] = r.v[0].x; L[1] = r.v[0].y; L[2] = r.v[0].z; L[3] = r.v[0].w;
         L[4] = r.v[1].x; L[5] = r.v[1].y; L[6] = r.v[1].z; L[7] = r.v[1].w;
         H[0] = r.v[2].x; H[1] = r.v[2].y; H[2] = r.v[2].z; H[3] = r.v[2].w;
         H[4] = r.v[3].x; H[5] = r.v[3].y; H[6] = r.v[3].z; H[7] = r.v[3].w;
-        float slo = 0.f, shi = 0.f;
+        if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
+            float slo = 0.f, shi = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            slo += __builtin_bit_cast(float, L[j] << 16) + __builtin_bit_cast(float, L[j] & 0xFFFF0000u);
-            shi += __builtin_bit_cast(float, H[j] << 16) + __builtin_bit_cast(float, H[j] & 0xFFFF0000u);
+            for (int j = 0; j < 8; ++j) {
+                slo += __builtin_bit_cast(float, L[j] << 16) + __builtin_bit_cast(float, L[j] & 0xFFFF0000u);
+                shi += __builtin_bit_cast(float, H[j] << 16) + __builtin_bit_cast(float, H[j] & 0xFFFF0000u);
+            }
+            xc.slo = slo;
+            xc.shi = shi;
         }
-        xc.slo = slo;
-        xc.shi = shi;
         if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
             /* pair i = {x_lo(i), x_hi(i)}: byte i's two nibbles */
 #pragma unroll
@@ -236,6 +240,46 @@ __device__ __forceinline__ void chunk_dot(const r9vx_u32x4 &qs, const Hdr &h, ui
     }
 }
 
+
+/* Sums each of the V values over the `width` lanes of its aligned lane
+ * group (width a power of two, 8..64), halving the live values at every
+ * butterfly step: the lane whose step bit is set keeps the upper half and
+ * sends the lower half, the other keeps the lower half.  Afterwards the lane
+ * holds ceil-halved subsets of fully reduced values; owner(i, lane_in_group)
+ * tells which original index ends in slot 0..  This costs about 4 ops per
+ * value in total instead of 2 per value per step.
+ *
+ * Returns the number of live slots; idx[s] = original index of slot s. */
+template <int V>
+__device__ __forceinline__ int reduce_scatter(float (&v)[V], int (&idx)[V], uint32_t lane, int width) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) idx[i] = i;
+    int c = V;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        if (d >= width) continue;
+        const bool up = (lane & (uint32_t)d) != 0;
+        const int h = c / 2;
+#pragma unroll
+        for (int i = 0; i < V / 2 + 1; ++i) {
+            if (i >= h) break;
+            float a = v[i], b = v[i + h];
+            float send = up ? a : b;
+            float keep = up ? b : a;
+            v[i] = keep + __shfl_xor(send, d, 64);
+            idx[i] = up ? idx[i + h] : idx[i];
+        }
+        if (c & 1) { /* odd leftover: reduce it whole, keep it as slot h */
+            float a = v[c - 1];
+            v[h] = a + __shfl_xor(a, d, 64);
+            idx[h] = idx[c - 1];
+            c = h + 1;
+        } else {
+            c = h;
+        }
+    }
+    return c;
+}
 
 /* IQ4_XS bf16 codebook-pair table: entry b = {kv[b & 15], kv[b >> 4]}. */
 __device__ __forceinline__ void init_iq4_lut(uint32_t *lut, uint32_t tid, uint32_t nthreads) {

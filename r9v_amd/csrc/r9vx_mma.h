@@ -1,0 +1,277 @@
+/*
+ * r9vx_mma.h -- the shared main loop of the dequant-to-LDS MFMA GEMMs (dense
+ * prefill matmul, grouped MoE gate/up and down).
+ *
+ * Workgroup: 256 threads = 4 waves, output tile BM x 256.  Wave w owns the
+ * 64 output columns [64w, 64w+64) and all BM rows: (BM/32) x 2 tiles of
+ * v_mfma_f32_32x32x16_f16, BM accumulator registers.  Per K step of 64:
+ *   A: BM rows x 64 fp16 from the caller's activation source -> LDS
+ *   B: 256 weight rows x 32 payload bytes (one row per thread) -> dequantized
+ *      with the exact f32 formula (crates/r9v-format/src/ggml.rs:1131-1150,
+ *      iq.rs:578-598), rounded once to fp16 -> LDS
+ * LDS rows are 128 bytes of eight 16-byte chunks stored at chunk ^ (row & 7).
+ * NBUF = 2 double-buffers LDS (one barrier per step, next step's loads and
+ * dequant overlap this step's MFMAs); NBUF = 1 single-buffers it (two barriers
+ * per step) so that two workgroups share a CU and interleave.
+ */
+#ifndef R9VX_MMA_H
+#define R9VX_MMA_H
+
+#include "r9vx_mfma.h"
+
+namespace r9vx {
+
+template <int BM, int NBUF>
+struct MmaShape {
+    static constexpr int kABytes = BM * 128;
+    static constexpr int kBBytes = 256 * 128;
+    static constexpr int kStage = kABytes + kBBytes;
+    static constexpr int kLds = NBUF * kStage + 256 * 8; /* + IQ4 f32 pair table */
+    static constexpr int kMT = BM / 32;                  /* 32-row tiles per wave */
+};
+
+/* IQ4_XS f32 codebook pairs: entry b = {kv[b & 15], kv[b >> 4]}. */
+__device__ __forceinline__ void init_iq4_lut_f32(r9vx_f32x4 *lut2 /* 128 x (2 pairs) */, uint32_t tid) {
+    if (tid < 128) {
+        uint32_t b0 = 2 * tid, b1 = 2 * tid + 1;
+        lut2[tid] = r9vx_f32x4{(float)r9vx_iq4_kvalue(b0 & 15), (float)r9vx_iq4_kvalue(b0 >> 4),
+                               (float)r9vx_iq4_kvalue(b1 & 15), (float)r9vx_iq4_kvalue(b1 >> 4)};
+    }
+}
+
+__device__ __forceinline__ uint32_t cvt_pk_h2(float a, float b) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    h2 r;
+    r.x = (_Float16)a;
+    r.y = (_Float16)b;
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+/* Weight bytes one thread carries for one K step. */
+struct WRegs {
+    r9vx_u32x4 q0, q1, hdr;
+};
+
+/* Dequantizes one weight row's 64 K values of step ks (0..3 in the super-
+ * block) and stores them as 8 chunks of LDS row `row`. */
+template <int SCHEME>
+__device__ __forceinline__ void dequant_store(const WRegs &w, uint32_t ks, uint8_t *B, uint32_t row,
+                                              const float *lutf) {
+    uint32_t b[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+    if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
+        const float d = r9vx_f16_to_f32((uint16_t)(w.hdr.x & 0xFFFF));
+        const float dmin = r9vx_f16_to_f32((uint16_t)(w.hdr.x >> 16));
+        uint32_t sc[2], mn[2];
+        r9vx_q4k_scale_pair(w.hdr, ks, sc, mn);
+        const float dl0 = d * (float)sc[0], nml0 = -(dmin * (float)mn[0]);
+        const float dl1 = d * (float)sc[1], nml1 = -(dmin * (float)mn[1]);
+        uint32_t lo[16], hi[16];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t l4 = b[i] & 0x0F0F0F0Fu, h4 = (b[i] >> 4) & 0x0F0F0F0Fu;
+            float l[4], h[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                l[j] = fmaf(dl0, (float)((l4 >> (8 * j)) & 0xFFu), nml0);
+                h[j] = fmaf(dl1, (float)((h4 >> (8 * j)) & 0xFFu), nml1);
+            }
+            lo[2 * i] = cvt_pk_h2(l[0], l[1]);
+            lo[2 * i + 1] = cvt_pk_h2(l[2], l[3]);
+            hi[2 * i] = cvt_pk_h2(h[0], h[1]);
+            hi[2 * i + 1] = cvt_pk_h2(h[2], h[3]);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            *reinterpret_cast<r9vx_u32x4 *>(B + lds_chunk(row, c)) =
+                r9vx_u32x4{lo[4 * c], lo[4 * c + 1], lo[4 * c + 2], lo[4 * c + 3]};
+            *reinterpret_cast<r9vx_u32x4 *>(B + lds_chunk(row, 4 + c)) =
+                r9vx_u32x4{hi[4 * c], hi[4 * c + 1], hi[4 * c + 2], hi[4 * c + 3]};
+        }
+    } else {
+        const float d = r9vx_f16_to_f32((uint16_t)(w.hdr.x & 0xFFFF));
+        const r9vx_u32x2 h2{w.hdr.x, w.hdr.y};
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const float dl = d * r9vx_iq4xs_scale(h2, 2 * ks + s);
+            uint32_t lo[8], hi[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t wd = b[4 * s + i];
+                float l[4], h[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float *e = lutf + 2 * ((wd >> (8 * j)) & 0xFFu);
+                    l[j] = dl * e[0];
+                    h[j] = dl * e[1];
+                }
+                lo[2 * i] = cvt_pk_h2(l[0], l[1]);
+                lo[2 * i + 1] = cvt_pk_h2(l[2], l[3]);
+                hi[2 * i] = cvt_pk_h2(h[0], h[1]);
+                hi[2 * i + 1] = cvt_pk_h2(h[2], h[3]);
+            }
+            *reinterpret_cast<r9vx_u32x4 *>(B + lds_chunk(row, 4 * s + 0)) = r9vx_u32x4{lo[0], lo[1], lo[2], lo[3]};
+            *reinterpret_cast<r9vx_u32x4 *>(B + lds_chunk(row, 4 * s + 1)) = r9vx_u32x4{lo[4], lo[5], lo[6], lo[7]};
+            *reinterpret_cast<r9vx_u32x4 *>(B + lds_chunk(row, 4 * s + 2)) = r9vx_u32x4{hi[0], hi[1], hi[2], hi[3]};
+            *reinterpret_cast<r9vx_u32x4 *>(B + lds_chunk(row, 4 * s + 3)) = r9vx_u32x4{hi[4], hi[5], hi[6], hi[7]};
+        }
+    }
+}
+
+template <int SCHEME>
+__device__ __forceinline__ void load_w(const uint8_t *row, uint32_t kt, WRegs &w) {
+    load_w64<SCHEME>(row, kt, w.q0, w.q1, w.hdr);
+}
+
+/* MFMAs of one K step from LDS stage (A, B) into acc[BM/32][2].  The
+ * fragments of slice s+1 are read while slice s's MFMAs run (two fragment
+ * sets in registers), so no MFMA waits on its own LDS read. */
+template <int BM>
+__device__ __forceinline__ void mma_step(const uint8_t *A, const uint8_t *B, uint32_t wave, uint32_t lane,
+                                         r9vx_f32x16 (&acc)[BM / 32][2]) {
+    constexpr int MT = BM / 32;
+    const uint32_t frow = lane & 31, fchk = lane >> 5;
+    half8 af[2][MT], bf[2][2];
+    auto load = [&](int s, int buf) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            bf[buf][j] = *reinterpret_cast<const half8 *>(B + lds_chunk(wave * 64 + j * 32 + frow, 2 * s + fchk));
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            af[buf][i] = *reinterpret_cast<const half8 *>(A + lds_chunk(i * 32 + frow, 2 * s + fchk));
+    };
+    load(0, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int cur = s & 1;
+        if (s < 3) load(s + 1, cur ^ 1);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][i], bf[cur][j], acc[i][j], 0, 0, 0);
+    }
+}
+
+/*
+ * The main loop.  ASrc supplies activations:
+ *   typename ASrc::Regs;  void load(uint32_t kt, Regs&);  void store(const Regs&, uint8_t *A)
+ * `wrow` is this thread's weight row (LDS B row = threadIdx.x); kt_n K steps.
+ */
+template <int SCHEME, int BM, int NBUF, typename ASrc>
+__device__ __forceinline__ void mma_mainloop(uint8_t *lds, ASrc &asrc, const uint8_t *wrow, uint32_t kt_n,
+                                             r9vx_f32x16 (&acc)[BM / 32][2]) {
+    using S = MmaShape<BM, NBUF>;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *lutf = reinterpret_cast<const float *>(lds + NBUF * S::kStage);
+    if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS)
+        init_iq4_lut_f32(reinterpret_cast<r9vx_f32x4 *>(lds + NBUF * S::kStage), tid);
+#pragma unroll
+    for (int i = 0; i < BM / 32; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    typename ASrc::Regs ra;
+    WRegs wq;
+    asrc.load(0, ra);
+    load_w<SCHEME>(wrow, 0, wq);
+    __syncthreads(); /* the codebook table */
+    asrc.store(ra, lds);
+    dequant_store<SCHEME>(wq, 0, lds + S::kABytes, tid, lutf);
+    __syncthreads();
+    if constexpr (NBUF == 2) {
+        for (uint32_t kt = 0; kt < kt_n; ++kt) {
+            const uint32_t cur = kt & 1;
+            const bool more = kt + 1 < kt_n;
+            if (more) {
+                asrc.load(kt + 1, ra);
+                load_w<SCHEME>(wrow, kt + 1, wq);
+            }
+            uint8_t *st = lds + cur * S::kStage;
+            mma_step<BM>(st, st + S::kABytes, wave, lane, acc);
+            if (more) {
+                uint8_t *nx = lds + (cur ^ 1) * S::kStage;
+                asrc.store(ra, nx);
+                dequant_store<SCHEME>(wq, (kt + 1) & 3, nx + S::kABytes, tid, lutf);
+            }
+            __syncthreads();
+        }
+    } else {
+        for (uint32_t kt = 0; kt < kt_n; ++kt) {
+            const bool more = kt + 1 < kt_n;
+            if (more) {
+                asrc.load(kt + 1, ra);
+                load_w<SCHEME>(wrow, kt + 1, wq);
+            }
+            mma_step<BM>(lds, lds + S::kABytes, wave, lane, acc);
+            __syncthreads();
+            if (more) {
+                asrc.store(ra, lds);
+                dequant_store<SCHEME>(wq, (kt + 1) & 3, lds + S::kABytes, tid, lutf);
+            }
+            __syncthreads();
+        }
+    }
+}
+
+/* Row / column of accumulator register r of tile (i, j) for this lane. */
+__device__ __forceinline__ uint32_t acc_row(int i, int r, uint32_t lane) {
+    return (uint32_t)(i * 32 + 8 * (r >> 2) + 4 * (int)(lane >> 5) + (r & 3));
+}
+__device__ __forceinline__ uint32_t acc_col(uint32_t wave, int j, uint32_t lane) {
+    return wave * 64 + (uint32_t)j * 32 + (lane & 31);
+}
+
+/* A source: fp16 rows (row pointers precomputed per thread). */
+template <int BM>
+struct AF16Rows {
+    static constexpr int kPer = BM / 32; /* rows per thread (one 16-byte chunk each) */
+    struct Regs {
+        r9vx_u32x4 v[BM / 32];
+    };
+    const _Float16 *row[BM / 32];
+    uint32_t chunk, row0;
+    __device__ __forceinline__ void load(uint32_t kt, Regs &r) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) r.v[i] = *reinterpret_cast<const r9vx_u32x4 *>(row[i] + kt * 64);
+    }
+    __device__ __forceinline__ void store(const Regs &r, uint8_t *A) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) *reinterpret_cast<r9vx_u32x4 *>(A + lds_chunk(row0 + 32 * i, chunk)) = r.v[i];
+    }
+};
+
+/* A source: f32 rows scaled by a per-row power of two, rounded to fp16. */
+template <int BM>
+struct AF32ScaledRows {
+    static constexpr int kPer = BM / 32;
+    struct Regs {
+        r9vx_f32x4 v[BM / 32][2];
+    };
+    const float *row[BM / 32];
+    float inv[BM / 32];
+    uint32_t chunk, row0;
+    __device__ __forceinline__ void load(uint32_t kt, Regs &r) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const r9vx_f32x4 *p = reinterpret_cast<const r9vx_f32x4 *>(row[i] + kt * 64);
+            r.v[i][0] = p[0];
+            r.v[i][1] = p[1];
+        }
+    }
+    __device__ __forceinline__ void store(const Regs &r, uint8_t *A) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const float s = inv[i];
+            const r9vx_f32x4 a = r.v[i][0], b = r.v[i][1];
+            *reinterpret_cast<r9vx_u32x4 *>(A + lds_chunk(row0 + 32 * i, chunk)) =
+                r9vx_u32x4{cvt_pk_h2(a.x * s, a.y * s), cvt_pk_h2(a.z * s, a.w * s), cvt_pk_h2(b.x * s, b.y * s),
+                           cvt_pk_h2(b.z * s, b.w * s)};
+        }
+    }
+};
+
+}  // namespace r9vx
+
+#endif

@@ -59,7 +59,7 @@ __device__ __forceinline__ uint32_t total_order(float v) {
 }
 
 /* Status bits for one row (0 = valid). */
-__device__ uint32_t check_row(const RouteArgs &a, uint32_t row, uint32_t lane) {
+__device__ __forceinline__ uint32_t check_row(const RouteArgs &a, uint32_t row, uint32_t lane) {
     uint32_t bad = 0;
     float smax = -__builtin_huge_valf();
     for (uint32_t c = lane; c < a.e; c += 64) {
@@ -89,23 +89,28 @@ __device__ uint32_t check_row(const RouteArgs &a, uint32_t row, uint32_t lane) {
  * is broadcast with readlane, so the order and the roundings are exactly the
  * reference's sequential loop. */
 __device__ __forceinline__ float ordered_sum(const float (&v)[kMaxPerLane], uint32_t e) {
-    float sum = 0.0f;
+    /* a rotating copy keeps the register index static while the outer loop
+     * stays rolled (64 broadcasts per iteration, not 64 * 16) */
+    float q[kMaxPerLane];
 #pragma unroll
-    for (int i = 0; i < kMaxPerLane; ++i) {
-        if ((uint32_t)(64 * i) >= e) break;
-        const int bits = __builtin_bit_cast(int, v[i]);
-        if ((uint32_t)(64 * i + 64) <= e) {
+    for (int i = 0; i < kMaxPerLane; ++i) q[i] = v[i];
+    float sum = 0.0f;
+    for (uint32_t base = 0; base < e; base += 64) {
+        const int bits = __builtin_bit_cast(int, q[0]);
+        if (base + 64 <= e) {
 #pragma unroll
             for (int l = 0; l < 64; ++l) sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, l));
         } else {
-            for (uint32_t l = 0; l < e - 64 * i; ++l)
+            for (uint32_t l = 0; l < e - base; ++l)
                 sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, (int)l));
         }
+#pragma unroll
+        for (int i = 0; i + 1 < kMaxPerLane; ++i) q[i] = q[i + 1];
     }
     return sum;
 }
 
-__device__ void route_row(const RouteArgs &a, uint32_t row, uint32_t lane) {
+__device__ __forceinline__ void route_row(const RouteArgs &a, uint32_t row, uint32_t lane) {
     const uint32_t per = (a.e + 63) / 64;
     float sc[kMaxPerLane];
 #pragma unroll
