@@ -99,27 +99,63 @@ __global__ __launch_bounds__(256, NBUF == 1 ? 2 : 1) void gemm_kernel(GemmArgs a
     r9vx_f32x16 acc[BM / 32][2];
     mma_mainloop<SCHEME, BM, NBUF>(lds, as, a.w + (uint64_t)wrow * a.w_row_stride, a.k / kTileK, acc);
 
+    /* Epilogue through LDS, 32 rows at a time: the accumulators go to a
+     * 32 x 256 f32 stage (row stride 260 floats, so the two half-waves'
+     * rows land on different banks), then every wave writes whole output
+     * rows with 4 consecutive columns per lane.  acc is only ever indexed
+     * with compile-time constants, so it stays in registers. */
+    constexpr uint32_t kSRow = 260;
+    float *stage = reinterpret_cast<float *>(lds);
+    const bool vec = (a.n & 3u) == 0;
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < BM / 32; ++i) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t row = m0 + acc_row(i, r, lane);
-            if (row >= a.m) continue;
-            const float sc = a.scale[row];
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint32_t col = n0 + acc_col(wave, j, lane);
-                if (col >= a.n) continue;
-                float v = acc[i][j][r] * sc;
-                if (a.epilogue == R9VX_EPILOGUE_BIAS) v += a.bias[col];
-                if (a.epilogue == R9VX_EPILOGUE_RESIDUAL) v += a.residual[(uint64_t)row * a.n + col];
-                const uint64_t o = (uint64_t)row * a.n + col;
-                if (a.y_bf16)
-                    reinterpret_cast<uint16_t *>(a.y)[o] = r9vx_f32_to_bf16(v);
-                else
-                    reinterpret_cast<float *>(a.y)[o] = v;
+            for (int r = 0; r < 16; ++r)
+                stage[(acc_row(0, r, lane)) * kSRow + acc_col(wave, j, lane)] = acc[i][j][r];
+        __syncthreads();
+        const uint32_t cl = 4 * (tid & 63);
+        const uint32_t col = n0 + cl;
+        for (uint32_t q = 0; q < 8; ++q) {
+            const uint32_t rl = (tid >> 6) + 4 * q;
+            const uint32_t row = m0 + i * 32 + rl;
+            if (row >= a.m || col >= a.n) continue;
+            const r9vx_f32x4 acc4 = *reinterpret_cast<const r9vx_f32x4 *>(stage + rl * kSRow + cl);
+            const float sc = a.scale[row];
+            float v[4] = {acc4.x * sc, acc4.y * sc, acc4.z * sc, acc4.w * sc};
+            const uint64_t o = (uint64_t)row * a.n + col;
+            if (vec) {
+                if (a.epilogue == R9VX_EPILOGUE_BIAS) {
+                    const r9vx_f32x4 b = *reinterpret_cast<const r9vx_f32x4 *>(a.bias + col);
+                    v[0] += b.x, v[1] += b.y, v[2] += b.z, v[3] += b.w;
+                }
+                if (a.epilogue == R9VX_EPILOGUE_RESIDUAL) {
+                    const r9vx_f32x4 b = *reinterpret_cast<const r9vx_f32x4 *>(a.residual + o);
+                    v[0] += b.x, v[1] += b.y, v[2] += b.z, v[3] += b.w;
+                }
+                if (a.y_bf16) {
+                    const uint32_t lo = (uint32_t)r9vx_f32_to_bf16(v[0]) | ((uint32_t)r9vx_f32_to_bf16(v[1]) << 16);
+                    const uint32_t hi = (uint32_t)r9vx_f32_to_bf16(v[2]) | ((uint32_t)r9vx_f32_to_bf16(v[3]) << 16);
+                    *reinterpret_cast<r9vx_u32x2 *>(reinterpret_cast<uint16_t *>(a.y) + o) = r9vx_u32x2{lo, hi};
+                } else {
+                    *reinterpret_cast<r9vx_f32x4 *>(reinterpret_cast<float *>(a.y) + o) =
+                        r9vx_f32x4{v[0], v[1], v[2], v[3]};
+                }
+            } else {
+                for (uint32_t c = 0; c < 4 && col + c < a.n; ++c) {
+                    float x = v[c];
+                    if (a.epilogue == R9VX_EPILOGUE_BIAS) x += a.bias[col + c];
+                    if (a.epilogue == R9VX_EPILOGUE_RESIDUAL) x += a.residual[o + c];
+                    if (a.y_bf16)
+                        reinterpret_cast<uint16_t *>(a.y)[o + c] = r9vx_f32_to_bf16(x);
+                    else
+                        reinterpret_cast<float *>(a.y)[o + c] = x;
+                }
             }
         }
+        __syncthreads();
     }
 }
 

@@ -40,15 +40,21 @@ struct GemvArgs {
     uint32_t epilogue;
 };
 
-constexpr int kRows = 4; /* rows per lane group per wave */
+/* Rows per lane group per wave and waves per workgroup, by activation row
+ * count (measured on MI355X at K=2048/4096): two rows in two-wave groups
+ * for M <= 2, three rows in one-wave groups above, where the per-row math
+ * grows and the activation registers are shared by more rows. */
+constexpr int rows_for(int m) { return m <= 2 ? 2 : 3; }
+constexpr int waves_for(int m) { return m <= 2 ? 2 : 1; }
 
 using namespace r9vx;
 
 template <int SCHEME, int M, bool XF32, int SPL>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
+    constexpr int kRows = rows_for(M), kWaves = waves_for(M);
     __shared__ uint32_t lut[256];
     const uint32_t lane = threadIdx.x & 63;
-    const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
     const uint32_t lpr = 1u << a.lpr_log2;
     const uint32_t rpi = 64u >> a.lpr_log2; /* row slots per wave */
     const uint32_t lir = lane & (lpr - 1);
@@ -65,18 +71,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         uint32_t cis[SPL];
 #pragma unroll
         for (int s = 0; s < SPL; ++s) cis[s] = seg * lpr * SPL + s * lpr + lir;
-        /* 1. every weight load of this wave, first: they carry the HBM latency */
-        r9vx_u32x4 qs[kRows][SPL];
-        Hdr hd[kRows][SPL];
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-            uint32_t row = row0 + r * rpi;
-            uint32_t rr = row < a.n ? row : a.n - 1; /* clamp: loads stay in bounds */
-            const uint8_t *wrow = a.w + (uint64_t)rr * a.w_row_stride;
-#pragma unroll
-            for (int s = 0; s < SPL; ++s) load_chunk<SCHEME>(wrow, cis[s], qs[r][s], hd[r][s]);
-        }
-        /* 2. every activation load, still before any wait */
+        /* 1. the activation loads (L2-resident after the first wave), then
+         * every weight load of this wave: loads complete in order, so the
+         * math on row 0 can start while later rows are still in flight */
         XRaw<XF32> xr[SPL][M];
 #pragma unroll
         for (int s = 0; s < SPL; ++s) {
@@ -89,7 +86,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
                 load_x_raw<XF32>(xb, klo, khi, xr[s][t]);
             }
         }
-        /* 3. the codebook table is built while the loads are in flight */
+        r9vx_u32x4 qs[kRows][SPL];
+        Hdr hd[kRows][SPL];
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            uint32_t row = row0 + r * rpi;
+            uint32_t rr = row < a.n ? row : a.n - 1; /* clamp: loads stay in bounds */
+            const uint8_t *wrow = a.w + (uint64_t)rr * a.w_row_stride;
+#pragma unroll
+            for (int s = 0; s < SPL; ++s) load_chunk<SCHEME>(wrow, cis[s], qs[r][s], hd[r][s]);
+        }
+        /* 2. the codebook table is built while the loads are in flight */
         if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
             if (seg == 0) {
                 init_iq4_lut(lut, threadIdx.x, blockDim.x);
@@ -108,53 +115,50 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
                 chunk_dot<SCHEME, XF32, M>(qs[r][s], hd[r][s], cis[s] & 7, xc[s], acc[r], lut);
     }
 
-    /* cross-lane sums of all kRows*M partials at once, then every lane
-     * writes the values it ended up owning */
+    /* cross-lane sums of all kRows*M partials at once; the lanes that end
+     * up holding a sum apply the epilogue and store it */
     constexpr int V = kRows * M;
-    float v[V];
-    int idx[V];
+    float v[1][V];
 #pragma unroll
     for (int r = 0; r < kRows; ++r)
 #pragma unroll
-        for (int t = 0; t < M; ++t) v[r * M + t] = acc[r][t];
-    const int live = reduce_scatter<V>(v, idx, lane, (int)lpr);
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-        if (i >= live) break;
-        const int r = idx[i] / M, t = idx[i] % M;
+        for (int t = 0; t < M; ++t) v[0][r * M + t] = acc[r][t];
+    lane_reduce_w<V, 1>(v, lane, a.lpr_log2, [&](int idx, const float (&val)[1]) {
+        const int r = idx / M, t = idx % M;
         const uint32_t row = row0 + r * rpi;
-        if (row >= a.n) continue;
-        float val = v[i];
-        if (a.epilogue == R9VX_EPILOGUE_BIAS) val += a.bias[row];
-        if (a.epilogue == R9VX_EPILOGUE_RESIDUAL) val += a.residual[(uint64_t)t * a.n + row];
+        if (row >= a.n) return;
+        float y = val[0];
+        if (a.epilogue == R9VX_EPILOGUE_BIAS) y += a.bias[row];
+        if (a.epilogue == R9VX_EPILOGUE_RESIDUAL) y += a.residual[(uint64_t)t * a.n + row];
         const uint64_t o = (uint64_t)t * a.n + row;
         if (a.y_bf16)
-            reinterpret_cast<uint16_t *>(a.y)[o] = r9vx_f32_to_bf16(val);
+            reinterpret_cast<uint16_t *>(a.y)[o] = r9vx_f32_to_bf16(y);
         else
-            reinterpret_cast<float *>(a.y)[o] = val;
-    }
+            reinterpret_cast<float *>(a.y)[o] = y;
+    });
 }
 
-template <int SCHEME, bool XF32, int SPL>
-int launch_m(const GemvArgs &a, uint32_t m, dim3 grid, hipStream_t s) {
-    switch (m) {
-#define R9VX_CASE(MM)                                                                          \
-    case MM:                                                                                   \
-        hipLaunchKernelGGL((gemv_kernel<SCHEME, MM, XF32, SPL>), grid, dim3(256), 0, s, a); \
-        break;
-        R9VX_CASE(1) R9VX_CASE(2) R9VX_CASE(3) R9VX_CASE(4)
-        R9VX_CASE(5) R9VX_CASE(6) R9VX_CASE(7) R9VX_CASE(8)
-#undef R9VX_CASE
-    default:
+template <int SCHEME, bool XF32, int SPL, int MM>
+int launch_one(const GemvArgs &a, uint32_t m, uint32_t rows_per_slot_group, hipStream_t s) {
+    if constexpr (MM == 0) {
         return (int)hipErrorInvalidValue;
+    } else {
+        if (m != MM) return launch_one<SCHEME, XF32, SPL, MM - 1>(a, m, rows_per_slot_group, s);
+        /* rows_per_slot_group = lane groups per wave (64 / LPR) */
+        const uint32_t rows_per_wave = rows_per_slot_group * rows_for(MM);
+        const uint32_t waves = (a.n + rows_per_wave - 1) / rows_per_wave;
+        const dim3 grid((waves + waves_for(MM) - 1) / waves_for(MM));
+        hipLaunchKernelGGL((gemv_kernel<SCHEME, MM, XF32, SPL>), grid, dim3(waves_for(MM) * 64), 0, s, a);
+        return (int)hipGetLastError();
     }
-    return (int)hipGetLastError();
 }
 
+/* Two chunks per lane are only instantiated for the row counts the launcher
+ * picks them for (M <= 4 bf16, M <= 2 f32). */
 template <int SCHEME>
-int launch_scheme(const GemvArgs &a, uint32_t m, bool xf32, int spl, dim3 grid, hipStream_t s) {
-    if (xf32) return spl == 2 ? launch_m<SCHEME, true, 2>(a, m, grid, s) : launch_m<SCHEME, true, 1>(a, m, grid, s);
-    return spl == 2 ? launch_m<SCHEME, false, 2>(a, m, grid, s) : launch_m<SCHEME, false, 1>(a, m, grid, s);
+int launch_scheme(const GemvArgs &a, uint32_t m, bool xf32, int spl, uint32_t g, hipStream_t s) {
+    if (xf32) return spl == 2 ? launch_one<SCHEME, true, 2, 2>(a, m, g, s) : launch_one<SCHEME, true, 1, 8>(a, m, g, s);
+    return spl == 2 ? launch_one<SCHEME, false, 2, 4>(a, m, g, s) : launch_one<SCHEME, false, 1, 8>(a, m, g, s);
 }
 
 }  // namespace
@@ -184,10 +188,8 @@ int r9vx_launch_gemv(const r9vx_gemv_problem &p, hipStream_t stream) {
     a.nseg = cpr / (lpr * spl);
     a.y_bf16 = p.y_dtype == R9VX_DTYPE_BF16;
     a.epilogue = p.epilogue;
-    const uint32_t rows_per_wave = (64 / lpr) * kRows;
-    const uint32_t waves = (p.n + rows_per_wave - 1) / rows_per_wave;
-    dim3 grid((waves + 3) / 4);
+    const uint32_t groups = 64 / lpr;
     const bool xf32 = p.x_dtype == R9VX_DTYPE_F32;
-    if (p.scheme == R9VX_SCHEME_Q4_K) return launch_scheme<R9VX_SCHEME_Q4_K>(a, p.m, xf32, spl, grid, stream);
-    return launch_scheme<R9VX_SCHEME_IQ4_XS>(a, p.m, xf32, spl, grid, stream);
+    if (p.scheme == R9VX_SCHEME_Q4_K) return launch_scheme<R9VX_SCHEME_Q4_K>(a, p.m, xf32, spl, groups, stream);
+    return launch_scheme<R9VX_SCHEME_IQ4_XS>(a, p.m, xf32, spl, groups, stream);
 }

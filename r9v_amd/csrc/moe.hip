@@ -266,10 +266,24 @@ struct FfnArgs {
     uint32_t dn_lpr_log2, dn_nseg;
 };
 
-/* Rows per lane group per wave: fewer when more activation rows are live,
- * so that the activation registers of MT rows fit without spilling. */
-constexpr int pairs_for(int mt) { return mt <= 1 ? 4 : (mt <= 2 ? 4 : 2); }
-constexpr int dn_rows_for(int mt) { return mt <= 1 ? 8 : (mt <= 2 ? 4 : 2); }
+/* Decode launch shape (compile-time tuning constants): activation rows per
+ * pass, gate/up row pairs and down rows per lane group per wave, waves per
+ * workgroup. */
+#ifndef R9VX_DEC_MT
+#define R9VX_DEC_MT 1
+#endif
+#ifndef R9VX_DEC_GU_PAIRS
+#define R9VX_DEC_GU_PAIRS 1
+#endif
+#ifndef R9VX_DEC_DN_ROWS
+#define R9VX_DEC_DN_ROWS 2
+#endif
+#ifndef R9VX_DEC_WAVES
+#define R9VX_DEC_WAVES 2
+#endif
+constexpr int kDecPairs = R9VX_DEC_GU_PAIRS;
+constexpr int kDecDnRows = R9VX_DEC_DN_ROWS;
+constexpr int kDecWaves = R9VX_DEC_WAVES;
 
 __device__ __forceinline__ bool refused(const FfnArgs &a) {
     return reinterpret_cast<const uint32_t *>(a.ws + a.L.status)[0] != 0u;
@@ -282,17 +296,19 @@ __device__ __forceinline__ uint32_t token_of(const FfnArgs &a, uint32_t expert, 
 
 /* gate/up GEMV + SwiGLU for one work item; block = 4 waves over Dff rows. */
 template <int GU, int MT>
-__global__ __launch_bounds__(256) void moe_gu_kernel(FfnArgs a) {
-    constexpr int kPairs = pairs_for(MT);
+__global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
+    constexpr int kPairs = kDecPairs;
     __shared__ uint32_t lut[256];
+    __shared__ uint64_t etab[R9VX_EXP2F_N];
     const uint32_t *status = reinterpret_cast<const uint32_t *>(a.ws + a.L.status);
     if (status[0] != 0u || blockIdx.x >= status[2]) return;
+    r9vx_exp2_fill(etab, threadIdx.x, blockDim.x); /* ordered by the LUT's barrier */
     r9vx_u32x4 wk = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.work)[blockIdx.x];
     const uint32_t expert = wk.x, beg = wk.y, cnt = wk.z;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t lpr = 1u << a.gu_lpr_log2, rpi = 64u >> a.gu_lpr_log2;
     const uint32_t lir = lane & (lpr - 1), slot = lane >> a.gu_lpr_log2;
-    const uint32_t wave = blockIdx.y * 4 + (threadIdx.x >> 6);
+    const uint32_t wave = blockIdx.y * kDecWaves + (threadIdx.x >> 6);
     const uint32_t r0 = wave * rpi * kPairs + slot;
     const uint8_t *wexp = a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes;
     float *h = reinterpret_cast<float *>(a.ws + a.L.h);
@@ -314,7 +330,11 @@ __global__ __launch_bounds__(256) void moe_gu_kernel(FfnArgs a) {
         for (uint32_t seg = 0; seg < a.gu_nseg; ++seg) {
             uint32_t ci = seg * lpr + lir, klo, khi;
             chunk_k<GU>(ci, klo, khi);
-            /* weights first, then activations, then the table: one latency */
+            /* activations (L2-resident), then weights, then the table */
+            XRaw<false> xr[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                if (t < m) load_x_raw<false>(xrow[t], klo, khi, xr[t]);
             r9vx_u32x4 qg[kPairs], qu[kPairs];
             Hdr hg[kPairs], hu[kPairs];
 #pragma unroll
@@ -324,16 +344,10 @@ __global__ __launch_bounds__(256) void moe_gu_kernel(FfnArgs a) {
                 load_chunk<GU>(wexp + (uint64_t)rr * a.gu_row_bytes, ci, qg[r], hg[r]);
                 load_chunk<GU>(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes, ci, qu[r], hu[r]);
             }
-            XRaw<false> xr[MT];
-#pragma unroll
-            for (int t = 0; t < MT; ++t)
-                if (t < m) load_x_raw<false>(xrow[t], klo, khi, xr[t]);
-            if constexpr (GU == R9VX_SCHEME_IQ4_XS) {
-                if (!lut_ready) {
-                    init_iq4_lut(lut, threadIdx.x, blockDim.x);
-                    __syncthreads();
-                    lut_ready = true;
-                }
+            if (!lut_ready) { /* codebook and exp tables visible to every wave */
+                if constexpr (GU == R9VX_SCHEME_IQ4_XS) init_iq4_lut(lut, threadIdx.x, blockDim.x);
+                __syncthreads();
+                lut_ready = true;
             }
             XChunk<GU, false> xc[MT];
 #pragma unroll
@@ -345,37 +359,32 @@ __global__ __launch_bounds__(256) void moe_gu_kernel(FfnArgs a) {
                 chunk_dot<GU, false, MT>(qu[r], hu[r], ci & 7, xc, au[r], lut, m);
             }
         }
-        /* g and u go through the same reduce-scatter, so slot i of both
-         * holds the same (row, token) */
+        /* g and u go through the same reduction, so each emitted slot
+         * carries both halves of one (row, token) */
         constexpr int V = kPairs * MT;
-        float gv[V], uv[V];
-        int gi[V], ui[V];
+        float gu[2][V];
 #pragma unroll
         for (int r = 0; r < kPairs; ++r)
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
-                gv[r * MT + t] = ag[r][t];
-                uv[r * MT + t] = au[r][t];
+                gu[0][r * MT + t] = ag[r][t];
+                gu[1][r * MT + t] = au[r][t];
             }
-        const int live = reduce_scatter<V>(gv, gi, lane, (int)lpr);
-        reduce_scatter<V>(uv, ui, lane, (int)lpr);
-#pragma unroll
-        for (int i = 0; i < V; ++i) {
-            if (i >= live) break;
-            const int r = gi[i] / MT, t = gi[i] % MT;
+        lane_reduce_w<V, 2>(gu, lane, a.gu_lpr_log2, [&](int idx, const float (&val)[2]) {
+            const int r = idx / MT, t = idx % MT;
             const uint32_t row = r0 + r * rpi;
-            if (t >= m || row >= a.dff) continue;
-            const float g = gv[i];
-            const float act = g / (1.0f + r9vx_expf(-g));
-            h[(uint64_t)(beg + t0 + t) * a.dff + row] = act * uv[i];
-        }
+            if (t >= m || row >= a.dff) return;
+            const float g = val[0];
+            const float act = g / (1.0f + r9vx_expf_tab(-g, etab));
+            h[(uint64_t)(beg + t0 + t) * a.dff + row] = act * val[1];
+        });
     }
 }
 
 /* down GEMV for one work item: o[pos, d] = h[pos, :] . Wd[d, :]. */
 template <int DN, int MT>
-__global__ __launch_bounds__(256) void moe_down_kernel(FfnArgs a) {
-    constexpr int kDnRows = dn_rows_for(MT);
+__global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
+    constexpr int kDnRows = kDecDnRows;
     __shared__ uint32_t lut[256];
     const uint32_t *status = reinterpret_cast<const uint32_t *>(a.ws + a.L.status);
     if (status[0] != 0u || blockIdx.x >= status[2]) return;
@@ -384,7 +393,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(FfnArgs a) {
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t lpr = 1u << a.dn_lpr_log2, rpi = 64u >> a.dn_lpr_log2;
     const uint32_t lir = lane & (lpr - 1), slot = lane >> a.dn_lpr_log2;
-    const uint32_t wave = blockIdx.y * 4 + (threadIdx.x >> 6);
+    const uint32_t wave = blockIdx.y * kDecWaves + (threadIdx.x >> 6);
     const uint32_t r0 = wave * rpi * kDnRows + slot;
     const uint8_t *wexp = a.w_dn + (uint64_t)expert * a.dm * a.dn_row_bytes;
     const float *h = reinterpret_cast<const float *>(a.ws + a.L.h);
@@ -401,6 +410,10 @@ __global__ __launch_bounds__(256) void moe_down_kernel(FfnArgs a) {
         for (uint32_t seg = 0; seg < a.dn_nseg; ++seg) {
             uint32_t ci = seg * lpr + lir, klo, khi;
             chunk_k<DN>(ci, klo, khi);
+            XRaw<true> xr[MT];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                if (t < m) load_x_raw<true>(h + (uint64_t)(beg + t0 + t) * a.dff, klo, khi, xr[t]);
             r9vx_u32x4 q[kDnRows];
             Hdr hd[kDnRows];
 #pragma unroll
@@ -409,10 +422,6 @@ __global__ __launch_bounds__(256) void moe_down_kernel(FfnArgs a) {
                 uint32_t rr = row < a.dm ? row : a.dm - 1;
                 load_chunk<DN>(wexp + (uint64_t)rr * a.dn_row_bytes, ci, q[r], hd[r]);
             }
-            XRaw<true> xr[MT];
-#pragma unroll
-            for (int t = 0; t < MT; ++t)
-                if (t < m) load_x_raw<true>(h + (uint64_t)(beg + t0 + t) * a.dff, klo, khi, xr[t]);
             if constexpr (DN == R9VX_SCHEME_IQ4_XS) {
                 if (!lut_ready) {
                     init_iq4_lut(lut, threadIdx.x, blockDim.x);
@@ -428,21 +437,17 @@ __global__ __launch_bounds__(256) void moe_down_kernel(FfnArgs a) {
             for (int r = 0; r < kDnRows; ++r) chunk_dot<DN, true, MT>(q[r], hd[r], ci & 7, xc, acc[r], lut, m);
         }
         constexpr int V = kDnRows * MT;
-        float v[V];
-        int vi[V];
+        float v[1][V];
 #pragma unroll
         for (int r = 0; r < kDnRows; ++r)
 #pragma unroll
-            for (int t = 0; t < MT; ++t) v[r * MT + t] = acc[r][t];
-        const int live = reduce_scatter<V>(v, vi, lane, (int)lpr);
-#pragma unroll
-        for (int i = 0; i < V; ++i) {
-            if (i >= live) break;
-            const int r = vi[i] / MT, t = vi[i] % MT;
+            for (int t = 0; t < MT; ++t) v[0][r * MT + t] = acc[r][t];
+        lane_reduce_w<V, 1>(v, lane, a.dn_lpr_log2, [&](int idx, const float (&val)[1]) {
+            const int r = idx / MT, t = idx % MT;
             const uint32_t row = r0 + r * rpi;
-            if (t >= m || row >= a.dm) continue;
-            o[(uint64_t)(beg + t0 + t) * a.dm + row] = v[i];
-        }
+            if (t >= m || row >= a.dm) return;
+            o[(uint64_t)(beg + t0 + t) * a.dm + row] = val[0];
+        });
     }
 }
 
@@ -479,21 +484,25 @@ __global__ __launch_bounds__(256) void r9vx_moe_combine_kernel(MoeCombineArgs a)
     const uint32_t d0 = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (d0 >= a.dm) return;
     const float *o = reinterpret_cast<const float *>(a.ws + a.L.o);
-    r9vx_f32x4 rows[kMoeMaxK];
-#pragma unroll
-    for (uint32_t j = 0; j < kMoeMaxK; ++j) {
-        if (j >= kk) break;
-        rows[j] = *reinterpret_cast<const r9vx_f32x4 *>(o + (uint64_t)opos[j] * a.dm + d0);
-    }
     r9vx_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    /* Eight rows in flight at a time; rows[] is indexed by constants only so
+     * it stays in registers. */
+    for (uint32_t jb = 0; jb < kk; jb += 8) {
+        r9vx_f32x4 rows[8];
 #pragma unroll
-    for (uint32_t j = 0; j < kMoeMaxK; ++j) {
-        if (j >= kk) break;
-        const float w = ow[j];
-        acc.x = acc.x + w * rows[j].x;
-        acc.y = acc.y + w * rows[j].y;
-        acc.z = acc.z + w * rows[j].z;
-        acc.w = acc.w + w * rows[j].w;
+        for (uint32_t j = 0; j < 8; ++j)
+            if (jb + j < kk)
+                rows[j] = *reinterpret_cast<const r9vx_f32x4 *>(o + (uint64_t)opos[jb + j] * a.dm + d0);
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            if (jb + j < kk) {
+                const float w = ow[jb + j];
+                acc.x = acc.x + w * rows[j].x;
+                acc.y = acc.y + w * rows[j].y;
+                acc.z = acc.z + w * rows[j].z;
+                acc.w = acc.w + w * rows[j].w;
+            }
+        }
     }
     for (uint32_t s = 0; s < a.shared; ++s) {
         r9vx_f32x4 v = *reinterpret_cast<const r9vx_f32x4 *>(o + (uint64_t)(a.p + s * a.t + t) * a.dm + d0);
@@ -534,18 +543,18 @@ int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream
 template <int MT>
 static void launch_decode_mt(const FfnArgs &f, uint32_t gu_scheme, uint32_t dn_scheme, uint32_t max_work,
                              hipStream_t s) {
-    const uint32_t gu_rows_per_block = 4 * (64u >> f.gu_lpr_log2) * pairs_for(MT);
-    const uint32_t dn_rows_per_block = 4 * (64u >> f.dn_lpr_log2) * dn_rows_for(MT);
+    const uint32_t gu_rows_per_block = kDecWaves * (64u >> f.gu_lpr_log2) * kDecPairs;
+    const uint32_t dn_rows_per_block = kDecWaves * (64u >> f.dn_lpr_log2) * kDecDnRows;
     dim3 ggu(max_work, (f.dff + gu_rows_per_block - 1) / gu_rows_per_block);
     dim3 gdn(max_work, (f.dm + dn_rows_per_block - 1) / dn_rows_per_block);
     if (gu_scheme == R9VX_SCHEME_IQ4_XS)
-        hipLaunchKernelGGL((moe_gu_kernel<R9VX_SCHEME_IQ4_XS, MT>), ggu, dim3(256), 0, s, f);
+        hipLaunchKernelGGL((moe_gu_kernel<R9VX_SCHEME_IQ4_XS, MT>), ggu, dim3(kDecWaves * 64), 0, s, f);
     else
-        hipLaunchKernelGGL((moe_gu_kernel<R9VX_SCHEME_Q4_K, MT>), ggu, dim3(256), 0, s, f);
+        hipLaunchKernelGGL((moe_gu_kernel<R9VX_SCHEME_Q4_K, MT>), ggu, dim3(kDecWaves * 64), 0, s, f);
     if (dn_scheme == R9VX_SCHEME_Q4_K)
-        hipLaunchKernelGGL((moe_down_kernel<R9VX_SCHEME_Q4_K, MT>), gdn, dim3(256), 0, s, f);
+        hipLaunchKernelGGL((moe_down_kernel<R9VX_SCHEME_Q4_K, MT>), gdn, dim3(kDecWaves * 64), 0, s, f);
     else
-        hipLaunchKernelGGL((moe_down_kernel<R9VX_SCHEME_IQ4_XS, MT>), gdn, dim3(256), 0, s, f);
+        hipLaunchKernelGGL((moe_down_kernel<R9VX_SCHEME_IQ4_XS, MT>), gdn, dim3(kDecWaves * 64), 0, s, f);
 }
 
 int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s) {
@@ -569,10 +578,7 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
     f.gu_lpr_log2 = lpr_for(p.dm, f.gu_nseg);
     f.dn_lpr_log2 = lpr_for(p.dff, f.dn_nseg);
     uint32_t max_work = (f.p < p.e ? f.p : p.e) + p.shared;
-    /* Decode routes mostly one token to an expert: one activation row per
-     * pass keeps the registers for rows and loads in flight; an expert with
-     * more tokens re-reads its rows from L2 once per token. */
-    launch_decode_mt<1>(f, p.scheme_gu, p.scheme_dn, max_work, s);
+    launch_decode_mt<R9VX_DEC_MT>(f, p.scheme_gu, p.scheme_dn, max_work, s);
     return (int)hipGetLastError();
 }
 

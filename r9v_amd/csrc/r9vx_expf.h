@@ -57,55 +57,90 @@ static const uint64_t r9vx_exp2_table_host[32] = R9VX_EXP2_TAB_INIT;
 static inline uint64_t r9vx_exp2_tab(uint32_t i) { return r9vx_exp2_table_host[i & 31u]; }
 #endif
 
+/* The evaluation, with TAB(i) supplying table entry i (0..31). */
+#define R9VX_EXPF_BODY(TAB)                                                                       \
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * R9VX_EXP2F_N;                                 \
+    const double shift = 0x1.8p+52;                                                               \
+    /* Cubic for 2^(r/N), coefficients pre-divided by N^3, N^2, N. */                             \
+    const double c0 = 0x1.c6af84b912394p-5 / R9VX_EXP2F_N / R9VX_EXP2F_N / R9VX_EXP2F_N;          \
+    const double c1 = 0x1.ebfce50fac4f3p-3 / R9VX_EXP2F_N / R9VX_EXP2F_N;                         \
+    const double c2 = 0x1.62e42ff0c52d6p-1 / R9VX_EXP2F_N;                                        \
+    uint32_t ux;                                                                                  \
+    R9VX_BITS(ux, x);                                                                             \
+    uint32_t abstop = (ux >> 20) & 0x7ffu;                                                        \
+    if (abstop >= 0x42bu) { /* |x| >= 88, inf or nan (top12(88.0f) = 0x42b) */                   \
+        if (ux == 0xff800000u) return 0.0f;                                                       \
+        if (abstop >= 0x7f8u) return x + x;                                                       \
+        if (x > 0x1.62e42ep6f) return __builtin_huge_valf();                                      \
+        if (x < -0x1.9fe368p6f) return 0.0f;                                                      \
+    }                                                                                             \
+    double xd = (double)x;                                                                        \
+    double kd = fma(inv_ln2_n, xd, shift);                                                        \
+    uint64_t ki;                                                                                  \
+    R9VX_BITS(ki, kd);                                                                            \
+    kd -= shift;                                                                                  \
+    double r = fma(inv_ln2_n, xd, -kd);                                                           \
+    uint64_t t = TAB((uint32_t)(ki % R9VX_EXP2F_N));                                              \
+    t += ki << (52 - 5);                                                                          \
+    double s;                                                                                     \
+    R9VX_BITS(s, t);                                                                              \
+    double z = fma(c0, r, c1);                                                                    \
+    double r2 = r * r;                                                                            \
+    double y = fma(c2, r, 1.0);                                                                   \
+    y = fma(z, r2, y);                                                                            \
+    y = y * s;                                                                                    \
+    return (float)y;
+
 #if defined(__HIPCC__)
-__host__ __device__ inline
-#else
-static inline
-#endif
-float r9vx_expf(float x) {
+#define R9VX_BITS(dst, src) (dst) = __builtin_bit_cast(decltype(dst), (src))
+__host__ __device__ inline float r9vx_expf(float x) { R9VX_EXPF_BODY(r9vx_exp2_tab) }
+/* Same function with the table in LDS (or any memory the caller filled with
+ * r9vx_exp2_fill): a table lookup per call from constant memory is a global
+ * load, and the special-case branches keep the compiler from batching them. */
+__device__ inline float r9vx_expf_tab(float x, const uint64_t *tab) {
+#define R9VX_TAB_PTR(i) tab[(i)]
+    R9VX_EXPF_BODY(R9VX_TAB_PTR)
+#undef R9VX_TAB_PTR
+}
+/* Branch-free form of r9vx_expf_tab, bit-identical to it: the main path runs
+ * for every input (its table index is always in range) and the special
+ * cases are applied afterwards by selects in reverse priority, so a caller's
+ * loop over many inputs issues all of its table reads together. */
+__device__ inline float r9vx_expf_tab_nb(float x, const uint64_t *tab) {
     const double inv_ln2_n = 0x1.71547652b82fep+0 * R9VX_EXP2F_N;
     const double shift = 0x1.8p+52;
-    /* Cubic for 2^(r/N), coefficients pre-divided by N^3, N^2, N. */
     const double c0 = 0x1.c6af84b912394p-5 / R9VX_EXP2F_N / R9VX_EXP2F_N / R9VX_EXP2F_N;
     const double c1 = 0x1.ebfce50fac4f3p-3 / R9VX_EXP2F_N / R9VX_EXP2F_N;
     const double c2 = 0x1.62e42ff0c52d6p-1 / R9VX_EXP2F_N;
-    uint32_t ux;
-#if defined(__HIPCC__)
-    ux = __builtin_bit_cast(uint32_t, x);
-#else
-    memcpy(&ux, &x, 4);
-#endif
-    uint32_t abstop = (ux >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) { /* |x| >= 88, inf or nan (top12(88.0f) = 0x42b) */
-        if (ux == 0xff800000u) return 0.0f;
-        if (abstop >= 0x7f8u) return x + x;
-        if (x > 0x1.62e42ep6f) return __builtin_huge_valf();
-        if (x < -0x1.9fe368p6f) return 0.0f;
-    }
-    double xd = (double)x;
+    const uint32_t ux = __builtin_bit_cast(uint32_t, x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    const double xd = (double)x;
     double kd = fma(inv_ln2_n, xd, shift);
-    uint64_t ki;
-#if defined(__HIPCC__)
-    ki = __builtin_bit_cast(uint64_t, kd);
-#else
-    memcpy(&ki, &kd, 8);
-#endif
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
     kd -= shift;
-    double r = fma(inv_ln2_n, xd, -kd);
-    uint64_t t = r9vx_exp2_tab((uint32_t)(ki % R9VX_EXP2F_N));
+    const double r = fma(inv_ln2_n, xd, -kd);
+    uint64_t t = tab[(uint32_t)(ki % R9VX_EXP2F_N)];
     t += ki << (52 - 5);
-    double s;
-#if defined(__HIPCC__)
-    s = __builtin_bit_cast(double, t);
-#else
-    memcpy(&s, &t, 8);
-#endif
-    double z = fma(c0, r, c1);
-    double r2 = r * r;
+    const double sc = __builtin_bit_cast(double, t);
+    const double z = fma(c0, r, c1);
+    const double r2 = r * r;
     double y = fma(c2, r, 1.0);
     y = fma(z, r2, y);
-    y = y * s;
-    return (float)y;
+    y = y * sc;
+    const float main = (float)y;
+    float sp = main; /* 88 <= |x| inside the finite range: the main path */
+    sp = x < -0x1.9fe368p6f ? 0.0f : sp;
+    sp = x > 0x1.62e42ep6f ? __builtin_huge_valf() : sp;
+    sp = abstop >= 0x7f8u ? x + x : sp;
+    sp = ux == 0xff800000u ? 0.0f : sp;
+    return abstop >= 0x42bu ? sp : main;
 }
+__device__ inline void r9vx_exp2_fill(uint64_t *tab, uint32_t tid, uint32_t nthreads) {
+    for (uint32_t i = tid; i < R9VX_EXP2F_N; i += nthreads) tab[i] = r9vx_exp2_table[i];
+}
+#else
+#define R9VX_BITS(dst, src) memcpy(&(dst), &(src), sizeof(dst))
+static inline float r9vx_expf(float x) { R9VX_EXPF_BODY(r9vx_exp2_tab) }
+#endif
 
 #endif

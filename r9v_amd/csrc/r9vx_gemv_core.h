@@ -241,44 +241,131 @@ __device__ __forceinline__ void chunk_dot(const r9vx_u32x4 &qs, const Hdr &h, ui
 }
 
 
-/* Sums each of the V values over the `width` lanes of its aligned lane
- * group (width a power of two, 8..64), halving the live values at every
- * butterfly step: the lane whose step bit is set keeps the upper half and
- * sends the lower half, the other keeps the lower half.  Afterwards the lane
- * holds ceil-halved subsets of fully reduced values; owner(i, lane_in_group)
- * tells which original index ends in slot 0..  This costs about 4 ops per
- * value in total instead of 2 per value per step.
+/* ---- cross-lane sums of per-lane partials --------------------------------
  *
- * Returns the number of live slots; idx[s] = original index of slot s. */
-template <int V>
-__device__ __forceinline__ int reduce_scatter(float (&v)[V], int (&idx)[V], uint32_t lane, int width) {
+ * A row's partial sums sit in WIDTH consecutive lanes (an aligned group of 8,
+ * 16, 32 or 64).  lane_reduce sums N arrays of V partials over the group:
+ *  - across 32 and 16 lanes it reduce-scatters with the gfx950 permlane
+ *    swaps: v_permlane32_swap(a, b) leaves {a[0..31], b[0..31]} and
+ *    {a[32..63], b[32..63]}, so one add gives lanes 0..31 the sum of a and
+ *    lanes 32..63 the sum of b (permlane16_swap does the same between
+ *    neighbouring 16-lane rows).  Each step halves the live values; an odd
+ *    leftover is swapped with itself and so reduced whole in both halves.
+ *  - inside a 16-lane row it finishes with a DPP butterfly (row mirror, half-
+ *    row mirror, quad reversal, quad pair swap), after which all lanes of the
+ *    row hold the same live values.
+ * Lane l of each row then emits the live slots s with s % G == l % G (G =
+ * min(WIDTH, 16)) as emit(original index, values[N]); a leftover is emitted
+ * once, by the half that kept the lower values. */
+__device__ __forceinline__ float swap_sum32(float a, float b) {
+    auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                              false, false);
+    /* copy the elements out first: __builtin_bit_cast of r[1] in place
+     * reads element 0 with this compiler */
+    const uint32_t lo = r[0], hi = r[1];
+    return __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
+}
+__device__ __forceinline__ float swap_sum16(float a, float b) {
+    auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                              false, false);
+    /* copy the elements out first: __builtin_bit_cast of r[1] in place
+     * reads element 0 with this compiler */
+    const uint32_t lo = r[0], hi = r[1];
+    return __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+    return x + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF,
+                                                                     false));
+}
+
+template <int V, int WIDTH>
+struct LaneReduce {
+    static constexpr int kC32 = WIDTH > 32 ? (V + 1) / 2 : V;    /* live after the 32-lane step */
+    static constexpr int kLive = WIDTH > 16 ? (kC32 + 1) / 2 : kC32;
+    static constexpr int kG = WIDTH < 16 ? WIDTH : 16;
+};
+
+template <int V, int WIDTH, int N, typename Emit>
+__device__ __forceinline__ void lane_reduce(float (&v)[N][V], uint32_t lane, Emit &&emit) {
+    using LR = LaneReduce<V, WIDTH>;
+    if constexpr (WIDTH > 32) {
+        constexpr int h = V / 2;
 #pragma unroll
-    for (int i = 0; i < V; ++i) idx[i] = i;
-    int c = V;
+        for (int n = 0; n < N; ++n) {
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-        if (d >= width) continue;
-        const bool up = (lane & (uint32_t)d) != 0;
-        const int h = c / 2;
-#pragma unroll
-        for (int i = 0; i < V / 2 + 1; ++i) {
-            if (i >= h) break;
-            float a = v[i], b = v[i + h];
-            float send = up ? a : b;
-            float keep = up ? b : a;
-            v[i] = keep + __shfl_xor(send, d, 64);
-            idx[i] = up ? idx[i + h] : idx[i];
-        }
-        if (c & 1) { /* odd leftover: reduce it whole, keep it as slot h */
-            float a = v[c - 1];
-            v[h] = a + __shfl_xor(a, d, 64);
-            idx[h] = idx[c - 1];
-            c = h + 1;
-        } else {
-            c = h;
+            for (int i = 0; i < h; ++i) v[n][i] = swap_sum32(v[n][i], v[n][i + h]);
+            if constexpr (V & 1) v[n][h] = swap_sum32(v[n][V - 1], v[n][V - 1]);
         }
     }
-    return c;
+    if constexpr (WIDTH > 16) {
+        constexpr int C = LR::kC32, h = C / 2;
+#pragma unroll
+        for (int n = 0; n < N; ++n) {
+#pragma unroll
+            for (int i = 0; i < h; ++i) v[n][i] = swap_sum16(v[n][i], v[n][i + h]);
+            if constexpr (C & 1) v[n][h] = swap_sum16(v[n][C - 1], v[n][C - 1]);
+        }
+    }
+    constexpr int C = LR::kLive;
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+#pragma unroll
+        for (int i = 0; i < C; ++i) {
+            float x = v[n][i];
+            if constexpr (WIDTH > 8) x = dpp_add<0x140>(x); /* row_mirror: l <-> 15 - l */
+            x = dpp_add<0x141>(x);                          /* row_half_mirror: l <-> 7 - l */
+            x = dpp_add<0x1B>(x);                           /* quad_perm 3,2,1,0 */
+            x = dpp_add<0xB1>(x);                           /* quad_perm 1,0,3,2 */
+            v[n][i] = x;
+        }
+    constexpr int G = LR::kG;
+    const int gl = (int)(lane & (uint32_t)(G - 1));
+#pragma unroll
+    for (int q = 0; q < (C + G - 1) / G; ++q) {
+        const int s = gl + q * G;
+        if (s >= C) break;
+        float val[N];
+#pragma unroll
+        for (int n = 0; n < N; ++n) {
+            val[n] = v[n][0];
+#pragma unroll
+            for (int i = 1; i < C; ++i)
+                if (s == i) val[n] = v[n][i];
+        }
+        int j = s;
+        bool dup = false;
+        if constexpr (WIDTH > 16) {
+            constexpr int h = LR::kC32 / 2;
+            if (j < h) {
+                if (lane & 16u) j += h;
+            } else {
+                j = LR::kC32 - 1;
+                dup = dup || (lane & 16u) != 0;
+            }
+        }
+        if constexpr (WIDTH > 32) {
+            constexpr int h = V / 2;
+            if (j < h) {
+                if (lane & 32u) j += h;
+            } else {
+                j = V - 1;
+                dup = dup || (lane & 32u) != 0;
+            }
+        }
+        if (!dup) emit(j, val);
+    }
+}
+
+/* lane_reduce for a runtime group width (8, 16, 32 or 64 = 1 << log2). */
+template <int V, int N, typename Emit>
+__device__ __forceinline__ void lane_reduce_w(float (&v)[N][V], uint32_t lane, uint32_t width_log2, Emit &&emit) {
+    switch (width_log2) {
+    case 6: lane_reduce<V, 64, N>(v, lane, emit); break;
+    case 5: lane_reduce<V, 32, N>(v, lane, emit); break;
+    case 4: lane_reduce<V, 16, N>(v, lane, emit); break;
+    default: lane_reduce<V, 8, N>(v, lane, emit); break;
+    }
 }
 
 /* IQ4_XS bf16 codebook-pair table: entry b = {kv[b & 15], kv[b >> 4]}. */

@@ -27,7 +27,6 @@ namespace {
 
 __device__ uint32_t g_route_status;
 
-constexpr int kMaxPerLane = 16; /* E <= 1024 */
 constexpr int kMaxK = 32;
 
 struct RouteArgs {
@@ -39,17 +38,39 @@ struct RouteArgs {
     float scale;
 };
 
-__device__ __forceinline__ float wave_max(float v) {
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+/* Wave-wide max without LDS: a DPP butterfly inside each 16-lane row (row
+ * mirror, half-row mirror, quad reversal, quad pair swap), then the gfx950
+ * permlane swaps pair rows 0/1, 2/3 and halves 0/1.  Every lane ends with
+ * the result. */
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ void swap_halves16(uint32_t x, uint32_t &a, uint32_t &b) {
+    auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    a = r[0];
+    b = r[1];
+}
+__device__ __forceinline__ void swap_halves32(uint32_t x, uint32_t &a, uint32_t &b) {
+    auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    a = r[0];
+    b = r[1];
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-    for (int off = 32; off > 0; off >>= 1) {
-        uint64_t o = __shfl_xor(v, off, 64);
-        v = o > v ? o : v;
-    }
-    return v;
+__device__ __forceinline__ float wave_max(float v) {
+    uint32_t x = __builtin_bit_cast(uint32_t, v);
+#define R9VX_FMAX_STEP(CTRL) x = __builtin_bit_cast(uint32_t, fmaxf(__builtin_bit_cast(float, x), \
+                                                               __builtin_bit_cast(float, dpp_u32<CTRL>(x))))
+    R9VX_FMAX_STEP(0x140);
+    R9VX_FMAX_STEP(0x141);
+    R9VX_FMAX_STEP(0x1B);
+    R9VX_FMAX_STEP(0xB1);
+#undef R9VX_FMAX_STEP
+    uint32_t a, b;
+    swap_halves16(x, a, b);
+    x = __builtin_bit_cast(uint32_t, fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b)));
+    swap_halves32(x, a, b);
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
 }
 
 /* total_cmp order key of a float as an unsigned integer (larger = greater). */
@@ -85,90 +106,160 @@ __device__ __forceinline__ uint32_t check_row(const RouteArgs &a, uint32_t row, 
 }
 
 /* sum_{c=0}^{E-1} v[c] in ascending c with one f32 accumulator, v[c] held by
- * lane c % 64 in register c / 64.  Every lane runs the same chain: each term
- * is broadcast with readlane, so the order and the roundings are exactly the
- * reference's sequential loop. */
-__device__ __forceinline__ float ordered_sum(const float (&v)[kMaxPerLane], uint32_t e) {
-    /* a rotating copy keeps the register index static while the outer loop
-     * stays rolled (64 broadcasts per iteration, not 64 * 16) */
-    float q[kMaxPerLane];
+ * lane c % 64 in register c / 64.  The wave stores the values to its LDS
+ * slice in column order and every lane then runs the same sequential chain
+ * over broadcast LDS reads, so the order and the roundings are exactly the
+ * reference's loop. */
+template <int PER>
+__device__ __forceinline__ float ordered_sum(const float (&v)[PER], uint32_t e, uint32_t lane, float *buf) {
 #pragma unroll
-    for (int i = 0; i < kMaxPerLane; ++i) q[i] = v[i];
-    float sum = 0.0f;
-    for (uint32_t base = 0; base < e; base += 64) {
-        const int bits = __builtin_bit_cast(int, q[0]);
-        if (base + 64 <= e) {
-#pragma unroll
-            for (int l = 0; l < 64; ++l) sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, l));
-        } else {
-            for (uint32_t l = 0; l < e - base; ++l)
-                sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(bits, (int)l));
-        }
-#pragma unroll
-        for (int i = 0; i + 1 < kMaxPerLane; ++i) q[i] = q[i + 1];
+    for (int i = 0; i < PER; ++i) {
+        const uint32_t c = lane + 64 * i;
+        if (c < e) buf[c] = v[i];
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const r9vx_f32x4 *b4 = reinterpret_cast<const r9vx_f32x4 *>(buf);
+    float sum = 0.0f;
+    uint32_t c = 0;
+    for (; c + 16 <= e; c += 16) {
+        const r9vx_f32x4 q0 = b4[c / 4], q1 = b4[c / 4 + 1], q2 = b4[c / 4 + 2], q3 = b4[c / 4 + 3];
+        sum = sum + q0.x; sum = sum + q0.y; sum = sum + q0.z; sum = sum + q0.w;
+        sum = sum + q1.x; sum = sum + q1.y; sum = sum + q1.z; sum = sum + q1.w;
+        sum = sum + q2.x; sum = sum + q2.y; sum = sum + q2.z; sum = sum + q2.w;
+        sum = sum + q3.x; sum = sum + q3.y; sum = sum + q3.z; sum = sum + q3.w;
+    }
+    for (; c < e; ++c) sum = sum + buf[c];
     return sum;
 }
 
-__device__ __forceinline__ void route_row(const RouteArgs &a, uint32_t row, uint32_t lane) {
-    const uint32_t per = (a.e + 63) / 64;
-    float sc[kMaxPerLane];
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+#define R9VX_UMAX32_STEP(CTRL) x = max(x, dpp_u32<CTRL>(x))
+    R9VX_UMAX32_STEP(0x140);
+    R9VX_UMAX32_STEP(0x141);
+    R9VX_UMAX32_STEP(0x1B);
+    R9VX_UMAX32_STEP(0xB1);
+#undef R9VX_UMAX32_STEP
+    uint32_t a, b;
+    swap_halves16(x, a, b);
+    x = max(a, b);
+    swap_halves32(x, a, b);
+    return max(a, b);
+}
+
+/* Lane `lane` holds s[c] for c = lane + 64 i (i < PER, E <= 64 PER); -inf
+ * past E.  The loads are unconditional (clamped column) so that all of them
+ * are in flight at once; the bias branch is uniform. */
+template <int PER>
+__device__ __forceinline__ void load_row(const RouteArgs &a, uint32_t row, uint32_t lane, float (&sc)[PER],
+                                         float (&lg)[PER], float (&bs)[PER]) {
+    const float *lrow = a.logits + (uint64_t)row * a.e;
 #pragma unroll
-    for (int i = 0; i < kMaxPerLane; ++i) {
-        uint32_t c = lane + 64 * i;
-        float s = -__builtin_huge_valf();
-        if (i < (int)per && c < a.e) {
-            s = a.logits[(uint64_t)row * a.e + c];
-            if (a.bias) s = s + a.bias[c];
-        }
-        sc[i] = s;
+    for (int i = 0; i < PER; ++i) {
+        const uint32_t c = lane + 64 * i;
+        lg[i] = lrow[c < a.e ? c : a.e - 1];
     }
+    if (a.bias) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const uint32_t c = lane + 64 * i;
+            bs[i] = a.bias[c < a.e ? c : a.e - 1];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const uint32_t c = lane + 64 * i;
+        if (!a.bias) bs[i] = 0.0f;
+        sc[i] = c < a.e ? (a.bias ? lg[i] + bs[i] : lg[i]) : -__builtin_huge_valf();
+        if (c >= a.e) lg[i] = bs[i] = 0.0f;
+    }
+}
+
+/* Status bits of one loaded row (the tests of check_row). */
+template <int PER>
+__device__ __forceinline__ uint32_t check_loaded(const RouteArgs &a, uint32_t lane, const float (&sc)[PER],
+                                                 const float (&lg)[PER], const float (&bs)[PER],
+                                                 const uint64_t *etab) {
+    uint32_t bad = 0;
+    float smax = -__builtin_huge_valf();
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const uint32_t c = lane + 64 * i;
+        if (c < a.e) {
+            if (!__builtin_isfinite(lg[i]) || !__builtin_isfinite(bs[i]) || !__builtin_isfinite(sc[i]))
+                bad |= R9VX_STATUS_NONFINITE;
+            smax = fmaxf(smax, sc[i]);
+        }
+    }
+    if (a.scoring == R9VX_SCORING_SIGMOID && a.renormalize) {
+        smax = wave_max(smax);
+        float top = 1.0f / (1.0f + r9vx_expf_tab(-smax, etab));
+        if (top == 0.0f) bad |= R9VX_STATUS_DEGENERATE;
+    }
+    return bad;
+}
+
+/* Scores, top-K and weights of one loaded row; lane j < K returns the j-th
+ * selection in (id, w). */
+template <int PER>
+__device__ __forceinline__ void route_loaded(const RouteArgs &a, uint32_t lane, float (&sc)[PER],
+                                             const uint64_t *etab, float *buf, uint32_t &my_id, float &my_w) {
     if (a.scoring == R9VX_SCORING_SOFTMAX) {
         float mx = -__builtin_huge_valf();
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) mx = fmaxf(mx, sc[i]);
+        for (int i = 0; i < PER; ++i) mx = fmaxf(mx, sc[i]);
         mx = wave_max(mx);
+        /* padding holds -inf: exp(-inf - mx) = 0 */
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) {
-            uint32_t c = lane + 64 * i;
-            sc[i] = (i < (int)per && c < a.e) ? r9vx_expf(sc[i] - mx) : 0.0f;
-        }
-        const float sum = ordered_sum(sc, a.e);
+        for (int i = 0; i < PER; ++i) sc[i] = r9vx_expf_tab_nb(sc[i] - mx, etab);
+        const float sum = ordered_sum<PER>(sc, a.e, lane, buf);
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) {
-            uint32_t c = lane + 64 * i;
-            if (i < (int)per && c < a.e) sc[i] = sc[i] / sum;
-        }
+        for (int i = 0; i < PER; ++i) sc[i] = sc[i] / sum;
     } else {
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) {
-            uint32_t c = lane + 64 * i;
-            if (i < (int)per && c < a.e) sc[i] = 1.0f / (1.0f + r9vx_expf(-sc[i]));
-        }
+        for (int i = 0; i < PER; ++i) sc[i] = 1.0f / (1.0f + r9vx_expf_tab_nb(-sc[i], etab));
     }
     /* Top-K: the composite key (score order, ~id) makes every candidate
-     * distinct, so a wave max picks exactly the reference's next element. */
-    uint32_t my_id = 0;
-    float my_w = 0.0f;
-    float selected_sum = 0.0f;
-    uint32_t taken = 0; /* bit i: element lane+64i already selected */
-    for (uint32_t j = 0; j < a.k; ++j) {
-        uint64_t best = 0;
+     * distinct, so a wave max picks exactly the reference's next element.
+     * Keys are built once; a taken key or a padding slot is 0, below every
+     * valid key (scores are >= 0, whose order keys are >= 0x80000000).  The
+     * wave max runs on the score half; the id half is needed only when
+     * several lanes tie on it. */
+    uint64_t key[PER];
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; ++i) {
-            uint32_t c = lane + 64 * i;
-            if (i < (int)per && c < a.e && !((taken >> i) & 1u)) {
-                uint64_t key = ((uint64_t)total_order(sc[i]) << 32) | (uint64_t)(0xFFFFFFFFu - c);
-                best = key > best ? key : best;
-            }
+    for (int i = 0; i < PER; ++i) {
+        const uint32_t c = lane + 64 * i;
+        key[i] = c < a.e ? ((uint64_t)total_order(sc[i]) << 32) | (uint64_t)(0xFFFFFFFFu - c) : 0;
+    }
+    my_id = 0;
+    my_w = 0.0f;
+    float selected_sum = 0.0f;
+    for (uint32_t j = 0; j < a.k; ++j) {
+        uint64_t m[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) m[i] = key[i];
+#pragma unroll
+        for (int w = 1; w < PER; w *= 2)
+#pragma unroll
+            for (int i = 0; i + w < PER; i += 2 * w) m[i] = m[i + w] > m[i] ? m[i + w] : m[i];
+        const uint64_t best = m[0];
+        const uint32_t bh = (uint32_t)(best >> 32), bl = (uint32_t)best;
+        const uint32_t mh = wave_max_u32(bh);
+        const uint64_t tied = __ballot(bh == mh);
+        uint32_t ml;
+        if ((tied & (tied - 1)) == 0)
+            ml = (uint32_t)__builtin_amdgcn_readlane((int)bl, (int)__builtin_ctzll(tied));
+        else
+            ml = wave_max_u32(bh == mh ? bl : 0u);
+        const uint32_t col = 0xFFFFFFFFu - ml;
+        if ((col & 63u) == lane) {
+#pragma unroll
+            for (int i = 0; i < PER; ++i)
+                if ((uint32_t)i == (col >> 6)) key[i] = 0;
         }
-        best = wave_max_u64(best);
-        uint32_t col = 0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu);
-        if ((col & 63u) == lane) taken |= 1u << (col >> 6);
-        float score = __builtin_bit_cast(float, (uint32_t)(best >> 32) & 0x80000000u
-                                                    ? (uint32_t)(best >> 32) & 0x7FFFFFFFu
-                                                    : ~(uint32_t)(best >> 32));
-        float w = score * a.scale;
+        const float score = __builtin_bit_cast(float, (mh & 0x80000000u) ? (mh & 0x7FFFFFFFu) : ~mh);
+        const float w = score * a.scale;
         selected_sum = selected_sum + w;
         if (lane == j) {
             my_id = col;
@@ -176,10 +267,6 @@ __device__ __forceinline__ void route_row(const RouteArgs &a, uint32_t row, uint
         }
     }
     if (a.renormalize) my_w = my_w / selected_sum;
-    if (lane < a.k) {
-        a.ids[(uint64_t)row * a.k + lane] = my_id;
-        a.weights[(uint64_t)row * a.k + lane] = my_w;
-    }
 }
 
 __global__ void clear_status_kernel() { g_route_status = 0u; }
@@ -193,45 +280,84 @@ __global__ __launch_bounds__(256) void route_check_kernel(RouteArgs a) {
 }
 
 /* Grid-wide form: runs after route_check_kernel. */
+template <int PER>
 __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
-    uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    uint32_t row = blockIdx.x * 4 + wv;
+    __shared__ uint64_t etab[R9VX_EXP2F_N];
+    __shared__ __attribute__((aligned(16))) float sbuf[4][PER * 64];
+    r9vx_exp2_fill(etab, threadIdx.x, blockDim.x);
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t row = blockIdx.x * 4 + wv;
     if (row >= a.t) return;
     if (__atomic_load_n(&g_route_status, __ATOMIC_RELAXED) != 0u) return;
-    route_row(a, row, lane);
+    float sc[PER], lg[PER], bs[PER];
+    load_row<PER>(a, row, lane, sc, lg, bs);
+    uint32_t id;
+    float w;
+    route_loaded<PER>(a, lane, sc, etab, sbuf[wv], id, w);
+    if (lane < a.k) {
+        a.ids[(uint64_t)row * a.k + lane] = id;
+        a.weights[(uint64_t)row * a.k + lane] = w;
+    }
 }
 
-/* Single-workgroup form for small T: check every row, then compute. */
+/* Single-workgroup form for small T (one wave per row): each wave loads and
+ * routes its row, the rows' status bits are or-ed in LDS, and only a clean
+ * batch writes its results. */
+template <int PER>
 __global__ __launch_bounds__(512) void route_small_kernel(RouteArgs a) {
     __shared__ uint32_t bad_all;
-    uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __shared__ uint64_t etab[R9VX_EXP2F_N];
+    __shared__ __attribute__((aligned(16))) float sbuf[8][PER * 64];
+    const uint32_t lane = threadIdx.x & 63, row = threadIdx.x >> 6;
+    r9vx_exp2_fill(etab, threadIdx.x, blockDim.x);
     if (threadIdx.x == 0) bad_all = 0;
+    float sc[PER], lg[PER], bs[PER];
+    load_row<PER>(a, row, lane, sc, lg, bs);
     __syncthreads();
-    for (uint32_t row = wv; row < a.t; row += nw) {
-        uint32_t bad = check_row(a, row, lane);
-        if (bad && lane == 0) atomicOr(&bad_all, bad);
-    }
+    const uint32_t bad_row = check_loaded<PER>(a, lane, sc, lg, bs, etab);
+    /* or of the row's status bits: one ballot per bit */
+    uint32_t bad = 0;
+    if (__ballot(bad_row & R9VX_STATUS_NONFINITE)) bad |= R9VX_STATUS_NONFINITE;
+    if (__ballot(bad_row & R9VX_STATUS_DEGENERATE)) bad |= R9VX_STATUS_DEGENERATE;
+    if (bad && lane == 0) atomicOr(&bad_all, bad);
+    uint32_t id = 0;
+    float w = 0.0f;
+    if (!bad) route_loaded<PER>(a, lane, sc, etab, sbuf[row], id, w);
     __syncthreads();
-    uint32_t bad = bad_all;
+    bad = bad_all;
     if (threadIdx.x == 0) g_route_status = bad;
     if (bad) return;
-    for (uint32_t row = wv; row < a.t; row += nw) route_row(a, row, lane);
+    if (lane < a.k) {
+        a.ids[(uint64_t)row * a.k + lane] = id;
+        a.weights[(uint64_t)row * a.k + lane] = w;
+    }
 }
 
 }  // namespace
 
-int r9vx_launch_route(const r9vx_route_problem &p, hipStream_t stream) {
-    RouteArgs a{p.logits, p.bias, p.ids, p.weights, p.t, p.e, p.k, p.scoring, p.renormalize, p.scale};
-    if (p.t <= 8) {
-        uint32_t waves = p.t;
-        hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(64 * waves), 0, stream, a);
+template <int PER>
+static int launch_route_per(const RouteArgs &a, hipStream_t stream) {
+    if (a.t <= 8) {
+        hipLaunchKernelGGL((route_small_kernel<PER>), dim3(1), dim3(64 * a.t), 0, stream, a);
         return (int)hipGetLastError();
     }
     hipLaunchKernelGGL(clear_status_kernel, dim3(1), dim3(1), 0, stream);
-    dim3 grid((p.t + 3) / 4);
+    dim3 grid((a.t + 3) / 4);
     hipLaunchKernelGGL(route_check_kernel, grid, dim3(256), 0, stream, a);
-    hipLaunchKernelGGL(route_kernel, grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((route_kernel<PER>), grid, dim3(256), 0, stream, a);
     return (int)hipGetLastError();
+}
+
+int r9vx_launch_route(const r9vx_route_problem &p, hipStream_t stream) {
+    RouteArgs a{p.logits, p.bias, p.ids, p.weights, p.t, p.e, p.k, p.scoring, p.renormalize, p.scale};
+    /* registers per lane: the next power of two >= ceil(E / 64) */
+    const uint32_t per = (p.e + 63) / 64;
+    if (per <= 1) return launch_route_per<1>(a, stream);
+    if (per <= 2) return launch_route_per<2>(a, stream);
+    if (per <= 4) return launch_route_per<4>(a, stream);
+    if (per <= 8) return launch_route_per<8>(a, stream);
+    return launch_route_per<16>(a, stream);
 }
 
 int r9vx_read_route_status(uint32_t *status, hipStream_t stream) {
