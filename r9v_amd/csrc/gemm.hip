@@ -19,6 +19,7 @@
  *     tile run on the same XCD and hit its L2.
  */
 #include "r9vx_mma.h"
+#include "r9vx_mma2.h"
 
 using namespace r9vx;
 
@@ -37,6 +38,9 @@ struct GemmArgs {
     uint32_t y_bf16, epilogue;
 };
 
+/* PERM = 0: natural order; R9VX_SCHEME_Q4_K / R9VX_SCHEME_IQ4_XS: each 64-column
+ * step stored in that scheme's group order (r9vx_mma2.h). */
+template <int PERM>
 __global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t *__restrict__ x, uint32_t k,
                                                        _Float16 *__restrict__ x16, float *__restrict__ scale) {
     __shared__ float red[4];
@@ -61,8 +65,16 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t *__restric
     if (threadIdx.x == 0) scale[row] = ldexpf(1.0f, e);
     _Float16 *orow = x16 + (uint64_t)row * k;
     for (uint32_t c = threadIdx.x * 8; c < k; c += 256 * 8) {
-        r9vx_u32x4 v = *reinterpret_cast<const r9vx_u32x4 *>(xr + c);
-        uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t w[4];
+        if constexpr (PERM == 0) {
+            r9vx_u32x4 v = *reinterpret_cast<const r9vx_u32x4 *>(xr + c);
+            w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+        } else {
+            const uint32_t base = c & ~63u, q = (c & 63u) >> 3;
+            const r9vx_u32x2 lo = *reinterpret_cast<const r9vx_u32x2 *>(xr + base + group_k<PERM>(q, 0));
+            const r9vx_u32x2 hi = *reinterpret_cast<const r9vx_u32x2 *>(xr + base + group_k<PERM>(q, 4));
+            w[0] = lo.x, w[1] = lo.y, w[2] = hi.x, w[3] = hi.y;
+        }
         uint32_t o[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -159,6 +171,140 @@ __global__ __launch_bounds__(256, NBUF == 1 ? 2 : 1) void gemm_kernel(GemmArgs a
     }
 }
 
+/* 256 x 256 tiles, 8 waves, weights decoded into MFMA operand registers. */
+template <int SCHEME>
+__global__ __launch_bounds__(512, 1) void gemm2_kernel(GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t st0[kM2StageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t st1[kM2StageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t st2[kM2StageBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t st3[kM2StageBytes];
+    __shared__ __attribute__((aligned(16))) float lutf[512];
+    uint8_t *const stages[4] = {st0, st1, st2, st3};
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t total = a.m_tiles * a.n_tiles;
+    uint32_t t = blockIdx.x;
+    if (total % 8 == 0) t = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
+    const uint32_t n_tile = t / a.m_tiles, m_tile = t % a.m_tiles;
+    const uint32_t m0 = m_tile * kM2Rows, n0 = n_tile * kM2Cols;
+
+    if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) init_iq4_lut_f32(reinterpret_cast<r9vx_f32x4 *>(lutf), tid);
+    __syncthreads(); /* the codebook table, before any load is in flight */
+
+    const _Float16 *asrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = (wave * 4 + i) * 8 + (lane >> 3);
+        const uint32_t rr = m0 + r < a.m ? m0 + r : a.m - 1;
+        const uint32_t g = (lane & 7u) ^ m2_swz(r);
+        asrc[i] = a.x16 + (uint64_t)rr * a.k + 8 * g;
+    }
+    const uint32_t col = n0 + 32 * wave + (lane & 31), h = lane >> 5;
+    const uint8_t *wrow = a.w + (uint64_t)(col < a.n ? col : a.n - 1) * a.w_row_stride;
+
+    r9vx_f32x16 acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+
+    /* K % 256 == 0: nk is a multiple of 4 (one super-block per 4 steps) */
+    const uint32_t nk = a.k / kTileK;
+    /* Issue order (each step: A copy of step +3, then weights of step +2),
+     * so that before step k only the 6 loads issued during step k - 1 may
+     * still be in flight: */
+    BRaw b[4];
+    dma_a_step(stages[0], asrc, 0, wave);
+    dma_a_step(stages[1], asrc, 1, wave);
+    load_braw<SCHEME>(wrow, 0, h, b[0]);
+    dma_a_step(stages[2], asrc, 2, wave);
+    load_braw<SCHEME>(wrow, 1, h, b[1]);
+
+    /* Step k reads A stage k % 4 and weight set k % 4.  Its barrier also frees
+     * stage (k + 3) % 4 (read in step k - 1), which takes the A copy of step
+     * k + 3; set (k + 2) % 4 takes the weights of step k + 2 (both clamped
+     * past the end, so the count in flight is always the same). */
+    for (uint32_t k = 0; k < nk; k += 4) {
+#define R9VX_M2_STEP(J)                                                                       \
+    {                                                                                         \
+        wait_vm<6>(); /* this wave's A copy and weights of step k + J are in */              \
+        touch<SCHEME>(b[J]);                                                                  \
+        lds_barrier(); /* and every wave's A copy */                                          \
+        const uint32_t ka = k + J + 3 < nk ? k + J + 3 : nk - 1;                              \
+        const uint32_t kb = k + J + 2 < nk ? k + J + 2 : nk - 1;                              \
+        dma_a_step(stages[(J + 3) & 3], asrc, ka, wave);                                      \
+        load_braw<SCHEME>(wrow, kb, h, b[(J + 2) & 3]);                                       \
+        m2_step<SCHEME, J>(stages[J], b[J], lane, lutf, acc);                                 \
+    }
+        R9VX_M2_STEP(0)
+        R9VX_M2_STEP(1)
+        R9VX_M2_STEP(2)
+        R9VX_M2_STEP(3)
+#undef R9VX_M2_STEP
+    }
+    wait_vm<0>();
+    __syncthreads();
+
+    /* epilogue through LDS, 16 rows at a time (stage row stride 260 floats):
+     * accumulator registers 8u..8u+7 of tile i are rows 32i + 16u + .. */
+    constexpr uint32_t kSRow = 260;
+    float *stage = reinterpret_cast<float *>(st0);
+    const bool vec = (a.n & 3u) == 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                stage[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kSRow + 32 * wave + (lane & 31)] =
+                    acc[i][8 * u + r];
+            __syncthreads();
+            const uint32_t cl = 4 * (tid & 63);
+            const uint32_t c = n0 + cl;
+#pragma unroll
+            for (uint32_t q = 0; q < 2; ++q) {
+                const uint32_t rl = (tid >> 6) + 8 * q;
+                const uint32_t row = m0 + i * 32 + u * 16 + rl;
+                if (row >= a.m || c >= a.n) continue;
+                const r9vx_f32x4 acc4 = *reinterpret_cast<const r9vx_f32x4 *>(stage + rl * kSRow + cl);
+                const float sc = a.scale[row];
+                float v[4] = {acc4.x * sc, acc4.y * sc, acc4.z * sc, acc4.w * sc};
+                const uint64_t o = (uint64_t)row * a.n + c;
+                if (vec) {
+                    if (a.epilogue == R9VX_EPILOGUE_BIAS) {
+                        const r9vx_f32x4 bb = *reinterpret_cast<const r9vx_f32x4 *>(a.bias + c);
+                        v[0] += bb.x, v[1] += bb.y, v[2] += bb.z, v[3] += bb.w;
+                    }
+                    if (a.epilogue == R9VX_EPILOGUE_RESIDUAL) {
+                        const r9vx_f32x4 bb = *reinterpret_cast<const r9vx_f32x4 *>(a.residual + o);
+                        v[0] += bb.x, v[1] += bb.y, v[2] += bb.z, v[3] += bb.w;
+                    }
+                    if (a.y_bf16) {
+                        const uint32_t lo =
+                            (uint32_t)r9vx_f32_to_bf16(v[0]) | ((uint32_t)r9vx_f32_to_bf16(v[1]) << 16);
+                        const uint32_t hi =
+                            (uint32_t)r9vx_f32_to_bf16(v[2]) | ((uint32_t)r9vx_f32_to_bf16(v[3]) << 16);
+                        *reinterpret_cast<r9vx_u32x2 *>(reinterpret_cast<uint16_t *>(a.y) + o) = r9vx_u32x2{lo, hi};
+                    } else {
+                        *reinterpret_cast<r9vx_f32x4 *>(reinterpret_cast<float *>(a.y) + o) =
+                            r9vx_f32x4{v[0], v[1], v[2], v[3]};
+                    }
+                } else {
+                    for (uint32_t cc = 0; cc < 4 && c + cc < a.n; ++cc) {
+                        float x = v[cc];
+                        if (a.epilogue == R9VX_EPILOGUE_BIAS) x += a.bias[c + cc];
+                        if (a.epilogue == R9VX_EPILOGUE_RESIDUAL) x += a.residual[o + cc];
+                        if (a.y_bf16)
+                            reinterpret_cast<uint16_t *>(a.y)[o + cc] = r9vx_f32_to_bf16(x);
+                        else
+                            reinterpret_cast<float *>(a.y)[o + cc] = x;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
 }  // namespace
 
 size_t r9vx_gemm_workspace_bytes(uint32_t m_bucket, uint32_t k) {
@@ -167,7 +313,7 @@ size_t r9vx_gemm_workspace_bytes(uint32_t m_bucket, uint32_t k) {
 
 int r9vx_launch_x_to_f16(const uint16_t *x, uint32_t m, uint32_t k, _Float16 *x16, float *scale,
                          hipStream_t stream) {
-    hipLaunchKernelGGL(x_to_f16_kernel, dim3(m), dim3(256), 0, stream, x, k, x16, scale);
+    hipLaunchKernelGGL(x_to_f16_kernel<0>, dim3(m), dim3(256), 0, stream, x, k, x16, scale);
     return (int)hipGetLastError();
 }
 
@@ -175,7 +321,6 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     _Float16 *x16 = reinterpret_cast<_Float16 *>(p.workspace);
     float *scale = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(p.workspace) +
                                              (((size_t)p.m * p.k * 2 + 255) & ~(size_t)255));
-    hipLaunchKernelGGL(x_to_f16_kernel, dim3(p.m), dim3(256), 0, stream, p.x, p.k, x16, scale);
     GemmArgs a{};
     a.x16 = x16;
     a.scale = scale;
@@ -187,26 +332,33 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     a.m = p.m;
     a.n = p.n;
     a.k = p.k;
-    /* 256-row tiles, double-buffered, one workgroup per CU when there are
-     * enough rows to fill the chip; 128-row single-buffered tiles (two
-     * workgroups per CU) otherwise. */
-    const bool big = (uint64_t)((p.m + 255) / 256) * ((p.n + 255) / 256) >= 256;
-    const uint32_t bm = big ? 256 : 128;
-    a.m_tiles = (p.m + bm - 1) / bm;
-    a.n_tiles = (p.n + 255) / 256;
     a.y_bf16 = p.y_dtype == R9VX_DTYPE_BF16;
     a.epilogue = p.epilogue;
-    dim3 grid(a.m_tiles * a.n_tiles);
-    if (p.scheme == R9VX_SCHEME_Q4_K) {
-        if (big)
-            hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q4_K, 256, 2>), grid, dim3(256), 0, stream, a);
+    /* 256 x 256 register-decoded tiles when there are enough of them to fill
+     * the chip; 128-row LDS-decoded tiles (two workgroups per CU) otherwise. */
+    const bool big = (uint64_t)((p.m + 255) / 256) * ((p.n + 255) / 256) >= 256;
+    if (big) {
+        if (p.scheme == R9VX_SCHEME_Q4_K)
+            hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3(p.m), dim3(256), 0, stream, p.x, p.k, x16, scale);
         else
-            hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q4_K, 128, 1>), grid, dim3(256), 0, stream, a);
-    } else {
-        if (big)
-            hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_IQ4_XS, 256, 2>), grid, dim3(256), 0, stream, a);
+            hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3(p.m), dim3(256), 0, stream, p.x, p.k, x16,
+                               scale);
+        a.m_tiles = (p.m + kM2Rows - 1) / kM2Rows;
+        a.n_tiles = (p.n + kM2Cols - 1) / kM2Cols;
+        dim3 grid(a.m_tiles * a.n_tiles);
+        if (p.scheme == R9VX_SCHEME_Q4_K)
+            hipLaunchKernelGGL((gemm2_kernel<R9VX_SCHEME_Q4_K>), grid, dim3(512), 0, stream, a);
         else
-            hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_IQ4_XS, 128, 1>), grid, dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((gemm2_kernel<R9VX_SCHEME_IQ4_XS>), grid, dim3(512), 0, stream, a);
+        return (int)hipGetLastError();
     }
+    hipLaunchKernelGGL(x_to_f16_kernel<0>, dim3(p.m), dim3(256), 0, stream, p.x, p.k, x16, scale);
+    a.m_tiles = (p.m + 127) / 128;
+    a.n_tiles = (p.n + 255) / 256;
+    dim3 grid(a.m_tiles * a.n_tiles);
+    if (p.scheme == R9VX_SCHEME_Q4_K)
+        hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q4_K, 128, 1>), grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_IQ4_XS, 128, 1>), grid, dim3(256), 0, stream, a);
     return (int)hipGetLastError();
 }

@@ -178,6 +178,31 @@ def test_gemm_shapes(scheme, m, n, k):
     check_close(got, ref, f"m={m} n={n} k={k}")
 
 
+# Launches with >= 256 output tiles of 256 x 256 take the 8-wave path that
+# decodes the weights straight into MFMA operands; these shapes reach it with
+# ragged M and N tails and the smallest K (one super-block).
+@pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])
+@pytest.mark.parametrize("m,n,k", [(1000, 16400, 256), (1024, 16384, 512), (770, 21760, 1280)])
+def test_gemm_register_decoded_path(scheme, m, n, k):
+    rows = np.unique(np.concatenate([np.arange(0, m, 37), [0, 255, 256, m - 1]]))
+    cols = np.unique(np.concatenate([np.arange(0, n, 29), [0, 31, 32, 255, 256, n - 17, n - 1]]))
+    got, ref = _gemm_case(scheme, n, k, m, 7300 + m + k, rows=rows, cols=cols)
+    check_close(got, ref, f"m={m} n={n} k={k}")
+
+
+def test_gemm_register_decoded_epilogues():
+    m, n, k = 600, 28000, 256
+    rows = np.arange(0, m, 7)
+    cols = np.unique(np.concatenate([np.arange(0, n, 41), [n - 1]]))
+    got, ref = _gemm_case(O.IQ4_XS, n, k, m, 7400, bias=True, rows=rows, cols=cols)
+    check_close(got, ref, "bias")
+    got, ref = _gemm_case(O.Q4_K, n, k, m, 7401, residual=True, rows=rows, cols=cols)
+    check_close(got, ref, "residual")
+    got, ref = _gemm_case(O.Q4_K, n, k, m, 7402, out_dtype=O.BF16, rows=rows, cols=cols)
+    got32, _ = _gemm_case(O.Q4_K, n, k, m, 7402, out_dtype=O.F32, rows=rows, cols=cols, oracle=False)
+    check_bf16_out(got, got32, ref, "bf16 out")
+
+
 def test_gemm_epilogues_bf16_out():
     got, ref = _gemm_case(O.IQ4_XS, 200, 512, 40, 7200, bias=True)
     check_close(got, ref, "bias")
