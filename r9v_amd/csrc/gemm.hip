@@ -172,6 +172,8 @@ __global__ __launch_bounds__(256, NBUF == 1 ? 2 : 1) void gemm_kernel(GemmArgs a
 }
 
 /* 256 x 256 tiles, 8 waves, weights decoded into MFMA operand registers. */
+constexpr int kM2Rows = 256, kM2Cols = 256, kM2StageBytes = kM2Rows * 128;
+
 template <int SCHEME>
 __global__ __launch_bounds__(512, 1) void gemm2_kernel(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t st0[kM2StageBytes];
@@ -193,55 +195,16 @@ __global__ __launch_bounds__(512, 1) void gemm2_kernel(GemmArgs a) {
     const _Float16 *asrc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t r = (wave * 4 + i) * 8 + (lane >> 3);
+        const uint32_t r = dma_row(wave, i, lane);
         const uint32_t rr = m0 + r < a.m ? m0 + r : a.m - 1;
-        const uint32_t g = (lane & 7u) ^ m2_swz(r);
-        asrc[i] = a.x16 + (uint64_t)rr * a.k + 8 * g;
+        asrc[i] = a.x16 + (uint64_t)rr * a.k + 8 * dma_group(r, lane);
     }
-    const uint32_t col = n0 + 32 * wave + (lane & 31), h = lane >> 5;
-    const uint8_t *wrow = a.w + (uint64_t)(col < a.n ? col : a.n - 1) * a.w_row_stride;
+    const uint32_t col = n0 + 32 * wave + (lane & 31);
+    const uint8_t *const wrow[1] = {a.w + (uint64_t)(col < a.n ? col : a.n - 1) * a.w_row_stride};
 
-    r9vx_f32x16 acc[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
-
-    /* K % 256 == 0: nk is a multiple of 4 (one super-block per 4 steps) */
-    const uint32_t nk = a.k / kTileK;
-    /* Issue order (each step: A copy of step +3, then weights of step +2),
-     * so that before step k only the 6 loads issued during step k - 1 may
-     * still be in flight: */
-    BRaw b[4];
-    dma_a_step(stages[0], asrc, 0, wave);
-    dma_a_step(stages[1], asrc, 1, wave);
-    load_braw<SCHEME>(wrow, 0, h, b[0]);
-    dma_a_step(stages[2], asrc, 2, wave);
-    load_braw<SCHEME>(wrow, 1, h, b[1]);
-
-    /* Step k reads A stage k % 4 and weight set k % 4.  Its barrier also frees
-     * stage (k + 3) % 4 (read in step k - 1), which takes the A copy of step
-     * k + 3; set (k + 2) % 4 takes the weights of step k + 2 (both clamped
-     * past the end, so the count in flight is always the same). */
-    for (uint32_t k = 0; k < nk; k += 4) {
-#define R9VX_M2_STEP(J)                                                                       \
-    {                                                                                         \
-        wait_vm<6>(); /* this wave's A copy and weights of step k + J are in */              \
-        touch<SCHEME>(b[J]);                                                                  \
-        lds_barrier(); /* and every wave's A copy */                                          \
-        const uint32_t ka = k + J + 3 < nk ? k + J + 3 : nk - 1;                              \
-        const uint32_t kb = k + J + 2 < nk ? k + J + 2 : nk - 1;                              \
-        dma_a_step(stages[(J + 3) & 3], asrc, ka, wave);                                      \
-        load_braw<SCHEME>(wrow, kb, h, b[(J + 2) & 3]);                                       \
-        m2_step<SCHEME, J>(stages[J], b[J], lane, lutf, acc);                                 \
-    }
-        R9VX_M2_STEP(0)
-        R9VX_M2_STEP(1)
-        R9VX_M2_STEP(2)
-        R9VX_M2_STEP(3)
-#undef R9VX_M2_STEP
-    }
-    wait_vm<0>();
+    r9vx_f32x16 acc2[8][1];
+    /* K % 256 == 0: a multiple of 4 steps */
+    m2_mainloop<SCHEME, 8, 1>(stages, asrc, wrow, a.k / kTileK, wave, lane, lutf, acc2);
     __syncthreads();
 
     /* epilogue through LDS, 16 rows at a time (stage row stride 260 floats):
@@ -256,7 +219,7 @@ __global__ __launch_bounds__(512, 1) void gemm2_kernel(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 8; ++r)
                 stage[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * kSRow + 32 * wave + (lane & 31)] =
-                    acc[i][8 * u + r];
+                    acc2[i][0][8 * u + r];
             __syncthreads();
             const uint32_t cl = 4 * (tid & 63);
             const uint32_t c = n0 + cl;
@@ -312,8 +275,13 @@ size_t r9vx_gemm_workspace_bytes(uint32_t m_bucket, uint32_t k) {
 }
 
 int r9vx_launch_x_to_f16(const uint16_t *x, uint32_t m, uint32_t k, _Float16 *x16, float *scale,
-                         hipStream_t stream) {
-    hipLaunchKernelGGL(x_to_f16_kernel<0>, dim3(m), dim3(256), 0, stream, x, k, x16, scale);
+                         uint32_t perm_scheme, hipStream_t stream) {
+    if (perm_scheme == R9VX_SCHEME_Q4_K)
+        hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3(m), dim3(256), 0, stream, x, k, x16, scale);
+    else if (perm_scheme == R9VX_SCHEME_IQ4_XS)
+        hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3(m), dim3(256), 0, stream, x, k, x16, scale);
+    else
+        hipLaunchKernelGGL(x_to_f16_kernel<0>, dim3(m), dim3(256), 0, stream, x, k, x16, scale);
     return (int)hipGetLastError();
 }
 

@@ -7,20 +7,20 @@
  *
  *  tiles : each work item (expert with n pairs, or shared expert with t rows)
  *          becomes ceil(n / 128) row tiles; a one-workgroup scan lays them out.
- *  gate/up: a workgroup owns 128 permuted rows x 128 columns j of h; its
- *          B tile holds gate rows j and up rows Dff+j of the expert (256
- *          weight rows), so g and u of the same (row, j) land in the same lane
+ *  gate/up: a workgroup owns 128 permuted rows x 128 columns j of h; wave w's
+ *          two column tiles are gate rows j0+32w.. and the matching up rows
+ *          Dff+j0+32w.., so g and u of the same (row, j) land in the same lane
  *          and register: h = silu(g) * u is formed in registers (f32) and
  *          written with the row's running max|h|.  A rows are gathered from the
- *          fp16-scaled activations by the permutation (no permuted copy of x).
- *  down  : a workgroup owns 128 rows x 256 output columns; h rows are scaled
- *          by the power of two that brings max|h| below 2^15, rounded to fp16
- *          into LDS, and the scale is undone on the f32 accumulators.
- * Weight tiles are dequantized into LDS as fp16 exactly as in gemm.hip; LDS
- * is single-buffered (48 KiB) so two workgroups share a CU and one's MFMAs
- * overlap the other's dequantization.  Tiles past the scanned count exit.
+ *          scaled fp16 activations by the permutation (no permuted copy of x).
+ *  h16   : each h row scaled by the power of two that brings max|h| below
+ *          2^15 and rounded to fp16, in the down weights' K group order.
+ *  down  : a workgroup owns 128 rows x 256 output columns of o; the scale is
+ *          undone on the f32 accumulators.
+ * Both GEMMs run the register-decoded main loop of r9vx_mma2.h (4 waves,
+ * 128-row tiles, two workgroups per CU).  Tiles past the scanned count exit.
  */
-#include "r9vx_mma.h"
+#include "r9vx_mma2.h"
 #include "r9vx_moe.h"
 
 using namespace r9vx;
@@ -31,6 +31,7 @@ constexpr uint32_t kBM = kMoeTileM; /* 128 rows per tile */
 
 struct GroupedArgs {
     const _Float16 *x16;
+    _Float16 *h16;
     const float *xscale;
     const uint8_t *w_gu;
     const uint8_t *w_dn;
@@ -92,12 +93,20 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(GroupedArgs a) {
 
 /* ---------------------------------------------------------------- gate/up */
 
-constexpr int kNB = 1; /* single-buffered LDS: two workgroups share a CU */
+constexpr int kMT = 4;                       /* waves = 32-row tiles per workgroup */
+constexpr int kStage = 32 * kMT * 128;       /* 16 KiB per A stage */
+
+#define R9VX_MOE_STAGES                                                \
+    __shared__ __attribute__((aligned(16))) uint8_t st0[kStage];      \
+    __shared__ __attribute__((aligned(16))) uint8_t st1[kStage];      \
+    __shared__ __attribute__((aligned(16))) uint8_t st2[kStage];      \
+    __shared__ __attribute__((aligned(16))) uint8_t st3[kStage];      \
+    __shared__ __attribute__((aligned(16))) float lutf[512];          \
+    uint8_t *const stages[4] = {st0, st1, st2, st3};
 
 template <int GU>
 __global__ __launch_bounds__(256, 2) void moe_gu_mfma_kernel(GroupedArgs a) {
-    using S = MmaShape<kBM, kNB>;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
+    R9VX_MOE_STAGES
     __shared__ uint32_t rowmax[kBM];
     const uint32_t *status = ws_u32(a, a.L.status);
     const uint32_t ntile_n = a.dff / 128;
@@ -108,31 +117,28 @@ __global__ __launch_bounds__(256, 2) void moe_gu_mfma_kernel(GroupedArgs a) {
     const uint32_t j0 = nt * 128;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < kBM) rowmax[tid] = 0u;
+    if constexpr (GU == R9VX_SCHEME_IQ4_XS) init_iq4_lut_f32(reinterpret_cast<r9vx_f32x4 *>(lutf), tid);
+    __syncthreads();
 
-    AF16Rows<kBM> as;
-    as.chunk = tid & 7;
-    as.row0 = tid >> 3;
+    const _Float16 *asrc[4];
 #pragma unroll
-    for (int i = 0; i < kBM / 32; ++i) {
-        uint32_t r = as.row0 + 32 * i;
-        uint32_t tok = row_token(a, expert, pos0 + (r < rows ? r : 0));
-        as.row[i] = a.x16 + (uint64_t)tok * a.dm + 8 * as.chunk;
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = dma_row(wave, i, lane);
+        const uint32_t tok = row_token(a, expert, pos0 + (r < rows ? r : 0));
+        asrc[i] = a.x16 + (uint64_t)tok * a.dm + 8 * dma_group(r, lane);
     }
-    /* B row t: wave w = t/64 takes gate rows j0+32w.. (t%64 < 32) and the
-     * matching up rows, so acc[i][0] is g and acc[i][1] is u of the same j. */
-    const uint32_t bw = tid >> 6, bh = (tid >> 5) & 1, bj = tid & 31;
-    const uint32_t wr = (bh ? a.dff : 0u) + j0 + 32 * bw + bj;
-    const uint8_t *wptr = a.w_gu + ((uint64_t)expert * 2 * a.dff + wr) * a.gu_row_bytes;
-    r9vx_f32x16 acc[kBM / 32][2];
-    mma_mainloop<GU, kBM, kNB>(lds, as, wptr, a.dm / kTileK, acc);
+    const uint32_t col = j0 + 32 * wave + (lane & 31);
+    const uint8_t *wexp = a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes;
+    const uint8_t *const wrow[2] = {wexp + (uint64_t)col * a.gu_row_bytes, wexp + (uint64_t)(a.dff + col) * a.gu_row_bytes};
+    r9vx_f32x16 acc[kMT][2];
+    m2_mainloop<GU, kMT, 2>(stages, asrc, wrow, a.dm / kTileK, wave, lane, lutf, acc);
 
     float *h = reinterpret_cast<float *>(a.ws + a.L.h);
-    const uint32_t col = j0 + 32 * wave + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < kBM / 32; ++i) {
+    for (int i = 0; i < kMT; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const uint32_t rl = acc_row(i, r, lane);
+            const uint32_t rl = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (rl >= rows) continue;
             const float sc = a.xscale[row_token(a, expert, pos0 + rl)];
             const float g = acc[i][0][r] * sc, u = acc[i][1][r] * sc;
@@ -145,12 +151,35 @@ __global__ __launch_bounds__(256, 2) void moe_gu_mfma_kernel(GroupedArgs a) {
     if (tid < rows) atomicMax(reinterpret_cast<uint32_t *>(a.ws + a.L.hmax) + pos0 + tid, rowmax[tid]);
 }
 
+/* ---------------------------------------------------------------- h -> fp16 */
+
+/* One wave per h row: lane l writes group l % 8 of K step l / 8 (+ 8 per
+ * pass) as 8 fp16 in the down scheme's group order, scaled by 2^-e with
+ * e = row_shift(max|h|). */
+template <int DN>
+__global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t nrows) {
+    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= nrows) return;
+    const uint32_t *status = ws_u32(a, a.L.status);
+    if (status[0] != 0u) return;
+    const float *hr = reinterpret_cast<const float *>(a.ws + a.L.h) + (uint64_t)row * a.dff;
+    const float inv = ldexpf(1.0f, -row_shift(__builtin_bit_cast(float, ws_u32(a, a.L.hmax)[row])));
+    _Float16 *orow = a.h16 + (uint64_t)row * a.dff;
+    for (uint32_t c = lane; c < a.dff / 8; c += 64) {
+        const uint32_t base = (c >> 3) * 64, q = c & 7;
+        const r9vx_f32x4 lo = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + group_k<DN>(q, 0));
+        const r9vx_f32x4 hi = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + group_k<DN>(q, 4));
+        *reinterpret_cast<r9vx_u32x4 *>(orow + 8 * c) =
+            r9vx_u32x4{pack_h2(lo.x * inv, lo.y * inv), pack_h2(lo.z * inv, lo.w * inv), pack_h2(hi.x * inv, hi.y * inv),
+                       pack_h2(hi.z * inv, hi.w * inv)};
+    }
+}
+
 /* ---------------------------------------------------------------- down */
 
 template <int DN>
 __global__ __launch_bounds__(256, 2) void moe_dn_mfma_kernel(GroupedArgs a) {
-    using S = MmaShape<kBM, kNB>;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
+    R9VX_MOE_STAGES
     const uint32_t *status = ws_u32(a, a.L.status);
     const uint32_t ntile_n = a.dm / 256;
     const uint32_t tix = blockIdx.x / ntile_n, nt = blockIdx.x % ntile_n;
@@ -159,34 +188,32 @@ __global__ __launch_bounds__(256, 2) void moe_dn_mfma_kernel(GroupedArgs a) {
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
     const uint32_t n0 = nt * 256;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if constexpr (DN == R9VX_SCHEME_IQ4_XS) init_iq4_lut_f32(reinterpret_cast<r9vx_f32x4 *>(lutf), tid);
+    __syncthreads();
 
-    AF32ScaledRows<kBM> as;
-    as.chunk = tid & 7;
-    as.row0 = tid >> 3;
-    const float *hbase = reinterpret_cast<const float *>(a.ws + a.L.h);
-    const uint32_t *hmax = ws_u32(a, a.L.hmax);
+    const _Float16 *asrc[4];
 #pragma unroll
-    for (int i = 0; i < kBM / 32; ++i) {
-        uint32_t r = as.row0 + 32 * i;
-        uint32_t pos = pos0 + (r < rows ? r : 0);
-        as.row[i] = hbase + (uint64_t)pos * a.dff + 8 * as.chunk;
-        as.inv[i] = ldexpf(1.0f, -row_shift(__builtin_bit_cast(float, hmax[pos])));
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = dma_row(wave, i, lane);
+        asrc[i] = a.h16 + (uint64_t)(pos0 + (r < rows ? r : 0)) * a.dff + 8 * dma_group(r, lane);
     }
-    const uint8_t *wptr = a.w_dn + ((uint64_t)expert * a.dm + n0 + tid) * a.dn_row_bytes;
-    r9vx_f32x16 acc[kBM / 32][2];
-    mma_mainloop<DN, kBM, kNB>(lds, as, wptr, a.dff / kTileK, acc);
+    const uint8_t *wexp = a.w_dn + (uint64_t)expert * a.dm * a.dn_row_bytes;
+    const uint32_t c0 = n0 + 64 * wave + (lane & 31);
+    const uint8_t *const wrow[2] = {wexp + (uint64_t)c0 * a.dn_row_bytes, wexp + (uint64_t)(c0 + 32) * a.dn_row_bytes};
+    r9vx_f32x16 acc[kMT][2];
+    m2_mainloop<DN, kMT, 2>(stages, asrc, wrow, a.dff / kTileK, wave, lane, lutf, acc);
 
     float *o = reinterpret_cast<float *>(a.ws + a.L.o);
+    const uint32_t *hmax = ws_u32(a, a.L.hmax);
 #pragma unroll
-    for (int i = 0; i < kBM / 32; ++i) {
+    for (int i = 0; i < kMT; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const uint32_t rl = acc_row(i, r, lane);
+            const uint32_t rl = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (rl >= rows) continue;
             const float sc = ldexpf(1.0f, row_shift(__builtin_bit_cast(float, hmax[pos0 + rl])));
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                o[(uint64_t)(pos0 + rl) * a.dm + n0 + acc_col(wave, j, lane)] = acc[i][j][r] * sc;
+            for (int j = 0; j < 2; ++j) o[(uint64_t)(pos0 + rl) * a.dm + c0 + 32 * j] = acc[i][j][r] * sc;
         }
     }
 }
@@ -196,6 +223,7 @@ __global__ __launch_bounds__(256, 2) void moe_dn_mfma_kernel(GroupedArgs a) {
 int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s) {
     GroupedArgs a{};
     a.x16 = reinterpret_cast<const _Float16 *>(p.ws + L.x16);
+    a.h16 = reinterpret_cast<_Float16 *>(p.ws + L.h16);
     a.xscale = reinterpret_cast<const float *>(p.ws + L.xscale);
     a.w_gu = p.w_gu;
     a.w_dn = p.w_dn;
@@ -211,7 +239,7 @@ int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStr
     a.p = p.t * p.k;
     a.shared = p.shared;
     int rc = r9vx_launch_x_to_f16(p.x, p.t, p.dm, reinterpret_cast<_Float16 *>(p.ws + L.x16),
-                                  reinterpret_cast<float *>(p.ws + L.xscale), s);
+                                  reinterpret_cast<float *>(p.ws + L.xscale), p.scheme_gu, s);
     if (rc) return rc;
     hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(1024), 0, s, a);
     /* upper bound on row tiles: ceil(P/128) + one partial tile per work item */
@@ -221,9 +249,13 @@ int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStr
         hipLaunchKernelGGL(moe_gu_mfma_kernel<R9VX_SCHEME_IQ4_XS>, ggu, dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL(moe_gu_mfma_kernel<R9VX_SCHEME_Q4_K>, ggu, dim3(256), 0, s, a);
-    if (p.scheme_dn == R9VX_SCHEME_Q4_K)
+    const uint32_t nrows = a.p + p.shared * p.t;
+    if (p.scheme_dn == R9VX_SCHEME_Q4_K) {
+        hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3((nrows + 3) / 4), dim3(256), 0, s, a, nrows);
         hipLaunchKernelGGL(moe_dn_mfma_kernel<R9VX_SCHEME_Q4_K>, gdn, dim3(256), 0, s, a);
-    else
+    } else {
+        hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3((nrows + 3) / 4), dim3(256), 0, s, a, nrows);
         hipLaunchKernelGGL(moe_dn_mfma_kernel<R9VX_SCHEME_IQ4_XS>, gdn, dim3(256), 0, s, a);
+    }
     return (int)hipGetLastError();
 }

@@ -30,15 +30,6 @@ struct MmaShape {
     static constexpr int kMT = BM / 32;                  /* 32-row tiles per wave */
 };
 
-/* IQ4_XS f32 codebook pairs: entry b = {kv[b & 15], kv[b >> 4]}. */
-__device__ __forceinline__ void init_iq4_lut_f32(r9vx_f32x4 *lut2 /* 128 x (2 pairs) */, uint32_t tid) {
-    if (tid < 128) {
-        uint32_t b0 = 2 * tid, b1 = 2 * tid + 1;
-        lut2[tid] = r9vx_f32x4{(float)r9vx_iq4_kvalue(b0 & 15), (float)r9vx_iq4_kvalue(b0 >> 4),
-                               (float)r9vx_iq4_kvalue(b1 & 15), (float)r9vx_iq4_kvalue(b1 >> 4)};
-    }
-}
-
 __device__ __forceinline__ uint32_t cvt_pk_h2(float a, float b) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     h2 r;
@@ -125,13 +116,12 @@ __device__ __forceinline__ void load_w(const uint8_t *row, uint32_t kt, WRegs &w
 /* MFMAs of one K step from LDS stage (A, B) into acc[BM/32][2].  The
  * fragments of slice s+1 are read while slice s's MFMAs run (two fragment
  * sets in registers), so no MFMA waits on its own LDS read. */
-template <int BM, bool PREFETCH = true>
+template <int BM>
 __device__ __forceinline__ void mma_step(const uint8_t *A, const uint8_t *B, uint32_t wave, uint32_t lane,
                                          r9vx_f32x16 (&acc)[BM / 32][2]) {
     constexpr int MT = BM / 32;
-    constexpr int NB = PREFETCH ? 2 : 1;
     const uint32_t frow = lane & 31, fchk = lane >> 5;
-    half8 af[NB][MT], bf[NB][2];
+    half8 af[2][MT], bf[2][2];
     auto load = [&](int s, int buf) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
@@ -140,15 +130,11 @@ __device__ __forceinline__ void mma_step(const uint8_t *A, const uint8_t *B, uin
         for (int i = 0; i < MT; ++i)
             af[buf][i] = *reinterpret_cast<const half8 *>(A + lds_chunk(i * 32 + frow, 2 * s + fchk));
     };
-    if constexpr (PREFETCH) load(0, 0);
+    load(0, 0);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-        const int cur = PREFETCH ? (s & 1) : 0;
-        if constexpr (PREFETCH) {
-            if (s < 3) load(s + 1, cur ^ 1);
-        } else {
-            load(s, 0);
-        }
+        const int cur = s & 1;
+        if (s < 3) load(s + 1, cur ^ 1);
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -220,82 +206,6 @@ __device__ __forceinline__ void mma_mainloop(uint8_t *lds, ASrc &asrc, const uin
     }
 }
 
-/*
- * Software-pipelined main loop (LDS double buffer, two register sets of raw
- * operands): while the MFMAs of step k read LDS stage k & 1, the same wave
- * dequantizes step k + 1 (loaded one step earlier) into the other stage and
- * has the loads of step k + 2 in flight.  The body has no branches, so the
- * scheduling hints below can interleave the dequant VALU work and the LDS
- * traffic between the MFMAs, which then overlap inside the wave.  The loads
- * past the last step re-read the last step (in bounds) and the dequant past
- * it writes the unused stage.
- */
-template <int BM>
-__device__ __forceinline__ void interleave_hints() {
-    /* per K step: 4 * (BM/32) * 2 MFMAs; spread VALU, LDS and VMEM between them */
-    constexpr int kMfma = 4 * (BM / 32) * 2;
-#pragma unroll
-    for (int i = 0; i < kMfma; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); /* MFMA */
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); /* DS read */
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0); /* VALU */
-        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0); /* DS write */
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); /* VMEM read */
-    }
-}
-
-template <int SCHEME, int BM, typename ASrc>
-__device__ __forceinline__ void pipe_step(uint8_t *lds, ASrc &asrc, const uint8_t *wrow, uint32_t k, uint32_t kt_n,
-                                          uint32_t cur, typename ASrc::Regs &pa, WRegs &pw,
-                                          typename ASrc::Regs &qa, WRegs &qw, const float *lutf,
-                                          r9vx_f32x16 (&acc)[BM / 32][2]) {
-    using S = MmaShape<BM, 2>;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t kp = k + 2 < kt_n ? k + 2 : kt_n - 1;
-    asrc.load(kp, qa);
-    load_w<SCHEME>(wrow, kp, qw);
-    const uint8_t *st = lds + cur * S::kStage;
-    mma_step<BM, false>(st, st + S::kABytes, wave, lane, acc);
-    uint8_t *nx = lds + (cur ^ 1u) * S::kStage;
-    asrc.store(pa, nx);
-    dequant_store<SCHEME>(pw, (k + 1) & 3, nx + S::kABytes, tid, lutf);
-    // interleave_hints<BM>();
-    __syncthreads();
-}
-
-template <int SCHEME, int BM, typename ASrc>
-__device__ __forceinline__ void mma_mainloop_pipe(uint8_t *lds, ASrc &asrc, const uint8_t *wrow, uint32_t kt_n,
-                                                  r9vx_f32x16 (&acc)[BM / 32][2]) {
-    using S = MmaShape<BM, 2>;
-    const uint32_t tid = threadIdx.x;
-    const float *lutf = reinterpret_cast<const float *>(lds + 2 * S::kStage);
-    if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS)
-        init_iq4_lut_f32(reinterpret_cast<r9vx_f32x4 *>(lds + 2 * S::kStage), tid);
-#pragma unroll
-    for (int i = 0; i < BM / 32; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-    typename ASrc::Regs ra0, ra1;
-    WRegs wq0, wq1;
-    asrc.load(0, ra0);
-    load_w<SCHEME>(wrow, 0, wq0);
-    const uint32_t k1 = kt_n > 1 ? 1 : 0;
-    asrc.load(k1, ra1);
-    load_w<SCHEME>(wrow, k1, wq1);
-    __syncthreads(); /* the codebook table */
-    asrc.store(ra0, lds);
-    dequant_store<SCHEME>(wq0, 0, lds + S::kABytes, tid, lutf);
-    __syncthreads();
-    for (uint32_t k = 0; k < kt_n; k += 2) {
-        /* step k: stage 0; step k+1's operands are in set 1; set 0 takes k+2 */
-        pipe_step<SCHEME, BM>(lds, asrc, wrow, k, kt_n, 0, ra1, wq1, ra0, wq0, lutf, acc);
-        if (k + 1 >= kt_n) break;
-        pipe_step<SCHEME, BM>(lds, asrc, wrow, k + 1, kt_n, 1, ra0, wq0, ra1, wq1, lutf, acc);
-    }
-}
-
 /* Row / column of accumulator register r of tile (i, j) for this lane. */
 __device__ __forceinline__ uint32_t acc_row(int i, int r, uint32_t lane) {
     return (uint32_t)(i * 32 + 8 * (r >> 2) + 4 * (int)(lane >> 5) + (r & 3));
@@ -320,36 +230,6 @@ struct AF16Rows {
     __device__ __forceinline__ void store(const Regs &r, uint8_t *A) const {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) *reinterpret_cast<r9vx_u32x4 *>(A + lds_chunk(row0 + 32 * i, chunk)) = r.v[i];
-    }
-};
-
-/* A source: f32 rows scaled by a per-row power of two, rounded to fp16. */
-template <int BM>
-struct AF32ScaledRows {
-    static constexpr int kPer = BM / 32;
-    struct Regs {
-        r9vx_f32x4 v[BM / 32][2];
-    };
-    const float *row[BM / 32];
-    float inv[BM / 32];
-    uint32_t chunk, row0;
-    __device__ __forceinline__ void load(uint32_t kt, Regs &r) const {
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const r9vx_f32x4 *p = reinterpret_cast<const r9vx_f32x4 *>(row[i] + kt * 64);
-            r.v[i][0] = p[0];
-            r.v[i][1] = p[1];
-        }
-    }
-    __device__ __forceinline__ void store(const Regs &r, uint8_t *A) const {
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const float s = inv[i];
-            const r9vx_f32x4 a = r.v[i][0], b = r.v[i][1];
-            *reinterpret_cast<r9vx_u32x4 *>(A + lds_chunk(row0 + 32 * i, chunk)) =
-                r9vx_u32x4{cvt_pk_h2(a.x * s, a.y * s), cvt_pk_h2(a.z * s, a.w * s), cvt_pk_h2(b.x * s, b.y * s),
-                           cvt_pk_h2(b.z * s, b.w * s)};
-        }
     }
 };
 

@@ -16,7 +16,10 @@
  *   h       f32[(P + S*T) * Dff]  SwiGLU rows in sorted order, shared rows after
  *   o       f32[(P + S*T) * Dm]   expert output rows in the same order
  *   hmax    u32[P + S*T]          bits of max|h| per row (grouped GEMM)
- *   x16     fp16[T * Dm], xscale f32[T]  scaled activations (grouped GEMM)
+ *   h16     fp16[(P + S*T) * Dff] h rows scaled by a power of two, in the down
+ *                                 weights' K group order (grouped GEMM)
+ *   x16     fp16[T * Dm], xscale f32[T]  scaled activations in the gate/up
+ *                                 weights' K group order (grouped GEMM)
  */
 #ifndef R9VX_MOE_H
 #define R9VX_MOE_H
@@ -31,7 +34,7 @@ constexpr uint32_t kMoeMaxK = 32;
 constexpr uint32_t kMoeTileM = 128; /* grouped-GEMM rows per tile */
 
 struct MoeLayout {
-    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, work, tiles, h, o, hmax, x16, xscale,
+    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, work, tiles, h, o, hmax, h16, x16, xscale,
         total;
     uint32_t max_tiles;
 };
@@ -62,6 +65,7 @@ inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint
     L.h = take(4ull * rows * dff);
     L.o = take(4ull * rows * dm);
     L.hmax = take(4ull * rows);
+    L.h16 = take(2ull * rows * dff);
     L.x16 = take(2ull * t_bucket * dm);
     L.xscale = take(4ull * t_bucket);
     L.total = off;
