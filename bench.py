@@ -4,10 +4,13 @@
 Headline: the IQ4_XS dequant-fused GEMV at
 K=2048, N=5120, M=5 (1 + 4 MTP draft tokens), bf16 x, f32 y.  A step is one
 GEMV launch over one batch; the weights rotate through enough distinct copies
-(>= 2x the 256 MB Infinity Cache) that every step reads them from HBM.
-`value` = algorithmic bytes / time of the K timed steps with every input
-resident in HBM.  `roofline` is the GEMV kernel's per-launch figure from
-back-to-back launches replayed from a HIP graph.
+(>= 2x the 256 MB Infinity Cache) that every step reads them from HBM.  The K
+timed steps are captured in one HIP graph and replayed once between two
+device synchronisations; `value` = algorithmic bytes per step / time per
+step, every input resident in HBM.  `roofline` is the same kernel's
+per-launch figure; `roofline.traffic` is the HBM bytes per launch that the
+FETCH_SIZE / WRITE_SIZE counters report (calibrated on a copy kernel of known
+size), read from the committed counter summary when it is present.
 
 `extras` carries the other configs with their own roofline figures:
 configs[0] Q4_K GEMV (HBM), configs[2] dense dequant-GEMM (MFMA),
@@ -17,6 +20,8 @@ restatement of R9V's T0 Branch-D path) on a bounded sample of the headline
 workload on this host.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c0,c2,...]
+    python bench.py --pmc-case c1m5          # short fixed run for rocprofv3 --pmc
+    python bench.py --pmc-summary DIR ...    # FETCH_SIZE/WRITE_SIZE dirs -> traffic text
 """
 from __future__ import annotations
 
@@ -42,6 +47,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list of extras: c0,c1m1,c2,c3,c4,ceilings")
+    ap.add_argument("--pmc-case", default="", help="run a short fixed workload for counter collection: c1m5")
+    ap.add_argument("--pmc-summary", nargs="*", default=None,
+                    help="rocprofv3 --pmc output dirs (FETCH_SIZE, WRITE_SIZE) to summarise as traffic")
     return ap.parse_args()
 
 
@@ -92,6 +100,32 @@ def graph_time(torch, fn, launches, reps=20):
     e1.record(cur)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / (reps * launches)
+
+
+def graph_steps(torch, fn, steps, warmup):
+    """ms per step of `steps` calls fn(i, stream) captured in one HIP graph:
+    `warmup` eager calls and one untimed replay first, then one replay timed
+    between two device synchronisations (events on the replay stream)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(max(warmup, 1)):
+            fn(i, s)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(steps):
+                fn(i, s)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(cur)
+    g.replay()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
 
 
 def hbm(bytes_, ms):
@@ -263,8 +297,96 @@ def bench_ceilings(torch, ffi):
     return out
 
 
+HEAD_KERNEL = "gemv_kernel<23, 5, false, 1>"  # IQ4_XS (type 23), M = 5, bf16 x, 1 chunk per lane
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_iq4xs_k2048_n5120_m5_traffic.txt")
+PMC_COPY_BYTES = 64 << 20
+
+
+def pmc_case(torch, ffi, synth, gsynth, name):
+    """A short fixed run for `rocprofv3 --pmc`: 200 headline GEMV launches over
+    rotated weight copies (the summary takes the median, so the first
+    launches' write-back of the copies' dirty cache lines does not count),
+    then 5 launches of a plain copy kernel of known size (torch.neg, f32 ->
+    f32, 64 MiB read + 64 MiB written) that calibrate what FETCH_SIZE /
+    WRITE_SIZE report per byte."""
+    if name != "c1m5":
+        raise SystemExit(f"unknown --pmc-case {name!r} (known: c1m5)")
+    head = Gemv(torch, ffi, synth, gsynth, ffi.IQ4_XS, 5120, 2048, 5, ffi.BF16, "c1m5")
+    for i in range(200):
+        head.launch(i)
+    src = torch.ones(PMC_COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_case": name, "gemv_launches": 200, "bytes_per_launch": head.bytes,
+                      "copy_bytes_read": PMC_COPY_BYTES, "copy_bytes_written": PMC_COPY_BYTES}))
+
+
+def pmc_summary(dirs):
+    """Medians of FETCH_SIZE / WRITE_SIZE (KiB per dispatch) from rocprofv3
+    counter-collection CSVs of `--pmc-case c1m5` runs, each scaled by the
+    copy kernel's reading of its known byte count."""
+    import csv
+    import glob
+    import statistics
+
+    per = {}
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                key = (r["Counter_Name"], r["Kernel_Name"])
+                per.setdefault(key, []).append(float(r["Counter_Value"]))
+    def find(counter, pred):
+        vals = [v for (c, k), v in per.items() if c == counter and pred(k)]
+        return [x for v in vals for x in v]
+    lines = ["counter      kernel                                      dispatches   median KiB/dispatch"]
+    out = {}
+    for counter, copy_bytes in (("FETCH_SIZE", PMC_COPY_BYTES), ("WRITE_SIZE", PMC_COPY_BYTES)):
+        g = find(counter, lambda k: HEAD_KERNEL.split("<")[0] in k and HEAD_KERNEL.split("<")[1][:6] in k)
+        c = find(counter, lambda k: "neg_kernel" in k or ("vectorized_elementwise_kernel" in k and "neg" in k.lower()))
+        if not g or not c:
+            lines.append(f"{counter:12s} (missing: headline {len(g)} / copy {len(c)} dispatches)")
+            continue
+        gm, cm = statistics.median(g), statistics.median(c)
+        factor = copy_bytes / (cm * 1024.0)
+        out[counter] = gm * 1024.0 * factor
+        lines.append(f"{counter:12s} {HEAD_KERNEL:43s} {len(g):10d}   {gm:12.1f}")
+        lines.append(f"{counter:12s} {'copy (torch.neg 64 MiB f32)':43s} {len(c):10d}   {cm:12.1f}")
+        lines.append(f"{counter:12s} calibration factor = {copy_bytes} B / ({cm:.1f} KiB * 1024) = {factor:.4f}")
+    if len(out) == 2:
+        lines.append(f"fetch_bytes_per_launch: {out['FETCH_SIZE']:.0f}")
+        lines.append(f"write_bytes_per_launch: {out['WRITE_SIZE']:.0f}")
+        lines.append(f"traffic_bytes_per_launch: {out['FETCH_SIZE'] + out['WRITE_SIZE']:.0f}")
+    print("\n".join(lines))
+
+
+def host_cpu():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return f"{line.split(':', 1)[1].strip()} ({os.cpu_count()} logical CPUs visible)"
+    except OSError:
+        pass
+    return "unknown host CPU"
+
+
+def read_traffic():
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     args = parse()
+    if args.pmc_summary is not None:
+        pmc_summary(args.pmc_summary)
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: multi-GPU figures are out of scope, "
                                    "run with --gpus 1"}))
@@ -280,6 +402,9 @@ def main():
         print(json.dumps({"error": "no GPU"}))
         return 1
     ffi.load()
+    if args.pmc_case:
+        pmc_case(torch, ffi, synth, gsynth, args.pmc_case)
+        return 0
     only = set(filter(None, args.only.split(",")))
 
     def want(name):
@@ -287,11 +412,10 @@ def main():
 
     log("c1 m5: IQ4_XS GEMV K=2048 N=5120 M=5")
     head = Gemv(torch, ffi, synth, gsynth, ffi.IQ4_XS, 5120, 2048, 5, ffi.BF16, "c1m5")
-    ms = event_time(torch, head.launch, args.steps, args.warmup)
+    ms = graph_steps(torch, lambda i, s: head.launch(i, s), args.steps, args.warmup)
     value = head.bytes / (ms * 1e-3) / 1e9
-    g_ms = head.graph_ms()
-    achieved = head.bytes / (g_ms * 1e-3) / 1e9
-    log(f"  {ms * 1e3:.2f} us/step stream, {g_ms * 1e3:.2f} us/launch graph -> {achieved:.0f} GB/s")
+    eager_ms = event_time(torch, head.launch, min(args.steps, 500), 20)
+    log(f"  {ms * 1e3:.2f} us/step graph-replayed ({value:.0f} GB/s), {eager_ms * 1e3:.2f} us/step eager")
 
     extras = {}
     if want("c1m1"):
@@ -319,7 +443,7 @@ def main():
         v, calls, el = head.cpu_baseline()
         cpu = {"value": round(v, 4), "unit": "GB/s", "cores": 1, "kind": "port",
                "sample": f"{calls} full configs[1] M=5 GEMVs by the oracle (scalar C restatement of T0 "
-                         f"Branch D, 1 thread) in {el:.1f} s"}
+                         f"Branch D, 1 thread) in {el:.1f} s on {host_cpu()}"}
 
     out = {
         "metric": METRIC,
@@ -336,11 +460,14 @@ def main():
         "data": "synthetic: seeded GGUF IQ4_XS blocks (uniform 4-bit indices / 6-bit scales, "
                 "d = f16|N(0,0.02)|), x ~ N(0,1) bf16",
         "config": {"workload": "configs[1]: IQ4_XS dequant GEMV K=2048 N=5120 M=5, x bf16, y f32",
-                   "weight_copies": len(head.ws), "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_kernel<IQ4_XS, M=5, bf16>", "bytes_per_launch": head.bytes,
-                     "us_per_launch": round(g_ms * 1e3, 3)},
+                   "weight_copies": len(head.ws), "parallelism": "single GPU",
+                   "timing": "K steps in one HIP graph, one replay between device synchronisations",
+                   "eager_us_per_step": round(eager_ms * 1e3, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+                     "kernel": HEAD_KERNEL, "bytes_per_launch": head.bytes,
+                     "us_per_launch": round(ms * 1e3, 3),
+                     "measured_ceiling": extras.get("measured_ceilings", {}).get("stream_5.6MB")},
         "cpu_baseline": cpu,
         "extras": extras,
     }

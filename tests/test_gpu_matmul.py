@@ -89,6 +89,44 @@ def test_gemv_config1_iq4xs_bf16(m):
 
 @pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])
 @pytest.mark.parametrize("x_dtype", [O.F32, O.BF16])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
+def test_gemv_k_and_n_sweep(scheme, x_dtype, m):
+    """Lanes-per-row widths 24 (K=768), 32, 64 with one and two chunks per lane."""
+    for n, k in ((77, 768), (130, 1024), (1000, 2048), (33, 4096), (9, 8192)):
+        got, ref = _gemv_case(scheme, n, k, m, x_dtype, seed=3500 + m + n)
+        check_close(got, ref, f"n={n} k={k} m={m}")
+
+
+def test_gemv_graph_replays_match_eager():
+    """GEMV launches captured in a HIP graph: every replay (with eager work
+    between replays) equals the eager result bit for bit."""
+    n, k, m = 5120, 2048, 5
+    w = dev(synth.quant_weights(O.IQ4_XS, 3701, n, k))
+    x = bf16_dev(synth.normal_bf16(3702, (m, k)))
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    ffi.matmul(w, O.IQ4_XS, n, k, x, y=y)
+    want = host(y).copy()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ffi.matmul(w, O.IQ4_XS, n, k, x, y=y, stream=s)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(3):
+                ffi.matmul(w, O.IQ4_XS, n, k, x, y=y, stream=s)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y.fill_(0.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(y), want)
+        ffi.matmul(w, O.IQ4_XS, n, k, x)  # eager work between replays
+        torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])
+@pytest.mark.parametrize("x_dtype", [O.F32, O.BF16])
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_gemv_all_m(scheme, x_dtype, m):
     got, ref = _gemv_case(scheme, 77, 1024, m, x_dtype, seed=3000 + m)
