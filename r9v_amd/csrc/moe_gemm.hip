@@ -87,8 +87,6 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(GroupedArgs a) {
         __syncthreads();
     }
     if (threadIdx.x == 0) status[3] = base;
-    uint32_t *hmax = reinterpret_cast<uint32_t *>(a.ws + a.L.hmax);
-    for (uint32_t i = threadIdx.x; i < a.p + a.shared * a.t; i += 1024) hmax[i] = 0u;
 }
 
 /* ---------------------------------------------------------------- gate/up */
@@ -107,7 +105,7 @@ constexpr int kStage = 32 * kMT * 128;       /* 16 KiB per A stage */
 template <int GU>
 __global__ __launch_bounds__(256, 2) void moe_gu_mfma_kernel(GroupedArgs a) {
     R9VX_MOE_STAGES
-    __shared__ uint32_t rowmax[kBM];
+    __shared__ float rowsc[kBM]; /* the tile rows' activation scales */
     const uint32_t *status = ws_u32(a, a.L.status);
     const uint32_t ntile_n = a.dff / 128;
     const uint32_t tix = blockIdx.x / ntile_n, nt = blockIdx.x % ntile_n;
@@ -116,7 +114,7 @@ __global__ __launch_bounds__(256, 2) void moe_gu_mfma_kernel(GroupedArgs a) {
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
     const uint32_t j0 = nt * 128;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid < kBM) rowmax[tid] = 0u;
+    if (tid < kBM) rowsc[tid] = tid < rows ? a.xscale[row_token(a, expert, pos0 + tid)] : 0.f;
     if constexpr (GU == R9VX_SCHEME_IQ4_XS) init_iq4_lut_f32(reinterpret_cast<r9vx_f32x4 *>(lutf), tid);
     __syncthreads();
 
@@ -133,6 +131,8 @@ __global__ __launch_bounds__(256, 2) void moe_gu_mfma_kernel(GroupedArgs a) {
     r9vx_f32x16 acc[kMT][2];
     m2_mainloop<GU, kMT, 2>(stages, asrc, wrow, a.dm / kTileK, wave, lane, lutf, acc);
 
+    /* SwiGLU on the accumulators; each h row's max|h| (its fp16 scale) is
+     * taken by h_to_f16, which reads the whole row anyway */
     float *h = reinterpret_cast<float *>(a.ws + a.L.h);
 #pragma unroll
     for (int i = 0; i < kMT; ++i) {
@@ -140,22 +140,20 @@ __global__ __launch_bounds__(256, 2) void moe_gu_mfma_kernel(GroupedArgs a) {
         for (int r = 0; r < 16; ++r) {
             const uint32_t rl = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (rl >= rows) continue;
-            const float sc = a.xscale[row_token(a, expert, pos0 + rl)];
+            const float sc = rowsc[rl];
             const float g = acc[i][0][r] * sc, u = acc[i][1][r] * sc;
             const float v = g / (1.0f + __expf(-g)) * u;
             h[(uint64_t)(pos0 + rl) * a.dff + col] = v;
-            atomicMax(&rowmax[rl], __builtin_bit_cast(uint32_t, fabsf(v)));
         }
     }
-    __syncthreads();
-    if (tid < rows) atomicMax(reinterpret_cast<uint32_t *>(a.ws + a.L.hmax) + pos0 + tid, rowmax[tid]);
 }
 
 /* ---------------------------------------------------------------- h -> fp16 */
 
-/* One wave per h row: lane l writes group l % 8 of K step l / 8 (+ 8 per
- * pass) as 8 fp16 in the down scheme's group order, scaled by 2^-e with
- * e = row_shift(max|h|). */
+/* One wave per h row: max|h| over the row (kept in hmax for the down GEMM's
+ * epilogue), then lane l writes group l % 8 of K step l / 8 (+ 8 per pass)
+ * as 8 fp16 in the down scheme's group order, scaled by 2^-e with e =
+ * row_shift(max|h|). */
 template <int DN>
 __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t nrows) {
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -163,7 +161,15 @@ __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t n
     const uint32_t *status = ws_u32(a, a.L.status);
     if (status[0] != 0u) return;
     const float *hr = reinterpret_cast<const float *>(a.ws + a.L.h) + (uint64_t)row * a.dff;
-    const float inv = ldexpf(1.0f, -row_shift(__builtin_bit_cast(float, ws_u32(a, a.L.hmax)[row])));
+    float mx = 0.f;
+    for (uint32_t c = lane; c < a.dff / 4; c += 64) {
+        const r9vx_f32x4 v = *reinterpret_cast<const r9vx_f32x4 *>(hr + 4 * c);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if (lane == 0) reinterpret_cast<uint32_t *>(a.ws + a.L.hmax)[row] = __builtin_bit_cast(uint32_t, mx);
+    const float inv = ldexpf(1.0f, -row_shift(mx));
     _Float16 *orow = a.h16 + (uint64_t)row * a.dff;
     for (uint32_t c = lane; c < a.dff / 8; c += 64) {
         const uint32_t base = (c >> 3) * 64, q = c & 7;
@@ -188,6 +194,10 @@ __global__ __launch_bounds__(256, 2) void moe_dn_mfma_kernel(GroupedArgs a) {
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
     const uint32_t n0 = nt * 256;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ float rowsc[kBM]; /* 2^e that undoes each h row's fp16 scale */
+    if (tid < kBM)
+        rowsc[tid] = tid < rows ? ldexpf(1.0f, row_shift(__builtin_bit_cast(float, ws_u32(a, a.L.hmax)[pos0 + tid])))
+                                : 0.f;
     if constexpr (DN == R9VX_SCHEME_IQ4_XS) init_iq4_lut_f32(reinterpret_cast<r9vx_f32x4 *>(lutf), tid);
     __syncthreads();
 
@@ -204,14 +214,13 @@ __global__ __launch_bounds__(256, 2) void moe_dn_mfma_kernel(GroupedArgs a) {
     m2_mainloop<DN, kMT, 2>(stages, asrc, wrow, a.dff / kTileK, wave, lane, lutf, acc);
 
     float *o = reinterpret_cast<float *>(a.ws + a.L.o);
-    const uint32_t *hmax = ws_u32(a, a.L.hmax);
 #pragma unroll
     for (int i = 0; i < kMT; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const uint32_t rl = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (rl >= rows) continue;
-            const float sc = ldexpf(1.0f, row_shift(__builtin_bit_cast(float, hmax[pos0 + rl])));
+            const float sc = rowsc[rl];
 #pragma unroll
             for (int j = 0; j < 2; ++j) o[(uint64_t)(pos0 + rl) * a.dm + c0 + 32 * j] = acc[i][j][r] * sc;
         }
