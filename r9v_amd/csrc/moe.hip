@@ -23,6 +23,7 @@
  */
 #include "r9vx_expf.h"
 #include "r9vx_gemv_core.h"
+#include "r9vx_mfma.h"
 #include "r9vx_moe.h"
 
 using namespace r9vx;
@@ -133,11 +134,14 @@ __global__ __launch_bounds__(1024) void sort_small_kernel(SortArgs a) {
     }
     if (tid == 0) offsets[a.e] = all;
     __syncthreads();
+    uint32_t *pinfo = reinterpret_cast<uint32_t *>(a.ws + L.pinfo);
     if (valid) {
         uint32_t pos = offs[id] + rank;
         reinterpret_cast<uint32_t *>(a.ws + L.sorted)[pos] = tid;
         reinterpret_cast<uint32_t *>(a.ws + L.inv)[tid] = pos;
+        if (!bad_sh) pinfo[pos] = (id << 16) | (tid / a.k);
     }
+    if (bad_sh && in) pinfo[tid] = ~0u; /* refused: no position is valid */
     /* compact work list of active experts, ascending id, then shared experts */
     uint32_t act = (tid < a.e && tot > 0) ? 1u : 0u;
     uint32_t n_act;
@@ -253,6 +257,7 @@ __global__ __launch_bounds__(256) void sort_place_kernel(SortArgs a, uint32_t nc
 
 struct FfnArgs {
     const uint16_t *x;
+    const uint32_t *ids;
     const uint8_t *w_gu;
     const uint8_t *w_dn;
     const float *weights;
@@ -262,16 +267,13 @@ struct FfnArgs {
     uint64_t gu_row_bytes; /* bytes per gate/up weight row (Dm/256 blocks) */
     uint64_t dn_row_bytes; /* bytes per down weight row (Dff/256 blocks) */
     uint32_t t, e, k, dm, dff, shared, p;
-    uint32_t gu_lpr_log2, gu_nseg;
-    uint32_t dn_lpr_log2, dn_nseg;
+    /* groups: row groups per sorted position; upw: units per wave */
+    uint32_t gu_lpr_log2, gu_nseg, gu_groups, gu_upw;
+    uint32_t dn_lpr_log2, dn_nseg, dn_groups, dn_upw;
 };
 
-/* Decode launch shape (compile-time tuning constants): activation rows per
- * pass, gate/up row pairs and down rows per lane group per wave, waves per
- * workgroup. */
-#ifndef R9VX_DEC_MT
-#define R9VX_DEC_MT 1
-#endif
+/* Decode launch shape (compile-time tuning constants): gate/up row pairs
+ * and down rows per lane group in one work unit, waves per workgroup. */
 #ifndef R9VX_DEC_GU_PAIRS
 #define R9VX_DEC_GU_PAIRS 1
 #endif
@@ -279,175 +281,301 @@ struct FfnArgs {
 #define R9VX_DEC_DN_ROWS 2
 #endif
 #ifndef R9VX_DEC_WAVES
-#define R9VX_DEC_WAVES 2
+#define R9VX_DEC_WAVES 4
 #endif
 constexpr int kDecPairs = R9VX_DEC_GU_PAIRS;
 constexpr int kDecDnRows = R9VX_DEC_DN_ROWS;
 constexpr int kDecWaves = R9VX_DEC_WAVES;
 
-__device__ __forceinline__ bool refused(const FfnArgs &a) {
-    return reinterpret_cast<const uint32_t *>(a.ws + a.L.status)[0] != 0u;
+/* Token and expert of sorted position pos (shared experts after the P
+ * routed pairs, T rows each); false when the call was refused. */
+__device__ __forceinline__ bool pos_meta(const FfnArgs &a, uint32_t pos, uint32_t &tok, uint32_t &expert) {
+    if (pos >= a.p) {
+        tok = (pos - a.p) % a.t;
+        expert = a.e + (pos - a.p) / a.t;
+        return true;
+    }
+    const uint32_t pi = reinterpret_cast<const uint32_t *>(a.ws + a.L.pinfo)[pos];
+    tok = pi & 0xFFFFu;
+    expert = pi >> 16;
+    return pi != ~0u;
 }
 
-__device__ __forceinline__ uint32_t token_of(const FfnArgs &a, uint32_t expert, uint32_t pos) {
-    if (expert >= a.e) return pos - (a.p + (expert - a.e) * a.t);
-    return reinterpret_cast<const uint32_t *>(a.ws + a.L.sorted)[pos] / a.k;
+/* Steps (unit, K segment) one wave carries; all of their weight loads are
+ * issued before any of them is used. */
+#ifndef R9VX_DEC_STEPS
+#define R9VX_DEC_STEPS 2
+#endif
+constexpr uint32_t kDecSteps = R9VX_DEC_STEPS;
+
+/* A wave's units: [u0, u0 + n), n <= upw, in sorted-position order, so that
+ * they walk consecutive weight rows; the host picks upw = max(1, kDecSteps /
+ * nseg) capped at the row groups per position, so a wave's units share at
+ * most two positions (expert, activation row).  A wave with more than
+ * kDecSteps steps (nseg > kDecSteps) takes them kDecSteps at a time. */
+__device__ __forceinline__ bool wave_units(uint32_t units, uint32_t upw, uint32_t &u0, uint32_t &n) {
+    const uint32_t gw = __builtin_amdgcn_readfirstlane(blockIdx.x * kDecWaves + (threadIdx.x >> 6));
+    u0 = gw * upw;
+    if (u0 >= units) return false;
+    n = units - u0 < upw ? units - u0 : upw;
+    return true;
 }
 
-/* gate/up GEMV + SwiGLU for one work item; block = 4 waves over Dff rows. */
-template <int GU, int MT>
+/* (position, row group, K segment) of a step, advanced without division */
+struct Cur {
+    uint32_t pos, g, seg;
+};
+__device__ __forceinline__ void advance(Cur &c, uint32_t nseg, uint32_t groups) {
+    if (++c.seg == nseg) {
+        c.seg = 0;
+        if (++c.g == groups) {
+            c.g = 0;
+            ++c.pos;
+        }
+    }
+}
+
+/* gate/up GEMV + SwiGLU.  A unit is kPairs * (64 / LPR) (gate, up) row
+ * pairs of one sorted position. */
+template <int GU>
 __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
     constexpr int kPairs = kDecPairs;
     __shared__ uint32_t lut[256];
     __shared__ uint64_t etab[R9VX_EXP2F_N];
-    const uint32_t *status = reinterpret_cast<const uint32_t *>(a.ws + a.L.status);
-    if (status[0] != 0u || blockIdx.x >= status[2]) return;
-    r9vx_exp2_fill(etab, threadIdx.x, blockDim.x); /* ordered by the LUT's barrier */
-    r9vx_u32x4 wk = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.work)[blockIdx.x];
-    const uint32_t expert = wk.x, beg = wk.y, cnt = wk.z;
+    if constexpr (GU == R9VX_SCHEME_IQ4_XS) init_iq4_lut(lut, threadIdx.x, blockDim.x);
+    r9vx_exp2_fill(etab, threadIdx.x, blockDim.x);
+    __syncthreads(); /* the last barrier: waves run independently from here */
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t lpr = 1u << a.gu_lpr_log2, rpi = 64u >> a.gu_lpr_log2;
     const uint32_t lir = lane & (lpr - 1), slot = lane >> a.gu_lpr_log2;
-    const uint32_t wave = blockIdx.y * kDecWaves + (threadIdx.x >> 6);
-    const uint32_t r0 = wave * rpi * kPairs + slot;
-    const uint8_t *wexp = a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes;
+    const uint32_t nseg = a.gu_nseg, groups = a.gu_groups;
+    uint32_t u0, n;
+    if (!wave_units((a.p + a.shared * a.t) * groups, a.gu_upw, u0, n)) return;
+    const uint32_t nsteps = n * nseg;
+    /* the (at most two) positions of the wave's units */
+    uint32_t tok[2], expert[2];
+    const uint32_t pos0 = u0 / groups, pos1 = (u0 + n - 1) / groups;
+    const bool ok0 = pos_meta(a, pos0, tok[0], expert[0]), ok1 = pos_meta(a, pos1, tok[1], expert[1]);
+    if (!ok0 || !ok1) return; /* refused: nothing is read or written */
     float *h = reinterpret_cast<float *>(a.ws + a.L.h);
-    bool lut_ready = false;
 
-    for (uint32_t t0 = 0; t0 < cnt; t0 += MT) {
-        const int m = (int)(cnt - t0 < (uint32_t)MT ? cnt - t0 : (uint32_t)MT);
-        const uint16_t *xrow[MT];
+    XChunk<GU, false> xc[1];
+    uint32_t xpos = ~0u, xseg = ~0u;
+    float ag[kPairs][1], au[kPairs][1];
+    Cur lc{pos0, u0 % groups, 0u}, c = lc; /* load and compute cursors */
+    r9vx_u32x4 qg[kDecSteps][kPairs], qu[kDecSteps][kPairs];
+    Hdr hg[kDecSteps][kPairs], hu[kDecSteps][kPairs];
+    for (uint32_t base = 0; base < nsteps; base += kDecSteps) {
+        /* 1. every weight load of the batch's steps (steps past the last repeat it) */
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-            uint32_t tok = token_of(a, expert, beg + t0 + (t < m ? t : 0));
-            xrow[t] = a.x + (uint64_t)tok * a.dm;
-        }
-        float ag[kPairs][MT], au[kPairs][MT];
-#pragma unroll
-        for (int r = 0; r < kPairs; ++r)
-#pragma unroll
-            for (int t = 0; t < MT; ++t) ag[r][t] = au[r][t] = 0.f;
-        for (uint32_t seg = 0; seg < a.gu_nseg; ++seg) {
-            uint32_t ci = seg * lpr + lir, klo, khi;
-            chunk_k<GU>(ci, klo, khi);
-            /* activations (L2-resident), then weights, then the table */
-            XRaw<false> xr[MT];
-#pragma unroll
-            for (int t = 0; t < MT; ++t)
-                if (t < m) load_x_raw<false>(xrow[t], klo, khi, xr[t]);
-            r9vx_u32x4 qg[kPairs], qu[kPairs];
-            Hdr hg[kPairs], hu[kPairs];
+        for (uint32_t s = 0; s < kDecSteps; ++s) {
+            const uint32_t w = lc.pos == pos0 ? 0u : 1u;
+            const uint32_t ci = lc.seg * lpr + lir;
+            const uint8_t *wexp = a.w_gu + (uint64_t)expert[w] * 2 * a.dff * a.gu_row_bytes;
 #pragma unroll
             for (int r = 0; r < kPairs; ++r) {
-                uint32_t row = r0 + r * rpi;
-                uint32_t rr = row < a.dff ? row : a.dff - 1;
-                load_chunk<GU>(wexp + (uint64_t)rr * a.gu_row_bytes, ci, qg[r], hg[r]);
-                load_chunk<GU>(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes, ci, qu[r], hu[r]);
+                const uint32_t row = (lc.g * kPairs + r) * rpi + slot;
+                const uint32_t rr = row < a.dff ? row : a.dff - 1;
+                load_chunk<GU>(wexp + (uint64_t)rr * a.gu_row_bytes, ci, qg[s][r], hg[s][r]);
+                load_chunk<GU>(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes, ci, qu[s][r], hu[s][r]);
             }
-            if (!lut_ready) { /* codebook and exp tables visible to every wave */
-                if constexpr (GU == R9VX_SCHEME_IQ4_XS) init_iq4_lut(lut, threadIdx.x, blockDim.x);
-                __syncthreads();
-                lut_ready = true;
-            }
-            XChunk<GU, false> xc[MT];
+            if (base + s + 1 < nsteps) advance(lc, nseg, groups);
+        }
+
+        /* 2. the steps in order; the arranged activation chunk is reused while
+         * (position, segment) stays the same */
 #pragma unroll
-            for (int t = 0; t < MT; ++t)
-                if (t < m) arrange_x<GU, false>(xr[t], xc[t]);
+        for (uint32_t s = 0; s < kDecSteps; ++s) {
+            if (base + s >= nsteps) break;
+            const uint32_t ci = c.seg * lpr + lir;
+            if (c.pos != xpos || c.seg != xseg) {
+                uint32_t klo, khi;
+                chunk_k<GU>(ci, klo, khi);
+                XRaw<false> xr;
+                load_x_raw<false>(a.x + (uint64_t)tok[c.pos == pos0 ? 0 : 1] * a.dm, klo, khi, xr);
+                arrange_x<GU, false>(xr, xc[0]);
+                xpos = c.pos;
+                xseg = c.seg;
+            }
+            if (c.seg == 0)
+#pragma unroll
+                for (int r = 0; r < kPairs; ++r) ag[r][0] = au[r][0] = 0.f;
 #pragma unroll
             for (int r = 0; r < kPairs; ++r) {
-                chunk_dot<GU, false, MT>(qg[r], hg[r], ci & 7, xc, ag[r], lut, m);
-                chunk_dot<GU, false, MT>(qu[r], hu[r], ci & 7, xc, au[r], lut, m);
+                chunk_dot<GU, false, 1>(qg[s][r], hg[s][r], ci & 7, xc, ag[r], lut);
+                chunk_dot<GU, false, 1>(qu[s][r], hu[s][r], ci & 7, xc, au[r], lut);
             }
+            if (c.seg + 1 == nseg) {
+                float gu[2][kPairs];
+#pragma unroll
+                for (int r = 0; r < kPairs; ++r) {
+                    gu[0][r] = ag[r][0];
+                    gu[1][r] = au[r][0];
+                }
+                const uint32_t pos = c.pos, g = c.g;
+                lane_reduce_w<kPairs, 2>(gu, lane, a.gu_lpr_log2, [&](int r, const float (&val)[2]) {
+                    const uint32_t row = (g * kPairs + r) * rpi + slot;
+                    if (row >= a.dff) return;
+                    const float gg = val[0];
+                    const float act = gg / (1.0f + r9vx_expf_tab(-gg, etab));
+                    h[(uint64_t)pos * a.dff + row] = act * val[1];
+                });
+            }
+            advance(c, nseg, groups);
         }
-        /* g and u go through the same reduction, so each emitted slot
-         * carries both halves of one (row, token) */
-        constexpr int V = kPairs * MT;
-        float gu[2][V];
-#pragma unroll
-        for (int r = 0; r < kPairs; ++r)
-#pragma unroll
-            for (int t = 0; t < MT; ++t) {
-                gu[0][r * MT + t] = ag[r][t];
-                gu[1][r * MT + t] = au[r][t];
-            }
-        lane_reduce_w<V, 2>(gu, lane, a.gu_lpr_log2, [&](int idx, const float (&val)[2]) {
-            const int r = idx / MT, t = idx % MT;
-            const uint32_t row = r0 + r * rpi;
-            if (t >= m || row >= a.dff) return;
-            const float g = val[0];
-            const float act = g / (1.0f + r9vx_expf_tab(-g, etab));
-            h[(uint64_t)(beg + t0 + t) * a.dff + row] = act * val[1];
-        });
     }
 }
 
-/* down GEMV for one work item: o[pos, d] = h[pos, :] . Wd[d, :]. */
-template <int DN, int MT>
+/* down GEMV: o[pos, d] = h[pos, :] . Wd[d, :]; a unit is kDecDnRows * (64 /
+ * LPR) rows of one sorted position. */
+template <int DN>
 __global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
-    constexpr int kDnRows = kDecDnRows;
+    constexpr int kRows = kDecDnRows;
     __shared__ uint32_t lut[256];
-    const uint32_t *status = reinterpret_cast<const uint32_t *>(a.ws + a.L.status);
-    if (status[0] != 0u || blockIdx.x >= status[2]) return;
-    r9vx_u32x4 wk = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.work)[blockIdx.x];
-    const uint32_t expert = wk.x, beg = wk.y, cnt = wk.z;
+    if constexpr (DN == R9VX_SCHEME_IQ4_XS) init_iq4_lut(lut, threadIdx.x, blockDim.x);
+    __syncthreads(); /* the last barrier: waves run independently from here */
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t lpr = 1u << a.dn_lpr_log2, rpi = 64u >> a.dn_lpr_log2;
     const uint32_t lir = lane & (lpr - 1), slot = lane >> a.dn_lpr_log2;
-    const uint32_t wave = blockIdx.y * kDecWaves + (threadIdx.x >> 6);
-    const uint32_t r0 = wave * rpi * kDnRows + slot;
-    const uint8_t *wexp = a.w_dn + (uint64_t)expert * a.dm * a.dn_row_bytes;
+    const uint32_t nseg = a.dn_nseg, groups = a.dn_groups;
+    uint32_t u0, n;
+    if (!wave_units((a.p + a.shared * a.t) * groups, a.dn_upw, u0, n)) return;
+    const uint32_t nsteps = n * nseg;
+    uint32_t tok[2], expert[2];
+    const uint32_t pos0 = u0 / groups, pos1 = (u0 + n - 1) / groups;
+    const bool ok0 = pos_meta(a, pos0, tok[0], expert[0]), ok1 = pos_meta(a, pos1, tok[1], expert[1]);
+    if (!ok0 || !ok1) return;
     const float *h = reinterpret_cast<const float *>(a.ws + a.L.h);
     float *o = reinterpret_cast<float *>(a.ws + a.L.o);
-    bool lut_ready = false;
 
-    for (uint32_t t0 = 0; t0 < cnt; t0 += MT) {
-        const int m = (int)(cnt - t0 < (uint32_t)MT ? cnt - t0 : (uint32_t)MT);
-        float acc[kDnRows][MT];
+    /* The h chunk of (position, segment), arranged once and reused while it
+     * stays the same.  Q4_K: h scaled by 2^-e (e from the row's max|h|, so
+     * |h| < 2^15) and rounded once to fp16, paired like the weights; weights
+     * as fp16 1024 + q, so one v_dot2_f32_f16 does two products exactly in
+     * f32, and the 1024 offset comes off with the sums of the same rounded
+     * values.  IQ4_XS: the f32 path of the dense GEMV. */
+    constexpr bool kF16 = DN == R9VX_SCHEME_Q4_K;
+    XChunk<DN, true> xc[1];
+    uint32_t hp[16];
+    float hsc = 1.f, slo = 0.f, shi = 0.f;
+    uint32_t xpos = ~0u, xseg = ~0u, rpos = ~0u;
+    float acc[kRows][1];
+    Cur lc{pos0, u0 % groups, 0u}, c = lc; /* load and compute cursors */
+    r9vx_u32x4 q[kDecSteps][kRows];
+    Hdr hd[kDecSteps][kRows];
+    for (uint32_t base = 0; base < nsteps; base += kDecSteps) {
+        /* every weight load of the batch's steps (steps past the last repeat it) */
 #pragma unroll
-        for (int r = 0; r < kDnRows; ++r)
+        for (uint32_t s = 0; s < kDecSteps; ++s) {
+            const uint32_t w = lc.pos == pos0 ? 0u : 1u;
+            const uint32_t ci = lc.seg * lpr + lir;
+            const uint8_t *wexp = a.w_dn + (uint64_t)expert[w] * a.dm * a.dn_row_bytes;
 #pragma unroll
-            for (int t = 0; t < MT; ++t) acc[r][t] = 0.f;
-        for (uint32_t seg = 0; seg < a.dn_nseg; ++seg) {
-            uint32_t ci = seg * lpr + lir, klo, khi;
-            chunk_k<DN>(ci, klo, khi);
-            XRaw<true> xr[MT];
-#pragma unroll
-            for (int t = 0; t < MT; ++t)
-                if (t < m) load_x_raw<true>(h + (uint64_t)(beg + t0 + t) * a.dff, klo, khi, xr[t]);
-            r9vx_u32x4 q[kDnRows];
-            Hdr hd[kDnRows];
-#pragma unroll
-            for (int r = 0; r < kDnRows; ++r) {
-                uint32_t row = r0 + r * rpi;
-                uint32_t rr = row < a.dm ? row : a.dm - 1;
-                load_chunk<DN>(wexp + (uint64_t)rr * a.dn_row_bytes, ci, q[r], hd[r]);
+            for (int r = 0; r < kRows; ++r) {
+                const uint32_t row = (lc.g * kRows + r) * rpi + slot;
+                const uint32_t rr = row < a.dm ? row : a.dm - 1;
+                load_chunk<DN>(wexp + (uint64_t)rr * a.dn_row_bytes, ci, q[s][r], hd[s][r]);
             }
-            if constexpr (DN == R9VX_SCHEME_IQ4_XS) {
-                if (!lut_ready) {
-                    init_iq4_lut(lut, threadIdx.x, blockDim.x);
-                    __syncthreads();
-                    lut_ready = true;
+            if (base + s + 1 < nsteps) advance(lc, nseg, groups);
+        }
+#pragma unroll
+        for (uint32_t s = 0; s < kDecSteps; ++s) {
+            if (base + s >= nsteps) break;
+            const uint32_t ci = c.seg * lpr + lir;
+            if (c.pos != xpos || c.seg != xseg) {
+                uint32_t klo, khi;
+                chunk_k<DN>(ci, klo, khi);
+                XRaw<true> xr;
+                const float *hrow = h + (uint64_t)c.pos * a.dff;
+                load_x_raw<true>(hrow, klo, khi, xr);
+                if constexpr (kF16) {
+                    if (c.pos != rpos) { /* the row's scale: max|h| over the row */
+                        float mx = 0.f;
+                        for (uint32_t i = lane; i < a.dff / 4; i += 64) {
+                            const r9vx_f32x4 v = *reinterpret_cast<const r9vx_f32x4 *>(hrow + 4 * i);
+                            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+                        }
+#pragma unroll
+                        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+                        hsc = ldexpf(1.0f, row_shift(mx));
+                        rpos = c.pos;
+                    }
+                    const float inv = 1.0f / hsc; /* a power of two: exact */
+                    float lo[16], hi[16];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            lo[4 * i + j] = xr.v[i][j] * inv;
+                            hi[4 * i + j] = xr.v[4 + i][j] * inv;
+                        }
+                    /* dword d of the payload holds bytes 4d..4d+3: pairs
+                     * {lo(4d), lo(4d+2)}, {lo(4d+1), lo(4d+3)}, {hi(4d), hi(4d+2)},
+                     * {hi(4d+1), hi(4d+3)} */
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        hp[4 * d + 0] = pack_h2(lo[4 * d], lo[4 * d + 2]);
+                        hp[4 * d + 1] = pack_h2(lo[4 * d + 1], lo[4 * d + 3]);
+                        hp[4 * d + 2] = pack_h2(hi[4 * d], hi[4 * d + 2]);
+                        hp[4 * d + 3] = pack_h2(hi[4 * d + 1], hi[4 * d + 3]);
+                    }
+                    const uint32_t one2 = 0x3C003C00u; /* fp16 {1, 1} */
+                    slo = 0.f;
+                    shi = 0.f;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        slo = r9vx_dot2_f16(hp[4 * d + 0], one2, slo);
+                        slo = r9vx_dot2_f16(hp[4 * d + 1], one2, slo);
+                        shi = r9vx_dot2_f16(hp[4 * d + 2], one2, shi);
+                        shi = r9vx_dot2_f16(hp[4 * d + 3], one2, shi);
+                    }
+                } else {
+                    arrange_x<DN, true>(xr, xc[0]);
+                }
+                xpos = c.pos;
+                xseg = c.seg;
+            }
+            if (c.seg == 0)
+#pragma unroll
+                for (int r = 0; r < kRows; ++r) acc[r][0] = 0.f;
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) {
+                if constexpr (kF16) {
+                    const uint32_t qw[4] = {q[s][r].x, q[s][r].y, q[s][r].z, q[s][r].w};
+                    const Hdr &hh = hd[s][r];
+                    const float d = r9vx_f16_to_f32((uint16_t)(hh.v.x & 0xFFFF));
+                    const float dmin = r9vx_f16_to_f32((uint16_t)(hh.v.x >> 16));
+                    uint32_t sc[2], mn[2];
+                    r9vx_q4k_scale_pair(hh.v, (ci & 7) >> 1, sc, mn);
+                    const float dl0 = d * (float)sc[0], dl1 = d * (float)sc[1];
+                    const float off0 = fmaf(1024.f, dl0, dmin * (float)mn[0]);
+                    const float off1 = fmaf(1024.f, dl1, dmin * (float)mn[1]);
+                    float dlo = 0.f, dhi = 0.f;
+#pragma unroll
+                    for (int dw = 0; dw < 4; ++dw) {
+                        dlo = r9vx_dot2_f16((qw[dw] & 0x000F000Fu) | 0x64006400u, hp[4 * dw + 0], dlo);
+                        dlo = r9vx_dot2_f16(((qw[dw] >> 8) & 0x000F000Fu) | 0x64006400u, hp[4 * dw + 1], dlo);
+                        dhi = r9vx_dot2_f16(((qw[dw] >> 4) & 0x000F000Fu) | 0x64006400u, hp[4 * dw + 2], dhi);
+                        dhi = r9vx_dot2_f16(((qw[dw] >> 12) & 0x000F000Fu) | 0x64006400u, hp[4 * dw + 3], dhi);
+                    }
+                    acc[r][0] += hsc * (dl0 * dlo + dl1 * dhi - (off0 * slo + off1 * shi));
+                } else {
+                    chunk_dot<DN, true, 1>(q[s][r], hd[s][r], ci & 7, xc, acc[r], lut);
                 }
             }
-            XChunk<DN, true> xc[MT];
+            if (c.seg + 1 == nseg) {
+                float v[1][kRows];
 #pragma unroll
-            for (int t = 0; t < MT; ++t)
-                if (t < m) arrange_x<DN, true>(xr[t], xc[t]);
-#pragma unroll
-            for (int r = 0; r < kDnRows; ++r) chunk_dot<DN, true, MT>(q[r], hd[r], ci & 7, xc, acc[r], lut, m);
+                for (int r = 0; r < kRows; ++r) v[0][r] = acc[r][0];
+                const uint32_t pos = c.pos, g = c.g;
+                lane_reduce_w<kRows, 1>(v, lane, a.dn_lpr_log2, [&](int r, const float (&val)[1]) {
+                    const uint32_t row = (g * kRows + r) * rpi + slot;
+                    if (row >= a.dm) return;
+                    o[(uint64_t)pos * a.dm + row] = val[0];
+                });
+            }
+            advance(c, nseg, groups);
         }
-        constexpr int V = kDnRows * MT;
-        float v[1][V];
-#pragma unroll
-        for (int r = 0; r < kDnRows; ++r)
-#pragma unroll
-            for (int t = 0; t < MT; ++t) v[0][r * MT + t] = acc[r][t];
-        lane_reduce_w<V, 1>(v, lane, a.dn_lpr_log2, [&](int idx, const float (&val)[1]) {
-            const int r = idx / MT, t = idx % MT;
-            const uint32_t row = r0 + r * rpi;
-            if (t >= m || row >= a.dm) return;
-            o[(uint64_t)(beg + t0 + t) * a.dm + row] = val[0];
-        });
     }
 }
 
@@ -540,26 +668,10 @@ int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream
     return (int)hipGetLastError();
 }
 
-template <int MT>
-static void launch_decode_mt(const FfnArgs &f, uint32_t gu_scheme, uint32_t dn_scheme, uint32_t max_work,
-                             hipStream_t s) {
-    const uint32_t gu_rows_per_block = kDecWaves * (64u >> f.gu_lpr_log2) * kDecPairs;
-    const uint32_t dn_rows_per_block = kDecWaves * (64u >> f.dn_lpr_log2) * kDecDnRows;
-    dim3 ggu(max_work, (f.dff + gu_rows_per_block - 1) / gu_rows_per_block);
-    dim3 gdn(max_work, (f.dm + dn_rows_per_block - 1) / dn_rows_per_block);
-    if (gu_scheme == R9VX_SCHEME_IQ4_XS)
-        hipLaunchKernelGGL((moe_gu_kernel<R9VX_SCHEME_IQ4_XS, MT>), ggu, dim3(kDecWaves * 64), 0, s, f);
-    else
-        hipLaunchKernelGGL((moe_gu_kernel<R9VX_SCHEME_Q4_K, MT>), ggu, dim3(kDecWaves * 64), 0, s, f);
-    if (dn_scheme == R9VX_SCHEME_Q4_K)
-        hipLaunchKernelGGL((moe_down_kernel<R9VX_SCHEME_Q4_K, MT>), gdn, dim3(kDecWaves * 64), 0, s, f);
-    else
-        hipLaunchKernelGGL((moe_down_kernel<R9VX_SCHEME_IQ4_XS, MT>), gdn, dim3(kDecWaves * 64), 0, s, f);
-}
-
 int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s) {
     FfnArgs f{};
     f.x = p.x;
+    f.ids = p.ids;
     f.w_gu = p.w_gu;
     f.w_dn = p.w_dn;
     f.weights = p.weights;
@@ -577,8 +689,32 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
     f.p = p.t * p.k;
     f.gu_lpr_log2 = lpr_for(p.dm, f.gu_nseg);
     f.dn_lpr_log2 = lpr_for(p.dff, f.dn_nseg);
-    uint32_t max_work = (f.p < p.e ? f.p : p.e) + p.shared;
-    launch_decode_mt<R9VX_DEC_MT>(f, p.scheme_gu, p.scheme_dn, max_work, s);
+    const uint32_t gu_rows = kDecPairs * (64u >> f.gu_lpr_log2), dn_rows = kDecDnRows * (64u >> f.dn_lpr_log2);
+    f.gu_groups = (p.dff + gu_rows - 1) / gu_rows;
+    f.dn_groups = (p.dm + dn_rows - 1) / dn_rows;
+    /* one wave per upw units of (position, row group); a unit is nseg steps */
+    const uint32_t npos = f.p + p.shared * p.t;
+    auto upw_for = [](uint32_t groups, uint32_t nseg) {
+        uint32_t upw = kDecSteps / nseg;
+        if (upw < 1) upw = 1;
+        return upw < groups ? upw : groups;
+    };
+    f.gu_upw = upw_for(f.gu_groups, f.gu_nseg);
+    f.dn_upw = upw_for(f.dn_groups, f.dn_nseg);
+    auto grid_for = [&](uint32_t groups, uint32_t upw) {
+        const uint32_t units = npos * groups;
+        const uint32_t waves = (units + upw - 1) / upw;
+        return dim3((waves + kDecWaves - 1) / kDecWaves);
+    };
+    const dim3 block(kDecWaves * 64);
+    if (p.scheme_gu == R9VX_SCHEME_IQ4_XS)
+        hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_IQ4_XS>, grid_for(f.gu_groups, f.gu_upw), block, 0, s, f);
+    else
+        hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_Q4_K>, grid_for(f.gu_groups, f.gu_upw), block, 0, s, f);
+    if (p.scheme_dn == R9VX_SCHEME_Q4_K)
+        hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_Q4_K>, grid_for(f.dn_groups, f.dn_upw), block, 0, s, f);
+    else
+        hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_IQ4_XS>, grid_for(f.dn_groups, f.dn_upw), block, 0, s, f);
     return (int)hipGetLastError();
 }
 

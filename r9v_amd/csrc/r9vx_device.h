@@ -51,6 +51,12 @@ __device__ __forceinline__ uint16_t r9vx_f32_to_bf16(float v) {
     return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
+typedef _Float16 r9vx_f16x2 __attribute__((ext_vector_type(2)));
+/* c + a.lo * b.lo + a.hi * b.hi, fp16 pairs, f32 accumulate (v_dot2_f32_f16). */
+__device__ __forceinline__ float r9vx_dot2_f16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(r9vx_f16x2, a), __builtin_bit_cast(r9vx_f16x2, b), c, false);
+}
+
 __device__ __forceinline__ float r9vx_dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(r9vx_bf16x2, a),
                                           __builtin_bit_cast(r9vx_bf16x2, b), c, false);

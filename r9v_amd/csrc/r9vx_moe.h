@@ -20,6 +20,8 @@
  *                                 weights' K group order (grouped GEMM)
  *   x16     fp16[T * Dm], xscale f32[T]  scaled activations in the gate/up
  *                                 weights' K group order (grouped GEMM)
+ *   pinfo   u32[P]   expert << 16 | token of each sorted position, all ones
+ *                    when the call is refused (decode path)
  */
 #ifndef R9VX_MOE_H
 #define R9VX_MOE_H
@@ -35,7 +37,7 @@ constexpr uint32_t kMoeTileM = 128; /* grouped-GEMM rows per tile */
 
 struct MoeLayout {
     uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, work, tiles, h, o, hmax, h16, x16, xscale,
-        total;
+        pinfo, total;
     uint32_t max_tiles;
 };
 
@@ -68,6 +70,7 @@ inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint
     L.h16 = take(2ull * rows * dff);
     L.x16 = take(2ull * t_bucket * dm);
     L.xscale = take(4ull * t_bucket);
+    L.pinfo = take(4 * p);
     L.total = off;
     return L;
 }
