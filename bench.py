@@ -297,7 +297,7 @@ def bench_ceilings(torch, ffi):
     return out
 
 
-HEAD_KERNEL = "gemv_kernel<23, 5, false, 1>"  # IQ4_XS (type 23), M = 5, bf16 x, 1 chunk per lane
+HEAD_KERNEL = "gemv_kernel<23, 5, false, 1, 6, 5>"  # IQ4_XS (type 23), M = 5, bf16 x, 1 chunk per lane, 64 lanes per row, 5 rows per lane group
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_iq4xs_k2048_n5120_m5_traffic.txt")
 PMC_COPY_BYTES = 64 << 20
 

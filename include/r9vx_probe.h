@@ -15,9 +15,11 @@
 extern "C" {
 #endif
 
-/* Streams `bytes` (a multiple of 16) from `src` with 128-bit loads and writes
- * one u32 checksum per workgroup to `sink` (>= r9vx_probe_stream_blocks()
- * u32).  Duration / bytes is the measured HBM read ceiling. */
+/* Streams `bytes` (a multiple of 16) from `src` with 128-bit loads; `sink`
+ * (>= r9vx_probe_stream_blocks() u32) is written only if a workgroup's
+ * checksum equals a sentinel the caller's fill pattern avoids, so a launch
+ * reads and does not write.  Duration / bytes is the measured HBM read
+ * ceiling. */
 int r9vx_probe_stream_launch(const void *src, uint64_t bytes, uint32_t *sink, r9vx_stream_t stream);
 uint32_t r9vx_probe_stream_blocks(uint64_t bytes);
 /* Runs `iters` dependent rounds of 16 independent v_mfma_f32_32x32x16_f16

@@ -49,16 +49,23 @@ constexpr int waves_for(int m) { return m <= 2 ? 2 : 1; }
 
 using namespace r9vx;
 
-template <int SCHEME, int M, bool XF32, int SPL>
+/* LPRL = 6: 64 lanes per row, a single K segment (K = 2048*SPL), f32 y and
+ * no epilogue, all fixed at compile time (measured 0.4-0.6 us faster per
+ * launch at configs[1] than the general form), and RR rows per lane group
+ * chosen by the launcher to balance the waves over the SIMDs; LPRL = 0:
+ * lanes per row, segment count and epilogue come from the arguments and
+ * the rows per lane group from rows_for(M). */
+template <int SCHEME, int M, bool XF32, int SPL, int LPRL, int RR>
 __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
-    constexpr int kRows = rows_for(M), kWaves = waves_for(M);
+    constexpr int kRows = RR ? RR : rows_for(M), kWaves = waves_for(M);
     __shared__ uint32_t lut[256];
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
-    const uint32_t lpr = 1u << a.lpr_log2;
-    const uint32_t rpi = 64u >> a.lpr_log2; /* row slots per wave */
+    const uint32_t lprl = LPRL ? (uint32_t)LPRL : a.lpr_log2;
+    const uint32_t lpr = 1u << lprl;
+    const uint32_t rpi = 64u >> lprl; /* row slots per wave */
     const uint32_t lir = lane & (lpr - 1);
-    const uint32_t slot = lane >> a.lpr_log2;
+    const uint32_t slot = lane >> lprl;
     const uint32_t row0 = wave * rpi * kRows + slot;
 
     float acc[kRows][M];
@@ -67,7 +74,8 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int t = 0; t < M; ++t) acc[r][t] = 0.f;
 
-    for (uint32_t seg = 0; seg < a.nseg; ++seg) {
+    const uint32_t nseg = LPRL ? 1u : a.nseg;
+    for (uint32_t seg = 0; seg < nseg; ++seg) {
         uint32_t cis[SPL];
 #pragma unroll
         for (int s = 0; s < SPL; ++s) cis[s] = seg * lpr * SPL + s * lpr + lir;
@@ -86,6 +94,10 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
                 load_x_raw<XF32>(xb, klo, khi, xr[s][t]);
             }
         }
+        /* keep every activation load ahead of the weight loads: loads
+         * complete in order, so an activation load scheduled after a weight
+         * load would hold the activation re-arrangement until HBM answers */
+        __builtin_amdgcn_sched_barrier(0);
         r9vx_u32x4 qs[kRows][SPL];
         Hdr hd[kRows][SPL];
 #pragma unroll
@@ -98,7 +110,7 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
         }
         /* 2. the codebook table is built while the loads are in flight */
         if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
-            if (seg == 0) {
+            if (LPRL != 0 || seg == 0) {
                 init_iq4_lut(lut, threadIdx.x, blockDim.x);
                 __syncthreads();
             }
@@ -123,11 +135,15 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
     for (int r = 0; r < kRows; ++r)
 #pragma unroll
         for (int t = 0; t < M; ++t) v[0][r * M + t] = acc[r][t];
-    lane_reduce_w<V, 1>(v, lane, a.lpr_log2, [&](int idx, const float (&val)[1]) {
+    auto emit = [&](int idx, const float (&val)[1]) {
         const int r = idx / M, t = idx % M;
         const uint32_t row = row0 + r * rpi;
         if (row >= a.n) return;
         float y = val[0];
+        if constexpr (LPRL != 0) {
+            reinterpret_cast<float *>(a.y)[(uint64_t)t * a.n + row] = y;
+            return;
+        }
         if (a.epilogue == R9VX_EPILOGUE_BIAS) y += a.bias[row];
         if (a.epilogue == R9VX_EPILOGUE_RESIDUAL) y += a.residual[(uint64_t)t * a.n + row];
         const uint64_t o = (uint64_t)t * a.n + row;
@@ -135,7 +151,49 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
             reinterpret_cast<uint16_t *>(a.y)[o] = r9vx_f32_to_bf16(y);
         else
             reinterpret_cast<float *>(a.y)[o] = y;
-    });
+    };
+    if constexpr (LPRL != 0)
+        lane_reduce<V, 1 << LPRL, 1>(v, lane, emit);
+    else
+        lane_reduce_w<V, 1>(v, lane, a.lpr_log2, emit);
+}
+
+/* SIMDs of the current device (4 per CU), for the wave-balance rule. */
+uint32_t device_simds() {
+    static uint32_t cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
+    if (!cached[dev]) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        cached[dev] = 4u * (uint32_t)cus;
+    }
+    return cached[dev];
+}
+
+/* Rows per lane group for the compile-time form at M >= 3: the R in 2..5 whose wave
+ * count ceil(n / R) puts the fewest rows on the busiest SIMD,
+ * ceil(waves / simds) * R; ties go to the smaller R.  At n = 5120 this is
+ * R = 5 (1024 waves, one per SIMD), measured 5.28 us against 5.47 us for
+ * R = 3 at M = 5. */
+uint32_t balanced_rows(uint32_t n, uint32_t simds) {
+    uint32_t best = 2, best_cost = ~0u;
+    for (uint32_t r = 2; r <= 5; ++r) {
+        const uint32_t waves = (n + r - 1) / r;
+        const uint32_t cost = (waves + simds - 1) / simds * r;
+        if (cost < best_cost) best = r, best_cost = cost;
+    }
+    return best;
+}
+
+template <int SCHEME, bool XF32, int SPL, int MM, int LPRL, int RR>
+int launch_rows(const GemvArgs &a, uint32_t rows_per_slot_group, hipStream_t s) {
+    /* rows_per_slot_group = lane groups per wave (64 / LPR) */
+    const uint32_t rows_per_wave = rows_per_slot_group * (RR ? RR : rows_for(MM));
+    const uint32_t waves = (a.n + rows_per_wave - 1) / rows_per_wave;
+    const dim3 grid((waves + waves_for(MM) - 1) / waves_for(MM));
+    hipLaunchKernelGGL((gemv_kernel<SCHEME, MM, XF32, SPL, LPRL, RR>), grid, dim3(waves_for(MM) * 64), 0, s, a);
+    return (int)hipGetLastError();
 }
 
 template <int SCHEME, bool XF32, int SPL, int MM>
@@ -144,12 +202,18 @@ int launch_one(const GemvArgs &a, uint32_t m, uint32_t rows_per_slot_group, hipS
         return (int)hipErrorInvalidValue;
     } else {
         if (m != MM) return launch_one<SCHEME, XF32, SPL, MM - 1>(a, m, rows_per_slot_group, s);
-        /* rows_per_slot_group = lane groups per wave (64 / LPR) */
-        const uint32_t rows_per_wave = rows_per_slot_group * rows_for(MM);
-        const uint32_t waves = (a.n + rows_per_wave - 1) / rows_per_wave;
-        const dim3 grid((waves + waves_for(MM) - 1) / waves_for(MM));
-        hipLaunchKernelGGL((gemv_kernel<SCHEME, MM, XF32, SPL>), grid, dim3(waves_for(MM) * 64), 0, s, a);
-        return (int)hipGetLastError();
+        if (a.lpr_log2 == 6 && a.nseg == 1 && a.epilogue == R9VX_EPILOGUE_NONE && !a.y_bf16) {
+            /* one or two activation rows: two rows per lane group measured
+             * best whatever the balance (3.65 us at n = 5120, M = 1, against
+             * 3.77 us for four rows) */
+            switch (MM <= 2 ? 2u : balanced_rows(a.n, device_simds())) {
+            case 2: return launch_rows<SCHEME, XF32, SPL, MM, 6, 2>(a, 1, s);
+            case 3: return launch_rows<SCHEME, XF32, SPL, MM, 6, 3>(a, 1, s);
+            case 4: return launch_rows<SCHEME, XF32, SPL, MM, 6, 4>(a, 1, s);
+            default: return launch_rows<SCHEME, XF32, SPL, MM, 6, 5>(a, 1, s);
+            }
+        }
+        return launch_rows<SCHEME, XF32, SPL, MM, 0, 0>(a, rows_per_slot_group, s);
     }
 }
 
