@@ -78,6 +78,52 @@ def test_route_ties_bias_sigmoid_scale():
     _assert_bit_exact(*_route_both(tied, 10))
 
 
+def _quotient_tie_rows(n_rows, e):
+    """Softmax rows where two experts' exp values differ by one ulp but their
+    quotients by the ordered sum round to the same f32, with the larger value
+    at the higher id (5) and the smaller at id 3; expert 0 holds the maximum
+    logit 0 and every other expert -200 (exp = 0).  Found by search with the
+    host libm expf (the function the oracle and the reference call)."""
+    import ctypes
+
+    libm = ctypes.CDLL("libm.so.6")
+    libm.expf.restype, libm.expf.argtypes = ctypes.c_float, [ctypes.c_float]
+    f32 = np.float32
+    rng = np.random.default_rng(2026)
+    rows = []
+    while len(rows) < n_rows:
+        l1 = f32(-0.105 + rng.uniform(-0.01, 0.01))
+        v1 = f32(libm.expf(l1))
+        l2, v2 = l1, v1
+        for _ in range(64):
+            l2 = np.nextafter(l2, f32(-1))
+            v2 = f32(libm.expf(l2))
+            if v2 < v1:
+                break
+        if v2 != np.nextafter(v1, f32(0)):
+            continue
+        s = f32(f32(f32(1.0) + v2) + v1)  # ascending id: 0, 3, 5
+        if f32(v1 / s) != f32(v2 / s):
+            continue
+        row = np.full(e, -200.0, np.float32)
+        row[0], row[3], row[5] = 0.0, l2, l1
+        rows.append(row)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("e", [64, 512])
+def test_route_quotient_ties_bit_exact(e):
+    """The reference ranks the divided scores, where id 3 beats id 5 on the
+    tie; ranking the undivided exp values would put id 5 first.  Covers the
+    router's tie test at the K-th/(K+1)-th boundary (K=2) and between two
+    selected neighbours (K=3), and the exact path it falls back to."""
+    logits = _quotient_tie_rows(6, e)
+    for k in (2, 3):
+        o, g = _route_both(logits, k)
+        assert (o[0][:, 1] == 3).all(), "oracle must take id 3 on the quotient tie"
+        _assert_bit_exact(o, g)
+
+
 @pytest.mark.parametrize("t", [4, 300])
 def test_route_refuses_nonfinite_before_writing(t):
     logits = synth.normal_f32(901, (t, 64))
