@@ -111,7 +111,7 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
         /* 2. the codebook table is built while the loads are in flight */
         if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
             if (LPRL != 0 || seg == 0) {
-                init_iq4_lut(lut, threadIdx.x, blockDim.x);
+                build_iq4_lut(lut, threadIdx.x, blockDim.x);
                 __syncthreads();
             }
         }
@@ -173,15 +173,16 @@ uint32_t device_simds() {
 
 /* Rows per lane group for the compile-time form at M >= 3: the R in 2..5 whose wave
  * count ceil(n / R) puts the fewest rows on the busiest SIMD,
- * ceil(waves / simds) * R; ties go to the smaller R.  At n = 5120 this is
- * R = 5 (1024 waves, one per SIMD), measured 5.28 us against 5.47 us for
- * R = 3 at M = 5. */
+ * ceil(waves / simds) * R; ties go to the larger R, which loads and
+ * re-arranges the activations for more rows at once (at large n every R
+ * ties).  At n = 5120 this is R = 5 (1024 waves, one per SIMD), measured
+ * 5.28 us against 5.47 us for R = 3 at M = 5. */
 uint32_t balanced_rows(uint32_t n, uint32_t simds) {
     uint32_t best = 2, best_cost = ~0u;
     for (uint32_t r = 2; r <= 5; ++r) {
         const uint32_t waves = (n + r - 1) / r;
         const uint32_t cost = (waves + simds - 1) / simds * r;
-        if (cost < best_cost) best = r, best_cost = cost;
+        if (cost <= best_cost) best = r, best_cost = cost;
     }
     return best;
 }

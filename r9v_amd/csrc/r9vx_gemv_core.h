@@ -368,8 +368,36 @@ __device__ __forceinline__ void lane_reduce_w(float (&v)[N][V], uint32_t lane, u
     }
 }
 
-/* IQ4_XS bf16 codebook-pair table: entry b = {kv[b & 15], kv[b >> 4]}. */
+/* IQ4_XS bf16 codebook-pair table: entry b = {kv[b & 15], kv[b >> 4]}
+ * (codebook crates/r9v-format/src/iq_lut.rs:23-25; every value is a small
+ * integer, so its bf16 is the top half of its f32 exactly).  Built at compile
+ * time; a workgroup copies it to LDS with one 16-byte load per thread
+ * (computing it per workgroup cost ~60 VALU per wave). */
+struct Iq4PairLut {
+    uint32_t v[256];
+};
+constexpr Iq4PairLut make_iq4_pair_lut() {
+    constexpr int kv[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+    Iq4PairLut t{};
+    for (int b = 0; b < 256; ++b) {
+        const uint32_t lo = __builtin_bit_cast(uint32_t, (float)kv[b & 15]) >> 16;
+        const uint32_t hi = __builtin_bit_cast(uint32_t, (float)kv[b >> 4]) >> 16;
+        t.v[b] = lo | (hi << 16);
+    }
+    return t;
+}
+__device__ const Iq4PairLut kIq4PairLut = make_iq4_pair_lut();
+
 __device__ __forceinline__ void init_iq4_lut(uint32_t *lut, uint32_t tid, uint32_t nthreads) {
+    const r9vx_u32x4 *src = reinterpret_cast<const r9vx_u32x4 *>(kIq4PairLut.v);
+    for (uint32_t i = tid; i < 64; i += nthreads) reinterpret_cast<r9vx_u32x4 *>(lut)[i] = src[i];
+}
+
+/* The table computed in VALU instead (r9vx_iq4_kvalue per nibble), for the
+ * latency-bound dense GEMV, which builds it while its HBM loads are in
+ * flight: any memory operation there (the copy above, issued before or after
+ * the HBM loads) measured 0.2-0.6 us slower per launch at configs[1]. */
+__device__ __forceinline__ void build_iq4_lut(uint32_t *lut, uint32_t tid, uint32_t nthreads) {
     for (uint32_t i = tid; i < 256; i += nthreads) {
         uint32_t lo = __builtin_bit_cast(uint32_t, (float)r9vx_iq4_kvalue(i & 15)) >> 16;
         uint32_t hi = __builtin_bit_cast(uint32_t, (float)r9vx_iq4_kvalue(i >> 4)) >> 16;
