@@ -204,10 +204,14 @@ int launch_one(const GemvArgs &a, uint32_t m, uint32_t rows_per_slot_group, hipS
     } else {
         if (m != MM) return launch_one<SCHEME, XF32, SPL, MM - 1>(a, m, rows_per_slot_group, s);
         if (a.lpr_log2 == 6 && a.nseg == 1 && a.epilogue == R9VX_EPILOGUE_NONE && !a.y_bf16) {
-            /* one or two activation rows: two rows per lane group measured
-             * best whatever the balance (3.65 us at n = 5120, M = 1, against
-             * 3.77 us for four rows) */
-            switch (MM <= 2 ? 2u : balanced_rows(a.n, device_simds())) {
+            /* one or two activation rows: two rows per lane group while
+             * the launch is latency-bound (n = 5120, M = 1: 3.90 us against
+             * 3.98-4.22 us for R = 3..5); from n >= 8 * SIMDs the launch is
+             * issue-bound and more rows per group amortise the per-wave work
+             * (n = 20480, M = 1: 7.52 us at R = 4 against 8.05 at R = 2;
+             * n = 51200: 15.0 against 16.6 us) */
+            const uint32_t simds = device_simds();
+            switch (MM <= 2 && a.n < 8 * simds ? 2u : balanced_rows(a.n, simds)) {
             case 2: return launch_rows<SCHEME, XF32, SPL, MM, 6, 2>(a, 1, s);
             case 3: return launch_rows<SCHEME, XF32, SPL, MM, 6, 3>(a, 1, s);
             case 4: return launch_rows<SCHEME, XF32, SPL, MM, 6, 4>(a, 1, s);
