@@ -57,6 +57,10 @@ uint32_t block_bytes(uint32_t s) {
 
 }  // namespace
 
+/* Sets the calling thread's r9vx_last_error() text (used by the other host
+ * sources of the library). */
+void r9vx_set_last_error(const std::string &text) { g_last_error = text; }
+
 extern "C" {
 
 const char *r9vx_last_error(void) { return g_last_error.c_str(); }

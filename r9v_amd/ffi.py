@@ -28,6 +28,7 @@ BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136}
 
 _P = ctypes.c_void_p
 _U32 = ctypes.c_uint32
+_U64 = ctypes.c_uint64
 
 
 class MatmulStatic(ctypes.Structure):
@@ -88,6 +89,40 @@ EXPORTS = [
     ("r9vx_probe_stream_launch", [_P, ctypes.c_uint64, _P, _P], ctypes.c_int),
     ("r9vx_probe_stream_blocks", [ctypes.c_uint64], _U32),
     ("r9vx_probe_mfma_launch", [_U32, _U32, _P, _P], ctypes.c_int),
+    # include/r9vx_gguf.h
+    ("r9vx_gguf_parse", [_P, _U64, _P], ctypes.c_int),
+    ("r9vx_gguf_parse_table", [_P, _U64, _U64, _P], ctypes.c_int),
+    ("r9vx_gguf_free", [_P], None),
+    ("r9vx_gguf_last_problems", [], _U32),
+    ("r9vx_gguf_version", [_P], _U32),
+    ("r9vx_gguf_alignment", [_P], _U64),
+    ("r9vx_gguf_data_start", [_P], _U64),
+    ("r9vx_gguf_file_size", [_P], _U64),
+    ("r9vx_gguf_ranges", [_P, _P], None),
+    ("r9vx_gguf_n_kv", [_P], _U64),
+    ("r9vx_gguf_find_kv", [_P, ctypes.c_char_p], ctypes.c_int64),
+    ("r9vx_gguf_kv_info", [_P, _U64, _P, _P, _P, _P, _P], ctypes.c_int),
+    ("r9vx_gguf_kv_value", [_P, _U64, _U64, _P], ctypes.c_int),
+    ("r9vx_gguf_n_tensors", [_P], _U64),
+    ("r9vx_gguf_find_tensor", [_P, ctypes.c_char_p], ctypes.c_int64),
+    ("r9vx_gguf_tensor_at", [_P, _U64, _P], ctypes.c_int),
+    ("r9vx_gguf_tensor_bytes", [_P, ctypes.c_char_p, _P, _U64, _P, _P], ctypes.c_int),
+    ("r9vx_gguf_entry_xxh3", [_P, ctypes.c_char_p, _P, _U64, _P], ctypes.c_int),
+    ("r9vx_gguf_is_native", [_P], ctypes.c_int),
+    ("r9vx_gguf_type_size", [_U32, _P, _P], ctypes.c_int),
+    ("r9vx_gguf_type_name", [_U32], ctypes.c_char_p),
+    ("r9vx_xxh3_64", [_P, _U64], _U64),
+    ("r9vx_gguf_shards_open", [_P, _U32, _P], ctypes.c_int),
+    ("r9vx_gguf_shards_free", [_P], None),
+    ("r9vx_gguf_shards_len", [_P], _U64),
+    ("r9vx_gguf_shards_tensor_at", [_P, _U64, _P, _P], ctypes.c_int),
+    ("r9vx_gguf_shards_find", [_P, ctypes.c_char_p], ctypes.c_int64),
+    ("r9vx_gguf_matmul_static", [_P, ctypes.c_char_p, _P], ctypes.c_int),
+    ("r9vx_gguf_moe_ffn_static", [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _P],
+     ctypes.c_int),
+    ("r9vx_gguf_upload", [_P, _P, _U64, ctypes.c_char_p, _P, _U64, _P], ctypes.c_int),
+    ("r9vx_gguf_upload_gate_up", [_P, _P, _U64, ctypes.c_char_p, _P, _P, _U64, ctypes.c_char_p,
+                                  _P, _U64, _P], ctypes.c_int),
 ]
 
 _lib = None

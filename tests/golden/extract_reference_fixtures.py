@@ -6,6 +6,9 @@ Data only (inputs and expected outputs); run once in the build container where
       consumed by crates/r9v-format/tests/schemes.rs:482-516)
   crates/r9v-format/tests/fixtures/r9v-format/iq_a24_reference.txt (the IQ4_XS and
       IQ4_NL cases, consumed by crates/r9v-format/tests/iq.rs:159-197)
+  crates/r9v-format/tests/fixtures/r9v-format/{a25_standard,a25_split-0000{1,2}-of-00002,
+      llama_tiny_q80}.hex (whole GGUF files as hex text, consumed by
+      crates/r9v-format/tests/container.rs:72-330, 897-930) -> tests/golden/gguf/
 The reference is Apache-2.0; the fixture data derives from llama.cpp / gguf-py (MIT).
 """
 import pathlib
@@ -34,6 +37,13 @@ def main() -> int:
     (DST / "iq4_reference.txt").write_text(
         HEADER.format(src="crates/r9v-format/tests/fixtures/r9v-format/iq_a24_reference.txt")
         + "\n".join(out) + "\n")
+    gdir = DST / "gguf"
+    gdir.mkdir(exist_ok=True)
+    for name in ("a25_standard", "a25_split-00001-of-00002", "a25_split-00002-of-00002",
+                 "llama_tiny_q80"):
+        src = f"crates/r9v-format/tests/fixtures/r9v-format/{name}.hex"
+        (gdir / f"{name}.hex").write_text(
+            HEADER.format(src=src) + (SRC / f"{name}.hex").read_text().strip() + "\n")
     return 0
 
 

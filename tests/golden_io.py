@@ -57,3 +57,11 @@ def iq4_cases():
             "y_bits": np.frombuffer(bytes.fromhex(c["y"]), dtype="<u4"),
         }
     return out
+
+
+def gguf_fixture(name: str) -> bytes:
+    """A whole GGUF file from tests/golden/gguf/<name>.hex (the reference's
+    crates/r9v-format/tests/fixtures/r9v-format/<name>.hex; '#' lines are the
+    provenance header)."""
+    text = (GOLDEN / "gguf" / f"{name}.hex").read_text()
+    return bytes.fromhex("".join(l for l in text.splitlines() if not l.startswith("#")))
