@@ -51,9 +51,20 @@ enum r9vx_dtype {
 /* Weight schemes: GGUF ggml type codes (crates/r9v-format/src/ggml.rs:38;
  * codes checked by crates/r9v-format/tests/iq.rs:131-141). */
 enum r9vx_scheme {
-    R9VX_SCHEME_Q4_K = 12,  /* 144-B super-block per 256 weights */
-    R9VX_SCHEME_IQ4_XS = 23 /* 136-B super-block per 256 weights */
+    R9VX_SCHEME_Q8_0 = 8,    /* 34-B block per 32 weights; device layout split (below) */
+    R9VX_SCHEME_Q4_K = 12,   /* 144-B super-block per 256 weights */
+    R9VX_SCHEME_Q6_K = 14,   /* 210-B super-block per 256 weights; device layout split */
+    R9VX_SCHEME_IQ4_XS = 23  /* 136-B super-block per 256 weights */
 };
+/* Q4_K and IQ4_XS are read as GGUF wire blocks.  Q8_0 and Q6_K blocks (34 and
+ * 210 bytes) are not 16-byte multiples, so the device reads them in a split
+ * layout made at load time by r9vx_repack_launch (or r9vx_gguf_upload_split):
+ *   Q8_0: body = int8 [N, K] (the 32 quants of each block, in order),
+ *         w_scales = f16 [N, K/32] (each block's d);
+ *   Q6_K: body = [N, K/256] blocks of 208 bytes (ql 128, qh 64, scales 16,
+ *         the wire block without its trailing d), w_scales = f16 [N, K/256].
+ * Bodies and scales together hold exactly the wire bytes.  A matmul on them
+ * passes the body as `w` and the d array as `w_scales`. */
 
 /* Matmul epilogues (crates/r9v-t0/src/matmul.rs:2421-2446). */
 enum r9vx_epilogue { R9VX_EPILOGUE_NONE = 0, R9VX_EPILOGUE_BIAS = 1, R9VX_EPILOGUE_RESIDUAL = 2 };
@@ -84,7 +95,7 @@ typedef struct r9vx_matmul_static {
     uint32_t m_bucket;       /* M bucket; the launch's dynamic m <= m_bucket */
     uint32_t n;              /* output columns N */
     uint32_t k;              /* reduction length K, a multiple of 256 */
-    uint32_t w_scheme;       /* enum r9vx_scheme; weights are GGUF wire blocks [N, K/256] */
+    uint32_t w_scheme;       /* enum r9vx_scheme: Q4_K / IQ4_XS wire blocks, or Q8_0 / Q6_K split */
     uint32_t in_dtype;       /* F32 (m <= 8 GEMV only) or BF16 */
     uint32_t out_dtype;      /* F32 or BF16 (RNE) */
     uint32_t epilogue;       /* enum r9vx_epilogue */
@@ -93,8 +104,8 @@ typedef struct r9vx_matmul_static {
 
 /* matmul ABI struct (crates/r9v-kgen/src/abi/per_op.rs:794-868). */
 typedef struct r9vx_matmul_args {
-    const uint8_t *w;         /* GGUF blocks, row n at n * (K/256) * block_bytes */
-    const void *w_scales;     /* must be NULL: GGUF scales are inline */
+    const uint8_t *w;         /* GGUF blocks (row n at n * (K/256) * block_bytes), or a split body */
+    const void *w_scales;     /* Q8_0 / Q6_K: f16 d per block; NULL for Q4_K / IQ4_XS (inline) */
     const uint8_t *w_indices; /* must be NULL: no sparsity on this path */
     const void *x;            /* [m, K] in_dtype */
     const float *x_scale;     /* must be NULL: activations are not quantized */
@@ -210,15 +221,25 @@ int r9vx_moe_sort_launch(const r9vx_moe_ffn_static *st, const uint32_t *expert_i
 /* ------------------------------------------------------------ weights / decode */
 
 /* Bit-exact decode of GGUF wire blocks to f32 [n_rows, k]: the
- * ggml_dequantize of crates/r9v-format/src/ggml.rs:1025-1150 (Q4_K) and
- * crates/r9v-format/src/iq.rs:578-598 (IQ4_XS). */
+ * ggml_dequantize of crates/r9v-format/src/ggml.rs:1025-1150 (Q4_K; Q8_0
+ * :1094-1100 and Q6_K :1154-1172 with block_values :627-640, :817-850) and
+ * crates/r9v-format/src/iq.rs:578-598 (IQ4_XS).  Q8_0 / Q6_K are read in wire
+ * form here. */
 int r9vx_dequantize_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k,
                            float *out, r9vx_stream_t stream);
 /* Load-time scale validation (check_wire_f16, crates/r9v-format/src/ggml.rs:421):
- * counts blocks with a non-finite d (or dmin) into *bad_blocks (device u32,
- * caller-zeroed). */
+ * counts wire blocks with a non-finite d (or dmin) into *bad_blocks (device
+ * u32, caller-zeroed). */
 int r9vx_validate_weights_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows,
                                  uint32_t k, uint32_t *bad_blocks, r9vx_stream_t stream);
+
+/* Load-time repack of Q8_0 / Q6_K wire blocks [n_rows, k] (device memory)
+ * into the split device layout above: body and scales may not overlap the
+ * wire.  The counterpart of the reference's load-time repack to its L1 layout
+ * (crates/r9v-format/src/repack.rs:282).  Q4_K and IQ4_XS need none and are
+ * refused. */
+int r9vx_repack_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k,
+                       uint8_t *body, uint16_t *scales, r9vx_stream_t stream);
 
 /* ------------------------------------------------------------------ misc */
 

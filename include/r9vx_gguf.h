@@ -169,8 +169,9 @@ int64_t r9vx_gguf_shards_find(const r9vx_gguf_shards *s, const char *name);
 
 /* ---------------------------------------------------- binding and upload */
 
-/* Variant key of a matmul over the 2-D Q4_K / IQ4_XS tensor `name` (file dims
- * {K, N}): sets st->n, st->k and st->w_scheme, leaves the other fields.  This
+/* Variant key of a matmul over the 2-D Q4_K / IQ4_XS / Q6_K / Q8_0 tensor
+ * `name` (file dims {K, N}): sets st->n, st->k and st->w_scheme, leaves the
+ * other fields.  Q6_K / Q8_0 weights are loaded with r9vx_gguf_upload_split.  This
  * is the shape-and-scheme part of a MatmulStatic the loader derives from a
  * checkpoint (crates/r9v-registry/src/types.rs:727-770). */
 int r9vx_gguf_matmul_static(const r9vx_gguf *f, const char *name, r9vx_matmul_static *st);
@@ -189,6 +190,14 @@ int r9vx_gguf_moe_ffn_static(const r9vx_gguf *f, const char *gate, const char *u
  * `bytes` must stay valid until the stream reaches it. */
 int r9vx_gguf_upload(const r9vx_gguf *f, const uint8_t *bytes, uint64_t len, const char *name,
                      void *dst, uint64_t dst_bytes, r9vx_stream_t stream);
+/* Loads a Q8_0 / Q6_K tensor into the split device layout of include/r9vx.h
+ * (body + f16 d array), the load-time repack of these types: the blocks are
+ * split on the host, non-finite d values are refused (check_wire_f16,
+ * crates/r9v-format/src/ggml.rs:421) before anything is copied, and the call
+ * returns after both copies have completed on `stream`. */
+int r9vx_gguf_upload_split(const r9vx_gguf *f, const uint8_t *bytes, uint64_t len, const char *name,
+                           void *body, uint64_t body_bytes, uint16_t *scales, uint64_t scales_bytes,
+                           r9vx_stream_t stream);
 /* Builds moe_ffn's w_gate_up [E, 2*Dff, Dm] in device memory from stacked
  * gate and up expert tensors [E, Dff, Dm] (which may sit in different shards):
  * expert e's gate rows, then its up rows (crates/r9v-t0/src/moe_ffn.rs:51-55),

@@ -76,12 +76,17 @@ static inline uint16_t rd_u16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1]
  * ---------------------------------------------------------------------- */
 
 uint32_t rxo_block_bytes(int scheme) {
-    /* crates/r9v-format/tests/iq.rs:131-141 and ggml.rs block table:
-     * Q4_K 144 B / 256 weights, IQ4_XS 136 B / 256 weights. */
+    /* crates/r9v-format/tests/iq.rs:131-141 and ggml.rs:336-350 block table:
+     * Q4_K 144 B / 256 weights, IQ4_XS 136 B / 256, Q6_K 210 B / 256,
+     * Q8_0 34 B / 32. */
     if (scheme == RXO_Q4_K) return 144;
     if (scheme == RXO_IQ4_XS) return 136;
+    if (scheme == RXO_Q6_K) return 210;
+    if (scheme == RXO_Q8_0) return 34;
     return 0;
 }
+
+uint32_t rxo_block_len(int scheme) { return scheme == RXO_Q8_0 ? 32 : (rxo_block_bytes(scheme) ? 256 : 0); }
 
 /* crates/r9v-format/src/ggml.rs:973-995 (unpack_k4_scales), identical to
  * records.rs:190-206 (I4KSuperblock::from_bytes). */
@@ -145,11 +150,39 @@ static void iq4xs_block(const uint8_t *blk, float *out) {
     }
 }
 
+/* One Q6_K block -> 256 f32.  crates/r9v-format/src/ggml.rs:817-850
+ * (block_values: value i = flat index big*32+big_p takes its low nibble from
+ * byte (i/128)*64 + i%64, nibble (i%128)/64, and its high two bits from byte
+ * 128 + (i/128)*32 + i%32, bit pair (i%128)/32) and :1154-1172 (dequant:
+ * dl = d * (i8)scales[j] for the j-th group of 16, w = dl * (q - 32)). */
+static void q6k_block(const uint8_t *blk, float *out) {
+    float d = rxo_f16_to_f32(rd_u16(blk + 208));
+    for (int j = 0; j < 16; ++j) {
+        float dl = d * (float)(int8_t)blk[192 + j];
+        for (int p = 0; p < 16; ++p) {
+            int i = j * 16 + p;
+            int lo = (blk[(i / 128) * 64 + i % 64] >> (4 * ((i % 128) / 64))) & 0x0F;
+            int hi = (blk[128 + (i / 128) * 32 + i % 32] >> (2 * ((i % 128) / 32))) & 0x03;
+            out[i] = dl * ((float)(lo | (hi << 4)) - 32.0f);
+        }
+    }
+}
+
+/* One Q8_0 block -> 32 f32.  crates/r9v-format/src/ggml.rs:627-640 (values
+ * are the raw bytes at 2+i) and :1094-1100 (w = d * (i8)v). */
+static void q80_block(const uint8_t *blk, float *out) {
+    float d = rxo_f16_to_f32(rd_u16(blk));
+    for (int i = 0; i < 32; ++i) out[i] = d * (float)(int8_t)blk[2 + i];
+}
+
+/* Byte offset of a block's f16 scale d that check_wire_f16 validates. */
+static uint32_t d_offset(int scheme) { return scheme == RXO_Q6_K ? 208 : 0; }
+
 static int check_scales(int scheme, const uint8_t *wire, uint64_t nblocks) {
     uint32_t bb = rxo_block_bytes(scheme);
     for (uint64_t b = 0; b < nblocks; ++b) {
         const uint8_t *blk = wire + b * bb;
-        if (!wire_scale_ok(rd_u16(blk))) return RXO_ERR_SCALE;
+        if (!wire_scale_ok(rd_u16(blk + d_offset(scheme)))) return RXO_ERR_SCALE;
         if (scheme == RXO_Q4_K && !wire_scale_ok(rd_u16(blk + 2))) return RXO_ERR_SCALE;
     }
     return RXO_OK;
@@ -157,12 +190,18 @@ static int check_scales(int scheme, const uint8_t *wire, uint64_t nblocks) {
 
 /* Row decode shared by dequantize and the matmul oracles. */
 static void decode_row(int scheme, const uint8_t *row, uint32_t k, float *out) {
-    uint32_t bb = rxo_block_bytes(scheme);
-    for (uint32_t b = 0; b < k / 256; ++b) {
+    uint32_t bb = rxo_block_bytes(scheme), bl = rxo_block_len(scheme);
+    for (uint32_t b = 0; b < k / bl; ++b) {
+        const uint8_t *blk = row + (uint64_t)b * bb;
+        float *o = out + (uint64_t)b * bl;
         if (scheme == RXO_Q4_K)
-            q4k_block(row + (uint64_t)b * bb, out + (uint64_t)b * 256);
+            q4k_block(blk, o);
+        else if (scheme == RXO_IQ4_XS)
+            iq4xs_block(blk, o);
+        else if (scheme == RXO_Q6_K)
+            q6k_block(blk, o);
         else
-            iq4xs_block(row + (uint64_t)b * bb, out + (uint64_t)b * 256);
+            q80_block(blk, o);
     }
 }
 
@@ -170,11 +209,12 @@ static void decode_row(int scheme, const uint8_t *row, uint32_t k, float *out) {
  * block, then decode in ascending order. */
 int rxo_dequantize(int scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k, float *out) {
     if (rxo_block_bytes(scheme) == 0) return RXO_ERR_SCHEME;
-    if (k == 0 || k % 256 != 0) return RXO_ERR_SHAPE;
-    uint64_t nblocks = (uint64_t)n_rows * (k / 256);
+    const uint32_t bl = rxo_block_len(scheme);
+    if (k == 0 || k % bl != 0) return RXO_ERR_SHAPE;
+    uint64_t nblocks = (uint64_t)n_rows * (k / bl);
     int rc = check_scales(scheme, wire, nblocks);
     if (rc) return rc;
-    uint64_t row_bytes = (uint64_t)(k / 256) * rxo_block_bytes(scheme);
+    uint64_t row_bytes = (uint64_t)(k / bl) * rxo_block_bytes(scheme);
     for (uint32_t r = 0; r < n_rows; ++r)
         decode_row(scheme, wire + r * row_bytes, k, out + (uint64_t)r * k);
     return RXO_OK;
@@ -203,7 +243,7 @@ static inline void write_y(int y_dtype, void *y, uint64_t i, float v) {
 static int matmul_rows(int scheme, const uint8_t *w, uint32_t n0, uint32_t n1, uint32_t n,
                        uint32_t k, int x_dtype, const void *x, uint32_t m, const float *bias,
                        const float *residual, int y_dtype, void *y, float *wrow, float *xrow) {
-    uint64_t row_bytes = (uint64_t)(k / 256) * rxo_block_bytes(scheme);
+    uint64_t row_bytes = (uint64_t)(k / rxo_block_len(scheme)) * rxo_block_bytes(scheme);
     (void)xrow;
     for (uint32_t col = n0; col < n1; ++col) {
         decode_row(scheme, w + col * row_bytes, k, wrow);
@@ -229,7 +269,7 @@ static int matmul_validate(int scheme, const uint8_t *w, uint32_t n, uint32_t k,
     if (x_dtype != RXO_F32 && x_dtype != RXO_BF16) return RXO_ERR_DTYPE;
     if (y_dtype != RXO_F32 && y_dtype != RXO_BF16) return RXO_ERR_DTYPE;
     if (bias && residual) return RXO_ERR_SHAPE;
-    return check_scales(scheme, w, (uint64_t)n * (k / 256));
+    return check_scales(scheme, w, (uint64_t)n * (k / rxo_block_len(scheme)));
 }
 
 int rxo_matmul(int scheme, const uint8_t *w, uint32_t n, uint32_t k, int x_dtype,

@@ -15,6 +15,9 @@
  *   rxo_f16_to_f32, rxo_f32_to_bf16 ... exhaustive/closed-form tests
  *   rxo_q4k_*  ... reference golden vectors q4k_reference.txt (6 cases)
  *   rxo_iq4xs_* ... reference golden vectors iq_a24_reference.txt (IQ4_XS)
+ *   Q6_K / Q8_0 decode ... reference golden vectors gguf_a23_reference.txt
+ *                  (gguf-py 0.19.0 dequantize), and a numpy restatement of
+ *                  the llama.cpp row loop (dequantize_row_q6_K form)
  *   rxo_matmul ... known answer 1408.0 (matmul_tests.rs:208-265), f64
  *                  brute force on tiny shapes, batch invariance
  *   rxo_moe_route ... equal-logit lowest-id answers (moe_route_tests.rs:107),
@@ -36,6 +39,8 @@ extern "C" {
 /* Weight schemes: GGUF type codes (r9v-format ggml.rs GgmlType codes). */
 #define RXO_Q4_K 12
 #define RXO_IQ4_XS 23
+#define RXO_Q6_K 14
+#define RXO_Q8_0 8
 
 /* Element dtypes: discriminant order of r9v-ir DType (dtype.rs:15-35). */
 #define RXO_F32 0
@@ -56,8 +61,9 @@ uint16_t rxo_f32_to_bf16(float v);
 float rxo_bf16_to_f32(uint16_t bits);
 
 /* ---- block decode ----------------------------------------------------- */
-/* GGUF block geometry. */
+/* GGUF block geometry: bytes per block and weights per block. */
 uint32_t rxo_block_bytes(int scheme);
+uint32_t rxo_block_len(int scheme);
 /* Q4_K: 12-byte packed 6-bit scales -> sc[8], mn[8]. */
 void rxo_q4k_unpack_scales(const uint8_t payload[12], uint8_t sc[8], uint8_t mn[8]);
 /* Decodes n_rows x k weights from GGUF wire blocks into out (row-major f32).

@@ -1,6 +1,6 @@
 /*
- * dequant.hip -- bit-exact GGUF Q4_K / IQ4_XS decode to f32, and load-time
- * scale validation.
+ * dequant.hip -- bit-exact GGUF Q4_K / IQ4_XS / Q8_0 / Q6_K decode to f32,
+ * load-time scale validation, and the Q8_0 / Q6_K split repack.
  *
  * Q4_K: crates/r9v-format/src/ggml.rs:744-790 (nibble order) and :1131-1150
  *   (w = (d*sc)*q - (dmin*mn), each product rounded, then the subtraction).
@@ -110,5 +110,143 @@ int r9vx_launch_validate(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, 
         hipLaunchKernelGGL(validate_kernel<R9VX_SCHEME_Q4_K>, grid, dim3(256), 0, stream, wire, n_blocks, bad);
     else
         hipLaunchKernelGGL(validate_kernel<R9VX_SCHEME_IQ4_XS>, grid, dim3(256), 0, stream, wire, n_blocks, bad);
+    return (int)hipGetLastError();
+}
+
+/* ------------------------------------------------------------------------
+ * Q8_0 and Q6_K: wire decode (bit-exact), scale validation, and the
+ * load-time split into the device layout the GEMV reads.  Wire blocks of 34
+ * and 210 bytes are only 2-byte aligned, so these kernels read them as
+ * 16-bit words; they run once per weight load, not per matmul.
+ * ---------------------------------------------------------------------- */
+namespace {
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
+
+/* Q8_0: one thread per block; w = d * (i8)v (crates/r9v-format/src/ggml.rs:1094-1100). */
+__global__ __launch_bounds__(256) void dequant_q80_kernel(const uint8_t *__restrict__ wire, uint64_t n_blocks,
+                                                          float *__restrict__ out) {
+    const uint64_t blk = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk >= n_blocks) return;
+    const uint8_t *b = wire + blk * R9VX_Q80_BYTES;
+    const float d = r9vx_f16_to_f32((uint16_t)ld_u16(b));
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t two = ld_u16(b + 2 + 2 * i);
+        v[2 * i] = d * (float)(int8_t)(two & 0xFF);
+        v[2 * i + 1] = d * (float)(int8_t)(two >> 8);
+    }
+    store16(out + blk * 32, v);
+    store16(out + blk * 32 + 16, v + 16);
+}
+
+/* Q6_K: one thread per group j of 16 weights; weight i of the block takes its
+ * low nibble from byte (i/128)*64 + i%64 (nibble (i%128)/64) and its high
+ * bits from byte 128 + (i/128)*32 + i%32 (pair (i%128)/32), then
+ * w = (d * (i8)scales[j]) * (q - 32)  (ggml.rs:817-850, 1154-1172). */
+__global__ __launch_bounds__(256) void dequant_q6k_kernel(const uint8_t *__restrict__ wire, uint64_t n_groups,
+                                                          float *__restrict__ out) {
+    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= n_groups) return;
+    const uint64_t blk = gid >> 4;
+    const uint32_t j = (uint32_t)(gid & 15);
+    const uint8_t *b = wire + blk * R9VX_Q6K_BYTES;
+    const float d = r9vx_f16_to_f32((uint16_t)ld_u16(b + 208));
+    const uint32_t scw = ld_u16(b + 192 + (j & ~1u));
+    const float dl = d * (float)(int8_t)((scw >> (8 * (j & 1))) & 0xFF);
+    const uint32_t i0 = 16 * j, half = i0 / 128, r = i0 % 128;
+    const uint8_t *ql = b + half * 64 + r % 64;
+    const uint8_t *qh = b + 128 + half * 32 + r % 32;
+    const uint32_t nib = 4 * (r / 64), pair = 2 * (r / 32);
+    float v[16];
+#pragma unroll
+    for (int p = 0; p < 16; p += 2) {
+        const uint32_t l2 = ld_u16(ql + p), h2 = ld_u16(qh + p);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t lo = (l2 >> (8 * e + nib)) & 0xF, hi = (h2 >> (8 * e + pair)) & 0x3;
+            v[p + e] = dl * ((float)(lo | (hi << 4)) - 32.0f);
+        }
+    }
+    store16(out + blk * 256 + i0, v);
+}
+
+/* Non-finite d (check_wire_f16, ggml.rs:421-445) of Q8_0 / Q6_K wire blocks. */
+__global__ __launch_bounds__(256) void validate_split_kernel(const uint8_t *__restrict__ wire, uint64_t n_blocks,
+                                                             uint32_t block_bytes, uint32_t d_offset,
+                                                             uint32_t *bad) {
+    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t isbad = 0;
+    if (gid < n_blocks) isbad = (ld_u16(wire + gid * block_bytes + d_offset) & 0x7C00u) == 0x7C00u;
+    const uint64_t mask = __ballot(isbad);
+    if ((threadIdx.x & 63) == 0 && mask) atomicAdd(bad, (uint32_t)__popcll(mask));
+}
+
+/* Wire -> split layout.  Q8_0: thread per block, the 32 quants to body
+ * [blk*32, +32) and d to scales[blk].  Q6_K: thread per 16-byte piece of the
+ * 208-byte body (13 per block); piece 0 also moves d. */
+__global__ __launch_bounds__(256) void repack_q80_kernel(const uint8_t *__restrict__ wire, uint64_t n_blocks,
+                                                         uint8_t *__restrict__ body, uint16_t *__restrict__ scales) {
+    const uint64_t blk = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (blk >= n_blocks) return;
+    const uint8_t *b = wire + blk * R9VX_Q80_BYTES;
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = ld_u16(b + 2 + 4 * i) | (ld_u16(b + 4 + 4 * i) << 16);
+    r9vx_u32x4 *o = reinterpret_cast<r9vx_u32x4 *>(body + blk * 32);
+    o[0] = r9vx_u32x4{w[0], w[1], w[2], w[3]};
+    o[1] = r9vx_u32x4{w[4], w[5], w[6], w[7]};
+    scales[blk] = (uint16_t)ld_u16(b);
+}
+
+__global__ __launch_bounds__(256) void repack_q6k_kernel(const uint8_t *__restrict__ wire, uint64_t n_pieces,
+                                                         uint8_t *__restrict__ body, uint16_t *__restrict__ scales) {
+    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= n_pieces) return;
+    const uint64_t blk = gid / 13;
+    const uint32_t piece = (uint32_t)(gid % 13);
+    const uint8_t *b = wire + blk * R9VX_Q6K_BYTES + 16 * piece;
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = ld_u16(b + 4 * i) | (ld_u16(b + 4 * i + 2) << 16);
+    *reinterpret_cast<r9vx_u32x4 *>(body + blk * R9VX_Q6K_BODY + 16 * piece) = r9vx_u32x4{w[0], w[1], w[2], w[3]};
+    if (piece == 0) scales[blk] = (uint16_t)ld_u16(wire + blk * R9VX_Q6K_BYTES + 208);
+}
+
+}  // namespace
+
+int r9vx_launch_dequant_split(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k, float *out,
+                              hipStream_t stream) {
+    if (scheme == R9VX_SCHEME_Q8_0) {
+        const uint64_t n = (uint64_t)n_rows * (k / 32);
+        hipLaunchKernelGGL(dequant_q80_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, wire, n, out);
+    } else {
+        const uint64_t n = (uint64_t)n_rows * (k / 256) * 16;
+        hipLaunchKernelGGL(dequant_q6k_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, wire, n, out);
+    }
+    return (int)hipGetLastError();
+}
+
+int r9vx_launch_validate_split(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k, uint32_t *bad,
+                               hipStream_t stream) {
+    const bool q8 = scheme == R9VX_SCHEME_Q8_0;
+    const uint64_t n = (uint64_t)n_rows * (k / (q8 ? 32 : 256));
+    hipLaunchKernelGGL(validate_split_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, wire, n,
+                       (uint32_t)(q8 ? R9VX_Q80_BYTES : R9VX_Q6K_BYTES), q8 ? 0u : 208u, bad);
+    return (int)hipGetLastError();
+}
+
+int r9vx_launch_repack(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k, uint8_t *body,
+                       uint16_t *scales, hipStream_t stream) {
+    if (scheme == R9VX_SCHEME_Q8_0) {
+        const uint64_t n = (uint64_t)n_rows * (k / 32);
+        hipLaunchKernelGGL(repack_q80_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, wire, n,
+                           body, scales);
+    } else {
+        const uint64_t n = (uint64_t)n_rows * (k / 256) * 13;
+        hipLaunchKernelGGL(repack_q6k_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, wire, n,
+                           body, scales);
+    }
     return (int)hipGetLastError();
 }

@@ -1,6 +1,7 @@
 /*
  * gemv.hip -- decode-time dequant-fused GEMV, y[m, n] = sum_k x[m, k] * w[n, k],
- * for GGUF Q4_K / IQ4_XS weights and m <= 8 activation rows.
+ * for GGUF Q4_K / IQ4_XS weights (wire blocks) and Q8_0 / Q6_K weights (split
+ * layout: body + f16 d array), and m <= 8 activation rows.
  *
  * T0 meaning: crates/r9v-t0/src/matmul.rs:1940-2414 (Branch D, f32
  * accumulate); weight decode crates/r9v-format/src/ggml.rs:1131-1150 (Q4_K)
@@ -20,12 +21,15 @@
  *  - f32 activations (config 0) use exact nibble->f32 conversion and f32 FMA.
  *  - Per-row partials are summed across the LPR lanes with a butterfly.
  */
+#include <type_traits>
+
 #include "r9vx_gemv_core.h"
 
 namespace {
 
 struct GemvArgs {
     const uint8_t *w;
+    const uint16_t *ws; /* split layouts: f16 d per block */
     const void *x;
     const float *bias;
     const float *residual;
@@ -38,7 +42,10 @@ struct GemvArgs {
     uint32_t nseg;     /* K segments of LPR*SPL chunks */
     uint32_t y_bf16;
     uint32_t epilogue;
+    uint32_t ws_row; /* d values per weight row */
 };
+
+constexpr bool split_scheme(int s) { return s == R9VX_SCHEME_Q8_0 || s == R9VX_SCHEME_Q6_K; }
 
 /* Rows per lane group per wave and waves per workgroup, by activation row
  * count (measured on MI355X at K=2048/4096): two rows in two-wave groups
@@ -98,7 +105,8 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
          * complete in order, so an activation load scheduled after a weight
          * load would hold the activation re-arrangement until HBM answers */
         __builtin_amdgcn_sched_barrier(0);
-        r9vx_u32x4 qs[kRows][SPL];
+        using Pay = typename std::conditional<split_scheme(SCHEME), Payload2, r9vx_u32x4>::type;
+        Pay qs[kRows][SPL];
         Hdr hd[kRows][SPL];
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
@@ -106,7 +114,12 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
             uint32_t rr = row < a.n ? row : a.n - 1; /* clamp: loads stay in bounds */
             const uint8_t *wrow = a.w + (uint64_t)rr * a.w_row_stride;
 #pragma unroll
-            for (int s = 0; s < SPL; ++s) load_chunk<SCHEME>(wrow, cis[s], qs[r][s], hd[r][s]);
+            for (int s = 0; s < SPL; ++s) {
+                if constexpr (split_scheme(SCHEME))
+                    load_chunk_split<SCHEME>(wrow, a.ws + (uint64_t)rr * a.ws_row, cis[s], qs[r][s], hd[r][s]);
+                else
+                    load_chunk<SCHEME>(wrow, cis[s], qs[r][s], hd[r][s]);
+            }
         }
         /* 2. the codebook table is built while the loads are in flight */
         if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
@@ -123,8 +136,12 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int r = 0; r < kRows; ++r)
 #pragma unroll
-            for (int s = 0; s < SPL; ++s)
-                chunk_dot<SCHEME, XF32, M>(qs[r][s], hd[r][s], cis[s] & 7, xc[s], acc[r], lut);
+            for (int s = 0; s < SPL; ++s) {
+                if constexpr (split_scheme(SCHEME))
+                    chunk_dot_split<SCHEME, M>(qs[r][s], hd[r][s], cis[s] & 7, xc[s], acc[r]);
+                else
+                    chunk_dot<SCHEME, XF32, M>(qs[r][s], hd[r][s], cis[s] & 7, xc[s], acc[r], lut);
+            }
     }
 
     /* cross-lane sums of all kRows*M partials at once; the lanes that end
@@ -230,6 +247,13 @@ int launch_scheme(const GemvArgs &a, uint32_t m, bool xf32, int spl, uint32_t g,
     return spl == 2 ? launch_one<SCHEME, false, 2, 4>(a, m, g, s) : launch_one<SCHEME, false, 1, 8>(a, m, g, s);
 }
 
+/* Q8_0 / Q6_K: bf16 activations only (T0 takes no f32 activations; the f32
+ * GEMV form exists for configs[0]'s Q4_K case). */
+template <int SCHEME>
+int launch_scheme_split(const GemvArgs &a, uint32_t m, int spl, uint32_t g, hipStream_t s) {
+    return spl == 2 ? launch_one<SCHEME, false, 2, 4>(a, m, g, s) : launch_one<SCHEME, false, 1, 8>(a, m, g, s);
+}
+
 }  // namespace
 
 /* m <= 8 rows, K % 256 == 0.  Rows of x are x_row_stride elements apart. */
@@ -245,6 +269,8 @@ int r9vx_launch_gemv(const r9vx_gemv_problem &p, hipStream_t stream) {
     while ((1u << lpr_log2) < lpr) ++lpr_log2;
     GemvArgs a;
     a.w = p.w;
+    a.ws = p.w_scales;
+    a.ws_row = p.scheme == R9VX_SCHEME_Q8_0 ? p.k / 32 : p.k / 256;
     a.x = p.x;
     a.bias = p.bias;
     a.residual = p.residual;
@@ -260,5 +286,8 @@ int r9vx_launch_gemv(const r9vx_gemv_problem &p, hipStream_t stream) {
     const uint32_t groups = 64 / lpr;
     const bool xf32 = p.x_dtype == R9VX_DTYPE_F32;
     if (p.scheme == R9VX_SCHEME_Q4_K) return launch_scheme<R9VX_SCHEME_Q4_K>(a, p.m, xf32, spl, groups, stream);
-    return launch_scheme<R9VX_SCHEME_IQ4_XS>(a, p.m, xf32, spl, groups, stream);
+    if (p.scheme == R9VX_SCHEME_IQ4_XS) return launch_scheme<R9VX_SCHEME_IQ4_XS>(a, p.m, xf32, spl, groups, stream);
+    if (xf32) return (int)hipErrorInvalidValue;
+    if (p.scheme == R9VX_SCHEME_Q6_K) return launch_scheme_split<R9VX_SCHEME_Q6_K>(a, p.m, spl, groups, stream);
+    return launch_scheme_split<R9VX_SCHEME_Q8_0>(a, p.m, spl, groups, stream);
 }

@@ -581,6 +581,7 @@ int entry_range(const char *op, const r9vx_gguf *f, const char *name, const uint
 }
 
 bool path_scheme(uint32_t type) { return type == R9VX_SCHEME_Q4_K || type == R9VX_SCHEME_IQ4_XS; }
+bool split_type(uint32_t type) { return type == R9VX_SCHEME_Q8_0 || type == R9VX_SCHEME_Q6_K; }
 
 std::string dims_text(const Tensor &t) {
     std::string s = "{";
@@ -816,13 +817,17 @@ int r9vx_gguf_matmul_static(const r9vx_gguf *f, const char *name, r9vx_matmul_st
     if (!f || !name || !st) return refuse(op, R9VX_ERR_NULL, "file, name and static are required");
     const Tensor *t = f->tensor(name);
     if (!t) return refuse(op, R9VX_ERR_INVALID, std::string("no tensor named \"") + name + "\"");
-    if (!path_scheme(t->type))
+    if (!path_scheme(t->type) && !split_type(t->type))
         return refuse(op, R9VX_ERR_UNSUPPORTED,
                       "tensor \"" + t->name + "\" is " + r9vx_gguf_type_name(t->type) +
-                          "; this path multiplies Q4_K (12) and IQ4_XS (23) weights");
+                          "; this path multiplies Q4_K (12), IQ4_XS (23), Q6_K (14) and Q8_0 (8) weights");
     if (t->dims.size() != 2 || t->dims[0] > UINT32_MAX || t->dims[1] > UINT32_MAX)
         return refuse(op, R9VX_ERR_INVALID,
                       "tensor \"" + t->name + "\" dims " + dims_text(*t) + " are not a {K, N} matrix of u32 sizes");
+    if (t->dims[0] % 256)
+        return refuse(op, R9VX_ERR_UNSUPPORTED,
+                      "tensor \"" + t->name + "\" has K=" + std::to_string(t->dims[0]) +
+                          "; the matmul kernels take K in multiples of 256");
     st->k = (uint32_t)t->dims[0];
     st->n = (uint32_t)t->dims[1];
     st->w_scheme = t->type;
@@ -902,6 +907,59 @@ int r9vx_gguf_upload(const r9vx_gguf *f, const uint8_t *bytes, uint64_t len, con
                       fmt("dst holds %llu bytes, tensor \"%s\" needs %llu", (unsigned long long)dst_bytes,
                           t->name.c_str(), (unsigned long long)t->nbytes));
     return hip_rc(op, hipMemcpyAsync(dst, data, t->nbytes, hipMemcpyHostToDevice, (hipStream_t)stream));
+}
+
+int r9vx_gguf_upload_split(const r9vx_gguf *f, const uint8_t *bytes, uint64_t len, const char *name, void *body,
+                           uint64_t body_bytes, uint16_t *scales, uint64_t scales_bytes, r9vx_stream_t stream) {
+    const char *op = "gguf_upload_split";
+    const Tensor *t;
+    const uint8_t *data;
+    int rc = entry_range(op, f, name, bytes, len, &t, &data);
+    if (rc != R9VX_OK) return rc;
+    if (!split_type(t->type))
+        return refuse(op, R9VX_ERR_UNSUPPORTED,
+                      "tensor \"" + t->name + "\" is " + r9vx_gguf_type_name(t->type) +
+                          "; the split layout is for Q8_0 (8) and Q6_K (14)");
+    if (!body || !scales) return refuse(op, R9VX_ERR_NULL, "body and scales are required");
+    const TypeRow *row = type_row(t->type);
+    const uint64_t nblocks = t->nbytes / row->block_bytes;
+    const uint32_t body_block = row->block_bytes - 2, d_off = t->type == R9VX_SCHEME_Q8_0 ? 0 : 208;
+    if (body_bytes < nblocks * body_block || scales_bytes < nblocks * 2)
+        return refuse(op, R9VX_ERR_INVALID,
+                      fmt("body holds %llu and scales %llu bytes; tensor \"%s\" needs %llu and %llu",
+                          (unsigned long long)body_bytes, (unsigned long long)scales_bytes, t->name.c_str(),
+                          (unsigned long long)(nblocks * body_block), (unsigned long long)(nblocks * 2)));
+    /* split on the host (body = the block without d, d to its own array),
+     * refusing non-finite d (check_wire_f16, crates/r9v-format/src/ggml.rs:421) */
+    std::vector<uint8_t> hb;
+    std::vector<uint16_t> hs;
+    try {
+        hb.resize(nblocks * body_block);
+        hs.resize(nblocks);
+    } catch (const std::bad_alloc &) {
+        return refuse(op, R9VX_ERR_INVALID, "out of host memory for the split copy");
+    }
+    uint64_t bad = 0;
+    for (uint64_t b = 0; b < nblocks; ++b) {
+        const uint8_t *blk = data + b * row->block_bytes;
+        const uint16_t d = (uint16_t)(blk[d_off] | (blk[d_off + 1] << 8));
+        bad += (d & 0x7C00u) == 0x7C00u;
+        hs[b] = d;
+        if (d_off == 0)
+            memcpy(&hb[b * body_block], blk + 2, body_block);
+        else
+            memcpy(&hb[b * body_block], blk, body_block);
+    }
+    if (bad)
+        return refuse(op, R9VX_ERR_INVALID,
+                      fmt("tensor \"%s\": %llu block(s) carry a non-finite scale", t->name.c_str(),
+                          (unsigned long long)bad));
+    hipStream_t s = (hipStream_t)stream;
+    rc = hip_rc(op, hipMemcpyAsync(body, hb.data(), hb.size(), hipMemcpyHostToDevice, s));
+    if (rc == R9VX_OK) rc = hip_rc(op, hipMemcpyAsync(scales, hs.data(), hs.size() * 2, hipMemcpyHostToDevice, s));
+    /* the host copies die with this call */
+    const int sync = hip_rc(op, hipStreamSynchronize(s));
+    return rc != R9VX_OK ? rc : sync;
 }
 
 int r9vx_gguf_upload_gate_up(const r9vx_gguf *gate_file, const uint8_t *gate_bytes, uint64_t gate_len,

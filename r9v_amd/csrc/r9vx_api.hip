@@ -49,10 +49,28 @@ int hip_status(const char *op, int rc) {
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+/* Schemes read as GGUF wire blocks (every op), and the ones read in the split
+ * layout of r9vx_repack_launch (matmul with m <= 8). */
 bool known_scheme(uint32_t s) { return s == R9VX_SCHEME_Q4_K || s == R9VX_SCHEME_IQ4_XS; }
+bool split_scheme(uint32_t s) { return s == R9VX_SCHEME_Q8_0 || s == R9VX_SCHEME_Q6_K; }
+bool matmul_scheme(uint32_t s) { return known_scheme(s) || split_scheme(s); }
 
 uint32_t block_bytes(uint32_t s) {
-    return s == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : (s == R9VX_SCHEME_IQ4_XS ? R9VX_IQ4XS_BYTES : 0);
+    switch (s) {
+    case R9VX_SCHEME_Q4_K: return R9VX_Q4K_BYTES;
+    case R9VX_SCHEME_IQ4_XS: return R9VX_IQ4XS_BYTES;
+    case R9VX_SCHEME_Q6_K: return R9VX_Q6K_BYTES;
+    case R9VX_SCHEME_Q8_0: return R9VX_Q80_BYTES;
+    default: return 0;
+    }
+}
+uint32_t block_len(uint32_t s) { return s == R9VX_SCHEME_Q8_0 ? 32 : 256; }
+
+/* Bytes of one weight row as the kernels read it. */
+uint64_t device_row_bytes(uint32_t s, uint32_t k) {
+    if (s == R9VX_SCHEME_Q8_0) return k;
+    if (s == R9VX_SCHEME_Q6_K) return (uint64_t)(k / 256) * R9VX_Q6K_BODY;
+    return (uint64_t)(k / 256) * block_bytes(s);
 }
 
 }  // namespace
@@ -70,8 +88,14 @@ uint32_t r9vx_abi_version(void) { return R9VX_ABI_VERSION; }
 /* ------------------------------------------------------------------ matmul */
 
 static void check_matmul_static(const r9vx_matmul_static *st, Problems &pr) {
-    if (!known_scheme(st->w_scheme))
-        pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u is not Q4_K (12) or IQ4_XS (23)", st->w_scheme);
+    if (!matmul_scheme(st->w_scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u is not Q4_K (12), IQ4_XS (23), Q6_K (14) or Q8_0 (8)",
+               st->w_scheme);
+    if (split_scheme(st->w_scheme) && st->in_dtype != R9VX_DTYPE_BF16)
+        pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u takes bf16 activations only", st->w_scheme);
+    if (split_scheme(st->w_scheme) && st->m_bucket > 8)
+        pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u: only the decode GEMV (m_bucket <= 8) is implemented",
+               st->w_scheme);
     if (st->k == 0 || st->k % 256)
         pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of the 256-weight super-block", st->k);
     if (st->n == 0) pr.add(R9VX_ERR_INVALID, "n must be positive");
@@ -93,8 +117,8 @@ size_t r9vx_matmul_workspace_bytes(const r9vx_matmul_static *st) {
 }
 
 uint64_t r9vx_matmul_static_bytes(const r9vx_matmul_static *st, uint32_t m) {
-    if (!st || !known_scheme(st->w_scheme)) return 0;
-    uint64_t w = (uint64_t)st->n * (st->k / 256) * block_bytes(st->w_scheme);
+    if (!st || !matmul_scheme(st->w_scheme)) return 0;
+    uint64_t w = (uint64_t)st->n * (st->k / block_len(st->w_scheme)) * block_bytes(st->w_scheme);
     uint64_t xe = st->in_dtype == R9VX_DTYPE_F32 ? 4 : 2;
     uint64_t ye = st->out_dtype == R9VX_DTYPE_F32 ? 4 : 2;
     return w + (uint64_t)m * st->k * xe + (uint64_t)m * st->n * ye;
@@ -120,7 +144,11 @@ int r9vx_matmul_launch(const r9vx_matmul_static *st, const r9vx_matmul_args *a,
         if (!a->x) pr.add(R9VX_ERR_NULL, "x is NULL");
         if (!a->y) pr.add(R9VX_ERR_NULL, "y is NULL");
     }
-    if (a->w_scales) pr.add(R9VX_ERR_UNSUPPORTED, "w_scales must be NULL: GGUF blocks carry inline scales");
+    if (a->w_scales && known_scheme(st->w_scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "w_scales must be NULL: Q4_K / IQ4_XS blocks carry inline scales");
+    if (split_scheme(st->w_scheme) && a->m > 0 && !a->w_scales)
+        pr.add(R9VX_ERR_NULL, "w_scales (the f16 d array of the split layout) is NULL");
+    if (a->w_scales && ((uintptr_t)a->w_scales & 1u)) pr.add(R9VX_ERR_ALIGN, "w_scales must be 2-byte aligned");
     if (a->w_indices) pr.add(R9VX_ERR_UNSUPPORTED, "w_indices must be NULL: no sparse weights");
     if (a->x_scale) pr.add(R9VX_ERR_UNSUPPORTED, "x_scale must be NULL: activations are not quantized");
     if (st->epilogue == R9VX_EPILOGUE_BIAS && !a->bias) pr.add(R9VX_ERR_NULL, "bias epilogue without bias");
@@ -141,7 +169,7 @@ int r9vx_matmul_launch(const r9vx_matmul_static *st, const r9vx_matmul_args *a,
     if (rc || a->m == 0) return rc;
 
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const uint64_t w_row = (uint64_t)(st->k / 256) * block_bytes(st->w_scheme);
+    const uint64_t w_row = device_row_bytes(st->w_scheme, st->k);
     const bool mfma = st->in_dtype == R9VX_DTYPE_BF16 && a->m > 8;
     if (mfma) {
         r9vx_gemm_problem g{};
@@ -165,6 +193,7 @@ int r9vx_matmul_launch(const r9vx_matmul_static *st, const r9vx_matmul_args *a,
     for (uint32_t m0 = 0; m0 < a->m; m0 += 8) {
         r9vx_gemv_problem p{};
         p.w = a->w;
+        p.w_scales = reinterpret_cast<const uint16_t *>(a->w_scales);
         p.x = reinterpret_cast<const uint8_t *>(a->x) + (uint64_t)m0 * st->k * xe;
         p.bias = a->bias;
         p.residual = a->residual ? reinterpret_cast<const float *>(a->residual) + (uint64_t)m0 * st->n : nullptr;
@@ -189,26 +218,59 @@ int r9vx_matmul_launch(const r9vx_matmul_static *st, const r9vx_matmul_args *a,
 int r9vx_dequantize_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k,
                            float *out, r9vx_stream_t stream) {
     Problems pr;
-    if (!known_scheme(scheme)) pr.add(R9VX_ERR_UNSUPPORTED, "scheme %u", scheme);
-    if (k == 0 || k % 256) pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of 256", k);
+    if (!matmul_scheme(scheme)) pr.add(R9VX_ERR_UNSUPPORTED, "scheme %u", scheme);
+    const uint32_t bl = block_len(scheme);
+    if (k == 0 || k % bl) pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of %u", k, bl);
     if (n_rows && (!wire || !out)) pr.add(R9VX_ERR_NULL, "wire and out must be non-NULL");
-    if ((wire && !aligned16(wire)) || (out && !aligned16(out))) pr.add(R9VX_ERR_ALIGN, "16-byte alignment");
+    /* Q8_0 / Q6_K wire blocks are read as 16-bit words */
+    const uintptr_t wmask = split_scheme(scheme) ? 1u : 15u;
+    if ((wire && ((uintptr_t)wire & wmask)) || (out && !aligned16(out))) pr.add(R9VX_ERR_ALIGN, "wire / out alignment");
     int rc = pr.finish("dequantize");
     if (rc || n_rows == 0) return rc;
-    return hip_status("dequantize", r9vx_launch_dequant(scheme, wire, n_rows, k, out,
-                                                        reinterpret_cast<hipStream_t>(stream)));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (split_scheme(scheme)) return hip_status("dequantize", r9vx_launch_dequant_split(scheme, wire, n_rows, k, out, s));
+    return hip_status("dequantize", r9vx_launch_dequant(scheme, wire, n_rows, k, out, s));
+}
+
+int r9vx_repack_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k, uint8_t *body,
+                       uint16_t *scales, r9vx_stream_t stream) {
+    Problems pr;
+    if (!split_scheme(scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "scheme %u: only Q8_0 (8) and Q6_K (14) are repacked; Q4_K / IQ4_XS wire "
+               "blocks are the device layout", scheme);
+    const uint32_t bl = block_len(scheme);
+    if (k == 0 || k % bl) pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of %u", k, bl);
+    if (n_rows && (!wire || !body || !scales)) pr.add(R9VX_ERR_NULL, "wire, body and scales must be non-NULL");
+    if ((wire && ((uintptr_t)wire & 1u)) || (body && !aligned16(body)) || (scales && ((uintptr_t)scales & 1u)))
+        pr.add(R9VX_ERR_ALIGN, "wire and scales 2-byte, body 16-byte aligned");
+    if (split_scheme(scheme) && n_rows && wire && body && scales && k % bl == 0) {
+        const uint64_t nb = (uint64_t)n_rows * (k / bl);
+        const uintptr_t w0 = (uintptr_t)wire, w1 = w0 + nb * block_bytes(scheme);
+        const uintptr_t b0 = (uintptr_t)body, b1 = b0 + (uint64_t)n_rows * device_row_bytes(scheme, k);
+        const uintptr_t s0 = (uintptr_t)scales, s1 = s0 + nb * 2;
+        if ((b0 < w1 && w0 < b1) || (s0 < w1 && w0 < s1) || (s0 < b1 && b0 < s1))
+            pr.add(R9VX_ERR_INVALID, "wire, body and scales must not overlap");
+    }
+    int rc = pr.finish("repack");
+    if (rc || n_rows == 0) return rc;
+    return hip_status("repack", r9vx_launch_repack(scheme, wire, n_rows, k, body, scales,
+                                                   reinterpret_cast<hipStream_t>(stream)));
 }
 
 int r9vx_validate_weights_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k,
                                  uint32_t *bad_blocks, r9vx_stream_t stream) {
     Problems pr;
-    if (!known_scheme(scheme)) pr.add(R9VX_ERR_UNSUPPORTED, "scheme %u", scheme);
-    if (k == 0 || k % 256) pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of 256", k);
+    if (!matmul_scheme(scheme)) pr.add(R9VX_ERR_UNSUPPORTED, "scheme %u", scheme);
+    const uint32_t bl = block_len(scheme);
+    if (k == 0 || k % bl) pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of %u", k, bl);
     if (n_rows && (!wire || !bad_blocks)) pr.add(R9VX_ERR_NULL, "wire and bad_blocks must be non-NULL");
+    if (wire && ((uintptr_t)wire & (split_scheme(scheme) ? 1u : 3u))) pr.add(R9VX_ERR_ALIGN, "wire alignment");
     int rc = pr.finish("validate_weights");
     if (rc || n_rows == 0) return rc;
-    return hip_status("validate_weights", r9vx_launch_validate(scheme, wire, n_rows, k, bad_blocks,
-                                                               reinterpret_cast<hipStream_t>(stream)));
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    if (split_scheme(scheme))
+        return hip_status("validate_weights", r9vx_launch_validate_split(scheme, wire, n_rows, k, bad_blocks, s));
+    return hip_status("validate_weights", r9vx_launch_validate(scheme, wire, n_rows, k, bad_blocks, s));
 }
 
 /* --------------------------------------------------------------- moe_route */

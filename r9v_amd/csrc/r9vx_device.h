@@ -21,6 +21,9 @@ typedef uint32_t r9vx_u32x2 __attribute__((ext_vector_type(2)));
 /* GGUF block geometry (crates/r9v-format/tests/iq.rs:131-141). */
 #define R9VX_Q4K_BYTES 144
 #define R9VX_IQ4XS_BYTES 136
+#define R9VX_Q6K_BYTES 210   /* wire block: ql 128, qh 64, scales 16, d 2 */
+#define R9VX_Q6K_BODY 208    /* split-layout body: the wire block without d */
+#define R9VX_Q80_BYTES 34    /* wire block: d 2, 32 int8 quants */
 
 /* IQ4 codebook (crates/r9v-format/src/iq_lut.rs:23-25). */
 __device__ __forceinline__ int r9vx_iq4_kvalue(uint32_t q) {

@@ -41,6 +41,15 @@ __device__ __forceinline__ void chunk_k(uint32_t ci, uint32_t &klo, uint32_t &kh
     if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
         klo = 256 * b + 64 * (c >> 1) + 16 * (c & 1);
         khi = klo + 32;
+    } else if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
+        /* chunk = 16 ql bytes of half c/4: low nibbles at 128h + 16(c%4),
+         * high nibbles 64 further */
+        klo = 256 * b + 128 * (c >> 2) + 16 * (c & 3);
+        khi = klo + 64;
+    } else if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+        /* chunk = one Q8_0 block of 32 quants */
+        klo = 32 * ci;
+        khi = klo + 16;
     } else {
         klo = 256 * b + 32 * c;
         khi = klo + 16;
@@ -101,7 +110,7 @@ __device__ __forceinline__ void arrange_x(const XRaw<XF32> &r, XChunk<SCHEME, XF
         L[4] = r.v[1].x; L[5] = r.v[1].y; L[6] = r.v[1].z; L[7] = r.v[1].w;
         H[0] = r.v[2].x; H[1] = r.v[2].y; H[2] = r.v[2].z; H[3] = r.v[2].w;
         H[4] = r.v[3].x; H[5] = r.v[3].y; H[6] = r.v[3].z; H[7] = r.v[3].w;
-        if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
+        if constexpr (SCHEME != R9VX_SCHEME_IQ4_XS) {
             float slo = 0.f, shi = 0.f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -140,9 +149,11 @@ __device__ __forceinline__ void load_x(const void *xbase, uint32_t klo, uint32_t
     arrange_x<SCHEME, XF32>(r, xc);
 }
 
-/* Block header of the chunk's super-block. */
+/* Block header of the chunk's super-block; `e` holds the f16 d of the
+ * split-layout schemes (Q8_0 / Q6_K), whose d lives in a separate array. */
 struct Hdr {
     r9vx_u32x4 v;
+    uint32_t e;
 };
 
 template <int SCHEME>
@@ -240,6 +251,111 @@ __device__ __forceinline__ void chunk_dot(const r9vx_u32x4 &qs, const Hdr &h, ui
     }
 }
 
+
+/* ---- Q8_0 / Q6_K in the split device layout ---------------------------------
+ *
+ * A chunk is 32 weights here too, but 32 payload bytes: Q8_0 reads one
+ * block's quants (body row = int8 [K]), Q6_K reads 16 ql bytes and the 16 qh
+ * bytes holding their high bits (body row = K/256 blocks of 208 bytes:
+ * ql 128, qh 64, scales 16).  d comes from the f16 scale row.  The
+ * activations use the Q4_K arrangement (pairs of positions 4d+{0,2} and
+ * 4d+{1,3}, plus the sums of the 16 low and 16 high positions). */
+struct Payload2 {
+    r9vx_u32x4 a, b;
+};
+
+template <int SCHEME>
+__device__ __forceinline__ void load_chunk_split(const uint8_t *row, const uint16_t *srow, uint32_t ci,
+                                                 Payload2 &p, Hdr &h) {
+    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+        p.a = r9vx_ld128_nt(row + 32 * (uint64_t)ci);
+        p.b = r9vx_ld128_nt(row + 32 * (uint64_t)ci + 16);
+        h.e = srow[ci];
+    } else {
+        const uint32_t b = ci >> 3, c = ci & 7;
+        const uint8_t *blk = row + (uint64_t)b * R9VX_Q6K_BODY;
+        p.a = r9vx_ld128_nt(blk + 64 * (c >> 2) + 16 * (c & 3));             /* ql */
+        p.b = r9vx_ld128_nt(blk + 128 + 32 * (c >> 2) + 16 * (c & 1));       /* qh */
+        h.v = r9vx_ld128(blk + 192);                                        /* 16 int8 scales */
+        h.e = srow[b];
+    }
+}
+
+/* One split-layout chunk of one row against M bf16 activation rows. */
+template <int SCHEME, int M>
+__device__ __forceinline__ void chunk_dot_split(const Payload2 &pl, const Hdr &h, uint32_t c,
+                                                const XChunk<SCHEME, false> (&xc)[M], float (&acc)[M], int m = M) {
+    const float d = r9vx_f16_to_f32((uint16_t)h.e);
+    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+        /* u = q + 128 (bytes XOR 0x80) = 16*hi + lo; 0x4300|n is the bf16 of
+         * 128 + n, so sl = sum (128+lo) x and sh = sum (128+hi) x give
+         * sum q x = 16 sh + sl - 2304 sum x. */
+        const uint32_t q[8] = {pl.a.x, pl.a.y, pl.a.z, pl.a.w, pl.b.x, pl.b.y, pl.b.z, pl.b.w};
+        uint32_t L[16], H[16];
+#pragma unroll
+        for (int dw = 0; dw < 8; ++dw) {
+            const uint32_t u = q[dw] ^ 0x80808080u;
+            L[2 * dw + 0] = (u & 0x000F000Fu) | 0x43004300u;
+            L[2 * dw + 1] = ((u >> 8) & 0x000F000Fu) | 0x43004300u;
+            H[2 * dw + 0] = ((u >> 4) & 0x000F000Fu) | 0x43004300u;
+            H[2 * dw + 1] = ((u >> 12) & 0x000F000Fu) | 0x43004300u;
+        }
+#pragma unroll
+        for (int t = 0; t < M; ++t) {
+            if (t >= m) break;
+            float sl = 0.f, sh = 0.f;
+#pragma unroll
+            for (int dw = 0; dw < 4; ++dw) {
+                /* first 16 bytes: low positions; last 16: high positions */
+                sl = r9vx_dot2_bf16(L[2 * dw + 0], xc[t].p[4 * dw + 0], sl);
+                sl = r9vx_dot2_bf16(L[2 * dw + 1], xc[t].p[4 * dw + 1], sl);
+                sh = r9vx_dot2_bf16(H[2 * dw + 0], xc[t].p[4 * dw + 0], sh);
+                sh = r9vx_dot2_bf16(H[2 * dw + 1], xc[t].p[4 * dw + 1], sh);
+                sl = r9vx_dot2_bf16(L[8 + 2 * dw + 0], xc[t].p[4 * dw + 2], sl);
+                sl = r9vx_dot2_bf16(L[8 + 2 * dw + 1], xc[t].p[4 * dw + 3], sl);
+                sh = r9vx_dot2_bf16(H[8 + 2 * dw + 0], xc[t].p[4 * dw + 2], sh);
+                sh = r9vx_dot2_bf16(H[8 + 2 * dw + 1], xc[t].p[4 * dw + 3], sh);
+            }
+            acc[t] = fmaf(d, fmaf(16.f, sh, sl) - 2304.f * (xc[t].slo + xc[t].shi), acc[t]);
+        }
+    } else {
+        /* 6-bit q = ql nibble | (qh bit pair << 4); low positions take pair
+         * (c%4)/2, high positions pair 2 + (c%4)/2, and scales 8h + c%4 and
+         * 8h + 4 + c%4 (h = c/4).  0x4300|q is the bf16 of 128 + q, so
+         * sum (q - 32) x = sum (128 + q) x - 160 sum x. */
+        const uint32_t cc = c & 3, hsel = c >> 2;
+        const uint32_t j0 = 8 * hsel + cc, j1 = j0 + 4;
+        const uint32_t sv[4] = {h.v.x, h.v.y, h.v.z, h.v.w};
+        const float dl0 = d * (float)(int8_t)((sv[j0 >> 2] >> (8 * (j0 & 3))) & 0xFF);
+        const float dl1 = d * (float)(int8_t)((sv[j1 >> 2] >> (8 * (j1 & 3))) & 0xFF);
+        const uint32_t pair_lo = 2 * (cc >> 1), pair_hi = pair_lo + 4;
+        const uint32_t ql[4] = {pl.a.x, pl.a.y, pl.a.z, pl.a.w};
+        const uint32_t qh[4] = {pl.b.x, pl.b.y, pl.b.z, pl.b.w};
+        uint32_t v[16];
+#pragma unroll
+        for (int dw = 0; dw < 4; ++dw) {
+            const uint32_t lo6 = (ql[dw] & 0x0F0F0F0Fu) | (((qh[dw] >> pair_lo) & 0x03030303u) << 4);
+            const uint32_t hi6 = ((ql[dw] >> 4) & 0x0F0F0F0Fu) | (((qh[dw] >> pair_hi) & 0x03030303u) << 4);
+            v[4 * dw + 0] = (lo6 & 0x00FF00FFu) | 0x43004300u;
+            v[4 * dw + 1] = ((lo6 >> 8) & 0x00FF00FFu) | 0x43004300u;
+            v[4 * dw + 2] = (hi6 & 0x00FF00FFu) | 0x43004300u;
+            v[4 * dw + 3] = ((hi6 >> 8) & 0x00FF00FFu) | 0x43004300u;
+        }
+#pragma unroll
+        for (int t = 0; t < M; ++t) {
+            if (t >= m) break;
+            float dlo = 0.f, dhi = 0.f;
+#pragma unroll
+            for (int dw = 0; dw < 4; ++dw) {
+                dlo = r9vx_dot2_bf16(v[4 * dw + 0], xc[t].p[4 * dw + 0], dlo);
+                dlo = r9vx_dot2_bf16(v[4 * dw + 1], xc[t].p[4 * dw + 1], dlo);
+                dhi = r9vx_dot2_bf16(v[4 * dw + 2], xc[t].p[4 * dw + 2], dhi);
+                dhi = r9vx_dot2_bf16(v[4 * dw + 3], xc[t].p[4 * dw + 3], dhi);
+            }
+            acc[t] += dl0 * (dlo - 160.f * xc[t].slo) + dl1 * (dhi - 160.f * xc[t].shi);
+        }
+    }
+}
 
 /* ---- cross-lane sums of per-lane partials --------------------------------
  *

@@ -51,9 +51,16 @@ int r9vx_launch_dequant(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, u
                         float *out, hipStream_t stream);
 int r9vx_launch_validate(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k,
                          uint32_t *bad, hipStream_t stream);
+int r9vx_launch_dequant_split(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k, float *out,
+                              hipStream_t stream);
+int r9vx_launch_validate_split(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k, uint32_t *bad,
+                               hipStream_t stream);
+int r9vx_launch_repack(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k, uint8_t *body,
+                       uint16_t *scales, hipStream_t stream);
 
 struct r9vx_gemv_problem {
     const uint8_t *w;
+    const uint16_t *w_scales; /* Q8_0 / Q6_K: f16 d per block, row-major [n, k/block] */
     const void *x;
     const float *bias;
     const float *residual;

@@ -19,12 +19,14 @@ LIB_PATH = PKG / "libr9vx.so"
 
 # enums (include/r9vx.h)
 F32, F16, BF16, U32 = 0, 1, 2, 8
-Q4_K, IQ4_XS = 12, 23
+Q4_K, IQ4_XS, Q6_K, Q8_0 = 12, 23, 14, 8
 EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_RESIDUAL = 0, 1, 2
 SCORING_SOFTMAX, SCORING_SIGMOID = 0, 1
 ACT_SILU = 0
 STATUS_NONFINITE, STATUS_DEGENERATE, STATUS_BAD_EXPERT = 1, 2, 4
-BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136}
+BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136, Q6_K: 210, Q8_0: 34}
+BLOCK_LEN = {Q4_K: 256, IQ4_XS: 256, Q6_K: 256, Q8_0: 32}
+SPLIT_SCHEMES = (Q6_K, Q8_0)      # read in the split device layout (body + f16 d array)
 
 _P = ctypes.c_void_p
 _U32 = ctypes.c_uint32
@@ -83,6 +85,7 @@ EXPORTS = [
     ("r9vx_moe_sort_launch", [_P, _P, _U32, _P, _P, _P, _P, _P], ctypes.c_int),
     ("r9vx_dequantize_launch", [_U32, _P, _U32, _U32, _P, _P], ctypes.c_int),
     ("r9vx_validate_weights_launch", [_U32, _P, _U32, _U32, _P, _P], ctypes.c_int),
+    ("r9vx_repack_launch", [_U32, _P, _U32, _U32, _P, _P, _P], ctypes.c_int),
     ("r9vx_last_error", [], ctypes.c_char_p),
     ("r9vx_abi_version", [], _U32),
     # include/r9vx_probe.h
@@ -121,6 +124,7 @@ EXPORTS = [
     ("r9vx_gguf_moe_ffn_static", [_P, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, _P],
      ctypes.c_int),
     ("r9vx_gguf_upload", [_P, _P, _U64, ctypes.c_char_p, _P, _U64, _P], ctypes.c_int),
+    ("r9vx_gguf_upload_split", [_P, _P, _U64, ctypes.c_char_p, _P, _U64, _P, _U64, _P], ctypes.c_int),
     ("r9vx_gguf_upload_gate_up", [_P, _P, _U64, ctypes.c_char_p, _P, _P, _U64, ctypes.c_char_p,
                                   _P, _U64, _P], ctypes.c_int),
 ]
@@ -190,9 +194,11 @@ def matmul_static(n, k, w_scheme, in_dtype, out_dtype, m_bucket=8, epilogue=EPIL
 
 
 def matmul(w, w_scheme, n, k, x, out_dtype=F32, bias=None, residual=None, y=None, workspace=None,
-           stream=None):
-    """y[m, n] = x[m, :] . w[n, :] (+ bias | + residual): T0 execute_matmul_op meaning."""
-    torch = _need_gpu(w, x, bias, residual, y)
+           stream=None, w_scales=None):
+    """y[m, n] = x[m, :] . w[n, :] (+ bias | + residual): T0 execute_matmul_op meaning.
+    Q6_K / Q8_0 weights are a split body `w` plus its f16 d array `w_scales`
+    (see `repack`)."""
+    torch = _need_gpu(w, x, bias, residual, y, w_scales)
     m = x.shape[0]
     if y is None:
         y = torch.empty((m, n), dtype=torch.float32 if out_dtype == F32 else torch.bfloat16,
@@ -202,7 +208,7 @@ def matmul(w, w_scheme, n, k, x, out_dtype=F32, bias=None, residual=None, y=None
     if workspace is None:
         nbytes = matmul_workspace_bytes(st)
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes else None
-    args = MatmulArgs(_ptr(w), None, None, _ptr(x), None, _ptr(bias), _ptr(residual), _ptr(y),
+    args = MatmulArgs(_ptr(w), _ptr(w_scales), None, _ptr(x), None, _ptr(bias), _ptr(residual), _ptr(y),
                       _ptr(workspace), m, 0)
     _check(load().r9vx_matmul_launch(ctypes.byref(st), ctypes.byref(args), _stream(torch, stream)))
     return y
@@ -224,6 +230,17 @@ def dequantize(wire, scheme, n_rows, k, out=None, stream=None):
         out = torch.empty((n_rows, k), dtype=torch.float32, device=wire.device)
     _check(load().r9vx_dequantize_launch(scheme, _ptr(wire), n_rows, k, _ptr(out), _stream(torch, stream)))
     return out
+
+
+def repack(wire, scheme, n_rows, k, stream=None):
+    """Q8_0 / Q6_K wire blocks on the device -> (body uint8, scales int16 holding f16 bits)."""
+    torch = _need_gpu(wire)
+    nb = n_rows * (k // BLOCK_LEN[scheme])
+    body = torch.empty(nb * (BLOCK_BYTES[scheme] - 2), dtype=torch.uint8, device=wire.device)
+    scales = torch.empty(nb, dtype=torch.int16, device=wire.device)
+    _check(load().r9vx_repack_launch(scheme, _ptr(wire), n_rows, k, _ptr(body), _ptr(scales),
+                                     _stream(torch, stream)))
+    return body, scales
 
 
 def validate_weights(wire, scheme, n_rows, k, stream=None) -> int:

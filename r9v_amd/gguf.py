@@ -384,18 +384,43 @@ def upload_gate_up(gate_file: GgufFile, gate_data, gate: str, up_file: GgufFile,
     return out
 
 
+def upload_split(file: GgufFile, data, name: str, stream=None):
+    """A Q8_0 / Q6_K tensor in the split device layout: (body uint8, scales
+    int16 holding the f16 d bits); non-finite scales are refused on the host."""
+    import torch
+
+    info = file.tensor(name)
+    if info is None:
+        raise GgufError(-1, f"no tensor named {name!r}")
+    nb = info.nbytes // info.block_bytes
+    body = torch.empty(nb * (info.block_bytes - 2), dtype=torch.uint8, device="cuda")
+    scales = torch.empty(nb, dtype=torch.int16, device="cuda")
+    ptr, n, _keep = _buf(data)
+    rc = ffi.load().r9vx_gguf_upload_split(file._h, ptr, n, name.encode(), ctypes.c_void_p(body.data_ptr()),
+                                           body.numel(), ctypes.c_void_p(scales.data_ptr()), 2 * scales.numel(),
+                                           ffi._stream(torch, stream))
+    if rc != 0:
+        _raise(rc)
+    return body, scales
+
+
 def load_matmul_weight(file: GgufFile, data, name: str, m_bucket: int = 8, in_dtype: int = ffi.BF16,
                        out_dtype: int = ffi.F32, validate: bool = True):
-    """(MatmulStatic, device wire blocks) for weight `name`; with `validate`,
-    the load-time scale check (check_wire_f16, crates/r9v-format/src/ggml.rs:421)
-    runs on the device and a block with a non-finite scale is refused."""
+    """(MatmulStatic, w, w_scales) on the device for weight `name`: Q4_K /
+    IQ4_XS wire blocks (w_scales None) or the Q8_0 / Q6_K split layout.  With
+    `validate` the load-time scale check (check_wire_f16,
+    crates/r9v-format/src/ggml.rs:421) refuses a block with a non-finite scale
+    (on the device for wire blocks; the split upload always checks)."""
     st = file.matmul_static(name, m_bucket=m_bucket, in_dtype=in_dtype, out_dtype=out_dtype)
+    if st.w_scheme in ffi.SPLIT_SCHEMES:
+        w, w_scales = upload_split(file, data, name)
+        return st, w, w_scales
     w = upload(file, data, name)
     if validate:
         bad = ffi.validate_weights(w, st.w_scheme, st.n, st.k)
         if bad:
             raise GgufError(-1, f"{name}: {bad} block(s) carry a non-finite scale")
-    return st, w
+    return st, w, None
 
 
 def load_moe_experts(file: GgufFile, data, gate: str, up: str | None, down: str, t_bucket: int,

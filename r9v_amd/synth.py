@@ -21,7 +21,11 @@ M2 = np.uint64(0x94D049BB133111EB)
 
 Q4_K = 12
 IQ4_XS = 23
-BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136}
+Q6_K = 14
+Q8_0 = 8
+BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136, Q6_K: 210, Q8_0: 34}
+BLOCK_LEN = {Q4_K: 256, IQ4_XS: 256, Q6_K: 256, Q8_0: 32}
+D_OFFSET = {Q4_K: 0, IQ4_XS: 0, Q6_K: 208, Q8_0: 0}  # byte offset of each block's f16 d
 
 
 def seed_for(config: str, case: str = "") -> int:
@@ -101,18 +105,21 @@ def half_normal_f16_bits(seed: int, n: int, sigma: float) -> np.ndarray:
 
 
 def quant_weights(scheme: int, seed: int, rows: int, k: int) -> np.ndarray:
-    """GGUF wire blocks for a [rows, k] weight: uint8 [rows, k/256*block_bytes]."""
-    if k % 256:
-        raise ValueError("k must be a multiple of 256")
-    bb = BLOCK_BYTES[scheme]
-    nblocks = rows * (k // 256)
+    """GGUF wire blocks for a [rows, k] weight: uint8 [rows, k/block_len*block_bytes].
+    Every byte is seeded-random except each block's f16 d (and Q4_K's dmin),
+    which is |N(0, 0.02)| (|N(0, 0.01)| for dmin)."""
+    bl, bb = BLOCK_LEN[scheme], BLOCK_BYTES[scheme]
+    if k % bl:
+        raise ValueError(f"k must be a multiple of {bl}")
+    nblocks = rows * (k // bl)
     blk = random_bytes(seed, nblocks * bb).reshape(nblocks, bb)
     d = half_normal_f16_bits(seed ^ 0xD1D1D1D1D1D1D1D1, nblocks, 0.02)
-    blk[:, 0:2] = d.view(np.uint8).reshape(nblocks, 2)
+    o = D_OFFSET[scheme]
+    blk[:, o:o + 2] = d.view(np.uint8).reshape(nblocks, 2)
     if scheme == Q4_K:
         dmin = half_normal_f16_bits(seed ^ 0x3C3C3C3C3C3C3C3C, nblocks, 0.01)
         blk[:, 2:4] = dmin.view(np.uint8).reshape(nblocks, 2)
-    return blk.reshape(rows, (k // 256) * bb)
+    return blk.reshape(rows, (k // bl) * bb)
 
 
 def zipf_logits(seed: int, t: int, e: int, s: float = 1.1) -> np.ndarray:

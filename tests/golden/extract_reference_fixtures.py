@@ -6,6 +6,9 @@ Data only (inputs and expected outputs); run once in the build container where
       consumed by crates/r9v-format/tests/schemes.rs:482-516)
   crates/r9v-format/tests/fixtures/r9v-format/iq_a24_reference.txt (the IQ4_XS and
       IQ4_NL cases, consumed by crates/r9v-format/tests/iq.rs:159-197)
+  crates/r9v-format/tests/fixtures/r9v-format/gguf_a23_reference.txt (the Q8_0, Q6_K
+      and Q4_K cases, consumed by crates/r9v-format/tests/gguf.rs:44-90,172-180)
+      -> gguf_a23_reference.txt
   crates/r9v-format/tests/fixtures/r9v-format/{a25_standard,a25_split-0000{1,2}-of-00002,
       llama_tiny_q80}.hex (whole GGUF files as hex text, consumed by
       crates/r9v-format/tests/container.rs:72-330, 897-930) -> tests/golden/gguf/
@@ -36,6 +39,18 @@ def main() -> int:
             out.append(line)
     (DST / "iq4_reference.txt").write_text(
         HEADER.format(src="crates/r9v-format/tests/fixtures/r9v-format/iq_a24_reference.txt")
+        + "\n".join(out) + "\n")
+    keep, out = False, []
+    for line in (SRC / "gguf_a23_reference.txt").read_text().splitlines():
+        if line.startswith("#"):
+            out.append(line)
+            continue
+        if line.startswith("case "):
+            keep = line.split()[1] in ("Q8_0", "Q6_K", "Q4_K")
+        if keep:
+            out.append(line)
+    (DST / "gguf_a23_reference.txt").write_text(
+        HEADER.format(src="crates/r9v-format/tests/fixtures/r9v-format/gguf_a23_reference.txt")
         + "\n".join(out) + "\n")
     gdir = DST / "gguf"
     gdir.mkdir(exist_ok=True)

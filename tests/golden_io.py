@@ -65,3 +65,17 @@ def gguf_fixture(name: str) -> bytes:
     provenance header)."""
     text = (GOLDEN / "gguf" / f"{name}.hex").read_text()
     return bytes.fromhex("".join(l for l in text.splitlines() if not l.startswith("#")))
+
+
+def a23_cases():
+    """crates/r9v-format/tests/gguf.rs:44-90 (load_reference) format: n, k, wire
+    hex, y = f32 LE bytes hex (gguf-py 0.19.0 dequantize); Q8_0, Q4_K, Q6_K."""
+    out = {}
+    for c in _records(GOLDEN / "gguf_a23_reference.txt"):
+        out[c["name"]] = {
+            "n": int(c["n"]),
+            "k": int(c["k"]),
+            "wire": np.frombuffer(bytes.fromhex(c["wire"]), dtype=np.uint8),
+            "y_bits": np.frombuffer(bytes.fromhex(c["y"]), dtype="<u4"),
+        }
+    return out

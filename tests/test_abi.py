@@ -126,3 +126,33 @@ def test_workspace_and_static_figures():
     lib = ffi.load()
     assert lib.r9vx_moe_ffn_static_flops(ctypes.byref(fst), 8192) == 515_396_075_520  # config 4
     assert ffi.ffn_workspace_bytes(fst) > 81920 * 2048 * 4
+
+
+def test_split_scheme_refusals_and_figures():
+    """Q8_0 / Q6_K: the decode GEMV only (m_bucket <= 8), bf16 activations,
+    and a w_scales array required; Q4_K / IQ4_XS take none; the device
+    repack refuses schemes that need none and overlapping buffers."""
+    lib = ffi.load()
+    for scheme in (ffi.Q6_K, ffi.Q8_0):
+        st = ffi.matmul_static(n=64, k=512, w_scheme=scheme, in_dtype=ffi.F32, out_dtype=ffi.F32, m_bucket=16)
+        args = ffi.MatmulArgs()
+        args.m = 1
+        assert _call(lib.r9vx_matmul_launch, st, args) < 0
+        msg = lib.r9vx_last_error().decode()
+        for part in ("bf16 activations only", "m_bucket <= 8", "w_scales (the f16 d array", "w is NULL"):
+            assert part in msg, msg
+        good = ffi.matmul_static(n=64, k=512, w_scheme=scheme, in_dtype=ffi.BF16, out_dtype=ffi.F32)
+        bb, bl = ffi.BLOCK_BYTES[scheme], ffi.BLOCK_LEN[scheme]
+        assert ffi.matmul_static_bytes(good, 1) == 64 * 512 // bl * bb + 512 * 2 + 64 * 4
+    st = ffi.matmul_static(n=64, k=512, w_scheme=ffi.Q4_K, in_dtype=ffi.BF16, out_dtype=ffi.F32)
+    args = ffi.MatmulArgs()
+    args.m = 1
+    args.w_scales = 16
+    assert _call(lib.r9vx_matmul_launch, st, args) < 0
+    assert "inline scales" in lib.r9vx_last_error().decode()
+    buf = ctypes.create_string_buffer(4096)
+    base = ctypes.addressof(buf) + (-ctypes.addressof(buf) % 16)
+    rc = lib.r9vx_repack_launch(ffi.Q4_K, base, 1, 256, base + 1024, base + 2048, None)
+    assert rc == -2 and "device layout" in lib.r9vx_last_error().decode()
+    rc = lib.r9vx_repack_launch(ffi.Q6_K, base, 4, 256, base + 16, base + 2048, None)
+    assert rc == -1 and "overlap" in lib.r9vx_last_error().decode()

@@ -391,6 +391,8 @@ def _model_file():
         ("blk.0.ffn_gate_up_exps.weight", (dm, 2 * dff, e), 23, gate + gate),
         ("blk.0.ffn_down_exps.weight", (dff, dm, e), 12, down),
         ("token_embd.weight", (32, 3), 8, bytes(102)),
+        ("blk.0.attn_k_f16.weight", (256, 2), 1, bytes(1024)),
+        ("blk.0.attn_v.weight", (512, 2), 8, bytes(2 * 16 * 34)),
         ("blk.0.ffn_up_bad.weight", (dm, dff, e), 12, bytes(e * dff * (dm // 256) * 144)),
     ]
     return build([("general.architecture", (8, "llama"))], tensors)
@@ -400,8 +402,12 @@ def test_matmul_and_moe_ffn_statics_from_a_checkpoint():
     f = gguf.GgufFile.parse(_model_file())
     st = f.matmul_static("blk.0.attn_q.weight", m_bucket=5)
     assert (st.n, st.k, st.w_scheme, st.m_bucket) == (3, 2048, ffi.Q4_K, 5)
-    with pytest.raises(gguf.GgufError, match="Q8_0"):
+    with pytest.raises(gguf.GgufError, match="K=32; the matmul kernels take K in multiples of 256"):
         f.matmul_static("token_embd.weight")
+    with pytest.raises(gguf.GgufError, match="is F16"):
+        f.matmul_static("blk.0.attn_k_f16.weight")
+    st8 = f.matmul_static("blk.0.attn_v.weight")
+    assert (st8.n, st8.k, st8.w_scheme) == (2, 512, ffi.Q8_0)
     with pytest.raises(gguf.GgufError, match="not a .K, N. matrix"):
         f.matmul_static("blk.0.ffn_gate_exps.weight")
     with pytest.raises(gguf.GgufError, match="no tensor named"):

@@ -71,7 +71,8 @@ def checkpoint():
 def test_loaded_matmul_weight_runs_like_a_direct_upload(checkpoint, name, key, m):
     b = checkpoint["shards"][0]
     f = gguf.GgufFile.parse(b)
-    st, w = gguf.load_matmul_weight(f, b, name, m_bucket=m)
+    st, w, ws = gguf.load_matmul_weight(f, b, name, m_bucket=m)
+    assert ws is None
     wire = checkpoint[key]
     assert np.array_equal(host(w), wire.reshape(-1))
     n, k = wire.shape[0], st.k

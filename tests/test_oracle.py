@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle_ffi as O
-from golden_io import iq4_cases, q4k_cases
+from golden_io import a23_cases, iq4_cases, q4k_cases
 from r9v_amd import synth
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
@@ -155,6 +155,71 @@ def test_dequantize_refuses_nonfinite_scale():
     w[0, 0:2] = np.frombuffer(struct.pack("<H", 0x7E00), np.uint8)  # d = nan
     with pytest.raises(O.OracleError):
         O.dequantize(O.IQ4_XS, w, 2, 256)
+
+
+# ------------------------------------------------------ Q6_K / Q8_0 decode
+
+def test_a23_golden_bit_exact():
+    """crates/r9v-format/tests/gguf.rs:172-180: Q8_0 (5x128), Q4_K and Q6_K
+    (3x1024) wire decode to gguf-py 0.19.0's dequantize, bit for bit."""
+    cases = a23_cases()
+    assert set(cases) == {"Q8_0", "Q4_K", "Q6_K"}
+    for name, scheme in (("Q8_0", O.Q8_0), ("Q4_K", O.Q4_K), ("Q6_K", O.Q6_K)):
+        c = cases[name]
+        got = O.dequantize(scheme, c["wire"], c["n"], c["k"])
+        assert np.array_equal(got.reshape(-1).view(np.uint32), c["y_bits"]), name
+
+
+def _q6k_llamacpp_rows(wire, n, k):
+    """The textbook Q6_K row loop (llama.cpp dequantize_row_q6_K form): per
+    128-weight half, l in 0..32 yields four weights from ql[l], ql[l+32] and
+    the four bit pairs of qh[l]; y = d * sc * (q - 32) in f32."""
+    blocks = wire.reshape(-1, 210)
+    out = np.empty((blocks.shape[0], 256), dtype=np.float32)
+    for b, blk in enumerate(blocks):
+        d = np.frombuffer(blk[208:210].tobytes(), dtype=np.float16).astype(np.float32)[0]
+        sc = blk[192:208].view(np.int8).astype(np.float32)
+        for half in range(2):
+            ql, qh, s = blk[64 * half:64 * half + 64].astype(np.int32), blk[128 + 32 * half:160 + 32 * half].astype(np.int32), sc[8 * half:8 * half + 8]
+            for l in range(32):
+                qs = [(ql[l] & 15) | ((qh[l] & 3) << 4), (ql[l + 32] & 15) | (((qh[l] >> 2) & 3) << 4),
+                      (ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4), (ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)]
+                for r in range(4):
+                    dl = np.float32(d * s[l // 16 + 2 * r])
+                    out[b, 128 * half + 32 * r + l] = np.float32(dl * np.float32(qs[r] - 32))
+    return out.reshape(n, k)
+
+
+def test_q6k_matches_the_llamacpp_row_loop():
+    """A restatement with a different structure (llama.cpp's loop over l with
+    four outputs per step) agrees bit for bit on random blocks, so a wrong
+    nibble, bit pair, byte index or scale index in either would show."""
+    n, k = 3, 512
+    w = synth.random_bytes(4242, n * (k // 256) * 210).reshape(-1, 210)
+    w[:, 208:210] = synth.half_normal_f16_bits(4243, w.shape[0], 0.02).view(np.uint8).reshape(-1, 2)
+    got = O.dequantize(O.Q6_K, w, n, k)
+    assert np.array_equal(got.view(np.uint32), _q6k_llamacpp_rows(w.reshape(-1), n, k).view(np.uint32))
+
+
+def test_q80_closed_form():
+    n, k = 4, 96
+    w = synth.random_bytes(77, n * (k // 32) * 34).reshape(-1, 34)
+    w[:, 0:2] = synth.half_normal_f16_bits(78, w.shape[0], 0.05).view(np.uint8).reshape(-1, 2)
+    d = w[:, 0:2].copy().view(np.float16).astype(np.float32)
+    want = (d * w[:, 2:].view(np.int8).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(O.dequantize(O.Q8_0, w, n, k).reshape(-1, 32), want)
+
+
+def test_q6k_q80_refuse_nonfinite_scales():
+    w = synth.random_bytes(5, 2 * 210).reshape(2, 210)
+    w[:, 208:210] = 0
+    w[1, 208:210] = np.frombuffer(struct.pack("<H", 0x7C00), np.uint8)
+    with pytest.raises(O.OracleError):
+        O.dequantize(O.Q6_K, w, 2, 256)
+    w = np.zeros((1, 34), dtype=np.uint8)
+    w[0, 0:2] = np.frombuffer(struct.pack("<H", 0xFE00), np.uint8)
+    with pytest.raises(O.OracleError):
+        O.dequantize(O.Q8_0, w, 1, 32)
 
 
 # ---------------------------------------------------------------- expf twin
