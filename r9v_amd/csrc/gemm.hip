@@ -1,6 +1,7 @@
 /*
  * gemm.hip -- prefill dequant-GEMM on MFMA: y[m, n] = sum_k x[m, k] * w[n, k]
- * for bf16 activations (m > 8) and GGUF Q4_K / IQ4_XS weights.
+ * for bf16 activations (m > 8) and GGUF Q4_K / IQ4_XS weights (wire blocks)
+ * or Q8_0 / Q6_K weights (split layout, LDS-decoded tiles only).
  *
  * T0 meaning: crates/r9v-t0/src/matmul.rs:1940-2414 (Branch D), output cast
  * crates/r9v-t0/src/dtype.rs:102-111 (bf16 RNE); epilogue matmul.rs:2421-2446.
@@ -29,6 +30,7 @@ struct GemmArgs {
     const _Float16 *x16;
     const float *scale;
     const uint8_t *w;
+    const uint16_t *ws; /* Q8_0 / Q6_K split layout: f16 d per block */
     const float *bias;
     const float *residual;
     void *y;
@@ -36,6 +38,7 @@ struct GemmArgs {
     uint32_t m, n, k;
     uint32_t m_tiles, n_tiles;
     uint32_t y_bf16, epilogue;
+    uint32_t ws_row; /* d values per weight row */
 };
 
 /* PERM = 0: natural order; R9VX_SCHEME_Q4_K / R9VX_SCHEME_IQ4_XS: each 64-column
@@ -109,7 +112,8 @@ __global__ __launch_bounds__(256, NBUF == 1 ? 2 : 1) void gemm_kernel(GemmArgs a
     }
     const uint32_t wrow = n0 + tid < a.n ? n0 + tid : a.n - 1;
     r9vx_f32x16 acc[BM / 32][2];
-    mma_mainloop<SCHEME, BM, NBUF>(lds, as, a.w + (uint64_t)wrow * a.w_row_stride, a.k / kTileK, acc);
+    mma_mainloop<SCHEME, BM, NBUF>(lds, as, a.w + (uint64_t)wrow * a.w_row_stride, a.k / kTileK, acc,
+                                   a.ws ? a.ws + (uint64_t)wrow * a.ws_row : nullptr);
 
     /* Epilogue through LDS, 32 rows at a time: the accumulators go to a
      * 32 x 256 f32 stage (row stride 260 floats, so the two half-waves'
@@ -296,7 +300,13 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     a.bias = p.bias;
     a.residual = p.residual;
     a.y = p.y;
-    a.w_row_stride = (uint64_t)(p.k / 256) * (p.scheme == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : R9VX_IQ4XS_BYTES);
+    a.ws = p.w_scales;
+    switch (p.scheme) {
+    case R9VX_SCHEME_Q4_K: a.w_row_stride = (uint64_t)(p.k / 256) * R9VX_Q4K_BYTES; break;
+    case R9VX_SCHEME_IQ4_XS: a.w_row_stride = (uint64_t)(p.k / 256) * R9VX_IQ4XS_BYTES; break;
+    case R9VX_SCHEME_Q6_K: a.w_row_stride = (uint64_t)(p.k / 256) * R9VX_Q6K_BODY, a.ws_row = p.k / 256; break;
+    default: a.w_row_stride = p.k, a.ws_row = p.k / 32; break; /* Q8_0 */
+    }
     a.m = p.m;
     a.n = p.n;
     a.k = p.k;
@@ -304,7 +314,8 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     a.epilogue = p.epilogue;
     /* 256 x 256 register-decoded tiles when there are enough of them to fill
      * the chip; 128-row LDS-decoded tiles (two workgroups per CU) otherwise. */
-    const bool big = (uint64_t)((p.m + 255) / 256) * ((p.n + 255) / 256) >= 256;
+    const bool split = p.scheme == R9VX_SCHEME_Q8_0 || p.scheme == R9VX_SCHEME_Q6_K;
+    const bool big = !split && (uint64_t)((p.m + 255) / 256) * ((p.n + 255) / 256) >= 256;
     if (big) {
         if (p.scheme == R9VX_SCHEME_Q4_K)
             hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3(p.m), dim3(256), 0, stream, p.x, p.k, x16, scale);
@@ -324,9 +335,13 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     a.m_tiles = (p.m + 127) / 128;
     a.n_tiles = (p.n + 255) / 256;
     dim3 grid(a.m_tiles * a.n_tiles);
-    if (p.scheme == R9VX_SCHEME_Q4_K)
-        hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q4_K, 128, 1>), grid, dim3(256), 0, stream, a);
-    else
-        hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_IQ4_XS, 128, 1>), grid, dim3(256), 0, stream, a);
+    /* Q8_0 / Q6_K always take this LDS-decoded tile (their 48- and 64-byte
+     * steps do not fit the register-decoded core's 16-byte lane payload). */
+    switch (p.scheme) {
+    case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q4_K, 128, 1>), grid, dim3(256), 0, stream, a); break;
+    case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_IQ4_XS, 128, 1>), grid, dim3(256), 0, stream, a); break;
+    case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q6_K, 128, 1>), grid, dim3(256), 0, stream, a); break;
+    default: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q8_0, 128, 1>), grid, dim3(256), 0, stream, a); break;
+    }
     return (int)hipGetLastError();
 }

@@ -93,9 +93,7 @@ static void check_matmul_static(const r9vx_matmul_static *st, Problems &pr) {
                st->w_scheme);
     if (split_scheme(st->w_scheme) && st->in_dtype != R9VX_DTYPE_BF16)
         pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u takes bf16 activations only", st->w_scheme);
-    if (split_scheme(st->w_scheme) && st->m_bucket > 8)
-        pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u: only the decode GEMV (m_bucket <= 8) is implemented",
-               st->w_scheme);
+
     if (st->k == 0 || st->k % 256)
         pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of the 256-weight super-block", st->k);
     if (st->n == 0) pr.add(R9VX_ERR_INVALID, "n must be positive");
@@ -174,6 +172,7 @@ int r9vx_matmul_launch(const r9vx_matmul_static *st, const r9vx_matmul_args *a,
     if (mfma) {
         r9vx_gemm_problem g{};
         g.w = a->w;
+        g.w_scales = reinterpret_cast<const uint16_t *>(a->w_scales);
         g.x = reinterpret_cast<const uint16_t *>(a->x);
         g.bias = a->bias;
         g.residual = reinterpret_cast<const float *>(a->residual);

@@ -74,6 +74,7 @@ int r9vx_launch_gemv(const r9vx_gemv_problem &p, hipStream_t stream);
 
 struct r9vx_gemm_problem {
     const uint8_t *w;
+    const uint16_t *w_scales; /* Q8_0 / Q6_K: f16 d per block */
     const uint16_t *x; /* bf16 [m, k] */
     const float *bias;
     const float *residual;

@@ -113,6 +113,106 @@ __device__ __forceinline__ void load_w(const uint8_t *row, uint32_t kt, WRegs &w
     load_w64<SCHEME>(row, kt, w.q0, w.q1, w.hdr);
 }
 
+/* Q8_0 / Q6_K in the split layout (body row + f16 d row).  One K step of 64:
+ *   Q8_0: blocks 2kt, 2kt+1: 64 body bytes and their two d values;
+ *   Q6_K: step ks = kt%4 of super-block kt/4 covers values 64ks..64ks+63:
+ *         value t takes nibble ks%2 of ql byte 64(ks/2)+t, bit pair
+ *         2(ks%2) + t/32 of qh byte 32(ks/2) + t%32, and scale 4ks + t/16
+ *         (crates/r9v-format/src/ggml.rs:817-850). */
+struct WRegsQ80 {
+    r9vx_u32x4 q[4];
+    uint32_t d2;
+};
+struct WRegsQ6K {
+    r9vx_u32x4 ql[4], qh[2];
+    uint32_t sc4, d;
+};
+template <int SCHEME>
+struct WRegsFor {
+    using T = WRegs;
+};
+template <>
+struct WRegsFor<R9VX_SCHEME_Q8_0> {
+    using T = WRegsQ80;
+};
+template <>
+struct WRegsFor<R9VX_SCHEME_Q6_K> {
+    using T = WRegsQ6K;
+};
+
+template <int SCHEME>
+__device__ __forceinline__ void load_w_any(const uint8_t *row, const uint16_t *srow, uint32_t kt,
+                                           typename WRegsFor<SCHEME>::T &w) {
+    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+        const uint8_t *p = row + 64 * (uint64_t)kt;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w.q[i] = r9vx_ld128(p + 16 * i);
+        w.d2 = *reinterpret_cast<const uint32_t *>(srow + 2 * kt);
+    } else if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
+        const uint32_t blk = kt >> 2, ks = kt & 3, g = ks >> 1;
+        const uint8_t *b = row + (uint64_t)blk * R9VX_Q6K_BODY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w.ql[i] = r9vx_ld128(b + 64 * g + 16 * i);
+        w.qh[0] = r9vx_ld128(b + 128 + 32 * g);
+        w.qh[1] = r9vx_ld128(b + 128 + 32 * g + 16);
+        w.sc4 = *reinterpret_cast<const uint32_t *>(b + 192 + 4 * ks);
+        w.d = srow[blk];
+    } else {
+        load_w<SCHEME>(row, kt, w);
+    }
+}
+
+__device__ __forceinline__ uint32_t u32x4_at(const r9vx_u32x4 &v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+/* Dequantizes one weight row's 64 K values of step ks in natural K order
+ * into the 8 LDS chunks of B row `row`: each value with the exact f32
+ * formula, then one fp16 rounding. */
+template <int SCHEME>
+__device__ __forceinline__ void dequant_store_any(const typename WRegsFor<SCHEME>::T &w, uint32_t ks, uint8_t *B,
+                                                  uint32_t row, const float *lutf) {
+    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+        const float d0 = r9vx_f16_to_f32((uint16_t)(w.d2 & 0xFFFF)), d1 = r9vx_f16_to_f32((uint16_t)(w.d2 >> 16));
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float d = c < 4 ? d0 : d1;
+            uint32_t h[4];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const uint32_t dw = u32x4_at(w.q[c >> 1], 2 * (c & 1) + half);
+                h[2 * half] = cvt_pk_h2(d * (float)(int8_t)(dw & 0xFF), d * (float)(int8_t)((dw >> 8) & 0xFF));
+                h[2 * half + 1] = cvt_pk_h2(d * (float)(int8_t)((dw >> 16) & 0xFF), d * (float)(int8_t)(dw >> 24));
+            }
+            *reinterpret_cast<r9vx_u32x4 *>(B + lds_chunk(row, c)) = r9vx_u32x4{h[0], h[1], h[2], h[3]};
+        }
+    } else if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
+        const float d = r9vx_f16_to_f32((uint16_t)w.d);
+        const uint32_t nib = 4 * (ks & 1);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float dl = d * (float)(int8_t)((w.sc4 >> (8 * (c >> 1))) & 0xFF);
+            const uint32_t pair = 4 * (ks & 1) + 2 * (c >> 2);
+            uint32_t h[4];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const int i = 2 * c + half; /* dword of the 64 values: t = 4i .. 4i+3 */
+                const uint32_t qlw = u32x4_at(w.ql[i >> 2], i & 3);
+                const uint32_t qhw = u32x4_at(w.qh[(i & 7) >> 2], i & 3);
+                const uint32_t q6 = ((qlw >> nib) & 0x0F0F0F0Fu) | (((qhw >> pair) & 0x03030303u) << 4);
+                float v[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = dl * ((float)((q6 >> (8 * j)) & 0xFF) - 32.0f);
+                h[2 * half] = cvt_pk_h2(v[0], v[1]);
+                h[2 * half + 1] = cvt_pk_h2(v[2], v[3]);
+            }
+            *reinterpret_cast<r9vx_u32x4 *>(B + lds_chunk(row, c)) = r9vx_u32x4{h[0], h[1], h[2], h[3]};
+        }
+    } else {
+        dequant_store<SCHEME>(w, ks, B, row, lutf);
+    }
+}
+
 /* MFMAs of one K step from LDS stage (A, B) into acc[BM/32][2].  The
  * fragments of slice s+1 are read while slice s's MFMAs run (two fragment
  * sets in registers), so no MFMA waits on its own LDS read. */
@@ -150,7 +250,7 @@ __device__ __forceinline__ void mma_step(const uint8_t *A, const uint8_t *B, uin
  */
 template <int SCHEME, int BM, int NBUF, typename ASrc>
 __device__ __forceinline__ void mma_mainloop(uint8_t *lds, ASrc &asrc, const uint8_t *wrow, uint32_t kt_n,
-                                             r9vx_f32x16 (&acc)[BM / 32][2]) {
+                                             r9vx_f32x16 (&acc)[BM / 32][2], const uint16_t *srow = nullptr) {
     using S = MmaShape<BM, NBUF>;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *lutf = reinterpret_cast<const float *>(lds + NBUF * S::kStage);
@@ -164,12 +264,12 @@ __device__ __forceinline__ void mma_mainloop(uint8_t *lds, ASrc &asrc, const uin
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     typename ASrc::Regs ra;
-    WRegs wq;
+    typename WRegsFor<SCHEME>::T wq;
     asrc.load(0, ra);
-    load_w<SCHEME>(wrow, 0, wq);
+    load_w_any<SCHEME>(wrow, srow, 0, wq);
     __syncthreads(); /* the codebook table */
     asrc.store(ra, lds);
-    dequant_store<SCHEME>(wq, 0, lds + S::kABytes, tid, lutf);
+    dequant_store_any<SCHEME>(wq, 0, lds + S::kABytes, tid, lutf);
     __syncthreads();
     if constexpr (NBUF == 2) {
         for (uint32_t kt = 0; kt < kt_n; ++kt) {
@@ -177,14 +277,14 @@ __device__ __forceinline__ void mma_mainloop(uint8_t *lds, ASrc &asrc, const uin
             const bool more = kt + 1 < kt_n;
             if (more) {
                 asrc.load(kt + 1, ra);
-                load_w<SCHEME>(wrow, kt + 1, wq);
+                load_w_any<SCHEME>(wrow, srow, kt + 1, wq);
             }
             uint8_t *st = lds + cur * S::kStage;
             mma_step<BM>(st, st + S::kABytes, wave, lane, acc);
             if (more) {
                 uint8_t *nx = lds + (cur ^ 1) * S::kStage;
                 asrc.store(ra, nx);
-                dequant_store<SCHEME>(wq, (kt + 1) & 3, nx + S::kABytes, tid, lutf);
+                dequant_store_any<SCHEME>(wq, (kt + 1) & 3, nx + S::kABytes, tid, lutf);
             }
             __syncthreads();
         }
@@ -193,13 +293,13 @@ __device__ __forceinline__ void mma_mainloop(uint8_t *lds, ASrc &asrc, const uin
             const bool more = kt + 1 < kt_n;
             if (more) {
                 asrc.load(kt + 1, ra);
-                load_w<SCHEME>(wrow, kt + 1, wq);
+                load_w_any<SCHEME>(wrow, srow, kt + 1, wq);
             }
             mma_step<BM>(lds, lds + S::kABytes, wave, lane, acc);
             __syncthreads();
             if (more) {
                 asrc.store(ra, lds);
-                dequant_store<SCHEME>(wq, (kt + 1) & 3, lds + S::kABytes, tid, lutf);
+                dequant_store_any<SCHEME>(wq, (kt + 1) & 3, lds + S::kABytes, tid, lutf);
             }
             __syncthreads();
         }

@@ -77,7 +77,7 @@ def matmul(scheme, w, n, k, x, x_dtype, y_dtype=F32, bias=None, residual=None, t
     m = x.shape[0]
     y = np.empty((m, n), dtype=np.float32 if y_dtype == F32 else np.uint16)
     w = np.ascontiguousarray(w)
-    if threads:
+    if threads and bias is None and residual is None:  # the threaded oracle has no epilogue
         rc = lib().rxo_matmul_mt(scheme, _p(w), n, k, x_dtype, _p(x), m, y_dtype, _p(y), threads)
     else:
         rc = lib().rxo_matmul(scheme, _p(w), n, k, x_dtype, _p(x), m, _p(bias), _p(residual),

@@ -155,3 +155,35 @@ def test_gguf_split_upload_runs_like_the_device_repack():
     b2 = build([], [("w", (k, n), 14, bad.tobytes())])
     with pytest.raises(gguf.GgufError, match="1 block"):
         gguf.load_matmul_weight(gguf.GgufFile.parse(b2), b2, "w")
+
+
+PREFILL = [(9, 320, 2048), (40, 1000, 4096), (300, 512, 2048), (129, 2304, 1024)]
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("m,n,k", PREFILL)
+def test_prefill_gemm_split_layout_parity(scheme, m, n, k):
+    """m > 8: the MFMA GEMM (LDS-decoded 128 x 256 tiles) on the split layout."""
+    w = synth.quant_weights(scheme, 3000 + m + n, n, k)
+    x = synth.normal_bf16(4000 + m + k, (m, k))
+    body, scales = ffi.repack(dev(w), scheme, n, k)
+    y = host(ffi.matmul(body, scheme, n, k, bf16_dev(x), w_scales=scales))
+    check_close(y, O.matmul(scheme, w, n, k, x, O.BF16, threads=8), f"scheme={scheme} m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+def test_prefill_gemm_split_large_sampled(scheme):
+    """A 1024 x 4096 x 4096 launch (16 K tiles of rows, 16 column tiles):
+    sampled rows against the oracle, residual epilogue and bf16 output."""
+    m, n, k = 1024, 4096, 4096
+    w = synth.quant_weights(scheme, 5151, n, k)
+    x = synth.normal_bf16(5152, (m, k))
+    res = synth.normal_f32(5153, (m, n))
+    body, scales = ffi.repack(dev(w), scheme, n, k)
+    y = host(ffi.matmul(body, scheme, n, k, bf16_dev(x), residual=dev(res), w_scales=scales))
+    yb = ffi.matmul(body, scheme, n, k, bf16_dev(x), residual=dev(res), out_dtype=ffi.BF16, w_scales=scales)
+    rows = np.array([0, 1, 127, 128, 511, 640, 1000, 1023])
+    ref = O.matmul(scheme, w, n, k, x[rows], O.BF16, residual=res[rows], threads=8)
+    check_close(y[rows], ref, f"scheme={scheme} sampled")
+    got16 = host(yb.view(torch.int16))[rows].view(np.uint16).astype(np.uint32) << 16
+    check_bf16_out(got16.view(np.float32), y[rows], ref, "bf16 out")
