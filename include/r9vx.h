@@ -66,8 +66,21 @@ enum r9vx_scheme {
  * Bodies and scales together hold exactly the wire bytes.  A matmul on them
  * passes the body as `w` and the d array as `w_scales`. */
 
-/* Matmul epilogues (crates/r9v-t0/src/matmul.rs:2421-2446). */
-enum r9vx_epilogue { R9VX_EPILOGUE_NONE = 0, R9VX_EPILOGUE_BIAS = 1, R9VX_EPILOGUE_RESIDUAL = 2 };
+/* Matmul epilogues (crates/r9v-t0/src/matmul.rs:2421-2446), plus the gated
+ * epilogue of the kernel generator's GEMM family ("gated (gate_up
+ * interleave)", specs/spec-04-kernel-generator.md:100): with SWIGLU the
+ * weights hold 2N rows, gate rows [0, N) then up rows [N, 2N) (the w_gate_up
+ * convention of crates/r9v-t0/src/moe_ffn.rs:51-55), and
+ * y[m, j] = silu(x[m].w[j]) * (x[m].w[N+j]) -- T0's matmul (f32 out) then
+ * act_mul with SiLU (crates/r9v-t0/src/act_mul.rs:86-99,
+ * crates/r9v-t0/src/activation.rs:135-138) in one launch.  bf16 activations,
+ * m_bucket <= 8. */
+enum r9vx_epilogue {
+    R9VX_EPILOGUE_NONE = 0,
+    R9VX_EPILOGUE_BIAS = 1,
+    R9VX_EPILOGUE_RESIDUAL = 2,
+    R9VX_EPILOGUE_SWIGLU = 3
+};
 
 /* Router scoring (crates/r9v-t0/src/moe_route.rs:329-351). */
 enum r9vx_scoring { R9VX_SCORING_SOFTMAX = 0, R9VX_SCORING_SIGMOID = 1 };

@@ -284,6 +284,16 @@ int rxo_matmul(int scheme, const uint8_t *w, uint32_t n, uint32_t k, int x_dtype
     return rc;
 }
 
+/* act_mul with SiLU: crates/r9v-t0/src/act_mul.rs:86-99 (y = act(g) * u, no
+ * clamp) with activation.rs:135-138 (silu(x) = x / (1 + exp(-x)), f32 exp =
+ * the host expf). */
+void rxo_act_mul_silu(const float *g, const float *u, uint64_t n, float *y) {
+    for (uint64_t i = 0; i < n; ++i) {
+        float act = g[i] / (1.0f + rxo_expf(-g[i]));
+        y[i] = act * u[i];
+    }
+}
+
 int rxo_matmul_mt(int scheme, const uint8_t *w, uint32_t n, uint32_t k, int x_dtype,
                   const void *x, uint32_t m, int y_dtype, void *y, int threads) {
     int rc = matmul_validate(scheme, w, n, k, x_dtype, m, NULL, NULL, y_dtype);

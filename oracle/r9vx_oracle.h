@@ -79,6 +79,9 @@ int rxo_matmul(int scheme, const uint8_t *w, uint32_t n, uint32_t k,
                const float *bias, const float *residual,
                int y_dtype, void *y);
 
+/* act_mul with SiLU (crates/r9v-t0/src/act_mul.rs:86-99): y = silu(g) * u. */
+void rxo_act_mul_silu(const float *g, const float *u, uint64_t n, float *y);
+
 /* ---- MoE -------------------------------------------------------------- */
 /* Reference glibc expf (the host libm the Rust T0 f32::exp resolves to). */
 float rxo_expf(float x);

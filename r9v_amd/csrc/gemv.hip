@@ -23,6 +23,7 @@
  */
 #include <type_traits>
 
+#include "r9vx_expf.h"
 #include "r9vx_gemv_core.h"
 
 namespace {
@@ -175,6 +176,139 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
         lane_reduce_w<V, 1>(v, lane, a.lpr_log2, emit);
 }
 
+/* The gated (SwiGLU) form: y[m, j] = silu(x[m] . w[j]) * (x[m] . w[n + j])
+ * over stacked weights (gate rows [0, n), up rows [n, 2n)), the matmul +
+ * act_mul pair of T0 (crates/r9v-t0/src/act_mul.rs:86-99 with SiLU
+ * x / (1 + exp(-x)), crates/r9v-t0/src/activation.rs:135-138) in one launch.
+ * A lane group computes the gate and the up row of each of its output rows;
+ * the two partial arrays are summed across the lanes together, so the lane
+ * that receives a row's gate sum also holds its up sum.  bf16 activations,
+ * general lane mapping (runtime lanes per row and K segments).  PAIRS gate/up
+ * row pairs per lane group: the launcher takes two when n >= 8 x SIMDs and
+ * one below (measured, Q4_K, graph replay: n = 14336, K = 4096, M = 4:
+ * 39.2 us at two against 49.1 at one and 64.9 at three; n = 2816, K = 2048,
+ * M = 8: 11.5 us at one against 21.3 at two). */
+template <int SCHEME, int M, int SPL, int PAIRS>
+__global__ __launch_bounds__(waves_for(M) * 64) void gemv_gated_kernel(GemvArgs a) {
+    constexpr int kRows = PAIRS, kWaves = waves_for(M);
+    __shared__ uint32_t lut[256];
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const uint32_t lprl = a.lpr_log2, lpr = 1u << lprl, rpi = 64u >> lprl;
+    const uint32_t lir = lane & (lpr - 1), slot = lane >> lprl;
+    const uint32_t row0 = wave * rpi * kRows + slot;
+
+    float acc[2][kRows][M];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int t = 0; t < M; ++t) acc[h][r][t] = 0.f;
+
+    for (uint32_t seg = 0; seg < a.nseg; ++seg) {
+        uint32_t cis[SPL];
+#pragma unroll
+        for (int s = 0; s < SPL; ++s) cis[s] = seg * lpr * SPL + s * lpr + lir;
+        XRaw<false> xr[SPL][M];
+#pragma unroll
+        for (int s = 0; s < SPL; ++s) {
+            uint32_t klo, khi;
+            chunk_k<SCHEME>(cis[s], klo, khi);
+#pragma unroll
+            for (int t = 0; t < M; ++t)
+                load_x_raw<false>(reinterpret_cast<const uint8_t *>(a.x) + (uint64_t)t * a.x_row_stride * 2, klo,
+                                  khi, xr[s][t]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        using Pay = typename std::conditional<split_scheme(SCHEME), Payload2, r9vx_u32x4>::type;
+        Pay qs[2][kRows][SPL];
+        Hdr hd[2][kRows][SPL];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) {
+                const uint32_t row = row0 + r * rpi;
+                const uint64_t wr = (uint64_t)(row < a.n ? row : a.n - 1) + (uint64_t)h * a.n;
+                const uint8_t *wrow = a.w + wr * a.w_row_stride;
+#pragma unroll
+                for (int s = 0; s < SPL; ++s) {
+                    if constexpr (split_scheme(SCHEME))
+                        load_chunk_split<SCHEME>(wrow, a.ws + wr * a.ws_row, cis[s], qs[h][r][s], hd[h][r][s]);
+                    else
+                        load_chunk<SCHEME>(wrow, cis[s], qs[h][r][s], hd[h][r][s]);
+                }
+            }
+        if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
+            if (seg == 0) {
+                build_iq4_lut(lut, threadIdx.x, blockDim.x);
+                __syncthreads();
+            }
+        }
+        XChunk<SCHEME, false> xc[SPL][M];
+#pragma unroll
+        for (int s = 0; s < SPL; ++s)
+#pragma unroll
+            for (int t = 0; t < M; ++t) arrange_x<SCHEME, false>(xr[s][t], xc[s][t]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int r = 0; r < kRows; ++r)
+#pragma unroll
+                for (int s = 0; s < SPL; ++s) {
+                    if constexpr (split_scheme(SCHEME))
+                        chunk_dot_split<SCHEME, M>(qs[h][r][s], hd[h][r][s], cis[s] & 7, xc[s], acc[h][r]);
+                    else
+                        chunk_dot<SCHEME, false, M>(qs[h][r][s], hd[h][r][s], cis[s] & 7, xc[s], acc[h][r], lut);
+                }
+    }
+
+    constexpr int V = kRows * M;
+    float v[2][V];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int t = 0; t < M; ++t) v[h][r * M + t] = acc[h][r][t];
+    lane_reduce_w<V, 2>(v, lane, a.lpr_log2, [&](int idx, const float (&val)[2]) {
+        const int r = idx / M, t = idx % M;
+        const uint32_t row = row0 + r * rpi;
+        if (row >= a.n) return;
+        const float g = val[0];
+        const float act = g / (1.0f + r9vx_expf(-g));
+        const float y = act * val[1];
+        const uint64_t o = (uint64_t)t * a.n + row;
+        if (a.y_bf16)
+            reinterpret_cast<uint16_t *>(a.y)[o] = r9vx_f32_to_bf16(y);
+        else
+            reinterpret_cast<float *>(a.y)[o] = y;
+    });
+}
+
+template <int SCHEME, int SPL, int PAIRS, int MM>
+int launch_gated(const GemvArgs &a, uint32_t m, uint32_t groups, hipStream_t s) {
+    if constexpr (MM == 0) {
+        return (int)hipErrorInvalidValue;
+    } else {
+        if (m != MM) return launch_gated<SCHEME, SPL, PAIRS, MM - 1>(a, m, groups, s);
+        const uint32_t rows_per_wave = groups * PAIRS;
+        const uint32_t waves = (a.n + rows_per_wave - 1) / rows_per_wave;
+        const dim3 grid((waves + waves_for(MM) - 1) / waves_for(MM));
+        hipLaunchKernelGGL((gemv_gated_kernel<SCHEME, MM, SPL, PAIRS>), grid, dim3(waves_for(MM) * 64), 0, s, a);
+        return (int)hipGetLastError();
+    }
+}
+
+uint32_t device_simds();
+
+template <int SCHEME>
+int launch_gated_scheme(const GemvArgs &a, uint32_t m, int spl, uint32_t g, hipStream_t s) {
+    if (a.n >= 8 * device_simds())
+        return spl == 2 ? launch_gated<SCHEME, 2, 2, 4>(a, m, g, s) : launch_gated<SCHEME, 1, 2, 8>(a, m, g, s);
+    return spl == 2 ? launch_gated<SCHEME, 2, 1, 4>(a, m, g, s) : launch_gated<SCHEME, 1, 1, 8>(a, m, g, s);
+}
+
 /* SIMDs of the current device (4 per CU), for the wave-balance rule. */
 uint32_t device_simds() {
     static uint32_t cached[64] = {};
@@ -285,6 +419,15 @@ int r9vx_launch_gemv(const r9vx_gemv_problem &p, hipStream_t stream) {
     a.epilogue = p.epilogue;
     const uint32_t groups = 64 / lpr;
     const bool xf32 = p.x_dtype == R9VX_DTYPE_F32;
+    if (p.epilogue == R9VX_EPILOGUE_SWIGLU) {
+        if (xf32) return (int)hipErrorInvalidValue;
+        switch (p.scheme) {
+        case R9VX_SCHEME_Q4_K: return launch_gated_scheme<R9VX_SCHEME_Q4_K>(a, p.m, spl, groups, stream);
+        case R9VX_SCHEME_IQ4_XS: return launch_gated_scheme<R9VX_SCHEME_IQ4_XS>(a, p.m, spl, groups, stream);
+        case R9VX_SCHEME_Q6_K: return launch_gated_scheme<R9VX_SCHEME_Q6_K>(a, p.m, spl, groups, stream);
+        default: return launch_gated_scheme<R9VX_SCHEME_Q8_0>(a, p.m, spl, groups, stream);
+        }
+    }
     if (p.scheme == R9VX_SCHEME_Q4_K) return launch_scheme<R9VX_SCHEME_Q4_K>(a, p.m, xf32, spl, groups, stream);
     if (p.scheme == R9VX_SCHEME_IQ4_XS) return launch_scheme<R9VX_SCHEME_IQ4_XS>(a, p.m, xf32, spl, groups, stream);
     if (xf32) return (int)hipErrorInvalidValue;

@@ -101,8 +101,10 @@ static void check_matmul_static(const r9vx_matmul_static *st, Problems &pr) {
         pr.add(R9VX_ERR_UNSUPPORTED, "in_dtype %u: only f32 and bf16 activations", st->in_dtype);
     if (st->out_dtype != R9VX_DTYPE_F32 && st->out_dtype != R9VX_DTYPE_BF16)
         pr.add(R9VX_ERR_UNSUPPORTED, "out_dtype %u: only f32 and bf16 outputs", st->out_dtype);
-    if (st->epilogue > R9VX_EPILOGUE_RESIDUAL)
-        pr.add(R9VX_ERR_UNSUPPORTED, "epilogue %u: only none/bias/residual", st->epilogue);
+    if (st->epilogue > R9VX_EPILOGUE_SWIGLU)
+        pr.add(R9VX_ERR_UNSUPPORTED, "epilogue %u: only none/bias/residual/swiglu", st->epilogue);
+    if (st->epilogue == R9VX_EPILOGUE_SWIGLU && (st->in_dtype != R9VX_DTYPE_BF16 || st->m_bucket > 8))
+        pr.add(R9VX_ERR_UNSUPPORTED, "the swiglu epilogue runs the decode GEMV only: bf16 activations, m_bucket <= 8");
     if (st->epilogue == R9VX_EPILOGUE_RESIDUAL && st->residual_dtype != R9VX_DTYPE_F32)
         pr.add(R9VX_ERR_UNSUPPORTED, "residual_dtype %u: only f32 residuals", st->residual_dtype);
 }
@@ -116,7 +118,8 @@ size_t r9vx_matmul_workspace_bytes(const r9vx_matmul_static *st) {
 
 uint64_t r9vx_matmul_static_bytes(const r9vx_matmul_static *st, uint32_t m) {
     if (!st || !matmul_scheme(st->w_scheme)) return 0;
-    uint64_t w = (uint64_t)st->n * (st->k / block_len(st->w_scheme)) * block_bytes(st->w_scheme);
+    const uint64_t w_rows = st->epilogue == R9VX_EPILOGUE_SWIGLU ? 2ull * st->n : st->n;
+    uint64_t w = w_rows * (st->k / block_len(st->w_scheme)) * block_bytes(st->w_scheme);
     uint64_t xe = st->in_dtype == R9VX_DTYPE_F32 ? 4 : 2;
     uint64_t ye = st->out_dtype == R9VX_DTYPE_F32 ? 4 : 2;
     return w + (uint64_t)m * st->k * xe + (uint64_t)m * st->n * ye;
@@ -124,7 +127,7 @@ uint64_t r9vx_matmul_static_bytes(const r9vx_matmul_static *st, uint32_t m) {
 
 uint64_t r9vx_matmul_static_flops(const r9vx_matmul_static *st, uint32_t m) {
     if (!st) return 0;
-    return 2ull * m * st->n * st->k;
+    return (st->epilogue == R9VX_EPILOGUE_SWIGLU ? 4ull : 2ull) * m * st->n * st->k;
 }
 
 int r9vx_matmul_launch(const r9vx_matmul_static *st, const r9vx_matmul_args *a,

@@ -20,7 +20,7 @@ LIB_PATH = PKG / "libr9vx.so"
 # enums (include/r9vx.h)
 F32, F16, BF16, U32 = 0, 1, 2, 8
 Q4_K, IQ4_XS, Q6_K, Q8_0 = 12, 23, 14, 8
-EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_RESIDUAL = 0, 1, 2
+EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_RESIDUAL, EPILOGUE_SWIGLU = 0, 1, 2, 3
 SCORING_SOFTMAX, SCORING_SIGMOID = 0, 1
 ACT_SILU = 0
 STATUS_NONFINITE, STATUS_DEGENERATE, STATUS_BAD_EXPERT = 1, 2, 4
@@ -194,7 +194,7 @@ def matmul_static(n, k, w_scheme, in_dtype, out_dtype, m_bucket=8, epilogue=EPIL
 
 
 def matmul(w, w_scheme, n, k, x, out_dtype=F32, bias=None, residual=None, y=None, workspace=None,
-           stream=None, w_scales=None):
+           stream=None, w_scales=None, swiglu=False):
     """y[m, n] = x[m, :] . w[n, :] (+ bias | + residual): T0 execute_matmul_op meaning.
     Q6_K / Q8_0 weights are a split body `w` plus its f16 d array `w_scales`
     (see `repack`)."""
@@ -204,6 +204,8 @@ def matmul(w, w_scheme, n, k, x, out_dtype=F32, bias=None, residual=None, y=None
         y = torch.empty((m, n), dtype=torch.float32 if out_dtype == F32 else torch.bfloat16,
                         device=x.device)
     epi = EPILOGUE_BIAS if bias is not None else (EPILOGUE_RESIDUAL if residual is not None else EPILOGUE_NONE)
+    if swiglu:  # w holds 2n rows: gate [0, n) then up [n, 2n); y = silu(gate) * up
+        epi = EPILOGUE_SWIGLU
     st = matmul_static(n, k, w_scheme, _dtype_code(x), out_dtype, m_bucket=max(m, 1), epilogue=epi)
     if workspace is None:
         nbytes = matmul_workspace_bytes(st)

@@ -42,6 +42,8 @@ def lib():
         L.rxo_dequantize.argtypes = [I, P, U, U, P]
         L.rxo_matmul.argtypes = [I, P, U, U, I, P, U, P, P, I, P]
         L.rxo_matmul_mt.argtypes = [I, P, U, U, I, P, U, I, P, I]
+        L.rxo_act_mul_silu.argtypes = [P, P, ctypes.c_uint64, P]
+        L.rxo_act_mul_silu.restype = None
         L.rxo_moe_route.argtypes = [P, P, U, U, U, ctypes.c_float, I, I, P, P]
         L.rxo_moe_sort.argtypes = [P, U, U, U, P, P, P]
         L.rxo_moe_ffn.argtypes = [I, P, U, U, U, U, U, U, P, P, I, P, I, P, I, P]
@@ -84,6 +86,20 @@ def matmul(scheme, w, n, k, x, x_dtype, y_dtype=F32, bias=None, residual=None, t
                               y_dtype, _p(y))
     _check(rc, "matmul")
     return y
+
+
+def act_mul_silu(g, u):
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    y = np.empty_like(g)
+    lib().rxo_act_mul_silu(_p(g), _p(u), g.size, _p(y))
+    return y
+
+
+def matmul_swiglu(scheme, w, n, k, x, x_dtype):
+    """T0's matmul over the stacked [gate; up] rows (f32 out), then act_mul."""
+    gu = matmul(scheme, w, 2 * n, k, x, x_dtype)
+    return act_mul_silu(gu[:, :n], gu[:, n:])
 
 
 def moe_route(logits, k, bias=None, scale=1.0, renormalize=True, scoring=0):

@@ -155,3 +155,19 @@ def test_split_scheme_refusals_and_figures():
     assert rc == -2 and "device layout" in lib.r9vx_last_error().decode()
     rc = lib.r9vx_repack_launch(ffi.Q6_K, base, 4, 256, base + 16, base + 2048, None)
     assert rc == -1 and "overlap" in lib.r9vx_last_error().decode()
+
+
+def test_swiglu_epilogue_refusals_and_figures():
+    lib = ffi.load()
+    st = ffi.matmul_static(n=64, k=512, w_scheme=ffi.Q4_K, in_dtype=ffi.F32, out_dtype=ffi.F32, m_bucket=16,
+                           epilogue=ffi.EPILOGUE_SWIGLU)
+    args = ffi.MatmulArgs()
+    args.m = 1
+    args.bias = 64
+    assert _call(lib.r9vx_matmul_launch, st, args) < 0
+    msg = lib.r9vx_last_error().decode()
+    assert "decode GEMV only" in msg and "bias given without bias epilogue" in msg
+    good = ffi.matmul_static(n=64, k=512, w_scheme=ffi.Q4_K, in_dtype=ffi.BF16, out_dtype=ffi.F32,
+                             epilogue=ffi.EPILOGUE_SWIGLU)
+    assert ffi.matmul_static_bytes(good, 1) == 128 * 2 * 144 + 512 * 2 + 64 * 4  # 2n weight rows
+    assert lib.r9vx_matmul_static_flops(ctypes.byref(good), 3) == 4 * 3 * 64 * 512

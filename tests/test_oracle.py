@@ -453,3 +453,16 @@ def test_moe_ffn_token_permutation_and_duplicates():
     single = O.moe_ffn(x, O.BF16, ids2[:, :1], np.ones_like(w[:, :1]), 4, 256, gu, dn)
     want = ((w[:, :1] * single).astype(np.float32) + (w[:, 1:2] * single).astype(np.float32))
     assert np.array_equal(y2, want.astype(np.float32))
+
+
+def test_act_mul_silu_against_f64():
+    """silu(g) * u in f32 (act_mul.rs:86-99): within 2 ulp-ish of the f64 value
+    over a wide range; exact special points."""
+    rng = np.random.default_rng(9)
+    g = np.concatenate([rng.normal(0, 4, 5000), [0.0, -0.0, 20.0, -20.0, 88.0, -88.0, 1e-30]]).astype(np.float32)
+    u = rng.normal(0, 2, g.size).astype(np.float32)
+    got = O.act_mul_silu(g, u)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    want = g64 / (1.0 + np.exp(-g64)) * u64
+    assert np.all(np.abs(got - want) <= 4 * np.finfo(np.float32).eps * np.abs(want) + 1e-37)
+    assert got[g.size - 7] == 0.0 and got[g.size - 6] == 0.0
