@@ -176,6 +176,38 @@ int r9vx_moe_route_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_
 int r9vx_moe_route_status(uint32_t *status, r9vx_stream_t stream);
 uint64_t r9vx_moe_route_static_bytes(const r9vx_moe_route_static *st, uint32_t t);
 
+/* Routing from hidden states (the router-logits matmul feeding moe_route,
+ * fused; decode form t <= 8).  No single op of the reference: it replaces the
+ * graph's router matmul (f32 weight [E, dm], the GGUF ffn_gate_inp tensor)
+ * followed by Op::MoeRoute.  Every logit is accumulated in T0's matmul order
+ * (crates/r9v-t0/src/matmul.rs:1940-2414: k ascending, one f32 accumulator,
+ * product rounded then added), so ids and weights equal T0's matmul +
+ * moe_route (crates/r9v-t0/src/moe_route.rs:89-419) bit for bit; refusals and
+ * r9vx_moe_route_status behave as for r9vx_moe_route_launch. */
+typedef struct r9vx_moe_route_hidden_args {
+    const void *x;          /* bf16 [t, dm] hidden states, 8-byte aligned */
+    const float *w_router;  /* f32 router weight in the k4 layout of r9vx_router_repack_launch, 16-byte aligned */
+    const float *bias;      /* [E] f32 or NULL (has_bias) */
+    uint32_t *expert_ids;   /* [t, K] */
+    float *weights;         /* [t, K] */
+    uint8_t *workspace;     /* r9vx_moe_route_hidden_workspace_bytes, 256-byte aligned,
+                               zero-filled once after allocation (the library leaves it so) */
+    uint32_t t;
+    uint32_t dm;            /* a multiple of 128, at most 8192 */
+} r9vx_moe_route_hidden_args;
+
+/* Load-time layout of the router weight for r9vx_moe_route_hidden_launch:
+ * f32 [E, dm] (the GGUF ffn_gate_inp tensor, rows of dm) -> [dm/4][E][4],
+ * so that a wave's load covers 4 consecutive K values of 64 consecutive
+ * experts.  out may not overlap w. */
+int r9vx_router_repack_launch(const float *w, uint32_t e, uint32_t dm, float *out, r9vx_stream_t stream);
+
+int r9vx_moe_route_hidden_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_hidden_args *args,
+                                 r9vx_stream_t stream);
+/* Workspace of r9vx_moe_route_hidden_launch: the [t_bucket, E] f32 logits and
+ * a completion counter. */
+size_t r9vx_moe_route_hidden_workspace_bytes(const r9vx_moe_route_static *st);
+
 /* ----------------------------------------------------------------- moe_ffn */
 
 /* MoeFfnStatic (crates/r9v-registry/src/types.rs:828-860). */

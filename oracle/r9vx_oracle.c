@@ -284,6 +284,21 @@ int rxo_matmul(int scheme, const uint8_t *w, uint32_t n, uint32_t k, int x_dtype
     return rc;
 }
 
+/* Router logits x . w^T for an f32 weight [e, dm] and bf16 x [t, dm]: Branch
+ * D's loop order (crates/r9v-t0/src/matmul.rs:1940-2414 -- one f32
+ * accumulator per output, k ascending, prod = x*w rounded, then acc += prod). */
+void rxo_router_logits(const uint16_t *x, const float *w, uint32_t t, uint32_t e, uint32_t dm, float *out) {
+    for (uint32_t r = 0; r < t; ++r)
+        for (uint32_t c = 0; c < e; ++c) {
+            float acc = 0.0f;
+            for (uint32_t k = 0; k < dm; ++k) {
+                float prod = rxo_bf16_to_f32(x[(uint64_t)r * dm + k]) * w[(uint64_t)c * dm + k];
+                acc += prod;
+            }
+            out[(uint64_t)r * e + c] = acc;
+        }
+}
+
 /* act_mul with SiLU: crates/r9v-t0/src/act_mul.rs:86-99 (y = act(g) * u, no
  * clamp) with activation.rs:135-138 (silu(x) = x / (1 + exp(-x)), f32 exp =
  * the host expf). */

@@ -79,6 +79,8 @@ int rxo_matmul(int scheme, const uint8_t *w, uint32_t n, uint32_t k,
                const float *bias, const float *residual,
                int y_dtype, void *y);
 
+/* Router logits [t, e] = bf16 x [t, dm] . f32 w [e, dm]^T in Branch D order. */
+void rxo_router_logits(const uint16_t *x, const float *w, uint32_t t, uint32_t e, uint32_t dm, float *out);
 /* act_mul with SiLU (crates/r9v-t0/src/act_mul.rs:86-99): y = silu(g) * u. */
 void rxo_act_mul_silu(const float *g, const float *u, uint64_t n, float *y);
 

@@ -311,6 +311,80 @@ int r9vx_moe_route_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_
     return hip_status("moe_route", r9vx_launch_route(p, reinterpret_cast<hipStream_t>(stream)));
 }
 
+static void check_route_static(const r9vx_moe_route_static *st, uint32_t t, Problems &pr, float &scale) {
+    memcpy(&scale, &st->scale_bits, 4);
+    if (st->top_k == 0) pr.add(R9VX_ERR_INVALID, "top_k must be > 0");
+    if (!(scale > 0.0f) || !(scale < __builtin_huge_valf()))
+        pr.add(R9VX_ERR_INVALID, "scale must be finite and > 0, got %g", (double)scale);
+    if (st->n_group != 0) pr.add(R9VX_ERR_UNSUPPORTED, "grouped expert routing is not implemented");
+    if (t == 0 || st->e_total == 0) pr.add(R9VX_ERR_INVALID, "T=%u and E=%u must be > 0", t, st->e_total);
+    if (st->top_k > st->e_total) pr.add(R9VX_ERR_INVALID, "top_k %u cannot exceed number of experts E=%u", st->top_k, st->e_total);
+    if (st->e_total > 1024) pr.add(R9VX_ERR_UNSUPPORTED, "E=%u exceeds 1024", st->e_total);
+    if (st->top_k > 32) pr.add(R9VX_ERR_UNSUPPORTED, "top_k=%u exceeds 32", st->top_k);
+    if (st->scoring > R9VX_SCORING_SIGMOID) pr.add(R9VX_ERR_UNSUPPORTED, "scoring %u", st->scoring);
+    if (t > st->t_bucket) pr.add(R9VX_ERR_INVALID, "t=%u exceeds t_bucket=%u", t, st->t_bucket);
+}
+
+size_t r9vx_moe_route_hidden_workspace_bytes(const r9vx_moe_route_static *st) {
+    if (!st) return 0;
+    return (((size_t)st->t_bucket * st->e_total * 4 + 255) & ~(size_t)255) + 256;
+}
+
+int r9vx_moe_route_hidden_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_hidden_args *a,
+                                 r9vx_stream_t stream) {
+    Problems pr;
+    if (!st || !a) {
+        pr.add(R9VX_ERR_NULL, "static and args must be non-NULL");
+        return pr.finish("moe_route_hidden");
+    }
+    float scale;
+    check_route_static(st, a->t, pr, scale);
+    if (a->t > 8) pr.add(R9VX_ERR_UNSUPPORTED, "t=%u: the fused router is the decode form (t <= 8)", a->t);
+    if (a->dm == 0 || a->dm % 128 || a->dm > 8192)
+        pr.add(R9VX_ERR_INVALID, "dm=%u must be a positive multiple of 128, at most 8192", a->dm);
+    if (!a->x || !a->w_router || !a->expert_ids || !a->weights)
+        pr.add(R9VX_ERR_NULL, "x, w_router, expert_ids and weights are required");
+    if (!a->workspace) pr.add(R9VX_ERR_WORKSPACE, "workspace of r9vx_moe_route_hidden_workspace_bytes required");
+    if (st->has_bias && !a->bias) pr.add(R9VX_ERR_NULL, "has_bias set but bias is NULL");
+    if (!st->has_bias && a->bias) pr.add(R9VX_ERR_INVALID, "bias given but has_bias is 0");
+    if ((a->x && ((uintptr_t)a->x & 7u)) || (a->w_router && !aligned16(a->w_router)) ||
+        (a->workspace && ((uintptr_t)a->workspace & 255u)))
+        pr.add(R9VX_ERR_ALIGN, "x 8-byte, w_router 16-byte and workspace 256-byte aligned");
+    int rc = pr.finish("moe_route_hidden");
+    if (rc) return rc;
+    const size_t logit_bytes = ((size_t)st->t_bucket * st->e_total * 4 + 255) & ~(size_t)255;
+    r9vx_route_hidden_problem p{};
+    p.x = reinterpret_cast<const uint16_t *>(a->x);
+    p.w = a->w_router;
+    p.bias = a->bias;
+    p.logits = reinterpret_cast<float *>(a->workspace);
+    p.counter = reinterpret_cast<uint32_t *>(a->workspace + logit_bytes);
+    p.ids = a->expert_ids;
+    p.weights = a->weights;
+    p.t = a->t;
+    p.e = st->e_total;
+    p.k = st->top_k;
+    p.dm = a->dm;
+    p.scoring = st->scoring;
+    p.renormalize = st->renormalize ? 1u : 0u;
+    p.scale = scale;
+    return hip_status("moe_route_hidden", r9vx_launch_route_hidden(p, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int r9vx_router_repack_launch(const float *w, uint32_t e, uint32_t dm, float *out, r9vx_stream_t stream) {
+    Problems pr;
+    if (e == 0 || dm == 0 || dm % 4) pr.add(R9VX_ERR_INVALID, "E=%u > 0 and dm=%u a positive multiple of 4", e, dm);
+    if (!w || !out) pr.add(R9VX_ERR_NULL, "w and out are required");
+    if ((w && !aligned16(w)) || (out && !aligned16(out))) pr.add(R9VX_ERR_ALIGN, "w and out must be 16-byte aligned");
+    if (w && out) {
+        const uintptr_t a0 = (uintptr_t)w, a1 = a0 + (uint64_t)e * dm * 4, b0 = (uintptr_t)out, b1 = b0 + (uint64_t)e * dm * 4;
+        if (a0 < b1 && b0 < a1) pr.add(R9VX_ERR_INVALID, "w and out must not overlap");
+    }
+    int rc = pr.finish("router_repack");
+    if (rc) return rc;
+    return hip_status("router_repack", r9vx_launch_router_repack(w, e, dm, out, reinterpret_cast<hipStream_t>(stream)));
+}
+
 int r9vx_moe_route_status(uint32_t *status, r9vx_stream_t stream) {
     if (!status) {
         g_last_error = "moe_route_status: status is NULL";

@@ -95,6 +95,20 @@ struct r9vx_route_problem {
     float scale;
 };
 int r9vx_launch_route(const r9vx_route_problem &p, hipStream_t stream);
+
+struct r9vx_route_hidden_problem {
+    const uint16_t *x; /* bf16 [t, dm] */
+    const float *w;    /* f32 [e, dm] */
+    const float *bias;
+    float *logits;     /* workspace [t, e] */
+    uint32_t *counter; /* workspace word, zero between launches */
+    uint32_t *ids;
+    float *weights;
+    uint32_t t, e, k, dm, scoring, renormalize;
+    float scale;
+};
+int r9vx_launch_route_hidden(const r9vx_route_hidden_problem &p, hipStream_t stream);
+int r9vx_launch_router_repack(const float *w, uint32_t e, uint32_t dm, float *out, hipStream_t stream);
 int r9vx_read_route_status(uint32_t *status, hipStream_t stream);
 
 struct r9vx_moe_problem {

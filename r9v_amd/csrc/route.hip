@@ -151,14 +151,21 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
 /* Lane `lane` holds s[c] for c = lane + 64 i (i < PER, E <= 64 PER); -inf
  * past E.  The loads are unconditional (clamped column) so that all of them
  * are in flight at once; the bias branch is uniform. */
-template <int PER>
+/* Device-coherent load (agent scope, past this CU's L1): the fused router
+ * reads logits that other workgroups wrote. */
+__device__ __forceinline__ float ld_coherent(const float *p) {
+    return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<uint32_t *>(const_cast<float *>(p)),
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+template <int PER, bool COH = false>
 __device__ __forceinline__ void load_row(const RouteArgs &a, uint32_t row, uint32_t lane, float (&sc)[PER],
                                          float (&lg)[PER], float (&bs)[PER]) {
     const float *lrow = a.logits + (uint64_t)row * a.e;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const uint32_t c = lane + 64 * i;
-        lg[i] = lrow[c < a.e ? c : a.e - 1];
+        lg[i] = COH ? ld_coherent(lrow + (c < a.e ? c : a.e - 1)) : lrow[c < a.e ? c : a.e - 1];
     }
     if (a.bias) {
 #pragma unroll
@@ -334,7 +341,182 @@ __global__ __launch_bounds__(512) void route_small_kernel(RouteArgs a) {
     }
 }
 
+/* Routing from hidden states, t <= 8: the router logits x . w_r^T and
+ * moe_route in one launch, with every logit accumulated in T0's order (one
+ * f32 accumulator, k ascending, each product rounded before it is added:
+ * crates/r9v-t0/src/matmul.rs:1940-2414; the library is built with
+ * -ffp-contract=off), so the ids and weights equal T0's matmul followed by
+ * moe_route bit for bit.  A logit is a sequential sum over K, so the
+ * parallelism is one lane per (expert, token): workgroup (bx, t) has its
+ * first wave compute experts 64bx .. 64bx+63 of token t.  The router weight
+ * is in the k4-interleaved device layout [dm/4][E][4] (r9vx_router_repack),
+ * so the 16-byte loads of a wave (4 consecutive K values of 64 consecutive
+ * experts) read 1 KiB contiguous, one stage of 32 K values ahead, and x is
+ * staged once as f32 in LDS (broadcast reads).  A logit's adds are a
+ * dependent chain -- measured 5.45 ns per K value on MI355X (multiply and
+ * dependent add), so 11 us per 2048 values whatever the memory system does;
+ * deeper weight prefetch (a four-stage ring) measured slower.
+ * The last workgroup to finish (a counter in the caller's workspace, left at
+ * zero again) routes the whole batch with all four waves and the batch-level
+ * refusal of route_small_kernel. */
+struct RouteHiddenArgs {
+    const uint16_t *x; /* bf16 [t, dm] */
+    const float *w;    /* f32 [e, dm] */
+    uint32_t *counter; /* workspace word, zero between launches */
+    uint32_t dm;       /* a multiple of 64 */
+    RouteArgs r;       /* r.logits: the workspace logits [t, e] */
+};
+
+constexpr int kRhStage = 8; /* 16-byte weight loads (32 K values) per stage */
+
+/* x values of one stage: f32 read from the token's row in LDS (the same
+ * address in every lane: a broadcast read). */
+struct RhX {
+    r9vx_f32x4 v[kRhStage];
+};
+
+__device__ __forceinline__ void rh_load_x(RhX &x, const float *xs) {
+#pragma unroll
+    for (int i = 0; i < kRhStage; ++i) x.v[i] = *reinterpret_cast<const r9vx_f32x4 *>(xs + 4 * i);
+}
+
+__device__ __forceinline__ float rh_stage(float acc, const r9vx_f32x4 (&w)[kRhStage], const RhX &x) {
+#pragma unroll
+    for (int i = 0; i < kRhStage; ++i) {
+        acc = acc + x.v[i].x * w[i].x;
+        acc = acc + x.v[i].y * w[i].y;
+        acc = acc + x.v[i].z * w[i].z;
+        acc = acc + x.v[i].w * w[i].w;
+    }
+    return acc;
+}
+
+/* Stage loads: slab j of the k4 layout holds K values 4j .. 4j+3 of every
+ * expert, 4 E floats per slab. */
+__device__ __forceinline__ void rh_load(r9vx_f32x4 (&w)[kRhStage], const float *wr, uint64_t slab_floats) {
+#pragma unroll
+    for (int i = 0; i < kRhStage; ++i) w[i] = *reinterpret_cast<const r9vx_f32x4 *>(wr + slab_floats * i);
+}
+
+constexpr uint32_t kRhMaxDm = 8192; /* x row staged in LDS as f32 */
+
+template <int PER>
+__global__ __launch_bounds__(256) void route_hidden_kernel(RouteHiddenArgs a) {
+    __shared__ __attribute__((aligned(16))) float xs[kRhMaxDm];
+    __shared__ uint32_t is_last, bad_all;
+    __shared__ uint64_t etab[R9VX_EXP2F_N];
+    __shared__ __attribute__((aligned(16))) float sbuf[4][PER * 64];
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t E = a.r.e, T = a.r.t;
+    if (wv == 0) {
+        const uint32_t e = blockIdx.x * 64 + lane, tok = blockIdx.y;
+        const uint64_t slab = 4ull * E; /* floats per 4-K slab */
+        const float *wr = a.w + 4ull * (e < E ? e : E - 1);
+        r9vx_f32x4 wa[kRhStage], wb[kRhStage];
+        rh_load(wa, wr, slab);
+        /* the token's x row -> LDS as f32 (exact), while the first weights load */
+        const uint16_t *xr = a.x + (uint64_t)tok * a.dm;
+        for (uint32_t k = 4 * lane; k < a.dm; k += 256) {
+            const r9vx_u32x2 xb = *reinterpret_cast<const r9vx_u32x2 *>(xr + k);
+            *reinterpret_cast<r9vx_f32x4 *>(xs + k) =
+                r9vx_f32x4{__builtin_bit_cast(float, xb.x << 16), __builtin_bit_cast(float, xb.x & 0xFFFF0000u),
+                           __builtin_bit_cast(float, xb.y << 16), __builtin_bit_cast(float, xb.y & 0xFFFF0000u)};
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float acc = 0.0f;
+        RhX xa, xb;
+        rh_load_x(xa, xs);
+        for (uint32_t k = 0; k < a.dm; k += 64) {
+            rh_load(wb, wr + slab * ((k + 32) / 4), slab);
+            rh_load_x(xb, xs + k + 32);
+            acc = rh_stage(acc, wa, xa);
+            if (k + 64 < a.dm) {
+                rh_load(wa, wr + slab * ((k + 64) / 4), slab);
+                rh_load_x(xa, xs + k + 64);
+            }
+            acc = rh_stage(acc, wb, xb);
+        }
+        if (e < E) const_cast<float *>(a.r.logits)[(uint64_t)tok * E + e] = acc;
+    }
+    __threadfence(); /* this workgroup's logits are visible device-wide before it is counted */
+    __syncthreads();
+    if (threadIdx.x == 0) is_last = atomicAdd(a.counter, 1u) == gridDim.x * gridDim.y - 1;
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    r9vx_exp2_fill(etab, threadIdx.x, blockDim.x);
+    if (threadIdx.x == 0) bad_all = 0;
+    __syncthreads();
+    uint32_t id[2] = {0, 0};
+    float w[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t row = wv + 4 * j;
+        if (row >= T) continue;
+        float sc[PER], lg[PER], bs[PER];
+        load_row<PER, true>(a.r, row, lane, sc, lg, bs);
+        const uint32_t bad_row = check_loaded<PER>(a.r, lane, sc, lg, bs, etab);
+        uint32_t bad = 0;
+        if (__ballot(bad_row & R9VX_STATUS_NONFINITE)) bad |= R9VX_STATUS_NONFINITE;
+        if (__ballot(bad_row & R9VX_STATUS_DEGENERATE)) bad |= R9VX_STATUS_DEGENERATE;
+        if (bad && lane == 0) atomicOr(&bad_all, bad);
+        if (!bad) route_loaded<PER>(a.r, lane, sc, etab, sbuf[wv], id[j], w[j]);
+    }
+    __syncthreads();
+    const uint32_t bad = bad_all;
+    if (threadIdx.x == 0) {
+        g_route_status = bad;
+        atomicExch(a.counter, 0u);
+    }
+    if (bad) return;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t row = wv + 4 * j;
+        if (row < T && lane < a.r.k) {
+            a.r.ids[(uint64_t)row * a.r.k + lane] = id[j];
+            a.r.weights[(uint64_t)row * a.r.k + lane] = w[j];
+        }
+    }
+}
+
 }  // namespace
+
+/* [E, dm] -> k4-interleaved [dm/4][E][4]: thread per (slab, expert). */
+__global__ __launch_bounds__(256) void router_repack_kernel(const float *__restrict__ w, uint32_t e, uint32_t dm,
+                                                            float *__restrict__ out) {
+    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (uint64_t)e * (dm / 4)) return;
+    const uint32_t ex = (uint32_t)(gid % e), j = (uint32_t)(gid / e);
+    *reinterpret_cast<r9vx_f32x4 *>(out + 4 * gid) =
+        *reinterpret_cast<const r9vx_f32x4 *>(w + (uint64_t)ex * dm + 4 * j);
+}
+
+int r9vx_launch_router_repack(const float *w, uint32_t e, uint32_t dm, float *out, hipStream_t stream) {
+    const uint64_t n = (uint64_t)e * (dm / 4);
+    hipLaunchKernelGGL(router_repack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, w, e, dm, out);
+    return (int)hipGetLastError();
+}
+
+int r9vx_launch_route_hidden(const r9vx_route_hidden_problem &p, hipStream_t stream) {
+    RouteHiddenArgs a{p.x, p.w, p.counter, p.dm,
+                      RouteArgs{p.logits, p.bias, p.ids, p.weights, p.t, p.e, p.k, p.scoring, p.renormalize, p.scale}};
+    const dim3 grid((p.e + 63) / 64, p.t);
+    const uint32_t per = (p.e + 63) / 64;
+    if (per <= 1)
+        hipLaunchKernelGGL((route_hidden_kernel<1>), grid, dim3(256), 0, stream, a);
+    else if (per <= 2)
+        hipLaunchKernelGGL((route_hidden_kernel<2>), grid, dim3(256), 0, stream, a);
+    else if (per <= 4)
+        hipLaunchKernelGGL((route_hidden_kernel<4>), grid, dim3(256), 0, stream, a);
+    else if (per <= 8)
+        hipLaunchKernelGGL((route_hidden_kernel<8>), grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((route_hidden_kernel<16>), grid, dim3(256), 0, stream, a);
+    return (int)hipGetLastError();
+}
 
 template <int PER>
 static int launch_route_per(const RouteArgs &a, hipStream_t stream) {

@@ -56,6 +56,11 @@ class MoeRouteArgs(ctypes.Structure):
                 ("_tail_pad", _U32)]
 
 
+class MoeRouteHiddenArgs(ctypes.Structure):
+    _fields_ = [("x", _P), ("w_router", _P), ("bias", _P), ("expert_ids", _P), ("weights", _P),
+                ("workspace", _P), ("t", _U32), ("dm", _U32)]
+
+
 class MoeFfnStatic(ctypes.Structure):
     _fields_ = [("t_bucket", _U32), ("e_local", _U32), ("k_topk", _U32), ("dm", _U32),
                 ("dff", _U32), ("gate_up_scheme", _U32), ("down_scheme", _U32),
@@ -78,6 +83,9 @@ EXPORTS = [
     ("r9vx_moe_route_launch", [_P, _P, _P], ctypes.c_int),
     ("r9vx_moe_route_status", [_P, _P], ctypes.c_int),
     ("r9vx_moe_route_static_bytes", [_P, _U32], ctypes.c_uint64),
+    ("r9vx_moe_route_hidden_launch", [_P, _P, _P], ctypes.c_int),
+    ("r9vx_moe_route_hidden_workspace_bytes", [_P], ctypes.c_size_t),
+    ("r9vx_router_repack_launch", [_P, _U32, _U32, _P, _P], ctypes.c_int),
     ("r9vx_moe_ffn_launch", [_P, _P, _P], ctypes.c_int),
     ("r9vx_moe_ffn_workspace_bytes", [_P], ctypes.c_size_t),
     ("r9vx_moe_ffn_status", [_P, _P, _P, _P], ctypes.c_int),
@@ -273,6 +281,39 @@ def moe_route(logits, k, bias=None, scoring=SCORING_SOFTMAX, renormalize=True, s
     args = MoeRouteArgs(_ptr(logits), _ptr(bias), _ptr(ids), _ptr(weights), t, 0)
     _check(load().r9vx_moe_route_launch(ctypes.byref(st), ctypes.byref(args), _stream(torch, stream)))
     return ids, weights
+
+
+def router_repack(w, stream=None):
+    """f32 router weight [E, dm] -> the k4-interleaved device layout [dm/4][E][4]."""
+    torch = _need_gpu(w)
+    e, dm = w.shape
+    out = torch.empty(e * dm, dtype=torch.float32, device=w.device)
+    _check(load().r9vx_router_repack_launch(_ptr(w), e, dm, _ptr(out), _stream(torch, stream)))
+    return out
+
+
+def moe_route_hidden(x, w_router, k, bias=None, scoring=SCORING_SOFTMAX, renormalize=True, scale=1.0,
+                     ids=None, weights=None, workspace=None, t_bucket=None, stream=None, e=None):
+    """Routing from bf16 hidden states x [t, dm] and an f32 router weight
+    (in the layout of `router_repack`; pass e= its expert count) in one
+    launch (t <= 8), bit-exact with T0's matmul + moe_route.
+    Returns (ids, weights, workspace); the workspace's first t*E floats are
+    the router logits.  A workspace passed in must have been zero-filled once."""
+    torch = _need_gpu(x, w_router, bias, ids, weights, workspace)
+    t, dm = x.shape
+    e = e if e is not None else w_router.numel() // dm
+    st = route_static(e, k, t_bucket or max(t, 1), scoring, renormalize, scale, bias is not None)
+    if workspace is None:
+        workspace = torch.zeros(int(load().r9vx_moe_route_hidden_workspace_bytes(ctypes.byref(st))),
+                                dtype=torch.uint8, device=x.device)
+    if ids is None:
+        ids = torch.empty((t, k), dtype=torch.int32, device=x.device)
+    if weights is None:
+        weights = torch.empty((t, k), dtype=torch.float32, device=x.device)
+    args = MoeRouteHiddenArgs(_ptr(x), _ptr(w_router), _ptr(bias), _ptr(ids), _ptr(weights), _ptr(workspace),
+                              t, dm)
+    _check(load().r9vx_moe_route_hidden_launch(ctypes.byref(st), ctypes.byref(args), _stream(torch, stream)))
+    return ids, weights, workspace
 
 
 def moe_route_status(stream=None) -> int:

@@ -439,3 +439,18 @@ def load_moe_experts(file: GgufFile, data, gate: str, up: str | None, down: str,
         if bad:
             raise GgufError(-1, f"{gate}/{down}: {bad} expert block(s) carry a non-finite scale")
     return st, w_gate_up, w_down
+
+
+def load_router_weight(file: GgufFile, data, name: str):
+    """(E, dm, device weight in the k4 layout of ffi.router_repack) for an F32
+    router tensor (ffn_gate_inp, file dims {dm, E}), for ffi.moe_route_hidden."""
+    import torch
+
+    info = file.tensor(name)
+    if info is None:
+        raise GgufError(-1, f"no tensor named {name!r}")
+    if info.dtype != 0 or len(info.dims) != 2:
+        raise GgufError(-2, f"{name}: the router weight must be a 2-D F32 tensor, got {info.type_name} {info.dims}")
+    dm, e = info.dims
+    raw = upload(file, data, name)
+    return e, dm, ffi.router_repack(raw.view(torch.float32).reshape(e, dm))

@@ -42,6 +42,8 @@ def lib():
         L.rxo_dequantize.argtypes = [I, P, U, U, P]
         L.rxo_matmul.argtypes = [I, P, U, U, I, P, U, P, P, I, P]
         L.rxo_matmul_mt.argtypes = [I, P, U, U, I, P, U, I, P, I]
+        L.rxo_router_logits.argtypes = [P, P, U, U, U, P]
+        L.rxo_router_logits.restype = None
         L.rxo_act_mul_silu.argtypes = [P, P, ctypes.c_uint64, P]
         L.rxo_act_mul_silu.restype = None
         L.rxo_moe_route.argtypes = [P, P, U, U, U, ctypes.c_float, I, I, P, P]
@@ -86,6 +88,16 @@ def matmul(scheme, w, n, k, x, x_dtype, y_dtype=F32, bias=None, residual=None, t
                               y_dtype, _p(y))
     _check(rc, "matmul")
     return y
+
+
+def router_logits(x_bf16, w):
+    x_bf16 = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    t, dm = x_bf16.shape
+    e = w.shape[0]
+    out = np.empty((t, e), dtype=np.float32)
+    lib().rxo_router_logits(_p(x_bf16), _p(w), t, e, dm, _p(out))
+    return out
 
 
 def act_mul_silu(g, u):

@@ -171,3 +171,16 @@ def test_swiglu_epilogue_refusals_and_figures():
                              epilogue=ffi.EPILOGUE_SWIGLU)
     assert ffi.matmul_static_bytes(good, 1) == 128 * 2 * 144 + 512 * 2 + 64 * 4  # 2n weight rows
     assert lib.r9vx_matmul_static_flops(ctypes.byref(good), 3) == 4 * 3 * 64 * 512
+
+
+def test_route_hidden_refusals():
+    lib = ffi.load()
+    st = ffi.route_static(e=512, k=10, t_bucket=16)
+    args = ffi.MoeRouteHiddenArgs()
+    args.t = 12
+    args.dm = 100
+    assert _call(lib.r9vx_moe_route_hidden_launch, st, args) < 0
+    msg = lib.r9vx_last_error().decode()
+    for part in ("decode form (t <= 8)", "dm=100", "x, w_router", "workspace of"):
+        assert part in msg, msg
+    assert lib.r9vx_moe_route_hidden_workspace_bytes(ctypes.byref(st)) == 16 * 512 * 4 + 256

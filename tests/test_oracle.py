@@ -466,3 +466,20 @@ def test_act_mul_silu_against_f64():
     want = g64 / (1.0 + np.exp(-g64)) * u64
     assert np.all(np.abs(got - want) <= 4 * np.finfo(np.float32).eps * np.abs(want) + 1e-37)
     assert got[g.size - 7] == 0.0 and got[g.size - 6] == 0.0
+
+
+def test_router_logits_sequential_order():
+    """The router-logit oracle is T0's loop: a numpy restatement that walks k
+    in ascending order with f32 mul-then-add agrees bit for bit, and an f64
+    dot agrees to rounding."""
+    t, e, dm = 3, 70, 256
+    x = synth.normal_bf16(11, (t, dm))
+    w = synth.normal_f32(12, (e, dm), 0.05)
+    got = O.router_logits(x, w)
+    xf = synth.bf16_bits_to_f32(x)
+    acc = np.zeros((t, e), dtype=np.float32)
+    for k in range(dm):
+        acc = (acc + (xf[:, k:k + 1] * w[None, :, k]).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), acc.view(np.uint32))
+    ref = xf.astype(np.float64) @ w.astype(np.float64).T
+    assert np.max(np.abs(got - ref)) <= 1e-4 * np.max(np.abs(ref))
