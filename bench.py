@@ -46,7 +46,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list of extras: c0,c1m1,c2,c3,c4,ceilings")
+    ap.add_argument("--only", default="",
+                    help="comma list of extras: c0,c1m1,c2,c3,c4,ceilings; 'paths' (not run by default) times "
+                         "the Q6_K / Q8_0, SwiGLU and fused-router paths")
     ap.add_argument("--pmc-case", default="", help="run a short fixed workload for counter collection: c1m5")
     ap.add_argument("--pmc-summary", nargs="*", default=None,
                     help="rocprofv3 --pmc output dirs (FETCH_SIZE, WRITE_SIZE) to summarise as traffic")
@@ -278,6 +280,74 @@ def bench_c4(torch, ffi, synth, gsynth, steps):
     return out
 
 
+def bench_paths(torch, ffi, synth):
+    """The paths beyond configs[0..4], timed at their documented shapes (run
+    with --only paths; not part of the default run): Q6_K / Q8_0 decode GEMVs
+    and prefill GEMMs on the split layout, the gated (SwiGLU) GEMV over
+    stacked gate/up rows, and routing from hidden states."""
+    out = {}
+
+    def weights(scheme, rows, k, seed, copies):
+        wire = torch.from_numpy(synth.quant_weights(scheme, seed, rows, k)).cuda()
+        if scheme in ffi.SPLIT_SCHEMES:
+            body, scales = ffi.repack(wire, scheme, rows, k)
+            return [(body, scales)] + [(body.clone(), scales.clone()) for _ in range(copies - 1)]
+        return [(wire, None)] + [(wire.clone(), None) for _ in range(copies - 1)]
+
+    def wbytes(scheme, rows, k):
+        return rows * (k // ffi.BLOCK_LEN[scheme]) * ffi.BLOCK_BYTES[scheme]
+
+    for name, scheme, n, k, m in (("q6k_head_gemv", ffi.Q6_K, 32768, 4096, 1),
+                                  ("q8_0_proj_gemv", ffi.Q8_0, 14336, 4096, 1),
+                                  ("q6k_gemv_c1shape", ffi.Q6_K, 5120, 2048, 1)):
+        nb = wbytes(scheme, n, k)
+        ws = weights(scheme, n, k, 11, copies_for(nb))
+        x = torch.from_numpy(synth.normal_bf16(3, (m, k)).view(np.int16)).cuda().view(torch.bfloat16)
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        ms = graph_time(torch, lambda i, s: ffi.matmul(ws[i % len(ws)][0], scheme, n, k, x, y=y, stream=s,
+                                                       w_scales=ws[i % len(ws)][1]), len(ws))
+        out[name] = {"n": n, "k": k, "m": m, "us_per_launch": round(ms * 1e3, 2), **hbm(nb, ms)}
+        log(f"  {name} {out[name]}")
+        del ws
+        torch.cuda.empty_cache()
+    for mm in (1, 4):
+        n, k = 14336, 4096
+        nb = wbytes(ffi.Q4_K, 2 * n, k)
+        ws = weights(ffi.Q4_K, 2 * n, k, 12, copies_for(nb))
+        x = torch.from_numpy(synth.normal_bf16(4, (mm, k)).view(np.int16)).cuda().view(torch.bfloat16)
+        y = torch.empty((mm, n), dtype=torch.float32, device="cuda")
+        ms = graph_time(torch, lambda i, s: ffi.matmul(ws[i % len(ws)][0], ffi.Q4_K, n, k, x, y=y, stream=s,
+                                                       swiglu=True), len(ws))
+        out[f"swiglu_gemv_m{mm}"] = {"dff": n, "k": k, "m": mm, "us_per_launch": round(ms * 1e3, 2), **hbm(nb, ms)}
+        log(f"  swiglu m{mm} {out[f'swiglu_gemv_m{mm}']}")
+        del ws
+        torch.cuda.empty_cache()
+    for name, scheme in (("q6k_prefill_gemm", ffi.Q6_K), ("q8_0_prefill_gemm", ffi.Q8_0)):
+        m, n, k = 2048, 14336, 4096
+        (w, sc), = weights(scheme, n, k, 13, 1)
+        x = torch.from_numpy(synth.normal_bf16(5, (m, k)).view(np.int16)).cuda().view(torch.bfloat16)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+        st = ffi.matmul_static(n, k, scheme, ffi.BF16, ffi.BF16, m_bucket=m)
+        wsp = torch.empty(ffi.matmul_workspace_bytes(st), dtype=torch.uint8, device="cuda")
+        ms = event_time(torch, lambda: ffi.matmul(w, scheme, n, k, x, out_dtype=ffi.BF16, y=y, workspace=wsp,
+                                                  w_scales=sc), 10, 3)
+        out[name] = {"m": m, "n": n, "k": k, "ms": round(ms, 4), **mfma(2 * m * n * k, ms)}
+        log(f"  {name} {out[name]}")
+        del w, sc
+        torch.cuda.empty_cache()
+    t, e, dm, kk = 5, 512, 2048, 10
+    x = torch.from_numpy(synth.normal_bf16(6, (t, dm)).view(np.int16)).cuda().view(torch.bfloat16)
+    wr = ffi.router_repack(torch.from_numpy(synth.normal_f32(7, (e, dm), 0.05)).cuda())
+    ids = torch.empty((t, kk), dtype=torch.int32, device="cuda")
+    wt = torch.empty((t, kk), dtype=torch.float32, device="cuda")
+    _, _, rws = ffi.moe_route_hidden(x, wr, kk, ids=ids, weights=wt, e=e)
+    ms = graph_time(torch, lambda i, s: ffi.moe_route_hidden(x, wr, kk, ids=ids, weights=wt, workspace=rws, e=e,
+                                                            stream=s), 50)
+    out["route_hidden_t5"] = {"t": t, "e": e, "dm": dm, "k": kk, "us_per_launch": round(ms * 1e3, 2)}
+    log(f"  route_hidden {out['route_hidden_t5']}")
+    return out
+
+
 def bench_ceilings(torch, ffi):
     """Measured ceilings of this device: 128-bit streaming reads at the
     configs' working-set sizes (rotated copies, graph-replayed launches) and
@@ -408,6 +478,8 @@ def main():
     only = set(filter(None, args.only.split(",")))
 
     def want(name):
+        if name == "paths":  # only when asked for
+            return name in only
         return not only or name in only
 
     log("c1 m5: IQ4_XS GEMV K=2048 N=5120 M=5")
@@ -431,6 +503,9 @@ def main():
     if want("ceilings"):
         extras["measured_ceilings"] = bench_ceilings(torch, ffi)
         log(f"  ceilings {extras['measured_ceilings']}")
+    if want("paths"):
+        log("other paths ...")
+        extras["paths"] = bench_paths(torch, ffi, synth)
     for name, fn, st in (("c2", bench_c2, 20), ("c3", bench_c3, 200), ("c4", bench_c4, 10)):
         if want(name):
             log(f"{name} ...")
