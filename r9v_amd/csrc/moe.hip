@@ -154,6 +154,66 @@ __global__ __launch_bounds__(1024) void sort_small_kernel(SortArgs a) {
     }
 }
 
+/* P <= 64 pairs (decode): the same outputs from one wave.  Pair p is lane
+ * p, so a lane's rank among its expert's peers is its stable (token, slot)
+ * rank; expert counts go through a 4-KiB LDS table, and lane l owns experts
+ * l*per .. l*per+per-1 for the ascending exclusive scans of the offsets and
+ * of the active-expert work list. */
+__global__ __launch_bounds__(64) void sort_tiny_kernel(SortArgs a) {
+    __shared__ uint32_t cnt[kMoeMaxE];
+    const MoeLayout &L = a.L;
+    const uint32_t lane = threadIdx.x;
+    for (uint32_t i = lane; i < a.e; i += 64) cnt[i] = 0;
+    const bool in = lane < a.p;
+    const uint32_t id = in ? a.ids[lane] : 0u;
+    const bool valid = in && id < a.e;
+    const bool bad = __ballot(in && !valid) != 0ull;
+    const uint64_t peers = match_peers(id, valid, id_bits(a.e));
+    const uint32_t rw = rank_below(peers, lane);
+    __syncthreads();
+    if (valid && rw == 0) cnt[id] = (uint32_t)__popcll(peers);
+    __syncthreads();
+    const uint32_t per = (a.e + 63) / 64, e0 = lane * per;
+    uint32_t mine = 0, act_mine = 0;
+    for (uint32_t j = 0; j < per; ++j)
+        if (e0 + j < a.e) {
+            mine += cnt[e0 + j];
+            act_mine += cnt[e0 + j] ? 1u : 0u;
+        }
+    const uint32_t incl = wave_incl_scan(mine, lane), act_incl = wave_incl_scan(act_mine, lane);
+    const uint32_t all = __shfl(incl, 63, 64), n_act = __shfl(act_incl, 63, 64);
+    uint32_t *counts = reinterpret_cast<uint32_t *>(a.ws + L.counts);
+    uint32_t *offsets = reinterpret_cast<uint32_t *>(a.ws + L.offsets);
+    uint32_t *status = reinterpret_cast<uint32_t *>(a.ws + L.status);
+    __syncthreads(); /* every lane has read its counts before the table turns into offsets */
+    uint32_t run = incl - mine, idx = act_incl - act_mine;
+    for (uint32_t j = 0; j < per; ++j) {
+        const uint32_t e = e0 + j;
+        if (e >= a.e) break;
+        const uint32_t c = cnt[e];
+        counts[e] = c;
+        offsets[e] = run;
+        cnt[e] = run;
+        if (c) put_work(L, a.ws, idx++, e, run, c);
+        run += c;
+    }
+    if (lane == 0) offsets[a.e] = all;
+    __syncthreads();
+    uint32_t *pinfo = reinterpret_cast<uint32_t *>(a.ws + L.pinfo);
+    if (valid) {
+        const uint32_t pos = cnt[id] + rw;
+        reinterpret_cast<uint32_t *>(a.ws + L.sorted)[pos] = lane;
+        reinterpret_cast<uint32_t *>(a.ws + L.inv)[lane] = pos;
+        if (!bad) pinfo[pos] = (id << 16) | (lane / a.k);
+    }
+    if (bad && in) pinfo[lane] = ~0u; /* refused: no position is valid */
+    for (uint32_t s2 = lane; s2 < a.shared; s2 += 64) put_work(L, a.ws, n_act + s2, a.e + s2, a.p + s2 * a.t, a.t);
+    if (lane == 0) {
+        status[0] = bad ? R9VX_STATUS_BAD_EXPERT : 0u;
+        status[2] = n_act + a.shared;
+    }
+}
+
 /* ---------------------------------------------------------------- sort: large */
 
 __global__ void sort_prep_kernel(uint8_t *ws, MoeLayout L) {
@@ -656,6 +716,10 @@ static uint32_t lpr_for(uint32_t k, uint32_t &nseg) {
 
 int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s) {
     SortArgs a{p.ids, p.ws, L, p.t * p.k, p.e, p.k, p.t, p.shared};
+    if (a.p <= 64) {
+        hipLaunchKernelGGL(sort_tiny_kernel, dim3(1), dim3(64), 0, s, a);
+        return (int)hipGetLastError();
+    }
     if (a.p <= 1024) {
         hipLaunchKernelGGL(sort_small_kernel, dim3(1), dim3(1024), 0, s, a);
         return (int)hipGetLastError();

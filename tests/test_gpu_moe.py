@@ -149,7 +149,8 @@ def test_route_host_refusals():
 
 # ---------------------------------------------------------------- permute
 
-@pytest.mark.parametrize("t,e,k", [(5, 512, 10), (8192, 512, 10), (1, 4, 2), (103, 1024, 32), (3000, 7, 3)])
+@pytest.mark.parametrize("t,e,k", [(5, 512, 10), (8192, 512, 10), (1, 4, 2), (103, 1024, 32), (3000, 7, 3),
+                                   (2, 1024, 32), (7, 100, 9), (64, 3, 1), (13, 5, 5)])
 def test_sort_bit_exact(t, e, k):
     if e >= 64:
         logits = synth.zipf_logits(1000 + t + e, t, e)
