@@ -110,16 +110,6 @@ __device__ __forceinline__ void arrange_x(const XRaw<XF32> &r, XChunk<SCHEME, XF
         L[4] = r.v[1].x; L[5] = r.v[1].y; L[6] = r.v[1].z; L[7] = r.v[1].w;
         H[0] = r.v[2].x; H[1] = r.v[2].y; H[2] = r.v[2].z; H[3] = r.v[2].w;
         H[4] = r.v[3].x; H[5] = r.v[3].y; H[6] = r.v[3].z; H[7] = r.v[3].w;
-        if constexpr (SCHEME != R9VX_SCHEME_IQ4_XS) {
-            float slo = 0.f, shi = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                slo += __builtin_bit_cast(float, L[j] << 16) + __builtin_bit_cast(float, L[j] & 0xFFFF0000u);
-                shi += __builtin_bit_cast(float, H[j] << 16) + __builtin_bit_cast(float, H[j] & 0xFFFF0000u);
-            }
-            xc.slo = slo;
-            xc.shi = shi;
-        }
         if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
             /* pair i = {x_lo(i), x_hi(i)}: byte i's two nibbles */
 #pragma unroll
@@ -138,6 +128,20 @@ __device__ __forceinline__ void arrange_x(const XRaw<XF32> &r, XChunk<SCHEME, XF
                 xc.p[4 * d + 2] = (H[2 * d] & 0xFFFFu) | (H[2 * d + 1] << 16);
                 xc.p[4 * d + 3] = (H[2 * d] >> 16) | (H[2 * d + 1] & 0xFFFF0000u);
             }
+            /* sums of the 16 low- and 16 high-position activations (the
+             * min and 128-offset terms): dot products with the bf16 pair
+             * (1, 1), two activations per instruction */
+            constexpr uint32_t kOnes = 0x3F803F80u;
+            float slo = 0.f, shi = 0.f;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                slo = r9vx_dot2_bf16(xc.p[4 * d + 0], kOnes, slo);
+                slo = r9vx_dot2_bf16(xc.p[4 * d + 1], kOnes, slo);
+                shi = r9vx_dot2_bf16(xc.p[4 * d + 2], kOnes, shi);
+                shi = r9vx_dot2_bf16(xc.p[4 * d + 3], kOnes, shi);
+            }
+            xc.slo = slo;
+            xc.shi = shi;
         }
     }
 }
