@@ -323,16 +323,19 @@ uint32_t device_simds() {
 }
 
 /* Rows per lane group for the compile-time form at M >= 3: the R in 2..5 whose wave
- * count ceil(n / R) puts the fewest rows on the busiest SIMD,
- * ceil(waves / simds) * R; ties go to the larger R, which loads and
- * re-arranges the activations for more rows at once (at large n every R
- * ties).  At n = 5120 this is R = 5 (1024 waves, one per SIMD), measured
- * 5.28 us against 5.47 us for R = 3 at M = 5. */
-uint32_t balanced_rows(uint32_t n, uint32_t simds) {
+ * count ceil(n / R) gives the busiest SIMD the least work,
+ * ceil(waves / simds) * (R + x): from M >= 3 a wave's activation loads and
+ * re-arrangement cost about one row's dot products whatever R is (x = 1);
+ * for one or two rows they are small (x = 0).  Ties go to the larger R.
+ * At n = 5120 this is R = 5 (1024 waves, one per SIMD), measured 5.28 us
+ * against 5.47 us for R = 3 at M = 5; at n = 14336, M = 4 it is R = 5 where
+ * x = 0 took R = 2 (Q4_K, K = 4096: 25.1 -> 21.6 us), while M = 1 there
+ * keeps R = 2 (12.5 us against 13.4 at R = 5). */
+uint32_t balanced_rows(uint32_t n, uint32_t simds, uint32_t x) {
     uint32_t best = 2, best_cost = ~0u;
     for (uint32_t r = 2; r <= 5; ++r) {
         const uint32_t waves = (n + r - 1) / r;
-        const uint32_t cost = (waves + simds - 1) / simds * r;
+        const uint32_t cost = (waves + simds - 1) / simds * (r + x);
         if (cost <= best_cost) best = r, best_cost = cost;
     }
     return best;
@@ -362,7 +365,7 @@ int launch_one(const GemvArgs &a, uint32_t m, uint32_t rows_per_slot_group, hipS
              * (n = 20480, M = 1: 7.52 us at R = 4 against 8.05 at R = 2;
              * n = 51200: 15.0 against 16.6 us) */
             const uint32_t simds = device_simds();
-            switch (MM <= 2 && a.n < 8 * simds ? 2u : balanced_rows(a.n, simds)) {
+            switch (MM <= 2 && a.n < 8 * simds ? 2u : balanced_rows(a.n, simds, MM >= 3 ? 1u : 0u)) {
             case 2: return launch_rows<SCHEME, XF32, SPL, MM, 6, 2>(a, 1, s);
             case 3: return launch_rows<SCHEME, XF32, SPL, MM, 6, 3>(a, 1, s);
             case 4: return launch_rows<SCHEME, XF32, SPL, MM, 6, 4>(a, 1, s);
