@@ -60,10 +60,11 @@ using namespace r9vx;
 /* LPRL = 6: 64 lanes per row, a single K segment (K = 2048*SPL), f32 y and
  * no epilogue, all fixed at compile time (measured 0.4-0.6 us faster per
  * launch at configs[1] than the general form), and RR rows per lane group
- * chosen by the launcher to balance the waves over the SIMDs; LPRL = 0:
+ * chosen by the launcher to balance the waves over the SIMDs (NS = 0: the
+ * same with the K segment count read from the arguments); LPRL = 0:
  * lanes per row, segment count and epilogue come from the arguments and
  * the rows per lane group from rows_for(M). */
-template <int SCHEME, int M, bool XF32, int SPL, int LPRL, int RR>
+template <int SCHEME, int M, bool XF32, int SPL, int LPRL, int RR, int NS = 1>
 __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
     constexpr int kRows = RR ? RR : rows_for(M), kWaves = waves_for(M);
     __shared__ uint32_t lut[256];
@@ -82,7 +83,7 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int t = 0; t < M; ++t) acc[r][t] = 0.f;
 
-    const uint32_t nseg = LPRL ? 1u : a.nseg;
+    const uint32_t nseg = (LPRL && NS == 1) ? 1u : a.nseg;
     for (uint32_t seg = 0; seg < nseg; ++seg) {
         uint32_t cis[SPL];
 #pragma unroll
@@ -124,7 +125,7 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
         }
         /* 2. the codebook table is built while the loads are in flight */
         if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
-            if (LPRL != 0 || seg == 0) {
+            if ((LPRL != 0 && NS == 1) || seg == 0) {
                 build_iq4_lut(lut, threadIdx.x, blockDim.x);
                 __syncthreads();
             }
@@ -341,13 +342,13 @@ uint32_t balanced_rows(uint32_t n, uint32_t simds, uint32_t x) {
     return best;
 }
 
-template <int SCHEME, bool XF32, int SPL, int MM, int LPRL, int RR>
+template <int SCHEME, bool XF32, int SPL, int MM, int LPRL, int RR, int NS = 1>
 int launch_rows(const GemvArgs &a, uint32_t rows_per_slot_group, hipStream_t s) {
     /* rows_per_slot_group = lane groups per wave (64 / LPR) */
     const uint32_t rows_per_wave = rows_per_slot_group * (RR ? RR : rows_for(MM));
     const uint32_t waves = (a.n + rows_per_wave - 1) / rows_per_wave;
     const dim3 grid((waves + waves_for(MM) - 1) / waves_for(MM));
-    hipLaunchKernelGGL((gemv_kernel<SCHEME, MM, XF32, SPL, LPRL, RR>), grid, dim3(waves_for(MM) * 64), 0, s, a);
+    hipLaunchKernelGGL((gemv_kernel<SCHEME, MM, XF32, SPL, LPRL, RR, NS>), grid, dim3(waves_for(MM) * 64), 0, s, a);
     return (int)hipGetLastError();
 }
 
@@ -370,6 +371,20 @@ int launch_one(const GemvArgs &a, uint32_t m, uint32_t rows_per_slot_group, hipS
             case 3: return launch_rows<SCHEME, XF32, SPL, MM, 6, 3>(a, 1, s);
             case 4: return launch_rows<SCHEME, XF32, SPL, MM, 6, 4>(a, 1, s);
             default: return launch_rows<SCHEME, XF32, SPL, MM, 6, 5>(a, 1, s);
+            }
+        }
+        if constexpr (!XF32) {
+            /* several K segments of 64 lanes (K >= 8192, K = 14336, or
+             * K = 4096 at M >= 5): the same compile-time form with the
+             * segment count read at run time */
+            if (a.lpr_log2 == 6 && a.nseg > 1 && a.epilogue == R9VX_EPILOGUE_NONE && !a.y_bf16) {
+                const uint32_t simds = device_simds();
+                switch (MM <= 2 && a.n < 8 * simds ? 2u : balanced_rows(a.n, simds, MM >= 3 ? 1u : 0u)) {
+                case 2: return launch_rows<SCHEME, XF32, SPL, MM, 6, 2, 0>(a, 1, s);
+                case 3: return launch_rows<SCHEME, XF32, SPL, MM, 6, 3, 0>(a, 1, s);
+                case 4: return launch_rows<SCHEME, XF32, SPL, MM, 6, 4, 0>(a, 1, s);
+                default: return launch_rows<SCHEME, XF32, SPL, MM, 6, 5, 0>(a, 1, s);
+                }
             }
         }
         return launch_rows<SCHEME, XF32, SPL, MM, 0, 0>(a, rows_per_slot_group, s);

@@ -97,6 +97,19 @@ def test_gemv_k_and_n_sweep(scheme, x_dtype, m):
         check_close(got, ref, f"n={n} k={k} m={m}")
 
 
+@pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])
+@pytest.mark.parametrize("n,k,m", [(4096, 14336, 1), (2600, 14336, 4), (6000, 8192, 2), (9000, 8192, 5),
+                                   (14336, 4096, 8), (700, 4096, 6)])
+def test_gemv_multi_segment_rows(scheme, n, k, m):
+    """Rows of several 64-lane K segments (K = 14336 is seven, K = 8192 four,
+    K = 4096 at M >= 5 two) at row counts where the launcher picks each
+    number of rows per lane group."""
+    w = synth.quant_weights(scheme, 7100 + n + m, n, k)
+    x = synth.normal_bf16(7200 + k + m, (m, k))
+    y = host(ffi.matmul(dev(w), scheme, n, k, bf16_dev(x)))
+    check_close(y, O.matmul(scheme, w, n, k, x, O.BF16, threads=8), f"n={n} k={k} m={m}")
+
+
 def test_gemv_graph_replays_match_eager():
     """GEMV launches captured in a HIP graph: every replay (with eager work
     between replays) equals the eager result bit for bit."""
