@@ -9,6 +9,8 @@
 #include "r9vx_oracle.h"
 
 #include <math.h>
+
+#include "../r9v_amd/csrc/r9vx_iq3s_grid.h"
 #include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
@@ -78,8 +80,9 @@ static inline uint16_t rd_u16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1]
 uint32_t rxo_block_bytes(int scheme) {
     /* crates/r9v-format/tests/iq.rs:131-141 and ggml.rs:336-350 block table:
      * Q4_K 144 B / 256 weights, IQ4_XS 136 B / 256, Q6_K 210 B / 256,
-     * Q8_0 34 B / 32. */
+     * Q8_0 34 B / 32, IQ3_S 110 B / 256. */
     if (scheme == RXO_Q4_K) return 144;
+    if (scheme == RXO_IQ3_S) return 110;
     if (scheme == RXO_IQ4_XS) return 136;
     if (scheme == RXO_Q6_K) return 210;
     if (scheme == RXO_Q8_0) return 34;
@@ -175,6 +178,34 @@ static void q80_block(const uint8_t *blk, float *out) {
     for (int i = 0; i < 32; ++i) out[i] = d * (float)(int8_t)blk[2 + i];
 }
 
+/* IQ3_S codebook: crates/r9v-format/src/iq_lut.rs:629-630, 512 entries of
+ * four values, entry e's value b in byte b of word e. */
+static const uint32_t IQ3S_GRID[512] = {R9VX_IQ3S_GRID_WORDS};
+
+/* One IQ3_S block (d f16 | qs 64 | qh 8 | signs 32 | scales 4 = 110 B) -> 256
+ * f32.  crates/r9v-format/src/iq.rs:698-722 (source_block, Iq3S arm): group g
+ * of 32 has db = d * (1 + 2 s), s = nibble g%2 of scales[g/2]; index i = 8g+sg
+ * takes grid entry qs[i] | (bit sg of qh[g]) << 8, and value 4 sg + b of the
+ * group is (db * grid[b]) negated when bit 4 (sg%2) + b of signs[4g + sg/2]
+ * is set. */
+static void iq3s_block(const uint8_t *blk, float *out) {
+    float d = rxo_f16_to_f32(rd_u16(blk));
+    for (int g = 0; g < 8; ++g) {
+        uint32_t s = (blk[106 + g / 2] >> ((g % 2) * 4)) & 0x0F;
+        float db = d * (1.0f + 2.0f * (float)s);
+        for (int sg = 0; sg < 8; ++sg) {
+            int i = g * 8 + sg;
+            uint32_t idx = blk[2 + i] | (((uint32_t)(blk[66 + g] >> sg) & 1u) << 8);
+            uint8_t signs = blk[74 + g * 4 + sg / 2];
+            for (int b = 0; b < 4; ++b) {
+                float grid = (float)((IQ3S_GRID[idx] >> (8 * b)) & 0xFF);
+                float v = db * grid;
+                out[g * 32 + sg * 4 + b] = ((signs >> ((sg % 2) * 4 + b)) & 1) ? v * -1.0f : v;
+            }
+        }
+    }
+}
+
 /* Byte offset of a block's f16 scale d that check_wire_f16 validates. */
 static uint32_t d_offset(int scheme) { return scheme == RXO_Q6_K ? 208 : 0; }
 
@@ -200,6 +231,8 @@ static void decode_row(int scheme, const uint8_t *row, uint32_t k, float *out) {
             iq4xs_block(blk, o);
         else if (scheme == RXO_Q6_K)
             q6k_block(blk, o);
+        else if (scheme == RXO_IQ3_S)
+            iq3s_block(blk, o);
         else
             q80_block(blk, o);
     }

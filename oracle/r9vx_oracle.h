@@ -18,6 +18,10 @@
  *   Q6_K / Q8_0 decode ... reference golden vectors gguf_a23_reference.txt
  *                  (gguf-py 0.19.0 dequantize), and a numpy restatement of
  *                  the llama.cpp row loop (dequantize_row_q6_K form)
+ *   IQ3_S decode ... reference golden vectors iq_a24_reference.txt (IQ3_S,
+ *                  gguf-py 0.19.0), a numpy restatement of the llama.cpp row
+ *                  loop (dequantize_row_iq3_s form), and the codebook facts
+ *                  of crates/r9v-format/tests/iq.rs:505-516
  *   rxo_matmul ... known answer 1408.0 (matmul_tests.rs:208-265), f64
  *                  brute force on tiny shapes, batch invariance
  *   rxo_moe_route ... equal-logit lowest-id answers (moe_route_tests.rs:107),
@@ -41,6 +45,7 @@ extern "C" {
 #define RXO_IQ4_XS 23
 #define RXO_Q6_K 14
 #define RXO_Q8_0 8
+#define RXO_IQ3_S 21
 
 /* Element dtypes: discriminant order of r9v-ir DType (dtype.rs:15-35). */
 #define RXO_F32 0

@@ -4,8 +4,8 @@ Data only (inputs and expected outputs); run once in the build container where
 /root/reference exists.  Sources:
   crates/r9v-format/tests/fixtures/r9v-format/q4k_reference.txt  (all 6 Q4_K cases,
       consumed by crates/r9v-format/tests/schemes.rs:482-516)
-  crates/r9v-format/tests/fixtures/r9v-format/iq_a24_reference.txt (the IQ4_XS and
-      IQ4_NL cases, consumed by crates/r9v-format/tests/iq.rs:159-197)
+  crates/r9v-format/tests/fixtures/r9v-format/iq_a24_reference.txt (the IQ4_XS,
+      IQ4_NL and IQ3_S cases, consumed by crates/r9v-format/tests/iq.rs:159-197)
   crates/r9v-format/tests/fixtures/r9v-format/gguf_a23_reference.txt (the Q8_0, Q6_K
       and Q4_K cases, consumed by crates/r9v-format/tests/gguf.rs:44-90,172-180)
       -> gguf_a23_reference.txt
@@ -34,7 +34,7 @@ def main() -> int:
             out.append(line)
             continue
         if line.startswith("case "):
-            keep = line.split()[1] in ("IQ4_XS", "IQ4_NL")
+            keep = line.split()[1] in ("IQ4_XS", "IQ4_NL", "IQ3_S")
         if keep:
             out.append(line)
     (DST / "iq4_reference.txt").write_text(

@@ -13,7 +13,7 @@ import numpy as np
 ROOT = pathlib.Path(__file__).resolve().parent.parent
 LIB_PATH = ROOT / "oracle" / "liboracle.so"
 
-Q4_K, IQ4_XS, Q6_K, Q8_0 = 12, 23, 14, 8
+Q4_K, IQ4_XS, Q6_K, Q8_0, IQ3_S = 12, 23, 14, 8, 21
 F32, BF16 = 0, 2
 
 _lib = None

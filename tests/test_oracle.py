@@ -9,6 +9,7 @@ transposed operand fails.
 from __future__ import annotations
 
 import pathlib
+import re
 import struct
 import subprocess
 
@@ -123,6 +124,77 @@ def test_iq4xs_golden_bit_exact():
     c = iq4_cases()["IQ4_XS"]
     got = O.dequantize(O.IQ4_XS, c["wire"], c["n"], c["k"])
     assert np.array_equal(got.reshape(-1).view(np.uint32), c["y_bits"])
+
+
+def _iq3s_grid_words():
+    text = (ROOT / "r9v_amd" / "csrc" / "r9vx_iq3s_grid.h").read_text()
+    body = text.split("#define R9VX_IQ3S_GRID_WORDS")[1].split("#endif")[0]
+    return np.array([int(t, 16) for t in re.findall(r"0x([0-9a-f]{8})u", body)], dtype=np.uint32)
+
+
+def test_iq3s_golden_bit_exact():
+    """crates/r9v-format/tests/iq.rs:159-197: the IQ3_S 3x1024 case (seeded
+    payloads, all-zero and all-0xFF blocks) matches gguf-py 0.19.0."""
+    c = iq4_cases()["IQ3_S"]
+    got = O.dequantize(O.IQ3_S, c["wire"], c["n"], c["k"])
+    assert np.array_equal(got.reshape(-1).view(np.uint32), c["y_bits"])
+
+
+def test_iq3s_grid_facts():
+    """The codebook's facts from crates/r9v-format/tests/iq.rs:505,514-516
+    (2048 values, all odd and <= 15), plus strict ascent of the 512 words."""
+    w = _iq3s_grid_words()
+    assert w.size == 512 and np.all(np.diff(w.astype(np.int64)) > 0)
+    b = w.view(np.uint8)
+    assert np.all(b % 2 == 1) and np.all(b <= 15)
+    assert (w[0], w[1], w[511]) == (0x01010101, 0x01010103, 0x0F0F0101)
+
+
+def _iq3s_llama_loop(blocks, grid):
+    """llama.cpp's dequantize_row_iq3_s, restated in numpy: two groups of 32
+    per step, the grid index's ninth bit taken as (qh << (8 - 2l)) & 256 and
+    (qh << (7 - 2l)) & 256, signs through the 0x01..0x80 bit masks."""
+    out = []
+    g8 = grid.view(np.uint8).reshape(512, 4)
+    for blk in blocks:
+        d = np.float32(np.frombuffer(blk[0:2].tobytes(), np.float16)[0])
+        qs, qh, signs, scales = blk[2:66], blk[66:74], blk[74:106], blk[106:110]
+        y = []
+        for ib32 in range(0, 8, 2):
+            sc = int(scales[ib32 // 2])
+            for half, s in ((0, sc & 0xF), (1, sc >> 4)):
+                db = np.float32(d * np.float32(1 + 2 * s))
+                q = qs[8 * (ib32 + half):8 * (ib32 + half) + 8]
+                h = int(qh[ib32 + half])
+                sg = signs[4 * (ib32 + half):4 * (ib32 + half) + 4]
+                for l in range(4):
+                    i1 = int(q[2 * l]) | ((h << (8 - 2 * l)) & 256)
+                    i2 = int(q[2 * l + 1]) | ((h << (7 - 2 * l)) & 256)
+                    for j in range(4):
+                        v = np.float32(db * np.float32(g8[i1, j]))
+                        y.append(-v if int(sg[l]) & (1 << j) else v)
+                    for j in range(4):
+                        v = np.float32(db * np.float32(g8[i2, j]))
+                        y.append(-v if int(sg[l]) & (1 << (j + 4)) else v)
+        out.append(np.array(y, dtype=np.float32))
+    return np.concatenate(out)
+
+
+def test_iq3s_matches_llama_cpp_loop():
+    """Random blocks (finite d): the oracle equals the llama.cpp loop form."""
+    rng = np.random.default_rng(321)
+    blocks = rng.integers(0, 256, size=(24, 110), dtype=np.uint8)
+    blocks[:, 0:2] = np.frombuffer(rng.normal(0, 0.05, 24).astype(np.float16).tobytes(), np.uint8).reshape(24, 2)
+    got = O.dequantize(O.IQ3_S, blocks.reshape(-1), 3, 2048)
+    want = _iq3s_llama_loop(blocks, _iq3s_grid_words())
+    assert np.array_equal(got.reshape(-1).view(np.uint32), want.view(np.uint32))
+
+
+def test_iq3s_nonfinite_scale_refused():
+    blk = np.zeros(110, dtype=np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(np.inf).tobytes(), np.uint8)
+    with pytest.raises(O.OracleError):
+        O.dequantize(O.IQ3_S, blk, 1, 256)
 
 
 def test_iq4xs_closed_form_codebook():
