@@ -54,6 +54,7 @@ enum r9vx_scheme {
     R9VX_SCHEME_Q8_0 = 8,    /* 34-B block per 32 weights; device layout split (below) */
     R9VX_SCHEME_Q4_K = 12,   /* 144-B super-block per 256 weights */
     R9VX_SCHEME_Q6_K = 14,   /* 210-B super-block per 256 weights; device layout split */
+    R9VX_SCHEME_IQ3_S = 21,  /* 110-B super-block per 256 weights; device layout repacked */
     R9VX_SCHEME_IQ4_XS = 23  /* 136-B super-block per 256 weights */
 };
 /* Q4_K and IQ4_XS are read as GGUF wire blocks.  Q8_0 and Q6_K blocks (34 and
@@ -64,7 +65,12 @@ enum r9vx_scheme {
  *   Q6_K: body = [N, K/256] blocks of 208 bytes (ql 128, qh 64, scales 16,
  *         the wire block without its trailing d), w_scales = f16 [N, K/256].
  * Bodies and scales together hold exactly the wire bytes.  A matmul on them
- * passes the body as `w` and the d array as `w_scales`. */
+ * passes the body as `w` and the d array as `w_scales`.
+ * IQ3_S (110-byte blocks) is repacked into one array of 112-byte blocks,
+ * `scales` NULL: qs 64 | signs 32 | qh 8 | scales 4 | d 2 | two zero bytes
+ * (the wire fields, in this order; crates/r9v-format/src/iq.rs:362-367 names
+ * them), so the 4 sign bytes of each 32-weight group are one aligned word.
+ * A matmul passes that array as `w` with `w_scales` NULL; bf16 activations. */
 
 /* Matmul epilogues (crates/r9v-t0/src/matmul.rs:2421-2446), plus the gated
  * epilogue of the kernel generator's GEMM family ("gated (gate_up
@@ -278,11 +284,11 @@ int r9vx_dequantize_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows
 int r9vx_validate_weights_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows,
                                  uint32_t k, uint32_t *bad_blocks, r9vx_stream_t stream);
 
-/* Load-time repack of Q8_0 / Q6_K wire blocks [n_rows, k] (device memory)
- * into the split device layout above: body and scales may not overlap the
- * wire.  The counterpart of the reference's load-time repack to its L1 layout
- * (crates/r9v-format/src/repack.rs:282).  Q4_K and IQ4_XS need none and are
- * refused. */
+/* Load-time repack of Q8_0 / Q6_K / IQ3_S wire blocks [n_rows, k] (device
+ * memory) into the device layouts above: body and scales may not overlap the
+ * wire; IQ3_S takes scales = NULL.  The counterpart of the reference's
+ * load-time repack to its L1 layout (crates/r9v-format/src/repack.rs:282).
+ * Q4_K and IQ4_XS need none and are refused. */
 int r9vx_repack_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k,
                        uint8_t *body, uint16_t *scales, r9vx_stream_t stream);
 

@@ -172,7 +172,45 @@ __global__ __launch_bounds__(256) void dequant_q6k_kernel(const uint8_t *__restr
     store16(out + blk * 256 + i0, v);
 }
 
-/* Non-finite d (check_wire_f16, ggml.rs:421-445) of Q8_0 / Q6_K wire blocks. */
+/* IQ3_S: one thread per group g of 32 weights (crates/r9v-format/src/iq.rs:
+ * 698-722): db = d * (1 + 2 s) with s = nibble g%2 of scales[g/2]; index i
+ * of the group takes grid entry qs[8g+i] | (bit i of qh[g]) << 8, and weight
+ * 4i + b is db * grid[b], negated when bit 4(i%2) + b of signs[4g + i/2] is
+ * set. */
+__global__ __launch_bounds__(256) void dequant_iq3s_kernel(const uint8_t *__restrict__ wire, uint64_t n_groups,
+                                                           float *__restrict__ out) {
+    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= n_groups) return;
+    const uint64_t blk = gid >> 3;
+    const uint32_t g = (uint32_t)(gid & 7);
+    const uint8_t *b = wire + blk * R9VX_IQ3S_BYTES;
+    const float d = r9vx_f16_to_f32((uint16_t)ld_u16(b));
+    /* scales[g/2] is byte (g/2)%2 of the 16-bit word at 106 + 2(g/4) */
+    const uint32_t s = (ld_u16(b + 106 + 2 * (g >> 2)) >> (8 * ((g >> 1) & 1) + 4 * (g & 1))) & 0xF;
+    const float db = d * (1.0f + 2.0f * (float)s);
+    const uint32_t qh = (ld_u16(b + 66 + (g & ~1u)) >> (8 * (g & 1))) & 0xFF;
+    const uint32_t sg = ld_u16(b + 74 + 4 * g) | (ld_u16(b + 76 + 4 * g) << 16); /* bit v signs weight v */
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+        const uint32_t two = ld_u16(b + 2 + 8 * g + i);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const uint32_t idx = ((two >> (8 * e)) & 0xFF) | (((qh >> (i + e)) & 1u) << 8);
+            const uint32_t gw = kIq3sGrid[idx];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t w = 4 * (i + e) + c;
+                const float m = db * (float)((gw >> (8 * c)) & 0xFF);
+                v[w] = ((sg >> w) & 1u) ? m * -1.0f : m;
+            }
+        }
+    }
+    store16(out + blk * 256 + 32 * g, v);
+    store16(out + blk * 256 + 32 * g + 16, v + 16);
+}
+
+/* Non-finite d (check_wire_f16, ggml.rs:421-445) of Q8_0 / Q6_K / IQ3_S wire blocks. */
 __global__ __launch_bounds__(256) void validate_split_kernel(const uint8_t *__restrict__ wire, uint64_t n_blocks,
                                                              uint32_t block_bytes, uint32_t d_offset,
                                                              uint32_t *bad) {
@@ -214,11 +252,38 @@ __global__ __launch_bounds__(256) void repack_q6k_kernel(const uint8_t *__restri
     if (piece == 0) scales[blk] = (uint16_t)ld_u16(wire + blk * R9VX_Q6K_BYTES + 208);
 }
 
+/* Wire -> IQ3_S device block: thread per 16-byte piece of the 112-byte
+ * block (7 per block); device byte j takes wire byte 2 + j (qs, j < 64),
+ * 10 + j (signs, j < 96), j - 30 (qh, j < 104), j + 2 (scales, j < 108),
+ * j - 108 (d, j < 110), and zero. */
+__device__ __forceinline__ uint32_t iq3s_wire_byte(uint32_t j) {
+    return j < 64 ? 2 + j : j < 96 ? 10 + j : j < 104 ? j - 30 : j < 108 ? j + 2 : j - 108;
+}
+
+__global__ __launch_bounds__(256) void repack_iq3s_kernel(const uint8_t *__restrict__ wire, uint64_t n_pieces,
+                                                          uint8_t *__restrict__ body) {
+    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= n_pieces) return;
+    const uint64_t blk = gid / 7;
+    const uint32_t piece = (uint32_t)(gid % 7);
+    const uint8_t *b = wire + blk * R9VX_IQ3S_BYTES;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t j = 16 * piece + i;
+        if (j < 110) w[i >> 2] |= (uint32_t)b[iq3s_wire_byte(j)] << (8 * (i & 3));
+    }
+    *reinterpret_cast<r9vx_u32x4 *>(body + blk * R9VX_IQ3S_DEV_BYTES + 16 * piece) = r9vx_u32x4{w[0], w[1], w[2], w[3]};
+}
+
 }  // namespace
 
 int r9vx_launch_dequant_split(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k, float *out,
                               hipStream_t stream) {
-    if (scheme == R9VX_SCHEME_Q8_0) {
+    if (scheme == R9VX_SCHEME_IQ3_S) {
+        const uint64_t n = (uint64_t)n_rows * (k / 256) * 8;
+        hipLaunchKernelGGL(dequant_iq3s_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, wire, n, out);
+    } else if (scheme == R9VX_SCHEME_Q8_0) {
         const uint64_t n = (uint64_t)n_rows * (k / 32);
         hipLaunchKernelGGL(dequant_q80_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, wire, n, out);
     } else {
@@ -230,16 +295,20 @@ int r9vx_launch_dequant_split(uint32_t scheme, const uint8_t *wire, uint32_t n_r
 
 int r9vx_launch_validate_split(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k, uint32_t *bad,
                                hipStream_t stream) {
-    const bool q8 = scheme == R9VX_SCHEME_Q8_0;
+    const bool q8 = scheme == R9VX_SCHEME_Q8_0, iq3 = scheme == R9VX_SCHEME_IQ3_S;
     const uint64_t n = (uint64_t)n_rows * (k / (q8 ? 32 : 256));
     hipLaunchKernelGGL(validate_split_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, wire, n,
-                       (uint32_t)(q8 ? R9VX_Q80_BYTES : R9VX_Q6K_BYTES), q8 ? 0u : 208u, bad);
+                       (uint32_t)(q8 ? R9VX_Q80_BYTES : iq3 ? R9VX_IQ3S_BYTES : R9VX_Q6K_BYTES),
+                       (q8 || iq3) ? 0u : 208u, bad);
     return (int)hipGetLastError();
 }
 
 int r9vx_launch_repack(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k, uint8_t *body,
                        uint16_t *scales, hipStream_t stream) {
-    if (scheme == R9VX_SCHEME_Q8_0) {
+    if (scheme == R9VX_SCHEME_IQ3_S) {
+        const uint64_t n = (uint64_t)n_rows * (k / 256) * 7;
+        hipLaunchKernelGGL(repack_iq3s_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, wire, n, body);
+    } else if (scheme == R9VX_SCHEME_Q8_0) {
         const uint64_t n = (uint64_t)n_rows * (k / 32);
         hipLaunchKernelGGL(repack_q80_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, wire, n,
                            body, scales);

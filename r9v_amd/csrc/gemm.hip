@@ -1,7 +1,8 @@
 /*
  * gemm.hip -- prefill dequant-GEMM on MFMA: y[m, n] = sum_k x[m, k] * w[n, k]
  * for bf16 activations (m > 8) and GGUF Q4_K / IQ4_XS weights (wire blocks)
- * or Q8_0 / Q6_K weights (split layout, LDS-decoded tiles only).
+ * or Q8_0 / Q6_K weights (split layout) and IQ3_S weights (112-byte repacked
+ * blocks), LDS-decoded tiles only.
  *
  * T0 meaning: crates/r9v-t0/src/matmul.rs:1940-2414 (Branch D), output cast
  * crates/r9v-t0/src/dtype.rs:102-111 (bf16 RNE); epilogue matmul.rs:2421-2446.
@@ -305,6 +306,7 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     case R9VX_SCHEME_Q4_K: a.w_row_stride = (uint64_t)(p.k / 256) * R9VX_Q4K_BYTES; break;
     case R9VX_SCHEME_IQ4_XS: a.w_row_stride = (uint64_t)(p.k / 256) * R9VX_IQ4XS_BYTES; break;
     case R9VX_SCHEME_Q6_K: a.w_row_stride = (uint64_t)(p.k / 256) * R9VX_Q6K_BODY, a.ws_row = p.k / 256; break;
+    case R9VX_SCHEME_IQ3_S: a.w_row_stride = (uint64_t)(p.k / 256) * R9VX_IQ3S_DEV_BYTES; break;
     default: a.w_row_stride = p.k, a.ws_row = p.k / 32; break; /* Q8_0 */
     }
     a.m = p.m;
@@ -314,7 +316,7 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     a.epilogue = p.epilogue;
     /* 256 x 256 register-decoded tiles when there are enough of them to fill
      * the chip; 128-row LDS-decoded tiles (two workgroups per CU) otherwise. */
-    const bool split = p.scheme == R9VX_SCHEME_Q8_0 || p.scheme == R9VX_SCHEME_Q6_K;
+    const bool split = p.scheme == R9VX_SCHEME_Q8_0 || p.scheme == R9VX_SCHEME_Q6_K || p.scheme == R9VX_SCHEME_IQ3_S;
     const bool big = !split && (uint64_t)((p.m + 255) / 256) * ((p.n + 255) / 256) >= 256;
     if (big) {
         if (p.scheme == R9VX_SCHEME_Q4_K)
@@ -335,12 +337,13 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     a.m_tiles = (p.m + 127) / 128;
     a.n_tiles = (p.n + 255) / 256;
     dim3 grid(a.m_tiles * a.n_tiles);
-    /* Q8_0 / Q6_K always take this LDS-decoded tile (their 48- and 64-byte
-     * steps do not fit the register-decoded core's 16-byte lane payload). */
+    /* Q8_0 / Q6_K / IQ3_S always take this LDS-decoded tile (their steps do
+     * not fit the register-decoded core's 16-byte lane payload). */
     switch (p.scheme) {
     case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q4_K, 128, 1>), grid, dim3(256), 0, stream, a); break;
     case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_IQ4_XS, 128, 1>), grid, dim3(256), 0, stream, a); break;
     case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q6_K, 128, 1>), grid, dim3(256), 0, stream, a); break;
+    case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_IQ3_S, 128, 1>), grid, dim3(256), 0, stream, a); break;
     default: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q8_0, 128, 1>), grid, dim3(256), 0, stream, a); break;
     }
     return (int)hipGetLastError();

@@ -1,7 +1,8 @@
 /*
  * gemv.hip -- decode-time dequant-fused GEMV, y[m, n] = sum_k x[m, k] * w[n, k],
- * for GGUF Q4_K / IQ4_XS weights (wire blocks) and Q8_0 / Q6_K weights (split
- * layout: body + f16 d array), and m <= 8 activation rows.
+ * for GGUF Q4_K / IQ4_XS weights (wire blocks), Q8_0 / Q6_K weights (split
+ * layout: body + f16 d array) and IQ3_S weights (112-byte repacked blocks),
+ * and m <= 8 activation rows.
  *
  * T0 meaning: crates/r9v-t0/src/matmul.rs:1940-2414 (Branch D, f32
  * accumulate); weight decode crates/r9v-format/src/ggml.rs:1131-1150 (Q4_K)
@@ -47,6 +48,10 @@ struct GemvArgs {
 };
 
 constexpr bool split_scheme(int s) { return s == R9VX_SCHEME_Q8_0 || s == R9VX_SCHEME_Q6_K; }
+/* schemes whose chunks are carried as a Payload2 */
+constexpr bool pay2_scheme(int s) { return split_scheme(s) || s == R9VX_SCHEME_IQ3_S; }
+/* LDS table words: the IQ3_S codebook as bf16 quads, the IQ4_XS pair table */
+constexpr int lut_words(int s) { return s == R9VX_SCHEME_IQ3_S ? 1024 : 256; }
 
 /* Rows per lane group per wave and waves per workgroup, by activation row
  * count (measured on MI355X at K=2048/4096): two rows in two-wave groups
@@ -67,7 +72,7 @@ using namespace r9vx;
 template <int SCHEME, int M, bool XF32, int SPL, int LPRL, int RR, int NS = 1>
 __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
     constexpr int kRows = RR ? RR : rows_for(M), kWaves = waves_for(M);
-    __shared__ uint32_t lut[256];
+    __shared__ __attribute__((aligned(16))) uint32_t lut[lut_words(SCHEME)];
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
     const uint32_t lprl = LPRL ? (uint32_t)LPRL : a.lpr_log2;
@@ -107,7 +112,7 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
          * complete in order, so an activation load scheduled after a weight
          * load would hold the activation re-arrangement until HBM answers */
         __builtin_amdgcn_sched_barrier(0);
-        using Pay = typename std::conditional<split_scheme(SCHEME), Payload2, r9vx_u32x4>::type;
+        using Pay = typename std::conditional<pay2_scheme(SCHEME), Payload2, r9vx_u32x4>::type;
         Pay qs[kRows][SPL];
         Hdr hd[kRows][SPL];
 #pragma unroll
@@ -117,7 +122,9 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
             const uint8_t *wrow = a.w + (uint64_t)rr * a.w_row_stride;
 #pragma unroll
             for (int s = 0; s < SPL; ++s) {
-                if constexpr (split_scheme(SCHEME))
+                if constexpr (SCHEME == R9VX_SCHEME_IQ3_S)
+                    load_chunk_iq3s(wrow, cis[s], qs[r][s], hd[r][s]);
+                else if constexpr (split_scheme(SCHEME))
                     load_chunk_split<SCHEME>(wrow, a.ws + (uint64_t)rr * a.ws_row, cis[s], qs[r][s], hd[r][s]);
                 else
                     load_chunk<SCHEME>(wrow, cis[s], qs[r][s], hd[r][s]);
@@ -127,6 +134,11 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
         if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
             if ((LPRL != 0 && NS == 1) || seg == 0) {
                 build_iq4_lut(lut, threadIdx.x, blockDim.x);
+                __syncthreads();
+            }
+        } else if constexpr (SCHEME == R9VX_SCHEME_IQ3_S) {
+            if ((LPRL != 0 && NS == 1) || seg == 0) {
+                build_iq3s_lut(lut, threadIdx.x, blockDim.x);
                 __syncthreads();
             }
         }
@@ -139,7 +151,9 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
         for (int r = 0; r < kRows; ++r)
 #pragma unroll
             for (int s = 0; s < SPL; ++s) {
-                if constexpr (split_scheme(SCHEME))
+                if constexpr (SCHEME == R9VX_SCHEME_IQ3_S)
+                    chunk_dot_iq3s<M>(qs[r][s], hd[r][s], cis[s] & 7, xc[s], acc[r], lut);
+                else if constexpr (split_scheme(SCHEME))
                     chunk_dot_split<SCHEME, M>(qs[r][s], hd[r][s], cis[s] & 7, xc[s], acc[r]);
                 else
                     chunk_dot<SCHEME, XF32, M>(qs[r][s], hd[r][s], cis[s] & 7, xc[s], acc[r], lut);
@@ -192,7 +206,7 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
 template <int SCHEME, int M, int SPL, int PAIRS>
 __global__ __launch_bounds__(waves_for(M) * 64) void gemv_gated_kernel(GemvArgs a) {
     constexpr int kRows = PAIRS, kWaves = waves_for(M);
-    __shared__ uint32_t lut[256];
+    __shared__ __attribute__((aligned(16))) uint32_t lut[lut_words(SCHEME)];
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
     const uint32_t lprl = a.lpr_log2, lpr = 1u << lprl, rpi = 64u >> lprl;
@@ -222,7 +236,7 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_gated_kernel(GemvArgs 
                                   khi, xr[s][t]);
         }
         __builtin_amdgcn_sched_barrier(0);
-        using Pay = typename std::conditional<split_scheme(SCHEME), Payload2, r9vx_u32x4>::type;
+        using Pay = typename std::conditional<pay2_scheme(SCHEME), Payload2, r9vx_u32x4>::type;
         Pay qs[2][kRows][SPL];
         Hdr hd[2][kRows][SPL];
 #pragma unroll
@@ -234,7 +248,9 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_gated_kernel(GemvArgs 
                 const uint8_t *wrow = a.w + wr * a.w_row_stride;
 #pragma unroll
                 for (int s = 0; s < SPL; ++s) {
-                    if constexpr (split_scheme(SCHEME))
+                    if constexpr (SCHEME == R9VX_SCHEME_IQ3_S)
+                        load_chunk_iq3s(wrow, cis[s], qs[h][r][s], hd[h][r][s]);
+                    else if constexpr (split_scheme(SCHEME))
                         load_chunk_split<SCHEME>(wrow, a.ws + wr * a.ws_row, cis[s], qs[h][r][s], hd[h][r][s]);
                     else
                         load_chunk<SCHEME>(wrow, cis[s], qs[h][r][s], hd[h][r][s]);
@@ -243,6 +259,11 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_gated_kernel(GemvArgs 
         if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
             if (seg == 0) {
                 build_iq4_lut(lut, threadIdx.x, blockDim.x);
+                __syncthreads();
+            }
+        } else if constexpr (SCHEME == R9VX_SCHEME_IQ3_S) {
+            if (seg == 0) {
+                build_iq3s_lut(lut, threadIdx.x, blockDim.x);
                 __syncthreads();
             }
         }
@@ -257,7 +278,9 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_gated_kernel(GemvArgs 
             for (int r = 0; r < kRows; ++r)
 #pragma unroll
                 for (int s = 0; s < SPL; ++s) {
-                    if constexpr (split_scheme(SCHEME))
+                    if constexpr (SCHEME == R9VX_SCHEME_IQ3_S)
+                        chunk_dot_iq3s<M>(qs[h][r][s], hd[h][r][s], cis[s] & 7, xc[s], acc[h][r], lut);
+                    else if constexpr (split_scheme(SCHEME))
                         chunk_dot_split<SCHEME, M>(qs[h][r][s], hd[h][r][s], cis[s] & 7, xc[s], acc[h][r]);
                     else
                         chunk_dot<SCHEME, false, M>(qs[h][r][s], hd[h][r][s], cis[s] & 7, xc[s], acc[h][r], lut);
@@ -443,6 +466,7 @@ int r9vx_launch_gemv(const r9vx_gemv_problem &p, hipStream_t stream) {
         case R9VX_SCHEME_Q4_K: return launch_gated_scheme<R9VX_SCHEME_Q4_K>(a, p.m, spl, groups, stream);
         case R9VX_SCHEME_IQ4_XS: return launch_gated_scheme<R9VX_SCHEME_IQ4_XS>(a, p.m, spl, groups, stream);
         case R9VX_SCHEME_Q6_K: return launch_gated_scheme<R9VX_SCHEME_Q6_K>(a, p.m, spl, groups, stream);
+        case R9VX_SCHEME_IQ3_S: return launch_gated_scheme<R9VX_SCHEME_IQ3_S>(a, p.m, spl, groups, stream);
         default: return launch_gated_scheme<R9VX_SCHEME_Q8_0>(a, p.m, spl, groups, stream);
         }
     }
@@ -450,5 +474,6 @@ int r9vx_launch_gemv(const r9vx_gemv_problem &p, hipStream_t stream) {
     if (p.scheme == R9VX_SCHEME_IQ4_XS) return launch_scheme<R9VX_SCHEME_IQ4_XS>(a, p.m, xf32, spl, groups, stream);
     if (xf32) return (int)hipErrorInvalidValue;
     if (p.scheme == R9VX_SCHEME_Q6_K) return launch_scheme_split<R9VX_SCHEME_Q6_K>(a, p.m, spl, groups, stream);
+    if (p.scheme == R9VX_SCHEME_IQ3_S) return launch_scheme_split<R9VX_SCHEME_IQ3_S>(a, p.m, spl, groups, stream);
     return launch_scheme_split<R9VX_SCHEME_Q8_0>(a, p.m, spl, groups, stream);
 }

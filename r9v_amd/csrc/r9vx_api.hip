@@ -49,11 +49,14 @@ int hip_status(const char *op, int rc) {
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-/* Schemes read as GGUF wire blocks (every op), and the ones read in the split
- * layout of r9vx_repack_launch (matmul with m <= 8). */
+/* Schemes read as GGUF wire blocks (every op), the ones read in the split
+ * layout of r9vx_repack_launch (body + d array), and IQ3_S, read as the
+ * 112-byte blocks of r9vx_repack_launch (one array). */
 bool known_scheme(uint32_t s) { return s == R9VX_SCHEME_Q4_K || s == R9VX_SCHEME_IQ4_XS; }
 bool split_scheme(uint32_t s) { return s == R9VX_SCHEME_Q8_0 || s == R9VX_SCHEME_Q6_K; }
-bool matmul_scheme(uint32_t s) { return known_scheme(s) || split_scheme(s); }
+bool packed_scheme(uint32_t s) { return s == R9VX_SCHEME_IQ3_S; }
+bool repacked_scheme(uint32_t s) { return split_scheme(s) || packed_scheme(s); }
+bool matmul_scheme(uint32_t s) { return known_scheme(s) || repacked_scheme(s); }
 
 uint32_t block_bytes(uint32_t s) {
     switch (s) {
@@ -61,6 +64,7 @@ uint32_t block_bytes(uint32_t s) {
     case R9VX_SCHEME_IQ4_XS: return R9VX_IQ4XS_BYTES;
     case R9VX_SCHEME_Q6_K: return R9VX_Q6K_BYTES;
     case R9VX_SCHEME_Q8_0: return R9VX_Q80_BYTES;
+    case R9VX_SCHEME_IQ3_S: return R9VX_IQ3S_BYTES;
     default: return 0;
     }
 }
@@ -70,6 +74,7 @@ uint32_t block_len(uint32_t s) { return s == R9VX_SCHEME_Q8_0 ? 32 : 256; }
 uint64_t device_row_bytes(uint32_t s, uint32_t k) {
     if (s == R9VX_SCHEME_Q8_0) return k;
     if (s == R9VX_SCHEME_Q6_K) return (uint64_t)(k / 256) * R9VX_Q6K_BODY;
+    if (s == R9VX_SCHEME_IQ3_S) return (uint64_t)(k / 256) * R9VX_IQ3S_DEV_BYTES;
     return (uint64_t)(k / 256) * block_bytes(s);
 }
 
@@ -89,9 +94,9 @@ uint32_t r9vx_abi_version(void) { return R9VX_ABI_VERSION; }
 
 static void check_matmul_static(const r9vx_matmul_static *st, Problems &pr) {
     if (!matmul_scheme(st->w_scheme))
-        pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u is not Q4_K (12), IQ4_XS (23), Q6_K (14) or Q8_0 (8)",
+        pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u is not Q4_K (12), IQ4_XS (23), Q6_K (14), Q8_0 (8) or IQ3_S (21)",
                st->w_scheme);
-    if (split_scheme(st->w_scheme) && st->in_dtype != R9VX_DTYPE_BF16)
+    if (repacked_scheme(st->w_scheme) && st->in_dtype != R9VX_DTYPE_BF16)
         pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u takes bf16 activations only", st->w_scheme);
 
     if (st->k == 0 || st->k % 256)
@@ -145,8 +150,8 @@ int r9vx_matmul_launch(const r9vx_matmul_static *st, const r9vx_matmul_args *a,
         if (!a->x) pr.add(R9VX_ERR_NULL, "x is NULL");
         if (!a->y) pr.add(R9VX_ERR_NULL, "y is NULL");
     }
-    if (a->w_scales && known_scheme(st->w_scheme))
-        pr.add(R9VX_ERR_UNSUPPORTED, "w_scales must be NULL: Q4_K / IQ4_XS blocks carry inline scales");
+    if (a->w_scales && !split_scheme(st->w_scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "w_scales must be NULL: Q4_K / IQ4_XS / IQ3_S blocks carry inline scales");
     if (split_scheme(st->w_scheme) && a->m > 0 && !a->w_scales)
         pr.add(R9VX_ERR_NULL, "w_scales (the f16 d array of the split layout) is NULL");
     if (a->w_scales && ((uintptr_t)a->w_scales & 1u)) pr.add(R9VX_ERR_ALIGN, "w_scales must be 2-byte aligned");
@@ -224,27 +229,38 @@ int r9vx_dequantize_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows
     const uint32_t bl = block_len(scheme);
     if (k == 0 || k % bl) pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of %u", k, bl);
     if (n_rows && (!wire || !out)) pr.add(R9VX_ERR_NULL, "wire and out must be non-NULL");
-    /* Q8_0 / Q6_K wire blocks are read as 16-bit words */
-    const uintptr_t wmask = split_scheme(scheme) ? 1u : 15u;
+    /* Q8_0 / Q6_K / IQ3_S wire blocks are read as 16-bit words */
+    const uintptr_t wmask = repacked_scheme(scheme) ? 1u : 15u;
     if ((wire && ((uintptr_t)wire & wmask)) || (out && !aligned16(out))) pr.add(R9VX_ERR_ALIGN, "wire / out alignment");
     int rc = pr.finish("dequantize");
     if (rc || n_rows == 0) return rc;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (split_scheme(scheme)) return hip_status("dequantize", r9vx_launch_dequant_split(scheme, wire, n_rows, k, out, s));
+    if (repacked_scheme(scheme)) return hip_status("dequantize", r9vx_launch_dequant_split(scheme, wire, n_rows, k, out, s));
     return hip_status("dequantize", r9vx_launch_dequant(scheme, wire, n_rows, k, out, s));
 }
 
 int r9vx_repack_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k, uint8_t *body,
                        uint16_t *scales, r9vx_stream_t stream) {
     Problems pr;
-    if (!split_scheme(scheme))
-        pr.add(R9VX_ERR_UNSUPPORTED, "scheme %u: only Q8_0 (8) and Q6_K (14) are repacked; Q4_K / IQ4_XS wire "
-               "blocks are the device layout", scheme);
+    if (!repacked_scheme(scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "scheme %u: only Q8_0 (8), Q6_K (14) and IQ3_S (21) are repacked; Q4_K / "
+               "IQ4_XS wire blocks are the device layout", scheme);
     const uint32_t bl = block_len(scheme);
     if (k == 0 || k % bl) pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of %u", k, bl);
-    if (n_rows && (!wire || !body || !scales)) pr.add(R9VX_ERR_NULL, "wire, body and scales must be non-NULL");
+    if (packed_scheme(scheme) && scales)
+        pr.add(R9VX_ERR_INVALID, "scales must be NULL for IQ3_S: its 112-byte device blocks keep d inline");
+    if (packed_scheme(scheme) && n_rows && (!wire || !body))
+        pr.add(R9VX_ERR_NULL, "wire and body must be non-NULL");
+    if (split_scheme(scheme) && n_rows && (!wire || !body || !scales))
+        pr.add(R9VX_ERR_NULL, "wire, body and scales must be non-NULL");
     if ((wire && ((uintptr_t)wire & 1u)) || (body && !aligned16(body)) || (scales && ((uintptr_t)scales & 1u)))
         pr.add(R9VX_ERR_ALIGN, "wire and scales 2-byte, body 16-byte aligned");
+    if (packed_scheme(scheme) && n_rows && wire && body && k % bl == 0) {
+        const uint64_t nb = (uint64_t)n_rows * (k / bl);
+        const uintptr_t w0 = (uintptr_t)wire, w1 = w0 + nb * block_bytes(scheme);
+        const uintptr_t b0 = (uintptr_t)body, b1 = b0 + (uint64_t)n_rows * device_row_bytes(scheme, k);
+        if (b0 < w1 && w0 < b1) pr.add(R9VX_ERR_INVALID, "wire and body must not overlap");
+    }
     if (split_scheme(scheme) && n_rows && wire && body && scales && k % bl == 0) {
         const uint64_t nb = (uint64_t)n_rows * (k / bl);
         const uintptr_t w0 = (uintptr_t)wire, w1 = w0 + nb * block_bytes(scheme);
@@ -266,11 +282,11 @@ int r9vx_validate_weights_launch(uint32_t scheme, const uint8_t *wire, uint32_t 
     const uint32_t bl = block_len(scheme);
     if (k == 0 || k % bl) pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of %u", k, bl);
     if (n_rows && (!wire || !bad_blocks)) pr.add(R9VX_ERR_NULL, "wire and bad_blocks must be non-NULL");
-    if (wire && ((uintptr_t)wire & (split_scheme(scheme) ? 1u : 3u))) pr.add(R9VX_ERR_ALIGN, "wire alignment");
+    if (wire && ((uintptr_t)wire & (repacked_scheme(scheme) ? 1u : 3u))) pr.add(R9VX_ERR_ALIGN, "wire alignment");
     int rc = pr.finish("validate_weights");
     if (rc || n_rows == 0) return rc;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    if (split_scheme(scheme))
+    if (repacked_scheme(scheme))
         return hip_status("validate_weights", r9vx_launch_validate_split(scheme, wire, n_rows, k, bad_blocks, s));
     return hip_status("validate_weights", r9vx_launch_validate(scheme, wire, n_rows, k, bad_blocks, s));
 }

@@ -8,6 +8,7 @@
 #include <stdint.h>
 
 #include "r9vx.h"
+#include "r9vx_iq3s_grid.h"
 
 #define R9VX_WAVE 64
 
@@ -24,6 +25,16 @@ typedef uint32_t r9vx_u32x2 __attribute__((ext_vector_type(2)));
 #define R9VX_Q6K_BYTES 210   /* wire block: ql 128, qh 64, scales 16, d 2 */
 #define R9VX_Q6K_BODY 208    /* split-layout body: the wire block without d */
 #define R9VX_Q80_BYTES 34    /* wire block: d 2, 32 int8 quants */
+/* IQ3_S: 110-byte wire block (d f16 | qs 64 | qh 8 | signs 32 | scales 4);
+ * the device reads the 112-byte repacked block (qs 64 | signs 32 | qh 8 |
+ * scales 4 | d 2 | 0 0), in which the four sign bytes of 32-weight group g
+ * form the little-endian word at 64 + 4g whose bit v signs weight v of the
+ * group. */
+#define R9VX_IQ3S_BYTES 110
+#define R9VX_IQ3S_DEV_BYTES 112
+
+/* The IQ3_S codebook (entry e = word e, value b in byte b). */
+static __device__ const uint32_t kIq3sGrid[512] = {R9VX_IQ3S_GRID_WORDS};
 
 /* IQ4 codebook (crates/r9v-format/src/iq_lut.rs:23-25). */
 __device__ __forceinline__ int r9vx_iq4_kvalue(uint32_t q) {

@@ -110,7 +110,14 @@ __device__ __forceinline__ void arrange_x(const XRaw<XF32> &r, XChunk<SCHEME, XF
         L[4] = r.v[1].x; L[5] = r.v[1].y; L[6] = r.v[1].z; L[7] = r.v[1].w;
         H[0] = r.v[2].x; H[1] = r.v[2].y; H[2] = r.v[2].z; H[3] = r.v[2].w;
         H[4] = r.v[3].x; H[5] = r.v[3].y; H[6] = r.v[3].z; H[7] = r.v[3].w;
-        if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
+        if constexpr (SCHEME == R9VX_SCHEME_IQ3_S) {
+            /* natural order: p[j] = positions 2j, 2j+1 of the 32 */
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                xc.p[j] = L[j];
+                xc.p[8 + j] = H[j];
+            }
+        } else if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
             /* pair i = {x_lo(i), x_hi(i)}: byte i's two nibbles */
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -358,6 +365,62 @@ __device__ __forceinline__ void chunk_dot_split(const Payload2 &pl, const Hdr &h
             }
             acc[t] += dl0 * (dlo - 160.f * xc[t].slo) + dl1 * (dhi - 160.f * xc[t].shi);
         }
+    }
+}
+
+/* ---- IQ3_S in its 112-byte device blocks ------------------------------------
+ *
+ * Chunk c of a block is 32-weight group c in natural K order: index bytes
+ * 8c..8c+7 (index i covers weights 4i..4i+3), the sign word at 64 + 4c (bit v
+ * signs weight v), and the block's side word at 96 (qh bytes 0..7, scale
+ * nibbles, d).  Weights come from an LDS table of the codebook as bf16
+ * quads (entry e at lut[2e], lut[2e+1]); a sign flips the bf16 sign bit. */
+__device__ __forceinline__ void build_iq3s_lut(uint32_t *lut, uint32_t tid, uint32_t nthreads) {
+    for (uint32_t e = tid; e < 512; e += nthreads) {
+        const uint32_t gw = kIq3sGrid[e];
+        uint32_t h[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) h[b] = __builtin_bit_cast(uint32_t, (float)((gw >> (8 * b)) & 0xFF)) >> 16;
+        lut[2 * e] = h[0] | (h[1] << 16);
+        lut[2 * e + 1] = h[2] | (h[3] << 16);
+    }
+}
+
+__device__ __forceinline__ void load_chunk_iq3s(const uint8_t *row, uint32_t ci, Payload2 &p, Hdr &h) {
+    const uint32_t b = ci >> 3, c = ci & 7;
+    const uint8_t *blk = row + (uint64_t)b * R9VX_IQ3S_DEV_BYTES;
+    const r9vx_u32x2 q = *reinterpret_cast<const r9vx_u32x2 *>(blk + 8 * c);
+    const uint32_t sg = *reinterpret_cast<const uint32_t *>(blk + 64 + 4 * c);
+    p.a = r9vx_u32x4{q.x, q.y, sg, 0u};
+    h.v = r9vx_ld128(blk + 96);
+}
+
+/* acc[t] += db * sum_v (sign_v grid_v) x_v with db = d (1 + 2 s_c)
+ * (crates/r9v-format/src/iq.rs:698-722 for the weight law). */
+template <int M>
+__device__ __forceinline__ void chunk_dot_iq3s(const Payload2 &pl, const Hdr &h, uint32_t c,
+                                               const XChunk<R9VX_SCHEME_IQ3_S, false> (&xc)[M], float (&acc)[M],
+                                               const uint32_t *lut, int m = M) {
+    const uint32_t qh = ((c < 4 ? h.v.x : h.v.y) >> (8 * (c & 3))) & 0xFF;
+    const uint32_t sc = (h.v.z >> (4 * c)) & 0xF;
+    const float db = r9vx_f16_to_f32((uint16_t)(h.v.w & 0xFFFF)) * (1.0f + 2.0f * (float)sc);
+    const uint32_t sg = pl.a.z;
+    uint32_t w[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t idx = (((i < 4 ? pl.a.x : pl.a.y) >> (8 * (i & 3))) & 0xFF) | (((qh >> i) & 1u) << 8);
+        const r9vx_u32x2 e = *reinterpret_cast<const r9vx_u32x2 *>(lut + 2 * idx);
+        const uint32_t nib = sg >> (4 * i);
+        w[2 * i] = e.x ^ (((nib & 1u) << 15) | ((nib & 2u) << 30));
+        w[2 * i + 1] = e.y ^ (((nib & 4u) << 13) | ((nib & 8u) << 28));
+    }
+#pragma unroll
+    for (int t = 0; t < M; ++t) {
+        if (t >= m) break;
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s = r9vx_dot2_bf16(w[j], xc[t].p[j], s);
+        acc[t] = fmaf(db, s, acc[t]);
     }
 }
 

@@ -127,9 +127,20 @@ struct WRegsQ6K {
     r9vx_u32x4 ql[4], qh[2];
     uint32_t sc4, d;
 };
+/* IQ3_S in its 112-byte device blocks: step ks = kt%4 of block kt/4 covers
+ * groups 2ks and 2ks+1: index bytes 16ks..16ks+15, sign words 2ks and
+ * 2ks+1 (bytes 64 + 8ks), and the block's side word (qh, scales, d). */
+struct WRegsIq3 {
+    r9vx_u32x4 q, side;
+    r9vx_u32x2 sg;
+};
 template <int SCHEME>
 struct WRegsFor {
     using T = WRegs;
+};
+template <>
+struct WRegsFor<R9VX_SCHEME_IQ3_S> {
+    using T = WRegsIq3;
 };
 template <>
 struct WRegsFor<R9VX_SCHEME_Q8_0> {
@@ -148,6 +159,12 @@ __device__ __forceinline__ void load_w_any(const uint8_t *row, const uint16_t *s
 #pragma unroll
         for (int i = 0; i < 4; ++i) w.q[i] = r9vx_ld128(p + 16 * i);
         w.d2 = *reinterpret_cast<const uint32_t *>(srow + 2 * kt);
+    } else if constexpr (SCHEME == R9VX_SCHEME_IQ3_S) {
+        const uint8_t *b = row + (uint64_t)(kt >> 2) * R9VX_IQ3S_DEV_BYTES;
+        const uint32_t ks = kt & 3;
+        w.q = r9vx_ld128(b + 16 * ks);
+        w.sg = *reinterpret_cast<const r9vx_u32x2 *>(b + 64 + 8 * ks);
+        w.side = r9vx_ld128(b + 96);
     } else if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
         const uint32_t blk = kt >> 2, ks = kt & 3, g = ks >> 1;
         const uint8_t *b = row + (uint64_t)blk * R9VX_Q6K_BODY;
@@ -185,6 +202,37 @@ __device__ __forceinline__ void dequant_store_any(const typename WRegsFor<SCHEME
                 h[2 * half + 1] = cvt_pk_h2(d * (float)(int8_t)((dw >> 16) & 0xFF), d * (float)(int8_t)(dw >> 24));
             }
             *reinterpret_cast<r9vx_u32x4 *>(B + lds_chunk(row, c)) = r9vx_u32x4{h[0], h[1], h[2], h[3]};
+        }
+    } else if constexpr (SCHEME == R9VX_SCHEME_IQ3_S) {
+        /* weight 4i + b of group g = (d (1 + 2 s_g)) grid[idx_i][b], negated
+         * when bit 4i + b of the group's sign word is set
+         * (crates/r9v-format/src/iq.rs:698-722) */
+        const float d = r9vx_f16_to_f32((uint16_t)(w.side.w & 0xFFFF));
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg) {
+            const uint32_t g = 2 * ks + gg;
+            const uint32_t qh = ((g < 4 ? w.side.x : w.side.y) >> (8 * (g & 3))) & 0xFF;
+            const float db = d * (1.0f + 2.0f * (float)((w.side.z >> (4 * g)) & 0xF));
+            const uint32_t sgw = gg ? w.sg.y : w.sg.x;
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4) {
+                uint32_t h[4];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int i = 2 * c4 + e, byte = 8 * gg + i;
+                    const uint32_t idx = ((u32x4_at(w.q, byte >> 2) >> (8 * (byte & 3))) & 0xFF) | (((qh >> i) & 1u) << 8);
+                    const uint32_t gw = kIq3sGrid[idx];
+                    float v[4];
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const float m = db * (float)((gw >> (8 * b)) & 0xFF);
+                        v[b] = ((sgw >> (4 * i + b)) & 1u) ? m * -1.0f : m;
+                    }
+                    h[2 * e] = cvt_pk_h2(v[0], v[1]);
+                    h[2 * e + 1] = cvt_pk_h2(v[2], v[3]);
+                }
+                *reinterpret_cast<r9vx_u32x4 *>(B + lds_chunk(row, 4 * gg + c4)) = r9vx_u32x4{h[0], h[1], h[2], h[3]};
+            }
         }
     } else if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
         const float d = r9vx_f16_to_f32((uint16_t)w.d);

@@ -19,14 +19,15 @@ LIB_PATH = PKG / "libr9vx.so"
 
 # enums (include/r9vx.h)
 F32, F16, BF16, U32 = 0, 1, 2, 8
-Q4_K, IQ4_XS, Q6_K, Q8_0 = 12, 23, 14, 8
+Q4_K, IQ4_XS, Q6_K, Q8_0, IQ3_S = 12, 23, 14, 8, 21
 EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_RESIDUAL, EPILOGUE_SWIGLU = 0, 1, 2, 3
 SCORING_SOFTMAX, SCORING_SIGMOID = 0, 1
 ACT_SILU = 0
 STATUS_NONFINITE, STATUS_DEGENERATE, STATUS_BAD_EXPERT = 1, 2, 4
-BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136, Q6_K: 210, Q8_0: 34}
-BLOCK_LEN = {Q4_K: 256, IQ4_XS: 256, Q6_K: 256, Q8_0: 32}
+BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136, Q6_K: 210, Q8_0: 34, IQ3_S: 110}
+BLOCK_LEN = {Q4_K: 256, IQ4_XS: 256, Q6_K: 256, Q8_0: 32, IQ3_S: 256}
 SPLIT_SCHEMES = (Q6_K, Q8_0)      # read in the split device layout (body + f16 d array)
+IQ3S_DEV_BYTES = 112              # IQ3_S is read as repacked 112-byte blocks (one array)
 
 _P = ctypes.c_void_p
 _U32 = ctypes.c_uint32
@@ -204,8 +205,8 @@ def matmul_static(n, k, w_scheme, in_dtype, out_dtype, m_bucket=8, epilogue=EPIL
 def matmul(w, w_scheme, n, k, x, out_dtype=F32, bias=None, residual=None, y=None, workspace=None,
            stream=None, w_scales=None, swiglu=False):
     """y[m, n] = x[m, :] . w[n, :] (+ bias | + residual): T0 execute_matmul_op meaning.
-    Q6_K / Q8_0 weights are a split body `w` plus its f16 d array `w_scales`
-    (see `repack`)."""
+    Q6_K / Q8_0 weights are a split body `w` plus its f16 d array `w_scales`,
+    IQ3_S weights the repacked 112-byte blocks (see `repack`)."""
     torch = _need_gpu(w, x, bias, residual, y, w_scales)
     m = x.shape[0]
     if y is None:
@@ -243,9 +244,15 @@ def dequantize(wire, scheme, n_rows, k, out=None, stream=None):
 
 
 def repack(wire, scheme, n_rows, k, stream=None):
-    """Q8_0 / Q6_K wire blocks on the device -> (body uint8, scales int16 holding f16 bits)."""
+    """Q8_0 / Q6_K wire blocks on the device -> (body uint8, scales int16 holding
+    f16 bits); IQ3_S -> (112-byte blocks uint8, None)."""
     torch = _need_gpu(wire)
     nb = n_rows * (k // BLOCK_LEN[scheme])
+    if scheme == IQ3_S:
+        body = torch.empty(nb * IQ3S_DEV_BYTES, dtype=torch.uint8, device=wire.device)
+        _check(load().r9vx_repack_launch(scheme, _ptr(wire), n_rows, k, _ptr(body), None,
+                                         _stream(torch, stream)))
+        return body, None
     body = torch.empty(nb * (BLOCK_BYTES[scheme] - 2), dtype=torch.uint8, device=wire.device)
     scales = torch.empty(nb, dtype=torch.int16, device=wire.device)
     _check(load().r9vx_repack_launch(scheme, _ptr(wire), n_rows, k, _ptr(body), _ptr(scales),

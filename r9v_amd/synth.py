@@ -23,9 +23,10 @@ Q4_K = 12
 IQ4_XS = 23
 Q6_K = 14
 Q8_0 = 8
-BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136, Q6_K: 210, Q8_0: 34}
-BLOCK_LEN = {Q4_K: 256, IQ4_XS: 256, Q6_K: 256, Q8_0: 32}
-D_OFFSET = {Q4_K: 0, IQ4_XS: 0, Q6_K: 208, Q8_0: 0}  # byte offset of each block's f16 d
+IQ3_S = 21
+BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136, Q6_K: 210, Q8_0: 34, IQ3_S: 110}
+BLOCK_LEN = {Q4_K: 256, IQ4_XS: 256, Q6_K: 256, Q8_0: 32, IQ3_S: 256}
+D_OFFSET = {Q4_K: 0, IQ4_XS: 0, Q6_K: 208, Q8_0: 0, IQ3_S: 0}  # byte offset of each block's f16 d
 
 
 def seed_for(config: str, case: str = "") -> int:

@@ -157,6 +157,29 @@ def test_split_scheme_refusals_and_figures():
     assert rc == -1 and "overlap" in lib.r9vx_last_error().decode()
 
 
+def test_iq3s_refusals_and_figures():
+    """IQ3_S: bf16 activations, no w_scales (d is inline in the 112-byte block), and a repack that takes
+    no scales array and refuses an overlapping body."""
+    lib = ffi.load()
+    st = ffi.matmul_static(n=64, k=512, w_scheme=ffi.IQ3_S, in_dtype=ffi.F32, out_dtype=ffi.F32)
+    args = ffi.MatmulArgs()
+    args.m = 1
+    args.w_scales = 16
+    assert _call(lib.r9vx_matmul_launch, st, args) < 0
+    msg = lib.r9vx_last_error().decode()
+    assert "bf16 activations only" in msg and "inline scales" in msg, msg
+    good = ffi.matmul_static(n=64, k=512, w_scheme=ffi.IQ3_S, in_dtype=ffi.BF16, out_dtype=ffi.F32)
+    assert ffi.matmul_static_bytes(good, 1) == 64 * 2 * 110 + 512 * 2 + 64 * 4
+    buf = ctypes.create_string_buffer(8192)
+    base = ctypes.addressof(buf) + (-ctypes.addressof(buf) % 16)
+    rc = lib.r9vx_repack_launch(ffi.IQ3_S, base, 1, 256, base + 1024, base + 2048, None)
+    assert rc == -1 and "scales must be NULL for IQ3_S" in lib.r9vx_last_error().decode()
+    rc = lib.r9vx_repack_launch(ffi.IQ3_S, base, 4, 256, base + 16, None, None)
+    assert rc == -1 and "must not overlap" in lib.r9vx_last_error().decode()
+    rc = lib.r9vx_repack_launch(ffi.IQ3_S, base, 1, 300, base + 1024, None, None)
+    assert rc == -1 and "multiple of 256" in lib.r9vx_last_error().decode()
+
+
 def test_swiglu_epilogue_refusals_and_figures():
     lib = ffi.load()
     st = ffi.matmul_static(n=64, k=512, w_scheme=ffi.Q4_K, in_dtype=ffi.F32, out_dtype=ffi.F32, m_bucket=16,

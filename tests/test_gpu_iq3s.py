@@ -1,0 +1,148 @@
+"""GPU parity of the IQ3_S path (GGUF IQ3_S experts and projections,
+crates/r9v-format/src/iq.rs:698-722), through the C ABI.
+
+- wire decode is bit-exact with the oracle and with the reference's golden
+  case (iq_a24_reference.txt, gguf-py 0.19.0);
+- the load-time repack (r9vx_repack_launch) writes the 112-byte device block
+  (qs 64 | signs 32 | qh 8 | scales 4 | d 2 | 0 0) bit for bit;
+- the decode GEMV, its SwiGLU form and the prefill GEMM on the repacked
+  blocks meet the oracle (f32 decode, then the ascending-K dot of
+  crates/r9v-t0/src/matmul.rs:1940-2414) at the north-star tolerance.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle_ffi as O
+from golden_io import iq4_cases
+from r9v_amd import ffi, synth
+from tol import check_bf16_out, check_close
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+IQ3_S = ffi.IQ3_S
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def bf16_dev(bits):
+    return dev(bits.view(np.int16)).view(torch.bfloat16)
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+def device_blocks_np(wire):
+    """The 112-byte device block restated in numpy from the wire field offsets
+    (d 0:2, qs 2:66, qh 66:74, signs 74:106, scales 106:110)."""
+    b = wire.reshape(-1, 110)
+    z = np.zeros((b.shape[0], 2), dtype=np.uint8)
+    return np.concatenate([b[:, 2:66], b[:, 74:106], b[:, 66:74], b[:, 106:110], b[:, 0:2], z], axis=1).reshape(-1)
+
+
+def test_dequantize_golden_case():
+    c = iq4_cases()["IQ3_S"]
+    got = host(ffi.dequantize(dev(np.ascontiguousarray(c["wire"])), IQ3_S, c["n"], c["k"]))
+    assert np.array_equal(got.reshape(-1).view(np.uint32), c["y_bits"])
+
+
+def test_dequantize_bit_exact_random():
+    n, k = 41, 2048
+    w = synth.quant_weights(IQ3_S, 919, n, k)
+    got = host(ffi.dequantize(dev(w), IQ3_S, n, k))
+    assert np.array_equal(got.view(np.uint32), O.dequantize(IQ3_S, w, n, k).view(np.uint32))
+
+
+def test_validate_counts_nonfinite_d():
+    n, k = 3, 1024
+    w = synth.quant_weights(IQ3_S, 17, n, k).reshape(-1, 110).copy()
+    for b, bits in ((0, 0x7C00), (7, 0xFE00), (11, 0xFC00)):
+        w[b, 0:2] = np.frombuffer(np.uint16(bits).tobytes(), np.uint8)
+    assert ffi.validate_weights(dev(w.reshape(-1)), IQ3_S, n, k) == 3
+
+
+def test_repack_writes_the_device_block():
+    n, k = 29, 1536
+    w = synth.quant_weights(IQ3_S, 616, n, k)
+    body, scales = ffi.repack(dev(w), IQ3_S, n, k)
+    assert scales is None
+    assert np.array_equal(host(body), device_blocks_np(w))
+
+
+SHAPES = [(4096, 4096, 1), (1024, 4096, 5), (5120, 2048, 3), (333, 1280, 8), (64, 256, 2),
+          (777, 3072, 4), (2048, 2048, 7), (2600, 14336, 1), (3000, 8192, 6)]
+
+
+@pytest.mark.parametrize("n,k,m", SHAPES)
+def test_gemv_parity(n, k, m):
+    w = synth.quant_weights(IQ3_S, 1000 + n + m, n, k)
+    x = synth.normal_bf16(2000 + k + m, (m, k))
+    body, _ = ffi.repack(dev(w), IQ3_S, n, k)
+    y = host(ffi.matmul(body, IQ3_S, n, k, bf16_dev(x)))
+    check_close(y, O.matmul(IQ3_S, w, n, k, x, O.BF16, threads=8), f"n={n} k={k} m={m}")
+
+
+def test_gemv_epilogues_and_bf16_out():
+    n, k, m = 640, 2048, 3
+    w = synth.quant_weights(IQ3_S, 31, n, k)
+    x = synth.normal_bf16(32, (m, k))
+    body, _ = ffi.repack(dev(w), IQ3_S, n, k)
+    bias = synth.normal_f32(33, (n,))
+    res = synth.normal_f32(34, (m, n))
+    yb = host(ffi.matmul(body, IQ3_S, n, k, bf16_dev(x), bias=dev(bias)))
+    check_close(yb, O.matmul(IQ3_S, w, n, k, x, O.BF16, bias=bias), "bias")
+    yr = host(ffi.matmul(body, IQ3_S, n, k, bf16_dev(x), residual=dev(res)))
+    check_close(yr, O.matmul(IQ3_S, w, n, k, x, O.BF16, residual=res), "residual")
+    y16 = ffi.matmul(body, IQ3_S, n, k, bf16_dev(x), out_dtype=ffi.BF16)
+    y32 = host(ffi.matmul(body, IQ3_S, n, k, bf16_dev(x)))
+    got16 = host(y16.view(torch.int16)).view(np.uint16).astype(np.uint32) << 16
+    check_bf16_out(got16.view(np.float32), y32, O.matmul(IQ3_S, w, n, k, x, O.BF16), "bf16 out")
+
+
+@pytest.mark.parametrize("n,k,m", [(768, 2048, 1), (2816, 2048, 4), (512, 4096, 8)])
+def test_gemv_swiglu_parity(n, k, m):
+    w = synth.quant_weights(IQ3_S, 51 + n, 2 * n, k)
+    x = synth.normal_bf16(52 + m, (m, k))
+    body, _ = ffi.repack(dev(w), IQ3_S, 2 * n, k)
+    y = host(ffi.matmul(body, IQ3_S, n, k, bf16_dev(x), swiglu=True))
+    check_close(y, O.matmul_swiglu(IQ3_S, w, n, k, x, O.BF16), f"swiglu n={n} m={m}")
+
+
+def test_gemv_row_and_batch_invariance():
+    n, k = 1500, 2048
+    w = synth.quant_weights(IQ3_S, 41, n, k)
+    x = synth.normal_bf16(42, (6, k))
+    body, _ = ffi.repack(dev(w), IQ3_S, n, k)
+    full = host(ffi.matmul(body, IQ3_S, n, k, bf16_dev(x)))
+    for r in range(6):
+        one = host(ffi.matmul(body, IQ3_S, n, k, bf16_dev(x[r:r + 1])))
+        assert np.array_equal(one.view(np.uint32), full[r:r + 1].view(np.uint32)), r
+
+
+PREFILL = [(9, 320, 2048), (40, 1000, 4096), (300, 512, 2048), (129, 2304, 1024)]
+
+
+@pytest.mark.parametrize("m,n,k", PREFILL)
+def test_prefill_gemm_parity(m, n, k):
+    w = synth.quant_weights(IQ3_S, 3000 + m + n, n, k)
+    x = synth.normal_bf16(4000 + m + k, (m, k))
+    body, _ = ffi.repack(dev(w), IQ3_S, n, k)
+    y = host(ffi.matmul(body, IQ3_S, n, k, bf16_dev(x)))
+    check_close(y, O.matmul(IQ3_S, w, n, k, x, O.BF16, threads=8), f"m={m} n={n} k={k}")
+
+
+def test_prefill_gemm_large_sampled():
+    m, n, k = 1024, 4096, 4096
+    w = synth.quant_weights(IQ3_S, 5151, n, k)
+    x = synth.normal_bf16(5152, (m, k))
+    res = synth.normal_f32(5153, (m, n))
+    body, _ = ffi.repack(dev(w), IQ3_S, n, k)
+    y = host(ffi.matmul(body, IQ3_S, n, k, bf16_dev(x), residual=dev(res)))
+    rows = np.array([0, 1, 127, 128, 511, 640, 1000, 1023])
+    ref = O.matmul(IQ3_S, w, n, k, x[rows], O.BF16, residual=res[rows], threads=8)
+    check_close(y[rows], ref, "sampled")
