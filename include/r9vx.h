@@ -223,7 +223,8 @@ typedef struct r9vx_moe_ffn_static {
     uint32_t k_topk;         /* K */
     uint32_t dm;             /* hidden size, multiple of 256 */
     uint32_t dff;            /* expert intermediate size, multiple of 256 */
-    uint32_t gate_up_scheme; /* enum r9vx_scheme of w_gate_up [E+S, 2Dff, Dm] */
+    uint32_t gate_up_scheme; /* enum r9vx_scheme of w_gate_up [E+S, 2Dff, Dm]: Q4_K, IQ4_XS, or
+                              * IQ3_S as the 112-byte repacked blocks of r9vx_repack_launch */
     uint32_t down_scheme;    /* enum r9vx_scheme of w_down [E+S, Dm, Dff] */
     uint32_t in_dtype;       /* BF16 */
     uint32_t out_dtype;      /* F32 */

@@ -21,6 +21,8 @@
  *    in the workspace status word and every kernel that writes y or
  *    intermediate rows returns without writing.
  */
+#include <type_traits>
+
 #include "r9vx_expf.h"
 #include "r9vx_gemv_core.h"
 #include "r9vx_mfma.h"
@@ -400,9 +402,11 @@ __device__ __forceinline__ void advance(Cur &c, uint32_t nseg, uint32_t groups) 
 template <int GU>
 __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
     constexpr int kPairs = kDecPairs;
-    __shared__ uint32_t lut[256];
+    constexpr bool kIq3 = GU == R9VX_SCHEME_IQ3_S;
+    __shared__ __attribute__((aligned(16))) uint32_t lut[kIq3 ? 1024 : 256];
     __shared__ uint64_t etab[R9VX_EXP2F_N];
     if constexpr (GU == R9VX_SCHEME_IQ4_XS) init_iq4_lut(lut, threadIdx.x, blockDim.x);
+    if constexpr (kIq3) build_iq3s_lut(lut, threadIdx.x, blockDim.x);
     r9vx_exp2_fill(etab, threadIdx.x, blockDim.x);
     __syncthreads(); /* the last barrier: waves run independently from here */
     const uint32_t lane = threadIdx.x & 63;
@@ -423,7 +427,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
     uint32_t xpos = ~0u, xseg = ~0u;
     float ag[kPairs][1], au[kPairs][1];
     Cur lc{pos0, u0 % groups, 0u}, c = lc; /* load and compute cursors */
-    r9vx_u32x4 qg[kDecSteps][kPairs], qu[kDecSteps][kPairs];
+    using Pay = typename std::conditional<kIq3, Payload2, r9vx_u32x4>::type;
+    Pay qg[kDecSteps][kPairs], qu[kDecSteps][kPairs];
     Hdr hg[kDecSteps][kPairs], hu[kDecSteps][kPairs];
     for (uint32_t base = 0; base < nsteps; base += kDecSteps) {
         /* 1. every weight load of the batch's steps (steps past the last repeat it) */
@@ -436,8 +441,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
             for (int r = 0; r < kPairs; ++r) {
                 const uint32_t row = (lc.g * kPairs + r) * rpi + slot;
                 const uint32_t rr = row < a.dff ? row : a.dff - 1;
-                load_chunk<GU>(wexp + (uint64_t)rr * a.gu_row_bytes, ci, qg[s][r], hg[s][r]);
-                load_chunk<GU>(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes, ci, qu[s][r], hu[s][r]);
+                if constexpr (kIq3) {
+                    load_chunk_iq3s(wexp + (uint64_t)rr * a.gu_row_bytes, ci, qg[s][r], hg[s][r]);
+                    load_chunk_iq3s(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes, ci, qu[s][r], hu[s][r]);
+                } else {
+                    load_chunk<GU>(wexp + (uint64_t)rr * a.gu_row_bytes, ci, qg[s][r], hg[s][r]);
+                    load_chunk<GU>(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes, ci, qu[s][r], hu[s][r]);
+                }
             }
             if (base + s + 1 < nsteps) advance(lc, nseg, groups);
         }
@@ -462,8 +472,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
                 for (int r = 0; r < kPairs; ++r) ag[r][0] = au[r][0] = 0.f;
 #pragma unroll
             for (int r = 0; r < kPairs; ++r) {
-                chunk_dot<GU, false, 1>(qg[s][r], hg[s][r], ci & 7, xc, ag[r], lut);
-                chunk_dot<GU, false, 1>(qu[s][r], hu[s][r], ci & 7, xc, au[r], lut);
+                if constexpr (kIq3) {
+                    chunk_dot_iq3s<1>(qg[s][r], hg[s][r], ci & 7, xc, ag[r], lut);
+                    chunk_dot_iq3s<1>(qu[s][r], hu[s][r], ci & 7, xc, au[r], lut);
+                } else {
+                    chunk_dot<GU, false, 1>(qg[s][r], hg[s][r], ci & 7, xc, ag[r], lut);
+                    chunk_dot<GU, false, 1>(qu[s][r], hu[s][r], ci & 7, xc, au[r], lut);
+                }
             }
             if (c.seg + 1 == nseg) {
                 float gu[2][kPairs];
@@ -742,7 +757,9 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
     f.y = p.y;
     f.ws = p.ws;
     f.L = L;
-    f.gu_row_bytes = (uint64_t)(p.dm / 256) * (p.scheme_gu == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : R9VX_IQ4XS_BYTES);
+    f.gu_row_bytes = (uint64_t)(p.dm / 256) * (p.scheme_gu == R9VX_SCHEME_Q4_K   ? R9VX_Q4K_BYTES
+                                               : p.scheme_gu == R9VX_SCHEME_IQ3_S ? R9VX_IQ3S_DEV_BYTES
+                                                                                  : R9VX_IQ4XS_BYTES);
     f.dn_row_bytes = (uint64_t)(p.dff / 256) * (p.scheme_dn == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : R9VX_IQ4XS_BYTES);
     f.t = p.t;
     f.e = p.e;
@@ -771,7 +788,9 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
         return dim3((waves + kDecWaves - 1) / kDecWaves);
     };
     const dim3 block(kDecWaves * 64);
-    if (p.scheme_gu == R9VX_SCHEME_IQ4_XS)
+    if (p.scheme_gu == R9VX_SCHEME_IQ3_S)
+        hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_IQ3_S>, grid_for(f.gu_groups, f.gu_upw), block, 0, s, f);
+    else if (p.scheme_gu == R9VX_SCHEME_IQ4_XS)
         hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_IQ4_XS>, grid_for(f.gu_groups, f.gu_upw), block, 0, s, f);
     else
         hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_Q4_K>, grid_for(f.gu_groups, f.gu_upw), block, 0, s, f);

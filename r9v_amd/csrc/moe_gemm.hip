@@ -20,6 +20,7 @@
  * Both GEMMs run the register-decoded main loop of r9vx_mma2.h (4 waves,
  * 128-row tiles, two workgroups per CU).  Tiles past the scanned count exit.
  */
+#include "r9vx_mma.h"
 #include "r9vx_mma2.h"
 #include "r9vx_moe.h"
 
@@ -148,6 +149,70 @@ __global__ __launch_bounds__(256, 2) void moe_gu_mfma_kernel(GroupedArgs a) {
     }
 }
 
+/* IQ3_S gate/up experts: the LDS-decoded main loop of r9vx_mma.h (a 128 x
+ * 256 tile; thread t decodes weight row t of the tile into LDS: threads
+ * 0..127 the gate rows j0..j0+127, threads 128..255 the up rows of the same
+ * columns, so tile column c pairs with column c + 128), with the activations
+ * in natural K order.  The accumulators pass through a 32 x 256 f32 LDS
+ * stage, 32 rows at a time, and each thread writes silu(g) * u for 4
+ * columns of 4 rows. */
+template <int GU>
+__global__ __launch_bounds__(256, 2) void moe_gu_lds_kernel(GroupedArgs a) {
+    using S = MmaShape<kBM, 1>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
+    __shared__ float rowsc[kBM];
+    const uint32_t *status = ws_u32(a, a.L.status);
+    const uint32_t ntile_n = a.dff / 128;
+    const uint32_t tix = blockIdx.x / ntile_n, nt = blockIdx.x % ntile_n;
+    if (status[0] != 0u || tix >= status[3]) return;
+    const r9vx_u32x4 tile = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles)[tix];
+    const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
+    const uint32_t j0 = nt * 128;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid < kBM) rowsc[tid] = tid < rows ? a.xscale[row_token(a, expert, pos0 + tid)] : 0.f;
+
+    AF16Rows<kBM> as;
+    as.chunk = tid & 7;
+    as.row0 = tid >> 3;
+#pragma unroll
+    for (int i = 0; i < (int)kBM / 32; ++i) {
+        const uint32_t r = as.row0 + 32 * i;
+        as.row[i] = a.x16 + (uint64_t)row_token(a, expert, pos0 + (r < rows ? r : 0)) * a.dm + 8 * as.chunk;
+    }
+    const uint64_t wr = tid < 128 ? j0 + tid : (uint64_t)a.dff + j0 + (tid - 128);
+    const uint8_t *wrow = a.w_gu + ((uint64_t)expert * 2 * a.dff + wr) * a.gu_row_bytes;
+    r9vx_f32x16 acc[kBM / 32][2];
+    mma_mainloop<GU, kBM, 1>(lds, as, wrow, a.dm / kTileK, acc);
+
+    constexpr uint32_t kSRow = 260;
+    float *stage = reinterpret_cast<float *>(lds);
+    float *h = reinterpret_cast<float *>(a.ws + a.L.h);
+    const uint32_t c4 = 4 * (tid & 31);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < (int)kBM / 32; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) stage[acc_row(0, r, lane) * kSRow + acc_col(wave, j, lane)] = acc[i][j][r];
+        __syncthreads();
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t rl = (tid >> 5) + 8 * q, row = 32 * i + rl;
+            if (row >= rows) continue;
+            const float sc = rowsc[row];
+            const r9vx_f32x4 g4 = *reinterpret_cast<const r9vx_f32x4 *>(stage + rl * kSRow + c4);
+            const r9vx_f32x4 u4 = *reinterpret_cast<const r9vx_f32x4 *>(stage + rl * kSRow + 128 + c4);
+            const float gv[4] = {g4.x * sc, g4.y * sc, g4.z * sc, g4.w * sc};
+            const float uv[4] = {u4.x * sc, u4.y * sc, u4.z * sc, u4.w * sc};
+            float v[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[c] = gv[c] / (1.0f + __expf(-gv[c])) * uv[c];
+            *reinterpret_cast<r9vx_f32x4 *>(h + (uint64_t)(pos0 + row) * a.dff + j0 + c4) = r9vx_f32x4{v[0], v[1], v[2], v[3]};
+        }
+        __syncthreads();
+    }
+}
+
 /* ---------------------------------------------------------------- h -> fp16 */
 
 /* One wave per h row: max|h| over the row (kept in hmax for the down GEMM's
@@ -238,7 +303,9 @@ int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStr
     a.w_dn = p.w_dn;
     a.ws = p.ws;
     a.L = L;
-    a.gu_row_bytes = (uint64_t)(p.dm / 256) * (p.scheme_gu == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : R9VX_IQ4XS_BYTES);
+    a.gu_row_bytes = (uint64_t)(p.dm / 256) * (p.scheme_gu == R9VX_SCHEME_Q4_K   ? R9VX_Q4K_BYTES
+                                               : p.scheme_gu == R9VX_SCHEME_IQ3_S ? R9VX_IQ3S_DEV_BYTES
+                                                                                  : R9VX_IQ4XS_BYTES);
     a.dn_row_bytes = (uint64_t)(p.dff / 256) * (p.scheme_dn == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : R9VX_IQ4XS_BYTES);
     a.t = p.t;
     a.e = p.e;
@@ -254,7 +321,9 @@ int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStr
     /* upper bound on row tiles: ceil(P/128) + one partial tile per work item */
     const uint32_t max_tiles = (a.p + kBM - 1) / kBM + (a.p < p.e ? a.p : p.e) + (p.shared ? p.shared * ((p.t + kBM - 1) / kBM) : 0);
     dim3 ggu(max_tiles * (p.dff / 128)), gdn(max_tiles * (p.dm / 256));
-    if (p.scheme_gu == R9VX_SCHEME_IQ4_XS)
+    if (p.scheme_gu == R9VX_SCHEME_IQ3_S)
+        hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_IQ3_S>, ggu, dim3(256), 0, s, a);
+    else if (p.scheme_gu == R9VX_SCHEME_IQ4_XS)
         hipLaunchKernelGGL(moe_gu_mfma_kernel<R9VX_SCHEME_IQ4_XS>, ggu, dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL(moe_gu_mfma_kernel<R9VX_SCHEME_Q4_K>, ggu, dim3(256), 0, s, a);

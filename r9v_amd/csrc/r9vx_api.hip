@@ -416,7 +416,8 @@ static void check_ffn_static(const r9vx_moe_ffn_static *st, Problems &pr) {
     if (st->k_topk == 0 || st->k_topk > kMoeMaxK) pr.add(R9VX_ERR_INVALID, "K=%u must be in 1..32", st->k_topk);
     if (st->dm == 0 || st->dm % 256) pr.add(R9VX_ERR_INVALID, "Dm=%u must be a positive multiple of 256", st->dm);
     if (st->dff == 0 || st->dff % 256) pr.add(R9VX_ERR_INVALID, "Dff=%u must be a positive multiple of 256", st->dff);
-    if (!known_scheme(st->gate_up_scheme)) pr.add(R9VX_ERR_UNSUPPORTED, "gate_up_scheme %u", st->gate_up_scheme);
+    if (!known_scheme(st->gate_up_scheme) && !packed_scheme(st->gate_up_scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "gate_up_scheme %u: Q4_K (12), IQ4_XS (23) or IQ3_S (21)", st->gate_up_scheme);
     if (!known_scheme(st->down_scheme)) pr.add(R9VX_ERR_UNSUPPORTED, "down_scheme %u", st->down_scheme);
     if (st->in_dtype != R9VX_DTYPE_BF16) pr.add(R9VX_ERR_UNSUPPORTED, "in_dtype %u: bf16 activations only", st->in_dtype);
     if (st->out_dtype != R9VX_DTYPE_F32) pr.add(R9VX_ERR_UNSUPPORTED, "out_dtype %u: f32 output only", st->out_dtype);

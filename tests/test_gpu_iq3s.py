@@ -146,3 +146,24 @@ def test_prefill_gemm_large_sampled():
     rows = np.array([0, 1, 127, 128, 511, 640, 1000, 1023])
     ref = O.matmul(IQ3_S, w, n, k, x[rows], O.BF16, residual=res[rows], threads=8)
     check_close(y[rows], ref, "sampled")
+
+
+@pytest.mark.parametrize("t,shared,dn", [(3, 0, ffi.Q4_K), (8, 1, ffi.IQ4_XS), (300, 0, ffi.Q4_K),
+                                         (300, 1, ffi.IQ4_XS)])
+def test_moe_ffn_iq3s_gate_up_experts(t, shared, dn):
+    """IQ3_S gate/up experts (repacked) with Q4_K / IQ4_XS down experts:
+    t <= 8 runs the decode kernels, larger t the grouped MFMA GEMMs."""
+    e, dm, dff, k = 6, 512, 256, 2
+    ea = e + shared
+    gu = synth.quant_weights(IQ3_S, 700 + t, ea * 2 * dff, dm)
+    down = synth.quant_weights(dn, 800 + t, ea * dm, dff)
+    logits = synth.normal_f32(31 + t, (t, e))
+    ids, w = O.moe_route(logits, k)
+    x = synth.normal_bf16(32 + t, (t, dm))
+    gu_dev, _ = ffi.repack(dev(gu), IQ3_S, ea * 2 * dff, dm)
+    y, ws, st = ffi.moe_ffn(bf16_dev(x), dev(ids.view(np.int32)), dev(w), gu_dev, dev(down), e, dff,
+                            shared=shared, gate_up_scheme=IQ3_S, down_scheme=dn)
+    torch.cuda.synchronize()
+    assert ffi.moe_ffn_status(st, ws) == 0
+    ref = O.moe_ffn(x, O.BF16, ids, w, e, dff, gu, down, scheme_gu=IQ3_S, scheme_dn=dn, shared=shared)
+    check_close(host(y), ref, f"moe t={t} shared={shared}")
