@@ -283,7 +283,7 @@ def bench_c4(torch, ffi, synth, gsynth, steps):
 def bench_paths(torch, ffi, synth):
     """The paths beyond configs[0..4], timed at their documented shapes (run
     with --only paths; not part of the default run): Q6_K / Q8_0 decode GEMVs
-    and prefill GEMMs on the split layout, the gated (SwiGLU) GEMV over
+    and prefill GEMMs on the split layout, IQ3_S ones on its 112-byte blocks, the gated (SwiGLU) GEMV over
     stacked gate/up rows, and routing from hidden states."""
     out = {}
 
@@ -292,14 +292,20 @@ def bench_paths(torch, ffi, synth):
         if scheme in ffi.SPLIT_SCHEMES:
             body, scales = ffi.repack(wire, scheme, rows, k)
             return [(body, scales)] + [(body.clone(), scales.clone()) for _ in range(copies - 1)]
+        if scheme == ffi.IQ3_S:  # the 112-byte device blocks
+            body, _ = ffi.repack(wire, scheme, rows, k)
+            return [(body, None)] + [(body.clone(), None) for _ in range(copies - 1)]
         return [(wire, None)] + [(wire.clone(), None) for _ in range(copies - 1)]
 
     def wbytes(scheme, rows, k):
-        return rows * (k // ffi.BLOCK_LEN[scheme]) * ffi.BLOCK_BYTES[scheme]
+        bb = ffi.IQ3S_DEV_BYTES if scheme == ffi.IQ3_S else ffi.BLOCK_BYTES[scheme]
+        return rows * (k // ffi.BLOCK_LEN[scheme]) * bb
 
     for name, scheme, n, k, m in (("q6k_head_gemv", ffi.Q6_K, 32768, 4096, 1),
                                   ("q8_0_proj_gemv", ffi.Q8_0, 14336, 4096, 1),
-                                  ("q6k_gemv_c1shape", ffi.Q6_K, 5120, 2048, 1)):
+                                  ("q6k_gemv_c1shape", ffi.Q6_K, 5120, 2048, 1),
+                                  ("iq3s_proj_gemv", ffi.IQ3_S, 14336, 4096, 1),
+                                  ("iq3s_gemv_c1shape", ffi.IQ3_S, 5120, 2048, 1)):
         nb = wbytes(scheme, n, k)
         ws = weights(scheme, n, k, 11, copies_for(nb))
         x = torch.from_numpy(synth.normal_bf16(3, (m, k)).view(np.int16)).cuda().view(torch.bfloat16)
@@ -322,7 +328,8 @@ def bench_paths(torch, ffi, synth):
         log(f"  swiglu m{mm} {out[f'swiglu_gemv_m{mm}']}")
         del ws
         torch.cuda.empty_cache()
-    for name, scheme in (("q6k_prefill_gemm", ffi.Q6_K), ("q8_0_prefill_gemm", ffi.Q8_0)):
+    for name, scheme in (("q6k_prefill_gemm", ffi.Q6_K), ("q8_0_prefill_gemm", ffi.Q8_0),
+                         ("iq3s_prefill_gemm", ffi.IQ3_S)):
         m, n, k = 2048, 14336, 4096
         (w, sc), = weights(scheme, n, k, 13, 1)
         x = torch.from_numpy(synth.normal_bf16(5, (m, k)).view(np.int16)).cuda().view(torch.bfloat16)
@@ -367,7 +374,7 @@ def bench_ceilings(torch, ffi):
     return out
 
 
-HEAD_KERNEL = "gemv_kernel<23, 5, false, 1, 6, 5>"  # IQ4_XS (type 23), M = 5, bf16 x, 1 chunk per lane, 64 lanes per row, 5 rows per lane group
+HEAD_KERNEL = "gemv_kernel<23, 5, false, 1, 6, 5, 1>"  # IQ4_XS (type 23), M = 5, bf16 x, 1 chunk per lane, 64 lanes per row, 5 rows per lane group, one K segment
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_iq4xs_k2048_n5120_m5_traffic.txt")
 PMC_COPY_BYTES = 64 << 20
 

@@ -582,6 +582,8 @@ int entry_range(const char *op, const r9vx_gguf *f, const char *name, const uint
 
 bool path_scheme(uint32_t type) { return type == R9VX_SCHEME_Q4_K || type == R9VX_SCHEME_IQ4_XS; }
 bool split_type(uint32_t type) { return type == R9VX_SCHEME_Q8_0 || type == R9VX_SCHEME_Q6_K; }
+/* IQ3_S: uploaded as wire blocks, then repacked on the device (r9vx_repack_launch) */
+bool repack_type(uint32_t type) { return type == R9VX_SCHEME_IQ3_S; }
 
 std::string dims_text(const Tensor &t) {
     std::string s = "{";
@@ -817,10 +819,10 @@ int r9vx_gguf_matmul_static(const r9vx_gguf *f, const char *name, r9vx_matmul_st
     if (!f || !name || !st) return refuse(op, R9VX_ERR_NULL, "file, name and static are required");
     const Tensor *t = f->tensor(name);
     if (!t) return refuse(op, R9VX_ERR_INVALID, std::string("no tensor named \"") + name + "\"");
-    if (!path_scheme(t->type) && !split_type(t->type))
+    if (!path_scheme(t->type) && !split_type(t->type) && !repack_type(t->type))
         return refuse(op, R9VX_ERR_UNSUPPORTED,
                       "tensor \"" + t->name + "\" is " + r9vx_gguf_type_name(t->type) +
-                          "; this path multiplies Q4_K (12), IQ4_XS (23), Q6_K (14) and Q8_0 (8) weights");
+                          "; this path multiplies Q4_K (12), IQ4_XS (23), Q6_K (14), Q8_0 (8) and IQ3_S (21) weights");
     if (t->dims.size() != 2 || t->dims[0] > UINT32_MAX || t->dims[1] > UINT32_MAX)
         return refuse(op, R9VX_ERR_INVALID,
                       "tensor \"" + t->name + "\" dims " + dims_text(*t) + " are not a {K, N} matrix of u32 sizes");
@@ -840,15 +842,16 @@ int r9vx_gguf_moe_ffn_static(const r9vx_gguf *f, const char *gate, const char *u
     if (!f || !gate || !down || !st) return refuse(op, R9VX_ERR_NULL, "file, gate, down and static are required");
     const Tensor *g = f->tensor(gate), *u = up ? f->tensor(up) : nullptr, *d = f->tensor(down);
     std::vector<Problem> pr;
-    auto need = [&](const Tensor *t, const char *name) {
+    auto need = [&](const Tensor *t, const char *name, bool gate_up) {
         if (!t) {
             pr.push_back({0, R9VX_ERR_INVALID, std::string("no tensor named \"") + name + "\""});
             return false;
         }
         bool ok = true;
-        if (!path_scheme(t->type)) {
+        if (!path_scheme(t->type) && !(gate_up && repack_type(t->type))) {
             pr.push_back({0, R9VX_ERR_UNSUPPORTED, "tensor \"" + t->name + "\" is " + r9vx_gguf_type_name(t->type) +
-                                                       "; experts must be Q4_K (12) or IQ4_XS (23)"});
+                                                       (gate_up ? "; gate/up experts must be Q4_K (12), IQ4_XS (23) or IQ3_S (21)"
+                                                                : "; down experts must be Q4_K (12) or IQ4_XS (23)")});
             ok = false;
         }
         if (t->dims.size() != 3 || t->dims[0] > UINT32_MAX || t->dims[1] > UINT32_MAX || t->dims[2] > UINT32_MAX) {
@@ -858,8 +861,8 @@ int r9vx_gguf_moe_ffn_static(const r9vx_gguf *f, const char *gate, const char *u
         }
         return ok;
     };
-    const bool gok = need(g, gate), dok = need(d, down);
-    const bool uok = up ? need(u, up) : true;
+    const bool gok = need(g, gate, true), dok = need(d, down, false);
+    const bool uok = up ? need(u, up, true) : true;
     if (gok && dok && uok) {
         const uint64_t dm = g->dims[0], e = g->dims[2];
         uint64_t dff = g->dims[1];
@@ -972,11 +975,12 @@ int r9vx_gguf_upload_gate_up(const r9vx_gguf *gate_file, const uint8_t *gate_byt
     if (rc != R9VX_OK) return rc;
     rc = entry_range(op, up_file, up, up_bytes, up_len, &u, &udata);
     if (rc != R9VX_OK) return rc;
-    if (!path_scheme(g->type) || g->dims.size() != 3 || u->dims != g->dims || u->type != g->type)
+    if ((!path_scheme(g->type) && !repack_type(g->type)) || g->dims.size() != 3 || u->dims != g->dims ||
+        u->type != g->type)
         return refuse(op, R9VX_ERR_INVALID,
                       "gate \"" + g->name + "\" " + dims_text(*g) + " " + r9vx_gguf_type_name(g->type) + " and up \"" +
                           u->name + "\" " + dims_text(*u) + " " + r9vx_gguf_type_name(u->type) +
-                          " must be stacked Q4_K / IQ4_XS experts {K, rows, E} of one dims and type");
+                          " must be stacked Q4_K / IQ4_XS / IQ3_S experts {K, rows, E} of one dims and type");
     if (!dst) return refuse(op, R9VX_ERR_NULL, "dst is NULL");
     if (dst_bytes / 2 < g->nbytes)
         return refuse(op, R9VX_ERR_INVALID,

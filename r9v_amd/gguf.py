@@ -407,7 +407,8 @@ def upload_split(file: GgufFile, data, name: str, stream=None):
 def load_matmul_weight(file: GgufFile, data, name: str, m_bucket: int = 8, in_dtype: int = ffi.BF16,
                        out_dtype: int = ffi.F32, validate: bool = True):
     """(MatmulStatic, w, w_scales) on the device for weight `name`: Q4_K /
-    IQ4_XS wire blocks (w_scales None) or the Q8_0 / Q6_K split layout.  With
+    IQ4_XS wire blocks (w_scales None), the Q8_0 / Q6_K split layout, or
+    IQ3_S repacked on the device into 112-byte blocks (w_scales None).  With
     `validate` the load-time scale check (check_wire_f16,
     crates/r9v-format/src/ggml.rs:421) refuses a block with a non-finite scale
     (on the device for wire blocks; the split upload always checks)."""
@@ -420,6 +421,8 @@ def load_matmul_weight(file: GgufFile, data, name: str, m_bucket: int = 8, in_dt
         bad = ffi.validate_weights(w, st.w_scheme, st.n, st.k)
         if bad:
             raise GgufError(-1, f"{name}: {bad} block(s) carry a non-finite scale")
+    if st.w_scheme == ffi.IQ3_S:  # wire blocks -> the 112-byte device blocks
+        w, _ = ffi.repack(w, ffi.IQ3_S, st.n, st.k)
     return st, w, None
 
 
@@ -438,6 +441,8 @@ def load_moe_experts(file: GgufFile, data, gate: str, up: str | None, down: str,
         bad += ffi.validate_weights(w_down, st.down_scheme, st.e_local * st.dm, st.dff)
         if bad:
             raise GgufError(-1, f"{gate}/{down}: {bad} expert block(s) carry a non-finite scale")
+    if st.gate_up_scheme == ffi.IQ3_S:  # wire blocks -> the 112-byte device blocks
+        w_gate_up, _ = ffi.repack(w_gate_up, ffi.IQ3_S, st.e_local * 2 * st.dff, st.dm)
     return st, w_gate_up, w_down
 
 

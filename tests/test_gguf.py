@@ -394,6 +394,9 @@ def _model_file():
         ("blk.0.attn_k_f16.weight", (256, 2), 1, bytes(1024)),
         ("blk.0.attn_v.weight", (512, 2), 8, bytes(2 * 16 * 34)),
         ("blk.0.ffn_up_bad.weight", (dm, dff, e), 12, bytes(e * dff * (dm // 256) * 144)),
+        ("blk.0.attn_o_iq3.weight", (512, 2), 21, bytes(2 * 2 * 110)),
+        ("blk.0.ffn_gate_iq3_exps.weight", (dm, dff, e), 21, bytes(e * dff * (dm // 256) * 110)),
+        ("blk.0.ffn_down_iq3_exps.weight", (dff, dm, e), 21, bytes(e * dm * (dff // 256) * 110)),
     ]
     return build([("general.architecture", (8, "llama"))], tensors)
 
@@ -420,6 +423,14 @@ def test_matmul_and_moe_ffn_statics_from_a_checkpoint():
     with pytest.raises(gguf.GgufError, match="must agree in dims and type"):
         f.moe_ffn_static("blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_bad.weight", "blk.0.ffn_down_exps.weight",
                          8, 2)
+    st3 = f.matmul_static("blk.0.attn_o_iq3.weight")
+    assert (st3.n, st3.k, st3.w_scheme) == (2, 512, ffi.IQ3_S)
+    s3 = f.moe_ffn_static("blk.0.ffn_gate_iq3_exps.weight", "blk.0.ffn_gate_iq3_exps.weight",
+                          "blk.0.ffn_down_exps.weight", t_bucket=8, k=2)
+    assert (s3.gate_up_scheme, s3.down_scheme) == (ffi.IQ3_S, ffi.Q4_K)
+    with pytest.raises(gguf.GgufError, match="down experts must be Q4_K"):
+        f.moe_ffn_static("blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_exps.weight",
+                         "blk.0.ffn_down_iq3_exps.weight", 8, 2)
     with pytest.raises(gguf.GgufError, match="must be \\{256, 512, 3\\}"):
         f.moe_ffn_static("blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_exps.weight", "blk.0.ffn_gate_exps.weight",
                          8, 2)

@@ -16,7 +16,8 @@ import pytest
 
 import oracle_ffi as O
 from golden_io import iq4_cases
-from r9v_amd import ffi, synth
+from gguf_build import build
+from r9v_amd import ffi, gguf, synth
 from tol import check_bf16_out, check_close
 
 pytestmark = pytest.mark.gpu
@@ -167,3 +168,35 @@ def test_moe_ffn_iq3s_gate_up_experts(t, shared, dn):
     assert ffi.moe_ffn_status(st, ws) == 0
     ref = O.moe_ffn(x, O.BF16, ids, w, e, dff, gu, down, scheme_gu=IQ3_S, scheme_dn=dn, shared=shared)
     check_close(host(y), ref, f"moe t={t} shared={shared}")
+
+
+def test_gguf_loads_repack_iq3s_weights_and_experts():
+    """IQ3_S tensors of a checkpoint: load_matmul_weight and load_moe_experts
+    upload the wire blocks, check every d, and repack them on the device."""
+    n, k = 320, 2048
+    wq = synth.quant_weights(IQ3_S, 61, n, k)
+    e, dm, dff = 4, 512, 256
+    gate = synth.quant_weights(IQ3_S, 62, e * dff, dm)
+    up = synth.quant_weights(IQ3_S, 63, e * dff, dm)
+    down = synth.quant_weights(ffi.Q4_K, 64, e * dm, dff)
+    b = build([("general.architecture", (8, "qwen3moe"))], [
+        ("blk.0.attn_o.weight", (k, n), 21, wq.tobytes()),
+        ("blk.0.ffn_gate_exps.weight", (dm, dff, e), 21, gate.tobytes()),
+        ("blk.0.ffn_up_exps.weight", (dm, dff, e), 21, up.tobytes()),
+        ("blk.0.ffn_down_exps.weight", (dff, dm, e), 12, down.tobytes())])
+    f = gguf.GgufFile.parse(b)
+    st, w, ws = gguf.load_matmul_weight(f, b, "blk.0.attn_o.weight", m_bucket=2)
+    assert ws is None and st.w_scheme == IQ3_S
+    assert np.array_equal(host(w), device_blocks_np(wq))
+    x = synth.normal_bf16(65, (2, k))
+    check_close(host(ffi.matmul(w, IQ3_S, n, k, bf16_dev(x))), O.matmul(IQ3_S, wq, n, k, x, O.BF16), "loaded")
+    fst, w_gu, w_dn = gguf.load_moe_experts(f, b, "blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_exps.weight",
+                                            "blk.0.ffn_down_exps.weight", t_bucket=16, k=2)
+    stacked = np.concatenate([gate.reshape(e, dff, -1), up.reshape(e, dff, -1)], axis=1).reshape(-1)
+    assert np.array_equal(host(w_gu), device_blocks_np(stacked))
+    assert (fst.gate_up_scheme, fst.down_scheme) == (IQ3_S, ffi.Q4_K)
+    bad = wq.reshape(-1, 110).copy()
+    bad[5, 0:2] = np.frombuffer(np.uint16(0x7C00).tobytes(), np.uint8)
+    b2 = build([], [("w", (k, n), 21, bad.tobytes())])
+    with pytest.raises(gguf.GgufError, match="1 block"):
+        gguf.load_matmul_weight(gguf.GgufFile.parse(b2), b2, "w")
