@@ -24,8 +24,11 @@
  *  - data-dependent refusals that only the device can see (non-finite router
  *    logits, expert ids >= E) follow T0's refuse-before-mutation rule: a
  *    check pass sets a status word and the compute kernels then write
- *    nothing.  The word is read back with r9vx_moe_route_status /
- *    r9vx_moe_ffn_status.
+ *    nothing.  Each launch owns its status word: moe_ffn's lives in its
+ *    workspace, r9vx_moe_route_launch_ex takes one from the caller, and
+ *    r9vx_moe_route_hidden_launch keeps one in its workspace.  The plain
+ *    r9vx_moe_route_launch uses one word per device shared by every plain
+ *    launch, so concurrent routings on different streams must use the _ex form.
  */
 #ifndef R9VX_H
 #define R9VX_H
@@ -45,8 +48,32 @@ enum r9vx_dtype {
     R9VX_DTYPE_F32 = 0,
     R9VX_DTYPE_F16 = 1,
     R9VX_DTYPE_BF16 = 2,
+    R9VX_DTYPE_I8 = 5, /* weight element type of Q8_0 / Q6_K blocks */
+    R9VX_DTYPE_I4 = 6, /* weight element type of Q4_K / IQ4_XS / IQ3_S blocks */
     R9VX_DTYPE_U32 = 8
 };
+
+/* Weight layouts: LayoutId codes (crates/r9v-ir/src/layout.rs:16-38).  0-3
+ * are the reference's own layouts (contiguous, row-major L0, tiled L1, tiled
+ * 2:4-sparse L1S) and are refused by every entry point here: an L1 tensor in
+ * `w` would otherwise be misread.  This path reads weights in the layouts
+ * below, one per scheme, and a static must name the one its scheme needs. */
+enum r9vx_layout {
+    R9VX_LAYOUT_CONTIGUOUS = 0,
+    R9VX_LAYOUT_L0 = 1,
+    R9VX_LAYOUT_L1 = 2,
+    R9VX_LAYOUT_L1S = 3,
+    R9VX_LAYOUT_GGUF_WIRE = 0x100, /* Q4_K / IQ4_XS: the GGUF blocks as stored in the file */
+    R9VX_LAYOUT_SPLIT = 0x101,     /* Q8_0 / Q6_K: body + f16 d array (r9vx_repack_launch) */
+    R9VX_LAYOUT_IQ3S_112 = 0x102   /* IQ3_S: 112-byte blocks (r9vx_repack_launch) */
+};
+
+/* Activation quantization scheme (QuantScheme, crates/r9v-ir/src/quant.rs:48-62):
+ * this path takes unquantized activations only. */
+#define R9VX_ACT_SCHEME_NONE 0u
+
+/* Placement (PlacementKind, crates/r9v-registry/src/types.rs:506-513): device only. */
+#define R9VX_PLACEMENT_DEVICE 0u
 
 /* Weight schemes: GGUF ggml type codes (crates/r9v-format/src/ggml.rs:38;
  * codes checked by crates/r9v-format/tests/iq.rs:131-141). */
@@ -109,16 +136,23 @@ enum r9vx_act { R9VX_ACT_SILU = 0 };
 
 /* ------------------------------------------------------------------ matmul */
 
-/* Variant key subset of MatmulStatic (crates/r9v-registry/src/types.rs:727-770). */
+/* MatmulStatic (crates/r9v-registry/src/types.rs:727-770), every variant key
+ * in its declaration order; bool keys are u32 0 / 1. */
 typedef struct r9vx_matmul_static {
     uint32_t m_bucket;       /* M bucket; the launch's dynamic m <= m_bucket */
     uint32_t n;              /* output columns N */
     uint32_t k;              /* reduction length K, a multiple of 256 */
-    uint32_t w_scheme;       /* enum r9vx_scheme: Q4_K / IQ4_XS wire blocks, or Q8_0 / Q6_K split */
+    uint32_t w_dtype;        /* I4 for Q4_K / IQ4_XS / IQ3_S, I8 for Q8_0 / Q6_K */
+    uint32_t w_scheme;       /* enum r9vx_scheme */
+    uint32_t w_layout;       /* enum r9vx_layout: GGUF_WIRE, SPLIT or IQ3S_112 as the scheme requires */
     uint32_t in_dtype;       /* F32 (m <= 8 GEMV only) or BF16 */
+    uint32_t act_scheme;     /* R9VX_ACT_SCHEME_NONE */
     uint32_t out_dtype;      /* F32 or BF16 (RNE) */
     uint32_t epilogue;       /* enum r9vx_epilogue */
     uint32_t residual_dtype; /* F32 when epilogue == RESIDUAL */
+    uint32_t transpose_w;    /* 0: w is [N, K] */
+    uint32_t interleave;     /* 0 */
+    uint32_t sparse;         /* 0 */
 } r9vx_matmul_static;
 
 /* matmul ABI struct (crates/r9v-kgen/src/abi/per_op.rs:794-868). */
@@ -177,10 +211,25 @@ typedef struct r9vx_moe_route_args {
  * (crates/r9v-t0/src/moe_route.rs:89-419).  Ids are bit-exact with T0. */
 int r9vx_moe_route_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_args *args,
                           r9vx_stream_t stream);
-/* Synchronises `stream`, returns the device status bits of the last
- * moe_route launch on this device in *status and clears them. */
+/* The same launch with a caller-owned status word: `status` is a device u32
+ * (4-byte aligned) that this launch overwrites with its own status bits
+ * (0 when it routed every row).  Launches with distinct words may run
+ * concurrently on different streams; read the word back after the stream
+ * reaches the launch (r9vx_status_read).  No counterpart in the reference,
+ * whose T0 refusal is a returned error: this is that error's device form. */
+int r9vx_moe_route_launch_ex(const r9vx_moe_route_static *st, const r9vx_moe_route_args *args,
+                             uint32_t *status, r9vx_stream_t stream);
+/* Synchronises `stream`, returns the status bits of the last plain
+ * r9vx_moe_route_launch on this device in *status and clears them. */
 int r9vx_moe_route_status(uint32_t *status, r9vx_stream_t stream);
+/* Copies a device status word (of r9vx_moe_route_launch_ex) to *status after
+ * synchronising `stream`. */
+int r9vx_status_read(const uint32_t *device_word, uint32_t *status, r9vx_stream_t stream);
+/* LaunchEntry.static_bytes / static_flops (crates/r9v-registry/src/launch.rs:22-25):
+ * logits, bias, ids and weights; and the arithmetic of scoring, the ordered
+ * softmax sum and the renormalisation (about 4*E + 2*K per row). */
 uint64_t r9vx_moe_route_static_bytes(const r9vx_moe_route_static *st, uint32_t t);
+uint64_t r9vx_moe_route_static_flops(const r9vx_moe_route_static *st, uint32_t t);
 
 /* Routing from hidden states (the router-logits matmul feeding moe_route,
  * fused; decode form t <= 8).  No single op of the reference: it replaces the
@@ -210,27 +259,40 @@ int r9vx_router_repack_launch(const float *w, uint32_t e, uint32_t dm, float *ou
 
 int r9vx_moe_route_hidden_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_hidden_args *args,
                                  r9vx_stream_t stream);
-/* Workspace of r9vx_moe_route_hidden_launch: the [t_bucket, E] f32 logits and
- * a completion counter. */
+/* Workspace of r9vx_moe_route_hidden_launch: the [t_bucket, E] f32 logits, a
+ * completion counter and the launch's status word. */
 size_t r9vx_moe_route_hidden_workspace_bytes(const r9vx_moe_route_static *st);
+/* Synchronises `stream` and returns the status bits the last
+ * r9vx_moe_route_hidden_launch with this workspace left in it. */
+int r9vx_moe_route_hidden_status(const r9vx_moe_route_static *st, const uint8_t *workspace, uint32_t *status,
+                                 r9vx_stream_t stream);
 
 /* ----------------------------------------------------------------- moe_ffn */
 
-/* MoeFfnStatic (crates/r9v-registry/src/types.rs:828-860). */
+/* MoeFfnProjStatic (crates/r9v-registry/src/types.rs:801-818): one
+ * projection's weight element type, scheme and layout. */
+typedef struct r9vx_moe_ffn_proj {
+    uint32_t dtype;  /* I4 for Q4_K / IQ4_XS / IQ3_S, I8 for Q8_0 / Q6_K */
+    uint32_t scheme; /* enum r9vx_scheme */
+    uint32_t layout; /* enum r9vx_layout: GGUF_WIRE (Q4_K, IQ4_XS), IQ3S_112 (IQ3_S) */
+} r9vx_moe_ffn_proj;
+
+/* MoeFfnStatic (crates/r9v-registry/src/types.rs:828-860), every key in its
+ * declaration order. */
 typedef struct r9vx_moe_ffn_static {
     uint32_t t_bucket;
-    uint32_t e_local;        /* routed experts E */
-    uint32_t k_topk;         /* K */
-    uint32_t dm;             /* hidden size, multiple of 256 */
-    uint32_t dff;            /* expert intermediate size, multiple of 256 */
-    uint32_t gate_up_scheme; /* enum r9vx_scheme of w_gate_up [E+S, 2Dff, Dm]: Q4_K, IQ4_XS, or
-                              * IQ3_S as the 112-byte repacked blocks of r9vx_repack_launch */
-    uint32_t down_scheme;    /* enum r9vx_scheme of w_down [E+S, Dm, Dff] */
-    uint32_t in_dtype;       /* BF16 */
-    uint32_t out_dtype;      /* F32 */
-    uint32_t act;            /* enum r9vx_act */
-    uint32_t shared_experts; /* S shared experts stored after the E routed ones */
-    uint32_t _reserved;
+    uint32_t e_local;          /* routed experts E */
+    uint32_t k_topk;           /* K */
+    uint32_t dm;               /* hidden size, multiple of 256 */
+    uint32_t dff;              /* expert intermediate size, multiple of 256 */
+    r9vx_moe_ffn_proj gate_up; /* w_gate_up [E+S, 2Dff, Dm]: Q4_K, IQ4_XS or IQ3_S */
+    r9vx_moe_ffn_proj down;    /* w_down [E+S, Dm, Dff]: Q4_K, IQ4_XS or IQ3_S */
+    uint32_t in_dtype;         /* BF16 */
+    uint32_t act_scheme;       /* R9VX_ACT_SCHEME_NONE */
+    uint32_t act;              /* enum r9vx_act */
+    uint32_t out_dtype;        /* F32 */
+    uint32_t shared_experts;   /* S shared experts stored after the E routed ones */
+    uint32_t placement_kind;   /* R9VX_PLACEMENT_DEVICE */
 } r9vx_moe_ffn_static;
 
 /* moe_ffn ABI struct (crates/r9v-kgen/src/abi/per_op.rs:903-968). */
@@ -259,7 +321,15 @@ size_t r9vx_moe_ffn_workspace_bytes(const r9vx_moe_ffn_static *st);
  * this workspace left in it (R9VX_STATUS_BAD_EXPERT). */
 int r9vx_moe_ffn_status(const r9vx_moe_ffn_static *st, const uint8_t *sort_workspace,
                         uint32_t *status, r9vx_stream_t stream);
+/* LaunchEntry.static_flops (crates/r9v-registry/src/launch.rs:22-25):
+ * (t*K + t*S) rows of 2*(2Dff*Dm) + 2*Dm*Dff. */
 uint64_t r9vx_moe_ffn_static_flops(const r9vx_moe_ffn_static *st, uint32_t t);
+/* LaunchEntry.static_bytes: an upper bound on the HBM bytes of one launch --
+ * (min(E, t*K) + S) experts' gate/up and down weights, x (bf16), ids and
+ * weights, y (f32).  The bytes actually read depend on how many distinct
+ * experts the ids name; r9vx_moe_ffn_expert_bytes is one expert's share. */
+uint64_t r9vx_moe_ffn_static_bytes(const r9vx_moe_ffn_static *st, uint32_t t);
+uint64_t r9vx_moe_ffn_expert_bytes(const r9vx_moe_ffn_static *st);
 
 /* Permute pre-pass of moe_ffn on its own: counts [E], offsets [E+1] and
  * sorted [t*K] (= token*K + slot in stable (expert, token, slot) order), the
@@ -300,7 +370,7 @@ const char *r9vx_last_error(void);
 /* ABI version of this header (bumped on any struct change). */
 uint32_t r9vx_abi_version(void);
 
-#define R9VX_ABI_VERSION 1u
+#define R9VX_ABI_VERSION 2u
 
 #ifdef __cplusplus
 }

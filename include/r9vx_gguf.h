@@ -169,25 +169,33 @@ int64_t r9vx_gguf_shards_find(const r9vx_gguf_shards *s, const char *name);
 
 /* ---------------------------------------------------- binding and upload */
 
-/* Variant key of a matmul over the 2-D Q4_K / IQ4_XS / Q6_K / Q8_0 tensor
- * `name` (file dims {K, N}): sets st->n, st->k and st->w_scheme, leaves the
- * other fields.  Q6_K / Q8_0 weights are loaded with r9vx_gguf_upload_split.  This
- * is the shape-and-scheme part of a MatmulStatic the loader derives from a
+/* Variant key of a matmul over the 2-D Q4_K / IQ4_XS / Q6_K / Q8_0 / IQ3_S
+ * tensor `name` (file dims {K, N}): sets st->n, st->k, st->w_scheme and the
+ * w_dtype / w_layout of the device layout the weights must be loaded into,
+ * leaves the other fields: Q4_K / IQ4_XS GGUF_WIRE (r9vx_gguf_upload copies
+ * the blocks), IQ3_S IQ3S_112 (r9vx_gguf_upload repacks the 110-byte blocks
+ * into 112-byte ones), Q6_K / Q8_0 SPLIT (r9vx_gguf_upload_split).  This is
+ * the shape-and-scheme part of a MatmulStatic the loader derives from a
  * checkpoint (crates/r9v-registry/src/types.rs:727-770). */
 int r9vx_gguf_matmul_static(const r9vx_gguf *f, const char *name, r9vx_matmul_static *st);
 /* Variant key of a moe_ffn over stacked expert tensors: `gate` and `up`
  * (file dims {Dm, Dff, E} each) or one fused `gate` tensor {Dm, 2*Dff, E}
  * with up == NULL (the ffn_gate_up_exps form of
  * crates/r9v-models/src/generic.rs:1420), and `down` {Dff, Dm, E}.  Sets
- * e_local, dm, dff, gate_up_scheme and down_scheme. */
+ * e_local, dm, dff and the gate_up / down projection keys (dtype, scheme and
+ * the device layout r9vx_gguf_upload / r9vx_gguf_upload_gate_up write). */
 int r9vx_gguf_moe_ffn_static(const r9vx_gguf *f, const char *gate, const char *up,
                              const char *down, r9vx_moe_ffn_static *st);
-/* Copies tensor `name`'s wire blocks from the host buffer into device memory
- * `dst` (dst_bytes >= the entry's size) on `stream`.  GGUF Q4_K / IQ4_XS
- * blocks are the device layout of this path, so loading is one copy; it
- * replaces the load-time repack to R9V's L1 layout (crates/r9v-format/src/
- * repack.rs:282, iq.rs:1155).  Returns after the copy has been enqueued;
- * `bytes` must stay valid until the stream reaches it. */
+/* Loads tensor `name` from the host buffer into device memory `dst` in the
+ * device layout its static names, on `stream`; it replaces the load-time
+ * repack to R9V's L1 layout (crates/r9v-format/src/repack.rs:282,
+ * iq.rs:1155).  GGUF Q4_K / IQ4_XS blocks (and F32 tensors) are copied as
+ * they are (dst_bytes >= the entry's size): the call returns after the copy
+ * has been enqueued, and `bytes` must stay valid until the stream reaches
+ * it.  IQ3_S blocks are repacked on the host into the 112-byte device blocks
+ * (dst_bytes >= 112 per 110-byte block; a non-finite d is refused before
+ * anything is copied) and the call returns after the copy has completed.
+ * Q8_0 / Q6_K are refused: they load with r9vx_gguf_upload_split. */
 int r9vx_gguf_upload(const r9vx_gguf *f, const uint8_t *bytes, uint64_t len, const char *name,
                      void *dst, uint64_t dst_bytes, r9vx_stream_t stream);
 /* Loads a Q8_0 / Q6_K tensor into the split device layout of include/r9vx.h
@@ -201,7 +209,9 @@ int r9vx_gguf_upload_split(const r9vx_gguf *f, const uint8_t *bytes, uint64_t le
 /* Builds moe_ffn's w_gate_up [E, 2*Dff, Dm] in device memory from stacked
  * gate and up expert tensors [E, Dff, Dm] (which may sit in different shards):
  * expert e's gate rows, then its up rows (crates/r9v-t0/src/moe_ffn.rs:51-55),
- * with one strided copy per tensor. */
+ * with one strided copy per tensor.  IQ3_S experts are repacked on the host
+ * into 112-byte device blocks first (dst_bytes >= 2 * 112 per 110-byte
+ * block of one tensor), as r9vx_gguf_upload does. */
 int r9vx_gguf_upload_gate_up(const r9vx_gguf *gate_file, const uint8_t *gate_bytes,
                              uint64_t gate_len, const char *gate, const r9vx_gguf *up_file,
                              const uint8_t *up_bytes, uint64_t up_len, const char *up, void *dst,

@@ -256,9 +256,6 @@ __global__ __launch_bounds__(256) void repack_q6k_kernel(const uint8_t *__restri
  * block (7 per block); device byte j takes wire byte 2 + j (qs, j < 64),
  * 10 + j (signs, j < 96), j - 30 (qh, j < 104), j + 2 (scales, j < 108),
  * j - 108 (d, j < 110), and zero. */
-__device__ __forceinline__ uint32_t iq3s_wire_byte(uint32_t j) {
-    return j < 64 ? 2 + j : j < 96 ? 10 + j : j < 104 ? j - 30 : j < 108 ? j + 2 : j - 108;
-}
 
 __global__ __launch_bounds__(256) void repack_iq3s_kernel(const uint8_t *__restrict__ wire, uint64_t n_pieces,
                                                           uint8_t *__restrict__ body) {
@@ -271,7 +268,7 @@ __global__ __launch_bounds__(256) void repack_iq3s_kernel(const uint8_t *__restr
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const uint32_t j = 16 * piece + i;
-        if (j < 110) w[i >> 2] |= (uint32_t)b[iq3s_wire_byte(j)] << (8 * (i & 3));
+        if (j < 110) w[i >> 2] |= (uint32_t)b[r9vx_iq3s_wire_byte(j)] << (8 * (i & 3));
     }
     *reinterpret_cast<r9vx_u32x4 *>(body + blk * R9VX_IQ3S_DEV_BYTES + 16 * piece) = r9vx_u32x4{w[0], w[1], w[2], w[3]};
 }

@@ -25,6 +25,7 @@
 
 #include "r9vx.h"
 #include "r9vx_gguf.h"
+#include "r9vx_internal.h"
 #include "r9vx_xxh3.h"
 
 void r9vx_set_last_error(const std::string &text);  // r9vx_api.hip
@@ -582,8 +583,37 @@ int entry_range(const char *op, const r9vx_gguf *f, const char *name, const uint
 
 bool path_scheme(uint32_t type) { return type == R9VX_SCHEME_Q4_K || type == R9VX_SCHEME_IQ4_XS; }
 bool split_type(uint32_t type) { return type == R9VX_SCHEME_Q8_0 || type == R9VX_SCHEME_Q6_K; }
-/* IQ3_S: uploaded as wire blocks, then repacked on the device (r9vx_repack_launch) */
+/* IQ3_S: repacked on the host into the 112-byte device blocks while uploading */
 bool repack_type(uint32_t type) { return type == R9VX_SCHEME_IQ3_S; }
+
+/* Element type and device layout of the weights this path reads per type. */
+uint32_t type_dtype(uint32_t type) { return split_type(type) ? R9VX_DTYPE_I8 : R9VX_DTYPE_I4; }
+uint32_t type_layout(uint32_t type) {
+    return split_type(type) ? R9VX_LAYOUT_SPLIT : repack_type(type) ? R9VX_LAYOUT_IQ3S_112 : R9VX_LAYOUT_GGUF_WIRE;
+}
+
+/* Device bytes of a tensor of nbytes wire bytes. */
+uint64_t device_bytes(uint32_t type, uint64_t nbytes) {
+    return repack_type(type) ? nbytes / R9VX_IQ3S_BYTES * R9VX_IQ3S_DEV_BYTES : nbytes;
+}
+
+/* Host copy of `nblocks` IQ3_S wire blocks as 112-byte device blocks (the
+ * layout r9vx_repack_launch writes); counts blocks whose d is not finite
+ * (check_wire_f16, crates/r9v-format/src/ggml.rs:421) into *bad. */
+bool iq3s_repack_host(const uint8_t *wire, uint64_t nblocks, std::vector<uint8_t> &out, uint64_t *bad) {
+    try {
+        out.assign(nblocks * R9VX_IQ3S_DEV_BYTES, 0);
+    } catch (const std::bad_alloc &) {
+        return false;
+    }
+    for (uint64_t b = 0; b < nblocks; ++b) {
+        const uint8_t *w = wire + b * R9VX_IQ3S_BYTES;
+        uint8_t *o = &out[b * R9VX_IQ3S_DEV_BYTES];
+        for (uint32_t j = 0; j < R9VX_IQ3S_BYTES; ++j) o[j] = w[r9vx_iq3s_wire_byte(j)];
+        *bad += (w[1] & 0x7Cu) == 0x7Cu; /* f16 exponent all ones: inf or NaN */
+    }
+    return true;
+}
 
 std::string dims_text(const Tensor &t) {
     std::string s = "{";
@@ -833,6 +863,8 @@ int r9vx_gguf_matmul_static(const r9vx_gguf *f, const char *name, r9vx_matmul_st
     st->k = (uint32_t)t->dims[0];
     st->n = (uint32_t)t->dims[1];
     st->w_scheme = t->type;
+    st->w_dtype = type_dtype(t->type);
+    st->w_layout = type_layout(t->type);
     return R9VX_OK;
 }
 
@@ -886,8 +918,8 @@ int r9vx_gguf_moe_ffn_static(const r9vx_gguf *f, const char *gate, const char *u
             st->e_local = (uint32_t)e;
             st->dm = (uint32_t)dm;
             st->dff = (uint32_t)dff;
-            st->gate_up_scheme = g->type;
-            st->down_scheme = d->type;
+            st->gate_up = r9vx_moe_ffn_proj{type_dtype(g->type), g->type, type_layout(g->type)};
+            st->down = r9vx_moe_ffn_proj{type_dtype(d->type), d->type, type_layout(d->type)};
         }
     }
     if (pr.empty()) return R9VX_OK;
@@ -904,12 +936,31 @@ int r9vx_gguf_upload(const r9vx_gguf *f, const uint8_t *bytes, uint64_t len, con
     const uint8_t *data;
     const int rc = entry_range(op, f, name, bytes, len, &t, &data);
     if (rc != R9VX_OK) return rc;
+    if (split_type(t->type))
+        return refuse(op, R9VX_ERR_UNSUPPORTED,
+                      "tensor \"" + t->name + "\" is " + r9vx_gguf_type_name(t->type) +
+                          "; Q8_0 / Q6_K load into the split layout with r9vx_gguf_upload_split");
     if (!dst) return refuse(op, R9VX_ERR_NULL, "dst is NULL");
-    if (dst_bytes < t->nbytes)
+    const uint64_t need = device_bytes(t->type, t->nbytes);
+    if (dst_bytes < need)
         return refuse(op, R9VX_ERR_INVALID,
-                      fmt("dst holds %llu bytes, tensor \"%s\" needs %llu", (unsigned long long)dst_bytes,
-                          t->name.c_str(), (unsigned long long)t->nbytes));
-    return hip_rc(op, hipMemcpyAsync(dst, data, t->nbytes, hipMemcpyHostToDevice, (hipStream_t)stream));
+                      fmt("dst holds %llu bytes, tensor \"%s\" needs %llu%s", (unsigned long long)dst_bytes,
+                          t->name.c_str(), (unsigned long long)need,
+                          repack_type(t->type) ? " (112-byte IQ3_S device blocks)" : ""));
+    if (!repack_type(t->type))
+        return hip_rc(op, hipMemcpyAsync(dst, data, t->nbytes, hipMemcpyHostToDevice, (hipStream_t)stream));
+    std::vector<uint8_t> dev;
+    uint64_t bad = 0;
+    if (!iq3s_repack_host(data, t->nbytes / R9VX_IQ3S_BYTES, dev, &bad))
+        return refuse(op, R9VX_ERR_INVALID, "out of host memory for the IQ3_S repack");
+    if (bad)
+        return refuse(op, R9VX_ERR_INVALID,
+                      fmt("tensor \"%s\": %llu block(s) carry a non-finite scale", t->name.c_str(),
+                          (unsigned long long)bad));
+    hipStream_t s = (hipStream_t)stream;
+    const int cp = hip_rc(op, hipMemcpyAsync(dst, dev.data(), dev.size(), hipMemcpyHostToDevice, s));
+    const int sync = hip_rc(op, hipStreamSynchronize(s)); /* the host copy dies with this call */
+    return cp != R9VX_OK ? cp : sync;
 }
 
 int r9vx_gguf_upload_split(const r9vx_gguf *f, const uint8_t *bytes, uint64_t len, const char *name, void *body,
@@ -982,19 +1033,38 @@ int r9vx_gguf_upload_gate_up(const r9vx_gguf *gate_file, const uint8_t *gate_byt
                           u->name + "\" " + dims_text(*u) + " " + r9vx_gguf_type_name(u->type) +
                           " must be stacked Q4_K / IQ4_XS / IQ3_S experts {K, rows, E} of one dims and type");
     if (!dst) return refuse(op, R9VX_ERR_NULL, "dst is NULL");
-    if (dst_bytes / 2 < g->nbytes)
+    const uint64_t need = 2 * device_bytes(g->type, g->nbytes);
+    if (dst_bytes < need)
         return refuse(op, R9VX_ERR_INVALID,
-                      fmt("dst holds %llu bytes, the stacked gate_up needs %llu", (unsigned long long)dst_bytes,
-                          (unsigned long long)(2 * g->nbytes)));
+                      fmt("dst holds %llu bytes, the stacked gate_up needs %llu%s", (unsigned long long)dst_bytes,
+                          (unsigned long long)need, repack_type(g->type) ? " (112-byte IQ3_S device blocks)" : ""));
     const TypeRow *row = type_row(g->type);
-    const uint64_t slab = g->dims[0] / row->block_len * row->block_bytes * g->dims[1];  // one expert's rows
+    const uint64_t blocks_per_expert = g->dims[0] / row->block_len * g->dims[1];
     const uint64_t experts = g->dims[2];
     uint8_t *d = static_cast<uint8_t *>(dst);
-    rc = hip_rc(op, hipMemcpy2DAsync(d, 2 * slab, gdata, slab, slab, experts, hipMemcpyHostToDevice,
-                                     (hipStream_t)stream));
-    if (rc != R9VX_OK) return rc;
-    return hip_rc(op, hipMemcpy2DAsync(d + slab, 2 * slab, udata, slab, slab, experts, hipMemcpyHostToDevice,
-                                       (hipStream_t)stream));
+    hipStream_t s = (hipStream_t)stream;
+    if (!repack_type(g->type)) {
+        const uint64_t slab = blocks_per_expert * row->block_bytes;  // one expert's rows
+        rc = hip_rc(op, hipMemcpy2DAsync(d, 2 * slab, gdata, slab, slab, experts, hipMemcpyHostToDevice, s));
+        if (rc != R9VX_OK) return rc;
+        return hip_rc(op, hipMemcpy2DAsync(d + slab, 2 * slab, udata, slab, slab, experts, hipMemcpyHostToDevice, s));
+    }
+    /* IQ3_S: both tensors repacked on the host, then stacked the same way */
+    std::vector<uint8_t> gdev, udev;
+    uint64_t bad = 0;
+    if (!iq3s_repack_host(gdata, blocks_per_expert * experts, gdev, &bad) ||
+        !iq3s_repack_host(udata, blocks_per_expert * experts, udev, &bad))
+        return refuse(op, R9VX_ERR_INVALID, "out of host memory for the IQ3_S repack");
+    if (bad)
+        return refuse(op, R9VX_ERR_INVALID,
+                      fmt("gate \"%s\" / up \"%s\": %llu block(s) carry a non-finite scale", g->name.c_str(),
+                          u->name.c_str(), (unsigned long long)bad));
+    const uint64_t slab = blocks_per_expert * R9VX_IQ3S_DEV_BYTES;
+    rc = hip_rc(op, hipMemcpy2DAsync(d, 2 * slab, gdev.data(), slab, slab, experts, hipMemcpyHostToDevice, s));
+    if (rc == R9VX_OK)
+        rc = hip_rc(op, hipMemcpy2DAsync(d + slab, 2 * slab, udev.data(), slab, slab, experts, hipMemcpyHostToDevice, s));
+    const int sync = hip_rc(op, hipStreamSynchronize(s)); /* the host copies die with this call */
+    return rc != R9VX_OK ? rc : sync;
 }
 
 }  // extern "C"

@@ -6,22 +6,27 @@
  * gate/up Branch-D GEMM, act_mul SiLU, down GEMM); the combine is moe.hip's.
  *
  *  tiles : each work item (expert with n pairs, or shared expert with t rows)
- *          becomes ceil(n / 128) row tiles; a one-workgroup scan lays them out.
- *  gate/up: a workgroup owns 128 permuted rows x 128 columns j of h; wave w's
- *          two column tiles are gate rows j0+32w.. and the matching up rows
- *          Dff+j0+32w.., so g and u of the same (row, j) land in the same lane
- *          and register: h = silu(g) * u is formed in registers (f32) and
- *          written with the row's running max|h|.  A rows are gathered from the
- *          scaled fp16 activations by the permutation (no permuted copy of x).
+ *          becomes ceil(n / 256) row tiles (ceil(n / 128) for the IQ3_S
+ *          gate/up kernel); a one-workgroup scan lays them out.
+ *  gate/up: a workgroup owns 256 permuted rows x 128 columns j of h; its
+ *          weight tile is gate rows j0.. and the matching up rows Dff+j0..,
+ *          and a wave's two column tiles are a gate tile and its up tile, so
+ *          g and u of the same (row, j) land in the same lane and register:
+ *          h = silu(g) * u is formed in registers (f32).  A rows are gathered
+ *          from the scaled fp16 activations by the permutation (no permuted
+ *          copy of x).
  *  h16   : each h row scaled by the power of two that brings max|h| below
  *          2^15 and rounded to fp16, in the down weights' K group order.
- *  down  : a workgroup owns 128 rows x 256 output columns of o; the scale is
+ *  down  : a workgroup owns 256 rows x 256 output columns of o; the scale is
  *          undone on the f32 accumulators.
- * Both GEMMs run the register-decoded main loop of r9vx_mma2.h (4 waves,
- * 128-row tiles, two workgroups per CU).  Tiles past the scanned count exit.
+ * Both GEMMs run the main loop of r9vx_mma3.h (weights decoded once per
+ * workgroup into LDS, 8 waves, one workgroup per CU); a wave whose 128 rows
+ * hold fewer than 4 row tiles of the tile runs only the MFMAs of those.
+ * Tiles past the scanned count exit.
  */
 #include "r9vx_mma.h"
 #include "r9vx_mma2.h"
+#include "r9vx_mma3.h"
 #include "r9vx_moe.h"
 
 using namespace r9vx;
@@ -46,24 +51,39 @@ __device__ __forceinline__ const uint32_t *ws_u32(const GroupedArgs &a, uint64_t
     return reinterpret_cast<const uint32_t *>(a.ws + off);
 }
 
+/* Workgroup -> (row tile, column block), XCD-aware: the hardware deals
+ * workgroups to the 8 XCDs round-robin, so XCD x's j-th workgroup takes row
+ * tile 8 * (j / ncol) + x and column block j % ncol.  Every column block of a
+ * row tile then runs on one XCD, whose L2 fetches the tile's activation rows
+ * once instead of once per column block.  The grid is 8 * ncol * (row tiles
+ * rounded up to 8). */
+__device__ __forceinline__ void xcd_tile(uint32_t ncol, uint32_t &tix, uint32_t &nt) {
+    const uint32_t b = blockIdx.x, x = b & 7u, j = b >> 3;
+    tix = (j / ncol) * 8u + x;
+    nt = j % ncol;
+}
+
+/* silu(g) * u with the hardware exp and reciprocal (about 2 ulp each; T0's
+ * f32 expf and divide, crates/r9v-t0/src/activation.rs:135-138, are matched
+ * well inside the matmul tolerance). */
+__device__ __forceinline__ float swiglu_fast(float g, float u) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f)) * u;
+}
+
 __device__ __forceinline__ uint32_t row_token(const GroupedArgs &a, uint32_t expert, uint32_t pos) {
     if (expert >= a.e) return pos - (a.p + (expert - a.e) * a.t);
     return ws_u32(a, a.L.sorted)[pos] / a.k;
 }
 
-/* One workgroup: scan the work items' tile counts into the tile list and
- * zero the per-row max|h| words. */
-__global__ __launch_bounds__(1024) void build_tiles_kernel(GroupedArgs a) {
-    __shared__ uint32_t sh[16];
-    uint32_t *status = reinterpret_cast<uint32_t *>(a.ws + a.L.status);
-    const uint32_t nwork = status[2];
-    const r9vx_u32x4 *work = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.work);
-    r9vx_u32x4 *tiles = reinterpret_cast<r9vx_u32x4 *>(a.ws + a.L.tiles);
+/* Scans the work items' tile counts (TM rows per tile) into `tiles`;
+ * returns the tile count (in every thread). */
+template <uint32_t TM>
+__device__ uint32_t scan_tiles(const r9vx_u32x4 *work, uint32_t nwork, r9vx_u32x4 *tiles, uint32_t *sh) {
     uint32_t base = 0;
     for (uint32_t w0 = 0; w0 < nwork; w0 += 1024) {
         uint32_t i = w0 + threadIdx.x;
         r9vx_u32x4 wk = i < nwork ? work[i] : r9vx_u32x4{0u, 0u, 0u, 0u};
-        uint32_t nt = (wk.z + kBM - 1) / kBM;
+        uint32_t nt = (wk.z + TM - 1) / TM;
         /* block exclusive scan of nt */
         uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
         uint32_t inc = nt;
@@ -81,13 +101,28 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(GroupedArgs a) {
         }
         uint32_t first = base + pre + inc - nt;
         for (uint32_t j = 0; j < nt; ++j) {
-            uint32_t rows = wk.z - j * kBM < kBM ? wk.z - j * kBM : kBM;
-            tiles[first + j] = r9vx_u32x4{wk.x, wk.y + j * kBM, rows, 0u};
+            uint32_t rows = wk.z - j * TM < TM ? wk.z - j * TM : TM;
+            tiles[first + j] = r9vx_u32x4{wk.x, wk.y + j * TM, rows, 0u};
         }
         base += tot;
         __syncthreads();
     }
-    if (threadIdx.x == 0) status[3] = base;
+    return base;
+}
+
+/* One workgroup: the work items' 128-row tiles (status[3] of them) and
+ * 256-row tiles (status[4]). */
+__global__ __launch_bounds__(1024) void build_tiles_kernel(GroupedArgs a) {
+    __shared__ uint32_t sh[16];
+    uint32_t *status = reinterpret_cast<uint32_t *>(a.ws + a.L.status);
+    const uint32_t nwork = status[2];
+    const r9vx_u32x4 *work = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.work);
+    const uint32_t n128 = scan_tiles<kBM>(work, nwork, reinterpret_cast<r9vx_u32x4 *>(a.ws + a.L.tiles), sh);
+    const uint32_t n256 = scan_tiles<kMoeTileM3>(work, nwork, reinterpret_cast<r9vx_u32x4 *>(a.ws + a.L.tiles3), sh);
+    if (threadIdx.x == 0) {
+        status[3] = n128;
+        status[4] = n256;
+    }
 }
 
 /* ---------------------------------------------------------------- gate/up */
@@ -103,52 +138,6 @@ constexpr int kStage = 32 * kMT * 128;       /* 16 KiB per A stage */
     __shared__ __attribute__((aligned(16))) float lutf[512];          \
     uint8_t *const stages[4] = {st0, st1, st2, st3};
 
-template <int GU>
-__global__ __launch_bounds__(256, 2) void moe_gu_mfma_kernel(GroupedArgs a) {
-    R9VX_MOE_STAGES
-    __shared__ float rowsc[kBM]; /* the tile rows' activation scales */
-    const uint32_t *status = ws_u32(a, a.L.status);
-    const uint32_t ntile_n = a.dff / 128;
-    const uint32_t tix = blockIdx.x / ntile_n, nt = blockIdx.x % ntile_n;
-    if (status[0] != 0u || tix >= status[3]) return;
-    const r9vx_u32x4 tile = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles)[tix];
-    const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
-    const uint32_t j0 = nt * 128;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid < kBM) rowsc[tid] = tid < rows ? a.xscale[row_token(a, expert, pos0 + tid)] : 0.f;
-    if constexpr (GU == R9VX_SCHEME_IQ4_XS) init_iq4_lut_f32(reinterpret_cast<r9vx_f32x4 *>(lutf), tid);
-    __syncthreads();
-
-    const _Float16 *asrc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t r = dma_row(wave, i, lane);
-        const uint32_t tok = row_token(a, expert, pos0 + (r < rows ? r : 0));
-        asrc[i] = a.x16 + (uint64_t)tok * a.dm + 8 * dma_group(r, lane);
-    }
-    const uint32_t col = j0 + 32 * wave + (lane & 31);
-    const uint8_t *wexp = a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes;
-    const uint8_t *const wrow[2] = {wexp + (uint64_t)col * a.gu_row_bytes, wexp + (uint64_t)(a.dff + col) * a.gu_row_bytes};
-    r9vx_f32x16 acc[kMT][2];
-    m2_mainloop<GU, kMT, 2>(stages, asrc, wrow, a.dm / kTileK, wave, lane, lutf, acc);
-
-    /* SwiGLU on the accumulators; each h row's max|h| (its fp16 scale) is
-     * taken by h_to_f16, which reads the whole row anyway */
-    float *h = reinterpret_cast<float *>(a.ws + a.L.h);
-#pragma unroll
-    for (int i = 0; i < kMT; ++i) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t rl = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (rl >= rows) continue;
-            const float sc = rowsc[rl];
-            const float g = acc[i][0][r] * sc, u = acc[i][1][r] * sc;
-            const float v = g / (1.0f + __expf(-g)) * u;
-            h[(uint64_t)(pos0 + rl) * a.dff + col] = v;
-        }
-    }
-}
-
 /* IQ3_S gate/up experts: the LDS-decoded main loop of r9vx_mma.h (a 128 x
  * 256 tile; thread t decodes weight row t of the tile into LDS: threads
  * 0..127 the gate rows j0..j0+127, threads 128..255 the up rows of the same
@@ -162,8 +151,8 @@ __global__ __launch_bounds__(256, 2) void moe_gu_lds_kernel(GroupedArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
     __shared__ float rowsc[kBM];
     const uint32_t *status = ws_u32(a, a.L.status);
-    const uint32_t ntile_n = a.dff / 128;
-    const uint32_t tix = blockIdx.x / ntile_n, nt = blockIdx.x % ntile_n;
+    uint32_t tix, nt;
+    xcd_tile(a.dff / 128, tix, nt);
     if (status[0] != 0u || tix >= status[3]) return;
     const r9vx_u32x4 tile = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles)[tix];
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
@@ -206,7 +195,7 @@ __global__ __launch_bounds__(256, 2) void moe_gu_lds_kernel(GroupedArgs a) {
             const float uv[4] = {u4.x * sc, u4.y * sc, u4.z * sc, u4.w * sc};
             float v[4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) v[c] = gv[c] / (1.0f + __expf(-gv[c])) * uv[c];
+            for (int c = 0; c < 4; ++c) v[c] = swiglu_fast(gv[c], uv[c]);
             *reinterpret_cast<r9vx_f32x4 *>(h + (uint64_t)(pos0 + row) * a.dff + j0 + c4) = r9vx_f32x4{v[0], v[1], v[2], v[3]};
         }
         __syncthreads();
@@ -246,48 +235,107 @@ __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t n
     }
 }
 
-/* ---------------------------------------------------------------- down */
+/* ---------------------------------------------------------------- 256-row tiles */
 
-template <int DN>
-__global__ __launch_bounds__(256, 2) void moe_dn_mfma_kernel(GroupedArgs a) {
-    R9VX_MOE_STAGES
+/* Gate/up on the r9vx_mma3.h loop: a workgroup owns a 256-row tile of one
+ * expert and 128 columns j of h; its B tile is gate rows j0 .. j0+127 (B rows
+ * 0..127) and up rows Dff+j0 .. (B rows 128..255), and wave w's two column
+ * tiles are gate 32(w%4) and up 128 + 32(w%4), so g and u of one (row, j)
+ * share a lane and register. */
+template <int GU>
+__global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
+    __shared__ __attribute__((aligned(16))) M3Lds sm;
+    __shared__ __attribute__((aligned(16))) float lutf[512];
+    __shared__ float rowsc[kMoeTileM3];
     const uint32_t *status = ws_u32(a, a.L.status);
-    const uint32_t ntile_n = a.dm / 256;
-    const uint32_t tix = blockIdx.x / ntile_n, nt = blockIdx.x % ntile_n;
-    if (status[0] != 0u || tix >= status[3]) return;
-    const r9vx_u32x4 tile = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles)[tix];
+    uint32_t tix, nt;
+    xcd_tile(a.dff / 128, tix, nt);
+    if (status[0] != 0u || tix >= status[4]) return;
+    const r9vx_u32x4 tile = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles3)[tix];
+    const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
+    const uint32_t j0 = nt * 128;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid < kMoeTileM3) rowsc[tid] = tid < rows ? a.xscale[row_token(a, expert, pos0 + tid)] : 0.f;
+    if constexpr (GU == R9VX_SCHEME_IQ4_XS) init_iq4_lut_f32(reinterpret_cast<r9vx_f32x4 *>(lutf), tid);
+    __syncthreads();
+
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t aoff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = dma_row(wv, i, lane);
+        const uint32_t tok = row_token(a, expert, pos0 + (r < rows ? r : 0));
+        aoff[i] = (tok * a.dm + 8 * dma_group(r, lane)) * 2u;
+    }
+    const uint32_t c = tid >> 1;
+    const uint32_t wr = c < 128 ? j0 + c : a.dff + j0 + (c - 128);
+    const M3WRow w{a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes, wr * (uint32_t)a.gu_row_bytes};
+    const uint32_t rh = wv >> 2, cq = wv & 3;
+    const uint32_t nr = m3_active_tiles(rows, 128 * rh);
+    r9vx_f32x16 acc[4][2];
+    m3_run<GU>(nr, sm, a.x16, aoff, w, a.dm / kTileK, tid, wv, lutf, 128 * rh, 32 * cq, 128 + 32 * cq, acc);
+
+    float *h = reinterpret_cast<float *>(a.ws + a.L.h);
+    const uint32_t col = j0 + 32 * cq + (lane & 31);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        if ((uint32_t)t >= nr) break;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t rl = 128 * rh + 32 * t + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (rl >= rows) continue;
+            const float sc = rowsc[rl];
+            h[(uint64_t)(pos0 + rl) * a.dff + col] = swiglu_fast(acc[t][0][r] * sc, acc[t][1][r] * sc);
+        }
+    }
+}
+
+/* Down on the r9vx_mma3.h loop: 256 rows x 256 output columns per
+ * workgroup; wave w's column tiles are 64(w%4) and 64(w%4) + 32. */
+template <int DN>
+__global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
+    __shared__ __attribute__((aligned(16))) M3Lds sm;
+    __shared__ __attribute__((aligned(16))) float lutf[512];
+    __shared__ float rowsc[kMoeTileM3]; /* 2^e that undoes each h row's fp16 scale */
+    const uint32_t *status = ws_u32(a, a.L.status);
+    uint32_t tix, nt;
+    xcd_tile(a.dm / 256, tix, nt);
+    if (status[0] != 0u || tix >= status[4]) return;
+    const r9vx_u32x4 tile = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles3)[tix];
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
     const uint32_t n0 = nt * 256;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    __shared__ float rowsc[kBM]; /* 2^e that undoes each h row's fp16 scale */
-    if (tid < kBM)
+    if (tid < kMoeTileM3)
         rowsc[tid] = tid < rows ? ldexpf(1.0f, row_shift(__builtin_bit_cast(float, ws_u32(a, a.L.hmax)[pos0 + tid])))
                                 : 0.f;
     if constexpr (DN == R9VX_SCHEME_IQ4_XS) init_iq4_lut_f32(reinterpret_cast<r9vx_f32x4 *>(lutf), tid);
     __syncthreads();
 
-    const _Float16 *asrc[4];
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t aoff[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t r = dma_row(wave, i, lane);
-        asrc[i] = a.h16 + (uint64_t)(pos0 + (r < rows ? r : 0)) * a.dff + 8 * dma_group(r, lane);
+        const uint32_t r = dma_row(wv, i, lane);
+        aoff[i] = ((pos0 + (r < rows ? r : 0)) * a.dff + 8 * dma_group(r, lane)) * 2u;
     }
-    const uint8_t *wexp = a.w_dn + (uint64_t)expert * a.dm * a.dn_row_bytes;
-    const uint32_t c0 = n0 + 64 * wave + (lane & 31);
-    const uint8_t *const wrow[2] = {wexp + (uint64_t)c0 * a.dn_row_bytes, wexp + (uint64_t)(c0 + 32) * a.dn_row_bytes};
-    r9vx_f32x16 acc[kMT][2];
-    m2_mainloop<DN, kMT, 2>(stages, asrc, wrow, a.dff / kTileK, wave, lane, lutf, acc);
+    const M3WRow w{a.w_dn + ((uint64_t)expert * a.dm + n0) * a.dn_row_bytes, (tid >> 1) * (uint32_t)a.dn_row_bytes};
+    const uint32_t rh = wv >> 2, cq = wv & 3;
+    const uint32_t nr = m3_active_tiles(rows, 128 * rh);
+    r9vx_f32x16 acc[4][2];
+    m3_run<DN>(nr, sm, a.h16, aoff, w, a.dff / kTileK, tid, wv, lutf, 128 * rh, 64 * cq, 64 * cq + 32, acc);
 
     float *o = reinterpret_cast<float *>(a.ws + a.L.o);
+    const uint32_t c0 = n0 + 64 * cq + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < kMT; ++i) {
+    for (int t = 0; t < 4; ++t) {
+        if ((uint32_t)t >= nr) break;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const uint32_t rl = 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const uint32_t rl = 128 * rh + 32 * t + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (rl >= rows) continue;
             const float sc = rowsc[rl];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) o[(uint64_t)(pos0 + rl) * a.dm + c0 + 32 * j] = acc[i][j][r] * sc;
+            for (int j = 0; j < 2; ++j) o[(uint64_t)(pos0 + rl) * a.dm + c0 + 32 * j] = acc[t][j][r] * sc;
         }
     }
 }
@@ -320,20 +368,25 @@ int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStr
     hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(1024), 0, s, a);
     /* upper bound on row tiles: ceil(P/128) + one partial tile per work item */
     const uint32_t max_tiles = (a.p + kBM - 1) / kBM + (a.p < p.e ? a.p : p.e) + (p.shared ? p.shared * ((p.t + kBM - 1) / kBM) : 0);
-    dim3 ggu(max_tiles * (p.dff / 128)), gdn(max_tiles * (p.dm / 256));
+    const uint32_t tiles8 = (max_tiles + 7) / 8 * 8; /* xcd_tile's grid */
+    const uint32_t max_tiles3 = (a.p + kMoeTileM3 - 1) / kMoeTileM3 + (a.p < p.e ? a.p : p.e) +
+                                (p.shared ? p.shared * ((p.t + kMoeTileM3 - 1) / kMoeTileM3) : 0);
+    const uint32_t tiles3_8 = (max_tiles3 + 7) / 8 * 8;
+    dim3 ggu(tiles8 * (p.dff / 128));
+    dim3 ggu3(tiles3_8 * (p.dff / 128)), gdn3(tiles3_8 * (p.dm / 256));
     if (p.scheme_gu == R9VX_SCHEME_IQ3_S)
         hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_IQ3_S>, ggu, dim3(256), 0, s, a);
     else if (p.scheme_gu == R9VX_SCHEME_IQ4_XS)
-        hipLaunchKernelGGL(moe_gu_mfma_kernel<R9VX_SCHEME_IQ4_XS>, ggu, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_IQ4_XS>, ggu3, dim3(512), 0, s, a);
     else
-        hipLaunchKernelGGL(moe_gu_mfma_kernel<R9VX_SCHEME_Q4_K>, ggu, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q4_K>, ggu3, dim3(512), 0, s, a);
     const uint32_t nrows = a.p + p.shared * p.t;
     if (p.scheme_dn == R9VX_SCHEME_Q4_K) {
         hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3((nrows + 3) / 4), dim3(256), 0, s, a, nrows);
-        hipLaunchKernelGGL(moe_dn_mfma_kernel<R9VX_SCHEME_Q4_K>, gdn, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(moe_dn_m3_kernel<R9VX_SCHEME_Q4_K>, gdn3, dim3(512), 0, s, a);
     } else {
         hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3((nrows + 3) / 4), dim3(256), 0, s, a, nrows);
-        hipLaunchKernelGGL(moe_dn_mfma_kernel<R9VX_SCHEME_IQ4_XS>, gdn, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(moe_dn_m3_kernel<R9VX_SCHEME_IQ4_XS>, gdn3, dim3(512), 0, s, a);
     }
     return (int)hipGetLastError();
 }

@@ -70,6 +70,40 @@ uint32_t block_bytes(uint32_t s) {
 }
 uint32_t block_len(uint32_t s) { return s == R9VX_SCHEME_Q8_0 ? 32 : 256; }
 
+/* The weight element type and device layout each scheme is read in. */
+uint32_t scheme_dtype(uint32_t s) {
+    return s == R9VX_SCHEME_Q8_0 || s == R9VX_SCHEME_Q6_K ? R9VX_DTYPE_I8 : R9VX_DTYPE_I4;
+}
+uint32_t scheme_layout(uint32_t s) {
+    if (s == R9VX_SCHEME_Q8_0 || s == R9VX_SCHEME_Q6_K) return R9VX_LAYOUT_SPLIT;
+    if (s == R9VX_SCHEME_IQ3_S) return R9VX_LAYOUT_IQ3S_112;
+    return R9VX_LAYOUT_GGUF_WIRE;
+}
+const char *layout_name(uint32_t l) {
+    switch (l) {
+    case R9VX_LAYOUT_CONTIGUOUS: return "contiguous";
+    case R9VX_LAYOUT_L0: return "L0";
+    case R9VX_LAYOUT_L1: return "L1";
+    case R9VX_LAYOUT_L1S: return "L1S";
+    case R9VX_LAYOUT_GGUF_WIRE: return "gguf_wire";
+    case R9VX_LAYOUT_SPLIT: return "split";
+    case R9VX_LAYOUT_IQ3S_112: return "iq3s_112";
+    default: return "unknown";
+    }
+}
+
+/* A weight's element type and layout must be the ones this path reads for
+ * its scheme: the reference's native layouts (L0 row-major records, L1 / L1S
+ * tiles, crates/r9v-format/src/repack.rs:274-287) are refused, not misread. */
+void check_weight_keys(const char *what, uint32_t scheme, uint32_t dtype, uint32_t layout, Problems &pr) {
+    if (layout != scheme_layout(scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "%s layout %u (%s): scheme %u is read in the %s layout (code %u) only", what,
+               layout, layout_name(layout), scheme, layout_name(scheme_layout(scheme)), scheme_layout(scheme));
+    if (dtype != scheme_dtype(scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "%s dtype %u: scheme %u weights are dtype %u", what, dtype, scheme,
+               scheme_dtype(scheme));
+}
+
 /* Bytes of one weight row as the kernels read it. */
 uint64_t device_row_bytes(uint32_t s, uint32_t k) {
     if (s == R9VX_SCHEME_Q8_0) return k;
@@ -112,6 +146,12 @@ static void check_matmul_static(const r9vx_matmul_static *st, Problems &pr) {
         pr.add(R9VX_ERR_UNSUPPORTED, "the swiglu epilogue runs the decode GEMV only: bf16 activations, m_bucket <= 8");
     if (st->epilogue == R9VX_EPILOGUE_RESIDUAL && st->residual_dtype != R9VX_DTYPE_F32)
         pr.add(R9VX_ERR_UNSUPPORTED, "residual_dtype %u: only f32 residuals", st->residual_dtype);
+    if (matmul_scheme(st->w_scheme)) check_weight_keys("w", st->w_scheme, st->w_dtype, st->w_layout, pr);
+    if (st->act_scheme != R9VX_ACT_SCHEME_NONE)
+        pr.add(R9VX_ERR_UNSUPPORTED, "act_scheme %u: activations are not quantized on this path", st->act_scheme);
+    if (st->transpose_w) pr.add(R9VX_ERR_UNSUPPORTED, "transpose_w: weights are [N, K] rows of blocks");
+    if (st->interleave) pr.add(R9VX_ERR_UNSUPPORTED, "interleave is not implemented");
+    if (st->sparse) pr.add(R9VX_ERR_UNSUPPORTED, "sparse (2:4) weights are not implemented");
 }
 
 /* The MFMA path (bf16 activations, m > 8) stages x as fp16 rows plus per-row
@@ -124,7 +164,9 @@ size_t r9vx_matmul_workspace_bytes(const r9vx_matmul_static *st) {
 uint64_t r9vx_matmul_static_bytes(const r9vx_matmul_static *st, uint32_t m) {
     if (!st || !matmul_scheme(st->w_scheme)) return 0;
     const uint64_t w_rows = st->epilogue == R9VX_EPILOGUE_SWIGLU ? 2ull * st->n : st->n;
-    uint64_t w = w_rows * (st->k / block_len(st->w_scheme)) * block_bytes(st->w_scheme);
+    /* the device layout's bytes (IQ3_S: 112-byte blocks; split layouts hold the wire bytes) */
+    uint64_t w = w_rows * (split_scheme(st->w_scheme) ? (st->k / block_len(st->w_scheme)) * block_bytes(st->w_scheme)
+                                                       : device_row_bytes(st->w_scheme, st->k));
     uint64_t xe = st->in_dtype == R9VX_DTYPE_F32 ? 4 : 2;
     uint64_t ye = st->out_dtype == R9VX_DTYPE_F32 ? 4 : 2;
     return w + (uint64_t)m * st->k * xe + (uint64_t)m * st->n * ye;
@@ -298,13 +340,25 @@ uint64_t r9vx_moe_route_static_bytes(const r9vx_moe_route_static *st, uint32_t t
     return (uint64_t)t * st->e_total * 4 + (st->has_bias ? 4ull * st->e_total : 0) + (uint64_t)t * st->top_k * 8;
 }
 
-int r9vx_moe_route_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_args *a,
-                          r9vx_stream_t stream) {
+/* Per row (crates/r9v-t0/src/moe_route.rs:320-398): the bias add, the max,
+ * the subtraction, exp and sum of the softmax and its divide (or sigmoid's
+ * exp, add and divide), then the K scale multiplies, sum and divides. */
+uint64_t r9vx_moe_route_static_flops(const r9vx_moe_route_static *st, uint32_t t) {
+    if (!st) return 0;
+    const uint64_t per_e = (st->has_bias ? 1u : 0u) + 4u;
+    const uint64_t per_k = 1u + (st->renormalize ? 2u : 0u);
+    return (uint64_t)t * (per_e * st->e_total + per_k * st->top_k);
+}
+
+static int route_launch(const char *op, const r9vx_moe_route_static *st, const r9vx_moe_route_args *a,
+                        uint32_t *status, bool need_status, r9vx_stream_t stream) {
     Problems pr;
     if (!st || !a) {
         pr.add(R9VX_ERR_NULL, "static and args must be non-NULL");
-        return pr.finish("moe_route");
+        return pr.finish(op);
     }
+    if (need_status && !status) pr.add(R9VX_ERR_NULL, "status word is NULL");
+    if (status && ((uintptr_t)status & 3u)) pr.add(R9VX_ERR_ALIGN, "status word must be 4-byte aligned");
     float scale;
     memcpy(&scale, &st->scale_bits, 4);
     if (st->top_k == 0) pr.add(R9VX_ERR_INVALID, "top_k must be > 0");
@@ -320,11 +374,33 @@ int r9vx_moe_route_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_
     if (!a->logits || !a->expert_ids || !a->weights) pr.add(R9VX_ERR_NULL, "logits, expert_ids and weights are required");
     if (st->has_bias && !a->bias) pr.add(R9VX_ERR_NULL, "has_bias set but bias is NULL");
     if (!st->has_bias && a->bias) pr.add(R9VX_ERR_INVALID, "bias given but has_bias is 0");
-    int rc = pr.finish("moe_route");
+    int rc = pr.finish(op);
     if (rc) return rc;
-    r9vx_route_problem p{a->logits, a->bias, a->expert_ids, a->weights, a->t, st->e_total, st->top_k,
+    r9vx_route_problem p{a->logits, a->bias,        a->expert_ids, a->weights,
+                         status,   a->t,           st->e_total,   st->top_k,
                          st->scoring, st->renormalize ? 1u : 0u, scale};
-    return hip_status("moe_route", r9vx_launch_route(p, reinterpret_cast<hipStream_t>(stream)));
+    return hip_status(op, r9vx_launch_route(p, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int r9vx_moe_route_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_args *a,
+                          r9vx_stream_t stream) {
+    return route_launch("moe_route", st, a, nullptr, false, stream);
+}
+
+int r9vx_moe_route_launch_ex(const r9vx_moe_route_static *st, const r9vx_moe_route_args *a, uint32_t *status,
+                             r9vx_stream_t stream) {
+    return route_launch("moe_route_ex", st, a, status, true, stream);
+}
+
+int r9vx_status_read(const uint32_t *word, uint32_t *status, r9vx_stream_t stream) {
+    if (!word || !status) {
+        g_last_error = "status_read: device word and status are required";
+        return R9VX_ERR_NULL;
+    }
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    int rc = (int)hipMemcpyAsync(status, word, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
+    if (!rc) rc = (int)hipStreamSynchronize(s);
+    return hip_status("status_read", rc);
 }
 
 static void check_route_static(const r9vx_moe_route_static *st, uint32_t t, Problems &pr, float &scale) {
@@ -375,6 +451,7 @@ int r9vx_moe_route_hidden_launch(const r9vx_moe_route_static *st, const r9vx_moe
     p.bias = a->bias;
     p.logits = reinterpret_cast<float *>(a->workspace);
     p.counter = reinterpret_cast<uint32_t *>(a->workspace + logit_bytes);
+    p.status = reinterpret_cast<uint32_t *>(a->workspace + logit_bytes + 4);
     p.ids = a->expert_ids;
     p.weights = a->weights;
     p.t = a->t;
@@ -401,6 +478,18 @@ int r9vx_router_repack_launch(const float *w, uint32_t e, uint32_t dm, float *ou
     return hip_status("router_repack", r9vx_launch_router_repack(w, e, dm, out, reinterpret_cast<hipStream_t>(stream)));
 }
 
+int r9vx_moe_route_hidden_status(const r9vx_moe_route_static *st, const uint8_t *workspace, uint32_t *status,
+                                 r9vx_stream_t stream) {
+    if (!st || !workspace || !status) {
+        g_last_error = "moe_route_hidden_status: static, workspace and status are required";
+        return R9VX_ERR_NULL;
+    }
+    const size_t logit_bytes = ((size_t)st->t_bucket * st->e_total * 4 + 255) & ~(size_t)255;
+    const int rc = r9vx_status_read(reinterpret_cast<const uint32_t *>(workspace + logit_bytes + 4), status, stream);
+    if (rc) g_last_error = "moe_route_hidden_status: " + g_last_error;
+    return rc;
+}
+
 int r9vx_moe_route_status(uint32_t *status, r9vx_stream_t stream) {
     if (!status) {
         g_last_error = "moe_route_status: status is NULL";
@@ -416,19 +505,49 @@ static void check_ffn_static(const r9vx_moe_ffn_static *st, Problems &pr) {
     if (st->k_topk == 0 || st->k_topk > kMoeMaxK) pr.add(R9VX_ERR_INVALID, "K=%u must be in 1..32", st->k_topk);
     if (st->dm == 0 || st->dm % 256) pr.add(R9VX_ERR_INVALID, "Dm=%u must be a positive multiple of 256", st->dm);
     if (st->dff == 0 || st->dff % 256) pr.add(R9VX_ERR_INVALID, "Dff=%u must be a positive multiple of 256", st->dff);
-    if (!known_scheme(st->gate_up_scheme) && !packed_scheme(st->gate_up_scheme))
-        pr.add(R9VX_ERR_UNSUPPORTED, "gate_up_scheme %u: Q4_K (12), IQ4_XS (23) or IQ3_S (21)", st->gate_up_scheme);
-    if (!known_scheme(st->down_scheme)) pr.add(R9VX_ERR_UNSUPPORTED, "down_scheme %u", st->down_scheme);
+    if (!known_scheme(st->gate_up.scheme) && !packed_scheme(st->gate_up.scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "gate_up scheme %u: Q4_K (12), IQ4_XS (23) or IQ3_S (21)", st->gate_up.scheme);
+    else
+        check_weight_keys("gate_up", st->gate_up.scheme, st->gate_up.dtype, st->gate_up.layout, pr);
+    if (!known_scheme(st->down.scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "down scheme %u: Q4_K (12) or IQ4_XS (23)", st->down.scheme);
+    else
+        check_weight_keys("down", st->down.scheme, st->down.dtype, st->down.layout, pr);
+    if (st->act_scheme != R9VX_ACT_SCHEME_NONE)
+        pr.add(R9VX_ERR_UNSUPPORTED, "act_scheme %u: activations are not quantized on this path", st->act_scheme);
+    if (st->placement_kind != R9VX_PLACEMENT_DEVICE)
+        pr.add(R9VX_ERR_UNSUPPORTED, "placement_kind %u: device placement only", st->placement_kind);
     if (st->in_dtype != R9VX_DTYPE_BF16) pr.add(R9VX_ERR_UNSUPPORTED, "in_dtype %u: bf16 activations only", st->in_dtype);
     if (st->out_dtype != R9VX_DTYPE_F32) pr.add(R9VX_ERR_UNSUPPORTED, "out_dtype %u: f32 output only", st->out_dtype);
     if (st->act != R9VX_ACT_SILU) pr.add(R9VX_ERR_UNSUPPORTED, "act %u: SiLU only", st->act);
     if (st->shared_experts > 8) pr.add(R9VX_ERR_UNSUPPORTED, "shared_experts=%u exceeds 8", st->shared_experts);
     if (st->t_bucket == 0) pr.add(R9VX_ERR_INVALID, "t_bucket must be > 0");
+    /* the grouped GEMMs address the staged activations, the h rows and one
+     * expert's weights with 32-bit byte offsets */
+    const uint64_t rows = (uint64_t)st->t_bucket * (st->k_topk + st->shared_experts);
+    if (2ull * st->t_bucket * st->dm >= (1ull << 32) || 2ull * rows * st->dff >= (1ull << 32) ||
+        2ull * st->dff * device_row_bytes(R9VX_SCHEME_Q4_K, st->dm) >= (1ull << 32) ||
+        (uint64_t)st->dm * device_row_bytes(R9VX_SCHEME_Q4_K, st->dff) >= (1ull << 32))
+        pr.add(R9VX_ERR_UNSUPPORTED, "t_bucket=%u, Dm=%u, Dff=%u: staged operands or one expert exceed 4 GiB",
+               st->t_bucket, st->dm, st->dff);
 }
 
 size_t r9vx_moe_ffn_workspace_bytes(const r9vx_moe_ffn_static *st) {
     if (!st) return 0;
     return (size_t)r9vx_moe_layout(st->t_bucket, st->e_local, st->k_topk, st->dm, st->dff, st->shared_experts).total;
+}
+
+uint64_t r9vx_moe_ffn_expert_bytes(const r9vx_moe_ffn_static *st) {
+    if (!st) return 0;
+    return 2ull * st->dff * device_row_bytes(st->gate_up.scheme, st->dm) +
+           (uint64_t)st->dm * device_row_bytes(st->down.scheme, st->dff);
+}
+
+uint64_t r9vx_moe_ffn_static_bytes(const r9vx_moe_ffn_static *st, uint32_t t) {
+    if (!st) return 0;
+    const uint64_t pairs = (uint64_t)t * st->k_topk;
+    const uint64_t experts = (pairs < st->e_local ? pairs : st->e_local) + st->shared_experts;
+    return experts * r9vx_moe_ffn_expert_bytes(st) + (uint64_t)t * st->dm * 2 + pairs * 8 + (uint64_t)t * st->dm * 4;
 }
 
 uint64_t r9vx_moe_ffn_static_flops(const r9vx_moe_ffn_static *st, uint32_t t) {
@@ -464,8 +583,8 @@ static r9vx_moe_problem ffn_problem(const r9vx_moe_ffn_static *st, const r9vx_mo
     p.dff = st->dff;
     p.shared = st->shared_experts;
     p.t_bucket = st->t_bucket;
-    p.scheme_gu = st->gate_up_scheme;
-    p.scheme_dn = st->down_scheme;
+    p.scheme_gu = st->gate_up.scheme;
+    p.scheme_dn = st->down.scheme;
     return p;
 }
 

@@ -46,6 +46,14 @@ __device__ __forceinline__ float r9vx_iq4xs_scale(r9vx_u32x2 h, uint32_t c) {
 }
 #endif
 
+/* IQ3_S device block byte j (0..111) comes from wire byte r9vx_iq3s_wire_byte(j)
+ * (j < 110; bytes 110, 111 are zero): qs (wire 2..65), signs (74..105), qh
+ * (66..73), scales (106..109), d (0..1).  Used by the device repack and the
+ * host-side repack of r9vx_gguf_upload. */
+__host__ __device__ inline uint32_t r9vx_iq3s_wire_byte(uint32_t j) {
+    return j < 64 ? 2 + j : j < 96 ? 10 + j : j < 104 ? j - 30 : j < 108 ? j + 2 : j - 108;
+}
+
 /* Internal launchers (return hipError_t as int). */
 int r9vx_launch_dequant(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, uint32_t k,
                         float *out, hipStream_t stream);
@@ -91,6 +99,7 @@ struct r9vx_route_problem {
     const float *bias;
     uint32_t *ids;
     float *weights;
+    uint32_t *status; /* the launch's status word; NULL = the device's plain-launch word */
     uint32_t t, e, k, scoring, renormalize;
     float scale;
 };
@@ -102,6 +111,7 @@ struct r9vx_route_hidden_problem {
     const float *bias;
     float *logits;     /* workspace [t, e] */
     uint32_t *counter; /* workspace word, zero between launches */
+    uint32_t *status;  /* workspace word: this launch's status bits */
     uint32_t *ids;
     float *weights;
     uint32_t t, e, k, dm, scoring, renormalize;

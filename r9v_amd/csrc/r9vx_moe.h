@@ -3,7 +3,8 @@
  * crates/r9v-kgen/src/abi/workspace.rs:13-40) and the stage launchers.
  *
  * Workspace regions (each 256-byte aligned), sized for t_bucket tokens:
- *   status  u32[16]  [0] status bits, [1] scan counter, [2] work items
+ *   status  u32[16]  [0] status bits, [1] scan counter, [2] work items,
+ *                    [3] 128-row tiles, [4] 256-row tiles
  *   counts  u32[E]   pairs per expert
  *   offsets u32[E+1] exclusive scan of counts
  *   sorted  u32[P]   pair index (token*K + slot) at each sorted position
@@ -12,7 +13,8 @@
  *   ccount  u32[E*C] per-expert counts of each 256-pair chunk
  *   cbase   u32[E*C] exclusive scan of ccount over chunks
  *   work    u32x4[E+S] (expert, first position, pair count, 0) of active experts
- *   tiles   u32x4[...] grouped-GEMM tile schedule
+ *   tiles   u32x4[...] grouped-GEMM tile schedule, 128-row tiles
+ *   tiles3  u32x4[...] the same work in 256-row tiles (the r9vx_mma3.h kernels)
  *   h       f32[(P + S*T) * Dff]  SwiGLU rows in sorted order, shared rows after
  *   o       f32[(P + S*T) * Dm]   expert output rows in the same order
  *   hmax    u32[P + S*T]          bits of max|h| per row (grouped GEMM)
@@ -33,12 +35,13 @@
 
 constexpr uint32_t kMoeMaxE = 1024;
 constexpr uint32_t kMoeMaxK = 32;
-constexpr uint32_t kMoeTileM = 128; /* grouped-GEMM rows per tile */
+constexpr uint32_t kMoeTileM = 128;  /* grouped-GEMM rows per tile */
+constexpr uint32_t kMoeTileM3 = 256; /* rows per tile of the r9vx_mma3.h grouped GEMMs */
 
 struct MoeLayout {
-    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, work, tiles, h, o, hmax, h16, x16, xscale,
-        pinfo, total;
-    uint32_t max_tiles;
+    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, work, tiles, tiles3, h, o, hmax, h16, x16,
+        xscale, pinfo, total;
+    uint32_t max_tiles, max_tiles3;
 };
 
 inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint32_t dm, uint32_t dff,
@@ -54,6 +57,7 @@ inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint
         return at;
     };
     L.max_tiles = (uint32_t)((p + (uint64_t)shared * t_bucket) / kMoeTileM + e + shared + 1);
+    L.max_tiles3 = (uint32_t)((p + (uint64_t)shared * t_bucket) / kMoeTileM3 + e + shared + 1);
     L.status = take(64);
     L.counts = take(4ull * e);
     L.offsets = take(4ull * (e + 1));
@@ -64,6 +68,7 @@ inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint
     L.cbase = take(4ull * e * nchunk);
     L.work = take(16ull * (e + shared));
     L.tiles = take(16ull * L.max_tiles + 16);
+    L.tiles3 = take(16ull * L.max_tiles3 + 16);
     L.h = take(4ull * rows * dff);
     L.o = take(4ull * rows * dm);
     L.hmax = take(4ull * rows);

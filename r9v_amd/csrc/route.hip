@@ -16,15 +16,20 @@
  *
  * Refusal before mutation (:313-418): a check pass flags non-finite logits,
  * bias or post-bias scores, and a zero selected sum under sigmoid
- * renormalisation, in a device status word; the compute pass writes nothing
- * when the word is set.  T <= 8 runs both passes in one workgroup, one wave per row.
+ * renormalisation, in the launch's status word; the compute pass writes
+ * nothing when the word is set.  The word is the caller's (the _ex launch),
+ * the workspace's (routing from hidden states) or, for the plain launch, one
+ * library word per device.  T <= 8 runs both passes in one workgroup, one wave per row.
  */
+#include <mutex>
+
 #include "r9vx_device.h"
 #include "r9vx_expf.h"
 #include "r9vx_internal.h"
 
 namespace {
 
+/* The status word of plain r9vx_moe_route_launch calls on this device. */
 __device__ uint32_t g_route_status;
 
 constexpr int kMaxK = 32;
@@ -34,6 +39,7 @@ struct RouteArgs {
     const float *bias;
     uint32_t *ids;
     float *weights;
+    uint32_t *status; /* this launch's status word */
     uint32_t t, e, k, scoring, renormalize;
     float scale;
 };
@@ -276,14 +282,14 @@ __device__ __forceinline__ void route_loaded(const RouteArgs &a, uint32_t lane, 
     if (a.renormalize) my_w = my_w / selected_sum;
 }
 
-__global__ void clear_status_kernel() { g_route_status = 0u; }
+__global__ void clear_status_kernel(uint32_t *status) { *status = 0u; }
 
 __global__ __launch_bounds__(256) void route_check_kernel(RouteArgs a) {
     uint32_t lane = threadIdx.x & 63;
     uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.t) return;
     uint32_t bad = check_row(a, row, lane);
-    if (bad && lane == 0) atomicOr(&g_route_status, bad);
+    if (bad && lane == 0) atomicOr(a.status, bad);
 }
 
 /* Grid-wide form: runs after route_check_kernel. */
@@ -296,7 +302,7 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
     const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t row = blockIdx.x * 4 + wv;
     if (row >= a.t) return;
-    if (__atomic_load_n(&g_route_status, __ATOMIC_RELAXED) != 0u) return;
+    if (__atomic_load_n(a.status, __ATOMIC_RELAXED) != 0u) return;
     float sc[PER], lg[PER], bs[PER];
     load_row<PER>(a, row, lane, sc, lg, bs);
     uint32_t id;
@@ -333,7 +339,7 @@ __global__ __launch_bounds__(512) void route_small_kernel(RouteArgs a) {
     if (!bad) route_loaded<PER>(a, lane, sc, etab, sbuf[row], id, w);
     __syncthreads();
     bad = bad_all;
-    if (threadIdx.x == 0) g_route_status = bad;
+    if (threadIdx.x == 0) *a.status = bad;
     if (bad) return;
     if (lane < a.k) {
         a.ids[(uint64_t)row * a.k + lane] = id;
@@ -468,7 +474,7 @@ __global__ __launch_bounds__(256) void route_hidden_kernel(RouteHiddenArgs a) {
     __syncthreads();
     const uint32_t bad = bad_all;
     if (threadIdx.x == 0) {
-        g_route_status = bad;
+        *a.r.status = bad;
         atomicExch(a.counter, 0u);
     }
     if (bad) return;
@@ -502,7 +508,8 @@ int r9vx_launch_router_repack(const float *w, uint32_t e, uint32_t dm, float *ou
 
 int r9vx_launch_route_hidden(const r9vx_route_hidden_problem &p, hipStream_t stream) {
     RouteHiddenArgs a{p.x, p.w, p.counter, p.dm,
-                      RouteArgs{p.logits, p.bias, p.ids, p.weights, p.t, p.e, p.k, p.scoring, p.renormalize, p.scale}};
+                      RouteArgs{p.logits, p.bias, p.ids, p.weights, p.status, p.t, p.e, p.k, p.scoring, p.renormalize,
+                                p.scale}};
     const dim3 grid((p.e + 63) / 64, p.t);
     const uint32_t per = (p.e + 63) / 64;
     if (per <= 1)
@@ -524,15 +531,33 @@ static int launch_route_per(const RouteArgs &a, hipStream_t stream) {
         hipLaunchKernelGGL((route_small_kernel<PER>), dim3(1), dim3(64 * a.t), 0, stream, a);
         return (int)hipGetLastError();
     }
-    hipLaunchKernelGGL(clear_status_kernel, dim3(1), dim3(1), 0, stream);
+    hipLaunchKernelGGL(clear_status_kernel, dim3(1), dim3(1), 0, stream, a.status);
     dim3 grid((a.t + 3) / 4);
     hipLaunchKernelGGL(route_check_kernel, grid, dim3(256), 0, stream, a);
     hipLaunchKernelGGL((route_kernel<PER>), grid, dim3(256), 0, stream, a);
     return (int)hipGetLastError();
 }
 
+/* Device address of this device's plain-launch status word, looked up once
+ * per device. */
+static uint32_t *plain_status_word() {
+    static uint32_t *words[64];
+    static std::mutex mu;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> g(mu);
+    if (!words[dev]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_route_status)) != hipSuccess) return nullptr;
+        words[dev] = static_cast<uint32_t *>(ptr);
+    }
+    return words[dev];
+}
+
 int r9vx_launch_route(const r9vx_route_problem &p, hipStream_t stream) {
-    RouteArgs a{p.logits, p.bias, p.ids, p.weights, p.t, p.e, p.k, p.scoring, p.renormalize, p.scale};
+    uint32_t *status = p.status ? p.status : plain_status_word();
+    if (!status) return (int)hipErrorInvalidSymbol;
+    RouteArgs a{p.logits, p.bias, p.ids, p.weights, status, p.t, p.e, p.k, p.scoring, p.renormalize, p.scale};
     /* registers per lane: the next power of two >= ceil(E / 64) */
     const uint32_t per = (p.e + 63) / 64;
     if (per <= 1) return launch_route_per<1>(a, stream);
@@ -548,6 +573,8 @@ int r9vx_read_route_status(uint32_t *status, hipStream_t stream) {
     if (rc) return rc;
     rc = (int)hipStreamSynchronize(stream);
     if (rc) return rc;
-    hipLaunchKernelGGL(clear_status_kernel, dim3(1), dim3(1), 0, stream);
+    uint32_t *word = plain_status_word();
+    if (!word) return (int)hipErrorInvalidSymbol;
+    hipLaunchKernelGGL(clear_status_kernel, dim3(1), dim3(1), 0, stream, word);
     return (int)hipGetLastError();
 }

@@ -18,7 +18,9 @@ PKG = pathlib.Path(__file__).resolve().parent
 LIB_PATH = PKG / "libr9vx.so"
 
 # enums (include/r9vx.h)
-F32, F16, BF16, U32 = 0, 1, 2, 8
+F32, F16, BF16, I8, I4, U32 = 0, 1, 2, 5, 6, 8
+LAYOUT_L0, LAYOUT_L1, LAYOUT_L1S = 1, 2, 3                      # the reference's layouts: refused
+LAYOUT_GGUF_WIRE, LAYOUT_SPLIT, LAYOUT_IQ3S_112 = 0x100, 0x101, 0x102
 Q4_K, IQ4_XS, Q6_K, Q8_0, IQ3_S = 12, 23, 14, 8, 21
 EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_RESIDUAL, EPILOGUE_SWIGLU = 0, 1, 2, 3
 SCORING_SOFTMAX, SCORING_SIGMOID = 0, 1
@@ -35,9 +37,10 @@ _U64 = ctypes.c_uint64
 
 
 class MatmulStatic(ctypes.Structure):
-    _fields_ = [("m_bucket", _U32), ("n", _U32), ("k", _U32), ("w_scheme", _U32),
-                ("in_dtype", _U32), ("out_dtype", _U32), ("epilogue", _U32),
-                ("residual_dtype", _U32)]
+    _fields_ = [("m_bucket", _U32), ("n", _U32), ("k", _U32), ("w_dtype", _U32), ("w_scheme", _U32),
+                ("w_layout", _U32), ("in_dtype", _U32), ("act_scheme", _U32), ("out_dtype", _U32),
+                ("epilogue", _U32), ("residual_dtype", _U32), ("transpose_w", _U32), ("interleave", _U32),
+                ("sparse", _U32)]
 
 
 class MatmulArgs(ctypes.Structure):
@@ -62,11 +65,15 @@ class MoeRouteHiddenArgs(ctypes.Structure):
                 ("workspace", _P), ("t", _U32), ("dm", _U32)]
 
 
+class MoeFfnProj(ctypes.Structure):
+    _fields_ = [("dtype", _U32), ("scheme", _U32), ("layout", _U32)]
+
+
 class MoeFfnStatic(ctypes.Structure):
     _fields_ = [("t_bucket", _U32), ("e_local", _U32), ("k_topk", _U32), ("dm", _U32),
-                ("dff", _U32), ("gate_up_scheme", _U32), ("down_scheme", _U32),
-                ("in_dtype", _U32), ("out_dtype", _U32), ("act", _U32),
-                ("shared_experts", _U32), ("_reserved", _U32)]
+                ("dff", _U32), ("gate_up", MoeFfnProj), ("down", MoeFfnProj),
+                ("in_dtype", _U32), ("act_scheme", _U32), ("act", _U32), ("out_dtype", _U32),
+                ("shared_experts", _U32), ("placement_kind", _U32)]
 
 
 class MoeFfnArgs(ctypes.Structure):
@@ -82,15 +89,21 @@ EXPORTS = [
     ("r9vx_matmul_static_bytes", [_P, _U32], ctypes.c_uint64),
     ("r9vx_matmul_static_flops", [_P, _U32], ctypes.c_uint64),
     ("r9vx_moe_route_launch", [_P, _P, _P], ctypes.c_int),
+    ("r9vx_moe_route_launch_ex", [_P, _P, _P, _P], ctypes.c_int),
     ("r9vx_moe_route_status", [_P, _P], ctypes.c_int),
+    ("r9vx_status_read", [_P, _P, _P], ctypes.c_int),
     ("r9vx_moe_route_static_bytes", [_P, _U32], ctypes.c_uint64),
+    ("r9vx_moe_route_static_flops", [_P, _U32], ctypes.c_uint64),
     ("r9vx_moe_route_hidden_launch", [_P, _P, _P], ctypes.c_int),
     ("r9vx_moe_route_hidden_workspace_bytes", [_P], ctypes.c_size_t),
+    ("r9vx_moe_route_hidden_status", [_P, _P, _P, _P], ctypes.c_int),
     ("r9vx_router_repack_launch", [_P, _U32, _U32, _P, _P], ctypes.c_int),
     ("r9vx_moe_ffn_launch", [_P, _P, _P], ctypes.c_int),
     ("r9vx_moe_ffn_workspace_bytes", [_P], ctypes.c_size_t),
     ("r9vx_moe_ffn_status", [_P, _P, _P, _P], ctypes.c_int),
     ("r9vx_moe_ffn_static_flops", [_P, _U32], ctypes.c_uint64),
+    ("r9vx_moe_ffn_static_bytes", [_P, _U32], ctypes.c_uint64),
+    ("r9vx_moe_ffn_expert_bytes", [_P], ctypes.c_uint64),
     ("r9vx_moe_sort_launch", [_P, _P, _U32, _P, _P, _P, _P, _P], ctypes.c_int),
     ("r9vx_dequantize_launch", [_U32, _P, _U32, _U32, _P, _P], ctypes.c_int),
     ("r9vx_validate_weights_launch", [_U32, _P, _U32, _U32, _P, _P], ctypes.c_int),
@@ -197,9 +210,21 @@ def _dtype_code(t):
 
 # ---------------------------------------------------------------- matmul
 
+def weight_dtype(scheme):
+    """The weight element type a scheme's blocks are keyed with."""
+    return I8 if scheme in SPLIT_SCHEMES else I4
+
+
+def weight_layout(scheme):
+    """The device layout this path reads a scheme in."""
+    return LAYOUT_SPLIT if scheme in SPLIT_SCHEMES else LAYOUT_IQ3S_112 if scheme == IQ3_S else LAYOUT_GGUF_WIRE
+
+
 def matmul_static(n, k, w_scheme, in_dtype, out_dtype, m_bucket=8, epilogue=EPILOGUE_NONE,
-                  residual_dtype=F32):
-    return MatmulStatic(m_bucket, n, k, w_scheme, in_dtype, out_dtype, epilogue, residual_dtype)
+                  residual_dtype=F32, w_layout=None):
+    return MatmulStatic(m_bucket, n, k, weight_dtype(w_scheme), w_scheme,
+                        weight_layout(w_scheme) if w_layout is None else w_layout, in_dtype, 0, out_dtype,
+                        epilogue, residual_dtype, 0, 0, 0)
 
 
 def matmul(w, w_scheme, n, k, x, out_dtype=F32, bias=None, residual=None, y=None, workspace=None,
@@ -277,8 +302,11 @@ def route_static(e, k, t_bucket, scoring=SCORING_SOFTMAX, renormalize=True, scal
 
 
 def moe_route(logits, k, bias=None, scoring=SCORING_SOFTMAX, renormalize=True, scale=1.0,
-              ids=None, weights=None, stream=None):
-    torch = _need_gpu(logits, bias)
+              ids=None, weights=None, stream=None, status=None):
+    """T0 moe_route; with `status` (a device int32 tensor of one element) the
+    launch owns that status word (r9vx_moe_route_launch_ex), otherwise the
+    device's shared plain-launch word (read with moe_route_status)."""
+    torch = _need_gpu(logits, bias, status)
     t, e = logits.shape
     if ids is None:
         ids = torch.empty((t, k), dtype=torch.int32, device=logits.device)
@@ -286,8 +314,20 @@ def moe_route(logits, k, bias=None, scoring=SCORING_SOFTMAX, renormalize=True, s
         weights = torch.empty((t, k), dtype=torch.float32, device=logits.device)
     st = route_static(e, k, max(t, 1), scoring, renormalize, scale, bias is not None)
     args = MoeRouteArgs(_ptr(logits), _ptr(bias), _ptr(ids), _ptr(weights), t, 0)
-    _check(load().r9vx_moe_route_launch(ctypes.byref(st), ctypes.byref(args), _stream(torch, stream)))
+    if status is not None:
+        _check(load().r9vx_moe_route_launch_ex(ctypes.byref(st), ctypes.byref(args), _ptr(status),
+                                               _stream(torch, stream)))
+    else:
+        _check(load().r9vx_moe_route_launch(ctypes.byref(st), ctypes.byref(args), _stream(torch, stream)))
     return ids, weights
+
+
+def status_read(word, stream=None) -> int:
+    """The value of a device status word (of moe_route(status=...))."""
+    torch = _need_gpu(word)
+    s = ctypes.c_uint32(0)
+    _check(load().r9vx_status_read(_ptr(word), ctypes.byref(s), _stream(torch, stream)))
+    return s.value
 
 
 def router_repack(w, stream=None):
@@ -323,6 +363,16 @@ def moe_route_hidden(x, w_router, k, bias=None, scoring=SCORING_SOFTMAX, renorma
     return ids, weights, workspace
 
 
+def moe_route_hidden_status(workspace, e, k, t_bucket, stream=None) -> int:
+    """Status bits of the last moe_route_hidden launch with this workspace."""
+    torch = _need_gpu(workspace)
+    st = route_static(e, k, t_bucket)
+    s = ctypes.c_uint32(0)
+    _check(load().r9vx_moe_route_hidden_status(ctypes.byref(st), _ptr(workspace), ctypes.byref(s),
+                                               _stream(torch, stream)))
+    return s.value
+
+
 def moe_route_status(stream=None) -> int:
     import torch
 
@@ -334,8 +384,11 @@ def moe_route_status(stream=None) -> int:
 # ---------------------------------------------------------------- moe_ffn
 
 def ffn_static(t_bucket, e, k, dm, dff, shared=0, gate_up_scheme=IQ4_XS, down_scheme=Q4_K):
-    return MoeFfnStatic(t_bucket, e, k, dm, dff, gate_up_scheme, down_scheme, BF16, F32,
-                        ACT_SILU, shared, 0)
+    def proj(s):
+        return MoeFfnProj(weight_dtype(s), s, weight_layout(s))
+
+    return MoeFfnStatic(t_bucket, e, k, dm, dff, proj(gate_up_scheme), proj(down_scheme), BF16, 0,
+                        ACT_SILU, F32, shared, 0)
 
 
 def ffn_workspace_bytes(st: MoeFfnStatic) -> int:

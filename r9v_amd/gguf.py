@@ -344,16 +344,22 @@ class ShardSet:
 
 # ------------------------------------------------------------------ loading
 
+def device_bytes(info: TensorInfo) -> int:
+    """Bytes of a tensor in its device layout (IQ3_S: 112-byte blocks)."""
+    return info.nbytes // 110 * ffi.IQ3S_DEV_BYTES if info.dtype == ffi.IQ3_S else info.nbytes
+
+
 def upload(file: GgufFile, data, name: str, out=None, stream=None):
-    """Copies tensor `name`'s wire blocks into a device uint8 tensor (`out`, or a
-    new one) and returns it; the copy is enqueued on `stream`."""
+    """Loads tensor `name` into a device uint8 tensor (`out`, or a new one) in
+    its device layout -- Q4_K / IQ4_XS / F32 bytes as stored, IQ3_S repacked
+    into 112-byte blocks -- and returns it once the copy is done."""
     import torch
 
     info = file.tensor(name)
     if info is None:
         raise GgufError(-1, f"no tensor named {name!r}")
     if out is None:
-        out = torch.empty(info.nbytes, dtype=torch.uint8, device="cuda")
+        out = torch.empty(device_bytes(info), dtype=torch.uint8, device="cuda")
     ptr, n, _keep = _buf(data)
     rc = ffi.load().r9vx_gguf_upload(file._h, ptr, n, name.encode(), ctypes.c_void_p(out.data_ptr()),
                                      out.numel() * out.element_size(), ffi._stream(torch, stream))
@@ -372,7 +378,7 @@ def upload_gate_up(gate_file: GgufFile, gate_data, gate: str, up_file: GgufFile,
     if info is None:
         raise GgufError(-1, f"no tensor named {gate!r}")
     if out is None:
-        out = torch.empty(2 * info.nbytes, dtype=torch.uint8, device="cuda")
+        out = torch.empty(2 * device_bytes(info), dtype=torch.uint8, device="cuda")
     gp, gn, _gk = _buf(gate_data)
     up_, un, _uk = _buf(up_data)
     rc = ffi.load().r9vx_gguf_upload_gate_up(gate_file._h, gp, gn, gate.encode(), up_file._h, up_, un,
@@ -408,21 +414,19 @@ def load_matmul_weight(file: GgufFile, data, name: str, m_bucket: int = 8, in_dt
                        out_dtype: int = ffi.F32, validate: bool = True):
     """(MatmulStatic, w, w_scales) on the device for weight `name`: Q4_K /
     IQ4_XS wire blocks (w_scales None), the Q8_0 / Q6_K split layout, or
-    IQ3_S repacked on the device into 112-byte blocks (w_scales None).  With
+    IQ3_S repacked on the host into 112-byte blocks (w_scales None).  With
     `validate` the load-time scale check (check_wire_f16,
     crates/r9v-format/src/ggml.rs:421) refuses a block with a non-finite scale
-    (on the device for wire blocks; the split upload always checks)."""
+    (on the device for wire blocks; the split and IQ3_S uploads always check)."""
     st = file.matmul_static(name, m_bucket=m_bucket, in_dtype=in_dtype, out_dtype=out_dtype)
     if st.w_scheme in ffi.SPLIT_SCHEMES:
         w, w_scales = upload_split(file, data, name)
         return st, w, w_scales
     w = upload(file, data, name)
-    if validate:
+    if validate and st.w_scheme != ffi.IQ3_S:
         bad = ffi.validate_weights(w, st.w_scheme, st.n, st.k)
         if bad:
             raise GgufError(-1, f"{name}: {bad} block(s) carry a non-finite scale")
-    if st.w_scheme == ffi.IQ3_S:  # wire blocks -> the 112-byte device blocks
-        w, _ = ffi.repack(w, ffi.IQ3_S, st.n, st.k)
     return st, w, None
 
 
@@ -436,13 +440,14 @@ def load_moe_experts(file: GgufFile, data, gate: str, up: str | None, down: str,
     else:
         w_gate_up = upload_gate_up(file, data, gate, file, data, up)
     w_down = upload(file, data, down)
-    if validate:
-        bad = ffi.validate_weights(w_gate_up, st.gate_up_scheme, st.e_local * 2 * st.dff, st.dm)
-        bad += ffi.validate_weights(w_down, st.down_scheme, st.e_local * st.dm, st.dff)
+    if validate:  # IQ3_S blocks were checked on the host by the upload
+        bad = 0
+        if st.gate_up.scheme != ffi.IQ3_S:
+            bad += ffi.validate_weights(w_gate_up, st.gate_up.scheme, st.e_local * 2 * st.dff, st.dm)
+        if st.down.scheme != ffi.IQ3_S:
+            bad += ffi.validate_weights(w_down, st.down.scheme, st.e_local * st.dm, st.dff)
         if bad:
             raise GgufError(-1, f"{gate}/{down}: {bad} expert block(s) carry a non-finite scale")
-    if st.gate_up_scheme == ffi.IQ3_S:  # wire blocks -> the 112-byte device blocks
-        w_gate_up, _ = ffi.repack(w_gate_up, ffi.IQ3_S, st.e_local * 2 * st.dff, st.dm)
     return st, w_gate_up, w_down
 
 

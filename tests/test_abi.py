@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), n
     assert sorted(n for n, _, _ in ffi.EXPORTS) == names
-    assert lib.r9vx_abi_version() == 1
+    assert lib.r9vx_abi_version() == 2
 
 
 def kgen_layout(fields):
@@ -45,6 +45,88 @@ def kgen_layout(fields):
         off += al
         maxal = max(maxal, al)
     return offs, (off + maxal - 1) // maxal * maxal
+
+
+# Key declaration order of MatmulStatic / MoeFfnStatic
+# (crates/r9v-registry/src/types.rs:727-770, 801-860), u32 each.
+STATICS = {
+    "r9vx_matmul_static": ["m_bucket", "n", "k", "w_dtype", "w_scheme", "w_layout", "in_dtype", "act_scheme",
+                           "out_dtype", "epilogue", "residual_dtype", "transpose_w", "interleave", "sparse"],
+    "r9vx_moe_ffn_static": ["t_bucket", "e_local", "k_topk", "dm", "dff", "gate_up.dtype", "gate_up.scheme",
+                            "gate_up.layout", "down.dtype", "down.scheme", "down.layout", "in_dtype", "act_scheme",
+                            "act", "out_dtype", "shared_experts", "placement_kind"],
+}
+
+
+def test_static_structs_follow_the_registry_key_order(tmp_path):
+    src = tmp_path / "statics.c"
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "r9vx.h"', "int main(void){"]
+    for st, fields in STATICS.items():
+        lines.append(f'printf("{st} size %zu\\n", sizeof({st}));')
+        for name in fields:
+            lines.append(f'printf("{st} {name} %zu\\n", offsetof({st}, {name}));')
+    lines.append("return 0;}")
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "statics"
+    subprocess.run(["gcc", "-std=c11", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        st, field, val = line.split()
+        got[(st, field)] = int(val)
+    for st, fields in STATICS.items():
+        assert got[(st, "size")] == 4 * len(fields), st
+        for i, name in enumerate(fields):
+            assert got[(st, name)] == 4 * i, (st, name)
+    assert ctypes.sizeof(ffi.MatmulStatic) == got[("r9vx_matmul_static", "size")]
+    assert ctypes.sizeof(ffi.MoeFfnStatic) == got[("r9vx_moe_ffn_static", "size")]
+
+
+def test_reference_layouts_and_keys_are_refused():
+    """A weight in the reference's own L0 / L1 / L1S layout, a transposed or
+    interleaved or sparse weight, quantized activations, or a dtype that does not
+    match the scheme are typed refusals, never reinterpreted bytes."""
+    lib = ffi.load()
+    args = ffi.MatmulArgs()
+    args.m = 1
+    for layout, name in ((ffi.LAYOUT_L1, "(L1)"), (ffi.LAYOUT_L0, "(L0)"), (ffi.LAYOUT_L1S, "(L1S)"),
+                         (ffi.LAYOUT_SPLIT, "(split)")):
+        st = ffi.matmul_static(n=64, k=512, w_scheme=ffi.Q4_K, in_dtype=ffi.BF16, out_dtype=ffi.F32, w_layout=layout)
+        assert _call(lib.r9vx_matmul_launch, st, args) == -2
+        msg = lib.r9vx_last_error().decode()
+        assert name in msg and "gguf_wire layout (code 256) only" in msg, msg
+    st = ffi.matmul_static(n=64, k=512, w_scheme=ffi.IQ3_S, in_dtype=ffi.BF16, out_dtype=ffi.F32,
+                           w_layout=ffi.LAYOUT_GGUF_WIRE)
+    assert _call(lib.r9vx_matmul_launch, st, args) == -2
+    assert "iq3s_112 layout (code 258) only" in lib.r9vx_last_error().decode()
+    st = ffi.matmul_static(n=64, k=512, w_scheme=ffi.Q8_0, in_dtype=ffi.BF16, out_dtype=ffi.F32)
+    st.w_dtype, st.transpose_w, st.interleave, st.sparse, st.act_scheme = ffi.I4, 1, 1, 1, 3
+    assert _call(lib.r9vx_matmul_launch, st, args) == -2
+    msg = lib.r9vx_last_error().decode()
+    for part in ("w dtype 6", "transpose_w", "interleave", "sparse", "act_scheme 3"):
+        assert part in msg, msg
+    fst = ffi.ffn_static(t_bucket=4, e=4, k=2, dm=256, dff=256)
+    fst.gate_up.layout = ffi.LAYOUT_L1
+    fst.down.dtype = ffi.I8
+    fst.placement_kind = 2
+    fargs = ffi.MoeFfnArgs()
+    fargs.t = 2
+    assert _call(lib.r9vx_moe_ffn_launch, fst, fargs) < 0
+    msg = lib.r9vx_last_error().decode()
+    for part in ("gate_up layout 2 (L1)", "down dtype 5", "placement_kind 2"):
+        assert part in msg, msg
+
+
+def test_route_ex_needs_its_own_status_word():
+    lib = ffi.load()
+    st = ffi.route_static(e=64, k=4, t_bucket=8)
+    args = ffi.MoeRouteArgs()
+    args.t = 2
+    assert lib.r9vx_moe_route_launch_ex(ctypes.byref(st), ctypes.byref(args), None, None) == -3
+    msg = lib.r9vx_last_error().decode()
+    assert "status word is NULL" in msg and "logits" in msg, msg
+    assert lib.r9vx_moe_route_launch_ex(ctypes.byref(st), ctypes.byref(args), ctypes.c_void_p(0x1002), None) < 0
+    assert "4-byte aligned" in lib.r9vx_last_error().decode()
+    assert lib.r9vx_status_read(None, None, None) == -3
 
 
 # Field declaration order of crates/r9v-kgen/src/abi/per_op.rs:794-968
@@ -126,6 +208,17 @@ def test_workspace_and_static_figures():
     lib = ffi.load()
     assert lib.r9vx_moe_ffn_static_flops(ctypes.byref(fst), 8192) == 515_396_075_520  # config 4
     assert ffi.ffn_workspace_bytes(fst) > 81920 * 2048 * 4
+    # one expert = IQ4_XS gate/up [1024 x 2048] + Q4_K down [2048 x 512]
+    assert lib.r9vx_moe_ffn_expert_bytes(ctypes.byref(fst)) == 1_703_936
+    # config 4 upper bound: all 512 experts + x + ids/weights + y
+    assert lib.r9vx_moe_ffn_static_bytes(ctypes.byref(fst), 8192) == (512 * 1_703_936 + 8192 * 2048 * 2
+                                                                       + 81920 * 8 + 8192 * 2048 * 4)
+    # config 3: t=5, K=10 -> at most 50 routed experts, + the shared one
+    c3 = ffi.ffn_static(t_bucket=5, e=512, k=10, dm=2048, dff=512, shared=1)
+    assert lib.r9vx_moe_ffn_static_bytes(ctypes.byref(c3), 5) == 51 * 1_703_936 + 5 * 2048 * 6 + 50 * 8
+    rst = ffi.route_static(e=512, k=10, t_bucket=5)
+    assert lib.r9vx_moe_route_static_flops(ctypes.byref(rst), 5) == 5 * (4 * 512 + 3 * 10)
+    assert lib.r9vx_moe_route_static_bytes(ctypes.byref(rst), 5) == 5 * 512 * 4 + 5 * 10 * 8
 
 
 def test_split_scheme_refusals_and_figures():
@@ -169,7 +262,7 @@ def test_iq3s_refusals_and_figures():
     msg = lib.r9vx_last_error().decode()
     assert "bf16 activations only" in msg and "inline scales" in msg, msg
     good = ffi.matmul_static(n=64, k=512, w_scheme=ffi.IQ3_S, in_dtype=ffi.BF16, out_dtype=ffi.F32)
-    assert ffi.matmul_static_bytes(good, 1) == 64 * 2 * 110 + 512 * 2 + 64 * 4
+    assert ffi.matmul_static_bytes(good, 1) == 64 * 2 * 112 + 512 * 2 + 64 * 4  # the 112-byte device blocks
     buf = ctypes.create_string_buffer(8192)
     base = ctypes.addressof(buf) + (-ctypes.addressof(buf) % 16)
     rc = lib.r9vx_repack_launch(ffi.IQ3_S, base, 1, 256, base + 1024, base + 2048, None)

@@ -10,6 +10,8 @@ touches a GPU: parsing, validation and hashing are host code.
 """
 from __future__ import annotations
 
+import ctypes
+
 import random
 import struct
 
@@ -417,20 +419,43 @@ def test_matmul_and_moe_ffn_statics_from_a_checkpoint():
         f.matmul_static("absent")
     s = f.moe_ffn_static("blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_exps.weight",
                          "blk.0.ffn_down_exps.weight", t_bucket=8, k=2)
-    assert (s.e_local, s.dm, s.dff, s.gate_up_scheme, s.down_scheme, s.k_topk) == (3, 512, 256, 23, 12, 2)
+    assert (s.e_local, s.dm, s.dff, s.gate_up.scheme, s.down.scheme, s.k_topk) == (3, 512, 256, 23, 12, 2)
     fused = f.moe_ffn_static("blk.0.ffn_gate_up_exps.weight", None, "blk.0.ffn_down_exps.weight", 8, 2)
     assert (fused.e_local, fused.dm, fused.dff) == (3, 512, 256)
     with pytest.raises(gguf.GgufError, match="must agree in dims and type"):
         f.moe_ffn_static("blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_bad.weight", "blk.0.ffn_down_exps.weight",
                          8, 2)
+    assert (st.w_dtype, st.w_layout) == (ffi.I4, ffi.LAYOUT_GGUF_WIRE)
+    assert (st8.w_dtype, st8.w_layout) == (ffi.I8, ffi.LAYOUT_SPLIT)
     st3 = f.matmul_static("blk.0.attn_o_iq3.weight")
     assert (st3.n, st3.k, st3.w_scheme) == (2, 512, ffi.IQ3_S)
+    assert (st3.w_dtype, st3.w_layout) == (ffi.I4, ffi.LAYOUT_IQ3S_112)
     s3 = f.moe_ffn_static("blk.0.ffn_gate_iq3_exps.weight", "blk.0.ffn_gate_iq3_exps.weight",
                           "blk.0.ffn_down_exps.weight", t_bucket=8, k=2)
-    assert (s3.gate_up_scheme, s3.down_scheme) == (ffi.IQ3_S, ffi.Q4_K)
+    assert (s3.gate_up.scheme, s3.down.scheme) == (ffi.IQ3_S, ffi.Q4_K)
+    assert (s3.gate_up.layout, s3.down.layout) == (ffi.LAYOUT_IQ3S_112, ffi.LAYOUT_GGUF_WIRE)
+    assert (s.gate_up.layout, s.down.layout, s.gate_up.dtype) == (ffi.LAYOUT_GGUF_WIRE, ffi.LAYOUT_GGUF_WIRE, ffi.I4)
     with pytest.raises(gguf.GgufError, match="down experts must be Q4_K"):
         f.moe_ffn_static("blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_exps.weight",
                          "blk.0.ffn_down_iq3_exps.weight", 8, 2)
     with pytest.raises(gguf.GgufError, match="must be \\{256, 512, 3\\}"):
         f.moe_ffn_static("blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_exps.weight", "blk.0.ffn_gate_exps.weight",
                          8, 2)
+
+
+def test_upload_sizes_iq3s_for_its_device_blocks():
+    """An IQ3_S upload writes 112-byte device blocks, so a destination sized
+    for the 110-byte file blocks is refused before anything is copied, and
+    Q8_0 / Q6_K are pointed at the split upload (no device is touched)."""
+    f = gguf.GgufFile.parse(_model_file())
+    b = _model_file()
+    lib = ffi.load()
+    info = f.tensor("blk.0.attn_o_iq3.weight")
+    ptr = ctypes.create_string_buffer(b, len(b))
+    rc = lib.r9vx_gguf_upload(f._h, ptr, len(b), b"blk.0.attn_o_iq3.weight", ctypes.c_void_p(0x1000),
+                              info.nbytes, None)
+    msg = lib.r9vx_last_error().decode()
+    assert rc == -1 and f"needs {info.nbytes // 110 * 112}" in msg and "112-byte IQ3_S device blocks" in msg, msg
+    assert gguf.device_bytes(info) == info.nbytes // 110 * 112
+    rc = lib.r9vx_gguf_upload(f._h, ptr, len(b), b"blk.0.attn_v.weight", ctypes.c_void_p(0x1000), 1 << 20, None)
+    assert rc == -2 and "r9vx_gguf_upload_split" in lib.r9vx_last_error().decode()

@@ -194,7 +194,7 @@ def test_gguf_loads_repack_iq3s_weights_and_experts():
                                             "blk.0.ffn_down_exps.weight", t_bucket=16, k=2)
     stacked = np.concatenate([gate.reshape(e, dff, -1), up.reshape(e, dff, -1)], axis=1).reshape(-1)
     assert np.array_equal(host(w_gu), device_blocks_np(stacked))
-    assert (fst.gate_up_scheme, fst.down_scheme) == (IQ3_S, ffi.Q4_K)
+    assert (fst.gate_up.scheme, fst.down.scheme) == (IQ3_S, ffi.Q4_K)
     bad = wq.reshape(-1, 110).copy()
     bad[5, 0:2] = np.frombuffer(np.uint16(0x7C00).tobytes(), np.uint8)
     b2 = build([], [("w", (k, n), 21, bad.tobytes())])

@@ -317,3 +317,33 @@ def test_moe_ffn_prefill_permutation_invariance_full_size():
     yp, _, _ = ffi.moe_ffn(x[perm].contiguous(), ids_d[perm].contiguous(), w_d[perm].contiguous(), gu, dn, e,
                            dff, workspace=ws)
     assert torch.equal(yp, y[perm])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("t", [5, 300])
+def test_route_status_words_are_per_launch(t):
+    """Two routings on two streams, each with its own status word: the one
+    with a NaN row reports NONFINITE and writes nothing, the other reports 0
+    and writes its ids -- neither sees the other's status."""
+    bad = synth.normal_f32(911, (t, 64))
+    bad[t // 3, 7] = np.nan
+    good = synth.normal_f32(912, (t, 64))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    w1 = torch.full((1,), 0x55, dtype=torch.int32, device="cuda")
+    w2 = torch.full((1,), 0x55, dtype=torch.int32, device="cuda")
+    ids1 = torch.full((t, 4), 77, dtype=torch.int32, device="cuda")
+    wt1 = torch.full((t, 4), -1.0, dtype=torch.float32, device="cuda")
+    ids2 = torch.full((t, 4), 77, dtype=torch.int32, device="cuda")
+    wt2 = torch.full((t, 4), -1.0, dtype=torch.float32, device="cuda")
+    lb, lg = dev(bad), dev(good)
+    torch.cuda.synchronize()
+    for _ in range(3):  # interleaved launches on both streams
+        ffi.moe_route(lb, 4, ids=ids1, weights=wt1, stream=s1, status=w1)
+        ffi.moe_route(lg, 4, ids=ids2, weights=wt2, stream=s2, status=w2)
+    torch.cuda.synchronize()
+    assert ffi.status_read(w1) == ffi.STATUS_NONFINITE
+    assert ffi.status_read(w2) == 0
+    assert (host(ids1) == 77).all() and (host(wt1) == -1.0).all()
+    rid, rw = O.moe_route(good, 4)
+    assert np.array_equal(host(ids2).view(np.uint32), rid.astype(np.uint32))
+    assert np.array_equal(host(wt2).view(np.uint32), rw.view(np.uint32))

@@ -39,7 +39,7 @@ def run(x, w, k, bias=None, scoring=0, renormalize=True, scale=1.0):
     torch.cuda.synchronize()
     t, e = x.shape[0], w.shape[0]
     logits = host(ws[:t * e * 4].view(torch.float32)).reshape(t, e)
-    return host(ids).view(np.uint32), host(wts), logits, ffi.moe_route_status()
+    return host(ids).view(np.uint32), host(wts), logits, ffi.moe_route_hidden_status(ws, e, k, max(t, 1))
 
 
 @pytest.mark.parametrize("t,e,dm,k", [(1, 512, 2048, 10), (5, 512, 2048, 10), (8, 512, 4096, 8),
@@ -90,12 +90,12 @@ def test_route_hidden_back_to_back_and_refusal():
     ids = torch.full((t, k), 7, dtype=torch.int32, device="cuda")
     wts = torch.full((t, k), 0.5, dtype=torch.float32, device="cuda")
     ffi.moe_route_hidden(bf16_dev(xb), ffi.router_repack(dev(w)), k, ids=ids, weights=wts, workspace=ws)
-    assert ffi.moe_route_status() == ffi.STATUS_NONFINITE
+    assert ffi.moe_route_hidden_status(ws, e, k, t) == ffi.STATUS_NONFINITE
     assert np.all(host(ids) == 7) and np.all(host(wts) == 0.5)
     x, w = case(t, e, dm, 9)
     ids, wts, _ = ffi.moe_route_hidden(bf16_dev(x), ffi.router_repack(dev(w)), k, workspace=ws)
     torch.cuda.synchronize()
-    assert ffi.moe_route_status() == 0
+    assert ffi.moe_route_hidden_status(ws, e, k, t) == 0
     rid, _ = O.moe_route(O.router_logits(x, w), k)
     assert np.array_equal(host(ids).view(np.uint32), rid.astype(np.uint32))
 
