@@ -27,6 +27,16 @@ uint32_t r9vx_probe_stream_blocks(uint64_t bytes);
  * per thread to `sink`.  FLOPs = blocks * 4 waves * iters * 16 * 32768. */
 int r9vx_probe_mfma_launch(uint32_t blocks, uint32_t iters, float *sink, r9vx_stream_t stream);
 
+/* Relaunches one stage of the grouped (t > 8) moe_ffn path on a workspace
+ * that a completed r9vx_moe_ffn_launch with the same static and args left
+ * behind, so a stage's kernel can be timed on its own: stage 1 = the gate/up
+ * GEMM (writes the h rows), 2 = the down GEMM (writes the expert output
+ * rows), 3 = the weighted combine (writes y).  Each stage reads only what the
+ * full launch wrote, so repeating it reproduces the same outputs.  Refused
+ * for t <= 8 (the decode path) and for unknown stages. */
+int r9vx_probe_moe_stage_launch(const r9vx_moe_ffn_static *st, const r9vx_moe_ffn_args *args, uint32_t stage,
+                                r9vx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -641,6 +641,44 @@ int rxo_moe_ffn(int x_dtype, const void *x, uint32_t t, uint32_t dm, uint32_t df
     return RXO_OK;
 }
 
+/* One expert's FFN over the token rows `tokens` (the per-expert body of
+ * rxo_moe_ffn: gather, gate/up, act_mul, down; moe_ffn.rs:527-639), rows
+ * split over `threads` OpenMP threads (each row is independent, so the
+ * result does not depend on the split).  out: [n_tok, dm].  The CPU
+ * baseline of the grouped MoE GEMM times this on a subset of experts. */
+int rxo_moe_expert_mt(int x_dtype, const void *x, const uint32_t *tokens, uint32_t n_tok, uint32_t dm,
+                      uint32_t dff, int scheme_gu, const uint8_t *gu, int scheme_dn, const uint8_t *dn, float *out,
+                      int threads) {
+    if (dm == 0 || dff == 0 || dm % 256 || dff % 256) return RXO_ERR_SHAPE;
+    if (threads < 1) threads = 1;
+#ifdef _OPENMP
+#pragma omp parallel num_threads(threads)
+#endif
+    {
+#ifdef _OPENMP
+        int nt = omp_get_num_threads(), tid = omp_get_thread_num();
+#else
+        int nt = 1, tid = 0;
+#endif
+        uint32_t chunk = (n_tok + nt - 1) / nt;
+        uint32_t r0 = tid * chunk, r1 = r0 + chunk > n_tok ? n_tok : r0 + chunk;
+        if (r0 < r1) {
+            uint32_t rows = r1 - r0;
+            float *xr = (float *)malloc(sizeof(float) * (size_t)rows * dm);
+            float *wrow = (float *)malloc(sizeof(float) * (dm > dff ? dm : dff));
+            float *h = (float *)malloc(sizeof(float) * (size_t)rows * dff);
+            for (uint32_t r = 0; r < rows; ++r)
+                for (uint32_t kk = 0; kk < dm; ++kk)
+                    xr[(uint64_t)r * dm + kk] = read_x(x_dtype, x, (uint64_t)tokens[r0 + r] * dm + kk);
+            expert_rows(xr, rows, dm, dff, scheme_gu, gu, scheme_dn, dn, 0, out + (uint64_t)r0 * dm, wrow, h);
+            free(xr);
+            free(wrow);
+            free(h);
+        }
+    }
+    return RXO_OK;
+}
+
 /* Literal T0 form: gate/up over every expert's rows, then slice the
  * expert's columns (moe_ffn.rs:575-612).  Tiny E only. */
 int rxo_moe_ffn_full(int x_dtype, const void *x, uint32_t t, uint32_t dm, uint32_t dff,

@@ -127,6 +127,9 @@ int rxo_expert_ffn(int x_dtype, const void *x, uint32_t rows, uint32_t dm, uint3
 
 /* Multi-threaded (OpenMP over output rows) Branch-D matmul for the
  * all-cores CPU baseline; bit-identical to rxo_matmul. */
+int rxo_moe_expert_mt(int x_dtype, const void *x, const uint32_t *tokens, uint32_t n_tok, uint32_t dm,
+                      uint32_t dff, int scheme_gu, const uint8_t *gu, int scheme_dn, const uint8_t *dn, float *out,
+                      int threads);
 int rxo_matmul_mt(int scheme, const uint8_t *w, uint32_t n, uint32_t k,
                   int x_dtype, const void *x, uint32_t m, int y_dtype, void *y,
                   int threads);

@@ -717,6 +717,71 @@ __global__ __launch_bounds__(256) void r9vx_moe_combine_kernel(MoeCombineArgs a)
     *reinterpret_cast<r9vx_f32x4 *>(a.y + (uint64_t)t * a.dm + d0) = acc;
 }
 
+/* The same combine over the grouped path's fp16 rows: row value = o16 *
+ * oscale[row, d / 64] (exact: the scale is a power of two), summed in the
+ * same order. */
+__global__ __launch_bounds__(256) void r9vx_moe_combine16_kernel(MoeCombineArgs a) {
+    __shared__ uint32_t spos[kMoeMaxK], opos[kMoeMaxK];
+    __shared__ float sw[kMoeMaxK], ow[kMoeMaxK];
+    const uint32_t *status = reinterpret_cast<const uint32_t *>(a.ws + a.L.status);
+    if (status[0] != 0u) return;
+    const uint32_t t = blockIdx.y;
+    const uint32_t kk = a.k;
+    const uint32_t *inv = reinterpret_cast<const uint32_t *>(a.ws + a.L.inv);
+    if (threadIdx.x < kk) {
+        spos[threadIdx.x] = inv[(uint64_t)t * kk + threadIdx.x];
+        sw[threadIdx.x] = a.weights[(uint64_t)t * kk + threadIdx.x];
+    }
+    __syncthreads();
+    if (threadIdx.x < kk) {
+        const uint32_t p = spos[threadIdx.x];
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < kk; ++j) rank += spos[j] < p ? 1u : 0u;
+        opos[rank] = p;
+        ow[rank] = sw[threadIdx.x];
+    }
+    __syncthreads();
+    const uint32_t d0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (d0 >= a.dm) return;
+    const uint64_t nrows = (uint64_t)a.p + (uint64_t)a.shared * a.t;
+    const _Float16 *o16 = reinterpret_cast<const _Float16 *>(a.ws + a.L.o);
+    const float *oscale = reinterpret_cast<const float *>(a.ws + a.L.o + r9vx_moe_oscale_offset(nrows, a.dm));
+    const uint32_t nblk = a.dm / 64, blk = d0 / 64;
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    r9vx_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t jb = 0; jb < kk; jb += 8) {
+        h4 rows[8];
+        float scs[8];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j)
+            if (jb + j < kk) {
+                const uint64_t row = opos[jb + j];
+                rows[j] = *reinterpret_cast<const h4 *>(o16 + row * a.dm + d0);
+                scs[j] = oscale[row * nblk + blk];
+            }
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            if (jb + j < kk) {
+                const float w = ow[jb + j], sc = scs[j];
+                acc.x = acc.x + w * ((float)rows[j].x * sc);
+                acc.y = acc.y + w * ((float)rows[j].y * sc);
+                acc.z = acc.z + w * ((float)rows[j].z * sc);
+                acc.w = acc.w + w * ((float)rows[j].w * sc);
+            }
+        }
+    }
+    for (uint32_t s = 0; s < a.shared; ++s) {
+        const uint64_t row = (uint64_t)a.p + s * a.t + t;
+        const h4 v = *reinterpret_cast<const h4 *>(o16 + row * a.dm + d0);
+        const float sc = oscale[row * nblk + blk];
+        acc.x = acc.x + (float)v.x * sc;
+        acc.y = acc.y + (float)v.y * sc;
+        acc.z = acc.z + (float)v.z * sc;
+        acc.w = acc.w + (float)v.w * sc;
+    }
+    *reinterpret_cast<r9vx_f32x4 *>(a.y + (uint64_t)t * a.dm + d0) = acc;
+}
+
 /* ---------------------------------------------------------------- host side */
 
 static uint32_t lpr_for(uint32_t k, uint32_t &nseg) {
@@ -804,6 +869,9 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
 int r9vx_moe_combine_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s) {
     MoeCombineArgs c{p.weights, p.y, p.ws, L, p.t, p.k, p.dm, p.shared, p.t * p.k};
     dim3 grid((p.dm / 4 + 255) / 256, p.t);
-    hipLaunchKernelGGL(r9vx_moe_combine_kernel, grid, dim3(256), 0, s, c);
+    if (p.t <= 8)
+        hipLaunchKernelGGL(r9vx_moe_combine_kernel, grid, dim3(256), 0, s, c);
+    else /* the grouped path's fp16 rows */
+        hipLaunchKernelGGL(r9vx_moe_combine16_kernel, grid, dim3(256), 0, s, c);
     return (int)hipGetLastError();
 }

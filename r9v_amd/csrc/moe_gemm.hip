@@ -245,7 +245,7 @@ __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t n
 template <int GU>
 __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     __shared__ __attribute__((aligned(16))) M3Lds sm;
-    __shared__ __attribute__((aligned(16))) float lutf[512];
+    __shared__ uint32_t lut[256];
     __shared__ float rowsc[kMoeTileM3];
     const uint32_t *status = ws_u32(a, a.L.status);
     uint32_t tix, nt;
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     const uint32_t j0 = nt * 128;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < kMoeTileM3) rowsc[tid] = tid < rows ? a.xscale[row_token(a, expert, pos0 + tid)] : 0.f;
-    if constexpr (GU == R9VX_SCHEME_IQ4_XS) init_iq4_lut_f32(reinterpret_cast<r9vx_f32x4 *>(lutf), tid);
+    if constexpr (GU == R9VX_SCHEME_IQ4_XS) m3_init_iq4_lut(lut, tid, 512);
     __syncthreads();
 
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
@@ -269,11 +269,11 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     }
     const uint32_t c = tid >> 1;
     const uint32_t wr = c < 128 ? j0 + c : a.dff + j0 + (c - 128);
-    const M3WRow w{a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes, wr * (uint32_t)a.gu_row_bytes};
+    const M3WRow w{m3_uniform(a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes), wr * (uint32_t)a.gu_row_bytes};
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
-    m3_run<GU>(nr, sm, a.x16, aoff, w, a.dm / kTileK, tid, wv, lutf, 128 * rh, 32 * cq, 128 + 32 * cq, acc);
+    m3_run<GU>(nr, sm, a.x16, aoff, w, a.dm / kTileK, tid, wv, lut, 128 * rh, 32 * cq, 128 + 32 * cq, acc);
 
     float *h = reinterpret_cast<float *>(a.ws + a.L.h);
     const uint32_t col = j0 + 32 * cq + (lane & 31);
@@ -295,7 +295,7 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
 template <int DN>
 __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     __shared__ __attribute__((aligned(16))) M3Lds sm;
-    __shared__ __attribute__((aligned(16))) float lutf[512];
+    __shared__ uint32_t lut[256];
     __shared__ float rowsc[kMoeTileM3]; /* 2^e that undoes each h row's fp16 scale */
     const uint32_t *status = ws_u32(a, a.L.status);
     uint32_t tix, nt;
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     if (tid < kMoeTileM3)
         rowsc[tid] = tid < rows ? ldexpf(1.0f, row_shift(__builtin_bit_cast(float, ws_u32(a, a.L.hmax)[pos0 + tid])))
                                 : 0.f;
-    if constexpr (DN == R9VX_SCHEME_IQ4_XS) init_iq4_lut_f32(reinterpret_cast<r9vx_f32x4 *>(lutf), tid);
+    if constexpr (DN == R9VX_SCHEME_IQ4_XS) m3_init_iq4_lut(lut, tid, 512);
     __syncthreads();
 
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
@@ -318,31 +318,46 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
         const uint32_t r = dma_row(wv, i, lane);
         aoff[i] = ((pos0 + (r < rows ? r : 0)) * a.dff + 8 * dma_group(r, lane)) * 2u;
     }
-    const M3WRow w{a.w_dn + ((uint64_t)expert * a.dm + n0) * a.dn_row_bytes, (tid >> 1) * (uint32_t)a.dn_row_bytes};
+    const M3WRow w{m3_uniform(a.w_dn + ((uint64_t)expert * a.dm + n0) * a.dn_row_bytes),
+                   (tid >> 1) * (uint32_t)a.dn_row_bytes};
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
-    m3_run<DN>(nr, sm, a.h16, aoff, w, a.dff / kTileK, tid, wv, lutf, 128 * rh, 64 * cq, 64 * cq + 32, acc);
+    m3_run<DN>(nr, sm, a.h16, aoff, w, a.dff / kTileK, tid, wv, lut, 128 * rh, 64 * cq, 64 * cq + 32, acc);
 
-    float *o = reinterpret_cast<float *>(a.ws + a.L.o);
-    const uint32_t c0 = n0 + 64 * cq + (lane & 31);
+    /* o rows as fp16 scaled by a power of two per (row, 64-column block):
+     * the block is this wave's two column tiles, so its max is a reduction
+     * over the 32 lanes holding the row; the scale puts the block max in
+     * [2^14, 2^15) and is stored beside the rows for the combine. */
+    const uint64_t nrows_all = (uint64_t)a.p + (uint64_t)a.shared * a.t;
+    _Float16 *o16 = reinterpret_cast<_Float16 *>(a.ws + a.L.o);
+    float *oscale = reinterpret_cast<float *>(a.ws + a.L.o + r9vx_moe_oscale_offset(nrows_all, a.dm));
+    const uint32_t c0 = n0 + 64 * cq + (lane & 31), blk = (n0 + 64 * cq) / 64, nblk = a.dm / 64;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         if ((uint32_t)t >= nr) break;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const uint32_t rl = 128 * rh + 32 * t + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (rl >= rows) continue;
-            const float sc = rowsc[rl];
+            const float sc = rl < rows ? rowsc[rl] : 0.f;
+            const float v0 = acc[t][0][r] * sc, v1 = acc[t][1][r] * sc;
+            float m = fmaxf(fabsf(v0), fabsf(v1));
 #pragma unroll
-            for (int j = 0; j < 2; ++j) o[(uint64_t)(pos0 + rl) * a.dm + c0 + 32 * j] = acc[t][j][r] * sc;
+            for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+            int e = 0;
+            (void)frexpf(m, &e); /* m = f * 2^e, f in [0.5, 1): m * 2^(15 - e) < 2^15 */
+            if (rl >= rows) continue;
+            const uint64_t row = pos0 + rl;
+            o16[row * a.dm + c0] = (_Float16)ldexpf(v0, 15 - e);
+            o16[row * a.dm + c0 + 32] = (_Float16)ldexpf(v1, 15 - e);
+            if ((lane & 31) == 0) oscale[row * nblk + blk] = ldexpf(1.0f, e - 15);
         }
     }
 }
 
 }  // namespace
 
-int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s) {
+static GroupedArgs grouped_args(const r9vx_moe_problem &p, const MoeLayout &L) {
     GroupedArgs a{};
     a.x16 = reinterpret_cast<const _Float16 *>(p.ws + L.x16);
     a.h16 = reinterpret_cast<_Float16 *>(p.ws + L.h16);
@@ -362,31 +377,51 @@ int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStr
     a.dff = p.dff;
     a.p = p.t * p.k;
     a.shared = p.shared;
-    int rc = r9vx_launch_x_to_f16(p.x, p.t, p.dm, reinterpret_cast<_Float16 *>(p.ws + L.x16),
-                                  reinterpret_cast<float *>(p.ws + L.xscale), p.scheme_gu, s);
-    if (rc) return rc;
-    hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(1024), 0, s, a);
-    /* upper bound on row tiles: ceil(P/128) + one partial tile per work item */
-    const uint32_t max_tiles = (a.p + kBM - 1) / kBM + (a.p < p.e ? a.p : p.e) + (p.shared ? p.shared * ((p.t + kBM - 1) / kBM) : 0);
-    const uint32_t tiles8 = (max_tiles + 7) / 8 * 8; /* xcd_tile's grid */
+    return a;
+}
+
+
+int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s) {
+    return r9vx_moe_grouped_part(p, L, 0, s);
+}
+
+/* part 0: the whole grouped stage; 1: the gate/up GEMM only; 2: the down
+ * GEMM only (1 and 2 on a workspace the whole stage has filled). */
+int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_t part, hipStream_t s) {
+    GroupedArgs a = grouped_args(p, L);
+    if (part == 0) {
+        int rc = r9vx_launch_x_to_f16(p.x, p.t, p.dm, reinterpret_cast<_Float16 *>(p.ws + L.x16),
+                                      reinterpret_cast<float *>(p.ws + L.xscale), p.scheme_gu, s);
+        if (rc) return rc;
+        hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(1024), 0, s, a);
+    }
+    /* upper bounds on row tiles: ceil(P/TM) + one partial tile per work item */
+    const uint32_t max_tiles = (a.p + kBM - 1) / kBM + (a.p < p.e ? a.p : p.e) +
+                               (p.shared ? p.shared * ((p.t + kBM - 1) / kBM) : 0);
     const uint32_t max_tiles3 = (a.p + kMoeTileM3 - 1) / kMoeTileM3 + (a.p < p.e ? a.p : p.e) +
                                 (p.shared ? p.shared * ((p.t + kMoeTileM3 - 1) / kMoeTileM3) : 0);
-    const uint32_t tiles3_8 = (max_tiles3 + 7) / 8 * 8;
-    dim3 ggu(tiles8 * (p.dff / 128));
-    dim3 ggu3(tiles3_8 * (p.dff / 128)), gdn3(tiles3_8 * (p.dm / 256));
-    if (p.scheme_gu == R9VX_SCHEME_IQ3_S)
-        hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_IQ3_S>, ggu, dim3(256), 0, s, a);
-    else if (p.scheme_gu == R9VX_SCHEME_IQ4_XS)
-        hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_IQ4_XS>, ggu3, dim3(512), 0, s, a);
-    else
-        hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q4_K>, ggu3, dim3(512), 0, s, a);
+    const uint32_t tiles8 = (max_tiles + 7) / 8 * 8, tiles3_8 = (max_tiles3 + 7) / 8 * 8; /* xcd_tile's grids */
+    const dim3 ggu(tiles8 * (p.dff / 128)), ggu3(tiles3_8 * (p.dff / 128)), gdn3(tiles3_8 * (p.dm / 256));
+    if (part == 0 || part == 1) {
+        if (p.scheme_gu == R9VX_SCHEME_IQ3_S)
+            hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_IQ3_S>, ggu, dim3(256), 0, s, a);
+        else if (p.scheme_gu == R9VX_SCHEME_IQ4_XS)
+            hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_IQ4_XS>, ggu3, dim3(512), 0, s, a);
+        else
+            hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q4_K>, ggu3, dim3(512), 0, s, a);
+    }
     const uint32_t nrows = a.p + p.shared * p.t;
-    if (p.scheme_dn == R9VX_SCHEME_Q4_K) {
-        hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3((nrows + 3) / 4), dim3(256), 0, s, a, nrows);
-        hipLaunchKernelGGL(moe_dn_m3_kernel<R9VX_SCHEME_Q4_K>, gdn3, dim3(512), 0, s, a);
-    } else {
-        hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3((nrows + 3) / 4), dim3(256), 0, s, a, nrows);
-        hipLaunchKernelGGL(moe_dn_m3_kernel<R9VX_SCHEME_IQ4_XS>, gdn3, dim3(512), 0, s, a);
+    if (part == 0) {
+        if (p.scheme_dn == R9VX_SCHEME_Q4_K)
+            hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3((nrows + 3) / 4), dim3(256), 0, s, a, nrows);
+        else
+            hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3((nrows + 3) / 4), dim3(256), 0, s, a, nrows);
+    }
+    if (part == 0 || part == 2) {
+        if (p.scheme_dn == R9VX_SCHEME_Q4_K)
+            hipLaunchKernelGGL(moe_dn_m3_kernel<R9VX_SCHEME_Q4_K>, gdn3, dim3(512), 0, s, a);
+        else
+            hipLaunchKernelGGL(moe_dn_m3_kernel<R9VX_SCHEME_IQ4_XS>, gdn3, dim3(512), 0, s, a);
     }
     return (int)hipGetLastError();
 }

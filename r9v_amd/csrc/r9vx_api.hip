@@ -15,6 +15,7 @@
 
 #include "r9vx_internal.h"
 #include "r9vx_moe.h"
+#include "r9vx_probe.h"
 
 namespace {
 
@@ -619,6 +620,26 @@ int r9vx_moe_ffn_status(const r9vx_moe_ffn_static *st, const uint8_t *ws, uint32
     int rc = (int)hipMemcpyAsync(status, ws + L.status, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
     if (!rc) rc = (int)hipStreamSynchronize(s);
     return hip_status("moe_ffn_status", rc);
+}
+
+int r9vx_probe_moe_stage_launch(const r9vx_moe_ffn_static *st, const r9vx_moe_ffn_args *a, uint32_t stage,
+                                r9vx_stream_t stream) {
+    Problems pr;
+    if (!st || !a) {
+        pr.add(R9VX_ERR_NULL, "static and args must be non-NULL");
+        return pr.finish("probe_moe_stage");
+    }
+    if (stage < 1 || stage > 3) pr.add(R9VX_ERR_INVALID, "stage %u: 1 (gate/up), 2 (down) or 3 (combine)", stage);
+    if (a->t <= 8) pr.add(R9VX_ERR_UNSUPPORTED, "t=%u runs the decode path, which has no separate GEMM stages", a->t);
+    if (!a->x || !a->weights || !a->w_gate_up || !a->w_down || !a->y)
+        pr.add(R9VX_ERR_NULL, "x, weights, w_gate_up, w_down and y are required");
+    int rc = ffn_common("probe_moe_stage", st, a->expert_ids, a->t, a->sort_workspace, pr);
+    if (rc) return rc;
+    r9vx_moe_problem p = ffn_problem(st, a);
+    MoeLayout L = r9vx_moe_layout(p.t_bucket, p.e, p.k, p.dm, p.dff, p.shared);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    return hip_status("probe_moe_stage", stage == 3 ? r9vx_moe_combine_stage(p, L, s)
+                                                    : r9vx_moe_grouped_part(p, L, stage, s));
 }
 
 int r9vx_moe_sort_launch(const r9vx_moe_ffn_static *st, const uint32_t *ids, uint32_t t, uint8_t *ws,

@@ -44,6 +44,10 @@ struct M3Lds {
     uint8_t b[kM3Stage];
 };
 
+__device__ __forceinline__ uint32_t pack_h2h(_Float16 a, _Float16 b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
 /* Byte address of an LDS object, for M0. */
 __device__ __forceinline__ uint32_t m3_lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
@@ -55,6 +59,15 @@ struct M3WRow {
     const uint8_t *base; /* uniform */
     uint32_t off;        /* this thread's row */
 };
+
+/* A pointer the caller knows to be wave-uniform, moved to scalar registers
+ * (the loads take it as their SGPR base whatever the compiler's divergence
+ * analysis concludes). */
+__device__ __forceinline__ const uint8_t *m3_uniform(const uint8_t *p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const uint8_t *>((uintptr_t)(((uint64_t)hi << 32) | lo));
+}
 
 /* Payload / header loads with the destination tied in and out. */
 template <int SCHEME>
@@ -96,69 +109,125 @@ __device__ __forceinline__ void m3_write_b(uint8_t *b, uint32_t c, uint32_t hh, 
     for (int s = 0; s < 4; ++s) *reinterpret_cast<r9vx_u32x4 *>(row + (((4u * hh + s) ^ sw) << 4)) = v[s];
 }
 
-/* Scheduling groups of MFMA pair I of a step (m3_compute): the fragment
- * reads that run one pair ahead plus a share of the codebook reads, the
- * pair, a share of the decode VALU work. */
-template <int NR, int I, int KV, int KL>
-__device__ __forceinline__ void m3_sched() {
-    if constexpr (I < 4 * NR) {
-        constexpr int kReads = (I + 1 < 4 * NR ? ((I + 1) % NR == 0 ? 3 : 1) : 0) + KL;
-        __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0); /* DS read */
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);      /* MFMA */
-        __builtin_amdgcn_sched_group_barrier(0x002, KV, 0);     /* VALU */
-        m3_sched<NR, I + 1, KV, KL>();
+/* IQ4_XS codebook pairs as fp16: entry b = {kv[b & 15], kv[b >> 4]} (1 KiB,
+ * exact: the values are integers below 128). */
+__device__ __forceinline__ void m3_init_iq4_lut(uint32_t *lut, uint32_t tid, uint32_t nthreads) {
+    for (uint32_t b = tid; b < 256; b += nthreads) {
+        const _Float16 lo = (_Float16)(float)r9vx_iq4_kvalue(b & 15), hi = (_Float16)(float)r9vx_iq4_kvalue(b >> 4);
+        lut[b] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
     }
+}
+
+/* Decode unit u (0..7) of a step: payload bytes 2u, 2u + 1 (bytes 4q + 2m,
+ * 4q + 2m + 1 of dword q = u / 2, m = u % 2), whose low nibbles are elements
+ * 2m, 2m + 1 and high nibbles elements 4 + 2m, 4 + 2m + 1 of group q.  Each
+ * weight is the exact f32 formula rounded once to fp16
+ * (crates/r9v-format/src/ggml.rs:1131-1150, iq.rs:578-598).  Returns the two
+ * packed dwords {low pair, high pair}.  IQ4_XS: kv0 / kv1 are the bytes'
+ * codebook pairs {kv[low], kv[high]}. */
+typedef _Float16 m3_h2 __attribute__((ext_vector_type(2)));
+template <int SCHEME>
+__device__ __forceinline__ void m3_dec_unit(uint32_t dw, int m, const BScale &sc, uint32_t kv0, uint32_t kv1,
+                                            uint32_t &lo2, uint32_t &hi2) {
+    m3_h2 l, h;
+    if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
+        uint32_t l4 = dw & 0x0F0F0F0Fu, h4 = (dw >> 4) & 0x0F0F0F0Fu;
+        /* hide the masks' known-zero bits, so that each nibble becomes one
+         * byte-select conversion (v_cvt_f32_ubyteN) */
+        asm volatile("" : "+v"(l4), "+v"(h4));
+        l.x = (_Float16)fmaf(sc.dl0, (float)((l4 >> (16 * m)) & 0xFFu), sc.nml0);
+        l.y = (_Float16)fmaf(sc.dl0, (float)((l4 >> (16 * m + 8)) & 0xFFu), sc.nml0);
+        h.x = (_Float16)fmaf(sc.dl1, (float)((h4 >> (16 * m)) & 0xFFu), sc.nml1);
+        h.y = (_Float16)fmaf(sc.dl1, (float)((h4 >> (16 * m + 8)) & 0xFFu), sc.nml1);
+    } else {
+        /* dl * kv is exact in f32 (dl = d * s has 17 significant bits, kv
+         * 8), so v_fma_mix with the fp16 codebook value as its operand and
+         * 0 as the addend rounds exactly that product to fp16 -- the value
+         * of the f32 multiply followed by one fp16 rounding.  mixlo / mixhi
+         * write the low / high half of the destination (op_sel picks the
+         * codebook half, op_sel_hi marks it as fp16). */
+        uint32_t a = 0, b = 0;
+        asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "+v"(a) : "v"(sc.dl0), "v"(kv0));
+        asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "+v"(a) : "v"(sc.dl0), "v"(kv1));
+        asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(b) : "v"(sc.dl0), "v"(kv0));
+        asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(b) : "v"(sc.dl0), "v"(kv1));
+        lo2 = a;
+        hi2 = b;
+        asm volatile("" : "+v"(lo2), "+v"(hi2));
+        return;
+    }
+    lo2 = __builtin_bit_cast(uint32_t, l);
+    hi2 = __builtin_bit_cast(uint32_t, h);
+    /* keep the computation here: its only use is at the end of the step,
+     * where the compiler's IR passes would otherwise sink it */
+    asm volatile("" : "+v"(lo2), "+v"(hi2));
 }
 
 /*
  * One K step's compute: the MFMAs of this step (A rows arow0 + 32t for t <
  * NR, B rows bc0 / bc1; the bases are multiples of 32, so a fragment row's
  * swizzle is that of lane % 32) and the decode of the next step's B into
- * `out`.  Fragment reads run one MFMA pair ahead (B of a slice with the last
- * A read of the previous one); the decode's VALU work and codebook reads are
- * spread between the MFMAs by the scheduling groups at the end.
+ * `out`.  Scheduled by hand, each stage fenced so the compiler keeps it:
+ * the step's 16 codebook reads (IQ4_XS) and first fragments, then per MFMA
+ * pair the fragment reads of the next pair (B of a slice with the last A of
+ * the previous one), the pair, and the decode of one or more payload bytes.
  */
 template <int SCHEME, int KS, int NR>
 __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bsm, uint32_t lane, uint32_t arow0,
                                            uint32_t bc0, uint32_t bc1, r9vx_f32x16 (&acc)[4][2],
                                            const r9vx_u32x4 &pay, const r9vx_u32x4 &hd, uint32_t hh,
-                                           const float *lutf, r9vx_u32x4 (&out)[4]) {
+                                           const uint32_t *lut, r9vx_u32x4 (&out)[4]) {
+    constexpr bool kIq4 = SCHEME == R9VX_SCHEME_IQ4_XS;
+    constexpr int P = 4 * NR; /* MFMA pairs */
     const uint32_t h = lane >> 5, r32 = lane & 31, sw = m2_swz(r32);
     const uint8_t *arow = ast + (arow0 + r32) * 128u;
     const uint8_t *brow0 = bsm + (bc0 + r32) * 128u, *brow1 = bsm + (bc1 + r32) * 128u;
     auto goff = [&](int s) { return ((4u * h + (uint32_t)s) ^ sw) << 4; };
-    if constexpr (NR > 0) {
-        half8 a[2], b[2][2];
+    const uint32_t dws[4] = {pay.x, pay.y, pay.z, pay.w};
+    uint32_t kv[16];
+    if constexpr (kIq4) {
+#pragma unroll
+        for (int b = 0; b < 16; ++b) kv[b] = lut[(dws[b >> 2] >> (8 * (b & 3))) & 0xFFu];
+    } else {
+#pragma unroll
+        for (int b = 0; b < 16; ++b) kv[b] = 0u;
+    }
+    const BScale sc = bscale<SCHEME, KS>(hd, hh);
+    uint32_t o[4][4]; /* out[q] words */
+    half8 a[2], b[2][2];
+    if constexpr (P > 0) {
         b[0][0] = *reinterpret_cast<const half8 *>(brow0 + goff(0));
         b[0][1] = *reinterpret_cast<const half8 *>(brow1 + goff(0));
         a[0] = *reinterpret_cast<const half8 *>(arow + goff(0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < 4 * NR; ++i) {
-            const int s = i / NR, t = i % NR;
-            if (i + 1 < 4 * NR) {
-                const int s1 = (i + 1) / NR, t1 = (i + 1) % NR;
-                if (t1 == 0) {
-                    b[s1 & 1][0] = *reinterpret_cast<const half8 *>(brow0 + goff(s1));
-                    b[s1 & 1][1] = *reinterpret_cast<const half8 *>(brow1 + goff(s1));
-                }
-                a[(i + 1) & 1] = *reinterpret_cast<const half8 *>(arow + 4096u * t1 + goff(s1));
+    for (int i = 0; i < P; ++i) {
+        const int s = i / NR, t = i % NR;
+        if (i + 1 < P) { /* the next pair's fragments, a whole pair ahead of their use */
+            const int s1 = (i + 1) / NR, t1 = (i + 1) % NR;
+            if (t1 == 0) {
+                b[s1 & 1][0] = *reinterpret_cast<const half8 *>(brow0 + goff(s1));
+                b[s1 & 1][1] = *reinterpret_cast<const half8 *>(brow1 + goff(s1));
             }
-            acc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i & 1], b[s & 1][0], acc[t][0], 0, 0, 0);
-            acc[t][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i & 1], b[s & 1][1], acc[t][1], 0, 0, 0);
+            a[(i + 1) & 1] = *reinterpret_cast<const half8 *>(arow + 4096u * t1 + goff(s1));
         }
-    }
-    const BScale sc = bscale<SCHEME, KS>(hd, hh);
+        __builtin_amdgcn_sched_barrier(0);
+        acc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i & 1], b[s & 1][0], acc[t][0], 0, 0, 0);
+        acc[t][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i & 1], b[s & 1][1], acc[t][1], 0, 0, 0);
+        /* decode units [8 i / P, 8 (i + 1) / P) */
 #pragma unroll
-    for (int s = 0; s < 4; ++s) out[s] = __builtin_bit_cast(r9vx_u32x4, decode_bfrag<SCHEME>(pay, sc, s, lutf));
-    if constexpr (NR > 0) {
-        /* per MFMA pair: its fragment read(s), the pair, a share of the
-         * decode (Q4_K ~100 VALU per step; IQ4_XS ~70 plus 16 codebook reads) */
-        constexpr int kPairs = 4 * NR;
-        constexpr int kValu = (SCHEME == R9VX_SCHEME_Q4_K ? 104 : 80) / kPairs + 1;
-        constexpr int kLut = SCHEME == R9VX_SCHEME_Q4_K ? 0 : (16 + kPairs - 1) / kPairs;
-        __builtin_amdgcn_sched_group_barrier(0x100, 3, 0); /* first B pair + A */
-        m3_sched<NR, 0, kValu, kLut>();
+        for (int u = 8 * i / P; u < 8 * (i + 1) / P; ++u)
+            m3_dec_unit<SCHEME>(dws[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
+        __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (P == 0) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            m3_dec_unit<SCHEME>(dws[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) out[q] = r9vx_u32x4{o[q][0], o[q][1], o[q][2], o[q][3]};
 }
 
 /* Loads in flight after step J's issue that may still be outstanding when
@@ -180,7 +249,7 @@ constexpr int m3_allowed() {
 template <int SCHEME, int NR>
 __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
                                             const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave,
-                                            const float *lutf, uint32_t arow0, uint32_t bc0, uint32_t bc1,
+                                            const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
                                             r9vx_f32x16 (&acc)[4][2]) {
     const uint32_t lane = tid & 63, c = tid >> 1, hh = tid & 1;
     const uint32_t a_lds = m3_lds_addr(&sm.a[0][0]);
@@ -199,7 +268,7 @@ __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, co
     touch_pay(pay[0]);
     touch_pay(hnext);
     hcur = hnext;
-    m3_compute<SCHEME, 0, 0>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], hcur, hh, lutf, bdec);
+    m3_compute<SCHEME, 0, 0>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], hcur, hh, lut, bdec);
 
     uint32_t s_cur = 0; /* A stage of step k; step k + 2 copies into (s_cur + 2) % 3 */
     for (uint32_t k0 = 0; k0 < nk; k0 += 4) {
@@ -222,9 +291,8 @@ __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, co
             hcur = hnext;                                                                                    \
         }                                                                                                    \
         lds_barrier(); /* every wave's A(k) copy and B(k) */                                                 \
-        __builtin_amdgcn_sched_barrier(0); /* the next decode stays after the barrier */                      \
         m3_compute<SCHEME, (J + 1) & 3, NR>(sm.a[s_cur], sm.b, lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3],  \
-                                            hcur, hh, lutf, bdec);                                           \
+                                            hcur, hh, lut, bdec);                                            \
         __builtin_amdgcn_sched_barrier(0);                                                                   \
         s_cur = s_cur == 2 ? 0u : s_cur + 1;                                                                 \
     }
@@ -253,7 +321,7 @@ __device__ __forceinline__ uint32_t m3_active_tiles(uint32_t rows, uint32_t row0
 /* Runs the main loop with the wave's active row-tile count as a constant. */
 template <int SCHEME>
 __device__ __forceinline__ void m3_run(uint32_t nr, M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
-                                       const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave, const float *lutf,
+                                       const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave, const uint32_t *lut,
                                        uint32_t arow0, uint32_t bc0, uint32_t bc1, r9vx_f32x16 (&acc)[4][2]) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -262,11 +330,11 @@ __device__ __forceinline__ void m3_run(uint32_t nr, M3Lds &sm, const _Float16 *a
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[t][j][r] = 0.f;
     switch (nr) {
-    case 4: m3_mainloop<SCHEME, 4>(sm, abase, aoff, w, nk, tid, wave, lutf, arow0, bc0, bc1, acc); break;
-    case 3: m3_mainloop<SCHEME, 3>(sm, abase, aoff, w, nk, tid, wave, lutf, arow0, bc0, bc1, acc); break;
-    case 2: m3_mainloop<SCHEME, 2>(sm, abase, aoff, w, nk, tid, wave, lutf, arow0, bc0, bc1, acc); break;
-    case 1: m3_mainloop<SCHEME, 1>(sm, abase, aoff, w, nk, tid, wave, lutf, arow0, bc0, bc1, acc); break;
-    default: m3_mainloop<SCHEME, 0>(sm, abase, aoff, w, nk, tid, wave, lutf, arow0, bc0, bc1, acc); break;
+    case 4: m3_mainloop<SCHEME, 4>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+    case 3: m3_mainloop<SCHEME, 3>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+    case 2: m3_mainloop<SCHEME, 2>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+    case 1: m3_mainloop<SCHEME, 1>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+    default: m3_mainloop<SCHEME, 0>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
     }
 }
 

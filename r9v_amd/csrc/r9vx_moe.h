@@ -16,7 +16,11 @@
  *   tiles   u32x4[...] grouped-GEMM tile schedule, 128-row tiles
  *   tiles3  u32x4[...] the same work in 256-row tiles (the r9vx_mma3.h kernels)
  *   h       f32[(P + S*T) * Dff]  SwiGLU rows in sorted order, shared rows after
- *   o       f32[(P + S*T) * Dm]   expert output rows in the same order
+ *   o       f32[(P + S*T) * Dm]   expert output rows in the same order (decode
+ *                                 path); the grouped path stores them in the
+ *                                 same region as fp16 [(P + S*T) * Dm] scaled
+ *                                 per (row, 64-column block), followed by the
+ *                                 f32 scales [(P + S*T) * Dm/64]
  *   hmax    u32[P + S*T]          bits of max|h| per row (grouped GEMM)
  *   h16     fp16[(P + S*T) * Dff] h rows scaled by a power of two, in the down
  *                                 weights' K group order (grouped GEMM)
@@ -91,6 +95,10 @@ struct MoeCombineArgs {
 int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
 int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
 int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
+int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_t part, hipStream_t s);
 int r9vx_moe_combine_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
+
+/* Byte offset (from L.o) of the grouped path's per-(row, 64-column) scales. */
+__host__ __device__ inline uint64_t r9vx_moe_oscale_offset(uint64_t rows, uint32_t dm) { return (2ull * rows * dm + 255) & ~255ull; }
 
 #endif

@@ -114,6 +114,7 @@ EXPORTS = [
     ("r9vx_probe_stream_launch", [_P, ctypes.c_uint64, _P, _P], ctypes.c_int),
     ("r9vx_probe_stream_blocks", [ctypes.c_uint64], _U32),
     ("r9vx_probe_mfma_launch", [_U32, _U32, _P, _P], ctypes.c_int),
+    ("r9vx_probe_moe_stage_launch", [_P, _P, _U32, _P], ctypes.c_int),
     # include/r9vx_gguf.h
     ("r9vx_gguf_parse", [_P, _U64, _P], ctypes.c_int),
     ("r9vx_gguf_parse_table", [_P, _U64, _U64, _P], ctypes.c_int),
@@ -451,3 +452,17 @@ def probe_mfma(blocks, iters, sink=None, stream=None):
         sink = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
     _check(load().r9vx_probe_mfma_launch(blocks, iters, _ptr(sink), _stream(torch, stream)))
     return sink
+
+
+def probe_moe_stage(x, ids, weights, w_gate_up, w_down, e, dff, stage, y, workspace, shared=0,
+                    gate_up_scheme=IQ4_XS, down_scheme=Q4_K, t_bucket=None, stream=None):
+    """Relaunches one stage (1 gate/up GEMM, 2 down GEMM, 3 combine) of the
+    grouped moe_ffn path on a workspace a full moe_ffn call with the same
+    operands filled."""
+    torch = _need_gpu(x, ids, weights, w_gate_up, w_down, y, workspace)
+    t, dm = x.shape
+    k = ids.shape[1]
+    st = ffn_static(t_bucket or max(t, 1), e, k, dm, dff, shared, gate_up_scheme, down_scheme)
+    args = MoeFfnArgs(_ptr(x), _ptr(ids), _ptr(weights), _ptr(w_gate_up), None, _ptr(w_down), None,
+                      _ptr(y), _ptr(workspace), t, 0)
+    _check(load().r9vx_probe_moe_stage_launch(ctypes.byref(st), ctypes.byref(args), stage, _stream(torch, stream)))

@@ -42,6 +42,7 @@ def lib():
         L.rxo_dequantize.argtypes = [I, P, U, U, P]
         L.rxo_matmul.argtypes = [I, P, U, U, I, P, U, P, P, I, P]
         L.rxo_matmul_mt.argtypes = [I, P, U, U, I, P, U, I, P, I]
+        L.rxo_moe_expert_mt.argtypes = [I, P, P, U, U, U, I, P, I, P, P, I]
         L.rxo_router_logits.argtypes = [P, P, U, U, U, P]
         L.rxo_router_logits.restype = None
         L.rxo_act_mul_silu.argtypes = [P, P, ctypes.c_uint64, P]
@@ -171,4 +172,17 @@ def expert_ffn(x, x_dtype, dff, w_gate_up, w_down, scheme_gu=IQ4_XS, scheme_dn=Q
                                 _p(np.ascontiguousarray(w_gate_up)), scheme_dn,
                                 _p(np.ascontiguousarray(w_down)), int(h_bf16), _p(out)),
            "expert_ffn")
+    return out
+
+
+def moe_expert(x, x_dtype, tokens, dff, gu_expert, dn_expert, scheme_gu=IQ4_XS, scheme_dn=Q4_K, threads=1):
+    """One expert's FFN over the rows `tokens` of x (the per-expert body of
+    moe_ffn), rows split over `threads` OpenMP threads."""
+    x = np.ascontiguousarray(x)
+    dm = x.shape[1]
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+    out = np.empty((len(tokens), dm), dtype=np.float32)
+    _check(lib().rxo_moe_expert_mt(x_dtype, _p(x), _p(tokens), len(tokens), dm, dff, scheme_gu,
+                                   _p(np.ascontiguousarray(gu_expert)), scheme_dn,
+                                   _p(np.ascontiguousarray(dn_expert)), _p(out), threads), "moe_expert")
     return out
