@@ -321,6 +321,22 @@ size_t r9vx_moe_ffn_workspace_bytes(const r9vx_moe_ffn_static *st);
  * this workspace left in it (R9VX_STATUS_BAD_EXPERT). */
 int r9vx_moe_ffn_status(const r9vx_moe_ffn_static *st, const uint8_t *sort_workspace,
                         uint32_t *status, r9vx_stream_t stream);
+/* No counterpart in the reference: moe_ffn for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same checks, kernels and results as r9vx_moe_ffn_launch, but
+ * the sort workspace is the library's own device array of
+ * R9VX_NOALLOC_SCRATCH_BYTES on each GPU it runs on (held until the process
+ * ends): args->sort_workspace must be NULL, and a static whose
+ * r9vx_moe_ffn_workspace_bytes exceeds that size is refused
+ * (R9VX_ERR_UNSUPPORTED).  Allocates nothing.  When `status` (a device u32)
+ * is not NULL the launch's status bits are copied there on `stream`
+ * (r9vx_status_read reads them).  Every call on one GPU shares that GPU's
+ * array, which keeps the last call's contents: calls on one stream are
+ * ordered, calls that overlap on one GPU (other streams, other threads)
+ * race. */
+#define R9VX_NOALLOC_SCRATCH_BYTES (16u << 20)
+int r9vx_moe_ffn_launch_noalloc(const r9vx_moe_ffn_static *st, const r9vx_moe_ffn_args *args, uint32_t *status,
+                                r9vx_stream_t stream);
 /* LaunchEntry.static_flops (crates/r9v-registry/src/launch.rs:22-25):
  * (t*K + t*S) rows of 2*(2Dff*Dm) + 2*Dm*Dff. */
 uint64_t r9vx_moe_ffn_static_flops(const r9vx_moe_ffn_static *st, uint32_t t);

@@ -11,6 +11,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "r9vx_internal.h"
@@ -557,12 +558,27 @@ uint64_t r9vx_moe_ffn_static_flops(const r9vx_moe_ffn_static *st, uint32_t t) {
     return per_row * ((uint64_t)t * st->k_topk + (uint64_t)t * st->shared_experts);
 }
 
-static int ffn_common(const char *op, const r9vx_moe_ffn_static *st, const uint32_t *ids, uint32_t t,
-                      const uint8_t *ws, Problems &pr) {
+static void ffn_checks(const r9vx_moe_ffn_static *st, const uint32_t *ids, uint32_t t, Problems &pr) {
     check_ffn_static(st, pr);
     if (t == 0) pr.add(R9VX_ERR_INVALID, "t must be > 0");
     if (t > st->t_bucket) pr.add(R9VX_ERR_INVALID, "t=%u exceeds t_bucket=%u", t, st->t_bucket);
     if (!ids) pr.add(R9VX_ERR_NULL, "expert_ids is NULL");
+}
+
+/* The operand checks of a moe_ffn launch, workspace aside. */
+static void ffn_arg_checks(const r9vx_moe_ffn_args *a, Problems &pr) {
+    if (!a->x || !a->weights || !a->w_gate_up || !a->w_down || !a->y)
+        pr.add(R9VX_ERR_NULL, "x, weights, w_gate_up, w_down and y are required");
+    if (a->w_gate_up_scales || a->w_down_scales)
+        pr.add(R9VX_ERR_UNSUPPORTED, "separate scale carriers must be NULL: GGUF blocks carry inline scales");
+    if ((a->x && !aligned16(a->x)) || (a->y && !aligned16(a->y)) || (a->w_gate_up && !aligned16(a->w_gate_up)) ||
+        (a->w_down && !aligned16(a->w_down)))
+        pr.add(R9VX_ERR_ALIGN, "x, y and weights must be 16-byte aligned");
+}
+
+static int ffn_common(const char *op, const r9vx_moe_ffn_static *st, const uint32_t *ids, uint32_t t,
+                      const uint8_t *ws, Problems &pr) {
+    ffn_checks(st, ids, t, pr);
     if (!ws) pr.add(R9VX_ERR_WORKSPACE, "sort_workspace is NULL (size r9vx_moe_ffn_workspace_bytes)");
     if (ws && ((uintptr_t)ws & 255u)) pr.add(R9VX_ERR_ALIGN, "sort_workspace must be 256-byte aligned");
     return pr.finish(op);
@@ -596,13 +612,7 @@ int r9vx_moe_ffn_launch(const r9vx_moe_ffn_static *st, const r9vx_moe_ffn_args *
         pr.add(R9VX_ERR_NULL, "static and args must be non-NULL");
         return pr.finish("moe_ffn");
     }
-    if (!a->x || !a->weights || !a->w_gate_up || !a->w_down || !a->y)
-        pr.add(R9VX_ERR_NULL, "x, weights, w_gate_up, w_down and y are required");
-    if (a->w_gate_up_scales || a->w_down_scales)
-        pr.add(R9VX_ERR_UNSUPPORTED, "separate scale carriers must be NULL: GGUF blocks carry inline scales");
-    if ((a->x && !aligned16(a->x)) || (a->y && !aligned16(a->y)) || (a->w_gate_up && !aligned16(a->w_gate_up)) ||
-        (a->w_down && !aligned16(a->w_down)))
-        pr.add(R9VX_ERR_ALIGN, "x, y and weights must be 16-byte aligned");
+    ffn_arg_checks(a, pr);
     int rc = ffn_common("moe_ffn", st, a->expert_ids, a->t, a->sort_workspace, pr);
     if (rc) return rc;
     r9vx_moe_problem p = ffn_problem(st, a);
@@ -620,6 +630,89 @@ int r9vx_moe_ffn_status(const r9vx_moe_ffn_static *st, const uint8_t *ws, uint32
     int rc = (int)hipMemcpyAsync(status, ws + L.status, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
     if (!rc) rc = (int)hipStreamSynchronize(s);
     return hip_status("moe_ffn_status", rc);
+}
+
+/* ------------------------------------------------------ moe_ffn, no alloc */
+
+}  // extern "C"
+
+/* The sort workspace of r9vx_moe_ffn_launch_noalloc: one array on each GPU
+ * the library runs on, held until the process ends.  In host code its name
+ * is a host-side stand-in, never a device address: host code uses only the
+ * address hipGetSymbolAddress returns for the current device (fetched once
+ * per device and kept in g_scratch). */
+static __device__ __align__(256) uint8_t scratch[R9VX_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch[kScratchDevices];
+
+/* Device address of the current device's scratch array, or nullptr with
+ * *err set. */
+uint8_t *device_scratch(hipError_t *err) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess && (dev < 0 || dev >= kScratchDevices)) e = hipErrorInvalidDevice;
+    if (e != hipSuccess) {
+        *err = e;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
+            return nullptr;
+        }
+        g_scratch[dev] = static_cast<uint8_t *>(ptr);
+    }
+    return g_scratch[dev];
+}
+
+__global__ void copy_status_kernel(const uint32_t *src, uint32_t *dst) { *dst = *src; }
+
+}  // namespace
+
+extern "C" {
+
+int r9vx_moe_ffn_launch_noalloc(const r9vx_moe_ffn_static *st, const r9vx_moe_ffn_args *a, uint32_t *status,
+                                r9vx_stream_t stream) {
+    Problems pr;
+    if (!st || !a) {
+        pr.add(R9VX_ERR_NULL, "static and args must be non-NULL");
+        return pr.finish("moe_ffn_noalloc");
+    }
+    ffn_arg_checks(a, pr);
+    ffn_checks(st, a->expert_ids, a->t, pr);
+    if (a->sort_workspace)
+        pr.add(R9VX_ERR_INVALID, "sort_workspace must be NULL: this launch uses the library's own scratch");
+    const size_t need = r9vx_moe_ffn_workspace_bytes(st);
+    if (need > R9VX_NOALLOC_SCRATCH_BYTES)
+        pr.add(R9VX_ERR_UNSUPPORTED,
+               "the workspace of this static (%zu bytes) exceeds the no-alloc scratch (%u bytes): lower t_bucket, "
+               "or call r9vx_moe_ffn_launch with a workspace",
+               need, (unsigned)R9VX_NOALLOC_SCRATCH_BYTES);
+    if (status && ((uintptr_t)status & 3u)) pr.add(R9VX_ERR_ALIGN, "status must be 4-byte aligned");
+    int rc = pr.finish("moe_ffn_noalloc");
+    if (rc) return rc;
+    hipError_t err = hipSuccess;
+    uint8_t *ws = device_scratch(&err);
+    if (!ws) return hip_status("moe_ffn_noalloc", (int)err);
+    r9vx_moe_ffn_args b = *a;
+    b.sort_workspace = ws;
+    const r9vx_moe_problem p = ffn_problem(st, &b);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    rc = r9vx_launch_moe(p, s);
+    if (!rc && status) {
+        const MoeLayout L = r9vx_moe_layout(p.t_bucket, p.e, p.k, p.dm, p.dff, p.shared);
+        hipLaunchKernelGGL(copy_status_kernel, dim3(1), dim3(1), 0, s,
+                           reinterpret_cast<const uint32_t *>(ws + L.status), status);
+        rc = (int)hipGetLastError();
+    }
+    return hip_status("moe_ffn_noalloc", rc);
 }
 
 int r9vx_probe_moe_stage_launch(const r9vx_moe_ffn_static *st, const r9vx_moe_ffn_args *a, uint32_t stage,

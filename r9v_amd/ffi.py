@@ -99,6 +99,7 @@ EXPORTS = [
     ("r9vx_moe_route_hidden_status", [_P, _P, _P, _P], ctypes.c_int),
     ("r9vx_router_repack_launch", [_P, _U32, _U32, _P, _P], ctypes.c_int),
     ("r9vx_moe_ffn_launch", [_P, _P, _P], ctypes.c_int),
+    ("r9vx_moe_ffn_launch_noalloc", [_P, _P, _P, _P], ctypes.c_int),
     ("r9vx_moe_ffn_workspace_bytes", [_P], ctypes.c_size_t),
     ("r9vx_moe_ffn_status", [_P, _P, _P, _P], ctypes.c_int),
     ("r9vx_moe_ffn_static_flops", [_P, _U32], ctypes.c_uint64),
@@ -410,6 +411,25 @@ def moe_ffn(x, ids, weights, w_gate_up, w_down, e, dff, shared=0, gate_up_scheme
                       _ptr(y), _ptr(workspace), t, 0)
     _check(load().r9vx_moe_ffn_launch(ctypes.byref(st), ctypes.byref(args), _stream(torch, stream)))
     return y, workspace, st
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20
+
+
+def moe_ffn_noalloc(x, ids, weights, w_gate_up, w_down, e, dff, y, shared=0, gate_up_scheme=IQ4_XS,
+                    down_scheme=Q4_K, status=None, t_bucket=None, stream=None):
+    """moe_ffn through r9vx_moe_ffn_launch_noalloc: no workspace (the
+    library's own per-GPU scratch), y given by the caller, optional device
+    u32 `status` receiving the launch's status bits."""
+    torch = _need_gpu(x, ids, weights, w_gate_up, w_down, y, status)
+    t, dm = x.shape
+    k = ids.shape[1]
+    st = ffn_static(t_bucket or max(t, 1), e, k, dm, dff, shared, gate_up_scheme, down_scheme)
+    args = MoeFfnArgs(_ptr(x), _ptr(ids), _ptr(weights), _ptr(w_gate_up), None, _ptr(w_down), None,
+                      _ptr(y), None, t, 0)
+    _check(load().r9vx_moe_ffn_launch_noalloc(ctypes.byref(st), ctypes.byref(args), _ptr(status),
+                                              _stream(torch, stream)))
+    return y
 
 
 def moe_ffn_status(st, workspace, stream=None) -> int:

@@ -300,3 +300,23 @@ def test_route_hidden_refusals():
     for part in ("decode form (t <= 8)", "dm=100", "x, w_router", "workspace of"):
         assert part in msg, msg
     assert lib.r9vx_moe_route_hidden_workspace_bytes(ctypes.byref(st)) == 16 * 512 * 4 + 256
+
+
+def test_moe_ffn_noalloc_host_refusals():
+    """The no-alloc moe_ffn launch refuses a caller workspace and statics whose
+    workspace exceeds its scratch before touching the device."""
+    lib = ffi.load()
+    fake = ctypes.c_void_p(1 << 20)  # 256-byte aligned, never dereferenced: the call is refused first
+    st = ffi.ffn_static(t_bucket=4, e=8, k=2, dm=256, dff=256)
+    args = ffi.MoeFfnArgs(fake, fake, fake, fake, None, fake, None, fake, fake, 4, 0)
+    assert lib.r9vx_moe_ffn_launch_noalloc(ctypes.byref(st), ctypes.byref(args), None, None) == -1
+    assert "sort_workspace must be NULL" in lib.r9vx_last_error().decode()
+    big = ffi.ffn_static(t_bucket=8192, e=512, k=10, dm=2048, dff=512)
+    assert ffi.ffn_workspace_bytes(big) > ffi.NOALLOC_SCRATCH_BYTES
+    args.sort_workspace = None
+    assert lib.r9vx_moe_ffn_launch_noalloc(ctypes.byref(big), ctypes.byref(args), None, None) == -2
+    assert "exceeds the no-alloc scratch (16777216 bytes)" in lib.r9vx_last_error().decode()
+    # configs[3] (T=5, E=512 + 1 shared, top-10, 2048 / 512) fits
+    c3 = ffi.ffn_static(t_bucket=5, e=512, k=10, dm=2048, dff=512, shared=1)
+    assert ffi.ffn_workspace_bytes(c3) <= ffi.NOALLOC_SCRATCH_BYTES
+    assert lib.r9vx_moe_ffn_launch_noalloc(None, ctypes.byref(args), None, None) == -3
