@@ -323,35 +323,45 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
-    m3_run<DN>(nr, sm, a.h16, aoff, w, a.dff / kTileK, tid, wv, lut, 128 * rh, 64 * cq, 64 * cq + 32, acc);
+    m3_run<DN, true>(nr, sm, a.h16, aoff, w, a.dff / kTileK, tid, wv, lut, 128 * rh, 64 * cq, 64 * cq + 32, acc);
 
-    /* o rows as fp16 scaled by a power of two per (row, 64-column block):
-     * the block is this wave's two column tiles, so its max is a reduction
-     * over the 32 lanes holding the row; the scale puts the block max in
-     * [2^14, 2^15) and is stored beside the rows for the combine. */
+    /* The tiles are transposed (m3_run<.., true>): lane l holds h row
+     * 128 rh + 32 t + (l & 31) and output columns n0 + 64 cq + 32 j +
+     * 8 (r >> 2) + 4 (l >> 5) + (r & 3).  o rows are stored as fp16 scaled by
+     * a power of two per (row, 64-column block), the block being this wave's
+     * two column tiles: its max is this lane's 32 values and lane l ^ 32's.
+     * The scale puts the block max in [2^14, 2^15); its inverse is stored
+     * beside the rows for the combine. */
     const uint64_t nrows_all = (uint64_t)a.p + (uint64_t)a.shared * a.t;
     _Float16 *o16 = reinterpret_cast<_Float16 *>(a.ws + a.L.o);
     float *oscale = reinterpret_cast<float *>(a.ws + a.L.o + r9vx_moe_oscale_offset(nrows_all, a.dm));
-    const uint32_t c0 = n0 + 64 * cq + (lane & 31), blk = (n0 + 64 * cq) / 64, nblk = a.dm / 64;
+    const uint32_t blk = (n0 + 64 * cq) / 64, nblk = a.dm / 64, cb = n0 + 64 * cq + 4 * (lane >> 5);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         if ((uint32_t)t >= nr) break;
+        const uint32_t rl = 128 * rh + 32 * t + (lane & 31);
+        const float sc = rl < rows ? rowsc[rl] : 0.f;
+        float m = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t rl = 128 * rh + 32 * t + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            const float sc = rl < rows ? rowsc[rl] : 0.f;
-            const float v0 = acc[t][0][r] * sc, v1 = acc[t][1][r] * sc;
-            float m = fmaxf(fabsf(v0), fabsf(v1));
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-            int e = 0;
-            (void)frexpf(m, &e); /* m = f * 2^e, f in [0.5, 1): m * 2^(15 - e) < 2^15 */
-            if (rl >= rows) continue;
-            const uint64_t row = pos0 + rl;
-            o16[row * a.dm + c0] = (_Float16)ldexpf(v0, 15 - e);
-            o16[row * a.dm + c0 + 32] = (_Float16)ldexpf(v1, 15 - e);
-            if ((lane & 31) == 0) oscale[row * nblk + blk] = ldexpf(1.0f, e - 15);
-        }
+            for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(acc[t][j][r]));
+        m *= sc; /* exact: sc is a power of two */
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        int e = 0;
+        (void)frexpf(m, &e); /* m = f 2^e, f in [0.5, 1) */
+        const float f = ldexpf(sc, 15 - e); /* a power of two: acc * f = (acc * sc) 2^(15 - e) exactly */
+        if (rl >= rows) continue;
+        _Float16 *orow = o16 + (uint64_t)(pos0 + rl) * a.dm + cb;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const r9vx_u32x2 v{pack_h2h((_Float16)(acc[t][j][4 * g] * f), (_Float16)(acc[t][j][4 * g + 1] * f)),
+                                   pack_h2h((_Float16)(acc[t][j][4 * g + 2] * f), (_Float16)(acc[t][j][4 * g + 3] * f))};
+                *reinterpret_cast<r9vx_u32x2 *>(orow + 32 * j + 8 * g) = v;
+            }
+        if (lane < 32) oscale[(uint64_t)(pos0 + rl) * nblk + blk] = ldexpf(1.0f, e - 15);
     }
 }
 

@@ -172,7 +172,7 @@ __device__ __forceinline__ void m3_dec_unit(uint32_t dw, int m, const BScale &sc
  * pair the fragment reads of the next pair (B of a slice with the last A of
  * the previous one), the pair, and the decode of one or more payload bytes.
  */
-template <int SCHEME, int KS, int NR>
+template <int SCHEME, int KS, int NR, bool TR>
 __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bsm, uint32_t lane, uint32_t arow0,
                                            uint32_t bc0, uint32_t bc1, r9vx_f32x16 (&acc)[4][2],
                                            const r9vx_u32x4 &pay, const r9vx_u32x4 &hd, uint32_t hh,
@@ -213,8 +213,13 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
             a[(i + 1) & 1] = *reinterpret_cast<const half8 *>(arow + 4096u * t1 + goff(s1));
         }
         __builtin_amdgcn_sched_barrier(0);
-        acc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i & 1], b[s & 1][0], acc[t][0], 0, 0, 0);
-        acc[t][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i & 1], b[s & 1][1], acc[t][1], 0, 0, 0);
+        if constexpr (TR) { /* operands swapped: the tile of B . A^T */
+            acc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[s & 1][0], a[i & 1], acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[s & 1][1], a[i & 1], acc[t][1], 0, 0, 0);
+        } else {
+            acc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i & 1], b[s & 1][0], acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i & 1], b[s & 1][1], acc[t][1], 0, 0, 0);
+        }
         /* decode units [8 i / P, 8 (i + 1) / P) */
 #pragma unroll
         for (int u = 8 * i / P; u < 8 * (i + 1) / P; ++u)
@@ -246,7 +251,7 @@ constexpr int m3_allowed() {
  * is in the next super-block when J == 3; that block's header arrives in
  * hnext (loaded at J == 1) and is copied to hcur once it has arrived.
  */
-template <int SCHEME, int NR>
+template <int SCHEME, int NR, bool TR>
 __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
                                             const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave,
                                             const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
@@ -268,7 +273,7 @@ __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, co
     touch_pay(pay[0]);
     touch_pay(hnext);
     hcur = hnext;
-    m3_compute<SCHEME, 0, 0>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], hcur, hh, lut, bdec);
+    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], hcur, hh, lut, bdec);
 
     uint32_t s_cur = 0; /* A stage of step k; step k + 2 copies into (s_cur + 2) % 3 */
     for (uint32_t k0 = 0; k0 < nk; k0 += 4) {
@@ -291,7 +296,7 @@ __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, co
             hcur = hnext;                                                                                    \
         }                                                                                                    \
         lds_barrier(); /* every wave's A(k) copy and B(k) */                                                 \
-        m3_compute<SCHEME, (J + 1) & 3, NR>(sm.a[s_cur], sm.b, lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3],  \
+        m3_compute<SCHEME, (J + 1) & 3, NR, TR>(sm.a[s_cur], sm.b, lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3],  \
                                             hcur, hh, lut, bdec);                                            \
         __builtin_amdgcn_sched_barrier(0);                                                                   \
         s_cur = s_cur == 2 ? 0u : s_cur + 1;                                                                 \
@@ -318,8 +323,11 @@ __device__ __forceinline__ uint32_t m3_active_tiles(uint32_t rows, uint32_t row0
     return n < 4 ? n : 4;
 }
 
-/* Runs the main loop with the wave's active row-tile count as a constant. */
-template <int SCHEME>
+/* Runs the main loop with the wave's active row-tile count as a constant.
+ * TR: acc[t][j] holds the transposed tile (B rows bc_j.. as its rows, A rows
+ * arow0 + 32 t.. as its columns): lane l then holds A row arow0 + 32 t +
+ * (l & 31) and B rows bc_j + 8 (r >> 2) + 4 (l >> 5) + (r & 3). */
+template <int SCHEME, bool TR = false>
 __device__ __forceinline__ void m3_run(uint32_t nr, M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
                                        const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave, const uint32_t *lut,
                                        uint32_t arow0, uint32_t bc0, uint32_t bc1, r9vx_f32x16 (&acc)[4][2]) {
@@ -330,11 +338,11 @@ __device__ __forceinline__ void m3_run(uint32_t nr, M3Lds &sm, const _Float16 *a
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[t][j][r] = 0.f;
     switch (nr) {
-    case 4: m3_mainloop<SCHEME, 4>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
-    case 3: m3_mainloop<SCHEME, 3>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
-    case 2: m3_mainloop<SCHEME, 2>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
-    case 1: m3_mainloop<SCHEME, 1>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
-    default: m3_mainloop<SCHEME, 0>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+    case 4: m3_mainloop<SCHEME, 4, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+    case 3: m3_mainloop<SCHEME, 3, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+    case 2: m3_mainloop<SCHEME, 2, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+    case 1: m3_mainloop<SCHEME, 1, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+    default: m3_mainloop<SCHEME, 0, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
     }
 }
 
