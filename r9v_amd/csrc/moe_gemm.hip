@@ -267,7 +267,7 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
         const uint32_t tok = row_token(a, expert, pos0 + (r < rows ? r : 0));
         aoff[i] = (tok * a.dm + 8 * dma_group(r, lane)) * 2u;
     }
-    const uint32_t c = tid >> 1;
+    const uint32_t c = m3_brow(tid);
     const uint32_t wr = c < 128 ? j0 + c : a.dff + j0 + (c - 128);
     const M3WRow w{m3_uniform(a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes), wr * (uint32_t)a.gu_row_bytes};
     const uint32_t rh = wv >> 2, cq = wv & 3;
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
         aoff[i] = ((pos0 + (r < rows ? r : 0)) * a.dff + 8 * dma_group(r, lane)) * 2u;
     }
     const M3WRow w{m3_uniform(a.w_dn + ((uint64_t)expert * a.dm + n0) * a.dn_row_bytes),
-                   (tid >> 1) * (uint32_t)a.dn_row_bytes};
+                   m3_brow(tid) * (uint32_t)a.dn_row_bytes};
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];

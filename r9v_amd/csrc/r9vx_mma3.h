@@ -3,24 +3,23 @@
  * workgroup into LDS, shared by the grouped MoE GEMMs.
  *
  * Tile: 256 rows x 256 columns, K steps of 64, 512 threads (8 waves, two per
- * SIMD, one workgroup per CU).
- *   B (weights): thread t decodes half hh = t & 1 of weight row c = t >> 1 for
- *     the next K step while the MFMAs of the current one run: its 16 payload
- *     bytes (groups 4hh .. 4hh+3 of the step, r9vx_mma2.h's K group order)
- *     become 32 fp16 by the exact f32 formula and one rounding, held in
- *     registers, and are written to the single LDS B tile after the step's
- *     first barrier.  Every weight is decoded once per 256 output rows.
+ * SIMD, one workgroup per CU).  LDS: two A stages and two B tiles (128 KiB).
+ *   B (weights): thread t decodes half hh = t & 1 of weight row m3_brow(t)
+ *     for the next K step while the MFMAs of the current one run: its 16
+ *     payload bytes (groups 4hh .. 4hh+3 of the step, r9vx_mma2.h's K group
+ *     order) become 32 fp16 by the exact f32 formula and one rounding, and
+ *     each 16-byte granule goes to the other B tile as soon as it is whole.
+ *     Every weight is decoded once per 256 output rows.
  *   A (activations, fp16 in the same group order): direct global->LDS copies
- *     into 3 stages, two steps ahead.
+ *     into the other A stage, one step ahead.
  *   MFMA: wave w owns rows 128 (w >> 2) .. +128 (four 32-row tiles, of which
  *     the first NR hold rows of this tile) and two 32-column tiles of B; per
  *     16-K slice it reads 2 B and NR A fragments for 2 NR MFMAs
- *     (v_mfma_f32_32x32x16_f16).
- * Per K step: barrier (every wave is done reading B and the oldest A stage),
- * B written, this step's loads issued (payload 3 steps ahead, block header
- * with the first payload of its super-block, A copy 2 steps ahead), wait for
- * this step's A copy and the next step's payload, barrier, MFMAs of this step
- * interleaved with the decode of the next.
+ *     (v_mfma_f32_32x32x16_f16), fragments two MFMA pairs ahead.
+ * Per K step: one barrier (B(k) and A(k) complete; step k - 1's tile and
+ * stage free), the A(k + 1) copy and the payload load of step k + 3 issued,
+ * then the MFMAs of step k interleaved with the decode and writes of
+ * B(k + 1), then a wait for the A(k + 1) copy.
  *
  * Loads are inline assembly waited by count, as in r9vx_mma2.h; their
  * registers are tied in and out of the load ("+v") so that a value crossing
@@ -37,11 +36,12 @@ namespace r9vx {
 constexpr uint32_t kM3Rows = 256;          /* output rows per tile */
 constexpr uint32_t kM3Cols = 256;          /* output columns per tile */
 constexpr uint32_t kM3Stage = 256u * 128u; /* one A stage or the B tile: 256 rows of 64 fp16 */
-constexpr int kM3AStages = 3;
+constexpr int kM3AStages = 2;
+constexpr int kM3BStages = 2;
 
 struct M3Lds {
     uint8_t a[kM3AStages][kM3Stage];
-    uint8_t b[kM3Stage];
+    uint8_t b[kM3BStages][kM3Stage];
 };
 
 __device__ __forceinline__ uint32_t pack_h2h(_Float16 a, _Float16 b) {
@@ -102,11 +102,15 @@ __device__ __forceinline__ void m3_dma_a(uint32_t stage_lds, const _Float16 *aba
     }
 }
 
-__device__ __forceinline__ void m3_write_b(uint8_t *b, uint32_t c, uint32_t hh, const r9vx_u32x4 (&v)[4]) {
-    uint8_t *row = b + c * 128u;
-    const uint32_t sw = m2_swz(c);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) *reinterpret_cast<r9vx_u32x4 *>(row + (((4u * hh + s) ^ sw) << 4)) = v[s];
+/* The B row (0..255) that thread tid decodes and writes, two threads per
+ * row (tid & 1 picks the 32-element half).  Rows are permuted inside each
+ * aligned group of 8 so that the 8 lanes a 128-bit LDS write serves per
+ * pass hold 4 rows with distinct swizzles (m2_swz pairs rows 2i, 2i + 1):
+ * lanes of threads 2j, 2j + 1, j = 8g .. 8g + 7, take rows 8g + {0, 2, 4, 6,
+ * 1, 3, 5, 7}.  With tid >> 1 as the row every write conflicted two ways. */
+__device__ __forceinline__ uint32_t m3_brow(uint32_t tid) {
+    const uint32_t j = tid >> 1;
+    return (j & ~7u) | ((j & 3u) << 1) | ((j >> 2) & 1u);
 }
 
 /* IQ4_XS codebook pairs as fp16: entry b = {kv[b & 15], kv[b >> 4]} (1 KiB,
@@ -146,10 +150,10 @@ __device__ __forceinline__ void m3_dec_unit(uint32_t dw, int m, const BScale &sc
          * of the f32 multiply followed by one fp16 rounding.  mixlo / mixhi
          * write the low / high half of the destination (op_sel picks the
          * codebook half, op_sel_hi marks it as fp16). */
-        uint32_t a = 0, b = 0;
-        asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "+v"(a) : "v"(sc.dl0), "v"(kv0));
+        uint32_t a, b; /* mixlo writes the low half (the high half is then written by mixhi) */
+        asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(a) : "v"(sc.dl0), "v"(kv0));
         asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "+v"(a) : "v"(sc.dl0), "v"(kv1));
-        asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(b) : "v"(sc.dl0), "v"(kv0));
+        asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(b) : "v"(sc.dl0), "v"(kv0));
         asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(b) : "v"(sc.dl0), "v"(kv1));
         lo2 = a;
         hi2 = b;
@@ -166,17 +170,17 @@ __device__ __forceinline__ void m3_dec_unit(uint32_t dw, int m, const BScale &sc
 /*
  * One K step's compute: the MFMAs of this step (A rows arow0 + 32t for t <
  * NR, B rows bc0 / bc1; the bases are multiples of 32, so a fragment row's
- * swizzle is that of lane % 32) and the decode of the next step's B into
- * `out`.  Scheduled by hand, each stage fenced so the compiler keeps it:
- * the step's 16 codebook reads (IQ4_XS) and first fragments, then per MFMA
- * pair the fragment reads of the next pair (B of a slice with the last A of
- * the previous one), the pair, and the decode of one or more payload bytes.
+ * swizzle is that of lane % 32) and the decode of the next step's B, whose
+ * granules go to bdst (this thread's row of the other B tile, swizzle bsw).
+ * Scheduled by hand, each stage fenced so the compiler keeps it: per MFMA
+ * pair the fragment and codebook reads that run ahead, the pair, and the
+ * decode of one or more payload bytes with the writes it completes.
  */
 template <int SCHEME, int KS, int NR, bool TR>
 __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bsm, uint32_t lane, uint32_t arow0,
                                            uint32_t bc0, uint32_t bc1, r9vx_f32x16 (&acc)[4][2],
                                            const r9vx_u32x4 &pay, const r9vx_u32x4 &hd, uint32_t hh,
-                                           const uint32_t *lut, r9vx_u32x4 (&out)[4]) {
+                                           const uint32_t *lut, uint8_t *bdst, uint32_t bsw) {
     constexpr bool kIq4 = SCHEME == R9VX_SCHEME_IQ4_XS;
     constexpr int P = 4 * NR; /* MFMA pairs */
     const uint32_t h = lane >> 5, r32 = lane & 31, sw = m2_swz(r32);
@@ -184,132 +188,150 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
     const uint8_t *brow0 = bsm + (bc0 + r32) * 128u, *brow1 = bsm + (bc1 + r32) * 128u;
     auto goff = [&](int s) { return ((4u * h + (uint32_t)s) ^ sw) << 4; };
     const uint32_t dws[4] = {pay.x, pay.y, pay.z, pay.w};
+    /* IQ4_XS codebook pairs of unit u are read kLead pairs before the pair
+     * that decodes it (pair dec_pair(u)), so that their LDS latency and bank
+     * conflicts overlap MFMAs; those due before pair 0 are read up front. */
+    constexpr int kLead = 2;
+    /* the pair after whose MFMAs unit u is decoded */
+    auto dec_pair = [](int u) { return ((u + 1) * P + 7) / 8 - 1; };
     uint32_t kv[16];
+    auto read_kv = [&](int u) {
+        kv[2 * u] = lut[(dws[u >> 1] >> (16 * (u & 1))) & 0xFFu];
+        kv[2 * u + 1] = lut[(dws[u >> 1] >> (16 * (u & 1) + 8)) & 0xFFu];
+    };
+#pragma unroll
+    for (int b = 0; b < 16; ++b) kv[b] = 0u;
     if constexpr (kIq4) {
 #pragma unroll
-        for (int b = 0; b < 16; ++b) kv[b] = lut[(dws[b >> 2] >> (8 * (b & 3))) & 0xFFu];
-    } else {
-#pragma unroll
-        for (int b = 0; b < 16; ++b) kv[b] = 0u;
+        for (int u = 0; u < 8; ++u)
+            if (P == 0 || dec_pair(u) - kLead < 0) read_kv(u);
     }
     const BScale sc = bscale<SCHEME, KS>(hd, hh);
-    uint32_t o[4][4]; /* out[q] words */
-    half8 a[2], b[2][2];
-    if constexpr (P > 0) {
-        b[0][0] = *reinterpret_cast<const half8 *>(brow0 + goff(0));
-        b[0][1] = *reinterpret_cast<const half8 *>(brow1 + goff(0));
-        a[0] = *reinterpret_cast<const half8 *>(arow + goff(0));
-    }
+    uint32_t o[4][4]; /* granule q of the decoded half row */
+    /* Fragments are read kAhead pairs before their MFMAs (two when the
+     * wave has several row tiles: B of a slice then lands after the slice
+     * two back has used its buffer; one otherwise), so that the LDS latency
+     * overlaps this wave's earlier MFMAs. */
+    constexpr int kAhead = NR >= 2 ? 2 : 1;
+    half8 a[kAhead + 1], b[2][2];
+    auto read_frags = [&](int j) {
+        const int sj = j / NR, tj = j % NR;
+        if (tj == 0) {
+            b[sj & 1][0] = *reinterpret_cast<const half8 *>(brow0 + goff(sj));
+            b[sj & 1][1] = *reinterpret_cast<const half8 *>(brow1 + goff(sj));
+        }
+        a[j % (kAhead + 1)] = *reinterpret_cast<const half8 *>(arow + 4096u * tj + goff(sj));
+    };
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j)
+        if (j < P) read_frags(j);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < P; ++i) {
         const int s = i / NR, t = i % NR;
-        if (i + 1 < P) { /* the next pair's fragments, a whole pair ahead of their use */
-            const int s1 = (i + 1) / NR, t1 = (i + 1) % NR;
-            if (t1 == 0) {
-                b[s1 & 1][0] = *reinterpret_cast<const half8 *>(brow0 + goff(s1));
-                b[s1 & 1][1] = *reinterpret_cast<const half8 *>(brow1 + goff(s1));
-            }
-            a[(i + 1) & 1] = *reinterpret_cast<const half8 *>(arow + 4096u * t1 + goff(s1));
+        if (i + kAhead < P) read_frags(i + kAhead);
+        if constexpr (kIq4) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (dec_pair(u) - kLead == i) read_kv(u);
         }
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (TR) { /* operands swapped: the tile of B . A^T */
-            acc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[s & 1][0], a[i & 1], acc[t][0], 0, 0, 0);
-            acc[t][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[s & 1][1], a[i & 1], acc[t][1], 0, 0, 0);
+            acc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[s & 1][0], a[i % (kAhead + 1)], acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[s & 1][1], a[i % (kAhead + 1)], acc[t][1], 0, 0, 0);
         } else {
-            acc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i & 1], b[s & 1][0], acc[t][0], 0, 0, 0);
-            acc[t][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i & 1], b[s & 1][1], acc[t][1], 0, 0, 0);
+            acc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i % (kAhead + 1)], b[s & 1][0], acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i % (kAhead + 1)], b[s & 1][1], acc[t][1], 0, 0, 0);
         }
-        /* decode units [8 i / P, 8 (i + 1) / P) */
 #pragma unroll
-        for (int u = 8 * i / P; u < 8 * (i + 1) / P; ++u)
-            m3_dec_unit<SCHEME>(dws[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
+        for (int u = 0; u < 8; ++u)
+            if (dec_pair(u) == i) m3_dec_unit<SCHEME>(dws[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
+        /* granule q of the row is whole once unit 2q + 1 is decoded */
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (dec_pair(2 * q + 1) == i)
+                *reinterpret_cast<r9vx_u32x4 *>(bdst + (((4u * hh + q) ^ bsw) << 4)) =
+                    r9vx_u32x4{o[q][0], o[q][1], o[q][2], o[q][3]};
         __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (P == 0) {
 #pragma unroll
         for (int u = 0; u < 8; ++u)
             m3_dec_unit<SCHEME>(dws[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
-    }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) out[q] = r9vx_u32x4{o[q][0], o[q][1], o[q][2], o[q][3]};
-}
-
-/* Loads in flight after step J's issue that may still be outstanding when
- * step J waits (those of steps J-1 and J; a step issues 5, 6 when it also
- * loads the next block header, which step J == 1 of a super-block does). */
-template <int J>
-constexpr int m3_allowed() {
-    return (J == 1 || J == 2) ? 11 : 10;
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<r9vx_u32x4 *>(bdst + (((4u * hh + q) ^ bsw) << 4)) =
+                r9vx_u32x4{o[q][0], o[q][1], o[q][2], o[q][3]};
+    }
 }
 
 /*
- * The main loop over nk K steps (nk a multiple of 4).  abase / aoff: the A
- * copy sources (m3_dma_a); w: the decoding thread's weight row; wave: the
- * uniform wave index.  acc must be zero on entry; rows of tiles t >= NR are
- * not computed.  Step J of a super-block decodes the next step's B, which
- * is in the next super-block when J == 3; that block's header arrives in
- * hnext (loaded at J == 1) and is copied to hcur once it has arrived.
+ * The main loop over nk K steps (nk a multiple of 4), with two B tiles and
+ * two A stages: one barrier per step.  abase / aoff: the A copy sources
+ * (m3_dma_a); w: the decoding thread's weight row; wave: the uniform wave
+ * index.  acc must be zero on entry; rows of tiles t >= NR are not computed.
+ * The decode of step k + 1's B needs the next super-block's header when
+ * J == 3; it is loaded at J == 1 into hnext and copied to hcur at J == 3.
+ * Step k: barrier (B(k) and A(k) are complete and visible, and every wave is
+ * done with step k - 1's A stage and B tile), the copy of A(k + 1) into the
+ * other A stage and the payload load of step k + 3 (plus the next block
+ * header when J == 1), then the MFMAs of step k interleaved with the decode
+ * of B(k + 1), each of whose four 16-byte granules is written into the other
+ * B tile as soon as it is whole, then a wait for the A(k + 1) copy.
  */
 template <int SCHEME, int NR, bool TR>
 __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
-                                            const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave,
-                                            const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
-                                            r9vx_f32x16 (&acc)[4][2]) {
-    const uint32_t lane = tid & 63, c = tid >> 1, hh = tid & 1;
+                                               const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave,
+                                               const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
+                                               r9vx_f32x16 (&acc)[4][2]) {
+    const uint32_t lane = tid & 63, c = m3_brow(tid), hh = tid & 1, bsw = m2_swz(c);
     const uint32_t a_lds = m3_lds_addr(&sm.a[0][0]);
-    r9vx_u32x4 pay[4], hnext, hcur, bdec[4];
+    r9vx_u32x4 pay[4], hnext, hcur;
 #pragma unroll
     for (int i = 0; i < 4; ++i) pay[i] = r9vx_u32x4{0u, 0u, 0u, 0u};
     hnext = r9vx_u32x4{0u, 0u, 0u, 0u};
-    /* prologue in the steady-state order: P0 H0 | P1 A0 | P2 A1 */
+    /* prologue: P0 H0 | A0 | P1 P2; B(0) decoded into B tile 0 */
     m3_load_pay<SCHEME>(w, 0, hh, pay[0]);
     m3_load_hdr<SCHEME>(w, 0, hnext);
-    m3_load_pay<SCHEME>(w, 1, hh, pay[1]);
     m3_dma_a(a_lds, abase, aoff, 0, wave);
+    m3_load_pay<SCHEME>(w, 1, hh, pay[1]);
     m3_load_pay<SCHEME>(w, 2, hh, pay[2]);
-    m3_dma_a(a_lds + kM3Stage, abase, aoff, 1, wave);
-    wait_vm<10>();
+    wait_vm<6>(); /* P0, H0 */
     touch_pay(pay[0]);
     touch_pay(hnext);
     hcur = hnext;
-    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], hcur, hh, lut, bdec);
+    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], hcur, hh, lut, sm.b[0] + c * 128u,
+                                 bsw);
+    wait_vm<1>(); /* A0, P1 */
+    touch_pay(pay[1]);
 
-    uint32_t s_cur = 0; /* A stage of step k; step k + 2 copies into (s_cur + 2) % 3 */
     for (uint32_t k0 = 0; k0 < nk; k0 += 4) {
-#define R9VX_M3_STEP(J)                                                                                      \
+#define R9VX_M3_STEP_DB(J)                                                                                   \
     {                                                                                                        \
         const uint32_t k = k0 + J;                                                                           \
-        lds_barrier(); /* every wave is done with B(k-1) and A stage (k-1) % 3 */                            \
-        m3_write_b(sm.b, c, hh, bdec);                                                                       \
+        lds_barrier(); /* B(k), A(k) visible; step k - 1's tile and stage are free */                        \
+        m3_dma_a(a_lds + ((k + 1) & 1u) * kM3Stage, abase, aoff, k + 1 < nk ? k + 1 : nk - 1, wave);          \
         m3_load_pay<SCHEME>(w, k + 3 < nk ? k + 3 : nk - 1, hh, pay[(J + 3) & 3]);                            \
         if (J == 1) {                                                                                        \
             const uint32_t blk = (k + 3) / 4 < nk / 4 ? (k + 3) / 4 : nk / 4 - 1;                             \
             m3_load_hdr<SCHEME>(w, blk, hnext);                                                              \
         }                                                                                                    \
-        const uint32_t s_next2 = s_cur == 0 ? 2u : s_cur - 1; /* (s_cur + 2) % 3 */                          \
-        m3_dma_a(a_lds + s_next2 * kM3Stage, abase, aoff, k + 2 < nk ? k + 2 : nk - 1, wave);                 \
-        wait_vm<m3_allowed<J>()>(); /* A(k) copied, payload (and header) of k + 1 here */                   \
-        touch_pay(pay[(J + 1) & 3]);                                                                         \
         if (J == 3) {                                                                                        \
             touch_pay(hnext);                                                                                \
             hcur = hnext;                                                                                    \
         }                                                                                                    \
-        lds_barrier(); /* every wave's A(k) copy and B(k) */                                                 \
-        m3_compute<SCHEME, (J + 1) & 3, NR, TR>(sm.a[s_cur], sm.b, lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3],  \
-                                            hcur, hh, lut, bdec);                                            \
+        m3_compute<SCHEME, (J + 1) & 3, NR, TR>(sm.a[k & 1u], sm.b[k & 1u], lane, arow0, bc0, bc1, acc,       \
+                                                pay[(J + 1) & 3], hcur, hh, lut, sm.b[(k + 1) & 1u] + c * 128u, bsw); \
         __builtin_amdgcn_sched_barrier(0);                                                                   \
-        s_cur = s_cur == 2 ? 0u : s_cur + 1;                                                                 \
+        wait_vm<(J == 1 ? 2 : 1)>(); /* A(k + 1) copied; payload k + 2 (and the header) arrived */           \
+        touch_pay(pay[(J + 2) & 3]);                                                                         \
     }
-        R9VX_M3_STEP(0)
-        R9VX_M3_STEP(1)
-        R9VX_M3_STEP(2)
-        R9VX_M3_STEP(3)
-#undef R9VX_M3_STEP
+        R9VX_M3_STEP_DB(0)
+        R9VX_M3_STEP_DB(1)
+        R9VX_M3_STEP_DB(2)
+        R9VX_M3_STEP_DB(3)
+#undef R9VX_M3_STEP_DB
     }
-    /* The clamped loads of the last steps are still in flight into registers
-     * the compiler sees as dead and LDS stages the caller may reuse: wait,
-     * and keep the registers reserved up to here. */
     wait_vm<0>();
 #pragma unroll
     for (int i = 0; i < 4; ++i) touch_pay(pay[i]);
@@ -331,6 +353,7 @@ template <int SCHEME, bool TR = false>
 __device__ __forceinline__ void m3_run(uint32_t nr, M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
                                        const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave, const uint32_t *lut,
                                        uint32_t arow0, uint32_t bc0, uint32_t bc1, r9vx_f32x16 (&acc)[4][2]) {
+
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
