@@ -540,23 +540,34 @@ static int launch_route_per(const RouteArgs &a, hipStream_t stream) {
 
 /* Device address of this device's plain-launch status word, looked up once
  * per device. */
-static uint32_t *plain_status_word() {
+/* The current device's plain status word, or nullptr with *err set. */
+static uint32_t *plain_status_word(hipError_t *err) {
     static uint32_t *words[64];
     static std::mutex mu;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess && (dev < 0 || dev >= 64)) e = hipErrorInvalidDevice;
+    if (e != hipSuccess) {
+        *err = e;
+        return nullptr;
+    }
     std::lock_guard<std::mutex> g(mu);
     if (!words[dev]) {
         void *ptr = nullptr;
-        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_route_status)) != hipSuccess) return nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_route_status));
+        if (e != hipSuccess || !ptr) {
+            *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
+            return nullptr;
+        }
         words[dev] = static_cast<uint32_t *>(ptr);
     }
     return words[dev];
 }
 
 int r9vx_launch_route(const r9vx_route_problem &p, hipStream_t stream) {
-    uint32_t *status = p.status ? p.status : plain_status_word();
-    if (!status) return (int)hipErrorInvalidSymbol;
+    hipError_t err = hipSuccess;
+    uint32_t *status = p.status ? p.status : plain_status_word(&err);
+    if (!status) return (int)err;
     RouteArgs a{p.logits, p.bias, p.ids, p.weights, status, p.t, p.e, p.k, p.scoring, p.renormalize, p.scale};
     /* registers per lane: the next power of two >= ceil(E / 64) */
     const uint32_t per = (p.e + 63) / 64;
@@ -573,8 +584,9 @@ int r9vx_read_route_status(uint32_t *status, hipStream_t stream) {
     if (rc) return rc;
     rc = (int)hipStreamSynchronize(stream);
     if (rc) return rc;
-    uint32_t *word = plain_status_word();
-    if (!word) return (int)hipErrorInvalidSymbol;
+    hipError_t err = hipSuccess;
+    uint32_t *word = plain_status_word(&err);
+    if (!word) return (int)err;
     hipLaunchKernelGGL(clear_status_kernel, dim3(1), dim3(1), 0, stream, word);
     return (int)hipGetLastError();
 }

@@ -170,9 +170,15 @@ def load():
     if _lib is None:
         if not LIB_PATH.exists():
             raise R9vxError(-100, f"{LIB_PATH} is missing: run `python -m r9v_amd.build`")
-        L = ctypes.CDLL(str(LIB_PATH))
+        try:
+            L = ctypes.CDLL(str(LIB_PATH))
+        except OSError as e:  # e.g. the HIP runtime it links is absent or lacks a symbol
+            raise R9vxError(-100, f"cannot load {LIB_PATH}: {e}") from None
         for name, argtypes, restype in EXPORTS:
-            fn = getattr(L, name)
+            try:
+                fn = getattr(L, name)
+            except AttributeError:
+                raise R9vxError(-100, f"{LIB_PATH} does not export {name}: rebuild it") from None
             fn.argtypes = argtypes
             fn.restype = restype
         _lib = L
