@@ -183,7 +183,9 @@ int r9vx_gguf_matmul_static(const r9vx_gguf *f, const char *name, r9vx_matmul_st
  * with up == NULL (the ffn_gate_up_exps form of
  * crates/r9v-models/src/generic.rs:1420), and `down` {Dff, Dm, E}.  Sets
  * e_local, dm, dff and the gate_up / down projection keys (dtype, scheme and
- * the device layout r9vx_gguf_upload / r9vx_gguf_upload_gate_up write). */
+ * the device layout the uploads write): Q4_K / IQ4_XS / IQ3_S through
+ * r9vx_gguf_upload / r9vx_gguf_upload_gate_up, Q8_0 / Q6_K (split) through
+ * r9vx_gguf_upload_split / r9vx_gguf_upload_gate_up_split. */
 int r9vx_gguf_moe_ffn_static(const r9vx_gguf *f, const char *gate, const char *up,
                              const char *down, r9vx_moe_ffn_static *st);
 /* Loads tensor `name` from the host buffer into device memory `dst` in the
@@ -216,6 +218,17 @@ int r9vx_gguf_upload_gate_up(const r9vx_gguf *gate_file, const uint8_t *gate_byt
                              uint64_t gate_len, const char *gate, const r9vx_gguf *up_file,
                              const uint8_t *up_bytes, uint64_t up_len, const char *up, void *dst,
                              uint64_t dst_bytes, r9vx_stream_t stream);
+/* The stacked w_gate_up [E, 2*Dff, Dm] of Q8_0 / Q6_K gate and up expert
+ * tensors in the split device layout: expert x's gate rows then its up rows
+ * in `body` (blocks without d) and their d values in `scales` (f16), the two
+ * arrays moe_ffn takes as w_gate_up and w_gate_up_scales (the gate/up
+ * stacking of crates/r9v-models/src/generic.rs:1420 with the split of
+ * r9vx_gguf_upload_split).  Split on the host; a non-finite d is refused
+ * before anything is copied; returns after the copies have completed. */
+int r9vx_gguf_upload_gate_up_split(const r9vx_gguf *gate_file, const uint8_t *gate_bytes, uint64_t gate_len,
+                                   const char *gate, const r9vx_gguf *up_file, const uint8_t *up_bytes,
+                                   uint64_t up_len, const char *up, void *body, uint64_t body_bytes, uint16_t *scales,
+                                   uint64_t scales_bytes, r9vx_stream_t stream);
 
 #ifdef __cplusplus
 }

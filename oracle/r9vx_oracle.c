@@ -91,6 +91,11 @@ uint32_t rxo_block_bytes(int scheme) {
 
 uint32_t rxo_block_len(int scheme) { return scheme == RXO_Q8_0 ? 32 : (rxo_block_bytes(scheme) ? 256 : 0); }
 
+/* GGUF wire bytes of one row of k weights (k a multiple of the block). */
+static uint64_t wire_row_bytes(int scheme, uint32_t k) {
+    return (uint64_t)(k / rxo_block_len(scheme)) * rxo_block_bytes(scheme);
+}
+
 /* crates/r9v-format/src/ggml.rs:973-995 (unpack_k4_scales), identical to
  * records.rs:190-206 (I4KSuperblock::from_bytes). */
 void rxo_q4k_unpack_scales(const uint8_t q[12], uint8_t sc[8], uint8_t mn[8]) {
@@ -507,8 +512,8 @@ static inline float silu_mul(float g, float u) {
 static void expert_rows(const float *x_rows, uint32_t rows, uint32_t dm, uint32_t dff,
                         int scheme_gu, const uint8_t *gu, int scheme_dn, const uint8_t *dn,
                         int h_bf16, float *out, float *wrow, float *h) {
-    uint64_t gu_row_bytes = (uint64_t)(dm / 256) * rxo_block_bytes(scheme_gu);
-    uint64_t dn_row_bytes = (uint64_t)(dff / 256) * rxo_block_bytes(scheme_dn);
+    uint64_t gu_row_bytes = wire_row_bytes(scheme_gu, dm);
+    uint64_t dn_row_bytes = wire_row_bytes(scheme_dn, dff);
     float *gate = (float *)malloc(sizeof(float) * (size_t)rows * dff);
     for (uint32_t c = 0; c < 2 * dff; ++c) {
         decode_row(scheme_gu, gu + c * gu_row_bytes, dm, wrow);
@@ -585,8 +590,8 @@ int rxo_moe_ffn(int x_dtype, const void *x, uint32_t t, uint32_t dm, uint32_t df
         free(sorted);
         return rc;
     }
-    uint64_t gu_expert = (uint64_t)2 * dff * (dm / 256) * rxo_block_bytes(scheme_gu);
-    uint64_t dn_expert = (uint64_t)dm * (dff / 256) * rxo_block_bytes(scheme_dn);
+    uint64_t gu_expert = (uint64_t)2 * dff * wire_row_bytes(scheme_gu, dm);
+    uint64_t dn_expert = (uint64_t)dm * wire_row_bytes(scheme_dn, dff);
     float *ytmp = (float *)calloc((size_t)t * dm, sizeof(float));
     float *xr = (float *)malloc(sizeof(float) * (size_t)t * dm);
     float *out = (float *)malloc(sizeof(float) * (size_t)t * dm);
@@ -706,8 +711,8 @@ int rxo_moe_ffn_full(int x_dtype, const void *x, uint32_t t, uint32_t dm, uint32
     float *out = (float *)malloc(sizeof(float) * (size_t)t * dm);
     float *wrow = (float *)malloc(sizeof(float) * (dm > dff ? dm : dff));
     uint32_t *tokens = (uint32_t *)malloc(sizeof(uint32_t) * (t + 1));
-    uint64_t gu_row_bytes = (uint64_t)(dm / 256) * rxo_block_bytes(scheme_gu);
-    uint64_t dn_row_bytes = (uint64_t)(dff / 256) * rxo_block_bytes(scheme_dn);
+    uint64_t gu_row_bytes = wire_row_bytes(scheme_gu, dm);
+    uint64_t dn_row_bytes = wire_row_bytes(scheme_dn, dff);
     for (uint32_t ex = 0; ex < e; ++ex) {
         uint32_t beg = offsets[ex], end = offsets[ex + 1];
         if (beg == end) continue;

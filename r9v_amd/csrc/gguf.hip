@@ -880,10 +880,11 @@ int r9vx_gguf_moe_ffn_static(const r9vx_gguf *f, const char *gate, const char *u
             return false;
         }
         bool ok = true;
-        if (!path_scheme(t->type) && !(gate_up && repack_type(t->type))) {
+        (void)gate_up;
+        if (!path_scheme(t->type) && !repack_type(t->type) && !split_type(t->type)) {
             pr.push_back({0, R9VX_ERR_UNSUPPORTED, "tensor \"" + t->name + "\" is " + r9vx_gguf_type_name(t->type) +
-                                                       (gate_up ? "; gate/up experts must be Q4_K (12), IQ4_XS (23) or IQ3_S (21)"
-                                                                : "; down experts must be Q4_K (12) or IQ4_XS (23)")});
+                                                       "; experts must be Q4_K (12), IQ4_XS (23), IQ3_S (21), Q8_0 (8) "
+                                                       "or Q6_K (14)"});
             ok = false;
         }
         if (t->dims.size() != 3 || t->dims[0] > UINT32_MAX || t->dims[1] > UINT32_MAX || t->dims[2] > UINT32_MAX) {
@@ -1063,6 +1064,67 @@ int r9vx_gguf_upload_gate_up(const r9vx_gguf *gate_file, const uint8_t *gate_byt
     rc = hip_rc(op, hipMemcpy2DAsync(d, 2 * slab, gdev.data(), slab, slab, experts, hipMemcpyHostToDevice, s));
     if (rc == R9VX_OK)
         rc = hip_rc(op, hipMemcpy2DAsync(d + slab, 2 * slab, udev.data(), slab, slab, experts, hipMemcpyHostToDevice, s));
+    const int sync = hip_rc(op, hipStreamSynchronize(s)); /* the host copies die with this call */
+    return rc != R9VX_OK ? rc : sync;
+}
+
+int r9vx_gguf_upload_gate_up_split(const r9vx_gguf *gate_file, const uint8_t *gate_bytes, uint64_t gate_len,
+                                   const char *gate, const r9vx_gguf *up_file, const uint8_t *up_bytes,
+                                   uint64_t up_len, const char *up, void *body, uint64_t body_bytes, uint16_t *scales,
+                                   uint64_t scales_bytes, r9vx_stream_t stream) {
+    const char *op = "gguf_upload_gate_up_split";
+    const Tensor *g, *u;
+    const uint8_t *gdata, *udata;
+    int rc = entry_range(op, gate_file, gate, gate_bytes, gate_len, &g, &gdata);
+    if (rc != R9VX_OK) return rc;
+    rc = entry_range(op, up_file, up, up_bytes, up_len, &u, &udata);
+    if (rc != R9VX_OK) return rc;
+    if (!split_type(g->type) || g->dims.size() != 3 || u->dims != g->dims || u->type != g->type)
+        return refuse(op, R9VX_ERR_INVALID,
+                      "gate \"" + g->name + "\" " + dims_text(*g) + " " + r9vx_gguf_type_name(g->type) + " and up \"" +
+                          u->name + "\" " + dims_text(*u) + " " + r9vx_gguf_type_name(u->type) +
+                          " must be stacked Q8_0 / Q6_K experts {K, rows, E} of one dims and type");
+    if (!body || !scales) return refuse(op, R9VX_ERR_NULL, "body and scales are required");
+    const TypeRow *row = type_row(g->type);
+    const uint64_t per_expert = g->dims[0] / row->block_len * g->dims[1]; /* blocks */
+    const uint64_t experts = g->dims[2], nblocks = per_expert * experts;
+    const uint32_t body_block = row->block_bytes - 2, d_off = g->type == R9VX_SCHEME_Q8_0 ? 0 : 208;
+    if (body_bytes < 2 * nblocks * body_block || scales_bytes < 2 * nblocks * 2)
+        return refuse(op, R9VX_ERR_INVALID,
+                      fmt("body holds %llu and scales %llu bytes; the stacked gate_up needs %llu and %llu",
+                          (unsigned long long)body_bytes, (unsigned long long)scales_bytes,
+                          (unsigned long long)(2 * nblocks * body_block), (unsigned long long)(4 * nblocks)));
+    /* expert x's gate blocks, then its up blocks, split on the host into the
+     * body and the d array (non-finite d refused, check_wire_f16,
+     * crates/r9v-format/src/ggml.rs:421) */
+    std::vector<uint8_t> hb;
+    std::vector<uint16_t> hs;
+    try {
+        hb.resize(2 * nblocks * body_block);
+        hs.resize(2 * nblocks);
+    } catch (const std::bad_alloc &) {
+        return refuse(op, R9VX_ERR_INVALID, "out of host memory for the split copy");
+    }
+    uint64_t bad = 0;
+    for (uint64_t x = 0; x < experts; ++x)
+        for (int half = 0; half < 2; ++half) {
+            const uint8_t *src = (half ? udata : gdata) + x * per_expert * row->block_bytes;
+            const uint64_t at = (2 * x + half) * per_expert;
+            for (uint64_t b = 0; b < per_expert; ++b) {
+                const uint8_t *blk = src + b * row->block_bytes;
+                const uint16_t d = (uint16_t)(blk[d_off] | (blk[d_off + 1] << 8));
+                bad += (d & 0x7C00u) == 0x7C00u;
+                hs[at + b] = d;
+                memcpy(&hb[(at + b) * body_block], d_off == 0 ? blk + 2 : blk, body_block);
+            }
+        }
+    if (bad)
+        return refuse(op, R9VX_ERR_INVALID,
+                      fmt("gate \"%s\" / up \"%s\": %llu block(s) carry a non-finite scale", g->name.c_str(),
+                          u->name.c_str(), (unsigned long long)bad));
+    hipStream_t s = (hipStream_t)stream;
+    rc = hip_rc(op, hipMemcpyAsync(body, hb.data(), hb.size(), hipMemcpyHostToDevice, s));
+    if (rc == R9VX_OK) rc = hip_rc(op, hipMemcpyAsync(scales, hs.data(), hs.size() * 2, hipMemcpyHostToDevice, s));
     const int sync = hip_rc(op, hipStreamSynchronize(s)); /* the host copies die with this call */
     return rc != R9VX_OK ? rc : sync;
 }

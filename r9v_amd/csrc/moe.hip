@@ -326,8 +326,11 @@ struct FfnArgs {
     float *y;
     uint8_t *ws;
     MoeLayout L;
-    uint64_t gu_row_bytes; /* bytes per gate/up weight row (Dm/256 blocks) */
-    uint64_t dn_row_bytes; /* bytes per down weight row (Dff/256 blocks) */
+    const uint16_t *s_gu;  /* split layout: f16 d rows of w_gu / w_dn (NULL otherwise) */
+    const uint16_t *s_dn;
+    uint64_t gu_row_bytes; /* device bytes per gate/up weight row (r9vx_row_bytes) */
+    uint64_t dn_row_bytes; /* device bytes per down weight row */
+    uint32_t gu_srow, dn_srow; /* f16 d values per row of s_gu / s_dn */
     uint32_t t, e, k, dm, dff, shared, p;
     /* groups: row groups per sorted position; upw: units per wave */
     uint32_t gu_lpr_log2, gu_nseg, gu_groups, gu_upw;
@@ -403,6 +406,7 @@ template <int GU>
 __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
     constexpr int kPairs = kDecPairs;
     constexpr bool kIq3 = GU == R9VX_SCHEME_IQ3_S;
+    constexpr bool kSplit = GU == R9VX_SCHEME_Q8_0 || GU == R9VX_SCHEME_Q6_K;
     __shared__ __attribute__((aligned(16))) uint32_t lut[kIq3 ? 1024 : 256];
     __shared__ uint64_t etab[R9VX_EXP2F_N];
     if constexpr (GU == R9VX_SCHEME_IQ4_XS) init_iq4_lut(lut, threadIdx.x, blockDim.x);
@@ -427,7 +431,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
     uint32_t xpos = ~0u, xseg = ~0u;
     float ag[kPairs][1], au[kPairs][1];
     Cur lc{pos0, u0 % groups, 0u}, c = lc; /* load and compute cursors */
-    using Pay = typename std::conditional<kIq3, Payload2, r9vx_u32x4>::type;
+    using Pay = typename std::conditional<kIq3 || kSplit, Payload2, r9vx_u32x4>::type;
     Pay qg[kDecSteps][kPairs], qu[kDecSteps][kPairs];
     Hdr hg[kDecSteps][kPairs], hu[kDecSteps][kPairs];
     for (uint32_t base = 0; base < nsteps; base += kDecSteps) {
@@ -437,11 +441,17 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
             const uint32_t w = lc.pos == pos0 ? 0u : 1u;
             const uint32_t ci = lc.seg * lpr + lir;
             const uint8_t *wexp = a.w_gu + (uint64_t)expert[w] * 2 * a.dff * a.gu_row_bytes;
+            const uint16_t *sexp = kSplit ? a.s_gu + (uint64_t)expert[w] * 2 * a.dff * a.gu_srow : nullptr;
 #pragma unroll
             for (int r = 0; r < kPairs; ++r) {
                 const uint32_t row = (lc.g * kPairs + r) * rpi + slot;
                 const uint32_t rr = row < a.dff ? row : a.dff - 1;
-                if constexpr (kIq3) {
+                if constexpr (kSplit) {
+                    load_chunk_split<GU>(wexp + (uint64_t)rr * a.gu_row_bytes, sexp + (uint64_t)rr * a.gu_srow, ci,
+                                         qg[s][r], hg[s][r]);
+                    load_chunk_split<GU>(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes,
+                                         sexp + (uint64_t)(a.dff + rr) * a.gu_srow, ci, qu[s][r], hu[s][r]);
+                } else if constexpr (kIq3) {
                     load_chunk_iq3s(wexp + (uint64_t)rr * a.gu_row_bytes, ci, qg[s][r], hg[s][r]);
                     load_chunk_iq3s(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes, ci, qu[s][r], hu[s][r]);
                 } else {
@@ -472,7 +482,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
                 for (int r = 0; r < kPairs; ++r) ag[r][0] = au[r][0] = 0.f;
 #pragma unroll
             for (int r = 0; r < kPairs; ++r) {
-                if constexpr (kIq3) {
+                if constexpr (kSplit) {
+                    chunk_dot_split<GU, 1>(qg[s][r], hg[s][r], ci & 7, xc, ag[r]);
+                    chunk_dot_split<GU, 1>(qu[s][r], hu[s][r], ci & 7, xc, au[r]);
+                } else if constexpr (kIq3) {
                     chunk_dot_iq3s<1>(qg[s][r], hg[s][r], ci & 7, xc, ag[r], lut);
                     chunk_dot_iq3s<1>(qu[s][r], hu[s][r], ci & 7, xc, au[r], lut);
                 } else {
@@ -506,8 +519,12 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
 template <int DN>
 __global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
     constexpr int kRows = kDecDnRows;
-    __shared__ uint32_t lut[256];
+    constexpr bool kIq3 = DN == R9VX_SCHEME_IQ3_S;
+    constexpr bool kSplit = DN == R9VX_SCHEME_Q8_0 || DN == R9VX_SCHEME_Q6_K;
+    constexpr bool kF32x = kIq3 || kSplit; /* chunk_dot_f32x against the f32 h rows */
+    __shared__ __attribute__((aligned(16))) uint32_t lut[kIq3 ? 1024 : 256];
     if constexpr (DN == R9VX_SCHEME_IQ4_XS) init_iq4_lut(lut, threadIdx.x, blockDim.x);
+    if constexpr (kIq3) build_iq3s_lut(lut, threadIdx.x, blockDim.x);
     __syncthreads(); /* the last barrier: waves run independently from here */
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t lpr = 1u << a.dn_lpr_log2, rpi = 64u >> a.dn_lpr_log2;
@@ -536,7 +553,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
     uint32_t xpos = ~0u, xseg = ~0u, rpos = ~0u;
     float acc[kRows][1];
     Cur lc{pos0, u0 % groups, 0u}, c = lc; /* load and compute cursors */
-    r9vx_u32x4 q[kDecSteps][kRows];
+    using Pay = typename std::conditional<kF32x, Payload2, r9vx_u32x4>::type;
+    Pay q[kDecSteps][kRows];
     Hdr hd[kDecSteps][kRows];
     for (uint32_t base = 0; base < nsteps; base += kDecSteps) {
         /* every weight load of the batch's steps (steps past the last repeat it) */
@@ -545,11 +563,18 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
             const uint32_t w = lc.pos == pos0 ? 0u : 1u;
             const uint32_t ci = lc.seg * lpr + lir;
             const uint8_t *wexp = a.w_dn + (uint64_t)expert[w] * a.dm * a.dn_row_bytes;
+            const uint16_t *sexp = kSplit ? a.s_dn + (uint64_t)expert[w] * a.dm * a.dn_srow : nullptr;
 #pragma unroll
             for (int r = 0; r < kRows; ++r) {
                 const uint32_t row = (lc.g * kRows + r) * rpi + slot;
                 const uint32_t rr = row < a.dm ? row : a.dm - 1;
-                load_chunk<DN>(wexp + (uint64_t)rr * a.dn_row_bytes, ci, q[s][r], hd[s][r]);
+                if constexpr (kSplit)
+                    load_chunk_split<DN>(wexp + (uint64_t)rr * a.dn_row_bytes, sexp + (uint64_t)rr * a.dn_srow, ci,
+                                         q[s][r], hd[s][r]);
+                else if constexpr (kIq3)
+                    load_chunk_iq3s(wexp + (uint64_t)rr * a.dn_row_bytes, ci, q[s][r], hd[s][r]);
+                else
+                    load_chunk<DN>(wexp + (uint64_t)rr * a.dn_row_bytes, ci, q[s][r], hd[s][r]);
             }
             if (base + s + 1 < nsteps) advance(lc, nseg, groups);
         }
@@ -615,7 +640,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
                 for (int r = 0; r < kRows; ++r) acc[r][0] = 0.f;
 #pragma unroll
             for (int r = 0; r < kRows; ++r) {
-                if constexpr (kF16) {
+                if constexpr (kF32x) {
+                    acc[r][0] += chunk_dot_f32x<DN>(q[s][r], hd[s][r], ci & 7, xc[0], lut);
+                } else if constexpr (kF16) {
                     const uint32_t qw[4] = {q[s][r].x, q[s][r].y, q[s][r].z, q[s][r].w};
                     const Hdr &hh = hd[s][r];
                     const float d = r9vx_f16_to_f32((uint16_t)(hh.v.x & 0xFFFF));
@@ -822,10 +849,12 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
     f.y = p.y;
     f.ws = p.ws;
     f.L = L;
-    f.gu_row_bytes = (uint64_t)(p.dm / 256) * (p.scheme_gu == R9VX_SCHEME_Q4_K   ? R9VX_Q4K_BYTES
-                                               : p.scheme_gu == R9VX_SCHEME_IQ3_S ? R9VX_IQ3S_DEV_BYTES
-                                                                                  : R9VX_IQ4XS_BYTES);
-    f.dn_row_bytes = (uint64_t)(p.dff / 256) * (p.scheme_dn == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : R9VX_IQ4XS_BYTES);
+    f.s_gu = p.s_gu;
+    f.s_dn = p.s_dn;
+    f.gu_row_bytes = r9vx_row_bytes(p.scheme_gu, p.dm);
+    f.dn_row_bytes = r9vx_row_bytes(p.scheme_dn, p.dff);
+    f.gu_srow = r9vx_row_scales(p.scheme_gu, p.dm);
+    f.dn_srow = r9vx_row_scales(p.scheme_dn, p.dff);
     f.t = p.t;
     f.e = p.e;
     f.k = p.k;
@@ -853,16 +882,21 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
         return dim3((waves + kDecWaves - 1) / kDecWaves);
     };
     const dim3 block(kDecWaves * 64);
-    if (p.scheme_gu == R9VX_SCHEME_IQ3_S)
-        hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_IQ3_S>, grid_for(f.gu_groups, f.gu_upw), block, 0, s, f);
-    else if (p.scheme_gu == R9VX_SCHEME_IQ4_XS)
-        hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_IQ4_XS>, grid_for(f.gu_groups, f.gu_upw), block, 0, s, f);
-    else
-        hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_Q4_K>, grid_for(f.gu_groups, f.gu_upw), block, 0, s, f);
-    if (p.scheme_dn == R9VX_SCHEME_Q4_K)
-        hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_Q4_K>, grid_for(f.dn_groups, f.dn_upw), block, 0, s, f);
-    else
-        hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_IQ4_XS>, grid_for(f.dn_groups, f.dn_upw), block, 0, s, f);
+    const dim3 ggu = grid_for(f.gu_groups, f.gu_upw), gdn = grid_for(f.dn_groups, f.dn_upw);
+    switch (p.scheme_gu) {
+    case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_IQ3_S>, ggu, block, 0, s, f); break;
+    case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_IQ4_XS>, ggu, block, 0, s, f); break;
+    case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_Q8_0>, ggu, block, 0, s, f); break;
+    case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_Q6_K>, ggu, block, 0, s, f); break;
+    default: hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_Q4_K>, ggu, block, 0, s, f); break;
+    }
+    switch (p.scheme_dn) {
+    case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_IQ3_S>, gdn, block, 0, s, f); break;
+    case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_IQ4_XS>, gdn, block, 0, s, f); break;
+    case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_Q8_0>, gdn, block, 0, s, f); break;
+    case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_Q6_K>, gdn, block, 0, s, f); break;
+    default: hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_Q4_K>, gdn, block, 0, s, f); break;
+    }
     return (int)hipGetLastError();
 }
 

@@ -41,9 +41,12 @@ struct GroupedArgs {
     const float *xscale;
     const uint8_t *w_gu;
     const uint8_t *w_dn;
+    const uint16_t *s_gu; /* split layout: f16 d rows of w_gu / w_dn (NULL otherwise) */
+    const uint16_t *s_dn;
     uint8_t *ws;
     MoeLayout L;
     uint64_t gu_row_bytes, dn_row_bytes;
+    uint32_t gu_srow, dn_srow; /* f16 d values per weight row */
     uint32_t t, e, k, dm, dff, p, shared;
 };
 
@@ -138,7 +141,8 @@ constexpr int kStage = 32 * kMT * 128;       /* 16 KiB per A stage */
     __shared__ __attribute__((aligned(16))) float lutf[512];          \
     uint8_t *const stages[4] = {st0, st1, st2, st3};
 
-/* IQ3_S gate/up experts: the LDS-decoded main loop of r9vx_mma.h (a 128 x
+/* Gate/up experts the r9vx_mma3.h loop does not decode (IQ3_S, and Q8_0 /
+ * Q6_K in the split layout): the LDS-decoded main loop of r9vx_mma.h (a 128 x
  * 256 tile; thread t decodes weight row t of the tile into LDS: threads
  * 0..127 the gate rows j0..j0+127, threads 128..255 the up rows of the same
  * columns, so tile column c pairs with column c + 128), with the activations
@@ -168,10 +172,11 @@ __global__ __launch_bounds__(256, 2) void moe_gu_lds_kernel(GroupedArgs a) {
         const uint32_t r = as.row0 + 32 * i;
         as.row[i] = a.x16 + (uint64_t)row_token(a, expert, pos0 + (r < rows ? r : 0)) * a.dm + 8 * as.chunk;
     }
-    const uint64_t wr = tid < 128 ? j0 + tid : (uint64_t)a.dff + j0 + (tid - 128);
-    const uint8_t *wrow = a.w_gu + ((uint64_t)expert * 2 * a.dff + wr) * a.gu_row_bytes;
+    const uint64_t wr = (uint64_t)expert * 2 * a.dff + (tid < 128 ? j0 + tid : (uint64_t)a.dff + j0 + (tid - 128));
+    const uint8_t *wrow = a.w_gu + wr * a.gu_row_bytes;
+    const uint16_t *srow = a.s_gu ? a.s_gu + wr * a.gu_srow : nullptr;
     r9vx_f32x16 acc[kBM / 32][2];
-    mma_mainloop<GU, kBM, 1>(lds, as, wrow, a.dm / kTileK, acc);
+    mma_mainloop<GU, kBM, 1>(lds, as, wrow, a.dm / kTileK, acc, srow);
 
     constexpr uint32_t kSRow = 260;
     float *stage = reinterpret_cast<float *>(lds);
@@ -208,6 +213,16 @@ __global__ __launch_bounds__(256, 2) void moe_gu_lds_kernel(GroupedArgs a) {
  * epilogue), then lane l writes group l % 8 of K step l / 8 (+ 8 per pass)
  * as 8 fp16 in the down scheme's group order, scaled by 2^-e with e =
  * row_shift(max|h|). */
+/* K position of element i of group q in a 64-wide step of the h16 rows: the
+ * group order of the r9vx_mma3.h schemes, natural order for the others. */
+template <int DN>
+__device__ __forceinline__ uint32_t h_group_k(uint32_t q, uint32_t i) {
+    if constexpr (DN == R9VX_SCHEME_Q4_K || DN == R9VX_SCHEME_IQ4_XS)
+        return group_k<DN>(q, i);
+    else
+        return 8 * q + i;
+}
+
 template <int DN>
 __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t nrows) {
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -227,11 +242,98 @@ __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t n
     _Float16 *orow = a.h16 + (uint64_t)row * a.dff;
     for (uint32_t c = lane; c < a.dff / 8; c += 64) {
         const uint32_t base = (c >> 3) * 64, q = c & 7;
-        const r9vx_f32x4 lo = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + group_k<DN>(q, 0));
-        const r9vx_f32x4 hi = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + group_k<DN>(q, 4));
+        const r9vx_f32x4 lo = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + h_group_k<DN>(q, 0));
+        const r9vx_f32x4 hi = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + h_group_k<DN>(q, 4));
         *reinterpret_cast<r9vx_u32x4 *>(orow + 8 * c) =
             r9vx_u32x4{pack_h2(lo.x * inv, lo.y * inv), pack_h2(lo.z * inv, lo.w * inv), pack_h2(hi.x * inv, hi.y * inv),
                        pack_h2(hi.z * inv, hi.w * inv)};
+    }
+}
+
+/* ---------------------------------------------------------------- down, LDS-decoded */
+
+/* Down experts the r9vx_mma3.h loop does not decode (IQ3_S, and Q8_0 / Q6_K
+ * in the split layout): the LDS-decoded main loop of r9vx_mma.h over a
+ * 128-row tile of h16 rows (natural K order) and output columns n0 .. n0 +
+ * 255 (thread t decodes weight row n0 + t).  The accumulators pass through
+ * a 32 x 256 f32 LDS stage, 32 rows at a time; thread t then owns 32
+ * consecutive columns of row t / 8 and writes them as the fp16 rows and
+ * per-(row, 64-column) power-of-two scales the grouped combine reads (the
+ * block's max: this thread's and its neighbour's). */
+template <int DN>
+__global__ __launch_bounds__(256, 2) void moe_dn_lds_kernel(GroupedArgs a) {
+    using S = MmaShape<kBM, 1>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
+    __shared__ float rowsc[kBM]; /* 2^e that undoes each h row's fp16 scale */
+    const uint32_t *status = ws_u32(a, a.L.status);
+    uint32_t tix, nt;
+    xcd_tile(a.dm / 256, tix, nt);
+    if (status[0] != 0u || tix >= status[3]) return;
+    const r9vx_u32x4 tile = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles)[tix];
+    const uint32_t pos0 = tile.y, rows = tile.z, expert = tile.x;
+    const uint32_t n0 = nt * 256;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid < kBM)
+        rowsc[tid] = tid < rows ? ldexpf(1.0f, row_shift(__builtin_bit_cast(float, ws_u32(a, a.L.hmax)[pos0 + tid])))
+                                : 0.f;
+    AF16Rows<kBM> as;
+    as.chunk = tid & 7;
+    as.row0 = tid >> 3;
+#pragma unroll
+    for (int i = 0; i < (int)kBM / 32; ++i) {
+        const uint32_t r = as.row0 + 32 * i;
+        as.row[i] = a.h16 + (uint64_t)(pos0 + (r < rows ? r : 0)) * a.dff + 8 * as.chunk;
+    }
+    const uint64_t wr = (uint64_t)expert * a.dm + n0 + tid;
+    const uint8_t *wrow = a.w_dn + wr * a.dn_row_bytes;
+    const uint16_t *srow = a.s_dn ? a.s_dn + wr * a.dn_srow : nullptr;
+    r9vx_f32x16 acc[kBM / 32][2];
+    mma_mainloop<DN, kBM, 1>(lds, as, wrow, a.dff / kTileK, acc, srow);
+
+    constexpr uint32_t kSRow = 260;
+    float *stage = reinterpret_cast<float *>(lds);
+    const uint64_t nrows_all = (uint64_t)a.p + (uint64_t)a.shared * a.t;
+    _Float16 *o16 = reinterpret_cast<_Float16 *>(a.ws + a.L.o);
+    float *oscale = reinterpret_cast<float *>(a.ws + a.L.o + r9vx_moe_oscale_offset(nrows_all, a.dm));
+    const uint32_t rl = tid >> 3, c0 = 32 * (tid & 7), nblk = a.dm / 64;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < (int)kBM / 32; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) stage[acc_row(0, r, lane) * kSRow + acc_col(wave, j, lane)] = acc[i][j][r];
+        __syncthreads();
+        const uint32_t row = 32 * i + rl;
+        const float sc = row < rows ? rowsc[row] : 0.f;
+        float v[32];
+        float m = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const r9vx_f32x4 q = *reinterpret_cast<const r9vx_f32x4 *>(stage + rl * kSRow + c0 + 4 * c);
+            v[4 * c] = q.x * sc;
+            v[4 * c + 1] = q.y * sc;
+            v[4 * c + 2] = q.z * sc;
+            v[4 * c + 3] = q.w * sc;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) m = fmaxf(m, fabsf(v[4 * c + u]));
+        }
+        m = fmaxf(m, __shfl_xor(m, 1, 64)); /* the 64-column block: threads 2b, 2b + 1 */
+        int e = 0;
+        (void)frexpf(m, &e); /* m = f 2^e, f in [0.5, 1) */
+        if (row < rows) {
+            const float f = ldexpf(1.0f, 15 - e);
+            _Float16 *orow = o16 + (uint64_t)(pos0 + row) * a.dm + n0 + c0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                *reinterpret_cast<r9vx_u32x4 *>(orow + 8 * c) =
+                    r9vx_u32x4{pack_h2h((_Float16)(v[8 * c] * f), (_Float16)(v[8 * c + 1] * f)),
+                               pack_h2h((_Float16)(v[8 * c + 2] * f), (_Float16)(v[8 * c + 3] * f)),
+                               pack_h2h((_Float16)(v[8 * c + 4] * f), (_Float16)(v[8 * c + 5] * f)),
+                               pack_h2h((_Float16)(v[8 * c + 6] * f), (_Float16)(v[8 * c + 7] * f))};
+            if ((tid & 1) == 0) oscale[(uint64_t)(pos0 + row) * nblk + (n0 + c0) / 64] = ldexpf(1.0f, e - 15);
+        }
+        __syncthreads();
     }
 }
 
@@ -374,12 +476,14 @@ static GroupedArgs grouped_args(const r9vx_moe_problem &p, const MoeLayout &L) {
     a.xscale = reinterpret_cast<const float *>(p.ws + L.xscale);
     a.w_gu = p.w_gu;
     a.w_dn = p.w_dn;
+    a.s_gu = p.s_gu;
+    a.s_dn = p.s_dn;
     a.ws = p.ws;
     a.L = L;
-    a.gu_row_bytes = (uint64_t)(p.dm / 256) * (p.scheme_gu == R9VX_SCHEME_Q4_K   ? R9VX_Q4K_BYTES
-                                               : p.scheme_gu == R9VX_SCHEME_IQ3_S ? R9VX_IQ3S_DEV_BYTES
-                                                                                  : R9VX_IQ4XS_BYTES);
-    a.dn_row_bytes = (uint64_t)(p.dff / 256) * (p.scheme_dn == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : R9VX_IQ4XS_BYTES);
+    a.gu_row_bytes = r9vx_row_bytes(p.scheme_gu, p.dm);
+    a.dn_row_bytes = r9vx_row_bytes(p.scheme_dn, p.dff);
+    a.gu_srow = r9vx_row_scales(p.scheme_gu, p.dm);
+    a.dn_srow = r9vx_row_scales(p.scheme_dn, p.dff);
     a.t = p.t;
     a.e = p.e;
     a.k = p.k;
@@ -411,27 +515,34 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
     const uint32_t max_tiles3 = (a.p + kMoeTileM3 - 1) / kMoeTileM3 + (a.p < p.e ? a.p : p.e) +
                                 (p.shared ? p.shared * ((p.t + kMoeTileM3 - 1) / kMoeTileM3) : 0);
     const uint32_t tiles8 = (max_tiles + 7) / 8 * 8, tiles3_8 = (max_tiles3 + 7) / 8 * 8; /* xcd_tile's grids */
-    const dim3 ggu(tiles8 * (p.dff / 128)), ggu3(tiles3_8 * (p.dff / 128)), gdn3(tiles3_8 * (p.dm / 256));
+    const dim3 ggu(tiles8 * (p.dff / 128)), ggu3(tiles3_8 * (p.dff / 128)), gdn(tiles8 * (p.dm / 256)),
+        gdn3(tiles3_8 * (p.dm / 256));
     if (part == 0 || part == 1) {
-        if (p.scheme_gu == R9VX_SCHEME_IQ3_S)
-            hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_IQ3_S>, ggu, dim3(256), 0, s, a);
-        else if (p.scheme_gu == R9VX_SCHEME_IQ4_XS)
-            hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_IQ4_XS>, ggu3, dim3(512), 0, s, a);
-        else
-            hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q4_K>, ggu3, dim3(512), 0, s, a);
+        switch (p.scheme_gu) {
+        case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_IQ4_XS>, ggu3, dim3(512), 0, s, a); break;
+        case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q4_K>, ggu3, dim3(512), 0, s, a); break;
+        case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_IQ3_S>, ggu, dim3(256), 0, s, a); break;
+        case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_Q8_0>, ggu, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_Q6_K>, ggu, dim3(256), 0, s, a); break;
+        }
     }
     const uint32_t nrows = a.p + p.shared * p.t;
+    const dim3 gh((nrows + 3) / 4);
     if (part == 0) {
-        if (p.scheme_dn == R9VX_SCHEME_Q4_K)
-            hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3((nrows + 3) / 4), dim3(256), 0, s, a, nrows);
-        else
-            hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3((nrows + 3) / 4), dim3(256), 0, s, a, nrows);
+        switch (p.scheme_dn) {
+        case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q4_K>, gh, dim3(256), 0, s, a, nrows); break;
+        case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, gh, dim3(256), 0, s, a, nrows); break;
+        default: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q8_0>, gh, dim3(256), 0, s, a, nrows); break; /* natural */
+        }
     }
     if (part == 0 || part == 2) {
-        if (p.scheme_dn == R9VX_SCHEME_Q4_K)
-            hipLaunchKernelGGL(moe_dn_m3_kernel<R9VX_SCHEME_Q4_K>, gdn3, dim3(512), 0, s, a);
-        else
-            hipLaunchKernelGGL(moe_dn_m3_kernel<R9VX_SCHEME_IQ4_XS>, gdn3, dim3(512), 0, s, a);
+        switch (p.scheme_dn) {
+        case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL(moe_dn_m3_kernel<R9VX_SCHEME_Q4_K>, gdn3, dim3(512), 0, s, a); break;
+        case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(moe_dn_m3_kernel<R9VX_SCHEME_IQ4_XS>, gdn3, dim3(512), 0, s, a); break;
+        case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_IQ3_S>, gdn, dim3(256), 0, s, a); break;
+        case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_Q8_0>, gdn, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_Q6_K>, gdn, dim3(256), 0, s, a); break;
+        }
     }
     return (int)hipGetLastError();
 }

@@ -106,13 +106,9 @@ void check_weight_keys(const char *what, uint32_t scheme, uint32_t dtype, uint32
                scheme_dtype(scheme));
 }
 
-/* Bytes of one weight row as the kernels read it. */
-uint64_t device_row_bytes(uint32_t s, uint32_t k) {
-    if (s == R9VX_SCHEME_Q8_0) return k;
-    if (s == R9VX_SCHEME_Q6_K) return (uint64_t)(k / 256) * R9VX_Q6K_BODY;
-    if (s == R9VX_SCHEME_IQ3_S) return (uint64_t)(k / 256) * R9VX_IQ3S_DEV_BYTES;
-    return (uint64_t)(k / 256) * block_bytes(s);
-}
+/* Bytes of one weight row as the kernels read it (the split layout's body;
+ * its d values add r9vx_row_scales f16 per row). */
+uint64_t device_row_bytes(uint32_t s, uint32_t k) { return r9vx_row_bytes(s, k); }
 
 }  // namespace
 
@@ -507,12 +503,14 @@ static void check_ffn_static(const r9vx_moe_ffn_static *st, Problems &pr) {
     if (st->k_topk == 0 || st->k_topk > kMoeMaxK) pr.add(R9VX_ERR_INVALID, "K=%u must be in 1..32", st->k_topk);
     if (st->dm == 0 || st->dm % 256) pr.add(R9VX_ERR_INVALID, "Dm=%u must be a positive multiple of 256", st->dm);
     if (st->dff == 0 || st->dff % 256) pr.add(R9VX_ERR_INVALID, "Dff=%u must be a positive multiple of 256", st->dff);
-    if (!known_scheme(st->gate_up.scheme) && !packed_scheme(st->gate_up.scheme))
-        pr.add(R9VX_ERR_UNSUPPORTED, "gate_up scheme %u: Q4_K (12), IQ4_XS (23) or IQ3_S (21)", st->gate_up.scheme);
+    if (!matmul_scheme(st->gate_up.scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "gate_up scheme %u: Q4_K (12), IQ4_XS (23), IQ3_S (21), Q8_0 (8) or Q6_K (14)",
+               st->gate_up.scheme);
     else
         check_weight_keys("gate_up", st->gate_up.scheme, st->gate_up.dtype, st->gate_up.layout, pr);
-    if (!known_scheme(st->down.scheme))
-        pr.add(R9VX_ERR_UNSUPPORTED, "down scheme %u: Q4_K (12) or IQ4_XS (23)", st->down.scheme);
+    if (!matmul_scheme(st->down.scheme))
+        pr.add(R9VX_ERR_UNSUPPORTED, "down scheme %u: Q4_K (12), IQ4_XS (23), IQ3_S (21), Q8_0 (8) or Q6_K (14)",
+               st->down.scheme);
     else
         check_weight_keys("down", st->down.scheme, st->down.dtype, st->down.layout, pr);
     if (st->act_scheme != R9VX_ACT_SCHEME_NONE)
@@ -528,8 +526,8 @@ static void check_ffn_static(const r9vx_moe_ffn_static *st, Problems &pr) {
      * expert's weights with 32-bit byte offsets */
     const uint64_t rows = (uint64_t)st->t_bucket * (st->k_topk + st->shared_experts);
     if (2ull * st->t_bucket * st->dm >= (1ull << 32) || 2ull * rows * st->dff >= (1ull << 32) ||
-        2ull * st->dff * device_row_bytes(R9VX_SCHEME_Q4_K, st->dm) >= (1ull << 32) ||
-        (uint64_t)st->dm * device_row_bytes(R9VX_SCHEME_Q4_K, st->dff) >= (1ull << 32))
+        2ull * st->dff * device_row_bytes(st->gate_up.scheme, st->dm) >= (1ull << 32) ||
+        (uint64_t)st->dm * device_row_bytes(st->down.scheme, st->dff) >= (1ull << 32))
         pr.add(R9VX_ERR_UNSUPPORTED, "t_bucket=%u, Dm=%u, Dff=%u: staged operands or one expert exceed 4 GiB",
                st->t_bucket, st->dm, st->dff);
 }
@@ -541,8 +539,8 @@ size_t r9vx_moe_ffn_workspace_bytes(const r9vx_moe_ffn_static *st) {
 
 uint64_t r9vx_moe_ffn_expert_bytes(const r9vx_moe_ffn_static *st) {
     if (!st) return 0;
-    return 2ull * st->dff * device_row_bytes(st->gate_up.scheme, st->dm) +
-           (uint64_t)st->dm * device_row_bytes(st->down.scheme, st->dff);
+    return 2ull * st->dff * (device_row_bytes(st->gate_up.scheme, st->dm) + 2ull * r9vx_row_scales(st->gate_up.scheme, st->dm)) +
+           (uint64_t)st->dm * (device_row_bytes(st->down.scheme, st->dff) + 2ull * r9vx_row_scales(st->down.scheme, st->dff));
 }
 
 uint64_t r9vx_moe_ffn_static_bytes(const r9vx_moe_ffn_static *st, uint32_t t) {
@@ -565,12 +563,28 @@ static void ffn_checks(const r9vx_moe_ffn_static *st, const uint32_t *ids, uint3
     if (!ids) pr.add(R9VX_ERR_NULL, "expert_ids is NULL");
 }
 
-/* The operand checks of a moe_ffn launch, workspace aside. */
-static void ffn_arg_checks(const r9vx_moe_ffn_args *a, Problems &pr) {
+/* The operand checks of a moe_ffn launch, workspace aside.  The split
+ * layout (Q8_0 / Q6_K) carries its d values in the scale array of its
+ * projection; the other layouts carry their scales inline. */
+static void ffn_arg_checks(const r9vx_moe_ffn_static *st, const r9vx_moe_ffn_args *a, Problems &pr) {
     if (!a->x || !a->weights || !a->w_gate_up || !a->w_down || !a->y)
         pr.add(R9VX_ERR_NULL, "x, weights, w_gate_up, w_down and y are required");
-    if (a->w_gate_up_scales || a->w_down_scales)
-        pr.add(R9VX_ERR_UNSUPPORTED, "separate scale carriers must be NULL: GGUF blocks carry inline scales");
+    if (st) {
+        const bool sg = split_scheme(st->gate_up.scheme), sd = split_scheme(st->down.scheme);
+        if (sg != (a->w_gate_up_scales != nullptr))
+            pr.add(sg ? R9VX_ERR_NULL : R9VX_ERR_UNSUPPORTED,
+                   sg ? "w_gate_up_scales is required: scheme %u is read in the split layout (body + f16 d array)"
+                      : "w_gate_up_scales must be NULL: scheme %u blocks carry their scales inline",
+                   st->gate_up.scheme);
+        if (sd != (a->w_down_scales != nullptr))
+            pr.add(sd ? R9VX_ERR_NULL : R9VX_ERR_UNSUPPORTED,
+                   sd ? "w_down_scales is required: scheme %u is read in the split layout (body + f16 d array)"
+                      : "w_down_scales must be NULL: scheme %u blocks carry their scales inline",
+                   st->down.scheme);
+    }
+    if ((a->w_gate_up_scales && ((uintptr_t)a->w_gate_up_scales & 3u)) ||
+        (a->w_down_scales && ((uintptr_t)a->w_down_scales & 3u)))
+        pr.add(R9VX_ERR_ALIGN, "scale arrays must be 4-byte aligned");
     if ((a->x && !aligned16(a->x)) || (a->y && !aligned16(a->y)) || (a->w_gate_up && !aligned16(a->w_gate_up)) ||
         (a->w_down && !aligned16(a->w_down)))
         pr.add(R9VX_ERR_ALIGN, "x, y and weights must be 16-byte aligned");
@@ -591,6 +605,8 @@ static r9vx_moe_problem ffn_problem(const r9vx_moe_ffn_static *st, const r9vx_mo
     p.weights = a->weights;
     p.w_gu = reinterpret_cast<const uint8_t *>(a->w_gate_up);
     p.w_dn = reinterpret_cast<const uint8_t *>(a->w_down);
+    p.s_gu = reinterpret_cast<const uint16_t *>(a->w_gate_up_scales);
+    p.s_dn = reinterpret_cast<const uint16_t *>(a->w_down_scales);
     p.y = reinterpret_cast<float *>(a->y);
     p.ws = a->sort_workspace;
     p.t = a->t;
@@ -612,7 +628,7 @@ int r9vx_moe_ffn_launch(const r9vx_moe_ffn_static *st, const r9vx_moe_ffn_args *
         pr.add(R9VX_ERR_NULL, "static and args must be non-NULL");
         return pr.finish("moe_ffn");
     }
-    ffn_arg_checks(a, pr);
+    ffn_arg_checks(st, a, pr);
     int rc = ffn_common("moe_ffn", st, a->expert_ids, a->t, a->sort_workspace, pr);
     if (rc) return rc;
     r9vx_moe_problem p = ffn_problem(st, a);
@@ -685,7 +701,7 @@ int r9vx_moe_ffn_launch_noalloc(const r9vx_moe_ffn_static *st, const r9vx_moe_ff
         pr.add(R9VX_ERR_NULL, "static and args must be non-NULL");
         return pr.finish("moe_ffn_noalloc");
     }
-    ffn_arg_checks(a, pr);
+    ffn_arg_checks(st, a, pr);
     ffn_checks(st, a->expert_ids, a->t, pr);
     if (a->sort_workspace)
         pr.add(R9VX_ERR_INVALID, "sort_workspace must be NULL: this launch uses the library's own scratch");

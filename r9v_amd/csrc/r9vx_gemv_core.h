@@ -424,6 +424,72 @@ __device__ __forceinline__ void chunk_dot_iq3s(const Payload2 &pl, const Hdr &h,
     }
 }
 
+/* ---- f32 activations against Q8_0 / Q6_K (split) and IQ3_S chunks ----------
+ *
+ * acc += the chunk's dot product with f32 activations (XChunk<SCHEME, true>:
+ * lo(i) the K position of the chunk's first 16 weights, hi(i) of its last
+ * 16), every weight taken as its exact value before the multiply: Q8_0
+ * d q, Q6_K d sc (q - 32), IQ3_S d (1 + 2 s) (sign grid) -- the laws of
+ * chunk_dot_split and chunk_dot_iq3s, kept in f32 for activations that are
+ * not bf16 (the MoE down projection's SwiGLU rows). */
+template <int SCHEME>
+__device__ __forceinline__ float chunk_dot_f32x(const Payload2 &pl, const Hdr &h, uint32_t c,
+                                                const XChunk<SCHEME, true> &xc, const uint32_t *lut) {
+    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+        const float d = r9vx_f16_to_f32((uint16_t)h.e);
+        const uint32_t q[8] = {pl.a.x, pl.a.y, pl.a.z, pl.a.w, pl.b.x, pl.b.y, pl.b.z, pl.b.w};
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s = fmaf((float)(int8_t)((q[i >> 2] >> (8 * (i & 3))) & 0xFF), xc.lo(i), s);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s = fmaf((float)(int8_t)((q[4 + (i >> 2)] >> (8 * (i & 3))) & 0xFF), xc.hi(i), s);
+        return d * s;
+    } else if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
+        const float d = r9vx_f16_to_f32((uint16_t)h.e);
+        const uint32_t cc = c & 3, hsel = c >> 2;
+        const uint32_t j0 = 8 * hsel + cc, j1 = j0 + 4;
+        const uint32_t sv[4] = {h.v.x, h.v.y, h.v.z, h.v.w};
+        const float dl0 = d * (float)(int8_t)((sv[j0 >> 2] >> (8 * (j0 & 3))) & 0xFF);
+        const float dl1 = d * (float)(int8_t)((sv[j1 >> 2] >> (8 * (j1 & 3))) & 0xFF);
+        const uint32_t pair_lo = 2 * (cc >> 1), pair_hi = pair_lo + 4;
+        const uint32_t ql[4] = {pl.a.x, pl.a.y, pl.a.z, pl.a.w};
+        const uint32_t qh[4] = {pl.b.x, pl.b.y, pl.b.z, pl.b.w};
+        float slo = 0.f, shi = 0.f;
+#pragma unroll
+        for (int dw = 0; dw < 4; ++dw) {
+            const uint32_t lo6 = (ql[dw] & 0x0F0F0F0Fu) | (((qh[dw] >> pair_lo) & 0x03030303u) << 4);
+            const uint32_t hi6 = ((ql[dw] >> 4) & 0x0F0F0F0Fu) | (((qh[dw] >> pair_hi) & 0x03030303u) << 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                slo = fmaf((float)((int)((lo6 >> (8 * i)) & 0xFF) - 32), xc.lo(4 * dw + i), slo);
+                shi = fmaf((float)((int)((hi6 >> (8 * i)) & 0xFF) - 32), xc.hi(4 * dw + i), shi);
+            }
+        }
+        return dl0 * slo + dl1 * shi;
+    } else {
+        const uint32_t qh = ((c < 4 ? h.v.x : h.v.y) >> (8 * (c & 3))) & 0xFF;
+        const uint32_t sc = (h.v.z >> (4 * c)) & 0xF;
+        const float db = r9vx_f16_to_f32((uint16_t)(h.v.w & 0xFFFF)) * (1.0f + 2.0f * (float)sc);
+        const uint32_t sg = pl.a.z;
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t idx = (((i < 4 ? pl.a.x : pl.a.y) >> (8 * (i & 3))) & 0xFF) | (((qh >> i) & 1u) << 8);
+            const r9vx_u32x2 e = *reinterpret_cast<const r9vx_u32x2 *>(lut + 2 * idx);
+            const uint32_t nib = sg >> (4 * i);
+            /* weights 4i .. 4i + 3 of the 32: bf16 grid values, sign bits of nib */
+            const uint32_t w2[4] = {e.x << 16, e.x & 0xFFFF0000u, e.y << 16, e.y & 0xFFFF0000u};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float w = __builtin_bit_cast(float, w2[v] ^ (((nib >> v) & 1u) << 31));
+                const int pos = 4 * i + v;
+                s = fmaf(w, pos < 16 ? xc.lo(pos) : xc.hi(pos - 16), s);
+            }
+        }
+        return db * s;
+    }
+}
+
 /* ---- cross-lane sums of per-lane partials --------------------------------
  *
  * A row's partial sums sit in WIDTH consecutive lanes (an aligned group of 8,

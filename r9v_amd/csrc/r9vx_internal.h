@@ -121,12 +121,31 @@ int r9vx_launch_route_hidden(const r9vx_route_hidden_problem &p, hipStream_t str
 int r9vx_launch_router_repack(const float *w, uint32_t e, uint32_t dm, float *out, hipStream_t stream);
 int r9vx_read_route_status(uint32_t *status, hipStream_t stream);
 
+/* Device-layout bytes of one weight row of k weights: GGUF blocks (Q4_K,
+ * IQ4_XS), 112-byte IQ3_S blocks, or the body of the split layout (Q8_0 int8
+ * quants, Q6_K blocks without d); and the f16 d values per row that the
+ * split layout keeps in its separate scale array (0 for the others). */
+__host__ __device__ inline uint64_t r9vx_row_bytes(uint32_t scheme, uint32_t k) {
+    switch (scheme) {
+    case R9VX_SCHEME_Q8_0: return k;
+    case R9VX_SCHEME_Q6_K: return (uint64_t)(k / 256) * R9VX_Q6K_BODY;
+    case R9VX_SCHEME_IQ3_S: return (uint64_t)(k / 256) * R9VX_IQ3S_DEV_BYTES;
+    case R9VX_SCHEME_Q4_K: return (uint64_t)(k / 256) * R9VX_Q4K_BYTES;
+    default: return (uint64_t)(k / 256) * R9VX_IQ4XS_BYTES;
+    }
+}
+__host__ __device__ inline uint32_t r9vx_row_scales(uint32_t scheme, uint32_t k) {
+    return scheme == R9VX_SCHEME_Q8_0 ? k / 32 : scheme == R9VX_SCHEME_Q6_K ? k / 256 : 0u;
+}
+
 struct r9vx_moe_problem {
     const uint16_t *x; /* bf16 [t, dm] */
     const uint32_t *ids;
     const float *weights;
     const uint8_t *w_gu;
     const uint8_t *w_dn;
+    const uint16_t *s_gu; /* split layout (Q8_0 / Q6_K): f16 d rows of w_gu / w_dn, else NULL */
+    const uint16_t *s_dn;
     float *y;
     uint8_t *ws;
     uint32_t t, e, k, dm, dff, shared, t_bucket;

@@ -151,6 +151,8 @@ EXPORTS = [
     ("r9vx_gguf_upload_split", [_P, _P, _U64, ctypes.c_char_p, _P, _U64, _P, _U64, _P], ctypes.c_int),
     ("r9vx_gguf_upload_gate_up", [_P, _P, _U64, ctypes.c_char_p, _P, _P, _U64, ctypes.c_char_p,
                                   _P, _U64, _P], ctypes.c_int),
+    ("r9vx_gguf_upload_gate_up_split", [_P, _P, _U64, ctypes.c_char_p, _P, _P, _U64, ctypes.c_char_p,
+                                        _P, _U64, _P, _U64, _P], ctypes.c_int),
 ]
 
 _lib = None
@@ -404,8 +406,13 @@ def ffn_workspace_bytes(st: MoeFfnStatic) -> int:
 
 
 def moe_ffn(x, ids, weights, w_gate_up, w_down, e, dff, shared=0, gate_up_scheme=IQ4_XS,
-            down_scheme=Q4_K, y=None, workspace=None, t_bucket=None, stream=None):
-    torch = _need_gpu(x, ids, weights, w_gate_up, w_down, y, workspace)
+            down_scheme=Q4_K, y=None, workspace=None, t_bucket=None, stream=None, w_gate_up_scales=None,
+            w_down_scales=None):
+    """y = moe_ffn(x, ids, weights): gate/up and down experts in the device
+    layout of their schemes (GGUF blocks; IQ3_S 112-byte blocks and Q8_0 /
+    Q6_K split bodies as repack() returns them, the split d arrays passed as
+    the *_scales tensors)."""
+    torch = _need_gpu(x, ids, weights, w_gate_up, w_down, y, workspace, w_gate_up_scales, w_down_scales)
     t, dm = x.shape
     k = ids.shape[1]
     st = ffn_static(t_bucket or max(t, 1), e, k, dm, dff, shared, gate_up_scheme, down_scheme)
@@ -413,8 +420,8 @@ def moe_ffn(x, ids, weights, w_gate_up, w_down, e, dff, shared=0, gate_up_scheme
         workspace = torch.empty(ffn_workspace_bytes(st), dtype=torch.uint8, device=x.device)
     if y is None:
         y = torch.empty((t, dm), dtype=torch.float32, device=x.device)
-    args = MoeFfnArgs(_ptr(x), _ptr(ids), _ptr(weights), _ptr(w_gate_up), None, _ptr(w_down), None,
-                      _ptr(y), _ptr(workspace), t, 0)
+    args = MoeFfnArgs(_ptr(x), _ptr(ids), _ptr(weights), _ptr(w_gate_up), _ptr(w_gate_up_scales), _ptr(w_down),
+                      _ptr(w_down_scales), _ptr(y), _ptr(workspace), t, 0)
     _check(load().r9vx_moe_ffn_launch(ctypes.byref(st), ctypes.byref(args), _stream(torch, stream)))
     return y, workspace, st
 

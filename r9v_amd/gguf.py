@@ -390,6 +390,29 @@ def upload_gate_up(gate_file: GgufFile, gate_data, gate: str, up_file: GgufFile,
     return out
 
 
+def upload_gate_up_split(gate_file: GgufFile, gate_data, gate: str, up_file: GgufFile, up_data, up: str,
+                         stream=None):
+    """Q8_0 / Q6_K gate and up expert tensors stacked into the split layout
+    of w_gate_up [E, 2*Dff, Dm]: (body uint8, scales int16 of f16 d bits)."""
+    import torch
+
+    info = gate_file.tensor(gate)
+    if info is None:
+        raise GgufError(-1, f"no tensor named {gate!r}")
+    nb = 2 * (info.nbytes // info.block_bytes)
+    body = torch.empty(nb * (info.block_bytes - 2), dtype=torch.uint8, device="cuda")
+    scales = torch.empty(nb, dtype=torch.int16, device="cuda")
+    gp, gn, _gk = _buf(gate_data)
+    up_, un, _uk = _buf(up_data)
+    rc = ffi.load().r9vx_gguf_upload_gate_up_split(gate_file._h, gp, gn, gate.encode(), up_file._h, up_, un,
+                                                   up.encode(), ctypes.c_void_p(body.data_ptr()), body.numel(),
+                                                   ctypes.c_void_p(scales.data_ptr()), 2 * scales.numel(),
+                                                   ffi._stream(torch, stream))
+    if rc != 0:
+        _raise(rc)
+    return body, scales
+
+
 def upload_split(file: GgufFile, data, name: str, stream=None):
     """A Q8_0 / Q6_K tensor in the split device layout: (body uint8, scales
     int16 holding the f16 d bits); non-finite scales are refused on the host."""
@@ -430,25 +453,45 @@ def load_matmul_weight(file: GgufFile, data, name: str, m_bucket: int = 8, in_dt
     return st, w, None
 
 
+class MoeExperts(tuple):
+    """(static, w_gate_up, w_down) -- unpacks as that triple -- plus the split
+    layout's d arrays `w_gate_up_scales` / `w_down_scales` (None unless the
+    projection is Q8_0 / Q6_K)."""
+
+    def __new__(cls, st, w_gate_up, w_down, w_gate_up_scales=None, w_down_scales=None):
+        self = super().__new__(cls, (st, w_gate_up, w_down))
+        self.w_gate_up_scales, self.w_down_scales = w_gate_up_scales, w_down_scales
+        return self
+
+
 def load_moe_experts(file: GgufFile, data, gate: str, up: str | None, down: str, t_bucket: int,
-                     k: int, validate: bool = True):
-    """(MoeFfnStatic, w_gate_up, w_down) on the device from stacked expert
-    tensors of one shard; up=None takes a fused ffn_gate_up_exps tensor."""
+                     k: int, validate: bool = True) -> MoeExperts:
+    """The experts of one shard on the device from stacked expert tensors
+    (up=None takes a fused ffn_gate_up_exps tensor): Q4_K / IQ4_XS wire
+    blocks, IQ3_S repacked into 112-byte blocks, Q8_0 / Q6_K in the split
+    layout (body + d array)."""
     st = file.moe_ffn_static(gate, up, down, t_bucket, k)
-    if up is None:
+    gs = ds = None
+    if st.gate_up.scheme in ffi.SPLIT_SCHEMES:
+        w_gate_up, gs = (upload_split(file, data, gate) if up is None
+                         else upload_gate_up_split(file, data, gate, file, data, up))
+    elif up is None:
         w_gate_up = upload(file, data, gate)
     else:
         w_gate_up = upload_gate_up(file, data, gate, file, data, up)
-    w_down = upload(file, data, down)
-    if validate:  # IQ3_S blocks were checked on the host by the upload
+    if st.down.scheme in ffi.SPLIT_SCHEMES:
+        w_down, ds = upload_split(file, data, down)
+    else:
+        w_down = upload(file, data, down)
+    if validate:  # IQ3_S and split blocks were checked on the host by their uploads
         bad = 0
-        if st.gate_up.scheme != ffi.IQ3_S:
+        if st.gate_up.scheme in (ffi.Q4_K, ffi.IQ4_XS):
             bad += ffi.validate_weights(w_gate_up, st.gate_up.scheme, st.e_local * 2 * st.dff, st.dm)
-        if st.down.scheme != ffi.IQ3_S:
+        if st.down.scheme in (ffi.Q4_K, ffi.IQ4_XS):
             bad += ffi.validate_weights(w_down, st.down.scheme, st.e_local * st.dm, st.dff)
         if bad:
             raise GgufError(-1, f"{gate}/{down}: {bad} expert block(s) carry a non-finite scale")
-    return st, w_gate_up, w_down
+    return MoeExperts(st, w_gate_up, w_down, gs, ds)
 
 
 def load_router_weight(file: GgufFile, data, name: str):

@@ -399,6 +399,9 @@ def _model_file():
         ("blk.0.attn_o_iq3.weight", (512, 2), 21, bytes(2 * 2 * 110)),
         ("blk.0.ffn_gate_iq3_exps.weight", (dm, dff, e), 21, bytes(e * dff * (dm // 256) * 110)),
         ("blk.0.ffn_down_iq3_exps.weight", (dff, dm, e), 21, bytes(e * dm * (dff // 256) * 110)),
+        ("blk.0.ffn_gate_q8_exps.weight", (dm, dff, e), 8, bytes(e * dff * (dm // 32) * 34)),
+        ("blk.0.ffn_down_q6_exps.weight", (dff, dm, e), 14, bytes(e * dm * (dff // 256) * 210)),
+        ("blk.0.ffn_down_f16_exps.weight", (dff, dm, e), 1, bytes(e * dm * dff * 2)),
     ]
     return build([("general.architecture", (8, "llama"))], tensors)
 
@@ -435,9 +438,16 @@ def test_matmul_and_moe_ffn_statics_from_a_checkpoint():
     assert (s3.gate_up.scheme, s3.down.scheme) == (ffi.IQ3_S, ffi.Q4_K)
     assert (s3.gate_up.layout, s3.down.layout) == (ffi.LAYOUT_IQ3S_112, ffi.LAYOUT_GGUF_WIRE)
     assert (s.gate_up.layout, s.down.layout, s.gate_up.dtype) == (ffi.LAYOUT_GGUF_WIRE, ffi.LAYOUT_GGUF_WIRE, ffi.I4)
-    with pytest.raises(gguf.GgufError, match="down experts must be Q4_K"):
+    s4 = f.moe_ffn_static("blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_exps.weight",
+                          "blk.0.ffn_down_iq3_exps.weight", 8, 2)
+    assert (s4.down.scheme, s4.down.dtype, s4.down.layout) == (ffi.IQ3_S, ffi.I4, ffi.LAYOUT_IQ3S_112)
+    s5 = f.moe_ffn_static("blk.0.ffn_gate_q8_exps.weight", "blk.0.ffn_gate_q8_exps.weight",
+                          "blk.0.ffn_down_q6_exps.weight", 8, 2)
+    assert (s5.gate_up.scheme, s5.gate_up.dtype, s5.gate_up.layout) == (ffi.Q8_0, ffi.I8, ffi.LAYOUT_SPLIT)
+    assert (s5.down.scheme, s5.down.dtype, s5.down.layout) == (ffi.Q6_K, ffi.I8, ffi.LAYOUT_SPLIT)
+    with pytest.raises(gguf.GgufError, match="experts must be Q4_K .12., IQ4_XS .23., IQ3_S .21., Q8_0 .8. or Q6_K"):
         f.moe_ffn_static("blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_exps.weight",
-                         "blk.0.ffn_down_iq3_exps.weight", 8, 2)
+                         "blk.0.ffn_down_f16_exps.weight", 8, 2)
     with pytest.raises(gguf.GgufError, match="must be \\{256, 512, 3\\}"):
         f.moe_ffn_static("blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_exps.weight", "blk.0.ffn_gate_exps.weight",
                          8, 2)

@@ -472,9 +472,9 @@ def test_sort_refuses_out_of_range_id():
 
 # ---------------------------------------------------------------- moe_ffn
 
-def _tiny_moe(seed, t=5, e=4, k=2, dm=256, dff=256, shared=0):
-    gu = synth.quant_weights(O.IQ4_XS, seed, (e + shared) * 2 * dff, dm)
-    dn = synth.quant_weights(O.Q4_K, seed + 1, (e + shared) * dm, dff)
+def _tiny_moe(seed, t=5, e=4, k=2, dm=256, dff=256, shared=0, schemes=(O.IQ4_XS, O.Q4_K)):
+    gu = synth.quant_weights(schemes[0], seed, (e + shared) * 2 * dff, dm)
+    dn = synth.quant_weights(schemes[1], seed + 1, (e + shared) * dm, dff)
     x = synth.normal_bf16(seed + 2, (t, dm))
     logits = synth.normal_f32(seed + 3, (t, e))
     ids, w = O.moe_route(logits, k)
@@ -490,13 +490,18 @@ def test_moe_ffn_sliced_equals_full_t0_form():
     assert np.array_equal(y, yf)
 
 
-def test_moe_ffn_vs_f64_bruteforce_and_shared():
+@pytest.mark.parametrize("schemes", [(O.IQ4_XS, O.Q4_K), (O.Q8_0, O.Q8_0), (O.Q6_K, O.Q6_K), (O.IQ3_S, O.IQ3_S),
+                                     (O.Q4_K, O.IQ4_XS)])
+def test_moe_ffn_vs_f64_bruteforce_and_shared(schemes):
+    """moe_ffn over every expert weight type against f64 arithmetic on the
+    pinned decodes (the dequantize goldens): gather, SwiGLU, down, the
+    weighted sum and a shared expert."""
     t, e, k, dm, dff = 4, 3, 2, 256, 256
-    x, ids, w, gu, dn = _tiny_moe(81, t=t, e=e, k=k, shared=1)
-    y = O.moe_ffn(x, O.BF16, ids, w, e, dff, gu, dn, shared=1)
+    x, ids, w, gu, dn = _tiny_moe(81, t=t, e=e, k=k, shared=1, schemes=schemes)
+    y = O.moe_ffn(x, O.BF16, ids, w, e, dff, gu, dn, scheme_gu=schemes[0], scheme_dn=schemes[1], shared=1)
     xf = synth.bf16_bits_to_f32(x).astype(np.float64)
-    G = O.dequantize(O.IQ4_XS, gu, (e + 1) * 2 * dff, dm).astype(np.float64).reshape(e + 1, 2 * dff, dm)
-    D = O.dequantize(O.Q4_K, dn, (e + 1) * dm, dff).astype(np.float64).reshape(e + 1, dm, dff)
+    G = O.dequantize(schemes[0], gu, (e + 1) * 2 * dff, dm).astype(np.float64).reshape(e + 1, 2 * dff, dm)
+    D = O.dequantize(schemes[1], dn, (e + 1) * dm, dff).astype(np.float64).reshape(e + 1, dm, dff)
 
     def ffn(ex, xr):
         g = xr @ G[ex, :dff].T
