@@ -263,8 +263,24 @@ __global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs a, uint32_t nch
     if (e < a.e) {
         const uint32_t *cc = reinterpret_cast<const uint32_t *>(a.ws + L.ccount) + (uint64_t)e * nchunk;
         uint32_t *cb = reinterpret_cast<uint32_t *>(a.ws + L.cbase) + (uint64_t)e * nchunk;
+        /* the first 512 chunk counts are loaded before the scan starts */
+        constexpr uint32_t kPre = 8;
+        uint32_t pre[kPre];
+#pragma unroll
+        for (uint32_t i = 0; i < kPre; ++i) {
+            const uint32_t c = 64 * i + lane;
+            pre[i] = c < nchunk ? cc[c] : 0u;
+        }
         uint32_t carry = 0;
-        for (uint32_t c0 = 0; c0 < nchunk; c0 += 64) {
+#pragma unroll
+        for (uint32_t i = 0; i < kPre; ++i) {
+            if (64 * i >= nchunk) break;
+            const uint32_t c = 64 * i + lane, v = pre[i];
+            const uint32_t inc = wave_incl_scan(v, lane);
+            if (c < nchunk) cb[c] = carry + inc - v;
+            carry += __shfl(inc, 63, 64);
+        }
+        for (uint32_t c0 = 64 * kPre; c0 < nchunk; c0 += 64) {
             uint32_t c = c0 + lane;
             uint32_t v = c < nchunk ? cc[c] : 0u;
             uint32_t inc = wave_incl_scan(v, lane);
@@ -278,12 +294,24 @@ __global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs a, uint32_t nch
         prev = __shfl(prev, 0, 64);
         if (prev != a.e - 1) return;
         __threadfence();
-        /* last expert finished: scan the totals (this wave only) */
+        /* last expert finished: scan the totals (this wave only), every
+         * count loaded before the first scan step so that the loads' latency
+         * is paid once */
         uint32_t *offsets = reinterpret_cast<uint32_t *>(a.ws + L.offsets);
+        constexpr uint32_t kPer = kMoeMaxE / 64;
+        uint32_t tot[kPer];
+#pragma unroll
+        for (uint32_t i = 0; i < kPer; ++i) {
+            const uint32_t ee = 64 * i + lane;
+            tot[i] = ee < a.e ? __hip_atomic_load(&counts[ee], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+        }
         uint32_t base = 0, nact = 0;
-        for (uint32_t e0 = 0; e0 < a.e; e0 += 64) {
+#pragma unroll
+        for (uint32_t i = 0; i < kPer; ++i) {
+            const uint32_t e0 = 64 * i;
+            if (e0 >= a.e) break;
             uint32_t ee = e0 + lane;
-            uint32_t v = ee < a.e ? __hip_atomic_load(&counts[ee], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+            uint32_t v = tot[i];
             uint32_t inc = wave_incl_scan(v, lane);
             uint32_t act = v > 0 ? 1u : 0u;
             uint32_t ainc = wave_incl_scan(act, lane);

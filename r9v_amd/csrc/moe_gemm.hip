@@ -347,7 +347,7 @@ __global__ __launch_bounds__(256, 2) void moe_dn_lds_kernel(GroupedArgs a) {
 template <int GU>
 __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     __shared__ __attribute__((aligned(16))) M3Lds sm;
-    __shared__ uint32_t lut[256];
+    uint32_t *const lut = sm.lut;
     __shared__ float rowsc[kMoeTileM3];
     const uint32_t *status = ws_u32(a, a.L.status);
     uint32_t tix, nt;
@@ -357,7 +357,9 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
     const uint32_t j0 = nt * 128;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid < kMoeTileM3) rowsc[tid] = tid < rows ? a.xscale[row_token(a, expert, pos0 + tid)] : 0.f;
+    /* each row's activation scale, loaded now and put in LDS after the main
+     * loop (the epilogue is its only reader) */
+    const float rsc = tid < rows ? a.xscale[row_token(a, expert, pos0 + (tid < kMoeTileM3 ? tid : 0))] : 0.f;
     if constexpr (GU == R9VX_SCHEME_IQ4_XS) m3_init_iq4_lut(lut, tid, 512);
     __syncthreads();
 
@@ -376,6 +378,8 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
     m3_run<GU>(nr, sm, a.x16, aoff, w, a.dm / kTileK, tid, wv, lut, 128 * rh, 32 * cq, 128 + 32 * cq, acc);
+    if (tid < kMoeTileM3) rowsc[tid] = rsc;
+    __syncthreads();
 
     float *h = reinterpret_cast<float *>(a.ws + a.L.h);
     const uint32_t col = j0 + 32 * cq + (lane & 31);
@@ -397,7 +401,7 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
 template <int DN>
 __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     __shared__ __attribute__((aligned(16))) M3Lds sm;
-    __shared__ uint32_t lut[256];
+    uint32_t *const lut = sm.lut;
     __shared__ float rowsc[kMoeTileM3]; /* 2^e that undoes each h row's fp16 scale */
     const uint32_t *status = ws_u32(a, a.L.status);
     uint32_t tix, nt;
@@ -407,9 +411,8 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
     const uint32_t n0 = nt * 256;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid < kMoeTileM3)
-        rowsc[tid] = tid < rows ? ldexpf(1.0f, row_shift(__builtin_bit_cast(float, ws_u32(a, a.L.hmax)[pos0 + tid])))
-                                : 0.f;
+    /* each h row's max, loaded now; its scale goes to LDS after the main loop */
+    const uint32_t hbits = tid < rows && tid < kMoeTileM3 ? ws_u32(a, a.L.hmax)[pos0 + tid] : 0u;
     if constexpr (DN == R9VX_SCHEME_IQ4_XS) m3_init_iq4_lut(lut, tid, 512);
     __syncthreads();
 
@@ -426,6 +429,8 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
     m3_run<DN, true>(nr, sm, a.h16, aoff, w, a.dff / kTileK, tid, wv, lut, 128 * rh, 64 * cq, 64 * cq + 32, acc);
+    if (tid < kMoeTileM3) rowsc[tid] = tid < rows ? ldexpf(1.0f, row_shift(__builtin_bit_cast(float, hbits))) : 0.f;
+    __syncthreads();
 
     /* The tiles are transposed (m3_run<.., true>): lane l holds h row
      * 128 rh + 32 t + (l & 31) and output columns n0 + 64 cq + 32 j +

@@ -145,6 +145,7 @@ __device__ __forceinline__ void wait_vm() {
 /* Per-step scale terms of one column. */
 struct BScale {
     float dl0, nml0, dl1, nml1; /* Q4_K: low nibbles (sub-block 2ks), high (2ks+1); IQ4_XS: dl0 */
+    float c0, c1;               /* Q4_K: nml - 1024 dl, the addend for fp16 operands 1024 + q */
 };
 
 template <int SCHEME, int KS>
@@ -159,9 +160,11 @@ __device__ __forceinline__ BScale bscale(const r9vx_u32x4 &hd, uint32_t h) {
         s.nml0 = -(dmin * (float)mn[0]);
         s.dl1 = d * (float)sc[1];
         s.nml1 = -(dmin * (float)mn[1]);
+        s.c0 = fmaf(-1024.f, s.dl0, s.nml0);
+        s.c1 = fmaf(-1024.f, s.dl1, s.nml1);
     } else {
         s.dl0 = d * r9vx_iq4xs_scale(r9vx_u32x2{hd.x, hd.y}, 2 * KS + h);
-        s.nml0 = s.dl1 = s.nml1 = 0.f;
+        s.nml0 = s.dl1 = s.nml1 = s.c0 = s.c1 = 0.f;
     }
     return s;
 }

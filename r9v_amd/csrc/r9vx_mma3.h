@@ -39,7 +39,11 @@ constexpr uint32_t kM3Stage = 256u * 128u; /* one A stage or the B tile: 256 row
 constexpr int kM3AStages = 2;
 constexpr int kM3BStages = 2;
 
+/* The IQ4_XS codebook-pair table comes first, so that its LDS address fits
+ * the 16-bit offset of ds_read (the byte index, shifted by one SDWA
+ * instruction, is the whole address computation of a lookup). */
 struct M3Lds {
+    uint32_t lut[256];
     uint8_t a[kM3AStages][kM3Stage];
     uint8_t b[kM3BStages][kM3Stage];
 };
@@ -125,24 +129,31 @@ __device__ __forceinline__ void m3_init_iq4_lut(uint32_t *lut, uint32_t tid, uin
 /* Decode unit u (0..7) of a step: payload bytes 2u, 2u + 1 (bytes 4q + 2m,
  * 4q + 2m + 1 of dword q = u / 2, m = u % 2), whose low nibbles are elements
  * 2m, 2m + 1 and high nibbles elements 4 + 2m, 4 + 2m + 1 of group q.  Each
- * weight is the exact f32 formula rounded once to fp16
- * (crates/r9v-format/src/ggml.rs:1131-1150, iq.rs:578-598).  Returns the two
- * packed dwords {low pair, high pair}.  IQ4_XS: kv0 / kv1 are the bytes'
- * codebook pairs {kv[low], kv[high]}. */
-typedef _Float16 m3_h2 __attribute__((ext_vector_type(2)));
+ * weight is the f32 formula (crates/r9v-format/src/ggml.rs:1131-1150,
+ * iq.rs:578-598) evaluated in one fused operation and rounded once to fp16.
+ * Returns the two packed dwords {low pair, high pair}.  IQ4_XS: kv0 / kv1
+ * are the bytes' codebook pairs {kv[low], kv[high]}. */
 template <int SCHEME>
 __device__ __forceinline__ void m3_dec_unit(uint32_t dw, int m, const BScale &sc, uint32_t kv0, uint32_t kv1,
                                             uint32_t &lo2, uint32_t &hi2) {
-    m3_h2 l, h;
     if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
-        uint32_t l4 = dw & 0x0F0F0F0Fu, h4 = (dw >> 4) & 0x0F0F0F0Fu;
-        /* hide the masks' known-zero bits, so that each nibble becomes one
-         * byte-select conversion (v_cvt_f32_ubyteN) */
-        asm volatile("" : "+v"(l4), "+v"(h4));
-        l.x = (_Float16)fmaf(sc.dl0, (float)((l4 >> (16 * m)) & 0xFFu), sc.nml0);
-        l.y = (_Float16)fmaf(sc.dl0, (float)((l4 >> (16 * m + 8)) & 0xFFu), sc.nml0);
-        h.x = (_Float16)fmaf(sc.dl1, (float)((h4 >> (16 * m)) & 0xFFu), sc.nml1);
-        h.y = (_Float16)fmaf(sc.dl1, (float)((h4 >> (16 * m + 8)) & 0xFFu), sc.nml1);
+        /* bytes 2m, 2m + 1 each under a 0x64 byte (v_perm), so that their
+         * nibbles read as the fp16 pairs {1024 + lo(2m), 1024 + lo(2m+1)}
+         * and {1024 + hi(2m), 1024 + hi(2m+1)}; then w = dl (1024 + q) + c
+         * with c = -dmin m - 1024 dl, fused and rounded once to fp16 -- the
+         * f32 value dl q - dmin m up to c's own f32 rounding. */
+        const uint32_t t = __builtin_amdgcn_perm(0x64646464u, dw, m ? 0x04030402u : 0x04010400u);
+        const uint32_t lo = t & 0x640F640Fu, hi = ((t >> 4) & 0x000F000Fu) | 0x64006400u;
+        uint32_t a, b;
+        asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(a) : "v"(sc.dl0), "v"(lo), "v"(sc.c0));
+        asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+            : "+v"(a) : "v"(sc.dl0), "v"(lo), "v"(sc.c0));
+        asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(b) : "v"(sc.dl1), "v"(hi), "v"(sc.c1));
+        asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+            : "+v"(b) : "v"(sc.dl1), "v"(hi), "v"(sc.c1));
+        lo2 = a;
+        hi2 = b;
+        asm volatile("" : "+v"(lo2), "+v"(hi2));
     } else {
         /* dl * kv is exact in f32 (dl = d * s has 17 significant bits, kv
          * 8), so v_fma_mix with the fp16 codebook value as its operand and
@@ -157,14 +168,10 @@ __device__ __forceinline__ void m3_dec_unit(uint32_t dw, int m, const BScale &sc
         asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(b) : "v"(sc.dl0), "v"(kv1));
         lo2 = a;
         hi2 = b;
+        /* keep the computation here: its only use is at the end of the step,
+         * where the compiler's IR passes would otherwise sink it */
         asm volatile("" : "+v"(lo2), "+v"(hi2));
-        return;
     }
-    lo2 = __builtin_bit_cast(uint32_t, l);
-    hi2 = __builtin_bit_cast(uint32_t, h);
-    /* keep the computation here: its only use is at the end of the step,
-     * where the compiler's IR passes would otherwise sink it */
-    asm volatile("" : "+v"(lo2), "+v"(hi2));
 }
 
 /*
@@ -195,9 +202,22 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
     /* the pair after whose MFMAs unit u is decoded */
     auto dec_pair = [](int u) { return ((u + 1) * P + 7) / 8 - 1; };
     uint32_t kv[16];
+    const uint8_t *lutb = reinterpret_cast<const uint8_t *>(lut);
     auto read_kv = [&](int u) {
-        kv[2 * u] = lut[(dws[u >> 1] >> (16 * (u & 1))) & 0xFFu];
-        kv[2 * u + 1] = lut[(dws[u >> 1] >> (16 * (u & 1) + 8)) & 0xFFu];
+        uint32_t o0, o1; /* 4 x bytes 2m, 2m + 1 of the dword, one SDWA shift each */
+        if (u & 1) {
+            asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+                : "=v"(o0) : "v"(dws[u >> 1]));
+            asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+                : "=v"(o1) : "v"(dws[u >> 1]));
+        } else {
+            asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+                : "=v"(o0) : "v"(dws[u >> 1]));
+            asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+                : "=v"(o1) : "v"(dws[u >> 1]));
+        }
+        kv[2 * u] = *reinterpret_cast<const uint32_t *>(lutb + o0);
+        kv[2 * u + 1] = *reinterpret_cast<const uint32_t *>(lutb + o1);
     };
 #pragma unroll
     for (int b = 0; b < 16; ++b) kv[b] = 0u;
