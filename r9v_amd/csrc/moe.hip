@@ -12,14 +12,16 @@
  *  - FFN per expert (:527-639): gate rows [0,Dff), up rows [Dff,2Dff) of the
  *    expert's [2Dff, Dm] block; h = silu(g)*u (activation.rs:135-138,
  *    act_mul.rs:86-99); o = h . Wd^T.  Decode (t <= 8) runs dequant-fused
- *    GEMVs over the active experts' rows (h kept in f32 between them); larger
- *    t runs the grouped MFMA GEMM of moe_gemm.hip.
+ *    GEMVs with the rows in pair order (token * K + slot), so it needs no
+ *    sort pass (h kept in f32 between them); larger t sorts and runs the
+ *    grouped MFMA GEMMs of moe_gemm.hip.
  *  - Combine (:641-653): y[t] = sum over the token's pairs in ascending
  *    (expert, slot) order of w * o, f32, then the shared experts' outputs are
  *    added (the residual_add of crates/r9v-models/src/generic.rs:1458-1495).
  *  - Refusal before mutation (:440-465): ids >= E set R9VX_STATUS_BAD_EXPERT
- *    in the workspace status word and every kernel that writes y or
- *    intermediate rows returns without writing.
+ *    in the workspace status word and y is not written (the grouped path's
+ *    sort flags them and every later kernel returns; on the decode path the
+ *    GEMVs read nothing for such a pair and the combine checks every id).
  */
 #include <type_traits>
 
@@ -382,16 +384,19 @@ constexpr int kDecWaves = R9VX_DEC_WAVES;
 
 /* Token and expert of sorted position pos (shared experts after the P
  * routed pairs, T rows each); false when the call was refused. */
+/* Token and expert of row pos: the decode path keeps the rows in pair order
+ * (pos = token * K + slot, no sort pass), the shared experts' T rows each
+ * after the P pairs; false for an id >= E (nothing is read for it, and the
+ * combine refuses the call). */
 __device__ __forceinline__ bool pos_meta(const FfnArgs &a, uint32_t pos, uint32_t &tok, uint32_t &expert) {
     if (pos >= a.p) {
         tok = (pos - a.p) % a.t;
         expert = a.e + (pos - a.p) / a.t;
         return true;
     }
-    const uint32_t pi = reinterpret_cast<const uint32_t *>(a.ws + a.L.pinfo)[pos];
-    tok = pi & 0xFFFFu;
-    expert = pi >> 16;
-    return pi != ~0u;
+    expert = a.ids[pos];
+    tok = pos / a.k;
+    return expert < a.e;
 }
 
 /* Steps (unit, K segment) one wave carries; all of their weight loads are
@@ -719,23 +724,33 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
  * distinct), so every thread then walks the same ordered list from LDS and
  * issues its K row loads before the ordered f32 sum. */
 __global__ __launch_bounds__(256) void r9vx_moe_combine_kernel(MoeCombineArgs a) {
-    __shared__ uint32_t spos[kMoeMaxK], opos[kMoeMaxK];
+    __shared__ uint32_t key[kMoeMaxK], opos[kMoeMaxK];
     __shared__ float sw[kMoeMaxK], ow[kMoeMaxK];
-    const uint32_t *status = reinterpret_cast<const uint32_t *>(a.ws + a.L.status);
-    if (status[0] != 0u) return;
+    __shared__ uint32_t bad;
+    /* the refusal of moe_ffn.rs:440-465 for the whole batch (the decode path
+     * has no sort pass): every block checks every id before writing y, and
+     * block (0, 0) leaves the call's status word */
+    if (threadIdx.x == 0) bad = 0u;
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < a.p; i += blockDim.x)
+        if (a.ids[i] >= a.e) bad = 1u;
+    __syncthreads();
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+        reinterpret_cast<uint32_t *>(a.ws + a.L.status)[0] = bad ? R9VX_STATUS_BAD_EXPERT : 0u;
+    if (bad) return;
     const uint32_t t = blockIdx.y;
     const uint32_t kk = a.k;
-    const uint32_t *inv = reinterpret_cast<const uint32_t *>(a.ws + a.L.inv);
+    /* the token's K rows (pair order) ranked by (expert, slot) */
     if (threadIdx.x < kk) {
-        spos[threadIdx.x] = inv[(uint64_t)t * kk + threadIdx.x];
+        key[threadIdx.x] = (a.ids[(uint64_t)t * kk + threadIdx.x] << 8) | threadIdx.x;
         sw[threadIdx.x] = a.weights[(uint64_t)t * kk + threadIdx.x];
     }
     __syncthreads();
     if (threadIdx.x < kk) {
-        const uint32_t p = spos[threadIdx.x];
+        const uint32_t kv = key[threadIdx.x];
         uint32_t rank = 0;
-        for (uint32_t j = 0; j < kk; ++j) rank += spos[j] < p ? 1u : 0u;
-        opos[rank] = p;
+        for (uint32_t j = 0; j < kk; ++j) rank += key[j] < kv ? 1u : 0u;
+        opos[rank] = t * kk + threadIdx.x;
         ow[rank] = sw[threadIdx.x];
     }
     __syncthreads();
@@ -929,7 +944,7 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
 }
 
 int r9vx_moe_combine_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s) {
-    MoeCombineArgs c{p.weights, p.y, p.ws, L, p.t, p.k, p.dm, p.shared, p.t * p.k};
+    MoeCombineArgs c{p.weights, p.ids, p.y, p.ws, L, p.t, p.k, p.dm, p.shared, p.t * p.k, p.e};
     dim3 grid((p.dm / 4 + 255) / 256, p.t);
     if (p.t <= 8)
         hipLaunchKernelGGL(r9vx_moe_combine_kernel, grid, dim3(256), 0, s, c);

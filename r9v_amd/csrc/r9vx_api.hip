@@ -775,9 +775,13 @@ int r9vx_moe_sort_launch(const r9vx_moe_ffn_static *st, const uint32_t *ids, uin
 
 int r9vx_launch_moe(const r9vx_moe_problem &p, hipStream_t s) {
     MoeLayout L = r9vx_moe_layout(p.t_bucket, p.e, p.k, p.dm, p.dff, p.shared);
-    int rc = r9vx_moe_sort_stage(p, L, s);
-    if (rc) return rc;
-    rc = p.t <= 8 ? r9vx_moe_decode_stage(p, L, s) : r9vx_moe_grouped_stage(p, L, s);
+    int rc = 0;
+    if (p.t <= 8) { /* pair-order rows: no sort; the combine checks the ids */
+        rc = r9vx_moe_decode_stage(p, L, s);
+    } else {
+        rc = r9vx_moe_sort_stage(p, L, s);
+        if (!rc) rc = r9vx_moe_grouped_stage(p, L, s);
+    }
     if (rc) return rc;
     return r9vx_moe_combine_stage(p, L, s);
 }

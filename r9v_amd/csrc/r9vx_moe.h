@@ -15,9 +15,10 @@
  *   work    u32x4[E+S] (expert, first position, pair count, 0) of active experts
  *   tiles   u32x4[...] grouped-GEMM tile schedule, 128-row tiles
  *   tiles3  u32x4[...] the same work in 256-row tiles (the r9vx_mma3.h kernels)
- *   h       f32[(P + S*T) * Dff]  SwiGLU rows in sorted order, shared rows after
- *   o       f32[(P + S*T) * Dm]   expert output rows in the same order (decode
- *                                 path); the grouped path stores them in the
+ *   h       f32[(P + S*T) * Dff]  SwiGLU rows in sorted order (decode path: pair
+ *                                 order), shared rows after
+ *   o       f32[(P + S*T) * Dm]   expert output rows (decode path: in pair
+ *                                 order, no sort); the grouped path stores them in the
  *                                 same region as fp16 [(P + S*T) * Dm] scaled
  *                                 per (row, 64-column block), followed by the
  *                                 f32 scales [(P + S*T) * Dm/64]
@@ -86,10 +87,11 @@ inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint
 
 struct MoeCombineArgs {
     const float *weights;
+    const uint32_t *ids;
     float *y;
     uint8_t *ws;
     MoeLayout L;
-    uint32_t t, k, dm, shared, p;
+    uint32_t t, k, dm, shared, p, e;
 };
 
 int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
