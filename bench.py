@@ -21,8 +21,8 @@ restatement of R9V's T0 path) on a bounded sample on this host, 1 thread,
 plus an all-threads OpenMP variant for the grouped MoE GEMM.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c0,c1,c2,c3,ceilings]
-    python bench.py --pmc-case c4            # short fixed run for rocprofv3 --pmc
-    python bench.py --pmc-summary DIR ...    # FETCH_SIZE/WRITE_SIZE dirs -> traffic text
+    python bench.py --pmc-case c4|c3|c2      # short fixed run for rocprofv3 --pmc
+    python bench.py --pmc-summary DIR ... [--pmc-kernels a,b]  # FETCH_SIZE/WRITE_SIZE dirs -> traffic text
 """
 from __future__ import annotations
 
@@ -59,9 +59,11 @@ def parse():
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU work per baseline sample")
     ap.add_argument("--only", default="", help="comma list of extras: c0,c1,c2,c3,ceilings ('none' for the headline "
                                                "only)")
-    ap.add_argument("--pmc-case", default="", help="run a short fixed workload for counter collection: c4")
+    ap.add_argument("--pmc-case", default="", help="run a short fixed workload for counter collection: c4, c3, c2")
     ap.add_argument("--pmc-summary", nargs="*", default=None,
                     help="rocprofv3 --pmc output dirs (FETCH_SIZE, WRITE_SIZE) to summarise as traffic")
+    ap.add_argument("--pmc-kernels", default="", help="comma list of kernel-name substrings for --pmc-summary "
+                                                      "(default: the headline kernel)")
     return ap.parse_args()
 
 
@@ -278,7 +280,7 @@ def gemv_extra(torch, ffi, synth, scheme, n, k, m, x_dtype, tag, cpu_s, workload
     return out
 
 
-def c2_extra(torch, ffi, synth, gsynth, steps, cpu_s):
+def c2_extra(torch, ffi, synth, gsynth, steps, cpu_s, steps_only=False):
     m, n, k = 2048, 14336, 4096
     w0 = gsynth.quant_weights_gpu(torch, ffi.Q4_K, 201, n, k)
     ws = [w0] + [w0.clone() for _ in range(copies_for(w0.numel()) - 1)]
@@ -291,6 +293,10 @@ def c2_extra(torch, ffi, synth, gsynth, steps, cpu_s):
     def step(i):
         ffi.matmul(ws[i % len(ws)], ffi.Q4_K, n, k, x, out_dtype=ffi.BF16, y=y, workspace=wsp)
 
+    if steps_only:  # a fixed run for counter collection
+        for i in range(steps):
+            step(i)
+        return None
     ms, med = timed_steps(torch, step, max(steps, len(ws)), 3)
     flops = 2 * m * n * k
     out = {"workload": "configs[2]: x bf16 [2048x4096] . Q4_K [14336x4096]^T -> bf16, fp16 MFMA",
@@ -310,7 +316,7 @@ def c2_extra(torch, ffi, synth, gsynth, steps, cpu_s):
     return out
 
 
-def c3_extra(torch, ffi, synth, gsynth, steps, cpu_s):
+def c3_extra(torch, ffi, synth, gsynth, steps, cpu_s, steps_only=False):
     """MoE decode: T=5, E=512 routed + 1 shared, top-10; per step the router
     and the FFN over freshly routed tokens (8 routing patterns rotate)."""
     t, e, k, dm, dff, shared = 5, 512, 10, 2048, 512, 1
@@ -336,6 +342,10 @@ def c3_extra(torch, ffi, synth, gsynth, steps, cpu_s):
         gu, dn = wsets[i % len(wsets)]
         ffi.moe_ffn(x, ids, w, gu, dn, e, dff, shared=shared, y=y, workspace=wsp, t_bucket=t)
 
+    if steps_only:  # a fixed run for counter collection
+        for i in range(steps):
+            step(i)
+        return None
     ms, med = timed_steps(torch, step, max(200, steps), 10)
     u = float(np.mean(uniq))
     per_expert = int(ffi.load().r9vx_moe_ffn_expert_bytes(__import__("ctypes").byref(st)))
@@ -384,16 +394,22 @@ def ceilings(torch, ffi):
 # ---------------------------------------------------------------- counters
 
 def pmc_case(torch, ffi, synth, gsynth, name):
-    """A short fixed run for `rocprofv3 --pmc`: 6 configs[4] moe_ffn steps
-    (the summary takes the median over the gate/up GEMM launches, so the
-    first launch's cold caches do not count), then 5 launches of a plain copy
+    """A short fixed run for `rocprofv3 --pmc`: 6 steps of configs[4]
+    (moe_ffn), configs[3] (route + moe_ffn) or configs[2] (the dense GEMM) --
+    the summaries take medians over a kernel's launches, so the first
+    launch's cold caches do not count -- then 5 launches of a plain copy
     kernel of known size (torch.neg, f32 -> f32, 64 MiB read + 64 MiB
     written) that calibrate what FETCH_SIZE / WRITE_SIZE report per byte."""
-    if name != "c4":
-        raise SystemExit(f"unknown --pmc-case {name!r} (known: c4)")
-    p = MoePrefill(torch, ffi, synth, gsynth)
-    for i in range(6):
-        p.step(i)
+    if name == "c4":
+        p = MoePrefill(torch, ffi, synth, gsynth)
+        for i in range(6):
+            p.step(i)
+    elif name == "c3":
+        c3_extra(torch, ffi, synth, gsynth, 6, 0, steps_only=True)
+    elif name == "c2":
+        c2_extra(torch, ffi, synth, gsynth, 6, 0, steps_only=True)
+    else:
+        raise SystemExit(f"unknown --pmc-case {name!r} (known: c2, c3, c4)")
     torch.cuda.synchronize()
     src = torch.ones(PMC_COPY_BYTES // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
@@ -401,14 +417,15 @@ def pmc_case(torch, ffi, synth, gsynth, name):
     for _ in range(5):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_case": name, "moe_ffn_steps": 6, "gate_up_flops_per_launch": C4_GU_FLOPS,
-                      "copy_bytes_read": PMC_COPY_BYTES, "copy_bytes_written": PMC_COPY_BYTES}))
+    print(json.dumps({"pmc_case": name, "steps": 6, "copy_bytes_read": PMC_COPY_BYTES,
+                      "copy_bytes_written": PMC_COPY_BYTES}))
 
 
-def pmc_summary(dirs):
-    """Medians of FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the headline
-    kernel from rocprofv3 counter-collection output of `--pmc-case c4` runs,
-    each scaled by the copy kernel's reading of its known byte count."""
+def pmc_summary(dirs, kernels=None):
+    """Medians of FETCH_SIZE / WRITE_SIZE (KiB per dispatch) from rocprofv3
+    counter-collection output of `--pmc-case` runs, each scaled by the copy
+    kernel's reading of its known byte count: the headline kernel, or each
+    kernel whose name contains one of `kernels`."""
     import csv
     import glob
     import sqlite3
@@ -427,24 +444,28 @@ def pmc_summary(dirs):
         return [x for (c, k), v in per.items() if c == counter and pred(k) for x in v]
 
     head = HEAD_KERNEL.split("<")[0]
+    targets = [(k, lambda name, k=k: k in name) for k in kernels] if kernels else \
+        [(HEAD_KERNEL, lambda name: head in name and "<23>" in name)]
     lines = ["counter      kernel                                      dispatches   median KiB/dispatch"]
-    out = {}
-    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        g = find(counter, lambda k: head in k and "<23>" in k)
-        c = find(counter, lambda k: "neg_kernel" in k or ("elementwise" in k and "neg" in k.lower()))
-        if not g or not c:
-            lines.append(f"{counter:12s} (missing: headline {len(g)} / copy {len(c)} dispatches)")
-            continue
-        gm, cm = statistics.median(g), statistics.median(c)
-        factor = PMC_COPY_BYTES / (cm * 1024.0)
-        out[counter] = gm * 1024.0 * factor
-        lines.append(f"{counter:12s} {HEAD_KERNEL:43s} {len(g):10d}   {gm:12.1f}")
-        lines.append(f"{counter:12s} {'copy (torch.neg 64 MiB f32)':43s} {len(c):10d}   {cm:12.1f}")
-        lines.append(f"{counter:12s} calibration factor = {PMC_COPY_BYTES} B / ({cm:.1f} KiB * 1024) = {factor:.4f}")
-    if len(out) == 2:
-        lines.append(f"fetch_bytes_per_launch: {out['FETCH_SIZE']:.0f}")
-        lines.append(f"write_bytes_per_launch: {out['WRITE_SIZE']:.0f}")
-        lines.append(f"traffic_bytes_per_launch: {out['FETCH_SIZE'] + out['WRITE_SIZE']:.0f}")
+    for label, pred in targets:
+        out = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            g = find(counter, pred)
+            c = find(counter, lambda k: "neg_kernel" in k or ("elementwise" in k and "neg" in k.lower()))
+            if not g or not c:
+                lines.append(f"{counter:12s} (missing: {label} {len(g)} / copy {len(c)} dispatches)")
+                continue
+            gm, cm = statistics.median(g), statistics.median(c)
+            factor = PMC_COPY_BYTES / (cm * 1024.0)
+            out[counter] = gm * 1024.0 * factor
+            lines.append(f"{counter:12s} {label[:43]:43s} {len(g):10d}   {gm:12.1f}")
+            lines.append(f"{counter:12s} {'copy (torch.neg 64 MiB f32)':43s} {len(c):10d}   {cm:12.1f}")
+            lines.append(f"{counter:12s} calibration factor = {PMC_COPY_BYTES} B / ({cm:.1f} KiB * 1024) = {factor:.4f}")
+        if len(out) == 2:
+            tag = "" if not kernels else f"{label} "
+            lines.append(f"{tag}fetch_bytes_per_launch: {out['FETCH_SIZE']:.0f}")
+            lines.append(f"{tag}write_bytes_per_launch: {out['WRITE_SIZE']:.0f}")
+            lines.append(f"{tag}traffic_bytes_per_launch: {out['FETCH_SIZE'] + out['WRITE_SIZE']:.0f}")
     print("\n".join(lines))
 
 
@@ -463,7 +484,7 @@ def read_traffic():
 def main():
     args = parse()
     if args.pmc_summary is not None:
-        pmc_summary(args.pmc_summary)
+        pmc_summary(args.pmc_summary, [k for k in args.pmc_kernels.split(",") if k] or None)
         return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: multi-GPU figures are out of scope, "
