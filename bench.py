@@ -582,7 +582,8 @@ def main():
                    "flops_per_step": C4_FLOPS, "median_ms_per_step": round(med, 6),
                    "tokens_per_s": round(C4_T / (ms * 1e-3), 1), "weight_copies": 2,
                    "arithmetic": "fp16 MFMA operands (bf16 activations and SwiGLU rows scaled per row by a power "
-                                 "of two, weights decoded by the exact f32 formula rounded once), f32 accumulate; "
+                                 "of two, weights decoded by the f32 formula rounded once to fp16; Q4_K up to the f32 rounding of a "
+                                 "precomputed addend), f32 accumulate; "
                                  "expert output rows kept as fp16 scaled by a power of two per (row, 64 columns) "
                                  "until the f32 weighted sum",
                    "parallelism": "single GPU",

@@ -130,7 +130,8 @@ __device__ __forceinline__ void m3_init_iq4_lut(uint32_t *lut, uint32_t tid, uin
  * 4q + 2m + 1 of dword q = u / 2, m = u % 2), whose low nibbles are elements
  * 2m, 2m + 1 and high nibbles elements 4 + 2m, 4 + 2m + 1 of group q.  Each
  * weight is the f32 formula (crates/r9v-format/src/ggml.rs:1131-1150,
- * iq.rs:578-598) evaluated in one fused operation and rounded once to fp16.
+ * iq.rs:578-598) evaluated in one fused operation and rounded once to fp16
+ * (Q4_K: up to the f32 rounding of the precomputed addend, below).
  * Returns the two packed dwords {low pair, high pair}.  IQ4_XS: kv0 / kv1
  * are the bytes' codebook pairs {kv[low], kv[high]}. */
 template <int SCHEME>
