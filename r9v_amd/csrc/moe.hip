@@ -84,13 +84,6 @@ __device__ __forceinline__ int id_bits(uint32_t e) {
     return b;
 }
 
-/* Work-list entry of one expert: (expert, first sorted position, pair count). */
-__device__ __forceinline__ void put_work(const MoeLayout &L, uint8_t *ws, uint32_t idx, uint32_t e,
-                                         uint32_t beg, uint32_t m) {
-    r9vx_u32x4 *work = reinterpret_cast<r9vx_u32x4 *>(ws + L.work);
-    work[idx] = r9vx_u32x4{e, beg, m, 0u};
-}
-
 /* ---------------------------------------------------------------- sort: small */
 
 struct SortArgs {
@@ -99,6 +92,46 @@ struct SortArgs {
     MoeLayout L;
     uint32_t p, e, k, t, shared;
 };
+
+/* The grouped GEMMs' row tiles (moe_gemm.hip): expert x with n pairs from
+ * sorted position `off` becomes ceil(n / 128) entries (expert, first
+ * position, rows, 0) of `tiles` and ceil(n / 256) of `tiles3`, experts in
+ * ascending id, then the shared experts (t rows each, after the P pair
+ * rows); status[3] / status[4] = the counts.  Thread x < E passes expert
+ * x's count and offset (blockDim.x >= E). */
+__device__ void put_tile_lists(const SortArgs &a, uint32_t tot, uint32_t off, uint32_t *sh) {
+    const MoeLayout &L = a.L;
+    r9vx_u32x4 *t1 = reinterpret_cast<r9vx_u32x4 *>(a.ws + L.tiles);
+    r9vx_u32x4 *t3 = reinterpret_cast<r9vx_u32x4 *>(a.ws + L.tiles3);
+    const uint32_t tid = threadIdx.x;
+    const bool mine = tid < a.e;
+    const uint32_t n1 = mine ? (tot + kMoeTileM - 1) / kMoeTileM : 0u, n3 = mine ? (tot + kMoeTileM3 - 1) / kMoeTileM3 : 0u;
+    uint32_t all1, all3;
+    const uint32_t b1 = block_excl_scan(n1, sh, all1);
+    const uint32_t b3 = block_excl_scan(n3, sh, all3);
+    for (uint32_t j = 0; j < n1; ++j) {
+        const uint32_t r = tot - j * kMoeTileM;
+        t1[b1 + j] = r9vx_u32x4{tid, off + j * kMoeTileM, r < kMoeTileM ? r : kMoeTileM, 0u};
+    }
+    for (uint32_t j = 0; j < n3; ++j) {
+        const uint32_t r = tot - j * kMoeTileM3;
+        t3[b3 + j] = r9vx_u32x4{tid, off + j * kMoeTileM3, r < kMoeTileM3 ? r : kMoeTileM3, 0u};
+    }
+    const uint32_t s1 = (a.t + kMoeTileM - 1) / kMoeTileM, s3 = (a.t + kMoeTileM3 - 1) / kMoeTileM3;
+    for (uint32_t i = tid; i < a.shared * s1; i += blockDim.x) {
+        const uint32_t sx = i / s1, j = i % s1, r = a.t - j * kMoeTileM;
+        t1[all1 + i] = r9vx_u32x4{a.e + sx, a.p + sx * a.t + j * kMoeTileM, r < kMoeTileM ? r : kMoeTileM, 0u};
+    }
+    for (uint32_t i = tid; i < a.shared * s3; i += blockDim.x) {
+        const uint32_t sx = i / s3, j = i % s3, r = a.t - j * kMoeTileM3;
+        t3[all3 + i] = r9vx_u32x4{a.e + sx, a.p + sx * a.t + j * kMoeTileM3, r < kMoeTileM3 ? r : kMoeTileM3, 0u};
+    }
+    if (tid == 0) {
+        uint32_t *status = reinterpret_cast<uint32_t *>(a.ws + L.status);
+        status[3] = all1 + a.shared * s1;
+        status[4] = all3 + a.shared * s3;
+    }
+}
 
 /* P <= 1024 pairs: everything in one workgroup of 1024 threads. */
 __global__ __launch_bounds__(1024) void sort_small_kernel(SortArgs a) {
@@ -136,98 +169,23 @@ __global__ __launch_bounds__(1024) void sort_small_kernel(SortArgs a) {
         offsets[tid] = off;
         offs[tid] = off;
     }
-    if (tid == 0) offsets[a.e] = all;
+    if (tid == 0) {
+        offsets[a.e] = all;
+        status[0] = bad_sh;
+    }
     __syncthreads();
-    uint32_t *pinfo = reinterpret_cast<uint32_t *>(a.ws + L.pinfo);
     if (valid) {
         uint32_t pos = offs[id] + rank;
         reinterpret_cast<uint32_t *>(a.ws + L.sorted)[pos] = tid;
         reinterpret_cast<uint32_t *>(a.ws + L.inv)[tid] = pos;
-        if (!bad_sh) pinfo[pos] = (id << 16) | (tid / a.k);
     }
-    if (bad_sh && in) pinfo[tid] = ~0u; /* refused: no position is valid */
-    /* compact work list of active experts, ascending id, then shared experts */
-    uint32_t act = (tid < a.e && tot > 0) ? 1u : 0u;
-    uint32_t n_act;
-    uint32_t idx = block_excl_scan(act, sh, n_act);
-    if (act) put_work(L, a.ws, idx, tid, off, tot);
-    if (tid < a.shared) put_work(L, a.ws, n_act + tid, a.e + tid, a.p + tid * a.t, a.t);
-    if (tid == 0) {
-        status[0] = bad_sh;
-        status[2] = n_act + a.shared;
-    }
-}
-
-/* P <= 64 pairs (decode): the same outputs from one wave.  Pair p is lane
- * p, so a lane's rank among its expert's peers is its stable (token, slot)
- * rank; expert counts go through a 4-KiB LDS table, and lane l owns experts
- * l*per .. l*per+per-1 for the ascending exclusive scans of the offsets and
- * of the active-expert work list. */
-__global__ __launch_bounds__(64) void sort_tiny_kernel(SortArgs a) {
-    __shared__ uint32_t cnt[kMoeMaxE];
-    const MoeLayout &L = a.L;
-    const uint32_t lane = threadIdx.x;
-    for (uint32_t i = lane; i < a.e; i += 64) cnt[i] = 0;
-    const bool in = lane < a.p;
-    const uint32_t id = in ? a.ids[lane] : 0u;
-    const bool valid = in && id < a.e;
-    const bool bad = __ballot(in && !valid) != 0ull;
-    const uint64_t peers = match_peers(id, valid, id_bits(a.e));
-    const uint32_t rw = rank_below(peers, lane);
-    __syncthreads();
-    if (valid && rw == 0) cnt[id] = (uint32_t)__popcll(peers);
-    __syncthreads();
-    const uint32_t per = (a.e + 63) / 64, e0 = lane * per;
-    uint32_t mine = 0, act_mine = 0;
-    for (uint32_t j = 0; j < per; ++j)
-        if (e0 + j < a.e) {
-            mine += cnt[e0 + j];
-            act_mine += cnt[e0 + j] ? 1u : 0u;
-        }
-    const uint32_t incl = wave_incl_scan(mine, lane), act_incl = wave_incl_scan(act_mine, lane);
-    const uint32_t all = __shfl(incl, 63, 64), n_act = __shfl(act_incl, 63, 64);
-    uint32_t *counts = reinterpret_cast<uint32_t *>(a.ws + L.counts);
-    uint32_t *offsets = reinterpret_cast<uint32_t *>(a.ws + L.offsets);
-    uint32_t *status = reinterpret_cast<uint32_t *>(a.ws + L.status);
-    __syncthreads(); /* every lane has read its counts before the table turns into offsets */
-    uint32_t run = incl - mine, idx = act_incl - act_mine;
-    for (uint32_t j = 0; j < per; ++j) {
-        const uint32_t e = e0 + j;
-        if (e >= a.e) break;
-        const uint32_t c = cnt[e];
-        counts[e] = c;
-        offsets[e] = run;
-        cnt[e] = run;
-        if (c) put_work(L, a.ws, idx++, e, run, c);
-        run += c;
-    }
-    if (lane == 0) offsets[a.e] = all;
-    __syncthreads();
-    uint32_t *pinfo = reinterpret_cast<uint32_t *>(a.ws + L.pinfo);
-    if (valid) {
-        const uint32_t pos = cnt[id] + rw;
-        reinterpret_cast<uint32_t *>(a.ws + L.sorted)[pos] = lane;
-        reinterpret_cast<uint32_t *>(a.ws + L.inv)[lane] = pos;
-        if (!bad) pinfo[pos] = (id << 16) | (lane / a.k);
-    }
-    if (bad && in) pinfo[lane] = ~0u; /* refused: no position is valid */
-    for (uint32_t s2 = lane; s2 < a.shared; s2 += 64) put_work(L, a.ws, n_act + s2, a.e + s2, a.p + s2 * a.t, a.t);
-    if (lane == 0) {
-        status[0] = bad ? R9VX_STATUS_BAD_EXPERT : 0u;
-        status[2] = n_act + a.shared;
-    }
+    put_tile_lists(a, tot, off, sh);
 }
 
 /* ---------------------------------------------------------------- sort: large */
 
-__global__ void sort_prep_kernel(uint8_t *ws, MoeLayout L) {
-    uint32_t *status = reinterpret_cast<uint32_t *>(ws + L.status);
-    status[0] = 0u; /* status bits */
-    status[1] = 0u; /* finished-expert counter */
-    status[2] = 0u; /* work items */
-}
-
-/* One 256-pair chunk per block: in-chunk ranks and per-expert chunk counts. */
+/* One 256-pair chunk per block: in-chunk ranks, per-expert chunk counts and
+ * whether the chunk holds an id >= E. */
 __global__ __launch_bounds__(256) void sort_count_kernel(SortArgs a) {
     __shared__ uint16_t cnt[4][kMoeMaxE];
     const MoeLayout &L = a.L;
@@ -239,11 +197,11 @@ __global__ __launch_bounds__(256) void sort_count_kernel(SortArgs a) {
     bool in = pair < a.p;
     uint32_t id = in ? a.ids[pair] : 0u;
     bool valid = in && id < a.e;
-    if (in && !valid) atomicOr(reinterpret_cast<uint32_t *>(a.ws + L.status), R9VX_STATUS_BAD_EXPERT);
     uint64_t peers = match_peers(id, valid, id_bits(a.e));
     uint32_t rw = rank_below(peers, lane);
     if (valid && rw == 0) cnt[w][id] = (uint16_t)__popcll(peers);
-    __syncthreads();
+    const int bad = __syncthreads_or(in && !valid);
+    if (tid == 0) reinterpret_cast<uint32_t *>(a.ws + L.cbad)[chunk] = bad ? 1u : 0u;
     if (valid) {
         uint32_t rank = rw;
         for (uint32_t i = 0; i < w; ++i) rank += cnt[i][id];
@@ -254,80 +212,61 @@ __global__ __launch_bounds__(256) void sort_count_kernel(SortArgs a) {
         cc[(uint64_t)e * nchunk + chunk] = (uint32_t)cnt[0][e] + cnt[1][e] + cnt[2][e] + cnt[3][e];
 }
 
-/* One wave per expert: exclusive scan of its chunk counts.  The last wave to
- * finish scans the expert totals into offsets and writes the work list. */
+/* One wave per expert: exclusive scan of its chunk counts, and its total. */
 __global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs a, uint32_t nchunk) {
     const MoeLayout &L = a.L;
     uint32_t lane = threadIdx.x & 63;
     uint32_t e = blockIdx.x * 4 + (threadIdx.x >> 6);
-    uint32_t *status = reinterpret_cast<uint32_t *>(a.ws + L.status);
-    uint32_t *counts = reinterpret_cast<uint32_t *>(a.ws + L.counts);
-    if (e < a.e) {
-        const uint32_t *cc = reinterpret_cast<const uint32_t *>(a.ws + L.ccount) + (uint64_t)e * nchunk;
-        uint32_t *cb = reinterpret_cast<uint32_t *>(a.ws + L.cbase) + (uint64_t)e * nchunk;
-        /* the first 512 chunk counts are loaded before the scan starts */
-        constexpr uint32_t kPre = 8;
-        uint32_t pre[kPre];
+    if (e >= a.e) return;
+    const uint32_t *cc = reinterpret_cast<const uint32_t *>(a.ws + L.ccount) + (uint64_t)e * nchunk;
+    uint32_t *cb = reinterpret_cast<uint32_t *>(a.ws + L.cbase) + (uint64_t)e * nchunk;
+    /* the first 512 chunk counts are loaded before the scan starts */
+    constexpr uint32_t kPre = 8;
+    uint32_t pre[kPre];
 #pragma unroll
-        for (uint32_t i = 0; i < kPre; ++i) {
-            const uint32_t c = 64 * i + lane;
-            pre[i] = c < nchunk ? cc[c] : 0u;
-        }
-        uint32_t carry = 0;
-#pragma unroll
-        for (uint32_t i = 0; i < kPre; ++i) {
-            if (64 * i >= nchunk) break;
-            const uint32_t c = 64 * i + lane, v = pre[i];
-            const uint32_t inc = wave_incl_scan(v, lane);
-            if (c < nchunk) cb[c] = carry + inc - v;
-            carry += __shfl(inc, 63, 64);
-        }
-        for (uint32_t c0 = 64 * kPre; c0 < nchunk; c0 += 64) {
-            uint32_t c = c0 + lane;
-            uint32_t v = c < nchunk ? cc[c] : 0u;
-            uint32_t inc = wave_incl_scan(v, lane);
-            if (c < nchunk) cb[c] = carry + inc - v;
-            carry += __shfl(inc, 63, 64);
-        }
-        if (lane == 0) counts[e] = carry;
-        __threadfence();
-        uint32_t prev = 0;
-        if (lane == 0) prev = atomicAdd(&status[1], 1u);
-        prev = __shfl(prev, 0, 64);
-        if (prev != a.e - 1) return;
-        __threadfence();
-        /* last expert finished: scan the totals (this wave only), every
-         * count loaded before the first scan step so that the loads' latency
-         * is paid once */
-        uint32_t *offsets = reinterpret_cast<uint32_t *>(a.ws + L.offsets);
-        constexpr uint32_t kPer = kMoeMaxE / 64;
-        uint32_t tot[kPer];
-#pragma unroll
-        for (uint32_t i = 0; i < kPer; ++i) {
-            const uint32_t ee = 64 * i + lane;
-            tot[i] = ee < a.e ? __hip_atomic_load(&counts[ee], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
-        }
-        uint32_t base = 0, nact = 0;
-#pragma unroll
-        for (uint32_t i = 0; i < kPer; ++i) {
-            const uint32_t e0 = 64 * i;
-            if (e0 >= a.e) break;
-            uint32_t ee = e0 + lane;
-            uint32_t v = tot[i];
-            uint32_t inc = wave_incl_scan(v, lane);
-            uint32_t act = v > 0 ? 1u : 0u;
-            uint32_t ainc = wave_incl_scan(act, lane);
-            if (ee < a.e) {
-                offsets[ee] = base + inc - v;
-                if (act) put_work(L, a.ws, nact + ainc - 1, ee, base + inc - v, v);
-            }
-            base += __shfl(inc, 63, 64);
-            nact += __shfl(ainc, 63, 64);
-        }
-        if (lane == 0) offsets[a.e] = base;
-        for (uint32_t s = lane; s < a.shared; s += 64) put_work(L, a.ws, nact + s, a.e + s, a.p + s * a.t, a.t);
-        if (lane == 0) status[2] = nact + a.shared;
+    for (uint32_t i = 0; i < kPre; ++i) {
+        const uint32_t c = 64 * i + lane;
+        pre[i] = c < nchunk ? cc[c] : 0u;
     }
+    uint32_t carry = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < kPre; ++i) {
+        if (64 * i >= nchunk) break;
+        const uint32_t c = 64 * i + lane, v = pre[i];
+        const uint32_t inc = wave_incl_scan(v, lane);
+        if (c < nchunk) cb[c] = carry + inc - v;
+        carry += __shfl(inc, 63, 64);
+    }
+    for (uint32_t c0 = 64 * kPre; c0 < nchunk; c0 += 64) {
+        uint32_t c = c0 + lane;
+        uint32_t v = c < nchunk ? cc[c] : 0u;
+        uint32_t inc = wave_incl_scan(v, lane);
+        if (c < nchunk) cb[c] = carry + inc - v;
+        carry += __shfl(inc, 63, 64);
+    }
+    if (lane == 0) reinterpret_cast<uint32_t *>(a.ws + L.counts)[e] = carry;
+}
+
+/* One workgroup (blockDim.x >= E): the status word, the expert offsets (an
+ * exclusive scan of the totals) and the tile lists. */
+__global__ __launch_bounds__(1024) void sort_finish_kernel(SortArgs a, uint32_t nchunk) {
+    __shared__ uint32_t sh[16];
+    const MoeLayout &L = a.L;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t *cbad = reinterpret_cast<const uint32_t *>(a.ws + L.cbad);
+    uint32_t bad = 0;
+    for (uint32_t c = tid; c < nchunk; c += blockDim.x) bad |= cbad[c];
+    const uint32_t tot = tid < a.e ? reinterpret_cast<const uint32_t *>(a.ws + L.counts)[tid] : 0u;
+    const int any_bad = __syncthreads_or(bad != 0u);
+    uint32_t all;
+    const uint32_t off = block_excl_scan(tot, sh, all);
+    uint32_t *offsets = reinterpret_cast<uint32_t *>(a.ws + L.offsets);
+    if (tid < a.e) offsets[tid] = off;
+    if (tid == 0) {
+        offsets[a.e] = all;
+        reinterpret_cast<uint32_t *>(a.ws + L.status)[0] = any_bad ? R9VX_STATUS_BAD_EXPERT : 0u;
+    }
+    put_tile_lists(a, tot, off, sh);
 }
 
 __global__ __launch_bounds__(256) void sort_place_kernel(SortArgs a, uint32_t nchunk) {
@@ -866,18 +805,14 @@ static uint32_t lpr_for(uint32_t k, uint32_t &nseg) {
 
 int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s) {
     SortArgs a{p.ids, p.ws, L, p.t * p.k, p.e, p.k, p.t, p.shared};
-    if (a.p <= 64) {
-        hipLaunchKernelGGL(sort_tiny_kernel, dim3(1), dim3(64), 0, s, a);
-        return (int)hipGetLastError();
-    }
     if (a.p <= 1024) {
         hipLaunchKernelGGL(sort_small_kernel, dim3(1), dim3(1024), 0, s, a);
         return (int)hipGetLastError();
     }
     uint32_t nchunk = (a.p + 255) / 256;
-    hipLaunchKernelGGL(sort_prep_kernel, dim3(1), dim3(1), 0, s, p.ws, L);
     hipLaunchKernelGGL(sort_count_kernel, dim3(nchunk), dim3(256), 0, s, a);
     hipLaunchKernelGGL(sort_scan_kernel, dim3((p.e + 3) / 4), dim3(256), 0, s, a, nchunk);
+    hipLaunchKernelGGL(sort_finish_kernel, dim3(1), dim3(1024), 0, s, a, nchunk);
     hipLaunchKernelGGL(sort_place_kernel, dim3(nchunk), dim3(256), 0, s, a, nchunk);
     return (int)hipGetLastError();
 }

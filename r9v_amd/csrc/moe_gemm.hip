@@ -5,9 +5,9 @@
  * T0 meaning: crates/r9v-t0/src/moe_ffn.rs:527-639 (per expert: gather rows,
  * gate/up Branch-D GEMM, act_mul SiLU, down GEMM); the combine is moe.hip's.
  *
- *  tiles : each work item (expert with n pairs, or shared expert with t rows)
- *          becomes ceil(n / 256) row tiles (ceil(n / 128) for the IQ3_S
- *          gate/up kernel); a one-workgroup scan lays them out.
+ *  tiles : each expert with n pairs (or shared expert with t rows) is
+ *          ceil(n / 256) row tiles (ceil(n / 128) for the LDS-decoded
+ *          kernels), listed by the sort (moe.hip).
  *  gate/up: a workgroup owns 256 permuted rows x 128 columns j of h; its
  *          weight tile is gate rows j0.. and the matching up rows Dff+j0..,
  *          and a wave's two column tiles are a gate tile and its up tile, so
@@ -76,56 +76,6 @@ __device__ __forceinline__ float swiglu_fast(float g, float u) {
 __device__ __forceinline__ uint32_t row_token(const GroupedArgs &a, uint32_t expert, uint32_t pos) {
     if (expert >= a.e) return pos - (a.p + (expert - a.e) * a.t);
     return ws_u32(a, a.L.sorted)[pos] / a.k;
-}
-
-/* Scans the work items' tile counts (TM rows per tile) into `tiles`;
- * returns the tile count (in every thread). */
-template <uint32_t TM>
-__device__ uint32_t scan_tiles(const r9vx_u32x4 *work, uint32_t nwork, r9vx_u32x4 *tiles, uint32_t *sh) {
-    uint32_t base = 0;
-    for (uint32_t w0 = 0; w0 < nwork; w0 += 1024) {
-        uint32_t i = w0 + threadIdx.x;
-        r9vx_u32x4 wk = i < nwork ? work[i] : r9vx_u32x4{0u, 0u, 0u, 0u};
-        uint32_t nt = (wk.z + TM - 1) / TM;
-        /* block exclusive scan of nt */
-        uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-        uint32_t inc = nt;
-        for (int off = 1; off < 64; off <<= 1) {
-            uint32_t o = __shfl_up(inc, off, 64);
-            if (lane >= (uint32_t)off) inc += o;
-        }
-        __syncthreads();
-        if (lane == 63) sh[wv] = inc;
-        __syncthreads();
-        uint32_t pre = 0, tot = 0;
-        for (uint32_t q = 0; q < 16; ++q) {
-            if (q < wv) pre += sh[q];
-            tot += sh[q];
-        }
-        uint32_t first = base + pre + inc - nt;
-        for (uint32_t j = 0; j < nt; ++j) {
-            uint32_t rows = wk.z - j * TM < TM ? wk.z - j * TM : TM;
-            tiles[first + j] = r9vx_u32x4{wk.x, wk.y + j * TM, rows, 0u};
-        }
-        base += tot;
-        __syncthreads();
-    }
-    return base;
-}
-
-/* One workgroup: the work items' 128-row tiles (status[3] of them) and
- * 256-row tiles (status[4]). */
-__global__ __launch_bounds__(1024) void build_tiles_kernel(GroupedArgs a) {
-    __shared__ uint32_t sh[16];
-    uint32_t *status = reinterpret_cast<uint32_t *>(a.ws + a.L.status);
-    const uint32_t nwork = status[2];
-    const r9vx_u32x4 *work = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.work);
-    const uint32_t n128 = scan_tiles<kBM>(work, nwork, reinterpret_cast<r9vx_u32x4 *>(a.ws + a.L.tiles), sh);
-    const uint32_t n256 = scan_tiles<kMoeTileM3>(work, nwork, reinterpret_cast<r9vx_u32x4 *>(a.ws + a.L.tiles3), sh);
-    if (threadIdx.x == 0) {
-        status[3] = n128;
-        status[4] = n256;
-    }
 }
 
 /* ---------------------------------------------------------------- gate/up */
@@ -512,7 +462,6 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
         int rc = r9vx_launch_x_to_f16(p.x, p.t, p.dm, reinterpret_cast<_Float16 *>(p.ws + L.x16),
                                       reinterpret_cast<float *>(p.ws + L.xscale), p.scheme_gu, s);
         if (rc) return rc;
-        hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(1024), 0, s, a);
     }
     /* upper bounds on row tiles: ceil(P/TM) + one partial tile per work item */
     const uint32_t max_tiles = (a.p + kBM - 1) / kBM + (a.p < p.e ? a.p : p.e) +

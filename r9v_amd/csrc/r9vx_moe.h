@@ -3,8 +3,7 @@
  * crates/r9v-kgen/src/abi/workspace.rs:13-40) and the stage launchers.
  *
  * Workspace regions (each 256-byte aligned), sized for t_bucket tokens:
- *   status  u32[16]  [0] status bits, [1] scan counter, [2] work items,
- *                    [3] 128-row tiles, [4] 256-row tiles
+ *   status  u32[16]  [0] status bits, [3] 128-row tiles, [4] 256-row tiles
  *   counts  u32[E]   pairs per expert
  *   offsets u32[E+1] exclusive scan of counts
  *   sorted  u32[P]   pair index (token*K + slot) at each sorted position
@@ -12,8 +11,9 @@
  *   rank    u32[P]   rank of a pair among its expert's pairs in its chunk
  *   ccount  u32[E*C] per-expert counts of each 256-pair chunk
  *   cbase   u32[E*C] exclusive scan of ccount over chunks
- *   work    u32x4[E+S] (expert, first position, pair count, 0) of active experts
- *   tiles   u32x4[...] grouped-GEMM tile schedule, 128-row tiles
+ *   cbad    u32[C]   1 where the chunk holds an id >= E
+ *   tiles   u32x4[...] grouped-GEMM tile schedule (expert, first position,
+ *                      rows, 0), 128-row tiles
  *   tiles3  u32x4[...] the same work in 256-row tiles (the r9vx_mma3.h kernels)
  *   h       f32[(P + S*T) * Dff]  SwiGLU rows in sorted order (decode path: pair
  *                                 order), shared rows after
@@ -27,8 +27,6 @@
  *                                 weights' K group order (grouped GEMM)
  *   x16     fp16[T * Dm], xscale f32[T]  scaled activations in the gate/up
  *                                 weights' K group order (grouped GEMM)
- *   pinfo   u32[P]   expert << 16 | token of each sorted position, all ones
- *                    when the call is refused (decode path)
  */
 #ifndef R9VX_MOE_H
 #define R9VX_MOE_H
@@ -44,8 +42,8 @@ constexpr uint32_t kMoeTileM = 128;  /* grouped-GEMM rows per tile */
 constexpr uint32_t kMoeTileM3 = 256; /* rows per tile of the r9vx_mma3.h grouped GEMMs */
 
 struct MoeLayout {
-    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, work, tiles, tiles3, h, o, hmax, h16, x16,
-        xscale, pinfo, total;
+    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, cbad, tiles, tiles3, h, o, hmax, h16, x16,
+        xscale, total;
     uint32_t max_tiles, max_tiles3;
 };
 
@@ -71,7 +69,7 @@ inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint
     L.rank = take(4 * p);
     L.ccount = take(4ull * e * nchunk);
     L.cbase = take(4ull * e * nchunk);
-    L.work = take(16ull * (e + shared));
+    L.cbad = take(4 * nchunk);
     L.tiles = take(16ull * L.max_tiles + 16);
     L.tiles3 = take(16ull * L.max_tiles3 + 16);
     L.h = take(4ull * rows * dff);
@@ -80,7 +78,6 @@ inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint
     L.h16 = take(2ull * rows * dff);
     L.x16 = take(2ull * t_bucket * dm);
     L.xscale = take(4ull * t_bucket);
-    L.pinfo = take(4 * p);
     L.total = off;
     return L;
 }
