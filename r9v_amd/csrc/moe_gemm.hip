@@ -388,11 +388,15 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
      * a power of two per (row, 64-column block), the block being this wave's
      * two column tiles: its max is this lane's 32 values and lane l ^ 32's.
      * The scale puts the block max in [2^14, 2^15); its inverse is stored
-     * beside the rows for the combine. */
+     * beside the rows for the combine.  The fp16 tile is staged in LDS (row
+     * R's 8-byte chunk c at chunk c ^ (R & 31): the 32 rows one write
+     * instruction covers hit distinct banks), then each row leaves as 32
+     * lanes x 16 contiguous bytes. */
     const uint64_t nrows_all = (uint64_t)a.p + (uint64_t)a.shared * a.t;
     _Float16 *o16 = reinterpret_cast<_Float16 *>(a.ws + a.L.o);
     float *oscale = reinterpret_cast<float *>(a.ws + a.L.o + r9vx_moe_oscale_offset(nrows_all, a.dm));
-    const uint32_t blk = (n0 + 64 * cq) / 64, nblk = a.dm / 64, cb = n0 + 64 * cq + 4 * (lane >> 5);
+    const uint32_t blk = (n0 + 64 * cq) / 64, nblk = a.dm / 64;
+    uint8_t *const ot = m3_out_tile(sm);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         if ((uint32_t)t >= nr) break;
@@ -408,17 +412,28 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
         int e = 0;
         (void)frexpf(m, &e); /* m = f 2^e, f in [0.5, 1) */
         const float f = ldexpf(sc, 15 - e); /* a power of two: acc * f = (acc * sc) 2^(15 - e) exactly */
-        if (rl >= rows) continue;
-        _Float16 *orow = o16 + (uint64_t)(pos0 + rl) * a.dm + cb;
+        uint8_t *const orow = ot + rl * 512u;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const r9vx_u32x2 v{pack_h2h((_Float16)(acc[t][j][4 * g] * f), (_Float16)(acc[t][j][4 * g + 1] * f)),
-                                   pack_h2h((_Float16)(acc[t][j][4 * g + 2] * f), (_Float16)(acc[t][j][4 * g + 3] * f))};
-                *reinterpret_cast<r9vx_u32x2 *>(orow + 32 * j + 8 * g) = v;
+                const uint32_t chunk = (16u * cq + 8u * j + 2u * g + (lane >> 5)) ^ (rl & 31u);
+                *reinterpret_cast<r9vx_u32x2 *>(orow + 8u * chunk) =
+                    r9vx_u32x2{pack_h2h((_Float16)(acc[t][j][4 * g] * f), (_Float16)(acc[t][j][4 * g + 1] * f)),
+                               pack_h2h((_Float16)(acc[t][j][4 * g + 2] * f), (_Float16)(acc[t][j][4 * g + 3] * f))};
             }
-        if (lane < 32) oscale[(uint64_t)(pos0 + rl) * nblk + blk] = ldexpf(1.0f, e - 15);
+        if (lane < 32 && rl < rows) oscale[(uint64_t)(pos0 + rl) * nblk + blk] = ldexpf(1.0f, e - 15);
+    }
+    __syncthreads();
+    const uint32_t q = lane & 31;
+#pragma unroll 4
+    for (uint32_t i = 0; i < 16; ++i) {
+        const uint32_t R = 16 * i + 2 * wv + (lane >> 5);
+        if (R >= rows) break; /* rows grow with i */
+        const uint32_t s = R & 31u;
+        r9vx_u32x4 v = *reinterpret_cast<const r9vx_u32x4 *>(ot + R * 512u + 16u * (q ^ (s >> 1)));
+        if (s & 1u) v = r9vx_u32x4{v.z, v.w, v.x, v.y}; /* the granule's halves were swapped */
+        *reinterpret_cast<r9vx_u32x4 *>(o16 + (uint64_t)(pos0 + R) * a.dm + n0 + 8 * q) = v;
     }
 }
 

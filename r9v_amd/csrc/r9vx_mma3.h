@@ -29,6 +29,8 @@
 #ifndef R9VX_MMA3_H
 #define R9VX_MMA3_H
 
+#include <stddef.h>
+
 #include "r9vx_mma2.h"
 
 namespace r9vx {
@@ -47,6 +49,11 @@ struct M3Lds {
     uint8_t a[kM3AStages][kM3Stage];
     uint8_t b[kM3BStages][kM3Stage];
 };
+static_assert(offsetof(M3Lds, b) == offsetof(M3Lds, a) + kM3AStages * kM3Stage, "a and b are contiguous");
+
+/* After the main loop: a and b as one 256 x 512-byte staging tile (an epilogue
+ * may stage a 256 x 256 fp16 output tile there). */
+__device__ __forceinline__ uint8_t *m3_out_tile(M3Lds &sm) { return reinterpret_cast<uint8_t *>(&sm) + offsetof(M3Lds, a); }
 
 __device__ __forceinline__ uint32_t pack_h2h(_Float16 a, _Float16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
