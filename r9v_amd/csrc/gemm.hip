@@ -45,13 +45,16 @@ struct GemmArgs {
 /* PERM = 0: natural order; R9VX_SCHEME_Q4_K / R9VX_SCHEME_IQ4_XS: each 64-column
  * step stored in that scheme's group order (r9vx_mma2.h). */
 template <int PERM>
-__global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t *__restrict__ x, uint32_t k,
+__global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t *__restrict__ x, uint32_t m, uint32_t k,
                                                        _Float16 *__restrict__ x16, float *__restrict__ scale) {
-    __shared__ float red[4];
-    const uint32_t row = blockIdx.x;
+    /* one wave per row, four rows per workgroup: no barrier */
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= m) return;
     const uint16_t *xr = x + (uint64_t)row * k;
     float mx = 0.f;
-    for (uint32_t c = threadIdx.x * 8; c < k; c += 256 * 8) {
+#pragma unroll 4
+    for (uint32_t c = lane * 8; c < k; c += 64 * 8) {
         r9vx_u32x4 v = *reinterpret_cast<const r9vx_u32x4 *>(xr + c);
         uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -61,14 +64,12 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t *__restric
         }
     }
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const int e = row_shift(mx);
     const float inv = ldexpf(1.0f, -e);
-    if (threadIdx.x == 0) scale[row] = ldexpf(1.0f, e);
+    if (lane == 0) scale[row] = ldexpf(1.0f, e);
     _Float16 *orow = x16 + (uint64_t)row * k;
-    for (uint32_t c = threadIdx.x * 8; c < k; c += 256 * 8) {
+#pragma unroll 4
+    for (uint32_t c = lane * 8; c < k; c += 64 * 8) {
         uint32_t w[4];
         if constexpr (PERM == 0) {
             r9vx_u32x4 v = *reinterpret_cast<const r9vx_u32x4 *>(xr + c);
@@ -282,11 +283,11 @@ size_t r9vx_gemm_workspace_bytes(uint32_t m_bucket, uint32_t k) {
 int r9vx_launch_x_to_f16(const uint16_t *x, uint32_t m, uint32_t k, _Float16 *x16, float *scale,
                          uint32_t perm_scheme, hipStream_t stream) {
     if (perm_scheme == R9VX_SCHEME_Q4_K)
-        hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3(m), dim3(256), 0, stream, x, k, x16, scale);
+        hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3((m + 3) / 4), dim3(256), 0, stream, x, m, k, x16, scale);
     else if (perm_scheme == R9VX_SCHEME_IQ4_XS)
-        hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3(m), dim3(256), 0, stream, x, k, x16, scale);
+        hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3((m + 3) / 4), dim3(256), 0, stream, x, m, k, x16, scale);
     else
-        hipLaunchKernelGGL(x_to_f16_kernel<0>, dim3(m), dim3(256), 0, stream, x, k, x16, scale);
+        hipLaunchKernelGGL(x_to_f16_kernel<0>, dim3((m + 3) / 4), dim3(256), 0, stream, x, m, k, x16, scale);
     return (int)hipGetLastError();
 }
 
@@ -320,10 +321,11 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     const bool big = !split && (uint64_t)((p.m + 255) / 256) * ((p.n + 255) / 256) >= 256;
     if (big) {
         if (p.scheme == R9VX_SCHEME_Q4_K)
-            hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3(p.m), dim3(256), 0, stream, p.x, p.k, x16, scale);
-        else
-            hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3(p.m), dim3(256), 0, stream, p.x, p.k, x16,
+            hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3((p.m + 3) / 4), dim3(256), 0, stream, p.x, p.m, p.k, x16,
                                scale);
+        else
+            hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3((p.m + 3) / 4), dim3(256), 0, stream, p.x, p.m, p.k,
+                               x16, scale);
         a.m_tiles = (p.m + kM2Rows - 1) / kM2Rows;
         a.n_tiles = (p.n + kM2Cols - 1) / kM2Cols;
         dim3 grid(a.m_tiles * a.n_tiles);
@@ -333,7 +335,7 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
             hipLaunchKernelGGL((gemm2_kernel<R9VX_SCHEME_IQ4_XS>), grid, dim3(512), 0, stream, a);
         return (int)hipGetLastError();
     }
-    hipLaunchKernelGGL(x_to_f16_kernel<0>, dim3(p.m), dim3(256), 0, stream, p.x, p.k, x16, scale);
+    hipLaunchKernelGGL(x_to_f16_kernel<0>, dim3((p.m + 3) / 4), dim3(256), 0, stream, p.x, p.m, p.k, x16, scale);
     a.m_tiles = (p.m + 127) / 128;
     a.n_tiles = (p.n + 255) / 256;
     dim3 grid(a.m_tiles * a.n_tiles);

@@ -65,27 +65,26 @@ __host__ __device__ constexpr uint32_t group_k(uint32_t q, uint32_t i) {
  * tell a copy into one LDS stage from reads of another and count only the
  * loads they know of, so with compiler-visible loads every step would stall
  * on the prefetches of later steps.  touch() marks the point after that wait
- * from which the registers hold the loaded data.
+ * from which the registers hold the loaded data.  Each load's destination is
+ * tied in and out ("+v") and nothing is built from it before the wait, so
+ * the register the load writes is the one later read, also for a value
+ * carried across the loop back-edge.
  */
 template <int SCHEME>
 __device__ __forceinline__ void load_bpay(const uint8_t *row, uint32_t kt, uint32_t h, r9vx_u32x4 &p) {
     const uint32_t blk = kt >> 2, ks = kt & 3;
     const uint8_t *pp = SCHEME == R9VX_SCHEME_Q4_K ? row + (uint64_t)blk * R9VX_Q4K_BYTES + 16 + 32 * ks + 16 * h
                                                    : row + (uint64_t)blk * R9VX_IQ4XS_BYTES + 8 + 32 * ks + 16 * h;
-    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(p) : "v"(pp) : "memory");
+    asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(p) : "v"(pp) : "memory");
 }
 
 template <int SCHEME>
 __device__ __forceinline__ void load_bhdr(const uint8_t *row, uint32_t blk, r9vx_u32x4 &hd) {
-    if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
-        const uint8_t *bp = row + (uint64_t)blk * R9VX_Q4K_BYTES;
-        asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(hd) : "v"(bp) : "memory");
-    } else {
-        const uint8_t *bp = row + (uint64_t)blk * R9VX_IQ4XS_BYTES;
-        r9vx_u32x2 hh;
-        asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(hh) : "v"(bp) : "memory");
-        hd = r9vx_u32x4{hh.x, hh.y, 0u, 0u};
-    }
+    /* Q4_K: the 16-byte header; IQ4_XS: the block's first 16 bytes (its
+     * 8-byte header and 8 payload bytes, inside the 136-byte block), of which
+     * .x / .y are used */
+    const uint8_t *bp = row + (uint64_t)blk * (SCHEME == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : R9VX_IQ4XS_BYTES);
+    asm volatile("global_load_dwordx4 %0, %1, off" : "+v"(hd) : "v"(bp) : "memory");
 }
 
 template <int SCHEME>
@@ -267,6 +266,12 @@ __device__ __forceinline__ void m2_mainloop(uint8_t *const (&stages)[4], const _
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     r9vx_u32x4 pay[4][NWN], hcur[NWN], hnext[NWN];
+#pragma unroll
+    for (int j = 0; j < NWN; ++j) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pay[q][j] = r9vx_u32x4{0u, 0u, 0u, 0u};
+        hnext[j] = r9vx_u32x4{0u, 0u, 0u, 0u};
+    }
     /* prologue in the steady-state order: A0 A1 H(blk 0) P0 | A2 P1 */
     dma_a_step(stages[0], asrc, 0, wave);
     dma_a_step(stages[1], asrc, 1, wave);

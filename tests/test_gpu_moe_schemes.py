@@ -56,6 +56,35 @@ def test_moe_ffn_expert_schemes(gu_s, dn_s, t):
     check_close(y.cpu().numpy(), ref, f"{NAMES[gu_s]}/{NAMES[dn_s]} t={t}")
 
 
+BIG_PAIRS = [(ffi.IQ3_S, ffi.Q4_K), (ffi.IQ3_S, ffi.IQ4_XS), (ffi.Q6_K, ffi.Q8_0)]
+
+
+@pytest.mark.parametrize("t", [4, 200])
+@pytest.mark.parametrize("gu_s,dn_s", BIG_PAIRS, ids=[f"{NAMES[g]}-{NAMES[d]}" for g, d in BIG_PAIRS])
+def test_moe_ffn_expert_schemes_model_shape(gu_s, dn_s, t):
+    """A model-like shape: E = 64, Dm = 2048 (several K segments in the
+    decode GEMVs), Dff = 768 (three 256-column blocks), top-8, expert tiles
+    past 128 rows at t = 200; tokens are independent, so at t = 200 the
+    oracle runs on 16 sampled tokens."""
+    e, k, dm, dff = 64, 8, 2048, 768
+    seed = 4100 + 7 * gu_s + dn_s + t
+    logits = synth.zipf_logits(seed, t, e)
+    ids, w = O.moe_route(logits, k)
+    gu = synth.quant_weights(gu_s, seed + 1, e * 2 * dff, dm)
+    dn = synth.quant_weights(dn_s, seed + 2, e * dm, dff)
+    x = synth.normal_bf16(seed + 3, (t, dm))
+    gw, gsc = device_weights(gu, gu_s, e * 2 * dff, dm)
+    dw, dsc = device_weights(dn, dn_s, e * dm, dff)
+    y, ws, st = ffi.moe_ffn(dev(x.view(np.int16)).view(torch.bfloat16), dev(ids.view(np.int32)), dev(w), gw, dw, e,
+                            dff, gate_up_scheme=gu_s, down_scheme=dn_s, w_gate_up_scales=gsc, w_down_scales=dsc)
+    torch.cuda.synchronize()
+    assert ffi.moe_ffn_status(st, ws) == 0
+    rows = np.arange(t) if t <= 8 else np.random.default_rng(seed).choice(t, 16, replace=False)
+    ref = O.moe_ffn(np.ascontiguousarray(x[rows]), O.BF16, np.ascontiguousarray(ids[rows]),
+                    np.ascontiguousarray(w[rows]), e, dff, gu, dn, scheme_gu=gu_s, scheme_dn=dn_s)
+    check_close(y.cpu().numpy()[rows], ref, f"{NAMES[gu_s]}/{NAMES[dn_s]} t={t} E={e} Dm={dm} Dff={dff}")
+
+
 def test_split_scales_are_required_and_inline_scales_refused():
     e, k, dm, dff, t = 4, 2, 256, 256, 3
     x = dev(synth.normal_bf16(1, (t, dm)).view(np.int16)).view(torch.bfloat16)
