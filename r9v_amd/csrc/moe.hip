@@ -321,8 +321,6 @@ constexpr int kDecPairs = R9VX_DEC_GU_PAIRS;
 constexpr int kDecDnRows = R9VX_DEC_DN_ROWS;
 constexpr int kDecWaves = R9VX_DEC_WAVES;
 
-/* Token and expert of sorted position pos (shared experts after the P
- * routed pairs, T rows each); false when the call was refused. */
 /* Token and expert of row pos: the decode path keeps the rows in pair order
  * (pos = token * K + slot, no sort pass), the shared experts' T rows each
  * after the P pairs; false for an id >= E (nothing is read for it, and the
@@ -346,10 +344,10 @@ __device__ __forceinline__ bool pos_meta(const FfnArgs &a, uint32_t pos, uint32_
 constexpr uint32_t kDecSteps = R9VX_DEC_STEPS;
 
 /* A wave's units: [u0, u0 + n), n <= upw, in sorted-position order, so that
- * they walk consecutive weight rows; the host picks upw = max(1, kDecSteps /
- * nseg) capped at the row groups per position, so a wave's units share at
- * most two positions (expert, activation row).  A wave with more than
- * kDecSteps steps (nseg > kDecSteps) takes them kDecSteps at a time. */
+ * they walk consecutive weight rows; the host caps upw at the row groups per
+ * position, so a wave's units share at most two positions (expert,
+ * activation row).  A wave with more than kDecSteps steps takes them
+ * kDecSteps at a time. */
 __device__ __forceinline__ bool wave_units(uint32_t units, uint32_t upw, uint32_t &u0, uint32_t &n) {
     const uint32_t gw = __builtin_amdgcn_readfirstlane(blockIdx.x * kDecWaves + (threadIdx.x >> 6));
     u0 = gw * upw;
@@ -372,13 +370,186 @@ __device__ __forceinline__ void advance(Cur &c, uint32_t nseg, uint32_t groups) 
     }
 }
 
+/* Weight registers of one gate/up step: chunk ci of kPairs (gate, up) row
+ * pairs. */
+template <int GU>
+struct GuRegs {
+    static constexpr bool kIq3 = GU == R9VX_SCHEME_IQ3_S;
+    static constexpr bool kSplit = GU == R9VX_SCHEME_Q8_0 || GU == R9VX_SCHEME_Q6_K;
+    using Pay = typename std::conditional<kIq3 || kSplit, Payload2, r9vx_u32x4>::type;
+    Pay qg[kDecPairs], qu[kDecPairs];
+    Hdr hg[kDecPairs], hu[kDecPairs];
+};
+
+/* Loads of a gate/up step: rows (g * kPairs + r) * rpi + slot of the
+ * expert's gate half and the same rows of its up half (clamped to Dff - 1;
+ * the rows past Dff are never stored). */
+template <int GU>
+__device__ __forceinline__ void gu_load(const FfnArgs &a, uint32_t expert, uint32_t g, uint32_t ci, uint32_t rpi,
+                                        uint32_t slot, GuRegs<GU> &w) {
+    const uint8_t *wexp = a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes;
+    const uint16_t *sexp = GuRegs<GU>::kSplit ? a.s_gu + (uint64_t)expert * 2 * a.dff * a.gu_srow : nullptr;
+#pragma unroll
+    for (int r = 0; r < kDecPairs; ++r) {
+        const uint32_t row = (g * kDecPairs + r) * rpi + slot;
+        const uint32_t rr = row < a.dff ? row : a.dff - 1;
+        if constexpr (GuRegs<GU>::kSplit) {
+            load_chunk_split<GU>(wexp + (uint64_t)rr * a.gu_row_bytes, sexp + (uint64_t)rr * a.gu_srow, ci, w.qg[r],
+                                 w.hg[r]);
+            load_chunk_split<GU>(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes,
+                                 sexp + (uint64_t)(a.dff + rr) * a.gu_srow, ci, w.qu[r], w.hu[r]);
+        } else if constexpr (GuRegs<GU>::kIq3) {
+            load_chunk_iq3s(wexp + (uint64_t)rr * a.gu_row_bytes, ci, w.qg[r], w.hg[r]);
+            load_chunk_iq3s(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes, ci, w.qu[r], w.hu[r]);
+        } else {
+            load_chunk<GU>(wexp + (uint64_t)rr * a.gu_row_bytes, ci, w.qg[r], w.hg[r]);
+            load_chunk<GU>(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes, ci, w.qu[r], w.hu[r]);
+        }
+    }
+}
+
+template <int GU>
+__device__ __forceinline__ void gu_dot(const GuRegs<GU> &w, uint32_t ci, const XChunk<GU, false> (&xc)[1],
+                                       float (&ag)[kDecPairs][1], float (&au)[kDecPairs][1], const uint32_t *lut) {
+#pragma unroll
+    for (int r = 0; r < kDecPairs; ++r) {
+        if constexpr (GuRegs<GU>::kSplit) {
+            chunk_dot_split<GU, 1>(w.qg[r], w.hg[r], ci & 7, xc, ag[r]);
+            chunk_dot_split<GU, 1>(w.qu[r], w.hu[r], ci & 7, xc, au[r]);
+        } else if constexpr (GuRegs<GU>::kIq3) {
+            chunk_dot_iq3s<1>(w.qg[r], w.hg[r], ci & 7, xc, ag[r], lut);
+            chunk_dot_iq3s<1>(w.qu[r], w.hu[r], ci & 7, xc, au[r], lut);
+        } else {
+            chunk_dot<GU, false, 1>(w.qg[r], w.hg[r], ci & 7, xc, ag[r], lut);
+            chunk_dot<GU, false, 1>(w.qu[r], w.hu[r], ci & 7, xc, au[r], lut);
+        }
+    }
+}
+
+/* Weight registers of one down step: chunk ci of kDnRows rows. */
+template <int DN>
+struct DnRegs {
+    static constexpr bool kIq3 = DN == R9VX_SCHEME_IQ3_S;
+    static constexpr bool kSplit = DN == R9VX_SCHEME_Q8_0 || DN == R9VX_SCHEME_Q6_K;
+    static constexpr bool kF32x = kIq3 || kSplit; /* chunk_dot_f32x against the f32 h rows */
+    static constexpr bool kF16 = DN == R9VX_SCHEME_Q4_K;
+    using Pay = typename std::conditional<kF32x, Payload2, r9vx_u32x4>::type;
+    Pay q[kDecDnRows];
+    Hdr hd[kDecDnRows];
+};
+
+template <int DN>
+__device__ __forceinline__ void dn_load(const FfnArgs &a, uint32_t expert, uint32_t g, uint32_t ci, uint32_t rpi,
+                                        uint32_t slot, DnRegs<DN> &w) {
+    const uint8_t *wexp = a.w_dn + (uint64_t)expert * a.dm * a.dn_row_bytes;
+    const uint16_t *sexp = DnRegs<DN>::kSplit ? a.s_dn + (uint64_t)expert * a.dm * a.dn_srow : nullptr;
+#pragma unroll
+    for (int r = 0; r < kDecDnRows; ++r) {
+        const uint32_t row = (g * kDecDnRows + r) * rpi + slot;
+        const uint32_t rr = row < a.dm ? row : a.dm - 1;
+        if constexpr (DnRegs<DN>::kSplit)
+            load_chunk_split<DN>(wexp + (uint64_t)rr * a.dn_row_bytes, sexp + (uint64_t)rr * a.dn_srow, ci, w.q[r],
+                                 w.hd[r]);
+        else if constexpr (DnRegs<DN>::kIq3)
+            load_chunk_iq3s(wexp + (uint64_t)rr * a.dn_row_bytes, ci, w.q[r], w.hd[r]);
+        else
+            load_chunk<DN>(wexp + (uint64_t)rr * a.dn_row_bytes, ci, w.q[r], w.hd[r]);
+    }
+}
+
+/* The h chunk of one (position, K segment) arranged for the down dots.
+ * Q4_K: the chunk's 32 h values scaled by 2^-e (e from the chunk's max|h|,
+ * so |h| 2^-e < 2^15; e = 0 unless max|h| >= 2^15) and rounded once to
+ * fp16, paired like the weights; weights as fp16 1024 + q, so one
+ * v_dot2_f32_f16 does two products exactly in f32, and the 1024 offset
+ * comes off with the sums of the same rounded values.  IQ4_XS: the f32 path
+ * of the dense GEMV. */
+template <int DN>
+struct DnX {
+    XChunk<DN, true> xc[1];
+    uint32_t hp[16];
+    float hsc, slo, shi;
+};
+
+template <int DN>
+__device__ __forceinline__ void dn_arrange(const XRaw<true> &xr, DnX<DN> &d) {
+    if constexpr (DnRegs<DN>::kF16) {
+        float mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xr.v[i].x), fabsf(xr.v[i].y)), fmaxf(fabsf(xr.v[i].z), fabsf(xr.v[i].w))));
+        d.hsc = ldexpf(1.0f, row_shift(mx));
+        const float inv = 1.0f / d.hsc; /* a power of two: exact */
+        float lo[16], hi[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                lo[4 * i + j] = xr.v[i][j] * inv;
+                hi[4 * i + j] = xr.v[4 + i][j] * inv;
+            }
+        /* dword dw of the payload holds bytes 4dw..4dw+3: pairs
+         * {lo(4dw), lo(4dw+2)}, {lo(4dw+1), lo(4dw+3)}, {hi(4dw), hi(4dw+2)},
+         * {hi(4dw+1), hi(4dw+3)} */
+#pragma unroll
+        for (int dw = 0; dw < 4; ++dw) {
+            d.hp[4 * dw + 0] = pack_h2(lo[4 * dw], lo[4 * dw + 2]);
+            d.hp[4 * dw + 1] = pack_h2(lo[4 * dw + 1], lo[4 * dw + 3]);
+            d.hp[4 * dw + 2] = pack_h2(hi[4 * dw], hi[4 * dw + 2]);
+            d.hp[4 * dw + 3] = pack_h2(hi[4 * dw + 1], hi[4 * dw + 3]);
+        }
+        const uint32_t one2 = 0x3C003C00u; /* fp16 {1, 1} */
+        float slo = 0.f, shi = 0.f;
+#pragma unroll
+        for (int dw = 0; dw < 4; ++dw) {
+            slo = r9vx_dot2_f16(d.hp[4 * dw + 0], one2, slo);
+            slo = r9vx_dot2_f16(d.hp[4 * dw + 1], one2, slo);
+            shi = r9vx_dot2_f16(d.hp[4 * dw + 2], one2, shi);
+            shi = r9vx_dot2_f16(d.hp[4 * dw + 3], one2, shi);
+        }
+        d.slo = slo;
+        d.shi = shi;
+    } else {
+        arrange_x<DN, true>(xr, d.xc[0]);
+    }
+}
+
+template <int DN>
+__device__ __forceinline__ void dn_dot(const DnRegs<DN> &w, uint32_t ci, const DnX<DN> &d,
+                                       float (&acc)[kDecDnRows][1], const uint32_t *lut) {
+#pragma unroll
+    for (int r = 0; r < kDecDnRows; ++r) {
+        if constexpr (DnRegs<DN>::kF32x) {
+            acc[r][0] += chunk_dot_f32x<DN>(w.q[r], w.hd[r], ci & 7, d.xc[0], lut);
+        } else if constexpr (DnRegs<DN>::kF16) {
+            const uint32_t qw[4] = {w.q[r].x, w.q[r].y, w.q[r].z, w.q[r].w};
+            const Hdr &hh = w.hd[r];
+            const float dd = r9vx_f16_to_f32((uint16_t)(hh.v.x & 0xFFFF));
+            const float dmin = r9vx_f16_to_f32((uint16_t)(hh.v.x >> 16));
+            const uint32_t sm = r9vx_q4k_pair_bytes(hh.v, (ci & 7) >> 1);
+            const float dl0 = dd * (float)(sm & 0xFFu), dl1 = dd * (float)((sm >> 8) & 0xFFu);
+            const float off0 = fmaf(1024.f, dl0, dmin * (float)((sm >> 16) & 0xFFu));
+            const float off1 = fmaf(1024.f, dl1, dmin * (float)(sm >> 24));
+            float dlo = 0.f, dhi = 0.f;
+#pragma unroll
+            for (int dw = 0; dw < 4; ++dw) {
+                dlo = r9vx_dot2_f16(r9vx_and_or(qw[dw], 0x000F000Fu, 0x64006400u), d.hp[4 * dw + 0], dlo);
+                dlo = r9vx_dot2_f16(r9vx_and_or(qw[dw] >> 8, 0x000F000Fu, 0x64006400u), d.hp[4 * dw + 1], dlo);
+                dhi = r9vx_dot2_f16(r9vx_and_or(qw[dw] >> 4, 0x000F000Fu, 0x64006400u), d.hp[4 * dw + 2], dhi);
+                dhi = r9vx_dot2_f16(r9vx_and_or(qw[dw] >> 12, 0x000F000Fu, 0x64006400u), d.hp[4 * dw + 3], dhi);
+            }
+            acc[r][0] += d.hsc * (dl0 * dlo + dl1 * dhi - (off0 * d.slo + off1 * d.shi));
+        } else {
+            chunk_dot<DN, true, 1>(w.q[r], w.hd[r], ci & 7, d.xc, acc[r], lut);
+        }
+    }
+}
+
 /* gate/up GEMV + SwiGLU.  A unit is kPairs * (64 / LPR) (gate, up) row
  * pairs of one sorted position. */
 template <int GU>
 __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
-    constexpr int kPairs = kDecPairs;
     constexpr bool kIq3 = GU == R9VX_SCHEME_IQ3_S;
-    constexpr bool kSplit = GU == R9VX_SCHEME_Q8_0 || GU == R9VX_SCHEME_Q6_K;
     __shared__ __attribute__((aligned(16))) uint32_t lut[kIq3 ? 1024 : 256];
     __shared__ uint64_t etab[R9VX_EXP2F_N];
     if constexpr (GU == R9VX_SCHEME_IQ4_XS) init_iq4_lut(lut, threadIdx.x, blockDim.x);
@@ -401,36 +572,14 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
 
     XChunk<GU, false> xc[1];
     uint32_t xpos = ~0u, xseg = ~0u;
-    float ag[kPairs][1], au[kPairs][1];
+    float ag[kDecPairs][1], au[kDecPairs][1];
     Cur lc{pos0, u0 % groups, 0u}, c = lc; /* load and compute cursors */
-    using Pay = typename std::conditional<kIq3 || kSplit, Payload2, r9vx_u32x4>::type;
-    Pay qg[kDecSteps][kPairs], qu[kDecSteps][kPairs];
-    Hdr hg[kDecSteps][kPairs], hu[kDecSteps][kPairs];
+    GuRegs<GU> wr[kDecSteps];
     for (uint32_t base = 0; base < nsteps; base += kDecSteps) {
         /* 1. every weight load of the batch's steps (steps past the last repeat it) */
 #pragma unroll
         for (uint32_t s = 0; s < kDecSteps; ++s) {
-            const uint32_t w = lc.pos == pos0 ? 0u : 1u;
-            const uint32_t ci = lc.seg * lpr + lir;
-            const uint8_t *wexp = a.w_gu + (uint64_t)expert[w] * 2 * a.dff * a.gu_row_bytes;
-            const uint16_t *sexp = kSplit ? a.s_gu + (uint64_t)expert[w] * 2 * a.dff * a.gu_srow : nullptr;
-#pragma unroll
-            for (int r = 0; r < kPairs; ++r) {
-                const uint32_t row = (lc.g * kPairs + r) * rpi + slot;
-                const uint32_t rr = row < a.dff ? row : a.dff - 1;
-                if constexpr (kSplit) {
-                    load_chunk_split<GU>(wexp + (uint64_t)rr * a.gu_row_bytes, sexp + (uint64_t)rr * a.gu_srow, ci,
-                                         qg[s][r], hg[s][r]);
-                    load_chunk_split<GU>(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes,
-                                         sexp + (uint64_t)(a.dff + rr) * a.gu_srow, ci, qu[s][r], hu[s][r]);
-                } else if constexpr (kIq3) {
-                    load_chunk_iq3s(wexp + (uint64_t)rr * a.gu_row_bytes, ci, qg[s][r], hg[s][r]);
-                    load_chunk_iq3s(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes, ci, qu[s][r], hu[s][r]);
-                } else {
-                    load_chunk<GU>(wexp + (uint64_t)rr * a.gu_row_bytes, ci, qg[s][r], hg[s][r]);
-                    load_chunk<GU>(wexp + (uint64_t)(a.dff + rr) * a.gu_row_bytes, ci, qu[s][r], hu[s][r]);
-                }
-            }
+            gu_load<GU>(a, expert[lc.pos == pos0 ? 0 : 1], lc.g, lc.seg * lpr + lir, rpi, slot, wr[s]);
             if (base + s + 1 < nsteps) advance(lc, nseg, groups);
         }
 
@@ -451,30 +600,18 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
             }
             if (c.seg == 0)
 #pragma unroll
-                for (int r = 0; r < kPairs; ++r) ag[r][0] = au[r][0] = 0.f;
-#pragma unroll
-            for (int r = 0; r < kPairs; ++r) {
-                if constexpr (kSplit) {
-                    chunk_dot_split<GU, 1>(qg[s][r], hg[s][r], ci & 7, xc, ag[r]);
-                    chunk_dot_split<GU, 1>(qu[s][r], hu[s][r], ci & 7, xc, au[r]);
-                } else if constexpr (kIq3) {
-                    chunk_dot_iq3s<1>(qg[s][r], hg[s][r], ci & 7, xc, ag[r], lut);
-                    chunk_dot_iq3s<1>(qu[s][r], hu[s][r], ci & 7, xc, au[r], lut);
-                } else {
-                    chunk_dot<GU, false, 1>(qg[s][r], hg[s][r], ci & 7, xc, ag[r], lut);
-                    chunk_dot<GU, false, 1>(qu[s][r], hu[s][r], ci & 7, xc, au[r], lut);
-                }
-            }
+                for (int r = 0; r < kDecPairs; ++r) ag[r][0] = au[r][0] = 0.f;
+            gu_dot<GU>(wr[s], ci, xc, ag, au, lut);
             if (c.seg + 1 == nseg) {
-                float gu[2][kPairs];
+                float gu[2][kDecPairs];
 #pragma unroll
-                for (int r = 0; r < kPairs; ++r) {
+                for (int r = 0; r < kDecPairs; ++r) {
                     gu[0][r] = ag[r][0];
                     gu[1][r] = au[r][0];
                 }
                 const uint32_t pos = c.pos, g = c.g;
-                lane_reduce_w<kPairs, 2>(gu, lane, a.gu_lpr_log2, [&](int r, const float (&val)[2]) {
-                    const uint32_t row = (g * kPairs + r) * rpi + slot;
+                lane_reduce_w<kDecPairs, 2>(gu, lane, a.gu_lpr_log2, [&](int r, const float (&val)[2]) {
+                    const uint32_t row = (g * kDecPairs + r) * rpi + slot;
                     if (row >= a.dff) return;
                     const float gg = val[0];
                     const float act = gg / (1.0f + r9vx_expf_tab(-gg, etab));
@@ -490,10 +627,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
  * LPR) rows of one sorted position. */
 template <int DN>
 __global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
-    constexpr int kRows = kDecDnRows;
     constexpr bool kIq3 = DN == R9VX_SCHEME_IQ3_S;
-    constexpr bool kSplit = DN == R9VX_SCHEME_Q8_0 || DN == R9VX_SCHEME_Q6_K;
-    constexpr bool kF32x = kIq3 || kSplit; /* chunk_dot_f32x against the f32 h rows */
     __shared__ __attribute__((aligned(16))) uint32_t lut[kIq3 ? 1024 : 256];
     if constexpr (DN == R9VX_SCHEME_IQ4_XS) init_iq4_lut(lut, threadIdx.x, blockDim.x);
     if constexpr (kIq3) build_iq3s_lut(lut, threadIdx.x, blockDim.x);
@@ -512,42 +646,18 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
     const float *h = reinterpret_cast<const float *>(a.ws + a.L.h);
     float *o = reinterpret_cast<float *>(a.ws + a.L.o);
 
-    /* The h chunk of (position, segment), arranged once and reused while it
-     * stays the same.  Q4_K: h scaled by 2^-e (e from the row's max|h|, so
-     * |h| < 2^15) and rounded once to fp16, paired like the weights; weights
-     * as fp16 1024 + q, so one v_dot2_f32_f16 does two products exactly in
-     * f32, and the 1024 offset comes off with the sums of the same rounded
-     * values.  IQ4_XS: the f32 path of the dense GEMV. */
-    constexpr bool kF16 = DN == R9VX_SCHEME_Q4_K;
-    XChunk<DN, true> xc[1];
-    uint32_t hp[16];
-    float hsc = 1.f, slo = 0.f, shi = 0.f;
-    uint32_t xpos = ~0u, xseg = ~0u, rpos = ~0u;
-    float acc[kRows][1];
+    /* the h chunk of (position, segment), arranged once and reused while it
+     * stays the same */
+    DnX<DN> hx;
+    uint32_t xpos = ~0u, xseg = ~0u;
+    float acc[kDecDnRows][1];
     Cur lc{pos0, u0 % groups, 0u}, c = lc; /* load and compute cursors */
-    using Pay = typename std::conditional<kF32x, Payload2, r9vx_u32x4>::type;
-    Pay q[kDecSteps][kRows];
-    Hdr hd[kDecSteps][kRows];
+    DnRegs<DN> wr[kDecSteps];
     for (uint32_t base = 0; base < nsteps; base += kDecSteps) {
         /* every weight load of the batch's steps (steps past the last repeat it) */
 #pragma unroll
         for (uint32_t s = 0; s < kDecSteps; ++s) {
-            const uint32_t w = lc.pos == pos0 ? 0u : 1u;
-            const uint32_t ci = lc.seg * lpr + lir;
-            const uint8_t *wexp = a.w_dn + (uint64_t)expert[w] * a.dm * a.dn_row_bytes;
-            const uint16_t *sexp = kSplit ? a.s_dn + (uint64_t)expert[w] * a.dm * a.dn_srow : nullptr;
-#pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-                const uint32_t row = (lc.g * kRows + r) * rpi + slot;
-                const uint32_t rr = row < a.dm ? row : a.dm - 1;
-                if constexpr (kSplit)
-                    load_chunk_split<DN>(wexp + (uint64_t)rr * a.dn_row_bytes, sexp + (uint64_t)rr * a.dn_srow, ci,
-                                         q[s][r], hd[s][r]);
-                else if constexpr (kIq3)
-                    load_chunk_iq3s(wexp + (uint64_t)rr * a.dn_row_bytes, ci, q[s][r], hd[s][r]);
-                else
-                    load_chunk<DN>(wexp + (uint64_t)rr * a.dn_row_bytes, ci, q[s][r], hd[s][r]);
-            }
+            dn_load<DN>(a, expert[lc.pos == pos0 ? 0 : 1], lc.g, lc.seg * lpr + lir, rpi, slot, wr[s]);
             if (base + s + 1 < nsteps) advance(lc, nseg, groups);
         }
 #pragma unroll
@@ -558,92 +668,22 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
                 uint32_t klo, khi;
                 chunk_k<DN>(ci, klo, khi);
                 XRaw<true> xr;
-                const float *hrow = h + (uint64_t)c.pos * a.dff;
-                load_x_raw<true>(hrow, klo, khi, xr);
-                if constexpr (kF16) {
-                    if (c.pos != rpos) { /* the row's scale: max|h| over the row */
-                        float mx = 0.f;
-                        for (uint32_t i = lane; i < a.dff / 4; i += 64) {
-                            const r9vx_f32x4 v = *reinterpret_cast<const r9vx_f32x4 *>(hrow + 4 * i);
-                            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-                        }
-#pragma unroll
-                        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-                        hsc = ldexpf(1.0f, row_shift(mx));
-                        rpos = c.pos;
-                    }
-                    const float inv = 1.0f / hsc; /* a power of two: exact */
-                    float lo[16], hi[16];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            lo[4 * i + j] = xr.v[i][j] * inv;
-                            hi[4 * i + j] = xr.v[4 + i][j] * inv;
-                        }
-                    /* dword d of the payload holds bytes 4d..4d+3: pairs
-                     * {lo(4d), lo(4d+2)}, {lo(4d+1), lo(4d+3)}, {hi(4d), hi(4d+2)},
-                     * {hi(4d+1), hi(4d+3)} */
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) {
-                        hp[4 * d + 0] = pack_h2(lo[4 * d], lo[4 * d + 2]);
-                        hp[4 * d + 1] = pack_h2(lo[4 * d + 1], lo[4 * d + 3]);
-                        hp[4 * d + 2] = pack_h2(hi[4 * d], hi[4 * d + 2]);
-                        hp[4 * d + 3] = pack_h2(hi[4 * d + 1], hi[4 * d + 3]);
-                    }
-                    const uint32_t one2 = 0x3C003C00u; /* fp16 {1, 1} */
-                    slo = 0.f;
-                    shi = 0.f;
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) {
-                        slo = r9vx_dot2_f16(hp[4 * d + 0], one2, slo);
-                        slo = r9vx_dot2_f16(hp[4 * d + 1], one2, slo);
-                        shi = r9vx_dot2_f16(hp[4 * d + 2], one2, shi);
-                        shi = r9vx_dot2_f16(hp[4 * d + 3], one2, shi);
-                    }
-                } else {
-                    arrange_x<DN, true>(xr, xc[0]);
-                }
+                load_x_raw<true>(h + (uint64_t)c.pos * a.dff, klo, khi, xr);
+                dn_arrange<DN>(xr, hx);
                 xpos = c.pos;
                 xseg = c.seg;
             }
             if (c.seg == 0)
 #pragma unroll
-                for (int r = 0; r < kRows; ++r) acc[r][0] = 0.f;
-#pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-                if constexpr (kF32x) {
-                    acc[r][0] += chunk_dot_f32x<DN>(q[s][r], hd[s][r], ci & 7, xc[0], lut);
-                } else if constexpr (kF16) {
-                    const uint32_t qw[4] = {q[s][r].x, q[s][r].y, q[s][r].z, q[s][r].w};
-                    const Hdr &hh = hd[s][r];
-                    const float d = r9vx_f16_to_f32((uint16_t)(hh.v.x & 0xFFFF));
-                    const float dmin = r9vx_f16_to_f32((uint16_t)(hh.v.x >> 16));
-                    uint32_t sc[2], mn[2];
-                    r9vx_q4k_scale_pair(hh.v, (ci & 7) >> 1, sc, mn);
-                    const float dl0 = d * (float)sc[0], dl1 = d * (float)sc[1];
-                    const float off0 = fmaf(1024.f, dl0, dmin * (float)mn[0]);
-                    const float off1 = fmaf(1024.f, dl1, dmin * (float)mn[1]);
-                    float dlo = 0.f, dhi = 0.f;
-#pragma unroll
-                    for (int dw = 0; dw < 4; ++dw) {
-                        dlo = r9vx_dot2_f16((qw[dw] & 0x000F000Fu) | 0x64006400u, hp[4 * dw + 0], dlo);
-                        dlo = r9vx_dot2_f16(((qw[dw] >> 8) & 0x000F000Fu) | 0x64006400u, hp[4 * dw + 1], dlo);
-                        dhi = r9vx_dot2_f16(((qw[dw] >> 4) & 0x000F000Fu) | 0x64006400u, hp[4 * dw + 2], dhi);
-                        dhi = r9vx_dot2_f16(((qw[dw] >> 12) & 0x000F000Fu) | 0x64006400u, hp[4 * dw + 3], dhi);
-                    }
-                    acc[r][0] += hsc * (dl0 * dlo + dl1 * dhi - (off0 * slo + off1 * shi));
-                } else {
-                    chunk_dot<DN, true, 1>(q[s][r], hd[s][r], ci & 7, xc, acc[r], lut);
-                }
-            }
+                for (int r = 0; r < kDecDnRows; ++r) acc[r][0] = 0.f;
+            dn_dot<DN>(wr[s], ci, hx, acc, lut);
             if (c.seg + 1 == nseg) {
-                float v[1][kRows];
+                float v[1][kDecDnRows];
 #pragma unroll
-                for (int r = 0; r < kRows; ++r) v[0][r] = acc[r][0];
+                for (int r = 0; r < kDecDnRows; ++r) v[0][r] = acc[r][0];
                 const uint32_t pos = c.pos, g = c.g;
-                lane_reduce_w<kRows, 1>(v, lane, a.dn_lpr_log2, [&](int r, const float (&val)[1]) {
-                    const uint32_t row = (g * kRows + r) * rpi + slot;
+                lane_reduce_w<kDecDnRows, 1>(v, lane, a.dn_lpr_log2, [&](int r, const float (&val)[1]) {
+                    const uint32_t row = (g * kDecDnRows + r) * rpi + slot;
                     if (row >= a.dm) return;
                     o[(uint64_t)pos * a.dm + row] = val[0];
                 });
@@ -651,6 +691,254 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
             advance(c, nseg, groups);
         }
     }
+}
+
+/* Pipelined forms for rows of one K segment (nseg == 1, K <= 2048): a wave
+ * walks its units (row groups of one position: the host makes the units per
+ * wave divide the row groups per position) in batches of kDecSteps and
+ * issues the weight loads of batch b + 1 before it computes batch b, so a
+ * batch's loads are in flight while the previous batch computes.  Every
+ * load of the loop is issued unconditionally (steps past the wave's last
+ * repeat its addresses): a load issued on one path only would make the next
+ * wait a wait for everything.  The step outputs wait in LDS and are stored
+ * after the wave's last load, because a store issued between two loads
+ * turns the wait for the older load into a wait for every outstanding
+ * memory operation; the gate/up kernel applies SiLU(g) * u there, one row
+ * per lane.  A lane's K chunk is the same in every step, so its activation
+ * chunk is loaded and arranged once.  The arithmetic per step is that of
+ * moe_gu_kernel / moe_down_kernel. */
+#ifndef R9VX_GU_PIPE_STEPS
+#define R9VX_GU_PIPE_STEPS 2
+#endif
+#ifndef R9VX_GU_PIPE_UPW
+#define R9VX_GU_PIPE_UPW 4
+#endif
+#ifndef R9VX_DN_PIPE_STEPS
+#define R9VX_DN_PIPE_STEPS 1
+#endif
+#ifndef R9VX_DN_PIPE_UPW
+#define R9VX_DN_PIPE_UPW 8
+#endif
+/* steps per batch and units per wave (at most) of the two kernels */
+constexpr uint32_t kGuPipeSteps = R9VX_GU_PIPE_STEPS, kGuPipeUpw = R9VX_GU_PIPE_UPW;
+constexpr uint32_t kDnPipeSteps = R9VX_DN_PIPE_STEPS, kDnPipeUpw = R9VX_DN_PIPE_UPW;
+static_assert((kDecPairs & (kDecPairs - 1)) == 0 && (kDecDnRows & (kDecDnRows - 1)) == 0,
+              "rows per step must be a power of two");
+
+/* The LDS tables of a decode kernel (IQ4_XS codebook pairs, IQ3_S grid,
+ * exp2 table for the SiLU), loaded to registers as the kernel's first
+ * memory operations and written to LDS after the first weight loads are
+ * issued: loads complete in order, so the LDS writes wait for the table
+ * words only, and the tables' latency overlaps the weights'. */
+template <int S, bool kExp>
+struct DecTables {
+    r9vx_u32x4 iq4;
+    uint32_t g[2];
+    uint64_t ex;
+    __device__ __forceinline__ void load(uint32_t tid) {
+        if constexpr (S == R9VX_SCHEME_IQ4_XS)
+            if (tid < 64) iq4 = reinterpret_cast<const r9vx_u32x4 *>(kIq4PairLut.v)[tid];
+        if constexpr (S == R9VX_SCHEME_IQ3_S) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                if (tid + 256 * i < 512) g[i] = kIq3sGrid[tid + 256 * i];
+        }
+        if constexpr (kExp)
+            if (tid < R9VX_EXP2F_N) ex = r9vx_exp2_table[tid];
+    }
+    __device__ __forceinline__ void store(uint32_t *lut, uint64_t *etab, uint32_t tid) const {
+        if constexpr (S == R9VX_SCHEME_IQ4_XS)
+            if (tid < 64) reinterpret_cast<r9vx_u32x4 *>(lut)[tid] = iq4;
+        if constexpr (S == R9VX_SCHEME_IQ3_S) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint32_t e = tid + 256 * i;
+                if (e >= 512) continue;
+                uint32_t h[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) h[b] = __builtin_bit_cast(uint32_t, (float)((g[i] >> (8 * b)) & 0xFF)) >> 16;
+                lut[2 * e] = h[0] | (h[1] << 16);
+                lut[2 * e + 1] = h[2] | (h[3] << 16);
+            }
+        }
+        if constexpr (kExp)
+            if (tid < R9VX_EXP2F_N) etab[tid] = ex;
+    }
+};
+
+/* Workgroup barrier over LDS only: the weight loads in flight are not
+ * waited for. */
+__device__ __forceinline__ void lds_only_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+/* The wave's position and first row group; a wave without units, or with a
+ * refused id, gets expert 0's rows of position 0 (in bounds, never used) so
+ * that every path issues the same loads and the waits after them stay
+ * counted.  Returns whether the wave computes. */
+__device__ __forceinline__ bool pipe_wave(const FfnArgs &a, uint32_t groups, uint32_t upw, uint32_t &u0, uint32_t &n,
+                                          uint32_t &pos, uint32_t &g0, uint32_t &tok, uint32_t &expert) {
+    n = 0;
+    bool ok = wave_units((a.p + a.shared * a.t) * groups, upw, u0, n);
+    pos = ok ? u0 / groups : 0u;
+    ok = pos_meta(a, pos, tok, expert) && ok; /* refused: nothing is read or written */
+    if (!ok) pos = tok = expert = 0;
+    g0 = ok ? u0 - pos * groups : 0u;
+    return ok;
+}
+
+template <int GU>
+__global__ __launch_bounds__(kDecWaves * 64) void moe_gu_pipe_kernel(FfnArgs a) {
+    constexpr bool kIq3 = GU == R9VX_SCHEME_IQ3_S;
+    constexpr uint32_t kObuf = kGuPipeUpw * kDecPairs * 8; /* rows per wave, at most */
+    __shared__ __attribute__((aligned(16))) uint32_t lut[kIq3 ? 1024 : 256];
+    __shared__ uint64_t etab[R9VX_EXP2F_N];
+    __shared__ float2 obuf[kDecWaves][kObuf]; /* (gate, up) dot of each row */
+    DecTables<GU, true> tb;
+    tb.load(threadIdx.x);
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t rpi = 64u >> a.gu_lpr_log2, rps = kDecPairs * rpi;
+    const uint32_t ci = lane & ((1u << a.gu_lpr_log2) - 1), slot = lane >> a.gu_lpr_log2;
+    uint32_t u0, n, pos, g0, tok, expert;
+    const bool ok = pipe_wave(a, a.gu_groups, a.gu_upw, u0, n, pos, g0, tok, expert);
+    float2 *ob = obuf[threadIdx.x >> 6];
+
+    uint32_t klo, khi;
+    chunk_k<GU>(ci, klo, khi);
+    XRaw<false> xr;
+    load_x_raw<false>(a.x + (uint64_t)tok * a.dm, klo, khi, xr);
+    uint32_t li = 0, cs = 0; /* step indices of the next load and the next compute */
+    auto issue = [&](GuRegs<GU> (&w)[kGuPipeSteps]) {
+#pragma unroll
+        for (uint32_t s = 0; s < kGuPipeSteps; ++s) {
+            gu_load<GU>(a, expert, g0 + li, ci, rpi, slot, w[s]);
+            if (li + 1 < n) ++li;
+        }
+    };
+    XChunk<GU, false> xc[1];
+    auto compute = [&](const GuRegs<GU> (&w)[kGuPipeSteps]) {
+#pragma unroll
+        for (uint32_t s = 0; s < kGuPipeSteps; ++s) {
+            if (cs >= n) break;
+            float ag[kDecPairs][1], au[kDecPairs][1];
+#pragma unroll
+            for (int r = 0; r < kDecPairs; ++r) ag[r][0] = au[r][0] = 0.f;
+            gu_dot<GU>(w[s], ci, xc, ag, au, lut);
+            float gu[2][kDecPairs];
+#pragma unroll
+            for (int r = 0; r < kDecPairs; ++r) {
+                gu[0][r] = ag[r][0];
+                gu[1][r] = au[r][0];
+            }
+            float2 *os = ob + cs * rps;
+            lane_reduce_w<kDecPairs, 2>(gu, lane, a.gu_lpr_log2, [&](int r, const float (&val)[2]) {
+                os[r * rpi + slot] = float2{val[0], val[1]};
+            });
+            ++cs;
+        }
+    };
+    GuRegs<GU> wa[kGuPipeSteps], wb[kGuPipeSteps];
+    issue(wa);
+    tb.store(lut, etab, threadIdx.x);
+    lds_only_barrier(); /* the last barrier: waves run independently from here */
+    if (!ok) return;
+    arrange_x<GU, false>(xr, xc[0]);
+    const uint32_t nb = (n + kGuPipeSteps - 1) / kGuPipeSteps;
+    for (uint32_t b = 0;; b += 2) {
+        issue(wb);
+        compute(wa);
+        if (b + 2 >= nb) {
+            compute(wb);
+            break;
+        }
+        issue(wa);
+        compute(wb);
+    }
+    /* h rows g0 * rps + j, j < n * rps: one row per lane */
+    wave_lds_sync();
+    float *h = reinterpret_cast<float *>(a.ws + a.L.h) + (uint64_t)pos * a.dff + g0 * rps;
+    const uint32_t nrows = min(n * rps, a.dff - g0 * rps);
+    for (uint32_t j = lane; j < nrows; j += 64) {
+        const float2 v = ob[j];
+        const float act = v.x / (1.0f + r9vx_expf_tab(-v.x, etab));
+        h[j] = act * v.y;
+    }
+}
+
+template <int DN>
+__global__ __launch_bounds__(kDecWaves * 64) void moe_down_pipe_kernel(FfnArgs a) {
+    constexpr bool kIq3 = DN == R9VX_SCHEME_IQ3_S;
+    constexpr uint32_t kObuf = kDnPipeUpw * kDecDnRows * 8;
+    __shared__ __attribute__((aligned(16))) uint32_t lut[kIq3 ? 1024 : 256];
+    __shared__ float obuf[kDecWaves][kObuf];
+    DecTables<DN, false> tb;
+    tb.load(threadIdx.x);
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t rpi = 64u >> a.dn_lpr_log2, rps = kDecDnRows * rpi;
+    const uint32_t ci = lane & ((1u << a.dn_lpr_log2) - 1), slot = lane >> a.dn_lpr_log2;
+    uint32_t u0, n, pos, g0, tok, expert;
+    const bool ok = pipe_wave(a, a.dn_groups, a.dn_upw, u0, n, pos, g0, tok, expert);
+    float *ob = obuf[threadIdx.x >> 6];
+
+    uint32_t klo, khi;
+    chunk_k<DN>(ci, klo, khi);
+    XRaw<true> xr;
+    load_x_raw<true>(reinterpret_cast<const float *>(a.ws + a.L.h) + (uint64_t)pos * a.dff, klo, khi, xr);
+    uint32_t li = 0, cs = 0;
+    auto issue = [&](DnRegs<DN> (&w)[kDnPipeSteps]) {
+#pragma unroll
+        for (uint32_t s = 0; s < kDnPipeSteps; ++s) {
+            dn_load<DN>(a, expert, g0 + li, ci, rpi, slot, w[s]);
+            if (li + 1 < n) ++li;
+        }
+    };
+    DnX<DN> hx;
+    auto compute = [&](const DnRegs<DN> (&w)[kDnPipeSteps]) {
+#pragma unroll
+        for (uint32_t s = 0; s < kDnPipeSteps; ++s) {
+            if (cs >= n) break;
+            float acc[kDecDnRows][1];
+#pragma unroll
+            for (int r = 0; r < kDecDnRows; ++r) acc[r][0] = 0.f;
+            dn_dot<DN>(w[s], ci, hx, acc, lut);
+            float v[1][kDecDnRows];
+#pragma unroll
+            for (int r = 0; r < kDecDnRows; ++r) v[0][r] = acc[r][0];
+            float *os = ob + cs * rps;
+            lane_reduce_w<kDecDnRows, 1>(v, lane, a.dn_lpr_log2,
+                                         [&](int r, const float (&val)[1]) { os[r * rpi + slot] = val[0]; });
+            ++cs;
+        }
+    };
+    DnRegs<DN> wa[kDnPipeSteps], wb[kDnPipeSteps];
+    issue(wa);
+    tb.store(lut, nullptr, threadIdx.x);
+    lds_only_barrier(); /* the last barrier: waves run independently from here */
+    if (!ok) return;
+    dn_arrange<DN>(xr, hx);
+    const uint32_t nb = (n + kDnPipeSteps - 1) / kDnPipeSteps;
+    for (uint32_t b = 0;; b += 2) {
+        issue(wb);
+        compute(wa);
+        if (b + 2 >= nb) {
+            compute(wb);
+            break;
+        }
+        issue(wa);
+        compute(wb);
+    }
+    wave_lds_sync();
+    float *o = reinterpret_cast<float *>(a.ws + a.L.o) + (uint64_t)pos * a.dm + g0 * rps;
+    const uint32_t nrows = min(n * rps, a.dm - g0 * rps);
+    for (uint32_t j = lane; j < nrows; j += 64) o[j] = ob[j];
 }
 
 }  // namespace
@@ -854,6 +1142,17 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
     };
     f.gu_upw = upw_for(f.gu_groups, f.gu_nseg);
     f.dn_upw = upw_for(f.dn_groups, f.dn_nseg);
+    /* rows of one K segment take the pipelined kernels: the largest units
+     * per wave <= kPipeUpw that divides the row groups per position, so a
+     * wave's units lie in one position */
+    auto pipe_upw = [](uint32_t groups, uint32_t most) {
+        uint32_t u = most;
+        while (groups % u) --u;
+        return u;
+    };
+    const bool gu_pipe = f.gu_nseg == 1, dn_pipe = f.dn_nseg == 1;
+    if (gu_pipe) f.gu_upw = pipe_upw(f.gu_groups, kGuPipeUpw);
+    if (dn_pipe) f.dn_upw = pipe_upw(f.dn_groups, kDnPipeUpw);
     auto grid_for = [&](uint32_t groups, uint32_t upw) {
         const uint32_t units = npos * groups;
         const uint32_t waves = (units + upw - 1) / upw;
@@ -861,20 +1160,24 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
     };
     const dim3 block(kDecWaves * 64);
     const dim3 ggu = grid_for(f.gu_groups, f.gu_upw), gdn = grid_for(f.dn_groups, f.dn_upw);
+#define R9VX_GU(S) (gu_pipe ? moe_gu_pipe_kernel<S> : moe_gu_kernel<S>)
+#define R9VX_DN(S) (dn_pipe ? moe_down_pipe_kernel<S> : moe_down_kernel<S>)
     switch (p.scheme_gu) {
-    case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_IQ3_S>, ggu, block, 0, s, f); break;
-    case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_IQ4_XS>, ggu, block, 0, s, f); break;
-    case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_Q8_0>, ggu, block, 0, s, f); break;
-    case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_Q6_K>, ggu, block, 0, s, f); break;
-    default: hipLaunchKernelGGL(moe_gu_kernel<R9VX_SCHEME_Q4_K>, ggu, block, 0, s, f); break;
+    case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(R9VX_GU(R9VX_SCHEME_IQ3_S), ggu, block, 0, s, f); break;
+    case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(R9VX_GU(R9VX_SCHEME_IQ4_XS), ggu, block, 0, s, f); break;
+    case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(R9VX_GU(R9VX_SCHEME_Q8_0), ggu, block, 0, s, f); break;
+    case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL(R9VX_GU(R9VX_SCHEME_Q6_K), ggu, block, 0, s, f); break;
+    default: hipLaunchKernelGGL(R9VX_GU(R9VX_SCHEME_Q4_K), ggu, block, 0, s, f); break;
     }
     switch (p.scheme_dn) {
-    case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_IQ3_S>, gdn, block, 0, s, f); break;
-    case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_IQ4_XS>, gdn, block, 0, s, f); break;
-    case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_Q8_0>, gdn, block, 0, s, f); break;
-    case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_Q6_K>, gdn, block, 0, s, f); break;
-    default: hipLaunchKernelGGL(moe_down_kernel<R9VX_SCHEME_Q4_K>, gdn, block, 0, s, f); break;
+    case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(R9VX_DN(R9VX_SCHEME_IQ3_S), gdn, block, 0, s, f); break;
+    case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(R9VX_DN(R9VX_SCHEME_IQ4_XS), gdn, block, 0, s, f); break;
+    case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(R9VX_DN(R9VX_SCHEME_Q8_0), gdn, block, 0, s, f); break;
+    case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL(R9VX_DN(R9VX_SCHEME_Q6_K), gdn, block, 0, s, f); break;
+    default: hipLaunchKernelGGL(R9VX_DN(R9VX_SCHEME_Q4_K), gdn, block, 0, s, f); break;
     }
+#undef R9VX_GU
+#undef R9VX_DN
     return (int)hipGetLastError();
 }
 

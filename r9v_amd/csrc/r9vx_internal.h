@@ -36,6 +36,26 @@ __device__ __forceinline__ void r9vx_q4k_scale_pair(r9vx_u32x4 h, uint32_t g, ui
     }
 }
 
+/* The same pair without a branch: bytes {sc(2g), sc(2g+1), mn(2g), mn(2g+1)}.
+ * X gathers scale bytes 2(g&1), +1, 4+2(g&1), +1 (one v_perm of dwords 1
+ * and 2), Y the same bytes of dword 3 and its nibbles shifted down; g < 2
+ * keeps X's six low bits, g >= 2 combines Y's nibbles with X's top two bits
+ * (the table of r9vx_q4k_scale_pair). */
+__device__ __forceinline__ uint32_t r9vx_q4k_pair_bytes(r9vx_u32x4 h, uint32_t g) {
+    const uint32_t sel = (g & 1u) ? 0x07060302u : 0x05040100u;
+    const uint32_t x = __builtin_amdgcn_perm(h.z, h.y, sel);
+    const uint32_t y = __builtin_amdgcn_perm(h.w >> 4, h.w, sel);
+    return g >= 2 ? ((y & 0x0F0F0F0Fu) | ((x >> 2) & 0x30303030u)) : (x & 0x3F3F3F3Fu);
+}
+
+/* (a & m) | o in one v_and_or_b32: with both masks as literals the compiler
+ * emits a v_and and a v_or (a three-operand VOP3 takes no literal here). */
+__device__ __forceinline__ uint32_t r9vx_and_or(uint32_t a, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(o));
+    return r;
+}
+
 /* IQ4_XS sub-block scale s - 32 as f32 from the 8-byte header
  * (crates/r9v-format/src/iq.rs:587-590): low nibble from scales_l, high two
  * bits from scales_h. */
