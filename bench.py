@@ -337,23 +337,28 @@ def c3_extra(torch, ffi, synth, gsynth, steps, cpu_s, steps_only=False):
         ffi.moe_route(p, k, ids=ids, weights=w)
         uniq.append(len(set(ids.cpu().numpy().reshape(-1).tolist())))
 
-    def step(i):
-        ffi.moe_route(pats[i % len(pats)], k, ids=ids, weights=w)
+    def step(i, stream=None):
+        ffi.moe_route(pats[i % len(pats)], k, ids=ids, weights=w, stream=stream)
         gu, dn = wsets[i % len(wsets)]
-        ffi.moe_ffn(x, ids, w, gu, dn, e, dff, shared=shared, y=y, workspace=wsp, t_bucket=t)
+        ffi.moe_ffn(x, ids, w, gu, dn, e, dff, shared=shared, y=y, workspace=wsp, t_bucket=t, stream=stream)
 
     if steps_only:  # a fixed run for counter collection
         for i in range(steps):
             step(i)
         return None
     ms, med = timed_steps(torch, step, max(200, steps), 10)
+    # the same steps captured in a HIP graph (56 steps: every routing pattern
+    # and weight copy), as a decode loop would replay them
+    gms = graph_time(torch, step, len(pats) * len(wsets))
     u = float(np.mean(uniq))
     per_expert = int(ffi.load().r9vx_moe_ffn_expert_bytes(__import__("ctypes").byref(st)))
     bytes_ = (u + shared) * per_expert + t * dm * 2 + t * dm * 4 + t * e * 4
     flops = (t * k + t * shared) * (2 * 2 * dff * dm + 2 * dm * dff)
     out = {"workload": "configs[3]: MoE decode T=5, E=512+1 shared, top-10, IQ4_XS gate/up + Q4_K down "
                        "(route + permute + expert GEMVs + combine per step)",
-           "ms_per_step": round(ms, 4), "median_ms_per_step": round(med, 4), "distinct_experts_mean": u,
+           "ms_per_step": round(ms, 4), "median_ms_per_step": round(med, 4),
+           "graph_ms_per_step": round(gms, 4), "graph_tokens/s": round(t / (gms * 1e-3), 1),
+           "graph_hbm_frac": round(bytes_ / (gms * 1e-3) / 8e12, 4), "distinct_experts_mean": u,
            "bytes_per_step": int(bytes_), "tokens/s": round(t / (ms * 1e-3), 1), "flops": flops,
            "weight_copies": len(wsets), **hbm(bytes_, ms)}
     if cpu_s:

@@ -947,63 +947,63 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_down_pipe_kernel(FfnArgs a
 
 /* y[t, d] = sum over the token's pairs in ascending sorted position (=
  * ascending expert, then slot) of w * o, then + each shared expert's o.
- * The first K threads rank the token's K positions in LDS (positions are
- * distinct), so every thread then walks the same ordered list from LDS and
- * issues its K row loads before the ordered f32 sum. */
+ * Every wave works alone: it loads all ids of the batch (the refusal below)
+ * and the token's K ids and weights in one round of loads, ranks the K
+ * slots by (expert, slot) across its lanes, and then issues the token's row
+ * loads in rank order (the order is the same in every lane) before the
+ * ordered f32 sum. */
 __global__ __launch_bounds__(256) void r9vx_moe_combine_kernel(MoeCombineArgs a) {
-    __shared__ uint32_t key[kMoeMaxK], opos[kMoeMaxK];
-    __shared__ float sw[kMoeMaxK], ow[kMoeMaxK];
-    __shared__ uint32_t bad;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t t = blockIdx.y, kk = a.k;
     /* the refusal of moe_ffn.rs:440-465 for the whole batch (the decode path
-     * has no sort pass): every block checks every id before writing y, and
-     * block (0, 0) leaves the call's status word */
-    if (threadIdx.x == 0) bad = 0u;
-    __syncthreads();
-    for (uint32_t i = threadIdx.x; i < a.p; i += blockDim.x)
-        if (a.ids[i] >= a.e) bad = 1u;
-    __syncthreads();
+     * has no sort pass): every wave checks every id (p = t * K <= 8 * 32,
+     * four per lane) before writing y, and block (0, 0) leaves the call's
+     * status word */
+    uint32_t badl = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        const uint32_t i = lane + 64 * j;
+        if (i < a.p && a.ids[i] >= a.e) badl = 1u;
+    }
+    uint32_t key = ~0u;
+    float wt = 0.f;
+    if (lane < kk) {
+        key = (a.ids[(uint64_t)t * kk + lane] << 8) | lane;
+        wt = a.weights[(uint64_t)t * kk + lane];
+    }
+    const bool bad = __ballot(badl) != 0ull;
     if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
         reinterpret_cast<uint32_t *>(a.ws + a.L.status)[0] = bad ? R9VX_STATUS_BAD_EXPERT : 0u;
     if (bad) return;
-    const uint32_t t = blockIdx.y;
-    const uint32_t kk = a.k;
-    /* the token's K rows (pair order) ranked by (expert, slot) */
-    if (threadIdx.x < kk) {
-        key[threadIdx.x] = (a.ids[(uint64_t)t * kk + threadIdx.x] << 8) | threadIdx.x;
-        sw[threadIdx.x] = a.weights[(uint64_t)t * kk + threadIdx.x];
-    }
-    __syncthreads();
-    if (threadIdx.x < kk) {
-        const uint32_t kv = key[threadIdx.x];
-        uint32_t rank = 0;
-        for (uint32_t j = 0; j < kk; ++j) rank += key[j] < kv ? 1u : 0u;
-        opos[rank] = t * kk + threadIdx.x;
-        ow[rank] = sw[threadIdx.x];
-    }
-    __syncthreads();
+    /* rank of the lane's slot by key (keys are distinct; lanes >= K rank K) */
+    uint32_t rank = 0;
+    for (uint32_t i = 0; i < kk; ++i) rank += (uint32_t)__builtin_amdgcn_readlane((int)key, (int)i) < key ? 1u : 0u;
     const uint32_t d0 = (blockIdx.x * 256 + threadIdx.x) * 4;
-    if (d0 >= a.dm) return;
+    const bool live = d0 < a.dm;
     const float *o = reinterpret_cast<const float *>(a.ws + a.L.o);
     r9vx_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     /* Eight rows in flight at a time; rows[] is indexed by constants only so
      * it stays in registers. */
     for (uint32_t jb = 0; jb < kk; jb += 8) {
         r9vx_f32x4 rows[8];
-#pragma unroll
-        for (uint32_t j = 0; j < 8; ++j)
-            if (jb + j < kk)
-                rows[j] = *reinterpret_cast<const r9vx_f32x4 *>(o + (uint64_t)opos[jb + j] * a.dm + d0);
+        float w[8];
 #pragma unroll
         for (uint32_t j = 0; j < 8; ++j) {
-            if (jb + j < kk) {
-                const float w = ow[jb + j];
-                acc.x = acc.x + w * rows[j].x;
-                acc.y = acc.y + w * rows[j].y;
-                acc.z = acc.z + w * rows[j].z;
-                acc.w = acc.w + w * rows[j].w;
-            }
+            if (jb + j >= kk) break;
+            const uint32_t slot = (uint32_t)__builtin_ctzll(__ballot(rank == jb + j));
+            w[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), (int)slot));
+            if (live) rows[j] = *reinterpret_cast<const r9vx_f32x4 *>(o + ((uint64_t)t * kk + slot) * a.dm + d0);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            if (jb + j >= kk) break;
+            acc.x = acc.x + w[j] * rows[j].x;
+            acc.y = acc.y + w[j] * rows[j].y;
+            acc.z = acc.z + w[j] * rows[j].z;
+            acc.w = acc.w + w[j] * rows[j].w;
         }
     }
+    if (!live) return;
     for (uint32_t s = 0; s < a.shared; ++s) {
         r9vx_f32x4 v = *reinterpret_cast<const r9vx_f32x4 *>(o + (uint64_t)(a.p + s * a.t + t) * a.dm + d0);
         acc.x = acc.x + v.x;

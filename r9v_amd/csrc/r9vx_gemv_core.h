@@ -196,10 +196,9 @@ __device__ __forceinline__ void chunk_dot(const r9vx_u32x4 &qs, const Hdr &h, ui
     if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
         float d = r9vx_f16_to_f32((uint16_t)(h.v.x & 0xFFFF));
         float dmin = r9vx_f16_to_f32((uint16_t)(h.v.x >> 16));
-        uint32_t sc[2], mn[2];
-        r9vx_q4k_scale_pair(h.v, c >> 1, sc, mn);
-        float dl0 = d * (float)sc[0], dl1 = d * (float)sc[1];
-        float ml0 = dmin * (float)mn[0], ml1 = dmin * (float)mn[1];
+        const uint32_t sm = r9vx_q4k_pair_bytes(h.v, c >> 1);
+        float dl0 = d * (float)(sm & 0xFFu), dl1 = d * (float)((sm >> 8) & 0xFFu);
+        float ml0 = dmin * (float)((sm >> 16) & 0xFFu), ml1 = dmin * (float)(sm >> 24);
         if constexpr (XF32) {
 #pragma unroll
             for (int t = 0; t < M; ++t) {
@@ -220,10 +219,10 @@ __device__ __forceinline__ void chunk_dot(const r9vx_u32x4 &qs, const Hdr &h, ui
             uint32_t v[16];
 #pragma unroll
             for (int dw = 0; dw < 4; ++dw) {
-                v[4 * dw + 0] = (q[dw] & 0x000F000Fu) | 0x43004300u;
-                v[4 * dw + 1] = ((q[dw] >> 8) & 0x000F000Fu) | 0x43004300u;
-                v[4 * dw + 2] = ((q[dw] >> 4) & 0x000F000Fu) | 0x43004300u;
-                v[4 * dw + 3] = ((q[dw] >> 12) & 0x000F000Fu) | 0x43004300u;
+                v[4 * dw + 0] = r9vx_and_or(q[dw], 0x000F000Fu, 0x43004300u);
+                v[4 * dw + 1] = r9vx_and_or(q[dw] >> 8, 0x000F000Fu, 0x43004300u);
+                v[4 * dw + 2] = r9vx_and_or(q[dw] >> 4, 0x000F000Fu, 0x43004300u);
+                v[4 * dw + 3] = r9vx_and_or(q[dw] >> 12, 0x000F000Fu, 0x43004300u);
             }
             /* sum (128+q)x = sum qx + 128 sum x; fold the offset into the min. */
             float off0 = fmaf(128.f, dl0, ml0), off1 = fmaf(128.f, dl1, ml1);

@@ -213,42 +213,26 @@ __device__ __forceinline__ uint32_t check_loaded(const RouteArgs &a, uint32_t la
     return bad;
 }
 
-/* Scores, top-K and weights of one loaded row; lane j < K returns the j-th
- * selection in (id, w). */
+/* The n largest of v (lane l holds v[c] for c = l + 64 i) in the
+ * reference's order: descending score, ties to the smaller column.  Lane
+ * j < n returns the j-th (column, score).  The composite key (score order,
+ * ~column) makes every candidate distinct, so a wave max picks exactly the
+ * reference's next element.  Keys are built once; a taken key or a padding
+ * slot is 0, below every valid key (scores are >= 0, whose order keys are
+ * >= 0x80000000).  The wave max runs on the score half; the column half is
+ * needed only when several lanes tie on it.  n <= E. */
 template <int PER>
-__device__ __forceinline__ void route_loaded(const RouteArgs &a, uint32_t lane, float (&sc)[PER],
-                                             const uint64_t *etab, float *buf, uint32_t &my_id, float &my_w) {
-    if (a.scoring == R9VX_SCORING_SOFTMAX) {
-        float mx = -__builtin_huge_valf();
-#pragma unroll
-        for (int i = 0; i < PER; ++i) mx = fmaxf(mx, sc[i]);
-        mx = wave_max(mx);
-        /* padding holds -inf: exp(-inf - mx) = 0 */
-#pragma unroll
-        for (int i = 0; i < PER; ++i) sc[i] = r9vx_expf_tab_nb(sc[i] - mx, etab);
-        const float sum = ordered_sum<PER>(sc, a.e, lane, buf);
-#pragma unroll
-        for (int i = 0; i < PER; ++i) sc[i] = sc[i] / sum;
-    } else {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) sc[i] = 1.0f / (1.0f + r9vx_expf_tab_nb(-sc[i], etab));
-    }
-    /* Top-K: the composite key (score order, ~id) makes every candidate
-     * distinct, so a wave max picks exactly the reference's next element.
-     * Keys are built once; a taken key or a padding slot is 0, below every
-     * valid key (scores are >= 0, whose order keys are >= 0x80000000).  The
-     * wave max runs on the score half; the id half is needed only when
-     * several lanes tie on it. */
+__device__ __forceinline__ void select_top(const float (&v)[PER], uint32_t e, uint32_t n, uint32_t lane,
+                                           uint32_t &my_col, float &my_v) {
     uint64_t key[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const uint32_t c = lane + 64 * i;
-        key[i] = c < a.e ? ((uint64_t)total_order(sc[i]) << 32) | (uint64_t)(0xFFFFFFFFu - c) : 0;
+        key[i] = c < e ? ((uint64_t)total_order(v[i]) << 32) | (uint64_t)(0xFFFFFFFFu - c) : 0;
     }
-    my_id = 0;
-    my_w = 0.0f;
-    float selected_sum = 0.0f;
-    for (uint32_t j = 0; j < a.k; ++j) {
+    my_col = 0;
+    my_v = 0.0f;
+    for (uint32_t j = 0; j < n; ++j) {
         uint64_t m[PER];
 #pragma unroll
         for (int i = 0; i < PER; ++i) m[i] = key[i];
@@ -271,15 +255,53 @@ __device__ __forceinline__ void route_loaded(const RouteArgs &a, uint32_t lane, 
             for (int i = 0; i < PER; ++i)
                 if ((uint32_t)i == (col >> 6)) key[i] = 0;
         }
-        const float score = __builtin_bit_cast(float, (mh & 0x80000000u) ? (mh & 0x7FFFFFFFu) : ~mh);
-        const float w = score * a.scale;
-        selected_sum = selected_sum + w;
         if (lane == j) {
-            my_id = col;
-            my_w = w;
+            my_col = col;
+            my_v = __builtin_bit_cast(float, (mh & 0x80000000u) ? (mh & 0x7FFFFFFFu) : ~mh);
         }
     }
-    if (a.renormalize) my_w = my_w / selected_sum;
+}
+
+/* Weights of the K selections (lane j < K holds the j-th score): w = score *
+ * scale, renormalised by their sum taken in selection order. */
+__device__ __forceinline__ float select_weight(const RouteArgs &a, uint32_t lane, float score) {
+    const float w = score * a.scale;
+    if (!a.renormalize) return w;
+    float selected_sum = 0.0f;
+    for (uint32_t j = 0; j < a.k; ++j)
+        selected_sum = selected_sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), (int)j));
+    return w / selected_sum;
+}
+
+/* Softmax numerators of one loaded row: sc <- exp(sc - max) (padding holds
+ * -inf: exp(-inf - max) = 0). */
+template <int PER>
+__device__ __forceinline__ void softmax_exp(float (&sc)[PER], const uint64_t *etab) {
+    float mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int i = 0; i < PER; ++i) mx = fmaxf(mx, sc[i]);
+    mx = wave_max(mx);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) sc[i] = r9vx_expf_tab_nb(sc[i] - mx, etab);
+}
+
+/* Scores, top-K and weights of one loaded row; lane j < K returns the j-th
+ * selection in (id, w). */
+template <int PER>
+__device__ __forceinline__ void route_loaded(const RouteArgs &a, uint32_t lane, float (&sc)[PER],
+                                             const uint64_t *etab, float *buf, uint32_t &my_id, float &my_w) {
+    if (a.scoring == R9VX_SCORING_SOFTMAX) {
+        softmax_exp<PER>(sc, etab);
+        const float sum = ordered_sum<PER>(sc, a.e, lane, buf);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) sc[i] = sc[i] / sum;
+    } else {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) sc[i] = 1.0f / (1.0f + r9vx_expf_tab_nb(-sc[i], etab));
+    }
+    float score;
+    select_top<PER>(sc, a.e, a.k, lane, my_id, score);
+    my_w = select_weight(a, lane, score);
 }
 
 __global__ void clear_status_kernel(uint32_t *status) { *status = 0u; }
@@ -314,15 +336,23 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
     }
 }
 
-/* Single-workgroup form for small T (one wave per row): each wave loads and
- * routes its row, the rows' status bits are or-ed in LDS, and only a clean
- * batch writes its results. */
+/* Single-workgroup form for small T, two waves per row.  Softmax: both
+ * waves compute the row's exp(s - max); wave 0 takes the ordered sum while
+ * wave 1 selects the K + 1 largest numerators (the quotients p = e / sum
+ * have the same order unless two of them round to the same p), then wave 1
+ * divides its K + 1 selections by the sum: if the K + 1 quotients strictly
+ * decrease, the numerators' order is the reference's and its K selections
+ * stand; otherwise (equal quotients, from equal or one-ulp-apart
+ * numerators) wave 1 divides every value and selects again on the
+ * quotients.  Sigmoid scores need no sum: wave 1 routes alone.  The rows'
+ * status bits are or-ed in LDS, and only a clean batch writes its results. */
 template <int PER>
-__global__ __launch_bounds__(512) void route_small_kernel(RouteArgs a) {
+__global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
     __shared__ uint32_t bad_all;
     __shared__ uint64_t etab[R9VX_EXP2F_N];
     __shared__ __attribute__((aligned(16))) float sbuf[8][PER * 64];
-    const uint32_t lane = threadIdx.x & 63, row = threadIdx.x >> 6;
+    __shared__ float row_sum[8];
+    const uint32_t lane = threadIdx.x & 63, row = threadIdx.x >> 7, role = (threadIdx.x >> 6) & 1u;
     r9vx_exp2_fill(etab, threadIdx.x, blockDim.x);
     if (threadIdx.x == 0) bad_all = 0;
     float sc[PER], lg[PER], bs[PER];
@@ -333,14 +363,41 @@ __global__ __launch_bounds__(512) void route_small_kernel(RouteArgs a) {
     uint32_t bad = 0;
     if (__ballot(bad_row & R9VX_STATUS_NONFINITE)) bad |= R9VX_STATUS_NONFINITE;
     if (__ballot(bad_row & R9VX_STATUS_DEGENERATE)) bad |= R9VX_STATUS_DEGENERATE;
-    if (bad && lane == 0) atomicOr(&bad_all, bad);
-    uint32_t id = 0;
-    float w = 0.0f;
-    if (!bad) route_loaded<PER>(a, lane, sc, etab, sbuf[row], id, w);
+    if (bad && lane == 0 && role == 0) atomicOr(&bad_all, bad);
+    const bool softmax = a.scoring == R9VX_SCORING_SOFTMAX;
+    uint32_t id = 0, col = 0;
+    float w = 0.0f, ev = 0.0f;
+    const uint32_t nsel = a.k < a.e ? a.k + 1 : a.k; /* the K + 1-th decides the boundary */
+    if (!bad && softmax) {
+        softmax_exp<PER>(sc, etab);
+        if (role == 0) {
+            const float sum = ordered_sum<PER>(sc, a.e, lane, sbuf[row]);
+            if (lane == 0) row_sum[row] = sum;
+        } else {
+            select_top<PER>(sc, a.e, nsel, lane, col, ev);
+        }
+    }
     __syncthreads();
     bad = bad_all;
     if (threadIdx.x == 0) *a.status = bad;
-    if (bad) return;
+    if (bad || role == 0) return;
+    if (softmax) {
+        const float sum = row_sum[row];
+        const float p = ev / sum;
+        const float pn = __shfl_down(p, 1, 64);
+        if (__ballot(lane + 1 < nsel && !(p > pn)) == 0ull) {
+            id = col;
+            w = select_weight(a, lane, p);
+        } else { /* equal quotients: select on the quotients themselves */
+#pragma unroll
+            for (int i = 0; i < PER; ++i) sc[i] = sc[i] / sum;
+            float score;
+            select_top<PER>(sc, a.e, a.k, lane, id, score);
+            w = select_weight(a, lane, score);
+        }
+    } else {
+        route_loaded<PER>(a, lane, sc, etab, sbuf[row], id, w);
+    }
     if (lane < a.k) {
         a.ids[(uint64_t)row * a.k + lane] = id;
         a.weights[(uint64_t)row * a.k + lane] = w;
@@ -528,7 +585,7 @@ int r9vx_launch_route_hidden(const r9vx_route_hidden_problem &p, hipStream_t str
 template <int PER>
 static int launch_route_per(const RouteArgs &a, hipStream_t stream) {
     if (a.t <= 8) {
-        hipLaunchKernelGGL((route_small_kernel<PER>), dim3(1), dim3(64 * a.t), 0, stream, a);
+        hipLaunchKernelGGL((route_small_kernel<PER>), dim3(1), dim3(128 * a.t), 0, stream, a);
         return (int)hipGetLastError();
     }
     hipLaunchKernelGGL(clear_status_kernel, dim3(1), dim3(1), 0, stream, a.status);
