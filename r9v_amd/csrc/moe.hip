@@ -708,10 +708,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
  * chunk is loaded and arranged once.  The arithmetic per step is that of
  * moe_gu_kernel / moe_down_kernel. */
 #ifndef R9VX_GU_PIPE_STEPS
-#define R9VX_GU_PIPE_STEPS 2
+#define R9VX_GU_PIPE_STEPS 1
 #endif
 #ifndef R9VX_GU_PIPE_UPW
-#define R9VX_GU_PIPE_UPW 4
+#define R9VX_GU_PIPE_UPW 2
 #endif
 #ifndef R9VX_DN_PIPE_STEPS
 #define R9VX_DN_PIPE_STEPS 1

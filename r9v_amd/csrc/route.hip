@@ -336,53 +336,100 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
     }
 }
 
-/* Single-workgroup form for small T, two waves per row.  Softmax: both
- * waves compute the row's exp(s - max); wave 0 takes the ordered sum while
- * wave 1 selects the K + 1 largest numerators (the quotients p = e / sum
- * have the same order unless two of them round to the same p), then wave 1
- * divides its K + 1 selections by the sum: if the K + 1 quotients strictly
+/* Small-T form: one workgroup of two waves per row.  Softmax: both waves
+ * compute the row's exp(s - max); wave 0 takes the ordered sum while wave 1
+ * selects the K + 1 largest numerators (the quotients p = e / sum have the
+ * same order unless two of them round to the same p), then wave 1 divides
+ * its K + 1 selections by the sum: if the K + 1 quotients strictly
  * decrease, the numerators' order is the reference's and its K selections
- * stand; otherwise (equal quotients, from equal or one-ulp-apart
- * numerators) wave 1 divides every value and selects again on the
- * quotients.  Sigmoid scores need no sum: wave 1 routes alone.  The rows'
- * status bits are or-ed in LDS, and only a clean batch writes its results. */
+ * stand; otherwise (equal or one-ulp-apart numerators whose quotients round
+ * equal) wave 1 divides every value and selects on the quotients.  Sigmoid
+ * scores need no sum: wave 1 routes alone.  The batch-level refusal (no row
+ * is written if any row is bad): every workgroup checks every row, its two
+ * waves taking alternate rows with all their loads in flight at once, so the
+ * rows' workgroups run on separate CUs without talking to each other;
+ * workgroup 0 writes the status word. */
+constexpr uint32_t kRouteSmallT = 8;
+
 template <int PER>
-__global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
+struct CheckRows {
+    static constexpr int R = kRouteSmallT / 2;
+    float lg[R][PER], bs[PER];
+    /* rows first, first + 2, ... (< T) and the bias: loads only */
+    __device__ __forceinline__ void load(const RouteArgs &a, uint32_t first, uint32_t lane) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const uint32_t r = first + 2 * j < a.t ? first + 2 * j : 0u; /* rows past T: row 0, unused */
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const uint32_t c = lane + 64 * i;
+                lg[j][i] = a.logits[(uint64_t)r * a.e + (c < a.e ? c : a.e - 1)];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const uint32_t c = lane + 64 * i;
+            bs[i] = a.bias ? a.bias[c < a.e ? c : a.e - 1] : 0.0f;
+        }
+    }
+    /* the rows' status bits, or-ed */
+    __device__ __forceinline__ uint32_t check(const RouteArgs &a, uint32_t first, uint32_t lane,
+                                              const uint64_t *etab) const {
+        uint32_t bad = 0;
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            if (first + 2 * j >= a.t) break;
+            float sc[PER], l[PER], b[PER];
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const uint32_t c = lane + 64 * i;
+                sc[i] = c < a.e ? (a.bias ? lg[j][i] + bs[i] : lg[j][i]) : -__builtin_huge_valf();
+                l[i] = c < a.e ? lg[j][i] : 0.0f;
+                b[i] = c < a.e ? bs[i] : 0.0f;
+            }
+            const uint32_t bad_row = check_loaded<PER>(a, lane, sc, l, b, etab);
+            if (__ballot(bad_row & R9VX_STATUS_NONFINITE)) bad |= R9VX_STATUS_NONFINITE;
+            if (__ballot(bad_row & R9VX_STATUS_DEGENERATE)) bad |= R9VX_STATUS_DEGENERATE;
+        }
+        return bad;
+    }
+};
+
+template <int PER>
+__global__ __launch_bounds__(128) void route_small_kernel(RouteArgs a) {
     __shared__ uint32_t bad_all;
     __shared__ uint64_t etab[R9VX_EXP2F_N];
-    __shared__ __attribute__((aligned(16))) float sbuf[8][PER * 64];
-    __shared__ float row_sum[8];
-    const uint32_t lane = threadIdx.x & 63, row = threadIdx.x >> 7, role = (threadIdx.x >> 6) & 1u;
+    __shared__ __attribute__((aligned(16))) float sbuf[PER * 64];
+    __shared__ float row_sum;
+    const uint32_t lane = threadIdx.x & 63, role = threadIdx.x >> 6, row = blockIdx.x;
     r9vx_exp2_fill(etab, threadIdx.x, blockDim.x);
     if (threadIdx.x == 0) bad_all = 0;
     float sc[PER], lg[PER], bs[PER];
     load_row<PER>(a, row, lane, sc, lg, bs);
+    CheckRows<PER> cr;
+    cr.load(a, role, lane);
     __syncthreads();
-    const uint32_t bad_row = check_loaded<PER>(a, lane, sc, lg, bs, etab);
-    /* or of the row's status bits: one ballot per bit */
-    uint32_t bad = 0;
-    if (__ballot(bad_row & R9VX_STATUS_NONFINITE)) bad |= R9VX_STATUS_NONFINITE;
-    if (__ballot(bad_row & R9VX_STATUS_DEGENERATE)) bad |= R9VX_STATUS_DEGENERATE;
-    if (bad && lane == 0 && role == 0) atomicOr(&bad_all, bad);
+    const uint32_t bad = cr.check(a, role, lane, etab);
+    if (bad && lane == 0) atomicOr(&bad_all, bad);
     const bool softmax = a.scoring == R9VX_SCORING_SOFTMAX;
     uint32_t id = 0, col = 0;
     float w = 0.0f, ev = 0.0f;
     const uint32_t nsel = a.k < a.e ? a.k + 1 : a.k; /* the K + 1-th decides the boundary */
-    if (!bad && softmax) {
+    if (softmax) {
         softmax_exp<PER>(sc, etab);
         if (role == 0) {
-            const float sum = ordered_sum<PER>(sc, a.e, lane, sbuf[row]);
-            if (lane == 0) row_sum[row] = sum;
+            const float sum = ordered_sum<PER>(sc, a.e, lane, sbuf);
+            if (lane == 0) row_sum = sum;
         } else {
             select_top<PER>(sc, a.e, nsel, lane, col, ev);
         }
     }
     __syncthreads();
-    bad = bad_all;
-    if (threadIdx.x == 0) *a.status = bad;
-    if (bad || role == 0) return;
+    const uint32_t bad_batch = bad_all;
+    if (row == 0 && threadIdx.x == 0) *a.status = bad_batch;
+    if (bad_batch || role == 0) return;
     if (softmax) {
-        const float sum = row_sum[row];
+        const float sum = row_sum;
         const float p = ev / sum;
         const float pn = __shfl_down(p, 1, 64);
         if (__ballot(lane + 1 < nsel && !(p > pn)) == 0ull) {
@@ -396,7 +443,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(RouteArgs a) {
             w = select_weight(a, lane, score);
         }
     } else {
-        route_loaded<PER>(a, lane, sc, etab, sbuf[row], id, w);
+        route_loaded<PER>(a, lane, sc, etab, sbuf, id, w);
     }
     if (lane < a.k) {
         a.ids[(uint64_t)row * a.k + lane] = id;
@@ -584,8 +631,8 @@ int r9vx_launch_route_hidden(const r9vx_route_hidden_problem &p, hipStream_t str
 
 template <int PER>
 static int launch_route_per(const RouteArgs &a, hipStream_t stream) {
-    if (a.t <= 8) {
-        hipLaunchKernelGGL((route_small_kernel<PER>), dim3(1), dim3(128 * a.t), 0, stream, a);
+    if (a.t <= kRouteSmallT) {
+        hipLaunchKernelGGL((route_small_kernel<PER>), dim3(a.t), dim3(128), 0, stream, a);
         return (int)hipGetLastError();
     }
     hipLaunchKernelGGL(clear_status_kernel, dim3(1), dim3(1), 0, stream, a.status);
