@@ -205,6 +205,36 @@ def test_moe_ffn_decode_shapes(t, e, k, dm, dff, shared):
     check_close(got, ref, f"t={t} e={e}")
 
 
+def test_moe_ffn_decode_repeated_calls_one_workspace():
+    """Back-to-back decode calls on one workspace, each with new routing and
+    activations: every y matches the oracle (the down GEMV's last wave per
+    row block sums rows the other waves of the same launch stored, counted
+    per launch), and a refused call in between leaves its y untouched and the
+    next call's status clean."""
+    t, e, k, dm, dff, shared = 5, 32, 4, 512, 256, 1
+    gu, dn = _experts(1401, e, shared, dm, dff, range(e))
+    gu_d, dn_d = dev(gu), dev(dn)
+    ws = st = None
+    for i in range(24):
+        logits = synth.normal_f32(1410 + i, (t, e))
+        ids, w = O.moe_route(logits, k)
+        x = synth.normal_bf16(1450 + i, (t, dm))
+        if i == 12:  # a refused call: an id >= E
+            bad = ids.copy()
+            bad[3, 2] = e
+            y2 = torch.full((t, dm), 7.0, dtype=torch.float32, device="cuda")
+            ffi.moe_ffn(bf16_dev(x), dev(bad.view(np.int32)), dev(w), gu_d, dn_d, e, dff, shared=shared, y=y2,
+                        workspace=ws)
+            assert ffi.moe_ffn_status(st, ws) & ffi.STATUS_BAD_EXPERT
+            assert (host(y2) == 7.0).all()
+        ref = O.moe_ffn(x, O.BF16, ids, w, e, dff, gu, dn, shared=shared)
+        y, ws, st = ffi.moe_ffn(bf16_dev(x), dev(ids.view(np.int32)), dev(w), gu_d, dn_d, e, dff, shared=shared,
+                                workspace=ws)
+        torch.cuda.synchronize()
+        assert ffi.moe_ffn_status(st, ws) == 0
+        check_close(host(y), ref, f"call {i}")
+
+
 def test_moe_ffn_duplicate_slots_and_refusal():
     t, e, k, dm, dff = 4, 8, 3, 256, 256
     ids = np.array([[1, 1, 5], [0, 7, 7], [2, 3, 4], [6, 6, 6]], dtype=np.uint32)
