@@ -25,7 +25,6 @@
  */
 #include <type_traits>
 
-#include "r9vx_expf.h"
 #include "r9vx_gemv_core.h"
 #include "r9vx_mfma.h"
 #include "r9vx_moe.h"
@@ -551,10 +550,8 @@ template <int GU>
 __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
     constexpr bool kIq3 = GU == R9VX_SCHEME_IQ3_S;
     __shared__ __attribute__((aligned(16))) uint32_t lut[kIq3 ? 1024 : 256];
-    __shared__ uint64_t etab[R9VX_EXP2F_N];
     if constexpr (GU == R9VX_SCHEME_IQ4_XS) init_iq4_lut(lut, threadIdx.x, blockDim.x);
     if constexpr (kIq3) build_iq3s_lut(lut, threadIdx.x, blockDim.x);
-    r9vx_exp2_fill(etab, threadIdx.x, blockDim.x);
     __syncthreads(); /* the last barrier: waves run independently from here */
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t lpr = 1u << a.gu_lpr_log2, rpi = 64u >> a.gu_lpr_log2;
@@ -613,9 +610,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_kernel(FfnArgs a) {
                 lane_reduce_w<kDecPairs, 2>(gu, lane, a.gu_lpr_log2, [&](int r, const float (&val)[2]) {
                     const uint32_t row = (g * kDecPairs + r) * rpi + slot;
                     if (row >= a.dff) return;
-                    const float gg = val[0];
-                    const float act = gg / (1.0f + r9vx_expf_tab(-gg, etab));
-                    h[(uint64_t)pos * a.dff + row] = act * val[1];
+                    h[(uint64_t)pos * a.dff + row] = swiglu_fast(val[0], val[1]);
                 });
             }
             advance(c, nseg, groups);
@@ -703,9 +698,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_down_kernel(FfnArgs a) {
  * wait a wait for everything.  The step outputs wait in LDS and are stored
  * after the wave's last load, because a store issued between two loads
  * turns the wait for the older load into a wait for every outstanding
- * memory operation; the gate/up kernel applies SiLU(g) * u there, one row
- * per lane.  A lane's K chunk is the same in every step, so its activation
- * chunk is loaded and arranged once.  The arithmetic per step is that of
+ * memory operation; the gate/up kernel applies SiLU(g) * u there (the
+ * hardware exp and reciprocal, as the grouped GEMMs), one row per lane.  A
+ * lane's K chunk is the same in every step, so its activation chunk is
+ * loaded and arranged once.  The arithmetic per step is that of
  * moe_gu_kernel / moe_down_kernel. */
 #ifndef R9VX_GU_PIPE_STEPS
 #define R9VX_GU_PIPE_STEPS 1
@@ -725,16 +721,15 @@ constexpr uint32_t kDnPipeSteps = R9VX_DN_PIPE_STEPS, kDnPipeUpw = R9VX_DN_PIPE_
 static_assert((kDecPairs & (kDecPairs - 1)) == 0 && (kDecDnRows & (kDecDnRows - 1)) == 0,
               "rows per step must be a power of two");
 
-/* The LDS tables of a decode kernel (IQ4_XS codebook pairs, IQ3_S grid,
- * exp2 table for the SiLU), loaded to registers as the kernel's first
- * memory operations and written to LDS after the first weight loads are
- * issued: loads complete in order, so the LDS writes wait for the table
- * words only, and the tables' latency overlaps the weights'. */
-template <int S, bool kExp>
+/* The LDS tables of a decode kernel (IQ4_XS codebook pairs, IQ3_S grid),
+ * loaded to registers as the kernel's first memory operations and written
+ * to LDS after the first weight loads are issued: loads complete in order,
+ * so the LDS writes wait for the table words only, and the tables' latency
+ * overlaps the weights'. */
+template <int S>
 struct DecTables {
     r9vx_u32x4 iq4;
     uint32_t g[2];
-    uint64_t ex;
     __device__ __forceinline__ void load(uint32_t tid) {
         if constexpr (S == R9VX_SCHEME_IQ4_XS)
             if (tid < 64) iq4 = reinterpret_cast<const r9vx_u32x4 *>(kIq4PairLut.v)[tid];
@@ -743,10 +738,8 @@ struct DecTables {
             for (int i = 0; i < 2; ++i)
                 if (tid + 256 * i < 512) g[i] = kIq3sGrid[tid + 256 * i];
         }
-        if constexpr (kExp)
-            if (tid < R9VX_EXP2F_N) ex = r9vx_exp2_table[tid];
     }
-    __device__ __forceinline__ void store(uint32_t *lut, uint64_t *etab, uint32_t tid) const {
+    __device__ __forceinline__ void store(uint32_t *lut, uint32_t tid) const {
         if constexpr (S == R9VX_SCHEME_IQ4_XS)
             if (tid < 64) reinterpret_cast<r9vx_u32x4 *>(lut)[tid] = iq4;
         if constexpr (S == R9VX_SCHEME_IQ3_S) {
@@ -761,8 +754,6 @@ struct DecTables {
                 lut[2 * e + 1] = h[2] | (h[3] << 16);
             }
         }
-        if constexpr (kExp)
-            if (tid < R9VX_EXP2F_N) etab[tid] = ex;
     }
 };
 
@@ -800,9 +791,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_pipe_kernel(FfnArgs a) 
     constexpr bool kIq3 = GU == R9VX_SCHEME_IQ3_S;
     constexpr uint32_t kObuf = kGuPipeUpw * kDecPairs * 8; /* rows per wave, at most */
     __shared__ __attribute__((aligned(16))) uint32_t lut[kIq3 ? 1024 : 256];
-    __shared__ uint64_t etab[R9VX_EXP2F_N];
     __shared__ float2 obuf[kDecWaves][kObuf]; /* (gate, up) dot of each row */
-    DecTables<GU, true> tb;
+    DecTables<GU> tb;
     tb.load(threadIdx.x);
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t rpi = 64u >> a.gu_lpr_log2, rps = kDecPairs * rpi;
@@ -847,7 +837,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_pipe_kernel(FfnArgs a) 
     };
     GuRegs<GU> wa[kGuPipeSteps], wb[kGuPipeSteps];
     issue(wa);
-    tb.store(lut, etab, threadIdx.x);
+    tb.store(lut, threadIdx.x);
     lds_only_barrier(); /* the last barrier: waves run independently from here */
     if (!ok) return;
     arrange_x<GU, false>(xr, xc[0]);
@@ -868,8 +858,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_gu_pipe_kernel(FfnArgs a) 
     const uint32_t nrows = min(n * rps, a.dff - g0 * rps);
     for (uint32_t j = lane; j < nrows; j += 64) {
         const float2 v = ob[j];
-        const float act = v.x / (1.0f + r9vx_expf_tab(-v.x, etab));
-        h[j] = act * v.y;
+        h[j] = swiglu_fast(v.x, v.y);
     }
 }
 
@@ -879,7 +868,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_down_pipe_kernel(FfnArgs a
     constexpr uint32_t kObuf = kDnPipeUpw * kDecDnRows * 8;
     __shared__ __attribute__((aligned(16))) uint32_t lut[kIq3 ? 1024 : 256];
     __shared__ float obuf[kDecWaves][kObuf];
-    DecTables<DN, false> tb;
+    DecTables<DN> tb;
     tb.load(threadIdx.x);
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t rpi = 64u >> a.dn_lpr_log2, rps = kDecDnRows * rpi;
@@ -920,7 +909,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void moe_down_pipe_kernel(FfnArgs a
     };
     DnRegs<DN> wa[kDnPipeSteps], wb[kDnPipeSteps];
     issue(wa);
-    tb.store(lut, nullptr, threadIdx.x);
+    tb.store(lut, threadIdx.x);
     lds_only_barrier(); /* the last barrier: waves run independently from here */
     if (!ok) return;
     dn_arrange<DN>(xr, hx);

@@ -66,13 +66,6 @@ __device__ __forceinline__ void xcd_tile(uint32_t ncol, uint32_t &tix, uint32_t 
     nt = j % ncol;
 }
 
-/* silu(g) * u with the hardware exp and reciprocal (about 2 ulp each; T0's
- * f32 expf and divide, crates/r9v-t0/src/activation.rs:135-138, are matched
- * well inside the matmul tolerance). */
-__device__ __forceinline__ float swiglu_fast(float g, float u) {
-    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f)) * u;
-}
-
 __device__ __forceinline__ uint32_t row_token(const GroupedArgs &a, uint32_t expert, uint32_t pos) {
     if (expert >= a.e) return pos - (a.p + (expert - a.e) * a.t);
     return ws_u32(a, a.L.sorted)[pos] / a.k;

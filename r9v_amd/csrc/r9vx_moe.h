@@ -98,6 +98,13 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
 int r9vx_moe_combine_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
 
 /* Byte offset (from L.o) of the grouped path's per-(row, 64-column) scales. */
+/* silu(g) * u with the hardware exp and reciprocal (about 2 ulp each; T0's
+ * f32 expf and divide, crates/r9v-t0/src/activation.rs:135-138, are matched
+ * well inside the matmul tolerance). */
+__device__ __forceinline__ float swiglu_fast(float g, float u) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f)) * u;
+}
+
 __host__ __device__ inline uint64_t r9vx_moe_oscale_offset(uint64_t rows, uint32_t dm) { return (2ull * rows * dm + 255) & ~255ull; }
 
 #endif
