@@ -173,6 +173,39 @@ __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t n
     const uint32_t *status = ws_u32(a, a.L.status);
     if (status[0] != 0u) return;
     const float *hr = reinterpret_cast<const float *>(a.ws + a.L.h) + (uint64_t)row * a.dff;
+    _Float16 *orow = a.h16 + (uint64_t)row * a.dff;
+    if (a.dff <= 1024) {
+        /* one pass: the lane loads the values it writes (all of the row
+         * between the wave's lanes), takes the row max from them and
+         * converts from registers */
+        r9vx_f32x4 lo[2], hi[2];
+        float mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t c = lane + 64 * i;
+            const uint32_t cc = c < a.dff / 8 ? c : 0u;
+            const uint32_t base = (cc >> 3) * 64, q = cc & 7;
+            lo[i] = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + h_group_k<DN>(q, 0));
+            hi[i] = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + h_group_k<DN>(q, 4));
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(lo[i].x), fabsf(lo[i].y)), fmaxf(fabsf(lo[i].z), fabsf(lo[i].w))),
+                                 fmaxf(fmaxf(fabsf(hi[i].x), fabsf(hi[i].y)), fmaxf(fabsf(hi[i].z), fabsf(hi[i].w)))));
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        if (lane == 0) reinterpret_cast<uint32_t *>(a.ws + a.L.hmax)[row] = __builtin_bit_cast(uint32_t, mx);
+        const float inv = ldexpf(1.0f, -row_shift(mx));
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t c = lane + 64 * i;
+            if (c >= a.dff / 8) break;
+            *reinterpret_cast<r9vx_u32x4 *>(orow + 8 * c) = r9vx_u32x4{
+                pack_h2(lo[i].x * inv, lo[i].y * inv), pack_h2(lo[i].z * inv, lo[i].w * inv),
+                pack_h2(hi[i].x * inv, hi[i].y * inv), pack_h2(hi[i].z * inv, hi[i].w * inv)};
+        }
+        return;
+    }
     float mx = 0.f;
     for (uint32_t c = lane; c < a.dff / 4; c += 64) {
         const r9vx_f32x4 v = *reinterpret_cast<const r9vx_f32x4 *>(hr + 4 * c);
@@ -182,7 +215,6 @@ __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t n
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
     if (lane == 0) reinterpret_cast<uint32_t *>(a.ws + a.L.hmax)[row] = __builtin_bit_cast(uint32_t, mx);
     const float inv = ldexpf(1.0f, -row_shift(mx));
-    _Float16 *orow = a.h16 + (uint64_t)row * a.dff;
     for (uint32_t c = lane; c < a.dff / 8; c += 64) {
         const uint32_t base = (c >> 3) * 64, q = c & 7;
         const r9vx_f32x4 lo = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + h_group_k<DN>(q, 0));
