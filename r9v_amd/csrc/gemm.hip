@@ -22,6 +22,7 @@
  */
 #include "r9vx_mma.h"
 #include "r9vx_mma2.h"
+#include "r9vx_mma3.h"
 
 using namespace r9vx;
 
@@ -274,6 +275,95 @@ __global__ __launch_bounds__(512, 1) void gemm2_kernel(GemmArgs a) {
     }
 }
 
+/* 256 x 256 tiles on the r9vx_mma3.h loop (the grouped MoE GEMMs' core): the
+ * weight tile is decoded once per workgroup into LDS, every wave reads its
+ * B fragments from there, and the accumulators are the transposed tile, so
+ * lane l holds output row 128 rh + 32 t + (l & 31) and columns 64 cq + 32 j +
+ * 8 (r >> 2) + 4 (l >> 5) + (r & 3) of acc[t][j][r].  The launcher takes it
+ * for n % 256 == 0 and m k < 2^31 (the A copy offsets are 32-bit). */
+template <int SCHEME>
+__global__ __launch_bounds__(512, 1) void gemm3_kernel(GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) M3Lds sm;
+    __shared__ float rowsc[kM3Rows];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t total = a.m_tiles * a.n_tiles;
+    uint32_t t = blockIdx.x;
+    if (total % 8 == 0) t = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
+    const uint32_t n_tile = t / a.m_tiles, m_tile = t % a.m_tiles;
+    const uint32_t m0 = m_tile * kM3Rows, n0 = n_tile * kM3Cols;
+    const uint32_t rows = a.m - m0 < kM3Rows ? a.m - m0 : kM3Rows;
+    const float rsc = tid < rows ? a.scale[m0 + tid] : 0.f;
+    if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) m3_init_iq4_lut(sm.lut, tid, 512);
+    __syncthreads();
+
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t aoff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = dma_row(wv, i, lane);
+        aoff[i] = ((m0 + (r < rows ? r : 0)) * a.k + 8 * dma_group(r, lane)) * 2u;
+    }
+    const M3WRow w{m3_uniform(a.w + (uint64_t)n0 * a.w_row_stride), m3_brow(tid) * (uint32_t)a.w_row_stride};
+    const uint32_t rh = wv >> 2, cq = wv & 3;
+    const uint32_t nr = m3_active_tiles(rows, 128 * rh);
+    r9vx_f32x16 acc[4][2];
+    m3_run<SCHEME, true>(nr, sm, a.x16, aoff, w, a.k / kTileK, tid, wv, sm.lut, 128 * rh, 64 * cq, 64 * cq + 32, acc);
+    if (tid < kM3Rows) rowsc[tid] = rsc;
+    __syncthreads();
+
+    /* y = acc * 2^e (the activation row's scale, exact) [+ bias | + residual]
+     * in f32, then the output cast.  bf16 rows are staged in LDS (row R's
+     * 8-byte chunk c at chunk c ^ (R & 31)) and leave as whole 512-byte
+     * rows; f32 rows are stored 16 bytes per lane from the accumulators. */
+    uint8_t *const ot = m3_out_tile(sm);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+        if ((uint32_t)tt >= nr) break;
+        const uint32_t rl = 128 * rh + 32 * tt + (lane & 31);
+        const uint32_t row = m0 + (rl < rows ? rl : 0);
+        const float sc = rowsc[rl];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t cl = 64u * cq + 32u * j + 8u * g + 4u * (lane >> 5);
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = acc[tt][j][4 * g + e] * sc;
+                if (a.epilogue == R9VX_EPILOGUE_BIAS) {
+                    const r9vx_f32x4 bb = *reinterpret_cast<const r9vx_f32x4 *>(a.bias + n0 + cl);
+                    v[0] += bb.x, v[1] += bb.y, v[2] += bb.z, v[3] += bb.w;
+                } else if (a.epilogue == R9VX_EPILOGUE_RESIDUAL) {
+                    const r9vx_f32x4 bb =
+                        *reinterpret_cast<const r9vx_f32x4 *>(a.residual + (uint64_t)row * a.n + n0 + cl);
+                    v[0] += bb.x, v[1] += bb.y, v[2] += bb.z, v[3] += bb.w;
+                }
+                if (a.y_bf16) {
+                    const uint32_t chunk = (cl >> 2) ^ (rl & 31u);
+                    *reinterpret_cast<r9vx_u32x2 *>(ot + rl * 512u + 8u * chunk) = r9vx_u32x2{
+                        (uint32_t)r9vx_f32_to_bf16(v[0]) | ((uint32_t)r9vx_f32_to_bf16(v[1]) << 16),
+                        (uint32_t)r9vx_f32_to_bf16(v[2]) | ((uint32_t)r9vx_f32_to_bf16(v[3]) << 16)};
+                } else if (rl < rows) {
+                    *reinterpret_cast<r9vx_f32x4 *>(reinterpret_cast<float *>(a.y) + (uint64_t)row * a.n + n0 + cl) =
+                        r9vx_f32x4{v[0], v[1], v[2], v[3]};
+                }
+            }
+    }
+    if (!a.y_bf16) return;
+    __syncthreads();
+    const uint32_t q = lane & 31;
+    uint16_t *const y = reinterpret_cast<uint16_t *>(a.y);
+#pragma unroll 4
+    for (uint32_t i = 0; i < 16; ++i) {
+        const uint32_t R = 16 * i + 2 * wv + (lane >> 5);
+        if (R >= rows) break; /* rows grow with i */
+        const uint32_t s = R & 31u;
+        r9vx_u32x4 v = *reinterpret_cast<const r9vx_u32x4 *>(ot + R * 512u + 16u * (q ^ (s >> 1)));
+        if (s & 1u) v = r9vx_u32x4{v.z, v.w, v.x, v.y}; /* the granule's halves were swapped */
+        *reinterpret_cast<r9vx_u32x4 *>(y + (uint64_t)(m0 + R) * a.n + n0 + 8 * q) = v;
+    }
+}
+
 }  // namespace
 
 size_t r9vx_gemm_workspace_bytes(uint32_t m_bucket, uint32_t k) {
@@ -329,6 +419,13 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
         a.m_tiles = (p.m + kM2Rows - 1) / kM2Rows;
         a.n_tiles = (p.n + kM2Cols - 1) / kM2Cols;
         dim3 grid(a.m_tiles * a.n_tiles);
+        if (p.n % kM3Cols == 0 && (uint64_t)p.m * p.k < (1ull << 31)) {
+            if (p.scheme == R9VX_SCHEME_Q4_K)
+                hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_Q4_K>), grid, dim3(512), 0, stream, a);
+            else
+                hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_IQ4_XS>), grid, dim3(512), 0, stream, a);
+            return (int)hipGetLastError();
+        }
         if (p.scheme == R9VX_SCHEME_Q4_K)
             hipLaunchKernelGGL((gemm2_kernel<R9VX_SCHEME_Q4_K>), grid, dim3(512), 0, stream, a);
         else
