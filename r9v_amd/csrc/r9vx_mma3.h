@@ -17,7 +17,8 @@
  *     16-K slice it reads 2 B and NR A fragments for 2 NR MFMAs
  *     (v_mfma_f32_32x32x16_f16), fragments two MFMA pairs ahead.
  * Per K step: one barrier (B(k) and A(k) complete; step k - 1's tile and
- * stage free), the A(k + 1) copy and the payload load of step k + 3 issued,
+ * stage free), the A(k + 1) copy and the payload load of step k + 4 issued
+ * (into the buffer of payload k, whose B was decoded in step k - 1),
  * then the MFMAs of step k interleaved with the decode and writes of
  * B(k + 1), then a wait for the A(k + 1) copy.
  *
@@ -302,8 +303,8 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
  * J == 3; it is loaded at J == 1 into hnext and copied to hcur at J == 3.
  * Step k: barrier (B(k) and A(k) are complete and visible, and every wave is
  * done with step k - 1's A stage and B tile), the copy of A(k + 1) into the
- * other A stage and the payload load of step k + 3 (plus the next block
- * header when J == 1), then the MFMAs of step k interleaved with the decode
+ * other A stage and the payload load of step k + 4 into the buffer of
+ * payload k (plus the next block header when J == 1), then the MFMAs of step k interleaved with the decode
  * of B(k + 1), each of whose four 16-byte granules is written into the other
  * B tile as soon as it is whole, then a wait for the A(k + 1) copy.
  */
@@ -318,19 +319,20 @@ __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, co
 #pragma unroll
     for (int i = 0; i < 4; ++i) pay[i] = r9vx_u32x4{0u, 0u, 0u, 0u};
     hnext = r9vx_u32x4{0u, 0u, 0u, 0u};
-    /* prologue: P0 H0 | A0 | P1 P2; B(0) decoded into B tile 0 */
+    /* prologue: P0 H0 | A0 | P1 P2 P3; B(0) decoded into B tile 0 */
     m3_load_pay<SCHEME>(w, 0, hh, pay[0]);
     m3_load_hdr<SCHEME>(w, 0, hnext);
     m3_dma_a(a_lds, abase, aoff, 0, wave);
     m3_load_pay<SCHEME>(w, 1, hh, pay[1]);
     m3_load_pay<SCHEME>(w, 2, hh, pay[2]);
-    wait_vm<6>(); /* P0, H0 */
+    m3_load_pay<SCHEME>(w, 3 < nk ? 3 : nk - 1, hh, pay[3]);
+    wait_vm<7>(); /* P0, H0 */
     touch_pay(pay[0]);
     touch_pay(hnext);
     hcur = hnext;
     m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], hcur, hh, lut, sm.b[0] + c * 128u,
                                  bsw);
-    wait_vm<1>(); /* A0, P1 */
+    wait_vm<2>(); /* A0, P1 */
     touch_pay(pay[1]);
 
     for (uint32_t k0 = 0; k0 < nk; k0 += 4) {
@@ -339,7 +341,7 @@ __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, co
         const uint32_t k = k0 + J;                                                                           \
         lds_barrier(); /* B(k), A(k) visible; step k - 1's tile and stage are free */                        \
         m3_dma_a(a_lds + ((k + 1) & 1u) * kM3Stage, abase, aoff, k + 1 < nk ? k + 1 : nk - 1, wave);          \
-        m3_load_pay<SCHEME>(w, k + 3 < nk ? k + 3 : nk - 1, hh, pay[(J + 3) & 3]);                            \
+        m3_load_pay<SCHEME>(w, k + 4 < nk ? k + 4 : nk - 1, hh, pay[J & 3]);                                  \
         if (J == 1) {                                                                                        \
             const uint32_t blk = (k + 3) / 4 < nk / 4 ? (k + 3) / 4 : nk / 4 - 1;                             \
             m3_load_hdr<SCHEME>(w, blk, hnext);                                                              \
