@@ -346,7 +346,7 @@ __global__ __launch_bounds__(512, 1) void gemm3_kernel(GemmArgs a) {
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
-    m3_run<SCHEME, true>(nr, sm, a.x16, aoff, w, a.k / kTileK, tid, wv, sm.lut, 128 * rh, 64 * cq, 64 * cq + 32, acc);
+    m3_run<SCHEME, true>(nr, rows <= 128, sm, a.x16, aoff, w, a.k / kTileK, tid, wv, sm.lut, 128 * rh, 64 * cq, 64 * cq + 32, acc);
     if (tid < kM3Rows) rowsc[tid] = rsc;
     __syncthreads();
 

@@ -352,7 +352,7 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
-    m3_run<GU>(nr, sm, a.x16, aoff, w, a.dm / kTileK, tid, wv, lut, 128 * rh, 32 * cq, 128 + 32 * cq, acc);
+    m3_run<GU>(nr, rows <= 128, sm, a.x16, aoff, w, a.dm / kTileK, tid, wv, lut, 128 * rh, 32 * cq, 128 + 32 * cq, acc);
     if (tid < kMoeTileM3) rowsc[tid] = rsc;
     __syncthreads();
 
@@ -403,7 +403,7 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
-    m3_run<DN, true>(nr, sm, a.h16, aoff, w, a.dff / kTileK, tid, wv, lut, 128 * rh, 64 * cq, 64 * cq + 32, acc);
+    m3_run<DN, true>(nr, rows <= 128, sm, a.h16, aoff, w, a.dff / kTileK, tid, wv, lut, 128 * rh, 64 * cq, 64 * cq + 32, acc);
     if (tid < kMoeTileM3) rowsc[tid] = tid < rows ? ldexpf(1.0f, row_shift(__builtin_bit_cast(float, hbits))) : 0.f;
     __syncthreads();
 

@@ -368,6 +368,94 @@ __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, co
     touch_pay(hnext);
 }
 
+/*
+ * The main loop for tiles of at most 128 rows (only waves 0-3 own rows: a
+ * wave of rows 128-255 decodes and runs no MFMA).  A step of such a tile has
+ * little MFMA work to hide the copy of the next A step behind, so A goes
+ * through a ring of four 128-row slots (16 KiB each, the two A stages' space):
+ * waves 0-3 copy A(k + 3) at step k into the slot A(k - 1) left, and the
+ * other waves copy nothing.  Per step the loads are issued in the order
+ * [next block header when J == 0], A(k + 3) (waves 0-3), payload k + 4; the
+ * wait at the end of step k is for A(k + 1) and payload k + 2, both issued
+ * in step k - 2, so the loads of steps k - 1 and k may stay in flight.  The
+ * prologue issues A(1) P(2) and A(2) P(3) as steps -2 and -1 would have.  The
+ * block header is loaded at J == 0 and used from J == 3 on (the wait at the
+ * end of J == 2 covers it).
+ */
+template <int SCHEME, int NR, bool TR>
+__device__ __forceinline__ void m3_mainloop_half(M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
+                                                 const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave,
+                                                 const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
+                                                 r9vx_f32x16 (&acc)[4][2]) {
+    constexpr uint32_t kSlot = kM3Stage / 2;
+    const uint32_t lane = tid & 63, c = m3_brow(tid), hh = tid & 1, bsw = m2_swz(c);
+    const uint32_t a_lds = m3_lds_addr(&sm.a[0][0]);
+    const bool dma = wave < 4; /* uniform */
+    r9vx_u32x4 pay[4], hnext, hcur;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pay[i] = r9vx_u32x4{0u, 0u, 0u, 0u};
+    hnext = r9vx_u32x4{0u, 0u, 0u, 0u};
+    /* prologue: P0 H0 A0 P1 | A1 P2 | A2 P3; B(0) decoded into B tile 0 */
+    m3_load_pay<SCHEME>(w, 0, hh, pay[0]);
+    m3_load_hdr<SCHEME>(w, 0, hnext);
+    if (dma) m3_dma_a(a_lds, abase, aoff, 0, wave);
+    m3_load_pay<SCHEME>(w, 1, hh, pay[1]);
+    if (dma) m3_dma_a(a_lds + kSlot, abase, aoff, 1, wave);
+    m3_load_pay<SCHEME>(w, 2, hh, pay[2]);
+    if (dma) m3_dma_a(a_lds + 2 * kSlot, abase, aoff, 2, wave);
+    m3_load_pay<SCHEME>(w, 3, hh, pay[3]);
+    if (dma)
+        wait_vm<15>(); /* P0, H0 */
+    else
+        wait_vm<3>();
+    touch_pay(pay[0]);
+    touch_pay(hnext);
+    hcur = hnext;
+    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], hcur, hh, lut, sm.b[0] + c * 128u,
+                                 bsw);
+    if (dma)
+        wait_vm<10>(); /* A0, P1 */
+    else
+        wait_vm<2>();
+    touch_pay(pay[1]);
+
+    for (uint32_t k0 = 0; k0 < nk; k0 += 4) {
+#define R9VX_M3H_STEP(J)                                                                                     \
+    {                                                                                                        \
+        const uint32_t k = k0 + J;                                                                           \
+        lds_barrier(); /* B(k), A(k) visible; step k - 1's tile and slot are free */                         \
+        if (J == 0) {                                                                                        \
+            const uint32_t blk = (k + 4) / 4 < nk / 4 ? (k + 4) / 4 : nk / 4 - 1;                             \
+            m3_load_hdr<SCHEME>(w, blk, hnext);                                                              \
+        }                                                                                                    \
+        if (dma) m3_dma_a(a_lds + ((J + 3) & 3) * kSlot, abase, aoff, k + 3 < nk ? k + 3 : nk - 1, wave);     \
+        m3_load_pay<SCHEME>(w, k + 4 < nk ? k + 4 : nk - 1, hh, pay[J & 3]);                                  \
+        if (J == 3) {                                                                                        \
+            touch_pay(hnext);                                                                                \
+            hcur = hnext;                                                                                    \
+        }                                                                                                    \
+        m3_compute<SCHEME, (J + 1) & 3, NR, TR>(sm.a[0] + J * kSlot, sm.b[k & 1u], lane, arow0, bc0, bc1, acc, \
+                                                pay[(J + 1) & 3], hcur, hh, lut, sm.b[(k + 1) & 1u] + c * 128u, bsw); \
+        __builtin_amdgcn_sched_barrier(0);                                                                   \
+        /* A(k + 1) and payload k + 2 (steps k - 1 and k may stay in flight) */                              \
+        if (dma)                                                                                             \
+            wait_vm<(J <= 1 ? 11 : 10)>();                                                                   \
+        else                                                                                                 \
+            wait_vm<(J <= 1 ? 3 : 2)>();                                                                     \
+        touch_pay(pay[(J + 2) & 3]);                                                                         \
+    }
+        R9VX_M3H_STEP(0)
+        R9VX_M3H_STEP(1)
+        R9VX_M3H_STEP(2)
+        R9VX_M3H_STEP(3)
+#undef R9VX_M3H_STEP
+    }
+    wait_vm<0>();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) touch_pay(pay[i]);
+    touch_pay(hnext);
+}
+
 /* Number of 32-row tiles of rows [row0, row0 + 128) that hold rows < rows. */
 __device__ __forceinline__ uint32_t m3_active_tiles(uint32_t rows, uint32_t row0) {
     if (rows <= row0) return 0;
@@ -375,14 +463,16 @@ __device__ __forceinline__ uint32_t m3_active_tiles(uint32_t rows, uint32_t row0
     return n < 4 ? n : 4;
 }
 
-/* Runs the main loop with the wave's active row-tile count as a constant.
+/* Runs the main loop with the wave's active row-tile count as a constant;
+ * half (tiles of at most 128 rows) takes m3_mainloop_half.
  * TR: acc[t][j] holds the transposed tile (B rows bc_j.. as its rows, A rows
  * arow0 + 32 t.. as its columns): lane l then holds A row arow0 + 32 t +
  * (l & 31) and B rows bc_j + 8 (r >> 2) + 4 (l >> 5) + (r & 3). */
 template <int SCHEME, bool TR = false>
-__device__ __forceinline__ void m3_run(uint32_t nr, M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
-                                       const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave, const uint32_t *lut,
-                                       uint32_t arow0, uint32_t bc0, uint32_t bc1, r9vx_f32x16 (&acc)[4][2]) {
+__device__ __forceinline__ void m3_run(uint32_t nr, bool half, M3Lds &sm, const _Float16 *abase,
+                                       const uint32_t (&aoff)[4], const M3WRow &w, uint32_t nk, uint32_t tid,
+                                       uint32_t wave, const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
+                                       r9vx_f32x16 (&acc)[4][2]) {
 
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -390,6 +480,16 @@ __device__ __forceinline__ void m3_run(uint32_t nr, M3Lds &sm, const _Float16 *a
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[t][j][r] = 0.f;
+    if (half) { /* the tile's rows fit waves 0-3 (uniform over the workgroup) */
+        switch (nr) {
+        case 4: m3_mainloop_half<SCHEME, 4, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+        case 3: m3_mainloop_half<SCHEME, 3, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+        case 2: m3_mainloop_half<SCHEME, 2, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+        case 1: m3_mainloop_half<SCHEME, 1, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+        default: m3_mainloop_half<SCHEME, 0, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+        }
+        return;
+    }
     switch (nr) {
     case 4: m3_mainloop<SCHEME, 4, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
     case 3: m3_mainloop<SCHEME, 3, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
