@@ -69,10 +69,21 @@ using namespace r9vx;
  * same with the K segment count read from the arguments); LPRL = 0:
  * lanes per row, segment count and epilogue come from the arguments and
  * the rows per lane group from rows_for(M). */
-template <int SCHEME, int M, bool XF32, int SPL, int LPRL, int RR, int NS = 1>
-__global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
-    constexpr int kRows = RR ? RR : rows_for(M), kWaves = waves_for(M);
+/* XS (single-segment 64-lane form only): four waves per workgroup, one per
+ * SIMD of a CU, share the activation slices: the workgroup copies them once
+ * into LDS in lane order (piece j of chunk s of row t for lane l at
+ * ((s M + t) NP + j) 64 + l, so each wave's 16-byte reads are contiguous
+ * across its lanes) and every wave reads its slices from there, instead of
+ * each wave loading all of x from L2. */
+template <int SCHEME, int M, bool XF32, int SPL, int LPRL, int RR, int NS = 1, bool XS = false>
+__global__ __launch_bounds__(XS ? 256 : waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
+    static_assert(!XS || (LPRL == 6 && NS == 1), "x staging needs the single-segment 64-lane form");
+    constexpr int kRows = RR ? RR : rows_for(M), kWaves = XS ? 4 : waves_for(M);
+    constexpr int kNP = XF32 ? 8 : 4; /* 16-byte pieces of a lane's chunk of one x row */
+    constexpr int kPieces = XS ? SPL * M * kNP * 64 : 1;
+    constexpr int kPass = (kPieces + 255) / 256;
     __shared__ __attribute__((aligned(16))) uint32_t lut[lut_words(SCHEME)];
+    __shared__ __attribute__((aligned(16))) r9vx_u32x4 xs[kPieces];
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
     const uint32_t lprl = LPRL ? (uint32_t)LPRL : a.lpr_log2;
@@ -97,15 +108,35 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
          * every weight load of this wave: loads complete in order, so the
          * math on row 0 can start while later rows are still in flight */
         XRaw<XF32> xr[SPL][M];
+        r9vx_u32x4 xst[kPass];
+        if constexpr (XS) {
+            /* this thread's pieces of the workgroup's copy */
 #pragma unroll
-        for (int s = 0; s < SPL; ++s) {
-            uint32_t klo, khi;
-            chunk_k<SCHEME>(cis[s], klo, khi);
+            for (int q = 0; q < kPass; ++q) {
+                const uint32_t idx = threadIdx.x + 256u * q;
+                if (kPieces % 256 == 0 || idx < (uint32_t)kPieces) {
+                    const uint32_t l = idx & 63u, j = (idx >> 6) % kNP, t = (idx >> 6) / kNP % M,
+                                   sp = (idx >> 6) / kNP / M;
+                    uint32_t klo, khi;
+                    chunk_k<SCHEME>(sp * 64u + l, klo, khi);
+                    constexpr uint32_t kPer = XF32 ? 4 : 8; /* elements per piece */
+                    const uint32_t e = j < kNP / 2 ? klo + kPer * j : khi + kPer * (j - kNP / 2);
+                    const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.x) +
+                                        ((uint64_t)t * a.x_row_stride + e) * (XF32 ? 4 : 2);
+                    xst[q] = *reinterpret_cast<const r9vx_u32x4 *>(xb);
+                }
+            }
+        } else {
 #pragma unroll
-            for (int t = 0; t < M; ++t) {
-                const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.x) +
-                                    (uint64_t)t * a.x_row_stride * (XF32 ? 4 : 2);
-                load_x_raw<XF32>(xb, klo, khi, xr[s][t]);
+            for (int s = 0; s < SPL; ++s) {
+                uint32_t klo, khi;
+                chunk_k<SCHEME>(cis[s], klo, khi);
+#pragma unroll
+                for (int t = 0; t < M; ++t) {
+                    const uint8_t *xb = reinterpret_cast<const uint8_t *>(a.x) +
+                                        (uint64_t)t * a.x_row_stride * (XF32 ? 4 : 2);
+                    load_x_raw<XF32>(xb, klo, khi, xr[s][t]);
+                }
             }
         }
         /* keep every activation load ahead of the weight loads: loads
@@ -130,17 +161,38 @@ __global__ __launch_bounds__(waves_for(M) * 64) void gemv_kernel(GemvArgs a) {
                     load_chunk<SCHEME>(wrow, cis[s], qs[r][s], hd[r][s]);
             }
         }
-        /* 2. the codebook table is built while the loads are in flight */
+        /* 2. the codebook table is built (and the activation copy stored)
+         * while the weight loads are in flight */
         if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
             if ((LPRL != 0 && NS == 1) || seg == 0) {
                 build_iq4_lut(lut, threadIdx.x, blockDim.x);
-                __syncthreads();
+                if constexpr (!XS) __syncthreads();
             }
         } else if constexpr (SCHEME == R9VX_SCHEME_IQ3_S) {
             if ((LPRL != 0 && NS == 1) || seg == 0) {
                 build_iq3s_lut(lut, threadIdx.x, blockDim.x);
-                __syncthreads();
+                if constexpr (!XS) __syncthreads();
             }
+        }
+        if constexpr (XS) {
+#pragma unroll
+            for (int q = 0; q < kPass; ++q) {
+                const uint32_t idx = threadIdx.x + 256u * q;
+                if (kPieces % 256 == 0 || idx < (uint32_t)kPieces) xs[idx] = xst[q];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int s = 0; s < SPL; ++s)
+#pragma unroll
+                for (int t = 0; t < M; ++t)
+#pragma unroll
+                    for (int j = 0; j < kNP; ++j) {
+                        const r9vx_u32x4 v = xs[((s * M + t) * kNP + j) * 64 + lane];
+                        if constexpr (XF32)
+                            xr[s][t].v[j] = __builtin_bit_cast(r9vx_f32x4, v);
+                        else
+                            xr[s][t].v[j] = v;
+                    }
         }
         XChunk<SCHEME, XF32> xc[SPL][M];
 #pragma unroll
@@ -365,15 +417,18 @@ uint32_t balanced_rows(uint32_t n, uint32_t simds, uint32_t x) {
     return best;
 }
 
-template <int SCHEME, bool XF32, int SPL, int MM, int LPRL, int RR, int NS = 1>
+template <int SCHEME, bool XF32, int SPL, int MM, int LPRL, int RR, int NS = 1, bool XS = false>
 int launch_rows(const GemvArgs &a, uint32_t rows_per_slot_group, hipStream_t s) {
     /* rows_per_slot_group = lane groups per wave (64 / LPR) */
     const uint32_t rows_per_wave = rows_per_slot_group * (RR ? RR : rows_for(MM));
     const uint32_t waves = (a.n + rows_per_wave - 1) / rows_per_wave;
-    const dim3 grid((waves + waves_for(MM) - 1) / waves_for(MM));
-    hipLaunchKernelGGL((gemv_kernel<SCHEME, MM, XF32, SPL, LPRL, RR, NS>), grid, dim3(waves_for(MM) * 64), 0, s, a);
+    const uint32_t wpg = XS ? 4 : waves_for(MM);
+    const dim3 grid((waves + wpg - 1) / wpg);
+    hipLaunchKernelGGL((gemv_kernel<SCHEME, MM, XF32, SPL, LPRL, RR, NS, XS>), grid, dim3(wpg * 64), 0, s, a);
     return (int)hipGetLastError();
 }
+
+constexpr bool kXStage = true;
 
 template <int SCHEME, bool XF32, int SPL, int MM>
 int launch_one(const GemvArgs &a, uint32_t m, uint32_t rows_per_slot_group, hipStream_t s) {
@@ -390,10 +445,10 @@ int launch_one(const GemvArgs &a, uint32_t m, uint32_t rows_per_slot_group, hipS
              * n = 51200: 15.0 against 16.6 us) */
             const uint32_t simds = device_simds();
             switch (MM <= 2 && a.n < 8 * simds ? 2u : balanced_rows(a.n, simds, MM >= 3 ? 1u : 0u)) {
-            case 2: return launch_rows<SCHEME, XF32, SPL, MM, 6, 2>(a, 1, s);
-            case 3: return launch_rows<SCHEME, XF32, SPL, MM, 6, 3>(a, 1, s);
-            case 4: return launch_rows<SCHEME, XF32, SPL, MM, 6, 4>(a, 1, s);
-            default: return launch_rows<SCHEME, XF32, SPL, MM, 6, 5>(a, 1, s);
+            case 2: return launch_rows<SCHEME, XF32, SPL, MM, 6, 2, 1, kXStage>(a, 1, s);
+            case 3: return launch_rows<SCHEME, XF32, SPL, MM, 6, 3, 1, kXStage>(a, 1, s);
+            case 4: return launch_rows<SCHEME, XF32, SPL, MM, 6, 4, 1, kXStage>(a, 1, s);
+            default: return launch_rows<SCHEME, XF32, SPL, MM, 6, 5, 1, kXStage>(a, 1, s);
             }
         }
         if constexpr (!XF32) {
