@@ -21,7 +21,7 @@ restatement of R9V's T0 path) on a bounded sample on this host, 1 thread,
 plus an all-threads OpenMP variant for the grouped MoE GEMM.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c0,c1,c2,c3,ceilings]
-    python bench.py --pmc-case c4|c3|c2      # short fixed run for rocprofv3 --pmc
+    python bench.py --pmc-case c4|c3|c2|c1m5|c0  # short fixed run for rocprofv3 --pmc
     python bench.py --pmc-summary DIR ... [--pmc-kernels a,b]  # FETCH_SIZE/WRITE_SIZE dirs -> traffic text
 """
 from __future__ import annotations
@@ -59,7 +59,7 @@ def parse():
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU work per baseline sample")
     ap.add_argument("--only", default="", help="comma list of extras: c0,c1,c2,c3,ceilings ('none' for the headline "
                                                "only)")
-    ap.add_argument("--pmc-case", default="", help="run a short fixed workload for counter collection: c4, c3, c2")
+    ap.add_argument("--pmc-case", default="", help="run a short fixed workload for counter collection: c4, c3, c2, c1m5, c0")
     ap.add_argument("--pmc-summary", nargs="*", default=None,
                     help="rocprofv3 --pmc output dirs (FETCH_SIZE, WRITE_SIZE) to summarise as traffic")
     ap.add_argument("--pmc-kernels", default="", help="comma list of kernel-name substrings for --pmc-summary "
@@ -400,7 +400,8 @@ def ceilings(torch, ffi):
 
 def pmc_case(torch, ffi, synth, gsynth, name):
     """A short fixed run for `rocprofv3 --pmc`: 6 steps of configs[4]
-    (moe_ffn), configs[3] (route + moe_ffn) or configs[2] (the dense GEMM) --
+    (moe_ffn), configs[3] (route + moe_ffn) or configs[2] (the dense GEMM),
+    or 200 launches of the configs[1] M=5 / configs[0] GEMV --
     the summaries take medians over a kernel's launches, so the first
     launch's cold caches do not count -- then 5 launches of a plain copy
     kernel of known size (torch.neg, f32 -> f32, 64 MiB read + 64 MiB
@@ -413,8 +414,15 @@ def pmc_case(torch, ffi, synth, gsynth, name):
         c3_extra(torch, ffi, synth, gsynth, 6, 0, steps_only=True)
     elif name == "c2":
         c2_extra(torch, ffi, synth, gsynth, 6, 0, steps_only=True)
+    elif name in ("c1m5", "c0"):
+        # 200 GEMV launches over the rotated weight copies (each launch reads
+        # its copy from HBM, not the Infinity Cache)
+        b = Gemv(torch, ffi, synth, *((ffi.IQ4_XS, 5120, 2048, 5, ffi.BF16) if name == "c1m5" else
+                                     (ffi.Q4_K, 4096, 4096, 1, ffi.F32)), name)
+        for i in range(200):
+            b.launch(i)
     else:
-        raise SystemExit(f"unknown --pmc-case {name!r} (known: c2, c3, c4)")
+        raise SystemExit(f"unknown --pmc-case {name!r} (known: c0, c1m5, c2, c3, c4)")
     torch.cuda.synchronize()
     src = torch.ones(PMC_COPY_BYTES // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
