@@ -28,6 +28,7 @@
 #include "r9vx_gemv_core.h"
 #include "r9vx_mfma.h"
 #include "r9vx_moe.h"
+#include "r9vx_x16.h"
 
 using namespace r9vx;
 
@@ -90,7 +91,25 @@ struct SortArgs {
     uint8_t *ws;
     MoeLayout L;
     uint32_t p, e, k, t, shared;
+    uint32_t nchunk;
+    /* the grouped path's activation rows (x16_row), carried by workgroups
+     * appended to the sort kernels' grids: the sort leaves most CUs idle and
+     * the rows do not depend on it (x == NULL: none) */
+    const uint16_t *x;
+    _Float16 *x16;
+    float *xscale;
+    uint32_t dm, xperm;
 };
+
+/* Workgroups b >= b0 of a sort kernel convert activation rows [r0, r1), one
+ * wave per row.  Returns true for them (the caller returns at once). */
+__device__ __forceinline__ bool sort_x16_part(const SortArgs &a, uint32_t b0, uint32_t r0, uint32_t r1) {
+    if (blockIdx.x < b0) return false;
+    const uint32_t wpb = blockDim.x >> 6;
+    const uint32_t row = r0 + (blockIdx.x - b0) * wpb + (threadIdx.x >> 6);
+    if (row < r1) x16_row_scheme(a.xperm, a.x, a.dm, a.x16, a.xscale, row, threadIdx.x & 63);
+    return true;
+}
 
 /* The grouped GEMMs' row tiles (moe_gemm.hip): expert x with n pairs from
  * sorted position `off` becomes ceil(n / 128) entries (expert, first
@@ -185,11 +204,12 @@ __global__ __launch_bounds__(1024) void sort_small_kernel(SortArgs a) {
 
 /* One 256-pair chunk per block: in-chunk ranks, per-expert chunk counts and
  * whether the chunk holds an id >= E. */
-__global__ __launch_bounds__(256) void sort_count_kernel(SortArgs a) {
+__global__ __launch_bounds__(256) void sort_count_kernel(SortArgs a, uint32_t xr0, uint32_t xr1) {
     __shared__ uint16_t cnt[4][kMoeMaxE];
+    if (sort_x16_part(a, a.nchunk, xr0, xr1)) return;
     const MoeLayout &L = a.L;
     uint32_t tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    uint32_t chunk = blockIdx.x, nchunk = gridDim.x;
+    uint32_t chunk = blockIdx.x, nchunk = a.nchunk;
     for (uint32_t i = tid; i < 4 * kMoeMaxE; i += 256) (&cnt[0][0])[i] = 0;
     __syncthreads();
     uint32_t pair = chunk * 256 + tid;
@@ -212,7 +232,8 @@ __global__ __launch_bounds__(256) void sort_count_kernel(SortArgs a) {
 }
 
 /* One wave per expert: exclusive scan of its chunk counts, and its total. */
-__global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs a, uint32_t nchunk) {
+__global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs a, uint32_t nchunk, uint32_t xr0, uint32_t xr1) {
+    if (sort_x16_part(a, (a.e + 3) / 4, xr0, xr1)) return;
     const MoeLayout &L = a.L;
     uint32_t lane = threadIdx.x & 63;
     uint32_t e = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -248,8 +269,9 @@ __global__ __launch_bounds__(256) void sort_scan_kernel(SortArgs a, uint32_t nch
 
 /* One workgroup (blockDim.x >= E): the status word, the expert offsets (an
  * exclusive scan of the totals) and the tile lists. */
-__global__ __launch_bounds__(1024) void sort_finish_kernel(SortArgs a, uint32_t nchunk) {
+__global__ __launch_bounds__(1024) void sort_finish_kernel(SortArgs a, uint32_t nchunk, uint32_t xr0, uint32_t xr1) {
     __shared__ uint32_t sh[16];
+    if (sort_x16_part(a, 1, xr0, xr1)) return;
     const MoeLayout &L = a.L;
     const uint32_t tid = threadIdx.x;
     const uint32_t *cbad = reinterpret_cast<const uint32_t *>(a.ws + L.cbad);
@@ -268,7 +290,8 @@ __global__ __launch_bounds__(1024) void sort_finish_kernel(SortArgs a, uint32_t 
     put_tile_lists(a, tot, off, sh);
 }
 
-__global__ __launch_bounds__(256) void sort_place_kernel(SortArgs a, uint32_t nchunk) {
+__global__ __launch_bounds__(256) void sort_place_kernel(SortArgs a, uint32_t nchunk, uint32_t xr0, uint32_t xr1) {
+    if (sort_x16_part(a, nchunk, xr0, xr1)) return;
     const MoeLayout &L = a.L;
     uint32_t pair = blockIdx.x * 256 + threadIdx.x;
     if (pair >= a.p) return;
@@ -1080,17 +1103,34 @@ static uint32_t lpr_for(uint32_t k, uint32_t &nseg) {
     return l2;
 }
 
-int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s) {
+int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s, bool *x16_done) {
     SortArgs a{p.ids, p.ws, L, p.t * p.k, p.e, p.k, p.t, p.shared};
+    if (x16_done) *x16_done = false;
     if (a.p <= 1024) {
         hipLaunchKernelGGL(sort_small_kernel, dim3(1), dim3(1024), 0, s, a);
         return (int)hipGetLastError();
     }
-    uint32_t nchunk = (a.p + 255) / 256;
-    hipLaunchKernelGGL(sort_count_kernel, dim3(nchunk), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(sort_scan_kernel, dim3((p.e + 3) / 4), dim3(256), 0, s, a, nchunk);
-    hipLaunchKernelGGL(sort_finish_kernel, dim3(1), dim3(1024), 0, s, a, nchunk);
-    hipLaunchKernelGGL(sort_place_kernel, dim3(nchunk), dim3(256), 0, s, a, nchunk);
+    const uint32_t nchunk = (a.p + 255) / 256;
+    a.nchunk = nchunk;
+    /* x16_done: the activation rows go with the four kernels, 20 / 20 / 40
+     * / 20 % of them (the one-workgroup finish kernel leaves the most CUs
+     * idle), four rows per 256-thread workgroup, sixteen per 1024 */
+    uint32_t xr[5] = {0, 0, 0, 0, 0};
+    if (x16_done) {
+        a.x = p.x;
+        a.x16 = reinterpret_cast<_Float16 *>(p.ws + L.x16);
+        a.xscale = reinterpret_cast<float *>(p.ws + L.xscale);
+        a.dm = p.dm;
+        a.xperm = p.scheme_gu == R9VX_SCHEME_Q4_K || p.scheme_gu == R9VX_SCHEME_IQ4_XS ? p.scheme_gu : 0u;
+        constexpr uint32_t kCum[5] = {0, 20, 40, 80, 100};
+        for (int i = 1; i <= 4; ++i) xr[i] = (uint32_t)((uint64_t)p.t * kCum[i] / 100);
+        *x16_done = true;
+    }
+    auto xblocks = [&](int i, uint32_t rows_per_block) { return (xr[i + 1] - xr[i] + rows_per_block - 1) / rows_per_block; };
+    hipLaunchKernelGGL(sort_count_kernel, dim3(nchunk + xblocks(0, 4)), dim3(256), 0, s, a, xr[0], xr[1]);
+    hipLaunchKernelGGL(sort_scan_kernel, dim3((p.e + 3) / 4 + xblocks(1, 4)), dim3(256), 0, s, a, nchunk, xr[1], xr[2]);
+    hipLaunchKernelGGL(sort_finish_kernel, dim3(1 + xblocks(2, 16)), dim3(1024), 0, s, a, nchunk, xr[2], xr[3]);
+    hipLaunchKernelGGL(sort_place_kernel, dim3(nchunk + xblocks(3, 4)), dim3(256), 0, s, a, nchunk, xr[3], xr[4]);
     return (int)hipGetLastError();
 }
 

@@ -490,15 +490,16 @@ static GroupedArgs grouped_args(const r9vx_moe_problem &p, const MoeLayout &L) {
 }
 
 
-int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s) {
-    return r9vx_moe_grouped_part(p, L, 0, s);
+int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s, bool x16_done) {
+    return r9vx_moe_grouped_part(p, L, 0, s, x16_done);
 }
 
 /* part 0: the whole grouped stage; 1: the gate/up GEMM only; 2: the down
  * GEMM only (1 and 2 on a workspace the whole stage has filled). */
-int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_t part, hipStream_t s) {
+int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_t part, hipStream_t s,
+                          bool x16_done) {
     GroupedArgs a = grouped_args(p, L);
-    if (part == 0) {
+    if (part == 0 && !x16_done) {
         int rc = r9vx_launch_x_to_f16(p.x, p.t, p.dm, reinterpret_cast<_Float16 *>(p.ws + L.x16),
                                       reinterpret_cast<float *>(p.ws + L.xscale), p.scheme_gu, s);
         if (rc) return rc;

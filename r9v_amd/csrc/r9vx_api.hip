@@ -779,8 +779,9 @@ int r9vx_launch_moe(const r9vx_moe_problem &p, hipStream_t s) {
     if (p.t <= 8) { /* pair-order rows: no sort; the combine checks the ids */
         rc = r9vx_moe_decode_stage(p, L, s);
     } else {
-        rc = r9vx_moe_sort_stage(p, L, s);
-        if (!rc) rc = r9vx_moe_grouped_stage(p, L, s);
+        bool x16_done = false;
+        rc = r9vx_moe_sort_stage(p, L, s, &x16_done);
+        if (!rc) rc = r9vx_moe_grouped_stage(p, L, s, x16_done);
     }
     if (rc) return rc;
     return r9vx_moe_combine_stage(p, L, s);

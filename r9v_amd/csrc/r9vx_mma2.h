@@ -41,6 +41,7 @@
 #define R9VX_MMA2_H
 
 #include "r9vx_mfma.h"
+#include "r9vx_x16.h"
 
 namespace r9vx {
 
@@ -49,15 +50,6 @@ constexpr int kM2Stages = 4;
 /* LDS slot swizzle of a 128-byte A row. */
 __host__ __device__ constexpr uint32_t m2_swz(uint32_t row) { return (row >> 1) & 7u; }
 
-/* K offset (within a 64-step) of element i (0..7) of group q. */
-template <int SCHEME>
-__host__ __device__ constexpr uint32_t group_k(uint32_t q, uint32_t i) {
-    if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
-        return (i < 4 ? 0u : 32u) + 4 * q + (i & 3);
-    } else {
-        return 32 * (q >> 2) + (i < 4 ? 0u : 16u) + 4 * (q & 3) + (i & 3);
-    }
-}
 
 /*
  * The main loop issues its loads as inline assembly and waits for them itself

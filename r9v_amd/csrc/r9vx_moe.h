@@ -91,10 +91,13 @@ struct MoeCombineArgs {
     uint32_t t, k, dm, shared, p, e;
 };
 
-int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
+/* x16_done != NULL: the sort kernels also convert the activation rows for
+ * the grouped GEMMs (only on the multi-kernel path; *x16_done says whether). */
+int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s, bool *x16_done = nullptr);
 int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
-int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
-int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_t part, hipStream_t s);
+int r9vx_moe_grouped_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s, bool x16_done = false);
+int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_t part, hipStream_t s,
+                          bool x16_done = false);
 int r9vx_moe_combine_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s);
 
 /* Byte offset (from L.o) of the grouped path's per-(row, 64-column) scales. */
