@@ -1033,13 +1033,22 @@ __global__ __launch_bounds__(256) void r9vx_moe_combine16_kernel(MoeCombineArgs 
     __shared__ uint32_t spos[kMoeMaxK], opos[kMoeMaxK];
     __shared__ float sw[kMoeMaxK], ow[kMoeMaxK];
     const uint32_t *status = reinterpret_cast<const uint32_t *>(a.ws + a.L.status);
-    if (status[0] != 0u) return;
     const uint32_t t = blockIdx.y;
     const uint32_t kk = a.k;
     const uint32_t *inv = reinterpret_cast<const uint32_t *>(a.ws + a.L.inv);
+    /* the status word, the token's positions and weights in one round of
+     * loads (all inside the workspace and the weights array) */
+    const uint32_t st = status[0];
+    uint32_t ps = 0;
+    float wv = 0.f;
     if (threadIdx.x < kk) {
-        spos[threadIdx.x] = inv[(uint64_t)t * kk + threadIdx.x];
-        sw[threadIdx.x] = a.weights[(uint64_t)t * kk + threadIdx.x];
+        ps = inv[(uint64_t)t * kk + threadIdx.x];
+        wv = a.weights[(uint64_t)t * kk + threadIdx.x];
+    }
+    if (st != 0u) return; /* uniform: a refused call writes no y */
+    if (threadIdx.x < kk) {
+        spos[threadIdx.x] = ps;
+        sw[threadIdx.x] = wv;
     }
     __syncthreads();
     if (threadIdx.x < kk) {
