@@ -327,8 +327,13 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     const uint32_t *status = ws_u32(a, a.L.status);
     uint32_t tix, nt;
     xcd_tile(a.dff / 128, tix, nt);
-    if (status[0] != 0u || tix >= status[4]) return;
-    const r9vx_u32x4 tile = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles3)[tix];
+    /* the status words and the tile entry in one round of loads (the entry
+     * index clamped into the list's space; it is used only when tix is a
+     * listed tile) */
+    const uint32_t st0 = status[0], ntile = status[4];
+    const r9vx_u32x4 tile =
+        reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles3)[tix < a.L.max_tiles3 ? tix : a.L.max_tiles3 - 1];
+    if (st0 != 0u || tix >= ntile) return;
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
     const uint32_t j0 = nt * 128;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -381,8 +386,10 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     const uint32_t *status = ws_u32(a, a.L.status);
     uint32_t tix, nt;
     xcd_tile(a.dm / 256, tix, nt);
-    if (status[0] != 0u || tix >= status[4]) return;
-    const r9vx_u32x4 tile = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles3)[tix];
+    const uint32_t st0 = status[0], ntile = status[4]; /* one round of loads, as in gate/up */
+    const r9vx_u32x4 tile =
+        reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles3)[tix < a.L.max_tiles3 ? tix : a.L.max_tiles3 - 1];
+    if (st0 != 0u || tix >= ntile) return;
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
     const uint32_t n0 = nt * 256;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
