@@ -1,6 +1,6 @@
 /*
  * r9vx_mma3.h -- dequant-GEMM main loop with the weight tile decoded once per
- * workgroup into LDS, shared by the grouped MoE GEMMs.
+ * workgroup into LDS, shared by the grouped MoE GEMMs and the dense GEMM.
  *
  * Tile: 256 rows x 256 columns, K steps of 64, 512 threads (8 waves, two per
  * SIMD, one workgroup per CU).  LDS: two A stages and two B tiles (128 KiB).
@@ -11,7 +11,8 @@
  *     each 16-byte granule goes to the other B tile as soon as it is whole.
  *     Every weight is decoded once per 256 output rows.
  *   A (activations, fp16 in the same group order): direct global->LDS copies
- *     into the other A stage, one step ahead.
+ *     into the other A stage, one step ahead (tiles of at most 128 rows:
+ *     m3_mainloop_half's ring of four 128-row slots, three steps ahead).
  *   MFMA: wave w owns rows 128 (w >> 2) .. +128 (four 32-row tiles, of which
  *     the first NR hold rows of this tile) and two 32-column tiles of B; per
  *     16-K slice it reads 2 B and NR A fragments for 2 NR MFMAs
