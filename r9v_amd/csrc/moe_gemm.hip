@@ -357,21 +357,31 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
-    m3_run<GU>(nr, rows <= 128, sm, a.x16, aoff, w, a.dm / kTileK, tid, wv, lut, 128 * rh, 32 * cq, 128 + 32 * cq, acc);
+    m3_run<GU, true>(nr, rows <= 128, sm, a.x16, aoff, w, a.dm / kTileK, tid, wv, lut, 128 * rh, 32 * cq,
+                     128 + 32 * cq, acc);
     if (tid < kMoeTileM3) rowsc[tid] = rsc;
     __syncthreads();
 
+    /* The tiles are transposed (m3_run<.., true>): lane l holds row 128 rh +
+     * 32 t + (l & 31) and, in acc[t][0][r] / acc[t][1][r], the gate and up
+     * values of h column j0 + 32 cq + 8 (r >> 2) + 4 (l >> 5) + (r & 3): four
+     * consecutive columns per r >> 2, stored 16 bytes at a time. */
     float *h = reinterpret_cast<float *>(a.ws + a.L.h);
-    const uint32_t col = j0 + 32 * cq + (lane & 31);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         if ((uint32_t)t >= nr) break;
+        const uint32_t rl = 128 * rh + 32 * t + (lane & 31);
+        if (rl >= rows) continue;
+        const float sc = rowsc[rl];
+        float *hrow = h + (uint64_t)(pos0 + rl) * a.dff + j0 + 32 * cq + 4 * (lane >> 5);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t rl = 128 * rh + 32 * t + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (rl >= rows) continue;
-            const float sc = rowsc[rl];
-            h[(uint64_t)(pos0 + rl) * a.dff + col] = swiglu_fast(acc[t][0][r] * sc, acc[t][1][r] * sc);
+        for (int g = 0; g < 4; ++g) {
+            r9vx_f32x4 v;
+            v.x = swiglu_fast(acc[t][0][4 * g + 0] * sc, acc[t][1][4 * g + 0] * sc);
+            v.y = swiglu_fast(acc[t][0][4 * g + 1] * sc, acc[t][1][4 * g + 1] * sc);
+            v.z = swiglu_fast(acc[t][0][4 * g + 2] * sc, acc[t][1][4 * g + 2] * sc);
+            v.w = swiglu_fast(acc[t][0][4 * g + 3] * sc, acc[t][1][4 * g + 3] * sc);
+            *reinterpret_cast<r9vx_f32x4 *>(hrow + 8 * g) = v;
         }
     }
 }
