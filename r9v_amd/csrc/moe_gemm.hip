@@ -365,15 +365,15 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     /* The tiles are transposed (m3_run<.., true>): lane l holds row 128 rh +
      * 32 t + (l & 31) and, in acc[t][0][r] / acc[t][1][r], the gate and up
      * values of h column j0 + 32 cq + 8 (r >> 2) + 4 (l >> 5) + (r & 3): four
-     * consecutive columns per r >> 2, stored 16 bytes at a time. */
-    float *h = reinterpret_cast<float *>(a.ws + a.L.h);
+     * consecutive columns per r >> 2.  The 256 x 128 f32 h tile is staged in
+     * LDS (row R's 16-byte chunk c at chunk c ^ (R & 31)) and leaves as whole
+     * 512-byte rows. */
+    uint8_t *const ot = m3_out_tile(sm);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         if ((uint32_t)t >= nr) break;
         const uint32_t rl = 128 * rh + 32 * t + (lane & 31);
-        if (rl >= rows) continue;
         const float sc = rowsc[rl];
-        float *hrow = h + (uint64_t)(pos0 + rl) * a.dff + j0 + 32 * cq + 4 * (lane >> 5);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             r9vx_f32x4 v;
@@ -381,8 +381,19 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
             v.y = swiglu_fast(acc[t][0][4 * g + 1] * sc, acc[t][1][4 * g + 1] * sc);
             v.z = swiglu_fast(acc[t][0][4 * g + 2] * sc, acc[t][1][4 * g + 2] * sc);
             v.w = swiglu_fast(acc[t][0][4 * g + 3] * sc, acc[t][1][4 * g + 3] * sc);
-            *reinterpret_cast<r9vx_f32x4 *>(hrow + 8 * g) = v;
+            const uint32_t chunk = (8u * cq + 2u * g + (lane >> 5)) ^ (rl & 31u);
+            *reinterpret_cast<r9vx_f32x4 *>(ot + rl * 512u + 16u * chunk) = v;
         }
+    }
+    __syncthreads();
+    float *h = reinterpret_cast<float *>(a.ws + a.L.h);
+    const uint32_t q = lane & 31;
+#pragma unroll 4
+    for (uint32_t i = 0; i < 16; ++i) {
+        const uint32_t R = 16 * i + 2 * wv + (lane >> 5);
+        if (R >= rows) break; /* rows grow with i */
+        const r9vx_f32x4 v = *reinterpret_cast<const r9vx_f32x4 *>(ot + R * 512u + 16u * (q ^ (R & 31u)));
+        *reinterpret_cast<r9vx_f32x4 *>(h + (uint64_t)(pos0 + R) * a.dff + j0 + 4 * q) = v;
     }
 }
 
