@@ -45,7 +45,7 @@ METRIC = "quant GEMV/MoE HBM GB/s (% of peak); prefill grouped-GEMM TFLOP/s (% M
 C4_T, C4_E, C4_K, C4_DM, C4_DFF = 8192, 512, 10, 2048, 512
 C4_FLOPS = C4_T * C4_K * (2 * 2 * C4_DFF * C4_DM + 2 * C4_DM * C4_DFF)  # 515,396,075,520
 C4_GU_FLOPS = C4_T * C4_K * 2 * 2 * C4_DFF * C4_DM                     # 343,597,383,680
-HEAD_KERNEL = "moe_gu_m3_kernel<23>"  # gate/up grouped GEMM, IQ4_XS (type 23)
+HEAD_KERNEL = "moe_gu_m3_kernel<15>"  # gate/up grouped GEMM, IQ4_XS (scheme code 15)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "moe_gu_m3_c4_traffic.txt")
 PMC_COPY_BYTES = 64 << 20
 
@@ -458,7 +458,7 @@ def pmc_summary(dirs, kernels=None):
 
     head = HEAD_KERNEL.split("<")[0]
     targets = [(k, lambda name, k=k: k in name) for k in kernels] if kernels else \
-        [(HEAD_KERNEL, lambda name: head in name and "<23>" in name)]
+        [(HEAD_KERNEL, lambda name: head in name and "<15>" in name)]
     lines = ["counter      kernel                                      dispatches   median KiB/dispatch"]
     for label, pred in targets:
         out = {}

@@ -75,15 +75,25 @@ enum r9vx_layout {
 /* Placement (PlacementKind, crates/r9v-registry/src/types.rs:506-513): device only. */
 #define R9VX_PLACEMENT_DEVICE 0u
 
-/* Weight schemes: GGUF ggml type codes (crates/r9v-format/src/ggml.rs:38;
- * codes checked by crates/r9v-format/tests/iq.rs:131-141). */
+/* Weight schemes: the reference's stable SchemeId codes
+ * (SchemeId::code, crates/r9v-format/src/scheme.rs:115-138), the values a
+ * MatmulStatic.w_scheme / MoeFfnProjStatic.scheme key carries
+ * (QuantScheme::Scheme, crates/r9v-registry/src/types.rs:739,812).  They are
+ * not GGUF ggml type ids (the reference keeps the two code spaces apart,
+ * scheme.rs:78-87): every other code, GGUF ids such as 12 or 23 included, is
+ * refused.  r9vx_scheme_from_ggml_type translates a GGUF tensor type. */
 enum r9vx_scheme {
-    R9VX_SCHEME_Q8_0 = 8,    /* 34-B block per 32 weights; device layout split (below) */
-    R9VX_SCHEME_Q4_K = 12,   /* 144-B super-block per 256 weights */
-    R9VX_SCHEME_Q6_K = 14,   /* 210-B super-block per 256 weights; device layout split */
-    R9VX_SCHEME_IQ3_S = 21,  /* 110-B super-block per 256 weights; device layout repacked */
-    R9VX_SCHEME_IQ4_XS = 23  /* 136-B super-block per 256 weights */
+    R9VX_SCHEME_Q4_K = 3,    /* SchemeId::I4K: GGUF Q4_K, 144-B super-block per 256 weights */
+    R9VX_SCHEME_Q8_0 = 5,    /* SchemeId::I8B32F: GGUF Q8_0, 34-B block per 32 weights; device layout split */
+    R9VX_SCHEME_Q6_K = 11,   /* SchemeId::I6K: GGUF Q6_K, 210-B super-block per 256 weights; device layout split */
+    R9VX_SCHEME_IQ4_XS = 15, /* SchemeId::I4Xs: GGUF IQ4_XS, 136-B super-block per 256 weights */
+    R9VX_SCHEME_IQ3_S = 17   /* SchemeId::Iq3S: GGUF IQ3_S, 110-B super-block per 256 weights; device layout repacked */
 };
+/* The one translation from a GGUF tensor's ggml type id (crates/r9v-format/
+ * src/ggml.rs:38: Q8_0 8, Q4_K 12, Q6_K 14, IQ3_S 21, IQ4_XS 23) to the
+ * scheme code above; 0 for a type this path does not read.  The mapping is
+ * the reference's own (GgmlType::scheme, crates/r9v-format/src/ggml.rs:253-276). */
+uint32_t r9vx_scheme_from_ggml_type(uint32_t ggml_type);
 /* Q4_K and IQ4_XS are read as GGUF wire blocks.  Q8_0 and Q6_K blocks (34 and
  * 210 bytes) are not 16-byte multiples, so the device reads them in a split
  * layout made at load time by r9vx_repack_launch (or r9vx_gguf_upload_split):
@@ -145,7 +155,7 @@ typedef struct r9vx_matmul_static {
     uint32_t w_dtype;        /* I4 for Q4_K / IQ4_XS / IQ3_S, I8 for Q8_0 / Q6_K */
     uint32_t w_scheme;       /* enum r9vx_scheme */
     uint32_t w_layout;       /* enum r9vx_layout: GGUF_WIRE, SPLIT or IQ3S_112 as the scheme requires */
-    uint32_t in_dtype;       /* F32 (m <= 8 GEMV only) or BF16 */
+    uint32_t in_dtype;       /* F32 (GEMV, m_bucket <= 8) or BF16 */
     uint32_t act_scheme;     /* R9VX_ACT_SCHEME_NONE */
     uint32_t out_dtype;      /* F32 or BF16 (RNE) */
     uint32_t epilogue;       /* enum r9vx_epilogue */
@@ -184,17 +194,21 @@ uint64_t r9vx_matmul_static_flops(const r9vx_matmul_static *st, uint32_t m);
 
 /* --------------------------------------------------------------- moe_route */
 
-/* MoeRouteStatic (crates/r9v-registry/src/types.rs:774-800); grouped routing
- * (n_group > 0) is not implemented and refused. */
+/* MoeRouteStatic (crates/r9v-registry/src/types.rs:774-800), every key in
+ * its declaration order.  `group: Option<MoeGroup>` (MoeGroup {n_group,
+ * topk_group}, crates/r9v-ir/src/op.rs:152-157) is the pair n_group /
+ * topk_group, n_group = 0 meaning None; grouped routing (n_group > 0) is not
+ * implemented and refused, as T0 refuses it (moe_route.rs:198-203). */
 typedef struct r9vx_moe_route_static {
     uint32_t t_bucket;
     uint32_t e_total;     /* E <= 1024 */
     uint32_t top_k;       /* K <= 32, K <= E */
     uint32_t scoring;     /* enum r9vx_scoring */
     uint32_t renormalize; /* 0 / 1 */
+    uint32_t n_group;     /* group: 0 (None) only */
+    uint32_t topk_group;  /* group: 0 with n_group = 0 */
     uint32_t scale_bits;  /* IEEE-754 bits of the f32 route scale */
     uint32_t has_bias;    /* 0 / 1 */
-    uint32_t n_group;     /* must be 0 */
 } r9vx_moe_route_static;
 
 /* moe_route ABI struct (crates/r9v-kgen/src/abi/per_op.rs:870-901). */
@@ -232,7 +246,7 @@ uint64_t r9vx_moe_route_static_bytes(const r9vx_moe_route_static *st, uint32_t t
 uint64_t r9vx_moe_route_static_flops(const r9vx_moe_route_static *st, uint32_t t);
 
 /* Routing from hidden states (the router-logits matmul feeding moe_route,
- * fused; decode form t <= 8).  No single op of the reference: it replaces the
+ * fused; decode form, t_bucket <= 8).  No single op of the reference: it replaces the
  * graph's router matmul (f32 weight [E, dm], the GGUF ffn_gate_inp tensor)
  * followed by Op::MoeRoute.  Every logit is accumulated in T0's matmul order
  * (crates/r9v-t0/src/matmul.rs:1940-2414: k ascending, one f32 accumulator,
@@ -273,8 +287,8 @@ int r9vx_moe_route_hidden_status(const r9vx_moe_route_static *st, const uint8_t 
  * projection's weight element type, scheme and layout. */
 typedef struct r9vx_moe_ffn_proj {
     uint32_t dtype;  /* I4 for Q4_K / IQ4_XS / IQ3_S, I8 for Q8_0 / Q6_K */
-    uint32_t scheme; /* enum r9vx_scheme */
-    uint32_t layout; /* enum r9vx_layout: GGUF_WIRE (Q4_K, IQ4_XS), IQ3S_112 (IQ3_S) */
+    uint32_t scheme; /* enum r9vx_scheme (SchemeId code): Q4_K, IQ4_XS, IQ3_S, Q8_0 or Q6_K */
+    uint32_t layout; /* enum r9vx_layout: GGUF_WIRE (Q4_K, IQ4_XS), IQ3S_112 (IQ3_S), SPLIT (Q8_0, Q6_K) */
 } r9vx_moe_ffn_proj;
 
 /* MoeFfnStatic (crates/r9v-registry/src/types.rs:828-860), every key in its
@@ -285,8 +299,8 @@ typedef struct r9vx_moe_ffn_static {
     uint32_t k_topk;           /* K */
     uint32_t dm;               /* hidden size, multiple of 256 */
     uint32_t dff;              /* expert intermediate size, multiple of 256 */
-    r9vx_moe_ffn_proj gate_up; /* w_gate_up [E+S, 2Dff, Dm]: Q4_K, IQ4_XS or IQ3_S */
-    r9vx_moe_ffn_proj down;    /* w_down [E+S, Dm, Dff]: Q4_K, IQ4_XS or IQ3_S */
+    r9vx_moe_ffn_proj gate_up; /* w_gate_up [E+S, 2Dff, Dm]: any of the five schemes */
+    r9vx_moe_ffn_proj down;    /* w_down [E+S, Dm, Dff]: any of the five schemes */
     uint32_t in_dtype;         /* BF16 */
     uint32_t act_scheme;       /* R9VX_ACT_SCHEME_NONE */
     uint32_t act;              /* enum r9vx_act */
@@ -300,10 +314,13 @@ typedef struct r9vx_moe_ffn_args {
     const void *x;                /* [t, Dm] in_dtype */
     const uint32_t *expert_ids;   /* [t, K] */
     const float *weights;         /* [t, K] */
-    const void *w_gate_up;        /* GGUF blocks, gate rows [0,Dff) then up rows [Dff,2Dff) */
-    const void *w_gate_up_scales; /* must be NULL (inline GGUF scales) */
-    const void *w_down;           /* GGUF blocks */
-    const void *w_down_scales;    /* must be NULL */
+    const void *w_gate_up;        /* expert e's gate rows [0,Dff) then up rows [Dff,2Dff), each row in
+                                     the device layout of gate_up.scheme: GGUF blocks (Q4_K, IQ4_XS),
+                                     112-byte blocks (IQ3_S) or the split body (Q8_0, Q6_K) */
+    const void *w_gate_up_scales; /* Q8_0 / Q6_K: the split layout's f16 d per block, [E+S, 2Dff,
+                                     Dm/blocklen] (blocklen 32 / 256), 4-byte aligned; NULL otherwise */
+    const void *w_down;           /* [E+S, Dm, Dff] rows in the device layout of down.scheme */
+    const void *w_down_scales;    /* Q8_0 / Q6_K: f16 d [E+S, Dm, Dff/blocklen]; NULL otherwise */
     void *y;                      /* [t, Dm] out_dtype */
     uint8_t *sort_workspace;      /* MoeSortBuffers, r9vx_moe_ffn_workspace_bytes */
     uint32_t t;
@@ -358,6 +375,8 @@ int r9vx_moe_sort_launch(const r9vx_moe_ffn_static *st, const uint32_t *expert_i
 
 /* ------------------------------------------------------------ weights / decode */
 
+/* `scheme` below is an enum r9vx_scheme code, as in the statics. */
+
 /* Bit-exact decode of GGUF wire blocks to f32 [n_rows, k]: the
  * ggml_dequantize of crates/r9v-format/src/ggml.rs:1025-1150 (Q4_K; Q8_0
  * :1094-1100 and Q6_K :1154-1172 with block_values :627-640, :817-850) and
@@ -386,7 +405,7 @@ const char *r9vx_last_error(void);
 /* ABI version of this header (bumped on any struct change). */
 uint32_t r9vx_abi_version(void);
 
-#define R9VX_ABI_VERSION 2u
+#define R9VX_ABI_VERSION 3u
 
 #ifdef __cplusplus
 }

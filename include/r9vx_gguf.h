@@ -170,7 +170,8 @@ int64_t r9vx_gguf_shards_find(const r9vx_gguf_shards *s, const char *name);
 /* ---------------------------------------------------- binding and upload */
 
 /* Variant key of a matmul over the 2-D Q4_K / IQ4_XS / Q6_K / Q8_0 / IQ3_S
- * tensor `name` (file dims {K, N}): sets st->n, st->k, st->w_scheme and the
+ * tensor `name` (file dims {K, N}): sets st->n, st->k, st->w_scheme (the
+ * SchemeId code of the tensor's GGUF type, r9vx_scheme_from_ggml_type) and the
  * w_dtype / w_layout of the device layout the weights must be loaded into,
  * leaves the other fields: Q4_K / IQ4_XS GGUF_WIRE (r9vx_gguf_upload copies
  * the blocks), IQ3_S IQ3S_112 (r9vx_gguf_upload repacks the 110-byte blocks
@@ -182,7 +183,7 @@ int r9vx_gguf_matmul_static(const r9vx_gguf *f, const char *name, r9vx_matmul_st
  * (file dims {Dm, Dff, E} each) or one fused `gate` tensor {Dm, 2*Dff, E}
  * with up == NULL (the ffn_gate_up_exps form of
  * crates/r9v-models/src/generic.rs:1420), and `down` {Dff, Dm, E}.  Sets
- * e_local, dm, dff and the gate_up / down projection keys (dtype, scheme and
+ * e_local, dm, dff and the gate_up / down projection keys (dtype, SchemeId code and
  * the device layout the uploads write): Q4_K / IQ4_XS / IQ3_S through
  * r9vx_gguf_upload / r9vx_gguf_upload_gate_up, Q8_0 / Q6_K (split) through
  * r9vx_gguf_upload_split / r9vx_gguf_upload_gate_up_split. */

@@ -278,23 +278,60 @@ static inline void write_y(int y_dtype, void *y, uint64_t i, float v) {
         ((float *)y)[i] = v;
 }
 
+/* Branch D's dot (crates/r9v-t0/src/matmul.rs:1940-2414): per output one
+ * f32 accumulator from 0, k ascending, prod = x * w rounded, then acc +=
+ * prod rounded.  `rows` x rows (stride `xs` floats) against one decoded weight
+ * row; four rows run as four independent chains in one pass over k, which
+ * changes no row's operations or their order (only how fast they issue). */
+static void dot_rows(const float *x, uint32_t rows, uint64_t xs, const float *w, uint32_t k, float *out,
+                     uint64_t os) {
+    uint32_t r = 0;
+    for (; r + 4 <= rows; r += 4) {
+        const float *x0 = x + r * xs, *x1 = x0 + xs, *x2 = x1 + xs, *x3 = x2 + xs;
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+        for (uint32_t kk = 0; kk < k; ++kk) {
+            const float wv = w[kk];
+            float p0 = x0[kk] * wv, p1 = x1[kk] * wv, p2 = x2[kk] * wv, p3 = x3[kk] * wv;
+            a0 += p0;
+            a1 += p1;
+            a2 += p2;
+            a3 += p3;
+        }
+        out[r * os] = a0;
+        out[(r + 1) * os] = a1;
+        out[(r + 2) * os] = a2;
+        out[(r + 3) * os] = a3;
+    }
+    for (; r < rows; ++r) {
+        float acc = 0.0f;
+        for (uint32_t kk = 0; kk < k; ++kk) {
+            float prod = x[r * xs + kk] * w[kk];
+            acc += prod;
+        }
+        out[r * os] = acc;
+    }
+}
+
+/* x [m, k] in x_dtype -> f32 (bf16 -> f32 is exact), NULL on allocation failure. */
+static float *x_to_f32(int x_dtype, const void *x, uint32_t m, uint32_t k) {
+    float *xf = (float *)malloc(sizeof(float) * (size_t)m * k);
+    if (xf)
+        for (uint64_t i = 0; i < (uint64_t)m * k; ++i) xf[i] = read_x(x_dtype, x, i);
+    return xf;
+}
+
 static int matmul_rows(int scheme, const uint8_t *w, uint32_t n0, uint32_t n1, uint32_t n,
-                       uint32_t k, int x_dtype, const void *x, uint32_t m, const float *bias,
-                       const float *residual, int y_dtype, void *y, float *wrow, float *xrow) {
+                       uint32_t k, const float *xf, uint32_t m, const float *bias,
+                       const float *residual, int y_dtype, void *y, float *wrow, float *acc) {
     uint64_t row_bytes = (uint64_t)(k / rxo_block_len(scheme)) * rxo_block_bytes(scheme);
-    (void)xrow;
     for (uint32_t col = n0; col < n1; ++col) {
         decode_row(scheme, w + col * row_bytes, k, wrow);
+        dot_rows(xf, m, k, wrow, k, acc, 1);
         for (uint32_t r = 0; r < m; ++r) {
-            float acc = 0.0f;
-            for (uint32_t kk = 0; kk < k; ++kk) {
-                float xv = read_x(x_dtype, x, (uint64_t)r * k + kk);
-                float prod = xv * wrow[kk];
-                acc += prod;
-            }
-            if (bias) acc += bias[col];
-            if (residual) acc += residual[(uint64_t)r * n + col];
-            write_y(y_dtype, y, (uint64_t)r * n + col, acc);
+            float v = acc[r];
+            if (bias) v += bias[col];
+            if (residual) v += residual[(uint64_t)r * n + col];
+            write_y(y_dtype, y, (uint64_t)r * n + col, v);
         }
     }
     return RXO_OK;
@@ -315,10 +352,13 @@ int rxo_matmul(int scheme, const uint8_t *w, uint32_t n, uint32_t k, int x_dtype
                int y_dtype, void *y) {
     int rc = matmul_validate(scheme, w, n, k, x_dtype, m, bias, residual, y_dtype);
     if (rc) return rc;
-    float *wrow = (float *)malloc(sizeof(float) * k);
-    if (!wrow) return RXO_ERR_SHAPE;
-    rc = matmul_rows(scheme, w, 0, n, n, k, x_dtype, x, m, bias, residual, y_dtype, y, wrow, NULL);
+    float *wrow = (float *)malloc(sizeof(float) * k), *acc = (float *)malloc(sizeof(float) * m);
+    float *xf = x_to_f32(x_dtype, x, m, k);
+    if (wrow && acc && xf) rc = matmul_rows(scheme, w, 0, n, n, k, xf, m, bias, residual, y_dtype, y, wrow, acc);
+    else rc = RXO_ERR_SHAPE;
     free(wrow);
+    free(acc);
+    free(xf);
     return rc;
 }
 
@@ -353,17 +393,25 @@ int rxo_matmul_mt(int scheme, const uint8_t *w, uint32_t n, uint32_t k, int x_dt
     if (rc) return rc;
 #ifdef _OPENMP
     if (threads < 1) threads = 1;
-#pragma omp parallel num_threads(threads)
+    float *xf = x_to_f32(x_dtype, x, m, k);
+    if (!xf) return RXO_ERR_SHAPE;
+    int failed = 0;
+#pragma omp parallel num_threads(threads) reduction(| : failed)
     {
-        float *wrow = (float *)malloc(sizeof(float) * k);
+        float *wrow = (float *)malloc(sizeof(float) * k), *acc = (float *)malloc(sizeof(float) * m);
         int nt = omp_get_num_threads(), tid = omp_get_thread_num();
         uint32_t chunk = (n + nt - 1) / nt;
         uint32_t n0 = tid * chunk, n1 = n0 + chunk > n ? n : n0 + chunk;
-        if (wrow && n0 < n1)
-            matmul_rows(scheme, w, n0, n1, n, k, x_dtype, x, m, NULL, NULL, y_dtype, y, wrow, NULL);
+        if (wrow && acc) {
+            if (n0 < n1) matmul_rows(scheme, w, n0, n1, n, k, xf, m, NULL, NULL, y_dtype, y, wrow, acc);
+        } else {
+            failed = 1;
+        }
         free(wrow);
+        free(acc);
     }
-    return RXO_OK;
+    free(xf);
+    return failed ? RXO_ERR_SHAPE : RXO_OK;
 #else
     (void)threads;
     return rxo_matmul(scheme, w, n, k, x_dtype, x, m, NULL, NULL, y_dtype, y);
@@ -376,6 +424,19 @@ int rxo_matmul_mt(int scheme, const uint8_t *w, uint32_t n, uint32_t k, int x_dt
 
 /* Rust f32::exp lowers to the platform libm expf (glibc on x86-64 Linux). */
 float rxo_expf(float x) { return expf(x); }
+
+/* out[i] = expf of the float whose bits are first_bits + i (the host libm
+ * the reference's f32::exp lowers to), for checking a device exp over a
+ * range of inputs; rows split over every OpenMP thread. */
+void rxo_expf_fill(uint32_t first_bits, uint64_t n, float *out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)n; ++i) {
+        const uint32_t u = first_bits + (uint32_t)i;
+        float x;
+        memcpy(&x, &u, 4);
+        out[i] = rxo_expf(x);
+    }
+}
 
 /* total_cmp order (moe_route.rs:373): for finite values this is the IEEE
  * order with -0.0 < +0.0. */
@@ -515,34 +576,25 @@ static void expert_rows(const float *x_rows, uint32_t rows, uint32_t dm, uint32_
     uint64_t gu_row_bytes = wire_row_bytes(scheme_gu, dm);
     uint64_t dn_row_bytes = wire_row_bytes(scheme_dn, dff);
     float *gate = (float *)malloc(sizeof(float) * (size_t)rows * dff);
+    float *up = (float *)malloc(sizeof(float) * (size_t)rows);
     for (uint32_t c = 0; c < 2 * dff; ++c) {
         decode_row(scheme_gu, gu + c * gu_row_bytes, dm, wrow);
+        if (c < dff) {
+            dot_rows(x_rows, rows, dm, wrow, dm, gate + c, dff);
+            continue;
+        }
+        dot_rows(x_rows, rows, dm, wrow, dm, up, 1);
         for (uint32_t r = 0; r < rows; ++r) {
-            float acc = 0.0f;
-            for (uint32_t kk = 0; kk < dm; ++kk) {
-                float prod = x_rows[(uint64_t)r * dm + kk] * wrow[kk];
-                acc += prod;
-            }
-            if (c < dff)
-                gate[(uint64_t)r * dff + c] = acc;
-            else {
-                float v = silu_mul(gate[(uint64_t)r * dff + (c - dff)], acc);
-                if (h_bf16) v = rxo_bf16_to_f32(rxo_f32_to_bf16(v));
-                h[(uint64_t)r * dff + (c - dff)] = v;
-            }
+            float v = silu_mul(gate[(uint64_t)r * dff + (c - dff)], up[r]);
+            if (h_bf16) v = rxo_bf16_to_f32(rxo_f32_to_bf16(v));
+            h[(uint64_t)r * dff + (c - dff)] = v;
         }
     }
+    free(up);
     free(gate);
     for (uint32_t d = 0; d < dm; ++d) {
         decode_row(scheme_dn, dn + d * dn_row_bytes, dff, wrow);
-        for (uint32_t r = 0; r < rows; ++r) {
-            float acc = 0.0f;
-            for (uint32_t kk = 0; kk < dff; ++kk) {
-                float prod = h[(uint64_t)r * dff + kk] * wrow[kk];
-                acc += prod;
-            }
-            out[(uint64_t)r * dm + d] = acc;
-        }
+        dot_rows(h, rows, dff, wrow, dff, out + d, dm);
     }
 }
 
@@ -572,78 +624,130 @@ int rxo_expert_ffn(int x_dtype, const void *x, uint32_t rows, uint32_t dm, uint3
     return RXO_OK;
 }
 
-int rxo_moe_ffn(int x_dtype, const void *x, uint32_t t, uint32_t dm, uint32_t dff, uint32_t e,
-                uint32_t s_shared, uint32_t k, const uint32_t *ids, const float *weights,
-                int scheme_gu, const uint8_t *gu, int scheme_dn, const uint8_t *dn, int h_bf16,
-                float *y) {
+/* rxo_moe_ffn with its expert FFNs spread over `threads` OpenMP threads:
+ * every routed expert's unique tokens (and every token for each shared
+ * expert) are cut into chunks of rows, each chunk computed independently
+ * (a row's result does not depend on the rows beside it), and the combine
+ * then runs serially in T0's order, so y is bit-identical for every thread
+ * count. */
+#define RXO_FFN_CHUNK 64u
+int rxo_moe_ffn_mt(int x_dtype, const void *x, uint32_t t, uint32_t dm, uint32_t dff, uint32_t e,
+                   uint32_t s_shared, uint32_t k, const uint32_t *ids, const float *weights, int scheme_gu,
+                   const uint8_t *gu, int scheme_dn, const uint8_t *dn, int h_bf16, float *y, int threads) {
     int rc = ffn_validate(x_dtype, t, dm, dff, e + s_shared, scheme_gu, gu, scheme_dn, dn);
     if (rc) return rc;
     if (k == 0) return RXO_ERR_SHAPE;
+    if (threads < 1) threads = 1;
     uint64_t p = (uint64_t)t * k;
     uint32_t *counts = (uint32_t *)malloc(sizeof(uint32_t) * e);
     uint32_t *offsets = (uint32_t *)malloc(sizeof(uint32_t) * (e + 1));
     uint32_t *sorted = (uint32_t *)malloc(sizeof(uint32_t) * p);
-    rc = rxo_moe_sort(ids, t, k, e, counts, offsets, sorted);
-    if (rc) {
-        free(counts);
-        free(offsets);
-        free(sorted);
-        return rc;
-    }
-    uint64_t gu_expert = (uint64_t)2 * dff * wire_row_bytes(scheme_gu, dm);
-    uint64_t dn_expert = (uint64_t)dm * wire_row_bytes(scheme_dn, dff);
+    /* rows of the unique-token runs: run of expert ex at [offsets[ex], +run_len[ex]) */
+    uint32_t *run_tok = (uint32_t *)malloc(sizeof(uint32_t) * p);
+    uint32_t *run_len = (uint32_t *)calloc(e, sizeof(uint32_t));
+    float *o = (float *)malloc(sizeof(float) * (size_t)(p + (uint64_t)s_shared * t) * dm);
     float *ytmp = (float *)calloc((size_t)t * dm, sizeof(float));
-    float *xr = (float *)malloc(sizeof(float) * (size_t)t * dm);
-    float *out = (float *)malloc(sizeof(float) * (size_t)t * dm);
-    float *h = (float *)malloc(sizeof(float) * (size_t)t * dff);
-    float *wrow = (float *)malloc(sizeof(float) * (dm > dff ? dm : dff));
-    uint32_t *tokens = (uint32_t *)malloc(sizeof(uint32_t) * (t + 1));
-    for (uint32_t ex = 0; ex < e; ++ex) {
-        uint32_t beg = offsets[ex], end = offsets[ex + 1];
-        if (beg == end) continue; /* unused expert skipped (moe_ffn_tests.rs:459) */
-        /* Unique ascending tokens of the run (moe_ffn.rs:527-545). */
-        uint32_t le = 0;
-        for (uint32_t i = beg; i < end; ++i) {
-            uint32_t tok = sorted[i] / k;
-            if (le == 0 || tokens[le - 1] != tok) tokens[le++] = tok;
+    if (!counts || !offsets || !sorted || !run_tok || !run_len || !o || !ytmp) rc = RXO_ERR_SHAPE;
+    if (!rc) rc = rxo_moe_sort(ids, t, k, e, counts, offsets, sorted);
+    uint64_t n_items = 0;
+    uint32_t *item_run = NULL, *item_r0 = NULL;
+    if (!rc) {
+        /* Unique ascending tokens of each expert's run (moe_ffn.rs:527-545). */
+        for (uint32_t ex = 0; ex < e; ++ex) {
+            uint32_t le = 0;
+            for (uint32_t i = offsets[ex]; i < offsets[ex + 1]; ++i) {
+                uint32_t tok = sorted[i] / k;
+                if (le == 0 || run_tok[offsets[ex] + le - 1] != tok) run_tok[offsets[ex] + le++] = tok;
+            }
+            run_len[ex] = le;
+            n_items += (le + RXO_FFN_CHUNK - 1) / RXO_FFN_CHUNK;
         }
-        for (uint32_t r = 0; r < le; ++r)
-            for (uint32_t kk = 0; kk < dm; ++kk)
-                xr[(uint64_t)r * dm + kk] = read_x(x_dtype, x, (uint64_t)tokens[r] * dm + kk);
-        expert_rows(xr, le, dm, dff, scheme_gu, gu + ex * gu_expert, scheme_dn, dn + ex * dn_expert,
-                    h_bf16, out, wrow, h);
-        /* Weighted combine in ascending (token, slot) order (moe_ffn.rs:641-653). */
-        uint32_t r = 0;
-        for (uint32_t i = beg; i < end; ++i) {
-            uint32_t tok = sorted[i] / k, slot = sorted[i] % k;
-            while (tokens[r] != tok) ++r;
-            float w = weights[(uint64_t)tok * k + slot];
-            for (uint32_t d = 0; d < dm; ++d) {
-                float prod = w * out[(uint64_t)r * dm + d];
-                ytmp[(uint64_t)tok * dm + d] += prod;
+        n_items += (uint64_t)s_shared * ((t + RXO_FFN_CHUNK - 1) / RXO_FFN_CHUNK);
+        item_run = (uint32_t *)malloc(sizeof(uint32_t) * (n_items + 1));
+        item_r0 = (uint32_t *)malloc(sizeof(uint32_t) * (n_items + 1));
+        if (!item_run || !item_r0) rc = RXO_ERR_SHAPE;
+    }
+    if (!rc) {
+        uint64_t it = 0;
+        for (uint32_t ex = 0; ex < e + s_shared; ++ex) {
+            const uint32_t len = ex < e ? run_len[ex] : t;
+            for (uint32_t r0 = 0; r0 < len; r0 += RXO_FFN_CHUNK) item_run[it] = ex, item_r0[it++] = r0;
+        }
+        const uint64_t gu_expert = (uint64_t)2 * dff * wire_row_bytes(scheme_gu, dm);
+        const uint64_t dn_expert = (uint64_t)dm * wire_row_bytes(scheme_dn, dff);
+        int failed = 0;
+#ifdef _OPENMP
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1) reduction(| : failed)
+#endif
+        for (int64_t i = 0; i < (int64_t)n_items; ++i) {
+            const uint32_t ex = item_run[i], r0 = item_r0[i];
+            const uint32_t len = ex < e ? run_len[ex] : t;
+            const uint32_t rows = len - r0 < RXO_FFN_CHUNK ? len - r0 : RXO_FFN_CHUNK;
+            /* output rows: routed runs at their pair offsets, shared experts after the P pair rows */
+            const uint64_t orow = ex < e ? (uint64_t)offsets[ex] + r0 : p + (uint64_t)(ex - e) * t + r0;
+            float *xr = (float *)malloc(sizeof(float) * (size_t)rows * dm);
+            float *h = (float *)malloc(sizeof(float) * (size_t)rows * dff);
+            float *wrow = (float *)malloc(sizeof(float) * (dm > dff ? dm : dff));
+            if (xr && h && wrow) {
+                for (uint32_t r = 0; r < rows; ++r) {
+                    const uint32_t tok = ex < e ? run_tok[offsets[ex] + r0 + r] : r0 + r;
+                    for (uint32_t kk = 0; kk < dm; ++kk)
+                        xr[(uint64_t)r * dm + kk] = read_x(x_dtype, x, (uint64_t)tok * dm + kk);
+                }
+                expert_rows(xr, rows, dm, dff, scheme_gu, gu + ex * gu_expert, scheme_dn, dn + ex * dn_expert,
+                            h_bf16, o + orow * dm, wrow, h);
+            } else {
+                failed = 1;
+            }
+            free(xr);
+            free(h);
+            free(wrow);
+        }
+        if (failed) rc = RXO_ERR_SHAPE;
+    }
+    if (!rc) {
+        /* Weighted combine, experts ascending, each run in (token, slot) order
+         * (moe_ffn.rs:641-653). */
+        for (uint32_t ex = 0; ex < e; ++ex) {
+            uint32_t r = 0;
+            const uint32_t *tokens = run_tok + offsets[ex];
+            const float *out = o + (uint64_t)offsets[ex] * dm;
+            for (uint32_t i = offsets[ex]; i < offsets[ex + 1]; ++i) {
+                uint32_t tok = sorted[i] / k, slot = sorted[i] % k;
+                while (tokens[r] != tok) ++r;
+                float w = weights[(uint64_t)tok * k + slot];
+                for (uint32_t d = 0; d < dm; ++d) {
+                    float prod = w * out[(uint64_t)r * dm + d];
+                    ytmp[(uint64_t)tok * dm + d] += prod;
+                }
             }
         }
+        /* Shared experts: every token, weight 1.0, added after the routed
+         * combine (crates/r9v-models/src/generic.rs:1458-1495 residual add). */
+        for (uint32_t sidx = 0; sidx < s_shared; ++sidx) {
+            const float *out = o + (p + (uint64_t)sidx * t) * dm;
+            for (uint64_t i = 0; i < (uint64_t)t * dm; ++i) ytmp[i] += out[i];
+        }
+        memcpy(y, ytmp, sizeof(float) * (size_t)t * dm);
     }
-    /* Shared experts: every token, weight 1.0, added after the routed
-     * combine (crates/r9v-models/src/generic.rs:1458-1495 residual add). */
-    for (uint32_t sidx = 0; sidx < s_shared; ++sidx) {
-        uint32_t ex = e + sidx;
-        for (uint64_t i = 0; i < (uint64_t)t * dm; ++i) xr[i] = read_x(x_dtype, x, i);
-        expert_rows(xr, t, dm, dff, scheme_gu, gu + ex * gu_expert, scheme_dn, dn + ex * dn_expert,
-                    h_bf16, out, wrow, h);
-        for (uint64_t i = 0; i < (uint64_t)t * dm; ++i) ytmp[i] += out[i];
-    }
-    memcpy(y, ytmp, sizeof(float) * (size_t)t * dm);
+    free(item_run);
+    free(item_r0);
     free(ytmp);
-    free(xr);
-    free(out);
-    free(h);
-    free(wrow);
-    free(tokens);
+    free(o);
+    free(run_len);
+    free(run_tok);
     free(counts);
     free(offsets);
     free(sorted);
-    return RXO_OK;
+    return rc;
+}
+
+int rxo_moe_ffn(int x_dtype, const void *x, uint32_t t, uint32_t dm, uint32_t dff, uint32_t e,
+                uint32_t s_shared, uint32_t k, const uint32_t *ids, const float *weights,
+                int scheme_gu, const uint8_t *gu, int scheme_dn, const uint8_t *dn, int h_bf16,
+                float *y) {
+    return rxo_moe_ffn_mt(x_dtype, x, t, dm, dff, e, s_shared, k, ids, weights, scheme_gu, gu, scheme_dn, dn, h_bf16,
+                          y, 1);
 }
 
 /* One expert's FFN over the token rows `tokens` (the per-expert body of

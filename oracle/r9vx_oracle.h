@@ -92,6 +92,7 @@ void rxo_act_mul_silu(const float *g, const float *u, uint64_t n, float *y);
 /* ---- MoE -------------------------------------------------------------- */
 /* Reference glibc expf (the host libm the Rust T0 f32::exp resolves to). */
 float rxo_expf(float x);
+void rxo_expf_fill(uint32_t first_bits, uint64_t n, float *out);
 /* moe_route with softmax scoring (scoring 0) or sigmoid (scoring 1). */
 int rxo_moe_route(const float *logits, const float *bias, uint32_t t, uint32_t e,
                   uint32_t k, float scale, int renormalize, int scoring,
@@ -112,6 +113,14 @@ int rxo_moe_ffn(int x_dtype, const void *x, uint32_t t, uint32_t dm, uint32_t df
                 int scheme_gu, const uint8_t *w_gate_up,
                 int scheme_dn, const uint8_t *w_down,
                 int h_bf16, float *y);
+/* rxo_moe_ffn with the expert FFNs over `threads` OpenMP threads;
+ * bit-identical to it for every thread count. */
+int rxo_moe_ffn_mt(int x_dtype, const void *x, uint32_t t, uint32_t dm, uint32_t dff,
+                   uint32_t e, uint32_t s_shared, uint32_t k,
+                   const uint32_t *expert_ids, const float *weights,
+                   int scheme_gu, const uint8_t *w_gate_up,
+                   int scheme_dn, const uint8_t *w_down,
+                   int h_bf16, float *y, int threads);
 /* Literal T0 form for tiny E: gate/up GEMM over the full [E*2Dff, Dm]
  * matrix, then slice (moe_ffn.rs:575-612).  Used to pin the sliced form. */
 int rxo_moe_ffn_full(int x_dtype, const void *x, uint32_t t, uint32_t dm, uint32_t dff,

@@ -1,6 +1,8 @@
 """Builds libr9vx.so (all HIP kernels + the C ABI) for gfx950 with hipcc.
 
     python -m r9v_amd.build        # compile every source, link r9v_amd/libr9vx.so
+    python -m r9v_amd.build --changed   # only sources newer than their object (or
+                                        # with a newer header), then link
 
 Objects go to r9v_amd/_build/; the library is written in-tree so it travels
 with the repository snapshot to the GPU box.
@@ -8,6 +10,7 @@ with the repository snapshot to the GPU box.
 from __future__ import annotations
 
 import concurrent.futures as cf
+import json
 import os
 import pathlib
 import subprocess
@@ -97,14 +100,33 @@ def _compile(src: pathlib.Path):
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError(f"hipcc failed on {src.name}")
-    return obj, parse_resources(r.stderr)
+    res = parse_resources(r.stderr)
+    obj.with_suffix(".res").write_text(json.dumps(res))
+    return obj, res
 
 
-def build(verbose: bool = True) -> pathlib.Path:
+def _up_to_date(src: pathlib.Path) -> bool:
+    """The object and its resource report are newer than the source and
+    every header it could include."""
+    obj, res = BUILD / (src.stem + ".o"), BUILD / (src.stem + ".res")
+    if not (obj.exists() and res.exists()):
+        return False
+    newest = max(p.stat().st_mtime for p in [src, *CSRC.glob("*.h"), *(ROOT / "include").glob("*.h")])
+    return min(obj.stat().st_mtime, res.stat().st_mtime) > newest
+
+
+def _reuse(src: pathlib.Path):
+    obj = BUILD / (src.stem + ".o")
+    return obj, json.loads(obj.with_suffix(".res").read_text())
+
+
+def build(verbose: bool = True, changed_only: bool = False) -> pathlib.Path:
     BUILD.mkdir(exist_ok=True)
     srcs = sources()
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        done = list(ex.map(_compile, srcs))
+    stale = [s for s in srcs if not (changed_only and _up_to_date(s))]
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(8, len(stale)))) as ex:
+        fresh = dict(zip(stale, ex.map(_compile, stale)))
+    done = [fresh[s] if s in fresh else _reuse(s) for s in srcs]
     objs = [o for o, _ in done]
     res = {}
     for _, r in done:
@@ -125,9 +147,9 @@ def build(verbose: bool = True) -> pathlib.Path:
         raise RuntimeError("link of libr9vx.so failed")
     os.replace(tmp, OUT)
     if verbose:
-        print(f"built {OUT} from {len(srcs)} sources; per-kernel registers in {RESOURCES}")
+        print(f"built {OUT} from {len(srcs)} sources ({len(stale)} compiled); per-kernel registers in {RESOURCES}")
     return OUT
 
 
 if __name__ == "__main__":
-    build()
+    build(changed_only="--changed" in sys.argv[1:])

@@ -1,6 +1,6 @@
 /*
  * gemm.hip -- prefill dequant-GEMM on MFMA: y[m, n] = sum_k x[m, k] * w[n, k]
- * for bf16 activations (m > 8) and GGUF Q4_K / IQ4_XS weights (wire blocks)
+ * for bf16 activations (variants with m_bucket > 8) and GGUF Q4_K / IQ4_XS weights (wire blocks)
  * or Q8_0 / Q6_K weights (split layout) and IQ3_S weights (112-byte repacked
  * blocks), LDS-decoded tiles only.
  *
@@ -369,11 +369,16 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     a.k = p.k;
     a.y_bf16 = p.y_dtype == R9VX_DTYPE_BF16;
     a.epilogue = p.epilogue;
-    /* 256 x 256 register-decoded tiles when there are enough of them to fill
-     * the chip; 128-row LDS-decoded tiles (two workgroups per CU) otherwise. */
+    /* The kernel, and with it each output element's arithmetic (the K order
+     * of the MFMA steps, how a weight is rounded to fp16), follows from the
+     * variant's static keys alone -- scheme, n, k and the bucket's 32-bit
+     * addressing bound -- never from the launch's row count: a row's outputs
+     * are the same bits whatever rows share the launch, at whatever index,
+     * and in every bucket above the decode GEMV's.  Q4_K / IQ4_XS run the
+     * 256 x 256 tiles (gemm3 for N % 256 == 0, gemm2 otherwise); Q8_0 / Q6_K /
+     * IQ3_S the 128-row LDS-decoded tile. */
     const bool split = p.scheme == R9VX_SCHEME_Q8_0 || p.scheme == R9VX_SCHEME_Q6_K || p.scheme == R9VX_SCHEME_IQ3_S;
-    const bool big = !split && (uint64_t)((p.m + 255) / 256) * ((p.n + 255) / 256) >= 256;
-    if (big) {
+    if (!split) {
         if (p.scheme == R9VX_SCHEME_Q4_K)
             hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3((p.m + 3) / 4), dim3(256), 0, stream, p.x, p.m, p.k, x16,
                                scale);
@@ -383,7 +388,7 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
         a.m_tiles = (p.m + kM2Rows - 1) / kM2Rows;
         a.n_tiles = (p.n + kM2Cols - 1) / kM2Cols;
         dim3 grid(a.m_tiles * a.n_tiles);
-        if (p.n % kM3Cols == 0 && (uint64_t)p.m * p.k < (1ull << 31)) {
+        if (p.n % kM3Cols == 0 && (uint64_t)p.m_bucket * p.k < (1ull << 31)) {
             if (p.scheme == R9VX_SCHEME_Q4_K)
                 hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_Q4_K>), grid, dim3(512), 0, stream, a);
             else
@@ -400,11 +405,9 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     a.m_tiles = (p.m + 127) / 128;
     a.n_tiles = (p.n + 255) / 256;
     dim3 grid(a.m_tiles * a.n_tiles);
-    /* Q8_0 / Q6_K / IQ3_S always take this LDS-decoded tile (their steps do
-     * not fit the register-decoded core's 16-byte lane payload). */
+    /* Q8_0 / Q6_K / IQ3_S take this LDS-decoded tile (their steps do not
+     * fit the register-decoded core's 16-byte lane payload). */
     switch (p.scheme) {
-    case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q4_K, 128, 1>), grid, dim3(256), 0, stream, a); break;
-    case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_IQ4_XS, 128, 1>), grid, dim3(256), 0, stream, a); break;
     case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q6_K, 128, 1>), grid, dim3(256), 0, stream, a); break;
     case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_IQ3_S, 128, 1>), grid, dim3(256), 0, stream, a); break;
     default: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q8_0, 128, 1>), grid, dim3(256), 0, stream, a); break;

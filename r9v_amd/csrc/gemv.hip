@@ -490,7 +490,12 @@ int launch_scheme_split(const GemvArgs &a, uint32_t m, int spl, uint32_t g, hipS
 int r9vx_launch_gemv(const r9vx_gemv_problem &p, hipStream_t stream) {
     const uint32_t cpr = p.k / 32; /* 16-byte chunks per row, a multiple of 8 */
     /* Two chunks per lane when a row has >= 128 chunks and the activation
-     * registers fit (M rows x 2 chunks). */
+     * registers fit (M rows x 2 chunks).  This choice, the rows per lane
+     * group and the activation staging follow m, but none of them changes a
+     * row's arithmetic: a lane always owns the chunks lir, lir + 64, ... of
+     * every row and adds them in that order (two per segment or one), and the
+     * cross-lane sum over the 64 lanes is the same tree for every value, so
+     * a row's outputs are the same bits for every m of a bucket <= 8. */
     int spl = (cpr % 128 == 0 && p.m <= (p.x_dtype == R9VX_DTYPE_F32 ? 2u : 4u)) ? 2 : 1;
     uint32_t lpr = 64;
     while (lpr > 8 && (cpr / spl) % lpr) lpr >>= 1;

@@ -581,10 +581,14 @@ int entry_range(const char *op, const r9vx_gguf *f, const char *name, const uint
     return R9VX_OK;
 }
 
-bool path_scheme(uint32_t type) { return type == R9VX_SCHEME_Q4_K || type == R9VX_SCHEME_IQ4_XS; }
-bool split_type(uint32_t type) { return type == R9VX_SCHEME_Q8_0 || type == R9VX_SCHEME_Q6_K; }
+/* The GGUF ggml type ids of the tensors this path reads (crates/r9v-format/
+ * src/ggml.rs:38).  They are file data: a static always carries the scheme
+ * code r9vx_scheme_from_ggml_type gives for them. */
+constexpr uint32_t kGgmlQ8_0 = 8, kGgmlQ4_K = 12, kGgmlQ6_K = 14, kGgmlIQ3_S = 21, kGgmlIQ4_XS = 23;
+bool path_scheme(uint32_t type) { return type == kGgmlQ4_K || type == kGgmlIQ4_XS; }
+bool split_type(uint32_t type) { return type == kGgmlQ8_0 || type == kGgmlQ6_K; }
 /* IQ3_S: repacked on the host into the 112-byte device blocks while uploading */
-bool repack_type(uint32_t type) { return type == R9VX_SCHEME_IQ3_S; }
+bool repack_type(uint32_t type) { return type == kGgmlIQ3_S; }
 
 /* Element type and device layout of the weights this path reads per type. */
 uint32_t type_dtype(uint32_t type) { return split_type(type) ? R9VX_DTYPE_I8 : R9VX_DTYPE_I4; }
@@ -629,6 +633,19 @@ int hip_rc(const char *op, hipError_t rc) {
 }  // namespace
 
 extern "C" {
+
+/* GgmlType::scheme (crates/r9v-format/src/ggml.rs:253-276) restricted to the
+ * five types this path reads. */
+uint32_t r9vx_scheme_from_ggml_type(uint32_t ggml_type) {
+    switch (ggml_type) {
+    case kGgmlQ8_0: return R9VX_SCHEME_Q8_0;
+    case kGgmlQ4_K: return R9VX_SCHEME_Q4_K;
+    case kGgmlQ6_K: return R9VX_SCHEME_Q6_K;
+    case kGgmlIQ3_S: return R9VX_SCHEME_IQ3_S;
+    case kGgmlIQ4_XS: return R9VX_SCHEME_IQ4_XS;
+    default: return 0;
+    }
+}
 
 int r9vx_gguf_parse(const uint8_t *bytes, uint64_t len, r9vx_gguf **out) {
     return parse(bytes, len, len, false, out);
@@ -852,7 +869,7 @@ int r9vx_gguf_matmul_static(const r9vx_gguf *f, const char *name, r9vx_matmul_st
     if (!path_scheme(t->type) && !split_type(t->type) && !repack_type(t->type))
         return refuse(op, R9VX_ERR_UNSUPPORTED,
                       "tensor \"" + t->name + "\" is " + r9vx_gguf_type_name(t->type) +
-                          "; this path multiplies Q4_K (12), IQ4_XS (23), Q6_K (14), Q8_0 (8) and IQ3_S (21) weights");
+                          "; this path multiplies Q4_K, IQ4_XS, Q6_K, Q8_0 and IQ3_S (GGUF types 12, 23, 14, 8, 21) weights");
     if (t->dims.size() != 2 || t->dims[0] > UINT32_MAX || t->dims[1] > UINT32_MAX)
         return refuse(op, R9VX_ERR_INVALID,
                       "tensor \"" + t->name + "\" dims " + dims_text(*t) + " are not a {K, N} matrix of u32 sizes");
@@ -862,7 +879,7 @@ int r9vx_gguf_matmul_static(const r9vx_gguf *f, const char *name, r9vx_matmul_st
                           "; the matmul kernels take K in multiples of 256");
     st->k = (uint32_t)t->dims[0];
     st->n = (uint32_t)t->dims[1];
-    st->w_scheme = t->type;
+    st->w_scheme = r9vx_scheme_from_ggml_type(t->type);
     st->w_dtype = type_dtype(t->type);
     st->w_layout = type_layout(t->type);
     return R9VX_OK;
@@ -919,8 +936,8 @@ int r9vx_gguf_moe_ffn_static(const r9vx_gguf *f, const char *gate, const char *u
             st->e_local = (uint32_t)e;
             st->dm = (uint32_t)dm;
             st->dff = (uint32_t)dff;
-            st->gate_up = r9vx_moe_ffn_proj{type_dtype(g->type), g->type, type_layout(g->type)};
-            st->down = r9vx_moe_ffn_proj{type_dtype(d->type), d->type, type_layout(d->type)};
+            st->gate_up = r9vx_moe_ffn_proj{type_dtype(g->type), r9vx_scheme_from_ggml_type(g->type), type_layout(g->type)};
+            st->down = r9vx_moe_ffn_proj{type_dtype(d->type), r9vx_scheme_from_ggml_type(d->type), type_layout(d->type)};
         }
     }
     if (pr.empty()) return R9VX_OK;
@@ -978,7 +995,7 @@ int r9vx_gguf_upload_split(const r9vx_gguf *f, const uint8_t *bytes, uint64_t le
     if (!body || !scales) return refuse(op, R9VX_ERR_NULL, "body and scales are required");
     const TypeRow *row = type_row(t->type);
     const uint64_t nblocks = t->nbytes / row->block_bytes;
-    const uint32_t body_block = row->block_bytes - 2, d_off = t->type == R9VX_SCHEME_Q8_0 ? 0 : 208;
+    const uint32_t body_block = row->block_bytes - 2, d_off = t->type == kGgmlQ8_0 ? 0 : 208;
     if (body_bytes < nblocks * body_block || scales_bytes < nblocks * 2)
         return refuse(op, R9VX_ERR_INVALID,
                       fmt("body holds %llu and scales %llu bytes; tensor \"%s\" needs %llu and %llu",
@@ -1088,7 +1105,7 @@ int r9vx_gguf_upload_gate_up_split(const r9vx_gguf *gate_file, const uint8_t *ga
     const TypeRow *row = type_row(g->type);
     const uint64_t per_expert = g->dims[0] / row->block_len * g->dims[1]; /* blocks */
     const uint64_t experts = g->dims[2], nblocks = per_expert * experts;
-    const uint32_t body_block = row->block_bytes - 2, d_off = g->type == R9VX_SCHEME_Q8_0 ? 0 : 208;
+    const uint32_t body_block = row->block_bytes - 2, d_off = g->type == kGgmlQ8_0 ? 0 : 208;
     if (body_bytes < 2 * nblocks * body_block || scales_bytes < 2 * nblocks * 2)
         return refuse(op, R9VX_ERR_INVALID,
                       fmt("body holds %llu and scales %llu bytes; the stacked gate_up needs %llu and %llu",

@@ -11,10 +11,10 @@
  *    atomics ordering, so `sorted`, `counts`, `offsets` are bit-exact.
  *  - FFN per expert (:527-639): gate rows [0,Dff), up rows [Dff,2Dff) of the
  *    expert's [2Dff, Dm] block; h = silu(g)*u (activation.rs:135-138,
- *    act_mul.rs:86-99); o = h . Wd^T.  Decode (t <= 8) runs dequant-fused
- *    GEMVs with the rows in pair order (token * K + slot), so it needs no
- *    sort pass (h kept in f32 between them); larger t sorts and runs the
- *    grouped MFMA GEMMs of moe_gemm.hip.
+ *    act_mul.rs:86-99); o = h . Wd^T.  Variants with t_bucket <= 8 run
+ *    dequant-fused GEMVs with the rows in pair order (token * K + slot), so
+ *    they need no sort pass (h kept in f32 between them); larger buckets sort
+ *    and run the grouped MFMA GEMMs of moe_gemm.hip, whatever the launch's t.
  *  - Combine (:641-653): y[t] = sum over the token's pairs in ascending
  *    (expert, slot) order of w * o, f32, then the shared experts' outputs are
  *    added (the residual_add of crates/r9v-models/src/generic.rs:1458-1495).
@@ -1222,7 +1222,7 @@ int r9vx_moe_decode_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStre
 int r9vx_moe_combine_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s) {
     MoeCombineArgs c{p.weights, p.ids, p.y, p.ws, L, p.t, p.k, p.dm, p.shared, p.t * p.k, p.e};
     dim3 grid((p.dm / 4 + 255) / 256, p.t);
-    if (p.t <= 8)
+    if (r9vx_moe_decode_form(p))
         hipLaunchKernelGGL(r9vx_moe_combine_kernel, grid, dim3(256), 0, s, c);
     else /* the grouped path's fp16 rows */
         hipLaunchKernelGGL(r9vx_moe_combine16_kernel, grid, dim3(256), 0, s, c);

@@ -4,6 +4,7 @@
  * reference's spikes/dot4-gemv and spikes/wmma-l1 measurements).
  */
 #include "r9vx_device.h"
+#include "r9vx_expf.h"
 #include "r9vx_probe.h"
 
 namespace {
@@ -57,9 +58,47 @@ __global__ __launch_bounds__(256) void mfma_kernel(uint32_t iters, float *sink) 
     sink[(uint64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+/* The three device forms of the routing exp, on the inputs whose bits are
+ * first .. first + n - 1, against `want`: bad[f] counts the inputs where
+ * form f (0 r9vx_expf, 1 r9vx_expf_tab, 2 r9vx_expf_tab_nb) gives other bits
+ * (two NaNs count as equal).  One atomic add per form per workgroup. */
+__global__ __launch_bounds__(256) void expf_check_kernel(uint32_t first, uint32_t n, const float *__restrict__ want,
+                                                         uint32_t *__restrict__ bad) {
+    __shared__ uint64_t tab[R9VX_EXP2F_N];
+    __shared__ uint32_t cnt[3];
+    r9vx_exp2_fill(tab, threadIdx.x, blockDim.x);
+    if (threadIdx.x < 3) cnt[threadIdx.x] = 0;
+    __syncthreads();
+    uint32_t b[3] = {0, 0, 0};
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const float x = __builtin_bit_cast(float, first + i);
+        const float w = want[i];
+        const float got[3] = {r9vx_expf(x), r9vx_expf_tab(x, tab), r9vx_expf_tab_nb(x, tab)};
+#pragma unroll
+        for (int f = 0; f < 3; ++f) {
+            const bool same = __builtin_bit_cast(uint32_t, got[f]) == __builtin_bit_cast(uint32_t, w) ||
+                              (got[f] != got[f] && w != w);
+            b[f] += same ? 0u : 1u;
+        }
+    }
+#pragma unroll
+    for (int f = 0; f < 3; ++f)
+        if (b[f]) atomicAdd(&cnt[f], b[f]);
+    __syncthreads();
+    if (threadIdx.x < 3 && cnt[threadIdx.x]) atomicAdd(&bad[threadIdx.x], cnt[threadIdx.x]);
+}
+
 }  // namespace
 
 extern "C" {
+
+int r9vx_probe_expf_check_launch(uint32_t first_bits, uint32_t n, const float *want, uint32_t *bad,
+                                 r9vx_stream_t stream) {
+    if (!want || !bad || n == 0 || (uint64_t)first_bits + n > (1ull << 32)) return R9VX_ERR_INVALID;
+    hipLaunchKernelGGL(expf_check_kernel, dim3(1024), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), first_bits,
+                       n, want, bad);
+    return (int)hipGetLastError();
+}
 
 uint32_t r9vx_probe_stream_blocks(uint64_t bytes) {
     uint64_t n16 = bytes / 16;

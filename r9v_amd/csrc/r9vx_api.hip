@@ -126,8 +126,8 @@ uint32_t r9vx_abi_version(void) { return R9VX_ABI_VERSION; }
 
 static void check_matmul_static(const r9vx_matmul_static *st, Problems &pr) {
     if (!matmul_scheme(st->w_scheme))
-        pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u is not Q4_K (12), IQ4_XS (23), Q6_K (14), Q8_0 (8) or IQ3_S (21)",
-               st->w_scheme);
+        pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u is not the SchemeId code of Q4_K (3), Q8_0 (5), Q6_K (11), IQ4_XS (15) "
+               "or IQ3_S (17)", st->w_scheme);
     if (repacked_scheme(st->w_scheme) && st->in_dtype != R9VX_DTYPE_BF16)
         pr.add(R9VX_ERR_UNSUPPORTED, "w_scheme %u takes bf16 activations only", st->w_scheme);
 
@@ -152,7 +152,7 @@ static void check_matmul_static(const r9vx_matmul_static *st, Problems &pr) {
     if (st->sparse) pr.add(R9VX_ERR_UNSUPPORTED, "sparse (2:4) weights are not implemented");
 }
 
-/* The MFMA path (bf16 activations, m > 8) stages x as fp16 rows plus per-row
+/* The MFMA path (bf16 activations, m_bucket > 8) stages x as fp16 rows plus per-row
  * scales in the workspace; the GEMV path needs none. */
 size_t r9vx_matmul_workspace_bytes(const r9vx_matmul_static *st) {
     if (!st || st->in_dtype != R9VX_DTYPE_BF16 || st->m_bucket <= 8) return 0;
@@ -205,9 +205,10 @@ int r9vx_matmul_launch(const r9vx_matmul_static *st, const r9vx_matmul_args *a,
         pr.add(R9VX_ERR_INVALID, "residual given without residual epilogue");
     if ((a->w && !aligned16(a->w)) || (a->x && !aligned16(a->x)) || (a->y && !aligned16(a->y)))
         pr.add(R9VX_ERR_ALIGN, "w, x and y must be 16-byte aligned");
-    if (st->in_dtype == R9VX_DTYPE_BF16 && a->m > 8) {
+    if (st->in_dtype == R9VX_DTYPE_BF16 && st->m_bucket > 8 && a->m > 0) {
         if (!a->workspace)
-            pr.add(R9VX_ERR_WORKSPACE, "m=%u > 8 runs the MFMA path: workspace of r9vx_matmul_workspace_bytes required", a->m);
+            pr.add(R9VX_ERR_WORKSPACE, "m_bucket=%u > 8 runs the MFMA path: workspace of r9vx_matmul_workspace_bytes required",
+                   st->m_bucket);
         else if ((uintptr_t)a->workspace & 255u)
             pr.add(R9VX_ERR_ALIGN, "workspace must be 256-byte aligned");
     }
@@ -216,7 +217,12 @@ int r9vx_matmul_launch(const r9vx_matmul_static *st, const r9vx_matmul_args *a,
 
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const uint64_t w_row = device_row_bytes(st->w_scheme, st->k);
-    const bool mfma = st->in_dtype == R9VX_DTYPE_BF16 && a->m > 8;
+    /* The path is chosen by the variant's bucket, not by m: every launch of
+     * one static runs the same kernels with the same per-element arithmetic,
+     * so a row's outputs do not depend on the rows beside it (the
+     * batch-invariance gate, crates/r9v-t0/src/harness.rs:903-948).  Buckets
+     * <= 8 run the GEMV, bf16 buckets above run the MFMA GEMM. */
+    const bool mfma = st->in_dtype == R9VX_DTYPE_BF16 && st->m_bucket > 8;
     if (mfma) {
         r9vx_gemm_problem g{};
         g.w = a->w;
@@ -229,6 +235,7 @@ int r9vx_matmul_launch(const r9vx_matmul_static *st, const r9vx_matmul_args *a,
         g.n = st->n;
         g.k = st->k;
         g.m = a->m;
+        g.m_bucket = st->m_bucket;
         g.scheme = st->w_scheme;
         g.y_dtype = st->out_dtype;
         g.epilogue = st->epilogue;
@@ -283,7 +290,7 @@ int r9vx_repack_launch(uint32_t scheme, const uint8_t *wire, uint32_t n_rows, ui
                        uint16_t *scales, r9vx_stream_t stream) {
     Problems pr;
     if (!repacked_scheme(scheme))
-        pr.add(R9VX_ERR_UNSUPPORTED, "scheme %u: only Q8_0 (8), Q6_K (14) and IQ3_S (21) are repacked; Q4_K / "
+        pr.add(R9VX_ERR_UNSUPPORTED, "scheme %u: only Q8_0 (5), Q6_K (11) and IQ3_S (17) are repacked; Q4_K / "
                "IQ4_XS wire blocks are the device layout", scheme);
     const uint32_t bl = block_len(scheme);
     if (k == 0 || k % bl) pr.add(R9VX_ERR_INVALID, "k=%u must be a positive multiple of %u", k, bl);
@@ -362,7 +369,9 @@ static int route_launch(const char *op, const r9vx_moe_route_static *st, const r
     if (st->top_k == 0) pr.add(R9VX_ERR_INVALID, "top_k must be > 0");
     if (!(scale > 0.0f) || !(scale < __builtin_huge_valf()))
         pr.add(R9VX_ERR_INVALID, "scale must be finite and > 0, got %g", (double)scale);
-    if (st->n_group != 0) pr.add(R9VX_ERR_UNSUPPORTED, "grouped expert routing is not implemented");
+    if (st->n_group != 0 || st->topk_group != 0)
+        pr.add(R9VX_ERR_UNSUPPORTED, "grouped expert routing (n_group %u, topk_group %u) is not implemented",
+               st->n_group, st->topk_group);
     if (a->t == 0 || st->e_total == 0) pr.add(R9VX_ERR_INVALID, "T=%u and E=%u must be > 0", a->t, st->e_total);
     if (st->top_k > st->e_total) pr.add(R9VX_ERR_INVALID, "top_k %u cannot exceed number of experts E=%u", st->top_k, st->e_total);
     if (st->e_total > 1024) pr.add(R9VX_ERR_UNSUPPORTED, "E=%u exceeds 1024", st->e_total);
@@ -406,7 +415,9 @@ static void check_route_static(const r9vx_moe_route_static *st, uint32_t t, Prob
     if (st->top_k == 0) pr.add(R9VX_ERR_INVALID, "top_k must be > 0");
     if (!(scale > 0.0f) || !(scale < __builtin_huge_valf()))
         pr.add(R9VX_ERR_INVALID, "scale must be finite and > 0, got %g", (double)scale);
-    if (st->n_group != 0) pr.add(R9VX_ERR_UNSUPPORTED, "grouped expert routing is not implemented");
+    if (st->n_group != 0 || st->topk_group != 0)
+        pr.add(R9VX_ERR_UNSUPPORTED, "grouped expert routing (n_group %u, topk_group %u) is not implemented",
+               st->n_group, st->topk_group);
     if (t == 0 || st->e_total == 0) pr.add(R9VX_ERR_INVALID, "T=%u and E=%u must be > 0", t, st->e_total);
     if (st->top_k > st->e_total) pr.add(R9VX_ERR_INVALID, "top_k %u cannot exceed number of experts E=%u", st->top_k, st->e_total);
     if (st->e_total > 1024) pr.add(R9VX_ERR_UNSUPPORTED, "E=%u exceeds 1024", st->e_total);
@@ -429,7 +440,8 @@ int r9vx_moe_route_hidden_launch(const r9vx_moe_route_static *st, const r9vx_moe
     }
     float scale;
     check_route_static(st, a->t, pr, scale);
-    if (a->t > 8) pr.add(R9VX_ERR_UNSUPPORTED, "t=%u: the fused router is the decode form (t <= 8)", a->t);
+    if (st->t_bucket > 8)
+        pr.add(R9VX_ERR_UNSUPPORTED, "t_bucket=%u: the fused router is the decode form (t_bucket <= 8)", st->t_bucket);
     if (a->dm == 0 || a->dm % 128 || a->dm > 8192)
         pr.add(R9VX_ERR_INVALID, "dm=%u must be a positive multiple of 128, at most 8192", a->dm);
     if (!a->x || !a->w_router || !a->expert_ids || !a->weights)
@@ -504,12 +516,12 @@ static void check_ffn_static(const r9vx_moe_ffn_static *st, Problems &pr) {
     if (st->dm == 0 || st->dm % 256) pr.add(R9VX_ERR_INVALID, "Dm=%u must be a positive multiple of 256", st->dm);
     if (st->dff == 0 || st->dff % 256) pr.add(R9VX_ERR_INVALID, "Dff=%u must be a positive multiple of 256", st->dff);
     if (!matmul_scheme(st->gate_up.scheme))
-        pr.add(R9VX_ERR_UNSUPPORTED, "gate_up scheme %u: Q4_K (12), IQ4_XS (23), IQ3_S (21), Q8_0 (8) or Q6_K (14)",
+        pr.add(R9VX_ERR_UNSUPPORTED, "gate_up scheme %u: Q4_K (3), Q8_0 (5), Q6_K (11), IQ4_XS (15) or IQ3_S (17)",
                st->gate_up.scheme);
     else
         check_weight_keys("gate_up", st->gate_up.scheme, st->gate_up.dtype, st->gate_up.layout, pr);
     if (!matmul_scheme(st->down.scheme))
-        pr.add(R9VX_ERR_UNSUPPORTED, "down scheme %u: Q4_K (12), IQ4_XS (23), IQ3_S (21), Q8_0 (8) or Q6_K (14)",
+        pr.add(R9VX_ERR_UNSUPPORTED, "down scheme %u: Q4_K (3), Q8_0 (5), Q6_K (11), IQ4_XS (15) or IQ3_S (17)",
                st->down.scheme);
     else
         check_weight_keys("down", st->down.scheme, st->down.dtype, st->down.layout, pr);
@@ -739,7 +751,8 @@ int r9vx_probe_moe_stage_launch(const r9vx_moe_ffn_static *st, const r9vx_moe_ff
         return pr.finish("probe_moe_stage");
     }
     if (stage < 1 || stage > 3) pr.add(R9VX_ERR_INVALID, "stage %u: 1 (gate/up), 2 (down) or 3 (combine)", stage);
-    if (a->t <= 8) pr.add(R9VX_ERR_UNSUPPORTED, "t=%u runs the decode path, which has no separate GEMM stages", a->t);
+    if (st->t_bucket <= 8)
+        pr.add(R9VX_ERR_UNSUPPORTED, "t_bucket=%u runs the decode path, which has no separate GEMM stages", st->t_bucket);
     if (!a->x || !a->weights || !a->w_gate_up || !a->w_down || !a->y)
         pr.add(R9VX_ERR_NULL, "x, weights, w_gate_up, w_down and y are required");
     int rc = ffn_common("probe_moe_stage", st, a->expert_ids, a->t, a->sort_workspace, pr);
@@ -776,7 +789,11 @@ int r9vx_moe_sort_launch(const r9vx_moe_ffn_static *st, const uint32_t *ids, uin
 int r9vx_launch_moe(const r9vx_moe_problem &p, hipStream_t s) {
     MoeLayout L = r9vx_moe_layout(p.t_bucket, p.e, p.k, p.dm, p.dff, p.shared);
     int rc = 0;
-    if (p.t <= 8) { /* pair-order rows: no sort; the combine checks the ids */
+    /* Decode or grouped by the variant's t_bucket, never by t: every launch
+     * of one static keeps h and o in the same precision and runs the same
+     * GEMMs, so a token's output is the same bits whatever tokens share the
+     * batch (crates/r9v-t0/src/harness.rs:903-948). */
+    if (r9vx_moe_decode_form(p)) { /* pair-order rows: no sort; the combine checks the ids */
         rc = r9vx_moe_decode_stage(p, L, s);
     } else {
         bool x16_done = false;

@@ -107,8 +107,9 @@ struct r9vx_gemm_problem {
     const float *bias;
     const float *residual;
     void *y;
-    void *workspace; /* r9vx_gemm_workspace_bytes(m, k): fp16 x rows + row scales */
+    void *workspace; /* r9vx_gemm_workspace_bytes(m_bucket, k): fp16 x rows + row scales */
     uint32_t n, k, m;
+    uint32_t m_bucket; /* the variant's bucket: the kernel is chosen from it, never from m */
     uint32_t scheme, y_dtype, epilogue;
 };
 size_t r9vx_gemm_workspace_bytes(uint32_t m_bucket, uint32_t k);

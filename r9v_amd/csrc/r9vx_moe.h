@@ -91,6 +91,11 @@ struct MoeCombineArgs {
     uint32_t t, k, dm, shared, p, e;
 };
 
+/* The decode form (pair-order rows, f32 h and o, GEMV kernels) serves the
+ * variants with t_bucket <= 8, the grouped MFMA form every larger bucket,
+ * whatever the launch's t. */
+inline bool r9vx_moe_decode_form(const r9vx_moe_problem &p) { return p.t_bucket <= 8; }
+
 /* x16_done != NULL: the sort kernels also convert the activation rows for
  * the grouped GEMMs (only on the multi-kernel path; *x16_done says whether). */
 int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream_t s, bool *x16_done = nullptr);

@@ -21,7 +21,12 @@ LIB_PATH = PKG / "libr9vx.so"
 F32, F16, BF16, I8, I4, U32 = 0, 1, 2, 5, 6, 8
 LAYOUT_L0, LAYOUT_L1, LAYOUT_L1S = 1, 2, 3                      # the reference's layouts: refused
 LAYOUT_GGUF_WIRE, LAYOUT_SPLIT, LAYOUT_IQ3S_112 = 0x100, 0x101, 0x102
-Q4_K, IQ4_XS, Q6_K, Q8_0, IQ3_S = 12, 23, 14, 8, 21
+# weight schemes: the reference's SchemeId codes (I4K, I4Xs, I6K, I8B32F, Iq3S;
+# crates/r9v-format/src/scheme.rs:115-138), which the statics carry
+Q4_K, IQ4_XS, Q6_K, Q8_0, IQ3_S = 3, 15, 11, 5, 17
+# GGUF ggml type ids of the same formats (file data only: GgufFile tensor types)
+GGML_Q4_K, GGML_IQ4_XS, GGML_Q6_K, GGML_Q8_0, GGML_IQ3_S = 12, 23, 14, 8, 21
+SCHEME_OF_GGML = {GGML_Q4_K: Q4_K, GGML_IQ4_XS: IQ4_XS, GGML_Q6_K: Q6_K, GGML_Q8_0: Q8_0, GGML_IQ3_S: IQ3_S}
 EPILOGUE_NONE, EPILOGUE_BIAS, EPILOGUE_RESIDUAL, EPILOGUE_SWIGLU = 0, 1, 2, 3
 SCORING_SOFTMAX, SCORING_SIGMOID = 0, 1
 ACT_SILU = 0
@@ -51,8 +56,8 @@ class MatmulArgs(ctypes.Structure):
 
 class MoeRouteStatic(ctypes.Structure):
     _fields_ = [("t_bucket", _U32), ("e_total", _U32), ("top_k", _U32), ("scoring", _U32),
-                ("renormalize", _U32), ("scale_bits", _U32), ("has_bias", _U32),
-                ("n_group", _U32)]
+                ("renormalize", _U32), ("n_group", _U32), ("topk_group", _U32), ("scale_bits", _U32),
+                ("has_bias", _U32)]
 
 
 class MoeRouteArgs(ctypes.Structure):
@@ -109,6 +114,7 @@ EXPORTS = [
     ("r9vx_dequantize_launch", [_U32, _P, _U32, _U32, _P, _P], ctypes.c_int),
     ("r9vx_validate_weights_launch", [_U32, _P, _U32, _U32, _P, _P], ctypes.c_int),
     ("r9vx_repack_launch", [_U32, _P, _U32, _U32, _P, _P, _P], ctypes.c_int),
+    ("r9vx_scheme_from_ggml_type", [_U32], _U32),
     ("r9vx_last_error", [], ctypes.c_char_p),
     ("r9vx_abi_version", [], _U32),
     # include/r9vx_probe.h
@@ -116,6 +122,7 @@ EXPORTS = [
     ("r9vx_probe_stream_blocks", [ctypes.c_uint64], _U32),
     ("r9vx_probe_mfma_launch", [_U32, _U32, _P, _P], ctypes.c_int),
     ("r9vx_probe_moe_stage_launch", [_P, _P, _U32, _P], ctypes.c_int),
+    ("r9vx_probe_expf_check_launch", [_U32, _U32, _P, _P, _P], ctypes.c_int),
     # include/r9vx_gguf.h
     ("r9vx_gguf_parse", [_P, _U64, _P], ctypes.c_int),
     ("r9vx_gguf_parse_table", [_P, _U64, _U64, _P], ctypes.c_int),
@@ -238,10 +245,11 @@ def matmul_static(n, k, w_scheme, in_dtype, out_dtype, m_bucket=8, epilogue=EPIL
 
 
 def matmul(w, w_scheme, n, k, x, out_dtype=F32, bias=None, residual=None, y=None, workspace=None,
-           stream=None, w_scales=None, swiglu=False):
+           stream=None, w_scales=None, swiglu=False, m_bucket=None):
     """y[m, n] = x[m, :] . w[n, :] (+ bias | + residual): T0 execute_matmul_op meaning.
     Q6_K / Q8_0 weights are a split body `w` plus its f16 d array `w_scales`,
-    IQ3_S weights the repacked 112-byte blocks (see `repack`)."""
+    IQ3_S weights the repacked 112-byte blocks (see `repack`).  The variant's
+    M bucket is `m_bucket` (default: m itself); it, not m, picks the kernels."""
     torch = _need_gpu(w, x, bias, residual, y, w_scales)
     m = x.shape[0]
     if y is None:
@@ -250,7 +258,7 @@ def matmul(w, w_scheme, n, k, x, out_dtype=F32, bias=None, residual=None, y=None
     epi = EPILOGUE_BIAS if bias is not None else (EPILOGUE_RESIDUAL if residual is not None else EPILOGUE_NONE)
     if swiglu:  # w holds 2n rows: gate [0, n) then up [n, 2n); y = silu(gate) * up
         epi = EPILOGUE_SWIGLU
-    st = matmul_static(n, k, w_scheme, _dtype_code(x), out_dtype, m_bucket=max(m, 1), epilogue=epi)
+    st = matmul_static(n, k, w_scheme, _dtype_code(x), out_dtype, m_bucket=m_bucket or max(m, 1), epilogue=epi)
     if workspace is None:
         nbytes = matmul_workspace_bytes(st)
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes else None
@@ -308,7 +316,7 @@ def validate_weights(wire, scheme, n_rows, k, stream=None) -> int:
 def route_static(e, k, t_bucket, scoring=SCORING_SOFTMAX, renormalize=True, scale=1.0,
                  has_bias=False):
     scale_bits = struct.unpack("<I", struct.pack("<f", scale))[0]
-    return MoeRouteStatic(t_bucket, e, k, scoring, int(renormalize), scale_bits, int(has_bias), 0)
+    return MoeRouteStatic(t_bucket, e, k, scoring, int(renormalize), 0, 0, scale_bits, int(has_bias))
 
 
 def moe_route(logits, k, bias=None, scoring=SCORING_SOFTMAX, renormalize=True, scale=1.0,

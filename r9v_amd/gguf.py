@@ -346,7 +346,7 @@ class ShardSet:
 
 def device_bytes(info: TensorInfo) -> int:
     """Bytes of a tensor in its device layout (IQ3_S: 112-byte blocks)."""
-    return info.nbytes // 110 * ffi.IQ3S_DEV_BYTES if info.dtype == ffi.IQ3_S else info.nbytes
+    return info.nbytes // 110 * ffi.IQ3S_DEV_BYTES if info.dtype == ffi.GGML_IQ3_S else info.nbytes
 
 
 def upload(file: GgufFile, data, name: str, out=None, stream=None):

@@ -19,11 +19,12 @@ GAMMA = np.uint64(0x9E3779B97F4A7C15)
 M1 = np.uint64(0xBF58476D1CE4E5B9)
 M2 = np.uint64(0x94D049BB133111EB)
 
-Q4_K = 12
-IQ4_XS = 23
-Q6_K = 14
-Q8_0 = 8
-IQ3_S = 21
+# weight schemes by their SchemeId codes (as r9v_amd.ffi)
+Q4_K = 3
+IQ4_XS = 15
+Q6_K = 11
+Q8_0 = 5
+IQ3_S = 17
 BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136, Q6_K: 210, Q8_0: 34, IQ3_S: 110}
 BLOCK_LEN = {Q4_K: 256, IQ4_XS: 256, Q6_K: 256, Q8_0: 32, IQ3_S: 256}
 D_OFFSET = {Q4_K: 0, IQ4_XS: 0, Q6_K: 208, Q8_0: 0, IQ3_S: 0}  # byte offset of each block's f16 d

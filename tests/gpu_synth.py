@@ -3,7 +3,8 @@
 seed on a given device, and tests hand the same bytes to the oracle)."""
 from __future__ import annotations
 
-BLOCK_BYTES = {12: 144, 23: 136}
+Q4_K, IQ4_XS = 3, 15  # SchemeId codes (r9v_amd.ffi)
+BLOCK_BYTES = {Q4_K: 144, IQ4_XS: 136}
 
 
 def quant_weights_gpu(torch, scheme, seed, rows, k, device="cuda"):
@@ -16,7 +17,7 @@ def quant_weights_gpu(torch, scheme, seed, rows, k, device="cuda"):
     blk = torch.randint(0, 256, (nblocks, bb), dtype=torch.uint8, generator=g, device=device)
     d = (torch.randn(nblocks, generator=g, device=device) * 0.02).abs().half()
     blk[:, 0:2] = d.view(torch.uint8).view(nblocks, 2)
-    if scheme == 12:
+    if scheme == Q4_K:
         dmin = (torch.randn(nblocks, generator=g, device=device) * 0.01).abs().half()
         blk[:, 2:4] = dmin.view(torch.uint8).view(nblocks, 2)
     return blk.view(rows, (k // 256) * bb)

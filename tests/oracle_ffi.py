@@ -13,8 +13,18 @@ import numpy as np
 ROOT = pathlib.Path(__file__).resolve().parent.parent
 LIB_PATH = ROOT / "oracle" / "liboracle.so"
 
-Q4_K, IQ4_XS, Q6_K, Q8_0, IQ3_S = 12, 23, 14, 8, 21
+# Schemes by the SchemeId codes the library's statics carry (r9v_amd.ffi); the
+# C oracle restates ggml_dequantize and is keyed by GGUF ggml type ids, so
+# every wrapper below translates with _gg.
+Q4_K, IQ4_XS, Q6_K, Q8_0, IQ3_S = 3, 15, 11, 5, 17
+_GGML = {Q4_K: 12, IQ4_XS: 23, Q6_K: 14, Q8_0: 8, IQ3_S: 21}
 F32, BF16 = 0, 2
+
+
+def _gg(scheme):
+    """The oracle's GGUF type id of a scheme code (unknown codes pass through
+    unchanged, so the oracle's own refusal of them is what a test sees)."""
+    return _GGML.get(scheme, scheme)
 
 _lib = None
 
@@ -38,6 +48,8 @@ def lib():
         L.rxo_f32_to_bf16.restype = ctypes.c_uint16
         L.rxo_expf.argtypes = [ctypes.c_float]
         L.rxo_expf.restype = ctypes.c_float
+        L.rxo_expf_fill.argtypes = [U, ctypes.c_uint64, P]
+        L.rxo_expf_fill.restype = None
         L.rxo_q4k_unpack_scales.argtypes = [P, P, P]
         L.rxo_dequantize.argtypes = [I, P, U, U, P]
         L.rxo_matmul.argtypes = [I, P, U, U, I, P, U, P, P, I, P]
@@ -50,6 +62,7 @@ def lib():
         L.rxo_moe_route.argtypes = [P, P, U, U, U, ctypes.c_float, I, I, P, P]
         L.rxo_moe_sort.argtypes = [P, U, U, U, P, P, P]
         L.rxo_moe_ffn.argtypes = [I, P, U, U, U, U, U, U, P, P, I, P, I, P, I, P]
+        L.rxo_moe_ffn_mt.argtypes = [I, P, U, U, U, U, U, U, P, P, I, P, I, P, I, P, I]
         L.rxo_moe_ffn_full.argtypes = [I, P, U, U, U, U, U, P, P, I, P, I, P, P]
         L.rxo_expert_ffn.argtypes = [I, P, U, U, U, I, P, I, P, I, P]
         _lib = L
@@ -71,9 +84,16 @@ def _check(rc, what):
         raise OracleError(rc, what)
 
 
+def expf_fill(first_bits, n, out=None):
+    """libm expf of the floats whose bits are first_bits .. first_bits + n - 1."""
+    out = np.empty(n, dtype=np.float32) if out is None else out
+    lib().rxo_expf_fill(first_bits, n, _p(out))
+    return out
+
+
 def dequantize(scheme, wire, n, k):
     out = np.empty((n, k), dtype=np.float32)
-    _check(lib().rxo_dequantize(scheme, _p(np.ascontiguousarray(wire)), n, k, _p(out)), "dequantize")
+    _check(lib().rxo_dequantize(_gg(scheme), _p(np.ascontiguousarray(wire)), n, k, _p(out)), "dequantize")
     return out
 
 
@@ -83,9 +103,9 @@ def matmul(scheme, w, n, k, x, x_dtype, y_dtype=F32, bias=None, residual=None, t
     y = np.empty((m, n), dtype=np.float32 if y_dtype == F32 else np.uint16)
     w = np.ascontiguousarray(w)
     if threads and bias is None and residual is None:  # the threaded oracle has no epilogue
-        rc = lib().rxo_matmul_mt(scheme, _p(w), n, k, x_dtype, _p(x), m, y_dtype, _p(y), threads)
+        rc = lib().rxo_matmul_mt(_gg(scheme), _p(w), n, k, x_dtype, _p(x), m, y_dtype, _p(y), threads)
     else:
-        rc = lib().rxo_matmul(scheme, _p(w), n, k, x_dtype, _p(x), m, _p(bias), _p(residual),
+        rc = lib().rxo_matmul(_gg(scheme), _p(w), n, k, x_dtype, _p(x), m, _p(bias), _p(residual),
                               y_dtype, _p(y))
     _check(rc, "matmul")
     return y
@@ -136,17 +156,31 @@ def moe_sort(ids, e):
 
 
 def moe_ffn(x, x_dtype, ids, weights, e, dff, w_gate_up, w_down, scheme_gu=IQ4_XS,
-            scheme_dn=Q4_K, shared=0, h_bf16=False):
+            scheme_dn=Q4_K, shared=0, h_bf16=False, threads=0):
+    """T0 moe_ffn; threads > 0 runs the expert FFNs on that many OpenMP
+    threads (bit-identical result)."""
     x = np.ascontiguousarray(x)
     t, dm = x.shape
     ids = np.ascontiguousarray(ids, dtype=np.uint32)
     weights = np.ascontiguousarray(weights, dtype=np.float32)
     k = ids.shape[1]
     y = np.empty((t, dm), dtype=np.float32)
-    _check(lib().rxo_moe_ffn(x_dtype, _p(x), t, dm, dff, e, shared, k, _p(ids), _p(weights),
-                             scheme_gu, _p(np.ascontiguousarray(w_gate_up)), scheme_dn,
-                             _p(np.ascontiguousarray(w_down)), int(h_bf16), _p(y)), "moe_ffn")
+    args = (x_dtype, _p(x), t, dm, dff, e, shared, k, _p(ids), _p(weights), _gg(scheme_gu),
+            _p(np.ascontiguousarray(w_gate_up)), _gg(scheme_dn), _p(np.ascontiguousarray(w_down)), int(h_bf16),
+            _p(y))
+    if threads:
+        _check(lib().rxo_moe_ffn_mt(*args, threads), "moe_ffn")
+    else:
+        _check(lib().rxo_moe_ffn(*args), "moe_ffn")
     return y
+
+
+def host_threads():
+    """Threads for the oracle's parallel forms: the host's CPUs, at most 16
+    (a GPU box's CPU share)."""
+    import os
+
+    return max(1, min(16, len(os.sched_getaffinity(0))))
 
 
 def moe_ffn_full(x, x_dtype, ids, weights, e, dff, w_gate_up, w_down, scheme_gu=IQ4_XS,
@@ -158,7 +192,7 @@ def moe_ffn_full(x, x_dtype, ids, weights, e, dff, w_gate_up, w_down, scheme_gu=
     k = ids.shape[1]
     y = np.empty((t, dm), dtype=np.float32)
     _check(lib().rxo_moe_ffn_full(x_dtype, _p(x), t, dm, dff, e, k, _p(ids), _p(weights),
-                                  scheme_gu, _p(np.ascontiguousarray(w_gate_up)), scheme_dn,
+                                  _gg(scheme_gu), _p(np.ascontiguousarray(w_gate_up)), _gg(scheme_dn),
                                   _p(np.ascontiguousarray(w_down)), _p(y)), "moe_ffn_full")
     return y
 
@@ -168,8 +202,8 @@ def expert_ffn(x, x_dtype, dff, w_gate_up, w_down, scheme_gu=IQ4_XS, scheme_dn=Q
     x = np.ascontiguousarray(x)
     rows, dm = x.shape
     out = np.empty((rows, dm), dtype=np.float32)
-    _check(lib().rxo_expert_ffn(x_dtype, _p(x), rows, dm, dff, scheme_gu,
-                                _p(np.ascontiguousarray(w_gate_up)), scheme_dn,
+    _check(lib().rxo_expert_ffn(x_dtype, _p(x), rows, dm, dff, _gg(scheme_gu),
+                                _p(np.ascontiguousarray(w_gate_up)), _gg(scheme_dn),
                                 _p(np.ascontiguousarray(w_down)), int(h_bf16), _p(out)),
            "expert_ffn")
     return out
@@ -182,7 +216,7 @@ def moe_expert(x, x_dtype, tokens, dff, gu_expert, dn_expert, scheme_gu=IQ4_XS, 
     dm = x.shape[1]
     tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
     out = np.empty((len(tokens), dm), dtype=np.float32)
-    _check(lib().rxo_moe_expert_mt(x_dtype, _p(x), _p(tokens), len(tokens), dm, dff, scheme_gu,
-                                   _p(np.ascontiguousarray(gu_expert)), scheme_dn,
+    _check(lib().rxo_moe_expert_mt(x_dtype, _p(x), _p(tokens), len(tokens), dm, dff, _gg(scheme_gu),
+                                   _p(np.ascontiguousarray(gu_expert)), _gg(scheme_dn),
                                    _p(np.ascontiguousarray(dn_expert)), _p(out), threads), "moe_expert")
     return out

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), n
     assert sorted(n for n, _, _ in ffi.EXPORTS) == names
-    assert lib.r9vx_abi_version() == 2
+    assert lib.r9vx_abi_version() == 3
 
 
 def kgen_layout(fields):
@@ -47,14 +47,18 @@ def kgen_layout(fields):
     return offs, (off + maxal - 1) // maxal * maxal
 
 
-# Key declaration order of MatmulStatic / MoeFfnStatic
-# (crates/r9v-registry/src/types.rs:727-770, 801-860), u32 each.
+# Key declaration order of MatmulStatic / MoeRouteStatic / MoeFfnStatic
+# (crates/r9v-registry/src/types.rs:727-770, 774-800, 801-860), u32 each;
+# MoeRouteStatic.group (Option<MoeGroup {n_group, topk_group}>) sits between
+# renormalize and scale_bits.
 STATICS = {
     "r9vx_matmul_static": ["m_bucket", "n", "k", "w_dtype", "w_scheme", "w_layout", "in_dtype", "act_scheme",
                            "out_dtype", "epilogue", "residual_dtype", "transpose_w", "interleave", "sparse"],
     "r9vx_moe_ffn_static": ["t_bucket", "e_local", "k_topk", "dm", "dff", "gate_up.dtype", "gate_up.scheme",
                             "gate_up.layout", "down.dtype", "down.scheme", "down.layout", "in_dtype", "act_scheme",
                             "act", "out_dtype", "shared_experts", "placement_kind"],
+    "r9vx_moe_route_static": ["t_bucket", "e_total", "top_k", "scoring", "renormalize", "n_group", "topk_group",
+                              "scale_bits", "has_bias"],
 }
 
 
@@ -79,6 +83,62 @@ def test_static_structs_follow_the_registry_key_order(tmp_path):
             assert got[(st, name)] == 4 * i, (st, name)
     assert ctypes.sizeof(ffi.MatmulStatic) == got[("r9vx_matmul_static", "size")]
     assert ctypes.sizeof(ffi.MoeFfnStatic) == got[("r9vx_moe_ffn_static", "size")]
+    assert ctypes.sizeof(ffi.MoeRouteStatic) == got[("r9vx_moe_route_static", "size")]
+    for st, cls in (("r9vx_matmul_static", ffi.MatmulStatic), ("r9vx_moe_route_static", ffi.MoeRouteStatic)):
+        for name in STATICS[st]:
+            assert getattr(cls, name).offset == got[(st, name)], (st, name)
+
+
+# SchemeId::code (crates/r9v-format/src/scheme.rs:115-138) of every scheme, and
+# the GGUF type ids the reference keeps out of that code space (:78-87).
+SCHEME_IDS = {"I4K": 3, "I8B32F": 5, "I6K": 11, "I4Xs": 15, "Iq3S": 17}
+GGML_IDS = {"Q4_K": 12, "Q8_0": 8, "Q6_K": 14, "IQ4_XS": 23, "IQ3_S": 21}
+
+
+def test_statics_carry_scheme_id_codes():
+    """w_scheme / proj.scheme are SchemeId codes: the five this path reads
+    are accepted, and the codes that are GGUF ids of the same formats -- 8, 12,
+    14, 21 -- are refused, being SchemeId codes of other schemes (I5B32F,
+    I3K, I4Nl, Iq1S) that a registry would pass for those; so is 23 (no
+    scheme).  The GGUF type -> scheme translation is the reference's."""
+    assert (ffi.Q4_K, ffi.Q8_0, ffi.Q6_K, ffi.IQ4_XS, ffi.IQ3_S) == tuple(SCHEME_IDS.values())
+    lib = ffi.load()
+    for name, code in GGML_IDS.items():
+        assert lib.r9vx_scheme_from_ggml_type(code) == getattr(ffi, name)
+    for code in (0, 1, 2, 4, 6, 7, 9, 10, 13, 16, 18, 19, 20, 22, 24, 30, 1001):
+        assert lib.r9vx_scheme_from_ggml_type(code) == 0, code
+    args = ffi.MatmulArgs()
+    args.m = 1
+    fargs = ffi.MoeFfnArgs()
+    fargs.t = 1
+    for code in (8, 12, 14, 21, 23):
+        st = ffi.matmul_static(n=64, k=512, w_scheme=ffi.Q4_K, in_dtype=ffi.BF16, out_dtype=ffi.F32)
+        st.w_scheme = code
+        assert _call(lib.r9vx_matmul_launch, st, args) == -2, code
+        assert f"w_scheme {code} is not the SchemeId code" in lib.r9vx_last_error().decode()
+        fst = ffi.ffn_static(t_bucket=4, e=4, k=2, dm=256, dff=256)
+        fst.gate_up.scheme = code
+        fst.down.scheme = code
+        assert _call(lib.r9vx_moe_ffn_launch, fst, fargs) < 0, code
+        msg = lib.r9vx_last_error().decode()
+        assert f"gate_up scheme {code}:" in msg and f"down scheme {code}:" in msg, msg
+        assert lib.r9vx_dequantize_launch(code, None, 0, 256, None, None) == -2
+    for code in SCHEME_IDS.values():  # accepted: only the missing operands are refused
+        st = ffi.matmul_static(n=64, k=512, w_scheme=code, in_dtype=ffi.BF16, out_dtype=ffi.F32)
+        assert _call(lib.r9vx_matmul_launch, st, args) == -3, code
+        assert "w_scheme" not in lib.r9vx_last_error().decode()
+
+
+def test_route_static_group_key_is_refused():
+    lib = ffi.load()
+    args = ffi.MoeRouteArgs()
+    args.t = 1
+    for n_group, topk_group in ((4, 2), (0, 1)):
+        st = ffi.route_static(e=64, k=4, t_bucket=1)
+        st.n_group, st.topk_group = n_group, topk_group
+        assert _call(lib.r9vx_moe_route_launch, st, args) == -2
+        assert f"grouped expert routing (n_group {n_group}, topk_group {topk_group})" in \
+            lib.r9vx_last_error().decode()
 
 
 def test_reference_layouts_and_keys_are_refused():
@@ -297,7 +357,7 @@ def test_route_hidden_refusals():
     args.dm = 100
     assert _call(lib.r9vx_moe_route_hidden_launch, st, args) < 0
     msg = lib.r9vx_last_error().decode()
-    for part in ("decode form (t <= 8)", "dm=100", "x, w_router", "workspace of"):
+    for part in ("decode form (t_bucket <= 8)", "dm=100", "x, w_router", "workspace of"):
         assert part in msg, msg
     assert lib.r9vx_moe_route_hidden_workspace_bytes(ctypes.byref(st)) == 16 * 512 * 4 + 256
 

@@ -422,7 +422,8 @@ def test_matmul_and_moe_ffn_statics_from_a_checkpoint():
         f.matmul_static("absent")
     s = f.moe_ffn_static("blk.0.ffn_gate_exps.weight", "blk.0.ffn_up_exps.weight",
                          "blk.0.ffn_down_exps.weight", t_bucket=8, k=2)
-    assert (s.e_local, s.dm, s.dff, s.gate_up.scheme, s.down.scheme, s.k_topk) == (3, 512, 256, 23, 12, 2)
+    # the file's GGUF types IQ4_XS (23) and Q4_K (12) become SchemeId codes I4Xs (15) and I4K (3)
+    assert (s.e_local, s.dm, s.dff, s.gate_up.scheme, s.down.scheme, s.k_topk) == (3, 512, 256, 15, 3, 2)
     fused = f.moe_ffn_static("blk.0.ffn_gate_up_exps.weight", None, "blk.0.ffn_down_exps.weight", 8, 2)
     assert (fused.e_local, fused.dm, fused.dff) == (3, 512, 256)
     with pytest.raises(gguf.GgufError, match="must agree in dims and type"):

@@ -211,15 +211,18 @@ def _gemm_case(scheme, n, k, m, seed, out_dtype=O.F32, bias=False, residual=Fals
     return got[np.ix_(rows, cols)], ref
 
 
-def test_gemm_config2_sampled():
-    """x bf16 [2048 x 4096] . Q4_K [14336 x 4096]^T -> bf16, full
-    launch; 48 rows (every M tile, tile edges) x 1536 columns checked."""
+def test_gemm_config2_full():
+    """x bf16 [2048 x 4096] . Q4_K [14336 x 4096]^T -> bf16; every
+    one of the 2048 x 14336 outputs against the oracle (its OpenMP form on
+    all host threads, bit-identical to the serial one)."""
     m, n, k = 2048, 14336, 4096
-    rows = np.unique(np.concatenate([np.arange(0, m, 97), [0, 1, 255, 256, 1023, 2047]]))
-    cols = np.unique(np.concatenate([np.arange(0, n, 11)[:1500], [0, 255, 256, 14335, 7000]]))
-    got, ref = _gemm_case(O.Q4_K, n, k, m, 7000, out_dtype=O.BF16, rows=rows, cols=cols)
-    got32, _ = _gemm_case(O.Q4_K, n, k, m, 7000, out_dtype=O.F32, rows=rows, cols=cols, oracle=False)
-    check_bf16_out(got, got32, ref, "config2 sampled")
+    w = synth.quant_weights(O.Q4_K, 7001, n, k)
+    x = synth.normal_bf16(7002, (m, k))
+    wd, xd = dev(w), bf16_dev(x)
+    got = host(ffi.matmul(wd, O.Q4_K, n, k, xd, out_dtype=O.BF16).float())
+    got32 = host(ffi.matmul(wd, O.Q4_K, n, k, xd, out_dtype=O.F32))
+    ref = O.matmul(O.Q4_K, w, n, k, x, O.BF16, threads=O.host_threads())
+    check_bf16_out(got, got32, ref, "config2 full")
 
 
 @pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])

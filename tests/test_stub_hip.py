@@ -80,7 +80,7 @@ def test_no_device_paths_return_hip_errors(tmp_path):
     stub = _stub(tmp_path)
     out = _child(stub, NO_DEVICE)
     assert out["hip"] == [str(stub / "libamdhip64.so.7")]  # the stand-in, not the installed runtime
-    assert out["abi"] == 2
+    assert out["abi"] == 3
     for op in ("matmul", "route", "route_ex", "ffn", "ffn_status", "ffn_noalloc"):
         rc, msg = out[op][:2]
         assert rc == 100, (op, rc, msg)
