@@ -154,9 +154,12 @@ def host_cpu():
 
 
 def oracle():
+    """The CPU oracle in T0's own loop structure (one row at a time through
+    each dot), which is what the CPU baseline times."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_ffi as O
 
+    O.set_rows_at_once(1)
     return O
 
 

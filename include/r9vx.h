@@ -27,8 +27,9 @@
  *    nothing.  Each launch owns its status word: moe_ffn's lives in its
  *    workspace, r9vx_moe_route_launch_ex takes one from the caller, and
  *    r9vx_moe_route_hidden_launch keeps one in its workspace.  The plain
- *    r9vx_moe_route_launch uses one word per device shared by every plain
- *    launch, so concurrent routings on different streams must use the _ex form.
+ *    r9vx_moe_route_launch uses a word of the library's per stream (up to 64
+ *    streams per device), so routings on different streams do not share one;
+ *    launches on one stream are ordered and each overwrites it.
  */
 #ifndef R9VX_H
 #define R9VX_H
@@ -234,7 +235,10 @@ int r9vx_moe_route_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_
 int r9vx_moe_route_launch_ex(const r9vx_moe_route_static *st, const r9vx_moe_route_args *args,
                              uint32_t *status, r9vx_stream_t stream);
 /* Synchronises `stream`, returns the status bits of the last plain
- * r9vx_moe_route_launch on this device in *status and clears them. */
+ * r9vx_moe_route_launch on `stream` in *status (0 when none ran there) and
+ * clears them.  Each stream has its own word (the library's, assigned on the
+ * stream's first plain launch; a 65th stream of one device is refused with
+ * R9VX_ERR_UNSUPPORTED and must use the _ex form). */
 int r9vx_moe_route_status(uint32_t *status, r9vx_stream_t stream);
 /* Copies a device status word (of r9vx_moe_route_launch_ex) to *status after
  * synchronising `stream`. */

@@ -278,6 +278,11 @@ static inline void write_y(int y_dtype, void *y, uint64_t i, float v) {
         ((float *)y)[i] = v;
 }
 
+/* Rows per pass of dot_rows: 4 (the checker's default) or 1 (T0's own loop,
+ * one row at a time; bench.py times the CPU baseline in this form). */
+static int g_rows_at_once = 4;
+void rxo_set_rows_at_once(int n) { g_rows_at_once = n == 1 ? 1 : 4; }
+
 /* Branch D's dot (crates/r9v-t0/src/matmul.rs:1940-2414): per output one
  * f32 accumulator from 0, k ascending, prod = x * w rounded, then acc +=
  * prod rounded.  `rows` x rows (stride `xs` floats) against one decoded weight
@@ -286,7 +291,7 @@ static inline void write_y(int y_dtype, void *y, uint64_t i, float v) {
 static void dot_rows(const float *x, uint32_t rows, uint64_t xs, const float *w, uint32_t k, float *out,
                      uint64_t os) {
     uint32_t r = 0;
-    for (; r + 4 <= rows; r += 4) {
+    for (; g_rows_at_once == 4 && r + 4 <= rows; r += 4) {
         const float *x0 = x + r * xs, *x1 = x0 + xs, *x2 = x1 + xs, *x3 = x2 + xs;
         float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
         for (uint32_t kk = 0; kk < k; ++kk) {

@@ -93,6 +93,9 @@ void rxo_act_mul_silu(const float *g, const float *u, uint64_t n, float *y);
 /* Reference glibc expf (the host libm the Rust T0 f32::exp resolves to). */
 float rxo_expf(float x);
 void rxo_expf_fill(uint32_t first_bits, uint64_t n, float *out);
+/* Rows per pass of the matmul / expert dots: 4 (default) or 1 (T0's loop
+ * structure).  Outputs are bit-identical either way; only speed differs. */
+void rxo_set_rows_at_once(int n);
 /* moe_route with softmax scoring (scoring 0) or sigmoid (scoring 1). */
 int rxo_moe_route(const float *logits, const float *bias, uint32_t t, uint32_t e,
                   uint32_t k, float scale, int renormalize, int scoring,

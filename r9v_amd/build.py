@@ -93,31 +93,39 @@ def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
+def _inputs_stamp(src: pathlib.Path) -> float:
+    """Newest modification time of the source and every header it could include."""
+    return max(p.stat().st_mtime for p in [src, *CSRC.glob("*.h"), *(ROOT / "include").glob("*.h")])
+
+
 def _compile(src: pathlib.Path):
     obj = BUILD / (src.stem + ".o")
+    stamp = _inputs_stamp(src)  # taken before the compiler reads the inputs
     cmd = [HIPCC, *FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError(f"hipcc failed on {src.name}")
     res = parse_resources(r.stderr)
-    obj.with_suffix(".res").write_text(json.dumps(res))
+    obj.with_suffix(".res").write_text(json.dumps({"stamp": stamp, "res": res}))
     return obj, res
 
 
 def _up_to_date(src: pathlib.Path) -> bool:
-    """The object and its resource report are newer than the source and
-    every header it could include."""
+    """The object was compiled from inputs no older than the current ones."""
     obj, res = BUILD / (src.stem + ".o"), BUILD / (src.stem + ".res")
     if not (obj.exists() and res.exists()):
         return False
-    newest = max(p.stat().st_mtime for p in [src, *CSRC.glob("*.h"), *(ROOT / "include").glob("*.h")])
-    return min(obj.stat().st_mtime, res.stat().st_mtime) > newest
+    try:
+        stamp = json.loads(res.read_text())["stamp"]
+    except (ValueError, KeyError, TypeError):
+        return False
+    return _inputs_stamp(src) <= stamp
 
 
 def _reuse(src: pathlib.Path):
     obj = BUILD / (src.stem + ".o")
-    return obj, json.loads(obj.with_suffix(".res").read_text())
+    return obj, json.loads(obj.with_suffix(".res").read_text())["res"]
 
 
 def build(verbose: bool = True, changed_only: bool = False) -> pathlib.Path:

@@ -380,8 +380,12 @@ uint32_t device_simds();
 
 template <int SCHEME>
 int launch_gated_scheme(const GemvArgs &a, uint32_t m, int spl, uint32_t g, hipStream_t s) {
-    if (a.n >= 8 * device_simds())
-        return spl == 2 ? launch_gated<SCHEME, 2, 2, 4>(a, m, g, s) : launch_gated<SCHEME, 1, 2, 8>(a, m, g, s);
+    /* IQ3_S carries a wider chunk (payload, signs and side word): two row
+     * pairs at M >= 6 need more registers than a wave has at two waves per
+     * SIMD and the compiler moves arrays to scratch, so those run one pair */
+    constexpr int kTwoPairMaxM = SCHEME == R9VX_SCHEME_IQ3_S ? 5 : 8;
+    if (a.n >= 8 * device_simds() && (int)m <= kTwoPairMaxM)
+        return spl == 2 ? launch_gated<SCHEME, 2, 2, 4>(a, m, g, s) : launch_gated<SCHEME, 1, 2, kTwoPairMaxM>(a, m, g, s);
     return spl == 2 ? launch_gated<SCHEME, 2, 1, 4>(a, m, g, s) : launch_gated<SCHEME, 1, 1, 8>(a, m, g, s);
 }
 

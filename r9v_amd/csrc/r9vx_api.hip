@@ -386,7 +386,14 @@ static int route_launch(const char *op, const r9vx_moe_route_static *st, const r
     r9vx_route_problem p{a->logits, a->bias,        a->expert_ids, a->weights,
                          status,   a->t,           st->e_total,   st->top_k,
                          st->scoring, st->renormalize ? 1u : 0u, scale};
-    return hip_status(op, r9vx_launch_route(p, reinterpret_cast<hipStream_t>(stream)));
+    bool no_word = false;
+    rc = r9vx_launch_route(p, reinterpret_cast<hipStream_t>(stream), &no_word);
+    if (no_word) {
+        pr.add(R9VX_ERR_UNSUPPORTED, "plain launches on more than %u streams of one device: use "
+               "r9vx_moe_route_launch_ex with a status word of the caller's", r9vx_route_stream_words());
+        return pr.finish(op);
+    }
+    return hip_status(op, rc);
 }
 
 int r9vx_moe_route_launch(const r9vx_moe_route_static *st, const r9vx_moe_route_args *a,

@@ -120,11 +120,15 @@ struct r9vx_route_problem {
     const float *bias;
     uint32_t *ids;
     float *weights;
-    uint32_t *status; /* the launch's status word; NULL = the device's plain-launch word */
+    uint32_t *status; /* the launch's status word; NULL = the plain-launch word of the stream */
     uint32_t t, e, k, scoring, renormalize;
     float scale;
 };
-int r9vx_launch_route(const r9vx_route_problem &p, hipStream_t stream);
+/* *no_word is set when a plain launch (status NULL) finds every per-stream
+ * status word of the device taken by other streams. */
+int r9vx_launch_route(const r9vx_route_problem &p, hipStream_t stream, bool *no_word = nullptr);
+/* Streams per device that can make plain moe_route launches. */
+uint32_t r9vx_route_stream_words();
 
 struct r9vx_route_hidden_problem {
     const uint16_t *x; /* bf16 [t, dm] */

@@ -21,6 +21,7 @@
  * the workspace's (routing from hidden states) or, for the plain launch, one
  * library word per device.  T <= 8 runs both passes in one workgroup, one wave per row.
  */
+#include <map>
 #include <mutex>
 
 #include "r9vx_device.h"
@@ -29,8 +30,11 @@
 
 namespace {
 
-/* The status word of plain r9vx_moe_route_launch calls on this device. */
-__device__ uint32_t g_route_status;
+/* The status words of plain r9vx_moe_route_launch calls on this device: one
+ * per stream that has made such a call (slot assigned on the stream's first
+ * call, at most kRouteStreamWords streams per device). */
+constexpr uint32_t kRouteStreamWords = 64;
+__device__ uint32_t g_route_status[kRouteStreamWords];
 
 constexpr int kMaxK = 32;
 
@@ -642,12 +646,15 @@ static int launch_route_per(const RouteArgs &a, hipStream_t stream) {
     return (int)hipGetLastError();
 }
 
-/* Device address of this device's plain-launch status word, looked up once
- * per device. */
-/* The current device's plain status word, or nullptr with *err set. */
-static uint32_t *plain_status_word(hipError_t *err) {
-    static uint32_t *words[64];
-    static std::mutex mu;
+/* The plain-launch status word of `stream` on the current device: the
+ * device array's address is looked up once per device, and a stream gets
+ * the next free slot on its first call.  nullptr with *err set when the
+ * device cannot be queried, or with *full set when every slot is taken. */
+static std::mutex g_word_mu;
+static uint32_t *g_words[64];
+static std::map<hipStream_t, uint32_t> g_word_slot[64];
+
+static uint32_t *stream_status_word(hipStream_t stream, bool assign, hipError_t *err, bool *full) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e == hipSuccess && (dev < 0 || dev >= 64)) e = hipErrorInvalidDevice;
@@ -655,23 +662,39 @@ static uint32_t *plain_status_word(hipError_t *err) {
         *err = e;
         return nullptr;
     }
-    std::lock_guard<std::mutex> g(mu);
-    if (!words[dev]) {
+    std::lock_guard<std::mutex> g(g_word_mu);
+    if (!g_words[dev]) {
         void *ptr = nullptr;
         e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_route_status));
         if (e != hipSuccess || !ptr) {
             *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
             return nullptr;
         }
-        words[dev] = static_cast<uint32_t *>(ptr);
+        g_words[dev] = static_cast<uint32_t *>(ptr);
     }
-    return words[dev];
+    auto &slots = g_word_slot[dev];
+    auto it = slots.find(stream);
+    if (it != slots.end()) return g_words[dev] + it->second;
+    if (!assign) return nullptr; /* no plain launch on this stream yet */
+    if (slots.size() >= kRouteStreamWords) {
+        *full = true;
+        return nullptr;
+    }
+    const uint32_t slot = (uint32_t)slots.size();
+    slots.emplace(stream, slot);
+    return g_words[dev] + slot;
 }
 
-int r9vx_launch_route(const r9vx_route_problem &p, hipStream_t stream) {
+uint32_t r9vx_route_stream_words() { return kRouteStreamWords; }
+
+int r9vx_launch_route(const r9vx_route_problem &p, hipStream_t stream, bool *no_word) {
     hipError_t err = hipSuccess;
-    uint32_t *status = p.status ? p.status : plain_status_word(&err);
-    if (!status) return (int)err;
+    bool full = false;
+    uint32_t *status = p.status ? p.status : stream_status_word(stream, true, &err, &full);
+    if (!status) {
+        if (full && no_word) *no_word = true;
+        return full ? (int)hipErrorOutOfMemory : (int)err;
+    }
     RouteArgs a{p.logits, p.bias, p.ids, p.weights, status, p.t, p.e, p.k, p.scoring, p.renormalize, p.scale};
     /* registers per lane: the next power of two >= ceil(E / 64) */
     const uint32_t per = (p.e + 63) / 64;
@@ -683,14 +706,18 @@ int r9vx_launch_route(const r9vx_route_problem &p, hipStream_t stream) {
 }
 
 int r9vx_read_route_status(uint32_t *status, hipStream_t stream) {
-    int rc = (int)hipMemcpyFromSymbolAsync(status, HIP_SYMBOL(g_route_status), sizeof(uint32_t), 0,
-                                           hipMemcpyDeviceToHost, stream);
+    hipError_t err = hipSuccess;
+    bool full = false;
+    uint32_t *word = stream_status_word(stream, false, &err, &full);
+    if (!word) {
+        if (err != hipSuccess) return (int)err;
+        *status = 0u; /* no plain launch on this stream: nothing refused */
+        return (int)hipStreamSynchronize(stream);
+    }
+    int rc = (int)hipMemcpyAsync(status, word, sizeof(uint32_t), hipMemcpyDeviceToHost, stream);
     if (rc) return rc;
     rc = (int)hipStreamSynchronize(stream);
     if (rc) return rc;
-    hipError_t err = hipSuccess;
-    uint32_t *word = plain_status_word(&err);
-    if (!word) return (int)err;
     hipLaunchKernelGGL(clear_status_kernel, dim3(1), dim3(1), 0, stream, word);
     return (int)hipGetLastError();
 }

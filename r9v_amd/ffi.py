@@ -323,7 +323,7 @@ def moe_route(logits, k, bias=None, scoring=SCORING_SOFTMAX, renormalize=True, s
               ids=None, weights=None, stream=None, status=None):
     """T0 moe_route; with `status` (a device int32 tensor of one element) the
     launch owns that status word (r9vx_moe_route_launch_ex), otherwise the
-    device's shared plain-launch word (read with moe_route_status)."""
+    stream's plain-launch word (read with moe_route_status(stream))."""
     torch = _need_gpu(logits, bias, status)
     t, e = logits.shape
     if ids is None:

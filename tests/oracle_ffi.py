@@ -50,6 +50,8 @@ def lib():
         L.rxo_expf.restype = ctypes.c_float
         L.rxo_expf_fill.argtypes = [U, ctypes.c_uint64, P]
         L.rxo_expf_fill.restype = None
+        L.rxo_set_rows_at_once.argtypes = [I]
+        L.rxo_set_rows_at_once.restype = None
         L.rxo_q4k_unpack_scales.argtypes = [P, P, P]
         L.rxo_dequantize.argtypes = [I, P, U, U, P]
         L.rxo_matmul.argtypes = [I, P, U, U, I, P, U, P, P, I, P]
@@ -82,6 +84,13 @@ class OracleError(RuntimeError):
 def _check(rc, what):
     if rc != 0:
         raise OracleError(rc, what)
+
+
+def set_rows_at_once(n):
+    """1: the dots walk one row at a time, as T0's loop does (the CPU
+    baseline's timing form); 4 (default): four rows per pass over k.  The
+    outputs are bit-identical."""
+    lib().rxo_set_rows_at_once(n)
 
 
 def expf_fill(first_bits, n, out=None):

@@ -352,3 +352,31 @@ def test_route_status_words_are_per_launch(t):
     rid, rw = O.moe_route(good, 4)
     assert np.array_equal(host(ids2).view(np.uint32), rid.astype(np.uint32))
     assert np.array_equal(host(wt2).view(np.uint32), rw.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", [5, 300])
+def test_plain_route_status_words_are_per_stream(t):
+    """The plain launch on two streams: each stream's word reports its own
+    routing (NONFINITE where a row holds a NaN, 0 on the other), reading a
+    word clears it, and a stream with no plain launch reads 0."""
+    bad = synth.normal_f32(921, (t, 64))
+    bad[t // 2, 3] = np.inf
+    good = synth.normal_f32(922, (t, 64))
+    s1, s2, s3 = torch.cuda.Stream(), torch.cuda.Stream(), torch.cuda.Stream()
+    ids1 = torch.full((t, 4), 77, dtype=torch.int32, device="cuda")
+    wt1 = torch.full((t, 4), -1.0, dtype=torch.float32, device="cuda")
+    ids2 = torch.empty((t, 4), dtype=torch.int32, device="cuda")
+    wt2 = torch.empty((t, 4), dtype=torch.float32, device="cuda")
+    lb, lg = dev(bad), dev(good)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        ffi.moe_route(lb, 4, ids=ids1, weights=wt1, stream=s1)
+        ffi.moe_route(lg, 4, ids=ids2, weights=wt2, stream=s2)
+    assert ffi.moe_route_status(stream=s1) == ffi.STATUS_NONFINITE
+    assert ffi.moe_route_status(stream=s2) == 0
+    assert ffi.moe_route_status(stream=s1) == 0  # read and cleared
+    assert ffi.moe_route_status(stream=s3) == 0  # never used
+    assert (host(ids1) == 77).all() and (host(wt1) == -1.0).all()
+    rid, rw = O.moe_route(good, 4)
+    assert np.array_equal(host(ids2).view(np.uint32), rid.astype(np.uint32))
+    assert np.array_equal(host(wt2).view(np.uint32), rw.view(np.uint32))
