@@ -16,7 +16,14 @@
  *          from the scaled fp16 activations by the permutation (no permuted
  *          copy of x).
  *  h16   : each h row scaled by the power of two that brings max|h| below
- *          2^15 and rounded to fp16, in the down weights' K group order.
+ *          2^15 and rounded to fp16, in the down weights' K group order.  The
+ *          256-row gate/up writes it directly, each 128-column block at its
+ *          own scale (max|block| below 2^15), and the 256-row down GEMM
+ *          rescales its f32 accumulators by the exponent step at each block
+ *          boundary; for the LDS-decoded down kernels h_fix_kernel first
+ *          brings a row's blocks to the row's scale.  The 128-row
+ *          LDS-decoded gate/up writes f32 h, which h_to_f16_kernel converts
+ *          at one scale per row.
  *  down  : a workgroup owns 256 rows x 256 output columns of o; the scale is
  *          undone on the f32 accumulators.
  * Both GEMMs run the main loop of r9vx_mma3.h (weights decoded once per
@@ -48,6 +55,7 @@ struct GroupedArgs {
     uint64_t gu_row_bytes, dn_row_bytes;
     uint32_t gu_srow, dn_srow; /* f16 d values per weight row */
     uint32_t t, e, k, dm, dff, p, shared;
+    uint32_t h_order; /* K order of the h16 rows: the down scheme for the group orders, 0 natural */
 };
 
 __device__ __forceinline__ const uint32_t *ws_u32(const GroupedArgs &a, uint64_t off) {
@@ -152,10 +160,10 @@ __global__ __launch_bounds__(256, 2) void moe_gu_lds_kernel(GroupedArgs a) {
 
 /* ---------------------------------------------------------------- h -> fp16 */
 
-/* One wave per h row: max|h| over the row (kept in hmax for the down GEMM's
- * epilogue), then lane l writes group l % 8 of K step l / 8 (+ 8 per pass)
- * as 8 fp16 in the down scheme's group order, scaled by 2^-e with e =
- * row_shift(max|h|). */
+/* One wave per h row: max|h| over the row, e = row_shift(max|h|) (kept in
+ * hexp and hbe for the down GEMMs), then lane l writes group l % 8 of K
+ * step l / 8 (+ 8 per pass) as 8 fp16 in the down scheme's group order,
+ * scaled by 2^-e. */
 /* K position of element i of group q in a 64-wide step of the h16 rows: the
  * group order of the r9vx_mma3.h schemes, natural order for the others. */
 template <int DN>
@@ -164,6 +172,14 @@ __device__ __forceinline__ uint32_t h_group_k(uint32_t q, uint32_t i) {
         return group_k<DN>(q, i);
     else
         return 8 * q + i;
+}
+
+/* A row converted at one scale 2^-e: e goes to hexp and to each of its
+ * blocks' hbe entries (the 256-row down GEMM reads those). */
+__device__ __forceinline__ void put_row_exp(const GroupedArgs &a, uint32_t row, int e, uint32_t lane) {
+    const uint32_t nb = a.dff / 128, stride = r9vx_moe_hbe_stride(a.dff);
+    if (lane == 0) reinterpret_cast<int32_t *>(a.ws + a.L.hexp)[row] = e;
+    for (uint32_t b = lane; b < nb; b += 64) reinterpret_cast<int8_t *>(a.ws + a.L.hbe)[(uint64_t)row * stride + b] = (int8_t)e;
 }
 
 template <int DN>
@@ -194,7 +210,7 @@ __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t n
                                  fmaxf(fmaxf(fabsf(hi[i].x), fabsf(hi[i].y)), fmaxf(fabsf(hi[i].z), fabsf(hi[i].w)))));
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-        if (lane == 0) reinterpret_cast<uint32_t *>(a.ws + a.L.hmax)[row] = __builtin_bit_cast(uint32_t, mx);
+        put_row_exp(a, row, row_shift(mx), lane);
         const float inv = ldexpf(1.0f, -row_shift(mx));
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -213,7 +229,7 @@ __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t n
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    if (lane == 0) reinterpret_cast<uint32_t *>(a.ws + a.L.hmax)[row] = __builtin_bit_cast(uint32_t, mx);
+    put_row_exp(a, row, row_shift(mx), lane);
     const float inv = ldexpf(1.0f, -row_shift(mx));
     for (uint32_t c = lane; c < a.dff / 8; c += 64) {
         const uint32_t base = (c >> 3) * 64, q = c & 7;
@@ -222,6 +238,66 @@ __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t n
         *reinterpret_cast<r9vx_u32x4 *>(orow + 8 * c) =
             r9vx_u32x4{pack_h2(lo.x * inv, lo.y * inv), pack_h2(lo.z * inv, lo.w * inv), pack_h2(hi.x * inv, hi.y * inv),
                        pack_h2(hi.z * inv, hi.w * inv)};
+    }
+}
+
+/* 4-byte load into a register that a later main loop's counted wait
+ * covers (it is issued before that loop's loads); the destination is tied
+ * in and out, and the reader touches it after that wait. */
+__device__ __forceinline__ void ld_ahead(uint32_t &d, const void *p) {
+    asm volatile("global_load_dword %0, %1, off" : "+v"(d) : "v"(p) : "memory");
+}
+
+/* x of the lane that DPP control CTRL names (within a row of 16 lanes). */
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+/* The 4-element chunk (K offset / 4 within a 64-wide step) that holds
+ * elements i .. i + 3 (i = 0 or 4) of group q of an h16 row in order
+ * `order` (h_group_k's orders, chosen at run time). */
+__device__ __forceinline__ uint32_t h_chunk(uint32_t order, uint32_t q, uint32_t i) {
+    if (order == R9VX_SCHEME_Q4_K) return group_k<R9VX_SCHEME_Q4_K>(q, i) / 4;
+    if (order == R9VX_SCHEME_IQ4_XS) return group_k<R9VX_SCHEME_IQ4_XS>(q, i) / 4;
+    return (8 * q + i) / 4;
+}
+
+/* After the 256-row gate/up GEMM, for the down kernels that undo one
+ * power-of-two scale per h16 row (the LDS-decoded ones, and the 256-row one
+ * past kM3MaxBlk blocks): gives each row that scale.  The row's e is the
+ * largest of its blocks' (hbe; row_shift is monotonic, so it is row_shift of
+ * the row's max|h|) and goes to hexp.  Each block at a smaller e is
+ * multiplied by 2^(e_block - e_row), a power of two below 1 -- exact unless
+ * a value lands in fp16's subnormal range, where it is rounded a second
+ * time -- and its hbe entry becomes e_row, so a second pass changes nothing.
+ * Rows whose blocks share one e (every row below 2^15) are only read.  One
+ * thread per row. */
+__global__ __launch_bounds__(256) void h_fix_kernel(GroupedArgs a, uint32_t nrows) {
+    const uint32_t row = blockIdx.x * 256 + threadIdx.x;
+    if (row >= nrows) return;
+    if (ws_u32(a, a.L.status)[0] != 0u) return;
+    const uint32_t nb = a.dff / 128;
+    int8_t *const be = reinterpret_cast<int8_t *>(a.ws + a.L.hbe) + (uint64_t)row * r9vx_moe_hbe_stride(a.dff);
+    int er = be[0];
+    for (uint32_t b = 1; b < nb; ++b) er = be[b] > er ? be[b] : er;
+    reinterpret_cast<int32_t *>(a.ws + a.L.hexp)[row] = er;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const int eb = be[b];
+        if (eb == er) continue;
+        const float f = ldexpf(1.0f, eb - er);
+        r9vx_u32x4 *const blk = reinterpret_cast<r9vx_u32x4 *>(a.h16 + (uint64_t)row * a.dff + 128 * b);
+        for (uint32_t c = 0; c < 16; ++c) {
+            const r9vx_u32x4 v = blk[c];
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                o[j] = pack_h2((float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xFFFFu)) * f,
+                               (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16)) * f);
+            blk[c] = r9vx_u32x4{o[0], o[1], o[2], o[3]};
+        }
+        be[b] = (int8_t)er;
     }
 }
 
@@ -249,8 +325,7 @@ __global__ __launch_bounds__(256, 2) void moe_dn_lds_kernel(GroupedArgs a) {
     const uint32_t n0 = nt * 256;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < kBM)
-        rowsc[tid] = tid < rows ? ldexpf(1.0f, row_shift(__builtin_bit_cast(float, ws_u32(a, a.L.hmax)[pos0 + tid])))
-                                : 0.f;
+        rowsc[tid] = tid < rows ? ldexpf(1.0f, reinterpret_cast<const int32_t *>(a.ws + a.L.hexp)[pos0 + tid]) : 0.f;
     AF16Rows<kBM> as;
     as.chunk = tid & 7;
     as.row0 = tid >> 3;
@@ -366,8 +441,7 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
      * 32 t + (l & 31) and, in acc[t][0][r] / acc[t][1][r], the gate and up
      * values of h column j0 + 32 cq + 8 (r >> 2) + 4 (l >> 5) + (r & 3): four
      * consecutive columns per r >> 2.  The 256 x 128 f32 h tile is staged in
-     * LDS (row R's 16-byte chunk c at chunk c ^ (R & 31)) and leaves as whole
-     * 512-byte rows. */
+     * LDS (row R's 16-byte chunk c at chunk c ^ (R & 31)). */
     uint8_t *const ot = m3_out_tile(sm);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -386,14 +460,39 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
         }
     }
     __syncthreads();
-    float *h = reinterpret_cast<float *>(a.ws + a.L.h);
-    const uint32_t q = lane & 31;
-#pragma unroll 4
-    for (uint32_t i = 0; i < 16; ++i) {
-        const uint32_t R = 16 * i + 2 * wv + (lane >> 5);
-        if (R >= rows) break; /* rows grow with i */
-        const r9vx_f32x4 v = *reinterpret_cast<const r9vx_f32x4 *>(ot + R * 512u + 16u * (q ^ (R & 31u)));
-        *reinterpret_cast<r9vx_f32x4 *>(h + (uint64_t)(pos0 + R) * a.dff + j0 + 4 * q) = v;
+    /* h leaves as fp16 (h16) in the down weights' K order, each (row, 128-
+     * column block) scaled by 2^-row_shift(the block's max|h|), with that max
+     * (its e) beside it (hbe), which the 256-row down GEMM undoes block by block
+     * (h_fix_kernel gives each row one scale for the other down kernels).  16 lanes
+     * take a row: lane g writes granule g & 7 of the block's 64-column step
+     * g >> 3, whose elements 0-3 and 4-7 are two 16-byte chunks of the staged
+     * f32 row. */
+    const uint32_t g = lane & 15, hs = g >> 3, hq = g & 7;
+    const uint32_t c_lo = 16 * hs + h_chunk(a.h_order, hq, 0), c_hi = 16 * hs + h_chunk(a.h_order, hq, 4);
+    int8_t *const hbe = reinterpret_cast<int8_t *>(a.ws + a.L.hbe);
+    const uint32_t hstride = r9vx_moe_hbe_stride(a.dff);
+    /* every row of the stage is converted (rows past the tile's hold stale
+     * values and are not stored), so the 16 lanes of a row reduce by DPP
+     * with the whole row active */
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+        const uint32_t R = 32 * i + 4 * wv + (lane >> 4);
+        const r9vx_f32x4 lo = *reinterpret_cast<const r9vx_f32x4 *>(ot + R * 512u + 16u * (c_lo ^ (R & 31u)));
+        const r9vx_f32x4 hi = *reinterpret_cast<const r9vx_f32x4 *>(ot + R * 512u + 16u * (c_hi ^ (R & 31u)));
+        float mx = fmaxf(fmaxf(fmaxf(fabsf(lo.x), fabsf(lo.y)), fmaxf(fabsf(lo.z), fabsf(lo.w))),
+                         fmaxf(fmaxf(fabsf(hi.x), fabsf(hi.y)), fmaxf(fabsf(hi.z), fabsf(hi.w))));
+        mx = fmaxf(mx, dpp_f32<0xB1>(mx));  /* quad_perm 1,0,3,2 */
+        mx = fmaxf(mx, dpp_f32<0x4E>(mx));  /* quad_perm 2,3,0,1 */
+        mx = fmaxf(mx, dpp_f32<0x141>(mx)); /* row_half_mirror: l <-> 7 - l */
+        mx = fmaxf(mx, dpp_f32<0x140>(mx)); /* row_mirror: l <-> 15 - l */
+        const int e = row_shift(mx);
+        const float inv = ldexpf(1.0f, -e);
+        if (R < rows) {
+            *reinterpret_cast<r9vx_u32x4 *>(a.h16 + (uint64_t)(pos0 + R) * a.dff + j0 + 64 * hs + 8 * hq) =
+                r9vx_u32x4{pack_h2(lo.x * inv, lo.y * inv), pack_h2(lo.z * inv, lo.w * inv),
+                           pack_h2(hi.x * inv, hi.y * inv), pack_h2(hi.z * inv, hi.w * inv)};
+            if (g == 0) hbe[(uint64_t)(pos0 + R) * hstride + nt] = (int8_t)e;
+        }
     }
 }
 
@@ -403,7 +502,8 @@ template <int DN>
 __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     __shared__ __attribute__((aligned(16))) M3Lds sm;
     uint32_t *const lut = sm.lut;
-    __shared__ float rowsc[kMoeTileM3]; /* 2^e that undoes each h row's fp16 scale */
+    __shared__ float rowsc[kMoeTileM3]; /* 2^e that undoes each h row's last block's fp16 scale */
+    __shared__ uint32_t bst[kM3MaxBlk * 64]; /* the rows' exponent steps per 128-K block (m3_bsd) */
     const uint32_t *status = ws_u32(a, a.L.status);
     uint32_t tix, nt;
     xcd_tile(a.dm / 256, tix, nt);
@@ -414,8 +514,46 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
     const uint32_t n0 = nt * 256;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    /* each h row's max, loaded now; its scale goes to LDS after the main loop */
-    const uint32_t hbits = tid < rows && tid < kMoeTileM3 ? ws_u32(a, a.L.hmax)[pos0 + tid] : 0u;
+    /* h16 row r's 128-column block b is at scale 2^-e(b) (hbe).  Thread
+     * r < 256 loads its row's exponents now (ahead of the main loop's loads,
+     * which the loop's prologue waits for first) and then puts the steps
+     * e(b - 1) - e(b) into bst (byte (r >> 5) & 3 of word 64 b + 32 (r >> 7)
+     * + (r & 31); block 0's are 0) and 2^e(last) into rowsc.  Past
+     * kM3MaxBlk blocks h_fix_kernel has given each row one scale: the
+     * steps are 0 and the thread loads the row's e (hexp) instead. */
+    const uint32_t nb = a.dff / 128;
+    const bool ahead = nb <= kM3MaxBlk;
+    uint32_t be0 = 0u, be1 = 0u;
+    if (tid < kMoeTileM3) {
+        const uint64_t row = pos0 + (tid < rows ? tid : 0);
+        if (ahead) {
+            const uint8_t *const berow = a.ws + a.L.hbe + row * r9vx_moe_hbe_stride(a.dff);
+            ld_ahead(be0, berow);
+            if (nb > 4) ld_ahead(be1, berow + 4);
+        } else {
+            ld_ahead(be0, a.ws + a.L.hexp + 4 * row);
+        }
+    }
+    auto fill_steps = [&]() {
+        if (tid >= kMoeTileM3) return;
+        asm volatile("" : "+v"(be0), "+v"(be1));
+        uint8_t *const tb = reinterpret_cast<uint8_t *>(bst) + 4 * (32 * (tid >> 7) + (tid & 31)) + ((tid >> 5) & 3);
+        int eprev = 0;
+        if (ahead) {
+#pragma unroll
+            for (uint32_t b = 0; b < kM3MaxBlk; ++b) {
+                if (b >= nb) break;
+                const int e = tid < rows ? (int)(int8_t)(((b < 4 ? be0 : be1) >> (8 * (b & 3))) & 0xFFu) : 0;
+                tb[256 * b] = (uint8_t)(b == 0 ? 0 : eprev - e);
+                eprev = e;
+            }
+        } else {
+#pragma unroll
+            for (uint32_t b = 0; b < kM3MaxBlk; ++b) tb[256 * b] = 0;
+            eprev = tid < rows ? (int)be0 : 0;
+        }
+        rowsc[tid] = tid < rows ? ldexpf(1.0f, eprev) : 0.f;
+    };
     if constexpr (DN == R9VX_SCHEME_IQ4_XS) m3_init_iq4_lut(lut, tid, 512);
     __syncthreads();
 
@@ -431,8 +569,8 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
-    m3_run<DN, true>(nr, rows <= 128, sm, a.h16, aoff, w, a.dff / kTileK, tid, wv, lut, 128 * rh, 64 * cq, 64 * cq + 32, acc);
-    if (tid < kMoeTileM3) rowsc[tid] = tid < rows ? ldexpf(1.0f, row_shift(__builtin_bit_cast(float, hbits))) : 0.f;
+    m3_run<DN, true, true>(nr, rows <= 128, sm, a.h16, aoff, w, a.dff / kTileK, tid, wv, lut, 128 * rh, 64 * cq,
+                           64 * cq + 32, acc, bst, fill_steps);
     __syncthreads();
 
     /* The tiles are transposed (m3_run<.., true>): lane l holds h row
@@ -514,6 +652,7 @@ static GroupedArgs grouped_args(const r9vx_moe_problem &p, const MoeLayout &L) {
     a.dff = p.dff;
     a.p = p.t * p.k;
     a.shared = p.shared;
+    a.h_order = p.scheme_dn == R9VX_SCHEME_Q4_K || p.scheme_dn == R9VX_SCHEME_IQ4_XS ? p.scheme_dn : 0u;
     return a;
 }
 
@@ -551,7 +690,14 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
     }
     const uint32_t nrows = a.p + p.shared * p.t;
     const dim3 gh((nrows + 3) / 4);
-    if (part == 0) {
+    /* the 256-row gate/up writes h16 at a scale per 128-column block, which
+     * the 256-row down GEMM takes as it is (up to kM3MaxBlk blocks); the
+     * LDS-decoded down kernels take one scale per row */
+    const bool gu_m3 = p.scheme_gu == R9VX_SCHEME_IQ4_XS || p.scheme_gu == R9VX_SCHEME_Q4_K;
+    const bool dn_m3 = p.scheme_dn == R9VX_SCHEME_IQ4_XS || p.scheme_dn == R9VX_SCHEME_Q4_K;
+    if (gu_m3 && (!dn_m3 || p.dff / 128 > kM3MaxBlk) && (part == 0 || part == 1))
+        hipLaunchKernelGGL(h_fix_kernel, dim3((nrows + 255) / 256), dim3(256), 0, s, a, nrows);
+    if (!gu_m3 && part == 0) {
         switch (p.scheme_dn) {
         case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q4_K>, gh, dim3(256), 0, s, a, nrows); break;
         case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, gh, dim3(256), 0, s, a, nrows); break;

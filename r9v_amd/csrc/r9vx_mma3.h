@@ -193,11 +193,11 @@ __device__ __forceinline__ void m3_dec_unit(uint32_t dw, int m, const BScale &sc
  * pair the fragment and codebook reads that run ahead, the pair, and the
  * decode of one or more payload bytes with the writes it completes.
  */
-template <int SCHEME, int KS, int NR, bool TR>
+template <int SCHEME, int KS, int NR, bool TR, bool BSTEP = false>
 __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bsm, uint32_t lane, uint32_t arow0,
                                            uint32_t bc0, uint32_t bc1, r9vx_f32x16 (&acc)[4][2],
                                            const r9vx_u32x4 &pay, const r9vx_u32x4 &hd, uint32_t hh,
-                                           const uint32_t *lut, uint8_t *bdst, uint32_t bsw) {
+                                           const uint32_t *lut, uint8_t *bdst, uint32_t bsw, uint32_t bsd = 0u) {
     constexpr bool kIq4 = SCHEME == R9VX_SCHEME_IQ4_XS;
     constexpr int P = 4 * NR; /* MFMA pairs */
     const uint32_t h = lane >> 5, r32 = lane & 31, sw = m2_swz(r32);
@@ -266,6 +266,18 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
                 if (dec_pair(u) - kLead == i) read_kv(u);
         }
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (BSTEP) {
+            /* a new 128-K block of A rows: tile t's accumulators (lane: one
+             * A row) times 2^(signed byte t of bsd), before its first MFMA of
+             * the step */
+            if (i < NR) {
+                const int d = (int)(int8_t)(uint8_t)(bsd >> (8 * i));
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_amdgcn_ldexpf(acc[i][j][r], d);
+            }
+        }
         if constexpr (TR) { /* operands swapped: the tile of B . A^T */
             acc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[s & 1][0], a[i % (kAhead + 1)], acc[t][0], 0, 0, 0);
             acc[t][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(b[s & 1][1], a[i % (kAhead + 1)], acc[t][1], 0, 0, 0);
@@ -295,6 +307,24 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
     }
 }
 
+/* Block-scale steps (BS): A rows whose 128-K blocks carry their own
+ * power-of-two scales.  bst (LDS) holds, for block b >= 1 and A-row half
+ * rh = arow0 / 128, one word per lane & 31 whose byte t is the exponent
+ * step e(b - 1) - e(b) of A row 128 rh + 32 t + (lane & 31); at the first
+ * step of block b (k = 2b) each tile's accumulators are multiplied by 2^that
+ * before the block's MFMAs, so that after the last block they hold the
+ * product at the last block's scale.  Block 0's words are 0 (no step). */
+constexpr uint32_t kM3MaxBlk = 8; /* blocks with their own words; later blocks read block 0's (no step) */
+template <bool ON>
+__device__ __forceinline__ uint32_t m3_bsd(const uint32_t *bst, uint32_t k, uint32_t arow0, uint32_t lane) {
+    if constexpr (!ON) {
+        return 0u;
+    } else {
+        const uint32_t b = k >> 1;
+        return bst[(b < kM3MaxBlk ? b : 0u) * 64u + (arow0 >> 2) + (lane & 31u)];
+    }
+}
+
 /*
  * The main loop over nk K steps (nk a multiple of 4), with two B tiles and
  * two A stages: one barrier per step.  abase / aoff: the A copy sources
@@ -309,11 +339,11 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
  * of B(k + 1), each of whose four 16-byte granules is written into the other
  * B tile as soon as it is whole, then a wait for the A(k + 1) copy.
  */
-template <int SCHEME, int NR, bool TR>
+template <int SCHEME, int NR, bool TR, bool BS, class Hook>
 __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
                                                const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave,
                                                const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
-                                               r9vx_f32x16 (&acc)[4][2]) {
+                                               r9vx_f32x16 (&acc)[4][2], const uint32_t *bst, Hook &hook) {
     const uint32_t lane = tid & 63, c = m3_brow(tid), hh = tid & 1, bsw = m2_swz(c);
     const uint32_t a_lds = m3_lds_addr(&sm.a[0][0]);
     r9vx_u32x4 pay[4], hnext, hcur;
@@ -327,10 +357,11 @@ __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, co
     m3_load_pay<SCHEME>(w, 1, hh, pay[1]);
     m3_load_pay<SCHEME>(w, 2, hh, pay[2]);
     m3_load_pay<SCHEME>(w, 3 < nk ? 3 : nk - 1, hh, pay[3]);
-    wait_vm<7>(); /* P0, H0 */
+    wait_vm<7>(); /* P0, H0 (and the caller's loads issued before) */
     touch_pay(pay[0]);
     touch_pay(hnext);
     hcur = hnext;
+    hook();
     m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], hcur, hh, lut, sm.b[0] + c * 128u,
                                  bsw);
     wait_vm<2>(); /* A0, P1 */
@@ -351,8 +382,9 @@ __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, co
             touch_pay(hnext);                                                                                \
             hcur = hnext;                                                                                    \
         }                                                                                                    \
-        m3_compute<SCHEME, (J + 1) & 3, NR, TR>(sm.a[k & 1u], sm.b[k & 1u], lane, arow0, bc0, bc1, acc,       \
-                                                pay[(J + 1) & 3], hcur, hh, lut, sm.b[(k + 1) & 1u] + c * 128u, bsw); \
+        m3_compute<SCHEME, (J + 1) & 3, NR, TR, BS && (J & 1) == 0>(                                          \
+            sm.a[k & 1u], sm.b[k & 1u], lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3], hcur, hh, lut,           \
+            sm.b[(k + 1) & 1u] + c * 128u, bsw, m3_bsd<BS && (J & 1) == 0>(bst, k, arow0, lane));              \
         __builtin_amdgcn_sched_barrier(0);                                                                   \
         wait_vm<(J == 1 ? 2 : 1)>(); /* A(k + 1) copied; payload k + 2 (and the header) arrived */           \
         touch_pay(pay[(J + 2) & 3]);                                                                         \
@@ -383,11 +415,11 @@ __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, co
  * block header is loaded at J == 0 and used from J == 3 on (the wait at the
  * end of J == 2 covers it).
  */
-template <int SCHEME, int NR, bool TR>
+template <int SCHEME, int NR, bool TR, bool BS, class Hook>
 __device__ __forceinline__ void m3_mainloop_half(M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
                                                  const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave,
                                                  const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
-                                                 r9vx_f32x16 (&acc)[4][2]) {
+                                                 r9vx_f32x16 (&acc)[4][2], const uint32_t *bst, Hook &hook) {
     constexpr uint32_t kSlot = kM3Stage / 2;
     const uint32_t lane = tid & 63, c = m3_brow(tid), hh = tid & 1, bsw = m2_swz(c);
     const uint32_t a_lds = m3_lds_addr(&sm.a[0][0]);
@@ -406,12 +438,13 @@ __device__ __forceinline__ void m3_mainloop_half(M3Lds &sm, const _Float16 *abas
     if (dma) m3_dma_a(a_lds + 2 * kSlot, abase, aoff, 2, wave);
     m3_load_pay<SCHEME>(w, 3, hh, pay[3]);
     if (dma)
-        wait_vm<15>(); /* P0, H0 */
+        wait_vm<15>(); /* P0, H0 (and the caller's loads issued before) */
     else
         wait_vm<3>();
     touch_pay(pay[0]);
     touch_pay(hnext);
     hcur = hnext;
+    hook();
     m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], hcur, hh, lut, sm.b[0] + c * 128u,
                                  bsw);
     if (dma)
@@ -435,8 +468,9 @@ __device__ __forceinline__ void m3_mainloop_half(M3Lds &sm, const _Float16 *abas
             touch_pay(hnext);                                                                                \
             hcur = hnext;                                                                                    \
         }                                                                                                    \
-        m3_compute<SCHEME, (J + 1) & 3, NR, TR>(sm.a[0] + J * kSlot, sm.b[k & 1u], lane, arow0, bc0, bc1, acc, \
-                                                pay[(J + 1) & 3], hcur, hh, lut, sm.b[(k + 1) & 1u] + c * 128u, bsw); \
+        m3_compute<SCHEME, (J + 1) & 3, NR, TR, BS && (J & 1) == 0>(                                          \
+            sm.a[0] + J * kSlot, sm.b[k & 1u], lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3], hcur, hh, lut,    \
+            sm.b[(k + 1) & 1u] + c * 128u, bsw, m3_bsd<BS && (J & 1) == 0>(bst, k, arow0, lane));              \
         __builtin_amdgcn_sched_barrier(0);                                                                   \
         /* A(k + 1) and payload k + 2 (steps k - 1 and k may stay in flight) */                              \
         if (dma)                                                                                             \
@@ -469,11 +503,15 @@ __device__ __forceinline__ uint32_t m3_active_tiles(uint32_t rows, uint32_t row0
  * TR: acc[t][j] holds the transposed tile (B rows bc_j.. as its rows, A rows
  * arow0 + 32 t.. as its columns): lane l then holds A row arow0 + 32 t +
  * (l & 31) and B rows bc_j + 8 (r >> 2) + 4 (l >> 5) + (r & 3). */
-template <int SCHEME, bool TR = false>
+struct M3NoHook {
+    __device__ void operator()() const {}
+};
+
+template <int SCHEME, bool TR = false, bool BS = false, class Hook = M3NoHook>
 __device__ __forceinline__ void m3_run(uint32_t nr, bool half, M3Lds &sm, const _Float16 *abase,
                                        const uint32_t (&aoff)[4], const M3WRow &w, uint32_t nk, uint32_t tid,
                                        uint32_t wave, const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
-                                       r9vx_f32x16 (&acc)[4][2]) {
+                                       r9vx_f32x16 (&acc)[4][2], const uint32_t *bst = nullptr, Hook &&hook = Hook{}) {
 
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -481,23 +519,26 @@ __device__ __forceinline__ void m3_run(uint32_t nr, bool half, M3Lds &sm, const 
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[t][j][r] = 0.f;
+#define R9VX_M3_CASE(LOOP, N) \
+    case N: LOOP<SCHEME, N, TR, BS>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst, hook); break;
     if (half) { /* the tile's rows fit waves 0-3 (uniform over the workgroup) */
         switch (nr) {
-        case 4: m3_mainloop_half<SCHEME, 4, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
-        case 3: m3_mainloop_half<SCHEME, 3, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
-        case 2: m3_mainloop_half<SCHEME, 2, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
-        case 1: m3_mainloop_half<SCHEME, 1, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
-        default: m3_mainloop_half<SCHEME, 0, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+            R9VX_M3_CASE(m3_mainloop_half, 4)
+            R9VX_M3_CASE(m3_mainloop_half, 3)
+            R9VX_M3_CASE(m3_mainloop_half, 2)
+            R9VX_M3_CASE(m3_mainloop_half, 1)
+        default: m3_mainloop_half<SCHEME, 0, TR, BS>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst, hook); break;
         }
         return;
     }
     switch (nr) {
-    case 4: m3_mainloop<SCHEME, 4, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
-    case 3: m3_mainloop<SCHEME, 3, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
-    case 2: m3_mainloop<SCHEME, 2, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
-    case 1: m3_mainloop<SCHEME, 1, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
-    default: m3_mainloop<SCHEME, 0, TR>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc); break;
+        R9VX_M3_CASE(m3_mainloop, 4)
+        R9VX_M3_CASE(m3_mainloop, 3)
+        R9VX_M3_CASE(m3_mainloop, 2)
+        R9VX_M3_CASE(m3_mainloop, 1)
+    default: m3_mainloop<SCHEME, 0, TR, BS>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst, hook); break;
     }
+#undef R9VX_M3_CASE
 }
 
 }  // namespace r9vx

@@ -22,9 +22,13 @@
  *                                 same region as fp16 [(P + S*T) * Dm] scaled
  *                                 per (row, 64-column block), followed by the
  *                                 f32 scales [(P + S*T) * Dm/64]
- *   hmax    u32[P + S*T]          bits of max|h| per row (grouped GEMM)
+ *   hexp    i32[P + S*T]          e of an h16 row's one scale 2^-e (grouped
+ *                                 GEMM's LDS-decoded down kernels)
  *   h16     fp16[(P + S*T) * Dff] h rows scaled by a power of two, in the down
  *                                 weights' K group order (grouped GEMM)
+ *   hbe     i8[(P + S*T) * NB4]   e of each (row, 128-column block)'s h16
+ *                                 scale 2^-e; NB4 = Dff/128 rounded up to a
+ *                                 multiple of 4 (r9vx_moe_hbe_stride)
  *   x16     fp16[T * Dm], xscale f32[T]  scaled activations in the gate/up
  *                                 weights' K group order (grouped GEMM)
  */
@@ -42,10 +46,14 @@ constexpr uint32_t kMoeTileM = 128;  /* grouped-GEMM rows per tile */
 constexpr uint32_t kMoeTileM3 = 256; /* rows per tile of the r9vx_mma3.h grouped GEMMs */
 
 struct MoeLayout {
-    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, cbad, tiles, tiles3, h, o, hmax, h16, x16,
+    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, cbad, tiles, tiles3, h, o, hexp, h16, hbe, x16,
         xscale, total;
     uint32_t max_tiles, max_tiles3;
 };
+
+/* bytes per row of the hbe exponents: one per 128-column block of h,
+ * rounded up to whole words */
+__host__ __device__ inline uint32_t r9vx_moe_hbe_stride(uint32_t dff) { return (dff / 128 + 3) & ~3u; }
 
 inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint32_t dm, uint32_t dff,
                                  uint32_t shared) {
@@ -74,8 +82,9 @@ inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint
     L.tiles3 = take(16ull * L.max_tiles3 + 16);
     L.h = take(4ull * rows * dff);
     L.o = take(4ull * rows * dm);
-    L.hmax = take(4ull * rows);
+    L.hexp = take(4ull * rows);
     L.h16 = take(2ull * rows * dff);
+    L.hbe = take(rows * r9vx_moe_hbe_stride(dff));
     L.x16 = take(2ull * t_bucket * dm);
     L.xscale = take(4ull * t_bucket);
     L.total = off;

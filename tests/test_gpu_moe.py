@@ -307,6 +307,38 @@ def test_moe_ffn_prefill_shapes(t, e, k, dm, dff, shared, gu_s, dn_s):
     check_close(host(y), ref, f"prefill t={t} e={e}")
 
 
+@pytest.mark.parametrize("dn_s", [O.Q4_K, O.IQ4_XS])
+def test_moe_ffn_prefill_h_blocks_at_different_scales(dn_s):
+    """h rows whose 128-column blocks need different fp16 scales, some none:
+    the gate/up d of h columns 128-511 is multiplied by 2^-8, so those
+    blocks of h stay below 2^15 (scale 1) while block 0 passes it (checked on
+    the shared expert's h).  The gate/up GEMM scales each block by its own
+    power of two and the down GEMM undoes them block by block; y must match
+    the oracle."""
+    t, e, k, dm, dff, shared = 300, 16, 4, 512, 512, 1
+    seed = 1700 + dn_s
+    logits = synth.zipf_logits(seed, t, e)
+    ids, w = O.moe_route(logits, k)
+    gu = synth.quant_weights(O.IQ4_XS, seed + 1, (e + shared) * 2 * dff, dm)
+    dn = synth.quant_weights(dn_s, seed + 2, (e + shared) * dm, dff)
+    bb = synth.BLOCK_BYTES[synth.IQ4_XS]
+    blocks = gu.reshape((e + shared) * 2 * dff, dm // 256, bb)
+    for ex in range(e + shared):  # d (the first fp16 of an IQ4_XS block) of gate and up rows 128-511
+        for base in (ex * 2 * dff + 128, ex * 2 * dff + dff + 128):
+            d = blocks[base:base + dff - 128, :, 0:2].copy().view(np.float16)
+            blocks[base:base + dff - 128, :, 0:2] = (d.astype(np.float32) / 256.0).astype(np.float16).view(np.uint8)
+    x = synth.normal_bf16(seed + 3, (t, dm))
+    h = O.matmul_swiglu(O.IQ4_XS, gu[e * 2 * dff:], dff, dm, x, O.BF16)  # the shared expert
+    bmax = np.abs(h).reshape(t, dff // 128, 128).max(axis=2)
+    assert ((bmax[:, 0] >= 32768) & (bmax[:, 1:].max(axis=1) < 32768)).sum() >= t // 4
+    ref = O.moe_ffn(x, O.BF16, ids, w, e, dff, gu, dn, scheme_gu=O.IQ4_XS, scheme_dn=dn_s, shared=shared)
+    y, ws, st = ffi.moe_ffn(bf16_dev(x), dev(ids.view(np.int32)), dev(w), dev(gu), dev(dn), e, dff,
+                            shared=shared, gate_up_scheme=O.IQ4_XS, down_scheme=dn_s)
+    torch.cuda.synchronize()
+    assert ffi.moe_ffn_status(st, ws) == 0
+    check_close(host(y), ref, f"h block scales down={dn_s}")
+
+
 def test_moe_ffn_prefill_permutation_invariance_full_size():
     """Permuting the 8192 tokens of configs[4] permutes y bit for bit (rows
     keep their K order wherever they land in the expert tiles)."""
