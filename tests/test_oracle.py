@@ -490,6 +490,37 @@ def test_moe_ffn_sliced_equals_full_t0_form():
     assert np.array_equal(y, yf)
 
 
+def test_dot_rows_four_at_once_equals_one_at_a_time():
+    """The oracle's dots run four rows per pass over k by default and one row
+    at a time (T0's loop, the CPU baseline's form) when asked: same bits,
+    including the rows left over past a multiple of four."""
+    n, k = 24, 768
+    w = synth.quant_weights(O.Q4_K, 33, n, k)
+    x = synth.normal_bf16(34, (7, k))
+    x_, ids, wt, gu, dn = _tiny_moe(97, t=11, e=3, k=2, shared=1)
+    y4 = O.matmul(O.Q4_K, w, n, k, x, O.BF16)
+    f4 = O.moe_ffn(x_, O.BF16, ids, wt, 3, 256, gu, dn, shared=1)
+    O.set_rows_at_once(1)
+    try:
+        y1 = O.matmul(O.Q4_K, w, n, k, x, O.BF16)
+        f1 = O.moe_ffn(x_, O.BF16, ids, wt, 3, 256, gu, dn, shared=1)
+    finally:
+        O.set_rows_at_once(4)
+    assert np.array_equal(y1, y4)
+    assert np.array_equal(f1, f4)
+
+
+def test_moe_ffn_threaded_equals_serial():
+    """The OpenMP form (each expert's rows split into 64-row chunks over the
+    threads, which the full-output GPU parity tests use) is the serial
+    oracle bit for bit: ~100 rows per expert, so every expert spans chunks,
+    plus a shared expert over all 200 tokens."""
+    x, ids, w, gu, dn = _tiny_moe(95, t=200, e=4, k=2, shared=1)
+    y = O.moe_ffn(x, O.BF16, ids, w, 4, 256, gu, dn, shared=1)
+    ymt = O.moe_ffn(x, O.BF16, ids, w, 4, 256, gu, dn, shared=1, threads=4)
+    assert np.array_equal(ymt, y)
+
+
 @pytest.mark.parametrize("schemes", [(O.IQ4_XS, O.Q4_K), (O.Q8_0, O.Q8_0), (O.Q6_K, O.Q6_K), (O.IQ3_S, O.IQ3_S),
                                      (O.Q4_K, O.IQ4_XS)])
 def test_moe_ffn_vs_f64_bruteforce_and_shared(schemes):
