@@ -57,8 +57,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU work per baseline sample")
-    ap.add_argument("--only", default="", help="comma list of extras: c0,c1,c2,c3,ceilings ('none' for the headline "
-                                               "only)")
+    ap.add_argument("--only", default="", help="comma list of extras: c0,c1,c2,c3,gemv_n,ceilings ('none' for the "
+                                               "headline only)")
     ap.add_argument("--pmc-case", default="", help="run a short fixed workload for counter collection: c4, c3, c2, c1m5, c0")
     ap.add_argument("--pmc-summary", nargs="*", default=None,
                     help="rocprofv3 --pmc output dirs (FETCH_SIZE, WRITE_SIZE) to summarise as traffic")
@@ -564,6 +564,12 @@ def main():
         extras["c0_q4k_gemv_f32"] = gemv_extra(torch, ffi, synth, ffi.Q4_K, 4096, 4096, 1, ffi.F32, "c0", cpu_s,
                                                "configs[0]: Q4_K GEMV 4096x4096, x f32, y f32")
         log(f"  {extras['c0_q4k_gemv_f32']}")
+    if want("gemv_n"):
+        log("gemv large N ...")
+        extras["gemv_q4k_32768x4096_m1"] = gemv_extra(torch, ffi, synth, ffi.Q4_K, 32768, 4096, 1, ffi.BF16, "gemvN", 0,
+                                                      "Q4_K GEMV N=32768 K=4096 M=1, x bf16, y f32 (75.5 MB of weights: "
+                                                      "the GEMV's steady streaming rate)")
+        log(f"  {extras['gemv_q4k_32768x4096_m1']}")
     if want("c2"):
         log("c2 ...")
         extras["c2"] = c2_extra(torch, ffi, synth, gsynth, args.steps, cpu_s)

@@ -243,6 +243,104 @@ __global__ __launch_bounds__(XS ? 256 : waves_for(M) * 64) void gemv_kernel(Gemv
         lane_reduce_w<V, 1>(v, lane, a.lpr_log2, emit);
 }
 
+/* The streaming form for one activation row over many output rows (m = 1,
+ * one 64-lane K segment per row, f32 y, no epilogue, n >= 12 x SIMDs): a
+ * wave walks the row groups gw, gw + W, ... (RR rows each, W waves in the
+ * grid, `steps` groups per wave at most), loading the next group's weights
+ * before it computes the current one (two register buffers; a group past
+ * the end repeats the last group's loads, so every path issues the same
+ * loads), with its activation slices loaded and arranged once.  The row
+ * sums wait in LDS until the wave's last load is issued: a store between
+ * two loads would make the next wait a wait for the store as well.  Per row
+ * the arithmetic is gemv_kernel's (the lane's chunks lir, lir + 64 in that
+ * order, the same cross-lane tree), so the outputs are the same bits. */
+constexpr uint32_t kStreamMaxSteps = 16;
+/* rows per group and waves per SIMD: measured (Q4_K 32768 x 4096, IQ4_XS
+ * 32768 x 2048, Q4_K 14336 x 4096, graph-replayed) against (2, 3), (4, 2),
+ * (1, 4), (2, 4) and (4, 3), which were 2-50% slower */
+constexpr uint32_t kStreamRows = 2, kStreamWavesPerSimd = 2;
+
+template <int SCHEME, bool XF32, int SPL, int RR>
+__global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs a, uint32_t steps) {
+    using Pay = typename std::conditional<pay2_scheme(SCHEME), Payload2, r9vx_u32x4>::type;
+    __shared__ __attribute__((aligned(16))) uint32_t lut[lut_words(SCHEME)];
+    __shared__ float ob[4][kStreamMaxSteps * RR];
+    const uint32_t lane = threadIdx.x & 63, wl = threadIdx.x >> 6;
+    const uint32_t gw = blockIdx.x * 4 + wl, nw = gridDim.x * 4;
+    const uint32_t ngroups = (a.n + RR - 1) / RR;
+    uint32_t cis[SPL];
+#pragma unroll
+    for (int s = 0; s < SPL; ++s) cis[s] = (uint32_t)s * 64u + lane;
+    XRaw<XF32> xr[SPL];
+#pragma unroll
+    for (int s = 0; s < SPL; ++s) {
+        uint32_t klo, khi;
+        chunk_k<SCHEME>(cis[s], klo, khi);
+        load_x_raw<XF32>(a.x, klo, khi, xr[s]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    Pay qa[RR][SPL], qb[RR][SPL];
+    Hdr ha[RR][SPL], hb[RR][SPL];
+    auto issue = [&](uint32_t step, Pay (&q)[RR][SPL], Hdr (&h)[RR][SPL]) {
+        uint32_t g = gw + step * nw;
+        if (g >= ngroups) g = ngroups - 1;
+#pragma unroll
+        for (int r = 0; r < RR; ++r) {
+            const uint32_t row = g * RR + (uint32_t)r, rr = row < a.n ? row : a.n - 1;
+            const uint8_t *wrow = a.w + (uint64_t)rr * a.w_row_stride;
+#pragma unroll
+            for (int s = 0; s < SPL; ++s) load_chunk<SCHEME>(wrow, cis[s], q[r][s], h[r][s]);
+        }
+    };
+    issue(0, qa, ha);
+    if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) {
+        build_iq4_lut(lut, threadIdx.x, blockDim.x);
+        __syncthreads();
+    }
+    XChunk<SCHEME, XF32> xc[SPL][1];
+#pragma unroll
+    for (int s = 0; s < SPL; ++s) arrange_x<SCHEME, XF32>(xr[s], xc[s][0]);
+    float *const obw = ob[wl];
+    auto compute = [&](uint32_t step, const Pay (&q)[RR][SPL], const Hdr (&h)[RR][SPL]) {
+        float acc[RR][1];
+#pragma unroll
+        for (int r = 0; r < RR; ++r) {
+            acc[r][0] = 0.f;
+#pragma unroll
+            for (int s = 0; s < SPL; ++s) chunk_dot<SCHEME, XF32, 1>(q[r][s], h[r][s], cis[s] & 7, xc[s], acc[r], lut);
+        }
+        float v[1][RR];
+#pragma unroll
+        for (int r = 0; r < RR; ++r) v[0][r] = acc[r][0];
+        lane_reduce<RR, 64, 1>(v, lane, [&](int idx, const float (&val)[1]) { obw[step * RR + idx] = val[0]; });
+    };
+    for (uint32_t step = 0; step < steps; step += 2) {
+        issue(step + 1, qb, hb);
+        compute(step, qa, ha);
+        if (step + 1 >= steps) break;
+        issue(step + 2, qa, ha);
+        compute(step + 1, qb, hb);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float *const y = reinterpret_cast<float *>(a.y);
+    for (uint32_t j = lane; j < steps * RR; j += 64) {
+        const uint32_t g = gw + (j / RR) * nw, row = g * RR + j % RR;
+        if (g < ngroups && row < a.n) y[row] = obw[j];
+    }
+}
+
+template <int SCHEME, bool XF32, int SPL>
+int launch_stream(const GemvArgs &a, uint32_t simds, hipStream_t s) {
+    const uint32_t ngroups = (a.n + kStreamRows - 1) / kStreamRows;
+    uint32_t waves = kStreamWavesPerSimd * simds;
+    if ((ngroups + waves - 1) / waves > kStreamMaxSteps) waves = (ngroups + kStreamMaxSteps - 1) / kStreamMaxSteps;
+    const uint32_t wgs = (waves + 3) / 4, steps = (ngroups + wgs * 4 - 1) / (wgs * 4);
+    hipLaunchKernelGGL((gemv_stream_kernel<SCHEME, XF32, SPL, kStreamRows>), dim3(wgs), dim3(256), 0, s, a, steps);
+    return (int)hipGetLastError();
+}
+
 /* The gated (SwiGLU) form: y[m, j] = silu(x[m] . w[j]) * (x[m] . w[n + j])
  * over stacked weights (gate rows [0, n), up rows [n, 2n)), the matmul +
  * act_mul pair of T0 (crates/r9v-t0/src/act_mul.rs:86-99 with SiLU
@@ -440,6 +538,13 @@ int launch_one(const GemvArgs &a, uint32_t m, uint32_t rows_per_slot_group, hipS
         return (int)hipErrorInvalidValue;
     } else {
         if (m != MM) return launch_one<SCHEME, XF32, SPL, MM - 1>(a, m, rows_per_slot_group, s);
+        if constexpr (MM == 1 && (SCHEME == R9VX_SCHEME_Q4_K || SCHEME == R9VX_SCHEME_IQ4_XS)) {
+            /* one activation row over many rows: the streaming form */
+            if (a.lpr_log2 == 6 && a.nseg == 1 && a.epilogue == R9VX_EPILOGUE_NONE && !a.y_bf16) {
+                const uint32_t simds = device_simds();
+                if (a.n >= 12 * simds) return launch_stream<SCHEME, XF32, SPL>(a, simds, s);
+            }
+        }
         if (a.lpr_log2 == 6 && a.nseg == 1 && a.epilogue == R9VX_EPILOGUE_NONE && !a.y_bf16) {
             /* one or two activation rows: two rows per lane group while
              * the launch is latency-bound (n = 5120, M = 1: 3.90 us against
@@ -495,8 +600,8 @@ int r9vx_launch_gemv(const r9vx_gemv_problem &p, hipStream_t stream) {
     const uint32_t cpr = p.k / 32; /* 16-byte chunks per row, a multiple of 8 */
     /* Two chunks per lane when a row has >= 128 chunks and the activation
      * registers fit (M rows x 2 chunks).  This choice, the rows per lane
-     * group and the activation staging follow m, but none of them changes a
-     * row's arithmetic: a lane always owns the chunks lir, lir + 64, ... of
+     * group, the activation staging and the streaming form for m = 1 follow
+     * m, but none of them changes a row's arithmetic: a lane always owns the chunks lir, lir + 64, ... of
      * every row and adds them in that order (two per segment or one), and the
      * cross-lane sum over the 64 lanes is the same tree for every value, so
      * a row's outputs are the same bits for every m of a bucket <= 8. */

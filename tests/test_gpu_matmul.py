@@ -110,6 +110,25 @@ def test_gemv_multi_segment_rows(scheme, n, k, m):
     check_close(y, O.matmul(scheme, w, n, k, x, O.BF16, threads=8), f"n={n} k={k} m={m}")
 
 
+@pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])
+@pytest.mark.parametrize("x_dtype", [O.BF16, O.F32])
+@pytest.mark.parametrize("n,k", [(20001, 4096), (13000, 2048), (32768, 4096)])
+def test_gemv_streaming_form(scheme, x_dtype, n, k):
+    """m = 1 over n >= 12 x SIMDs rows takes the streaming kernel (persistent
+    waves, two weight buffers); every output against the oracle, and each
+    row bit-equal to the same row in an m = 2 launch (the one-shot kernel):
+    the two forms share the per-row arithmetic.  n = 20001 leaves a ragged
+    last row group."""
+    w = synth.quant_weights(scheme, 7300 + n + k, n, k)
+    x = synth.normal_bf16(7400 + k, (2, k)) if x_dtype == O.BF16 else synth.normal_f32(7400 + k, (2, k))
+    xd = bf16_dev(x) if x_dtype == O.BF16 else dev(x)
+    wd = dev(w)
+    y1 = host(ffi.matmul(wd, scheme, n, k, xd[:1].contiguous(), m_bucket=8))
+    y2 = host(ffi.matmul(wd, scheme, n, k, xd, m_bucket=8))
+    assert np.array_equal(y1[0].view(np.int32), y2[0].view(np.int32)), "streaming and one-shot rows differ"
+    check_close(y1, O.matmul(scheme, w, n, k, x[:1], x_dtype, threads=8), f"n={n} k={k}")
+
+
 def test_gemv_graph_replays_match_eager():
     """GEMV launches captured in a HIP graph: every replay (with eager work
     between replays) equals the eager result bit for bit."""
