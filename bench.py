@@ -21,7 +21,7 @@ restatement of R9V's T0 path) on a bounded sample on this host, 1 thread,
 plus an all-threads OpenMP variant for the grouped MoE GEMM.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c0,c1,c2,c3,ceilings]
-    python bench.py --pmc-case c4|c3|c2|c1m5|c0  # short fixed run for rocprofv3 --pmc
+    python bench.py --pmc-case c4|c3|c2|c1m5|c0|gemvn  # short fixed run for rocprofv3 --pmc
     python bench.py --pmc-summary DIR ... [--pmc-kernels a,b]  # FETCH_SIZE/WRITE_SIZE dirs -> traffic text
 """
 from __future__ import annotations
@@ -59,7 +59,8 @@ def parse():
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU work per baseline sample")
     ap.add_argument("--only", default="", help="comma list of extras: c0,c1,c2,c3,gemv_n,ceilings ('none' for the "
                                                "headline only)")
-    ap.add_argument("--pmc-case", default="", help="run a short fixed workload for counter collection: c4, c3, c2, c1m5, c0")
+    ap.add_argument("--pmc-case", default="", help="run a short fixed workload for counter collection: c4, c3, c2, c1m5, "
+                                                   "c0, gemvn")
     ap.add_argument("--pmc-summary", nargs="*", default=None,
                     help="rocprofv3 --pmc output dirs (FETCH_SIZE, WRITE_SIZE) to summarise as traffic")
     ap.add_argument("--pmc-kernels", default="", help="comma list of kernel-name substrings for --pmc-summary "
@@ -417,15 +418,16 @@ def pmc_case(torch, ffi, synth, gsynth, name):
         c3_extra(torch, ffi, synth, gsynth, 6, 0, steps_only=True)
     elif name == "c2":
         c2_extra(torch, ffi, synth, gsynth, 6, 0, steps_only=True)
-    elif name in ("c1m5", "c0"):
+    elif name in ("c1m5", "c0", "gemvn"):
         # 200 GEMV launches over the rotated weight copies (each launch reads
         # its copy from HBM, not the Infinity Cache)
-        b = Gemv(torch, ffi, synth, *((ffi.IQ4_XS, 5120, 2048, 5, ffi.BF16) if name == "c1m5" else
-                                     (ffi.Q4_K, 4096, 4096, 1, ffi.F32)), name)
+        shape = {"c1m5": (ffi.IQ4_XS, 5120, 2048, 5, ffi.BF16), "c0": (ffi.Q4_K, 4096, 4096, 1, ffi.F32),
+                 "gemvn": (ffi.Q4_K, 32768, 4096, 1, ffi.BF16)}[name]
+        b = Gemv(torch, ffi, synth, *shape, name)
         for i in range(200):
             b.launch(i)
     else:
-        raise SystemExit(f"unknown --pmc-case {name!r} (known: c0, c1m5, c2, c3, c4)")
+        raise SystemExit(f"unknown --pmc-case {name!r} (known: c0, c1m5, gemvn, c2, c3, c4)")
     torch.cuda.synchronize()
     src = torch.ones(PMC_COPY_BYTES // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
