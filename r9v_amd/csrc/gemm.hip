@@ -16,9 +16,11 @@
  *     columns of x (fp16) and 32 payload bytes of 256 weight rows from HBM
  *     into registers while the MFMAs consume the previous step from LDS, then
  *     dequantizes the weights (exact f32 formula, one fp16 rounding) into the
- *     other LDS buffer.  Workgroups are mapped so that each XCD owns a
- *     contiguous band of weight columns: the 8 M-tiles that reuse a weight
- *     tile run on the same XCD and hit its L2.
+ *     other LDS buffer.  gemm2 maps workgroups so that each XCD owns a
+ *     contiguous band of weight columns (the 8 M-tiles that reuse a weight
+ *     tile run on the same XCD and hit its L2); gemm3 cuts each weight
+ *     block's rows into chunks sized so that the launch fills whole rounds
+ *     of the CUs (plan_chunks).
  */
 #include "r9vx_mma.h"
 #include "r9vx_mma2.h"
@@ -27,6 +29,12 @@
 using namespace r9vx;
 
 namespace {
+
+/* gemm3's row chunks: blocks [b0, b0 + nb) of 256 weight rows x chunk
+ * indices [c0, c0 + nc), nb * nc workgroups, block-fastest. */
+struct ChunkGroup {
+    uint32_t b0, nb, c0, nc;
+};
 
 struct GemmArgs {
     const _Float16 *x16;
@@ -41,6 +49,14 @@ struct GemmArgs {
     uint32_t m_tiles, n_tiles;
     uint32_t y_bf16, epilogue;
     uint32_t ws_row; /* d values per weight row */
+    /* gemm3: the 32-row tiles of the m rows (rt of them) are cut, per weight
+     * block, into nlo + 1 chunks for blocks < r0 and nlo chunks for the
+     * others, as evenly as whole row tiles allow; grp lists the chunks
+     * largest first, or with band set (every block nlo chunks, a multiple
+     * of 8 in all) XCD x takes the x-th eighth of the (block, chunk) list,
+     * a block's chunks consecutively */
+    uint32_t rt, nlo, r0, band;
+    ChunkGroup grp[4];
 };
 
 /* PERM = 0: natural order; R9VX_SCHEME_Q4_K / R9VX_SCHEME_IQ4_XS: each 64-column
@@ -239,23 +255,41 @@ __global__ __launch_bounds__(512, 1) void gemm2_kernel(GemmArgs a) {
     }
 }
 
-/* 256 x 256 tiles on the r9vx_mma3.h loop (the grouped MoE GEMMs' core): the
- * weight tile is decoded once per workgroup into LDS, every wave reads its
- * B fragments from there, and the accumulators are the transposed tile, so
- * lane l holds output row 128 rh + 32 t + (l & 31) and columns 64 cq + 32 j +
- * 8 (r >> 2) + 4 (l >> 5) + (r & 3) of acc[t][j][r].  The launcher takes it
- * for n % 256 == 0 and m k < 2^31 (the A copy offsets are 32-bit). */
+/* Tiles of up to 256 rows x 256 columns on the r9vx_mma3.h loop (the grouped
+ * MoE GEMMs' core): the weight tile is decoded once per workgroup into LDS,
+ * every wave reads its B fragments from there, and the accumulators are the
+ * transposed tile, so lane l holds output row 128 rh + 32 t + (l & 31) and
+ * columns 64 cq + 32 j + 8 (r >> 2) + 4 (l >> 5) + (r & 3) of acc[t][j][r].
+ * A workgroup takes the chunk of rows plan_chunks gave its index.  The
+ * launcher takes it for n % 256 == 0 and m k < 2^31 (the A copy offsets are
+ * 32-bit). */
 template <int SCHEME>
 __global__ __launch_bounds__(512, 1) void gemm3_kernel(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) M3Lds sm;
     __shared__ float rowsc[kM3Rows];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t total = a.m_tiles * a.n_tiles;
-    uint32_t t = blockIdx.x;
-    if (total % 8 == 0) t = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
-    const uint32_t n_tile = t / a.m_tiles, m_tile = t % a.m_tiles;
-    const uint32_t m0 = m_tile * kM3Rows, n0 = n_tile * kM3Cols;
-    const uint32_t rows = a.m - m0 < kM3Rows ? a.m - m0 : kM3Rows;
+    uint32_t wg = blockIdx.x, blk = 0, ch = 0;
+    if (a.band) {
+        const uint32_t t = (wg % 8u) * (gridDim.x / 8u) + wg / 8u;
+        blk = t / a.nlo;
+        ch = t % a.nlo;
+    } else {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint32_t cnt = a.grp[g].nb * a.grp[g].nc;
+            if (wg < cnt) {
+                blk = a.grp[g].b0 + wg % a.grp[g].nb;
+                ch = a.grp[g].c0 + wg / a.grp[g].nb;
+                break;
+            }
+            wg -= cnt;
+        }
+    }
+    /* chunk ch of the block's nch: row tiles ch * per + min(ch, rem) .. */
+    const uint32_t nch = blk < a.r0 ? a.nlo + 1 : a.nlo, per = a.rt / nch, rem = a.rt % nch;
+    const uint32_t m0 = 32u * (ch * per + (ch < rem ? ch : rem)), n0 = blk * kM3Cols;
+    const uint32_t span = 32u * (per + (ch < rem ? 1u : 0u));
+    const uint32_t rows = a.m - m0 < span ? a.m - m0 : span;
     const float rsc = tid < rows ? a.scale[m0 + tid] : 0.f;
     if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) m3_init_iq4_lut(sm.lut, tid, 512);
     __syncthreads();
@@ -328,7 +362,63 @@ __global__ __launch_bounds__(512, 1) void gemm3_kernel(GemmArgs a) {
     }
 }
 
+/* gemm3's plan: the rows of each 256-column weight block are cut into
+ * chunks of whole 32-row tiles (at most 8), so that the launch is a whole
+ * number of rounds of one workgroup per CU with the rows spread over the
+ * CUs as evenly as chunks allow.  A chunk's time is a fixed part (its
+ * weight block's loads and decode) plus a part per row tile, so every CU
+ * runs as many chunks as the 256-row tiling needs rounds and the row tiles
+ * are dealt evenly over them, largest chunks first (the hardware gives each
+ * next workgroup to the first CU that frees).  Example (m = 2048, n = 14336,
+ * 256 CUs): 448 tiles of 256 rows are 1.75 rounds, the second leaving 64 CUs
+ * idle; the plan makes 512 chunks, 48 of 8 row tiles, 416 of 7 and 48 of 6,
+ * so a CU runs 7 + 7 or 8 + 6.  With fewer tiles than CUs the chunks shrink
+ * until every CU has one.  Which rows share a chunk changes no output bit.
+ * Returns the workgroup count. */
+uint32_t plan_chunks(GemmArgs &a, uint32_t cus) {
+    const uint32_t nb = a.n / kM3Cols, rt = (a.m + 31) / 32;
+    const uint64_t tiles = (uint64_t)nb * ((rt + 7) / 8);
+    uint64_t q = (tiles + cus - 1) / cus * cus;
+    if (q > (uint64_t)nb * rt) q = (uint64_t)nb * rt;
+    /* one round either way and no smaller largest chunk: the extra chunks
+     * would only decode their weight blocks again (m = 1024, n = 14336) */
+    const uint32_t per8 = (rt + 7) / 8, nq = (uint32_t)(q / nb);
+    if (tiles <= cus && (rt + nq - 1) / nq == (rt + per8 - 1) / per8) q = tiles;
+    a.rt = rt;
+    a.nlo = (uint32_t)(q / nb); /* >= ceil(rt / 8): no chunk exceeds 8 row tiles */
+    a.r0 = (uint32_t)(q % nb);
+    const uint32_t na = a.nlo + 1, qa = rt / na, ra = rt % na, qb = rt / a.nlo, rb = rt % a.nlo;
+    struct Sized {
+        ChunkGroup g;
+        uint32_t tiles;
+    } gs[4] = {{{a.r0, nb - a.r0, 0, rb}, qb + 1},
+               {{a.r0, nb - a.r0, rb, a.nlo - rb}, qb},
+               {{0, a.r0, 0, ra}, qa + 1},
+               {{0, a.r0, ra, na - ra}, qa}};
+    for (int i = 1; i < 4; ++i)
+        for (int j = i; j > 0 && gs[j].tiles > gs[j - 1].tiles; --j) {
+            const Sized t = gs[j];
+            gs[j] = gs[j - 1];
+            gs[j - 1] = t;
+        }
+    for (int i = 0; i < 4; ++i) a.grp[i] = gs[i].g;
+    a.band = a.r0 == 0 && q % 8 == 0;
+    return (uint32_t)q;
+}
+
 }  // namespace
+
+uint32_t r9vx_device_cus() {
+    static uint32_t cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        cached[dev] = (uint32_t)cus;
+    }
+    return cached[dev];
+}
 
 size_t r9vx_gemm_workspace_bytes(uint32_t m_bucket, uint32_t k) {
     return (((size_t)m_bucket * k * 2 + 255) & ~(size_t)255) + (size_t)m_bucket * 4;
@@ -389,10 +479,11 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
         a.n_tiles = (p.n + kM2Cols - 1) / kM2Cols;
         dim3 grid(a.m_tiles * a.n_tiles);
         if (p.n % kM3Cols == 0 && (uint64_t)p.m_bucket * p.k < (1ull << 31)) {
+            const dim3 grid3(plan_chunks(a, r9vx_device_cus()));
             if (p.scheme == R9VX_SCHEME_Q4_K)
-                hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_Q4_K>), grid, dim3(512), 0, stream, a);
+                hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_Q4_K>), grid3, dim3(512), 0, stream, a);
             else
-                hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_IQ4_XS>), grid, dim3(512), 0, stream, a);
+                hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_IQ4_XS>), grid3, dim3(512), 0, stream, a);
             return (int)hipGetLastError();
         }
         if (p.scheme == R9VX_SCHEME_Q4_K)

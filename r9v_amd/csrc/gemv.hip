@@ -488,17 +488,7 @@ int launch_gated_scheme(const GemvArgs &a, uint32_t m, int spl, uint32_t g, hipS
 }
 
 /* SIMDs of the current device (4 per CU), for the wave-balance rule. */
-uint32_t device_simds() {
-    static uint32_t cached[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
-    if (!cached[dev]) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-        cached[dev] = 4u * (uint32_t)cus;
-    }
-    return cached[dev];
-}
+uint32_t device_simds() { return 4u * r9vx_device_cus(); }
 
 /* Rows per lane group for the compile-time form at M >= 3: the R in 2..5 whose wave
  * count ceil(n / R) gives the busiest SIMD the least work,

@@ -114,6 +114,8 @@ struct r9vx_gemm_problem {
 };
 size_t r9vx_gemm_workspace_bytes(uint32_t m_bucket, uint32_t k);
 int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream);
+/* Compute units of the current device (cached per device; 256 if the query fails). */
+uint32_t r9vx_device_cus();
 
 struct r9vx_route_problem {
     const float *logits;
