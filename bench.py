@@ -21,7 +21,7 @@ restatement of R9V's T0 path) on a bounded sample on this host, 1 thread,
 plus an all-threads OpenMP variant for the grouped MoE GEMM.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c0,c1,c2,c3,ceilings]
-    python bench.py --pmc-case c4|c3|c2|c1m5|c0|gemvn  # short fixed run for rocprofv3 --pmc
+    python bench.py --pmc-case c4|c3|c2|c1m5|c0|gemvn|ceil  # short fixed run for rocprofv3 --pmc
     python bench.py --pmc-summary DIR ... [--pmc-kernels a,b]  # FETCH_SIZE/WRITE_SIZE dirs -> traffic text
 """
 from __future__ import annotations
@@ -60,9 +60,12 @@ def parse():
     ap.add_argument("--only", default="", help="comma list of extras: c0,c1,c2,c3,gemv_n,ceilings ('none' for the "
                                                "headline only)")
     ap.add_argument("--pmc-case", default="", help="run a short fixed workload for counter collection: c4, c3, c2, c1m5, "
-                                                   "c0, gemvn")
+                                                   "c0, gemvn, ceil")
     ap.add_argument("--pmc-summary", nargs="*", default=None,
                     help="rocprofv3 --pmc output dirs (FETCH_SIZE, WRITE_SIZE) to summarise as traffic")
+    ap.add_argument("--clock-summary", nargs=2, default=None, metavar=("KT_DIR", "PMC_DIR"),
+                    help="rocprofv3 --kernel-trace and --pmc GRBM_GUI_ACTIVE output dirs of one workload: each "
+                         "kernel's mean shader clock")
     ap.add_argument("--pmc-kernels", default="", help="comma list of kernel-name substrings for --pmc-summary "
                                                       "(default: the headline kernel)")
     return ap.parse_args()
@@ -405,7 +408,8 @@ def ceilings(torch, ffi):
 def pmc_case(torch, ffi, synth, gsynth, name):
     """A short fixed run for `rocprofv3 --pmc`: 6 steps of configs[4]
     (moe_ffn), configs[3] (route + moe_ffn) or configs[2] (the dense GEMM),
-    or 200 launches of the configs[1] M=5 / configs[0] GEMV --
+    200 launches of the configs[1] M=5 / configs[0] GEMV, or (ceil) the
+    measured ceilings' MFMA-only loop and 1 GB streaming read --
     the summaries take medians over a kernel's launches, so the first
     launch's cold caches do not count -- then 5 launches of a plain copy
     kernel of known size (torch.neg, f32 -> f32, 64 MiB read + 64 MiB
@@ -418,6 +422,16 @@ def pmc_case(torch, ffi, synth, gsynth, name):
         c3_extra(torch, ffi, synth, gsynth, 6, 0, steps_only=True)
     elif name == "c2":
         c2_extra(torch, ffi, synth, gsynth, 6, 0, steps_only=True)
+    elif name == "ceil":
+        # the measured ceilings' two probes: 5 launches each of the MFMA-only
+        # loop and of the 1 GB streaming read
+        blocks, iters = 256 * 8, 256
+        sink = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+        for _ in range(5):
+            ffi.probe_mfma(blocks, iters, sink=sink)
+        buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+        for _ in range(5):
+            ffi.probe_stream(buf)
     elif name in ("c1m5", "c0", "gemvn"):
         # 200 GEMV launches over the rotated weight copies (each launch reads
         # its copy from HBM, not the Infinity Cache)
@@ -427,7 +441,7 @@ def pmc_case(torch, ffi, synth, gsynth, name):
         for i in range(200):
             b.launch(i)
     else:
-        raise SystemExit(f"unknown --pmc-case {name!r} (known: c0, c1m5, gemvn, c2, c3, c4)")
+        raise SystemExit(f"unknown --pmc-case {name!r} (known: c0, c1m5, gemvn, c2, c3, c4, ceil)")
     torch.cuda.synchronize()
     src = torch.ones(PMC_COPY_BYTES // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
@@ -487,6 +501,44 @@ def pmc_summary(dirs, kernels=None):
     print("\n".join(lines))
 
 
+def clock_summary(kt_dir, pmc_dir, kernels):
+    """Each kernel's median duration (a `rocprofv3 --kernel-trace` run) and
+    median GRBM_GUI_ACTIVE (a `--pmc GRBM_GUI_ACTIVE` run of the same
+    workload), and from them the mean shader clock while it ran: the counter
+    adds up the busy GPU clocks of the 8 XCDs, so clock = counter / 8 /
+    duration.  The counter's window also covers the dispatch's start and
+    drain, so for launches of a few microseconds the figure overstates the
+    clock; for the long GEMM launches it is the clock."""
+    import glob
+    import re
+    import sqlite3
+
+    def short(name):
+        name = name.replace("(anonymous namespace)::", "")
+        m = re.search(r"(\w+(<[^>]*>)?)\(", name)
+        return m.group(1) if m else name[:48]
+
+    dur, grbm = {}, {}
+    for f in glob.glob(os.path.join(kt_dir, "**", "*_results.db"), recursive=True):
+        for n, d in sqlite3.connect(f).execute("select name, duration from kernels"):
+            dur.setdefault(short(n), []).append(float(d))
+    for f in glob.glob(os.path.join(pmc_dir, "**", "*_results.db"), recursive=True):
+        q = "select counter_name, kernel_name, value from counters_collection"
+        for cn, kn, v in sqlite3.connect(f).execute(q):
+            if cn == "GRBM_GUI_ACTIVE":
+                grbm.setdefault(short(kn), []).append(float(v))
+    lines = ["kernel                                    dispatches  median_us  GRBM_GUI_ACTIVE  clock_GHz"]
+    for k in sorted(dur, key=lambda k: -statistics.median(dur[k]) * len(dur[k])):
+        if kernels and not any(s in k for s in kernels):
+            continue
+        if k not in grbm:
+            continue
+        d_us = statistics.median(dur[k]) / 1e3
+        g = statistics.median(grbm[k])
+        lines.append(f"{k[:41]:41s} {len(dur[k]):10d} {d_us:10.2f} {g:16.0f} {g / 8 / (d_us * 1e3):10.3f}")
+    print("\n".join(lines))
+
+
 def read_traffic():
     try:
         for line in open(TRAFFIC_FILE):
@@ -503,6 +555,9 @@ def main():
     args = parse()
     if args.pmc_summary is not None:
         pmc_summary(args.pmc_summary, [k for k in args.pmc_kernels.split(",") if k] or None)
+        return 0
+    if args.clock_summary:
+        clock_summary(args.clock_summary[0], args.clock_summary[1], [k for k in args.pmc_kernels.split(",") if k])
         return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: multi-GPU figures are out of scope, "
