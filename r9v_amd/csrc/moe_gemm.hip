@@ -498,7 +498,7 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
 
 /* Down on the r9vx_mma3.h loop: 256 rows x 256 output columns per
  * workgroup; wave w's column tiles are 64(w%4) and 64(w%4) + 32. */
-template <int DN>
+template <int DN, int PASSES>
 __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     __shared__ __attribute__((aligned(16))) M3Lds sm;
     uint32_t *const lut = sm.lut;
@@ -506,13 +506,12 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     __shared__ uint32_t bst[kM3MaxBlk * 64]; /* the rows' exponent steps per 128-K block (m3_bsd) */
     const uint32_t *status = ws_u32(a, a.L.status);
     uint32_t tix, nt;
-    xcd_tile(a.dm / 256, tix, nt);
+    xcd_tile(a.dm / 256 / PASSES, tix, nt);
     const uint32_t st0 = status[0], ntile = status[4]; /* one round of loads, as in gate/up */
     const r9vx_u32x4 tile =
         reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles3)[tix < a.L.max_tiles3 ? tix : a.L.max_tiles3 - 1];
     if (st0 != 0u || tix >= ntile) return;
     const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
-    const uint32_t n0 = nt * 256;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     /* h16 row r's 128-column block b is at scale 2^-e(b) (hbe).  Thread
      * r < 256 loads its row's exponents now (ahead of the main loop's loads,
@@ -564,67 +563,96 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
         const uint32_t r = dma_row(wv, i, lane);
         aoff[i] = ((pos0 + (r < rows ? r : 0)) * a.dff + 8 * dma_group(r, lane)) * 2u;
     }
-    const M3WRow w{m3_uniform(a.w_dn + ((uint64_t)expert * a.dm + n0) * a.dn_row_bytes),
-                   m3_brow(tid) * (uint32_t)a.dn_row_bytes};
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
-    r9vx_f32x16 acc[4][2];
-    m3_run<DN, true, true>(nr, rows <= 128, sm, a.h16, aoff, w, a.dff / kTileK, tid, wv, lut, 128 * rh, 64 * cq,
-                           64 * cq + 32, acc, bst, fill_steps);
-    __syncthreads();
-
-    /* The tiles are transposed (m3_run<.., true>): lane l holds h row
-     * 128 rh + 32 t + (l & 31) and output columns n0 + 64 cq + 32 j +
-     * 8 (r >> 2) + 4 (l >> 5) + (r & 3).  o rows are stored as fp16 scaled by
-     * a power of two per (row, 64-column block), the block being this wave's
-     * two column tiles: its max is this lane's 32 values and lane l ^ 32's.
-     * The scale puts the block max in [2^14, 2^15); its inverse is stored
-     * beside the rows for the combine.  The fp16 tile is staged in LDS (row
-     * R's 8-byte chunk c at chunk c ^ (R & 31): the 32 rows one write
-     * instruction covers hit distinct banks), then each row leaves as 32
-     * lanes x 16 contiguous bytes. */
-    const uint64_t nrows_all = (uint64_t)a.p + (uint64_t)a.shared * a.t;
-    _Float16 *o16 = reinterpret_cast<_Float16 *>(a.ws + a.L.o);
-    float *oscale = reinterpret_cast<float *>(a.ws + a.L.o + r9vx_moe_oscale_offset(nrows_all, a.dm));
-    const uint32_t blk = (n0 + 64 * cq) / 64, nblk = a.dm / 64;
-    uint8_t *const ot = m3_out_tile(sm);
+    /* one 256-column block of the output per pass.  With PASSES = 2 the
+     * workgroup's entry, its exponent steps and the h rows' copies (then in
+     * L2) serve two blocks, and for tiles of more than 128 rows the second
+     * block's weight payload loads are issued before the first block's
+     * epilogue, so that their latency passes under it. */
+    auto weights = [&](uint32_t n0) {
+        return M3WRow{m3_uniform(a.w_dn + ((uint64_t)expert * a.dm + n0) * a.dn_row_bytes),
+                      m3_brow(tid) * (uint32_t)a.dn_row_bytes};
+    };
+    const uint32_t nk = a.dff / kTileK;
+    auto epilogue = [&](uint32_t n0, r9vx_f32x16 (&acc)[4][2]) {
+        /* The tiles are transposed (m3_run<.., true>): lane l holds h row
+         * 128 rh + 32 t + (l & 31) and output columns n0 + 64 cq + 32 j +
+         * 8 (r >> 2) + 4 (l >> 5) + (r & 3).  o rows are stored as fp16 scaled by
+         * a power of two per (row, 64-column block), the block being this wave's
+         * two column tiles: its max is this lane's 32 values and lane l ^ 32's.
+         * The scale puts the block max in [2^14, 2^15); its inverse is stored
+         * beside the rows for the combine.  The fp16 tile is staged in LDS (row
+         * R's 8-byte chunk c at chunk c ^ (R & 31): the 32 rows one write
+         * instruction covers hit distinct banks), then each row leaves as 32
+         * lanes x 16 contiguous bytes. */
+        const uint64_t nrows_all = (uint64_t)a.p + (uint64_t)a.shared * a.t;
+        _Float16 *o16 = reinterpret_cast<_Float16 *>(a.ws + a.L.o);
+        float *oscale = reinterpret_cast<float *>(a.ws + a.L.o + r9vx_moe_oscale_offset(nrows_all, a.dm));
+        const uint32_t blk = (n0 + 64 * cq) / 64, nblk = a.dm / 64;
+        uint8_t *const ot = m3_out_tile(sm);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        if ((uint32_t)t >= nr) break;
-        const uint32_t rl = 128 * rh + 32 * t + (lane & 31);
-        const float sc = rl < rows ? rowsc[rl] : 0.f;
-        float m = 0.f;
+        for (int t = 0; t < 4; ++t) {
+            if ((uint32_t)t >= nr) break;
+            const uint32_t rl = 128 * rh + 32 * t + (lane & 31);
+            const float sc = rl < rows ? rowsc[rl] : 0.f;
+            float m = 0.f;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(acc[t][j][r]));
-        m *= sc; /* exact: sc is a power of two */
-        m = fmaxf(m, __shfl_xor(m, 32, 64));
-        int e = 0;
-        (void)frexpf(m, &e); /* m = f 2^e, f in [0.5, 1) */
-        const float f = ldexpf(sc, 15 - e); /* a power of two: acc * f = (acc * sc) 2^(15 - e) exactly */
-        uint8_t *const orow = ot + rl * 512u;
+                for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(acc[t][j][r]));
+            m *= sc; /* exact: sc is a power of two */
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            int e = 0;
+            (void)frexpf(m, &e); /* m = f 2^e, f in [0.5, 1) */
+            const float f = ldexpf(sc, 15 - e); /* a power of two: acc * f = (acc * sc) 2^(15 - e) exactly */
+            uint8_t *const orow = ot + rl * 512u;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const uint32_t chunk = (16u * cq + 8u * j + 2u * g + (lane >> 5)) ^ (rl & 31u);
-                *reinterpret_cast<r9vx_u32x2 *>(orow + 8u * chunk) =
-                    r9vx_u32x2{pack_h2h((_Float16)(acc[t][j][4 * g] * f), (_Float16)(acc[t][j][4 * g + 1] * f)),
-                               pack_h2h((_Float16)(acc[t][j][4 * g + 2] * f), (_Float16)(acc[t][j][4 * g + 3] * f))};
-            }
-        if (lane < 32 && rl < rows) oscale[(uint64_t)(pos0 + rl) * nblk + blk] = ldexpf(1.0f, e - 15);
-    }
-    __syncthreads();
-    const uint32_t q = lane & 31;
+                for (int g = 0; g < 4; ++g) {
+                    const uint32_t chunk = (16u * cq + 8u * j + 2u * g + (lane >> 5)) ^ (rl & 31u);
+                    *reinterpret_cast<r9vx_u32x2 *>(orow + 8u * chunk) =
+                        r9vx_u32x2{pack_h2h((_Float16)(acc[t][j][4 * g] * f), (_Float16)(acc[t][j][4 * g + 1] * f)),
+                                   pack_h2h((_Float16)(acc[t][j][4 * g + 2] * f), (_Float16)(acc[t][j][4 * g + 3] * f))};
+                }
+            if (lane < 32 && rl < rows) oscale[(uint64_t)(pos0 + rl) * nblk + blk] = ldexpf(1.0f, e - 15);
+        }
+        __syncthreads();
+        const uint32_t q = lane & 31;
 #pragma unroll 4
-    for (uint32_t i = 0; i < 16; ++i) {
-        const uint32_t R = 16 * i + 2 * wv + (lane >> 5);
-        if (R >= rows) break; /* rows grow with i */
-        const uint32_t s = R & 31u;
-        r9vx_u32x4 v = *reinterpret_cast<const r9vx_u32x4 *>(ot + R * 512u + 16u * (q ^ (s >> 1)));
-        if (s & 1u) v = r9vx_u32x4{v.z, v.w, v.x, v.y}; /* the granule's halves were swapped */
-        *reinterpret_cast<r9vx_u32x4 *>(o16 + (uint64_t)(pos0 + R) * a.dm + n0 + 8 * q) = v;
+        for (uint32_t i = 0; i < 16; ++i) {
+            const uint32_t R = 16 * i + 2 * wv + (lane >> 5);
+            if (R >= rows) break; /* rows grow with i */
+            const uint32_t s = R & 31u;
+            r9vx_u32x4 v = *reinterpret_cast<const r9vx_u32x4 *>(ot + R * 512u + 16u * (q ^ (s >> 1)));
+            if (s & 1u) v = r9vx_u32x4{v.z, v.w, v.x, v.y}; /* the granule's halves were swapped */
+            *reinterpret_cast<r9vx_u32x4 *>(o16 + (uint64_t)(pos0 + R) * a.dm + n0 + 8 * q) = v;
+        }
+    };
+    const uint32_t n0a = nt * PASSES * 256;
+    r9vx_f32x16 acc[4][2];
+    m3_run<DN, true, true>(nr, rows <= 128, sm, a.h16, aoff, weights(n0a), nk, tid, wv, lut, 128 * rh, 64 * cq,
+                           64 * cq + 32, acc, bst, fill_steps);
+    if constexpr (PASSES == 1) {
+        __syncthreads();
+        epilogue(n0a, acc);
+    } else {
+        const M3WRow wb = weights(n0a + 256);
+        r9vx_u32x4 pay[4], hnext;
+        m3_issue_head<DN>(wb, tid, pay, hnext);
+        __syncthreads();
+        epilogue(n0a, acc);
+        __syncthreads(); /* the staged tile is read before the next block's copies */
+        /* P0 and H0 have landed (and the epilogue's stores are done) before the
+         * loop takes their registers: its entry may copy them */
+        wait_vm<0>();
+        touch_pay(pay[0]);
+        touch_pay(hnext);
+        m3_run_pre<DN, true, true>(nr, sm, a.h16, aoff, wb, nk, tid, wv, lut, 128 * rh, 64 * cq, 64 * cq + 32, acc, bst,
+                                   pay, hnext);
+        __syncthreads();
+        epilogue(n0a + 256, acc);
     }
 }
 
@@ -705,9 +733,19 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
         }
     }
     if (part == 0 || part == 2) {
+        /* the 256-row Q4_K down GEMM takes two column blocks per workgroup when Dm / 256 is even */
+        const bool two = (p.dm / 256) % 2 == 0;
+        const dim3 gdn3_2(tiles3_8 * (p.dm / 512));
         switch (p.scheme_dn) {
-        case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL(moe_dn_m3_kernel<R9VX_SCHEME_Q4_K>, gdn3, dim3(512), 0, s, a); break;
-        case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(moe_dn_m3_kernel<R9VX_SCHEME_IQ4_XS>, gdn3, dim3(512), 0, s, a); break;
+        case R9VX_SCHEME_Q4_K:
+            if (two)
+                hipLaunchKernelGGL((moe_dn_m3_kernel<R9VX_SCHEME_Q4_K, 2>), gdn3_2, dim3(512), 0, s, a);
+            else
+                hipLaunchKernelGGL((moe_dn_m3_kernel<R9VX_SCHEME_Q4_K, 1>), gdn3, dim3(512), 0, s, a);
+            break;
+        case R9VX_SCHEME_IQ4_XS: /* (its codebook table leaves no registers for the two-block form) */
+            hipLaunchKernelGGL((moe_dn_m3_kernel<R9VX_SCHEME_IQ4_XS, 1>), gdn3, dim3(512), 0, s, a);
+            break;
         case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_IQ3_S>, gdn, dim3(256), 0, s, a); break;
         case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_Q8_0>, gdn, dim3(256), 0, s, a); break;
         default: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_Q6_K>, gdn, dim3(256), 0, s, a); break;

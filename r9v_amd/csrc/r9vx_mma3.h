@@ -339,25 +339,42 @@ __device__ __forceinline__ uint32_t m3_bsd(const uint32_t *bst, uint32_t k, uint
  * of B(k + 1), each of whose four 16-byte granules is written into the other
  * B tile as soon as it is whole, then a wait for the A(k + 1) copy.
  */
-template <int SCHEME, int NR, bool TR, bool BS, class Hook>
-__device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
-                                               const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave,
-                                               const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
-                                               r9vx_f32x16 (&acc)[4][2], const uint32_t *bst, Hook &hook) {
-    const uint32_t lane = tid & 63, c = m3_brow(tid), hh = tid & 1, bsw = m2_swz(c);
-    const uint32_t a_lds = m3_lds_addr(&sm.a[0][0]);
-    r9vx_u32x4 pay[4], hnext, hcur;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pay[i] = r9vx_u32x4{0u, 0u, 0u, 0u};
-    hnext = r9vx_u32x4{0u, 0u, 0u, 0u};
-    /* prologue: P0 H0 | A0 | P1 P2 P3; B(0) decoded into B tile 0 */
+/* The first prologue loads of the main loop -- payload 0 and the first
+ * block header, in the prologue's order -- issued ahead by a caller that
+ * still has LDS work to do (an epilogue); m3_run_pre then runs the loop from
+ * them.  Stores the caller issues in between are waited for with them. */
+template <int SCHEME>
+__device__ __forceinline__ void m3_issue_head(const M3WRow &w, uint32_t tid, r9vx_u32x4 (&pay)[4], r9vx_u32x4 &hnext) {
+    const uint32_t hh = tid & 1;
+    pay[0] = hnext = r9vx_u32x4{0u, 0u, 0u, 0u};
     m3_load_pay<SCHEME>(w, 0, hh, pay[0]);
     m3_load_hdr<SCHEME>(w, 0, hnext);
+}
+
+/* PRE: the caller issued P0 H0 (m3_issue_head), and perhaps stores after
+ * them; the prologue then issues what the plain one issues after them (the
+ * A(0) copy, payloads 1-3) and goes on with the same counted waits. */
+template <int SCHEME, int NR, bool TR, bool BS, bool PRE, class Hook>
+__device__ __forceinline__ void m3_mainloop_core(M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
+                                                 const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave,
+                                                 const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
+                                                 r9vx_f32x16 (&acc)[4][2], const uint32_t *bst, Hook &hook,
+                                                 r9vx_u32x4 (&pay)[4], r9vx_u32x4 &hnext) {
+    const uint32_t lane = tid & 63, c = m3_brow(tid), hh = tid & 1, bsw = m2_swz(c);
+    const uint32_t a_lds = m3_lds_addr(&sm.a[0][0]);
+    r9vx_u32x4 hcur;
+    /* prologue: P0 H0 | A0 | P1 P2 P3; B(0) decoded into B tile 0 */
+    if constexpr (!PRE) {
+        pay[0] = hnext = r9vx_u32x4{0u, 0u, 0u, 0u};
+        m3_load_pay<SCHEME>(w, 0, hh, pay[0]);
+        m3_load_hdr<SCHEME>(w, 0, hnext);
+    }
+    pay[1] = pay[2] = pay[3] = r9vx_u32x4{0u, 0u, 0u, 0u};
     m3_dma_a(a_lds, abase, aoff, 0, wave);
     m3_load_pay<SCHEME>(w, 1, hh, pay[1]);
     m3_load_pay<SCHEME>(w, 2, hh, pay[2]);
     m3_load_pay<SCHEME>(w, 3 < nk ? 3 : nk - 1, hh, pay[3]);
-    wait_vm<7>(); /* P0, H0 (and the caller's loads issued before) */
+    wait_vm<7>(); /* P0, H0 (and the loads and stores issued before) */
     touch_pay(pay[0]);
     touch_pay(hnext);
     hcur = hnext;
@@ -399,6 +416,16 @@ __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, co
 #pragma unroll
     for (int i = 0; i < 4; ++i) touch_pay(pay[i]);
     touch_pay(hnext);
+}
+
+template <int SCHEME, int NR, bool TR, bool BS, class Hook>
+__device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
+                                            const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave,
+                                            const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
+                                            r9vx_f32x16 (&acc)[4][2], const uint32_t *bst, Hook &hook) {
+    r9vx_u32x4 pay[4], hnext;
+    m3_mainloop_core<SCHEME, NR, TR, BS, false>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst,
+                                                hook, pay, hnext);
 }
 
 /*
@@ -539,6 +566,39 @@ __device__ __forceinline__ void m3_run(uint32_t nr, bool half, M3Lds &sm, const 
     default: m3_mainloop<SCHEME, 0, TR, BS>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst, hook); break;
     }
 #undef R9VX_M3_CASE
+}
+
+/* m3_run's full-tile loop (more than 128 rows) from loads m3_issue_head
+ * issued; no hook. */
+template <int SCHEME, bool TR = false, bool BS = false>
+__device__ __forceinline__ void m3_run_pre(uint32_t nr, M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
+                                           const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave,
+                                           const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
+                                           r9vx_f32x16 (&acc)[4][2], const uint32_t *bst, r9vx_u32x4 (&pay)[4],
+                                           r9vx_u32x4 &hnext) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[t][j][r] = 0.f;
+    M3NoHook hook;
+#define R9VX_M3P_CASE(N)                                                                                          \
+    case N:                                                                                                       \
+        m3_mainloop_core<SCHEME, N, TR, BS, true>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc,   \
+                                                  bst, hook, pay, hnext);                                         \
+        break;
+    switch (nr) {
+        R9VX_M3P_CASE(4)
+        R9VX_M3P_CASE(3)
+        R9VX_M3P_CASE(2)
+        R9VX_M3P_CASE(1)
+    default:
+        m3_mainloop_core<SCHEME, 0, TR, BS, true>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst,
+                                                  hook, pay, hnext);
+        break;
+    }
+#undef R9VX_M3P_CASE
 }
 
 }  // namespace r9vx
