@@ -279,6 +279,32 @@ def test_gemm_register_decoded_epilogues(n):
     check_bf16_out(got, got32, ref, "bf16 out")
 
 
+# The 256-column GEMM (gemm3_kernel) cuts each weight block's rows into
+# chunks sized to fill whole rounds of the CUs; these shapes reach its plans:
+# one block, one 32-row tile per chunk, every block with the same chunk
+# count (the XCD band order), two chunk counts across blocks, several
+# rounds, ragged last row tiles.
+@pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])
+@pytest.mark.parametrize("m,n", [(9, 256), (700, 2560), (2048, 4096), (1100, 5376), (2600, 14336)])
+def test_gemm_row_chunk_plans(scheme, m, n):
+    k = 512
+    rows = np.arange(m) if m * n <= 4_000_000 else np.unique(np.concatenate([np.arange(0, m, 7), [m - 1]]))
+    got, ref = _gemm_case(scheme, n, k, m, 7500 + m, rows=rows)
+    check_close(got, ref, f"m={m} n={n}")
+
+
+def test_gemm_row_chunk_plans_keep_row_bits():
+    """The same rows under two chunk plans of one static (m = 1100 and 2600 at
+    m_bucket 4096, n = 14336: one round of uniform chunks, three rounds of two
+    chunk counts) come out bit-equal."""
+    n, k = 14336, 512
+    w = dev(synth.quant_weights(O.Q4_K, 7601, n, k))
+    x = synth.normal_bf16(7602, (2600, k))
+    big = host(ffi.matmul(w, O.Q4_K, n, k, bf16_dev(x), m_bucket=4096).view(torch.int32))
+    small = host(ffi.matmul(w, O.Q4_K, n, k, bf16_dev(x[:1100]), m_bucket=4096).view(torch.int32))
+    assert np.array_equal(small, big[:1100])
+
+
 def test_gemm_epilogues_bf16_out():
     got, ref = _gemm_case(O.IQ4_XS, 200, 512, 40, 7200, bias=True)
     check_close(got, ref, "bias")
