@@ -20,7 +20,7 @@ measured ceilings, and CPU figures for every config: the oracle (a scalar C
 restatement of R9V's T0 path) on a bounded sample on this host, 1 thread,
 plus an all-threads OpenMP variant for the grouped MoE GEMM.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c0,c1,c2,c3,ceilings]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c0,c1,c2,c3,gemv_n,schemes,ceilings]
     python bench.py --pmc-case c4|c3|c2|c1m5|c0|gemvn|ceil  # short fixed run for rocprofv3 --pmc
     python bench.py --pmc-summary DIR ... [--pmc-kernels a,b]  # FETCH_SIZE/WRITE_SIZE dirs -> traffic text
 """
@@ -57,7 +57,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU work per baseline sample")
-    ap.add_argument("--only", default="", help="comma list of extras: c0,c1,c2,c3,gemv_n,ceilings ('none' for the "
+    ap.add_argument("--only", default="", help="comma list of extras: c0,c1,c2,c3,gemv_n,schemes,ceilings ('none' for the "
                                                "headline only)")
     ap.add_argument("--pmc-case", default="", help="run a short fixed workload for counter collection: c4, c3, c2, c1m5, "
                                                    "c0, gemvn, ceil")
@@ -320,6 +320,50 @@ def c2_extra(torch, ffi, synth, gsynth, steps, cpu_s, steps_only=False):
                                 f"per FLOP"}
     del ws, w0
     torch.cuda.empty_cache()
+    return out
+
+
+def schemes_extra(torch, ffi, synth, gsynth, steps):
+    """The other weight types at the headline shapes (measurement only; their
+    kernels are the 128-row LDS-decoded tiles): the configs[2] dense GEMM and
+    the configs[4] moe_ffn step with Q8_0, Q6_K and IQ3_S weights in their
+    device layouts (split body + f16 d array; 112-byte IQ3_S blocks)."""
+    out = {"gemm_c2_shape": {}, "moe_ffn_c4_shape": {}}
+    m, n, k = 2048, 14336, 4096
+    x_host = synth.normal_bf16(synth.seed_for("c2", "x"), (m, k))
+    x = torch.from_numpy(x_host.view(np.int16)).cuda().view(torch.bfloat16)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    names = {ffi.Q8_0: "Q8_0", ffi.Q6_K: "Q6_K", ffi.IQ3_S: "IQ3_S"}
+    for scheme, name in names.items():
+        body, sc = ffi.repack(gsynth.quant_weights_gpu(torch, scheme, 501 + scheme, n, k), scheme, n, k)
+        st = ffi.matmul_static(n, k, scheme, ffi.BF16, ffi.BF16, m_bucket=m)
+        wsp = torch.empty(ffi.matmul_workspace_bytes(st), dtype=torch.uint8, device="cuda")
+        ms, _ = timed_steps(torch, lambda i: ffi.matmul(body, scheme, n, k, x, out_dtype=ffi.BF16, y=y, workspace=wsp,
+                                                        w_scales=sc), steps, 2)
+        out["gemm_c2_shape"][name] = {"ms_per_step": round(ms, 4), **mfma(2 * m * n * k, ms)}
+        del body, sc, wsp
+        torch.cuda.empty_cache()
+    del x, y
+    t, e, kk, dm, dff = C4_T, C4_E, C4_K, C4_DM, C4_DFF
+    xm = torch.from_numpy(synth.normal_bf16(synth.seed_for("c4", "x"), (t, dm)).view(np.int16)).cuda().view(
+        torch.bfloat16)
+    ids = torch.empty((t, kk), dtype=torch.int32, device="cuda")
+    wts = torch.empty((t, kk), dtype=torch.float32, device="cuda")
+    ffi.moe_route(torch.from_numpy(synth.zipf_logits(synth.seed_for("c4", "logits"), t, e)).cuda(), kk, ids=ids,
+                  weights=wts)
+    ym = torch.empty((t, dm), dtype=torch.float32, device="cuda")
+    for scheme, name in names.items():
+        gu, gus = ffi.repack(gsynth.quant_weights_gpu(torch, scheme, 511 + scheme, e * 2 * dff, dm), scheme,
+                             e * 2 * dff, dm)
+        dn, dns = ffi.repack(gsynth.quant_weights_gpu(torch, scheme, 521 + scheme, e * dm, dff), scheme, e * dm, dff)
+        st = ffi.ffn_static(t, e, kk, dm, dff, 0, scheme, scheme)
+        wsp = torch.empty(ffi.ffn_workspace_bytes(st), dtype=torch.uint8, device="cuda")
+        ms, _ = timed_steps(torch, lambda i: ffi.moe_ffn(xm, ids, wts, gu, dn, e, dff, gate_up_scheme=scheme,
+                                                         down_scheme=scheme, y=ym, workspace=wsp,
+                                                         w_gate_up_scales=gus, w_down_scales=dns), steps, 2)
+        out["moe_ffn_c4_shape"][name] = {"ms_per_step": round(ms, 4), **mfma(C4_FLOPS, ms)}
+        del gu, gus, dn, dns, wsp
+        torch.cuda.empty_cache()
     return out
 
 
@@ -635,6 +679,10 @@ def main():
         log("c3 ...")
         extras["c3"] = c3_extra(torch, ffi, synth, gsynth, args.steps, cpu_s)
         log(f"  {extras['c3']}")
+    if want("schemes"):
+        log("Q8_0 / Q6_K / IQ3_S at the configs[2] and configs[4] shapes ...")
+        extras["other_schemes"] = schemes_extra(torch, ffi, synth, gsynth, 5)
+        log(f"  {extras['other_schemes']}")
     if want("ceilings"):
         extras["measured_ceilings"] = ceilings(torch, ffi)
         log(f"  ceilings {extras['measured_ceilings']}")
