@@ -301,7 +301,11 @@ __global__ __launch_bounds__(512, 1) void gemm3_kernel(GemmArgs a) {
         const uint32_t r = dma_row(wv, i, lane);
         aoff[i] = ((m0 + (r < rows ? r : 0)) * a.k + 8 * dma_group(r, lane)) * 2u;
     }
-    const M3WRow w{m3_uniform(a.w + (uint64_t)n0 * a.w_row_stride), m3_brow(tid) * (uint32_t)a.w_row_stride};
+    M3WRow w{m3_uniform(a.w + (uint64_t)n0 * a.w_row_stride), m3_brow(tid) * (uint32_t)a.w_row_stride};
+    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+        w.sbase = m3_uniform(reinterpret_cast<const uint8_t *>(a.ws + (uint64_t)n0 * a.ws_row));
+        w.soff = m3_brow(tid) * a.ws_row * 2u;
+    }
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
@@ -465,9 +469,21 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
      * addressing bound -- never from the launch's row count: a row's outputs
      * are the same bits whatever rows share the launch, at whatever index,
      * and in every bucket above the decode GEMV's.  Q4_K / IQ4_XS run the
-     * 256 x 256 tiles (gemm3 for N % 256 == 0, gemm2 otherwise); Q8_0 / Q6_K /
-     * IQ3_S the 128-row LDS-decoded tile. */
+     * 256 x 256 tiles (gemm3 for N % 256 == 0, gemm2 otherwise), Q8_0 gemm3
+     * for N % 256 == 0; Q6_K / IQ3_S, and Q8_0 otherwise, the 128-row
+     * LDS-decoded tile. */
     const bool split = p.scheme == R9VX_SCHEME_Q8_0 || p.scheme == R9VX_SCHEME_Q6_K || p.scheme == R9VX_SCHEME_IQ3_S;
+    const bool m3_shape = p.n % kM3Cols == 0 && (uint64_t)p.m_bucket * p.k < (1ull << 31);
+    if (p.scheme == R9VX_SCHEME_Q8_0 && m3_shape) {
+        /* Q8_0's step halves are whole blocks: IQ4_XS's group order */
+        hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3((p.m + 3) / 4), dim3(256), 0, stream, p.x, p.m, p.k,
+                           x16, scale);
+        a.m_tiles = (p.m + kM2Rows - 1) / kM2Rows;
+        a.n_tiles = (p.n + kM2Cols - 1) / kM2Cols;
+        const dim3 grid3(plan_chunks(a, r9vx_device_cus()));
+        hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_Q8_0>), grid3, dim3(512), 0, stream, a);
+        return (int)hipGetLastError();
+    }
     if (!split) {
         if (p.scheme == R9VX_SCHEME_Q4_K)
             hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3((p.m + 3) / 4), dim3(256), 0, stream, p.x, p.m, p.k, x16,
@@ -496,7 +512,7 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     a.m_tiles = (p.m + 127) / 128;
     a.n_tiles = (p.n + 255) / 256;
     dim3 grid(a.m_tiles * a.n_tiles);
-    /* Q8_0 / Q6_K / IQ3_S take this LDS-decoded tile (their steps do not
+    /* Q6_K / IQ3_S (and Q8_0 at N % 256 != 0) take this LDS-decoded tile (their steps do not
      * fit the register-decoded core's 16-byte lane payload). */
     switch (p.scheme) {
     case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q6_K, 128, 1>), grid, dim3(256), 0, stream, a); break;

@@ -1130,7 +1130,7 @@ int r9vx_moe_sort_stage(const r9vx_moe_problem &p, const MoeLayout &L, hipStream
         a.x16 = reinterpret_cast<_Float16 *>(p.ws + L.x16);
         a.xscale = reinterpret_cast<float *>(p.ws + L.xscale);
         a.dm = p.dm;
-        a.xperm = p.scheme_gu == R9VX_SCHEME_Q4_K || p.scheme_gu == R9VX_SCHEME_IQ4_XS ? p.scheme_gu : 0u;
+        a.xperm = r9vx_group_order(p.scheme_gu);
         constexpr uint32_t kCum[5] = {0, 20, 40, 80, 100};
         for (int i = 1; i <= 4; ++i) xr[i] = (uint32_t)((uint64_t)p.t * kCum[i] / 100);
         *x16_done = true;

@@ -92,8 +92,8 @@ constexpr int kStage = 32 * kMT * 128;       /* 16 KiB per A stage */
     __shared__ __attribute__((aligned(16))) float lutf[512];          \
     uint8_t *const stages[4] = {st0, st1, st2, st3};
 
-/* Gate/up experts the r9vx_mma3.h loop does not decode (IQ3_S, and Q8_0 /
- * Q6_K in the split layout): the LDS-decoded main loop of r9vx_mma.h (a 128 x
+/* Gate/up experts the r9vx_mma3.h loop does not decode (IQ3_S, and Q6_K in
+ * the split layout): the LDS-decoded main loop of r9vx_mma.h (a 128 x
  * 256 tile; thread t decodes weight row t of the tile into LDS: threads
  * 0..127 the gate rows j0..j0+127, threads 128..255 the up rows of the same
  * columns, so tile column c pairs with column c + 128), with the activations
@@ -164,8 +164,9 @@ __global__ __launch_bounds__(256, 2) void moe_gu_lds_kernel(GroupedArgs a) {
  * hexp and hbe for the down GEMMs), then lane l writes group l % 8 of K
  * step l / 8 (+ 8 per pass) as 8 fp16 in the down scheme's group order,
  * scaled by 2^-e. */
-/* K position of element i of group q in a 64-wide step of the h16 rows: the
- * group order of the r9vx_mma3.h schemes, natural order for the others. */
+/* K position of element i of group q in a 64-wide step of the h16 rows;
+ * DN: the rows' order (r9vx_group_order of the down scheme: the group order
+ * of the r9vx_mma3.h loop, 0 natural). */
 template <int DN>
 __device__ __forceinline__ uint32_t h_group_k(uint32_t q, uint32_t i) {
     if constexpr (DN == R9VX_SCHEME_Q4_K || DN == R9VX_SCHEME_IQ4_XS)
@@ -303,8 +304,8 @@ __global__ __launch_bounds__(256) void h_fix_kernel(GroupedArgs a, uint32_t nrow
 
 /* ---------------------------------------------------------------- down, LDS-decoded */
 
-/* Down experts the r9vx_mma3.h loop does not decode (IQ3_S, and Q8_0 / Q6_K
- * in the split layout): the LDS-decoded main loop of r9vx_mma.h over a
+/* Down experts the r9vx_mma3.h loop does not decode (IQ3_S, and Q6_K in the
+ * split layout): the LDS-decoded main loop of r9vx_mma.h over a
  * 128-row tile of h16 rows (natural K order) and output columns n0 .. n0 +
  * 255 (thread t decodes weight row n0 + t).  The accumulators pass through
  * a 32 x 256 f32 LDS stage, 32 rows at a time; thread t then owns 32
@@ -428,7 +429,11 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     }
     const uint32_t c = m3_brow(tid);
     const uint32_t wr = c < 128 ? j0 + c : a.dff + j0 + (c - 128);
-    const M3WRow w{m3_uniform(a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes), wr * (uint32_t)a.gu_row_bytes};
+    M3WRow w{m3_uniform(a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes), wr * (uint32_t)a.gu_row_bytes};
+    if constexpr (GU == R9VX_SCHEME_Q8_0) {
+        w.sbase = m3_uniform(reinterpret_cast<const uint8_t *>(a.s_gu + (uint64_t)expert * 2 * a.dff * a.gu_srow));
+        w.soff = wr * a.gu_srow * 2u;
+    }
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
@@ -571,8 +576,13 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
      * block's weight payload loads are issued before the first block's
      * epilogue, so that their latency passes under it. */
     auto weights = [&](uint32_t n0) {
-        return M3WRow{m3_uniform(a.w_dn + ((uint64_t)expert * a.dm + n0) * a.dn_row_bytes),
-                      m3_brow(tid) * (uint32_t)a.dn_row_bytes};
+        M3WRow w{m3_uniform(a.w_dn + ((uint64_t)expert * a.dm + n0) * a.dn_row_bytes),
+                 m3_brow(tid) * (uint32_t)a.dn_row_bytes};
+        if constexpr (DN == R9VX_SCHEME_Q8_0) {
+            w.sbase = m3_uniform(reinterpret_cast<const uint8_t *>(a.s_dn + ((uint64_t)expert * a.dm + n0) * a.dn_srow));
+            w.soff = m3_brow(tid) * a.dn_srow * 2u;
+        }
+        return w;
     };
     const uint32_t nk = a.dff / kTileK;
     auto epilogue = [&](uint32_t n0, r9vx_f32x16 (&acc)[4][2]) {
@@ -680,7 +690,7 @@ static GroupedArgs grouped_args(const r9vx_moe_problem &p, const MoeLayout &L) {
     a.dff = p.dff;
     a.p = p.t * p.k;
     a.shared = p.shared;
-    a.h_order = p.scheme_dn == R9VX_SCHEME_Q4_K || p.scheme_dn == R9VX_SCHEME_IQ4_XS ? p.scheme_dn : 0u;
+    a.h_order = r9vx_group_order(p.scheme_dn);
     return a;
 }
 
@@ -696,7 +706,7 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
     GroupedArgs a = grouped_args(p, L);
     if (part == 0 && !x16_done) {
         int rc = r9vx_launch_x_to_f16(p.x, p.t, p.dm, reinterpret_cast<_Float16 *>(p.ws + L.x16),
-                                      reinterpret_cast<float *>(p.ws + L.xscale), p.scheme_gu, s);
+                                      reinterpret_cast<float *>(p.ws + L.xscale), r9vx_group_order(p.scheme_gu), s);
         if (rc) return rc;
     }
     /* upper bounds on row tiles: ceil(P/TM) + one partial tile per work item */
@@ -711,8 +721,8 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
         switch (p.scheme_gu) {
         case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_IQ4_XS>, ggu3, dim3(512), 0, s, a); break;
         case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q4_K>, ggu3, dim3(512), 0, s, a); break;
+        case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q8_0>, ggu3, dim3(512), 0, s, a); break;
         case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_IQ3_S>, ggu, dim3(256), 0, s, a); break;
-        case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_Q8_0>, ggu, dim3(256), 0, s, a); break;
         default: hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_Q6_K>, ggu, dim3(256), 0, s, a); break;
         }
     }
@@ -721,15 +731,14 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
     /* the 256-row gate/up writes h16 at a scale per 128-column block, which
      * the 256-row down GEMM takes as it is (up to kM3MaxBlk blocks); the
      * LDS-decoded down kernels take one scale per row */
-    const bool gu_m3 = p.scheme_gu == R9VX_SCHEME_IQ4_XS || p.scheme_gu == R9VX_SCHEME_Q4_K;
-    const bool dn_m3 = p.scheme_dn == R9VX_SCHEME_IQ4_XS || p.scheme_dn == R9VX_SCHEME_Q4_K;
+    const bool gu_m3 = r9vx_m3_scheme(p.scheme_gu), dn_m3 = r9vx_m3_scheme(p.scheme_dn);
     if (gu_m3 && (!dn_m3 || p.dff / 128 > kM3MaxBlk) && (part == 0 || part == 1))
         hipLaunchKernelGGL(h_fix_kernel, dim3((nrows + 255) / 256), dim3(256), 0, s, a, nrows);
     if (!gu_m3 && part == 0) {
-        switch (p.scheme_dn) {
+        switch (a.h_order) {
         case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q4_K>, gh, dim3(256), 0, s, a, nrows); break;
         case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, gh, dim3(256), 0, s, a, nrows); break;
-        default: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q8_0>, gh, dim3(256), 0, s, a, nrows); break; /* natural */
+        default: hipLaunchKernelGGL(h_to_f16_kernel<0>, gh, dim3(256), 0, s, a, nrows); break; /* natural */
         }
     }
     if (part == 0 || part == 2) {
@@ -746,8 +755,8 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
         case R9VX_SCHEME_IQ4_XS: /* (its codebook table leaves no registers for the two-block form) */
             hipLaunchKernelGGL((moe_dn_m3_kernel<R9VX_SCHEME_IQ4_XS, 1>), gdn3, dim3(512), 0, s, a);
             break;
+        case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL((moe_dn_m3_kernel<R9VX_SCHEME_Q8_0, 1>), gdn3, dim3(512), 0, s, a); break;
         case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_IQ3_S>, gdn, dim3(256), 0, s, a); break;
-        case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_Q8_0>, gdn, dim3(256), 0, s, a); break;
         default: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_Q6_K>, gdn, dim3(256), 0, s, a); break;
         }
     }

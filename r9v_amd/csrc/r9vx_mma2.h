@@ -142,6 +142,15 @@ struct BScale {
 template <int SCHEME, int KS>
 __device__ __forceinline__ BScale bscale(const r9vx_u32x4 &hd, uint32_t h) {
     BScale s;
+    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+        /* hd: the f16 d of the eight 32-weight blocks of a 256-weight block;
+         * step KS, half h is block 2 KS + h */
+        const uint32_t dw = KS == 0 ? hd.x : KS == 1 ? hd.y : KS == 2 ? hd.z : hd.w;
+        s.dl0 = r9vx_f16_to_f32((uint16_t)(dw >> (16 * h)));
+        s.c0 = -1152.f * s.dl0; /* exact: 1152 = 9 * 2^7 */
+        s.nml0 = s.dl1 = s.nml1 = s.c1 = 0.f;
+        return s;
+    }
     const float d = r9vx_f16_to_f32((uint16_t)(hd.x & 0xFFFF));
     if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
         const float dmin = r9vx_f16_to_f32((uint16_t)(hd.x >> 16));

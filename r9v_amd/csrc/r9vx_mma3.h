@@ -7,9 +7,10 @@
  *   B (weights): thread t decodes half hh = t & 1 of weight row m3_brow(t)
  *     for the next K step while the MFMAs of the current one run: its 16
  *     payload bytes (groups 4hh .. 4hh+3 of the step, r9vx_mma2.h's K group
- *     order) become 32 fp16 by the exact f32 formula and one rounding, and
- *     each 16-byte granule goes to the other B tile as soon as it is whole.
- *     Every weight is decoded once per 256 output rows.
+ *     order; Q8_0: the 32 quant bytes of one block) become 32 fp16 by the
+ *     exact f32 formula and one rounding, and each 16-byte granule goes to
+ *     the other B tile as soon as it is whole.  Every weight is decoded once
+ *     per 256 output rows.
  *   A (activations, fp16 in the same group order): direct global->LDS copies
  *     into the other A stage, one step ahead (tiles of at most 128 rows:
  *     m3_mainloop_half's ring of four 128-row slots, three steps ahead).
@@ -67,11 +68,19 @@ __device__ __forceinline__ uint32_t m3_lds_addr(const void *p) {
 }
 
 /* Weight row of the decoding thread: a uniform base plus a 32-bit offset
- * (row offset; the step's block / payload offsets are added per load). */
+ * (row offset; the step's block / payload offsets are added per load); the
+ * split layout (Q8_0) keeps the row's f16 d values at sbase + soff. */
 struct M3WRow {
     const uint8_t *base; /* uniform */
     uint32_t off;        /* this thread's row */
+    const uint8_t *sbase = nullptr; /* uniform */
+    uint32_t soff = 0;
 };
+
+/* Q8_0: a thread's half of a K step is one whole block, 32 int8 quants (two
+ * 16-byte loads), so its payload ring holds two steps in the registers the
+ * 4-bit schemes use for four. */
+constexpr bool m3_wide(int s) { return s == R9VX_SCHEME_Q8_0; }
 
 /* A pointer the caller knows to be wave-uniform, moved to scalar registers
  * (the loads take it as their SGPR base whatever the compiler's divergence
@@ -91,13 +100,30 @@ __device__ __forceinline__ void m3_load_pay(const M3WRow &w, uint32_t kt, uint32
     asm volatile("global_load_dwordx4 %0, %1, %2" : "+v"(p) : "v"(off), "s"(w.base) : "memory");
 }
 
+/* Q8_0 (m3_wide): step kt's block 2 kt + hh, quants 0-15 into p0 and 16-31
+ * into p1. */
+__device__ __forceinline__ void m3_load_pay2(const M3WRow &w, uint32_t kt, uint32_t hh, r9vx_u32x4 &p0,
+                                             r9vx_u32x4 &p1) {
+    const uint32_t off = w.off + 64 * kt + 32 * hh;
+    asm volatile("global_load_dwordx4 %0, %2, %3\n\tglobal_load_dwordx4 %1, %2, %3 offset:16"
+                 : "+v"(p0), "+v"(p1)
+                 : "v"(off), "s"(w.base)
+                 : "memory");
+}
+
 /* Q4_K: the 16-byte header; IQ4_XS: the block's first 16 bytes (its 8-byte
  * header and 8 payload bytes, inside the 136-byte block), of which .x/.y are
- * used. */
+ * used; Q8_0: the f16 d values of the eight 32-weight blocks of 256-weight
+ * block blk. */
 template <int SCHEME>
 __device__ __forceinline__ void m3_load_hdr(const M3WRow &w, uint32_t blk, r9vx_u32x4 &hd) {
-    const uint32_t off = w.off + blk * (SCHEME == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : R9VX_IQ4XS_BYTES);
-    asm volatile("global_load_dwordx4 %0, %1, %2" : "+v"(hd) : "v"(off), "s"(w.base) : "memory");
+    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+        const uint32_t off = w.soff + 16 * blk;
+        asm volatile("global_load_dwordx4 %0, %1, %2" : "+v"(hd) : "v"(off), "s"(w.sbase) : "memory");
+    } else {
+        const uint32_t off = w.off + blk * (SCHEME == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : R9VX_IQ4XS_BYTES);
+        asm volatile("global_load_dwordx4 %0, %1, %2" : "+v"(hd) : "v"(off), "s"(w.base) : "memory");
+    }
 }
 
 /* Direct global->LDS copy of one K step of A (256 rows x 64 fp16, group
@@ -142,11 +168,31 @@ __device__ __forceinline__ void m3_init_iq4_lut(uint32_t *lut, uint32_t tid, uin
  * iq.rs:578-598) evaluated in one fused operation and rounded once to fp16
  * (Q4_K: up to the f32 rounding of the precomputed addend, below).
  * Returns the two packed dwords {low pair, high pair}.  IQ4_XS: kv0 / kv1
- * are the bytes' codebook pairs {kv[low], kv[high]}. */
+ * are the bytes' codebook pairs {kv[low], kv[high]}.  Q8_0: the low pair is
+ * quants 4q + 2m, +1 (bytes 2m, 2m + 1 of dword q of the first 16 quants,
+ * dw), the high pair the same bytes of the second 16 (dw2). */
 template <int SCHEME>
-__device__ __forceinline__ void m3_dec_unit(uint32_t dw, int m, const BScale &sc, uint32_t kv0, uint32_t kv1,
-                                            uint32_t &lo2, uint32_t &hi2) {
-    if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
+__device__ __forceinline__ void m3_dec_unit(uint32_t dw, uint32_t dw2, int m, const BScale &sc, uint32_t kv0,
+                                            uint32_t kv1, uint32_t &lo2, uint32_t &hi2) {
+    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+        /* q + 128 (the byte XOR 0x80) under a 0x64 byte reads as the fp16
+         * 1152 + q; w = d (1152 + q) - 1152 d, fused: d q is exact in f32
+         * (11 + 8 significant bits) and -1152 d too, so the one rounding is
+         * fp16(d q), the f32 value rounded once. */
+        const uint32_t sel = m ? 0x04030402u : 0x04010400u;
+        const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, dw ^ 0x80808080u, sel);
+        const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, dw2 ^ 0x80808080u, sel);
+        uint32_t a, b;
+        asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(a) : "v"(sc.dl0), "v"(lo), "v"(sc.c0));
+        asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+            : "+v"(a) : "v"(sc.dl0), "v"(lo), "v"(sc.c0));
+        asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(b) : "v"(sc.dl0), "v"(hi), "v"(sc.c0));
+        asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+            : "+v"(b) : "v"(sc.dl0), "v"(hi), "v"(sc.c0));
+        lo2 = a;
+        hi2 = b;
+        asm volatile("" : "+v"(lo2), "+v"(hi2));
+    } else if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
         /* bytes 2m, 2m + 1 each under a 0x64 byte (v_perm), so that their
          * nibbles read as the fp16 pairs {1024 + lo(2m), 1024 + lo(2m+1)}
          * and {1024 + hi(2m), 1024 + hi(2m+1)}; then w = dl (1024 + q) + c
@@ -196,8 +242,9 @@ __device__ __forceinline__ void m3_dec_unit(uint32_t dw, int m, const BScale &sc
 template <int SCHEME, int KS, int NR, bool TR, bool BSTEP = false>
 __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bsm, uint32_t lane, uint32_t arow0,
                                            uint32_t bc0, uint32_t bc1, r9vx_f32x16 (&acc)[4][2],
-                                           const r9vx_u32x4 &pay, const r9vx_u32x4 &hd, uint32_t hh,
-                                           const uint32_t *lut, uint8_t *bdst, uint32_t bsw, uint32_t bsd = 0u) {
+                                           const r9vx_u32x4 &pay, const r9vx_u32x4 &pay2, const r9vx_u32x4 &hd,
+                                           uint32_t hh, const uint32_t *lut, uint8_t *bdst, uint32_t bsw,
+                                           uint32_t bsd = 0u) {
     constexpr bool kIq4 = SCHEME == R9VX_SCHEME_IQ4_XS;
     constexpr int P = 4 * NR; /* MFMA pairs */
     const uint32_t h = lane >> 5, r32 = lane & 31, sw = m2_swz(r32);
@@ -205,6 +252,8 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
     const uint8_t *brow0 = bsm + (bc0 + r32) * 128u, *brow1 = bsm + (bc1 + r32) * 128u;
     auto goff = [&](int s) { return ((4u * h + (uint32_t)s) ^ sw) << 4; };
     const uint32_t dws[4] = {pay.x, pay.y, pay.z, pay.w};
+    /* Q8_0: the block's second 16 quants (unused by the 4-bit schemes) */
+    const uint32_t dws2[4] = {pay2.x, pay2.y, pay2.z, pay2.w};
     /* IQ4_XS codebook pairs of unit u are read kLead pairs before the pair
      * that decodes it (pair dec_pair(u)), so that their LDS latency and bank
      * conflicts overlap MFMAs; those due before pair 0 are read up front. */
@@ -287,7 +336,7 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u)
-            if (dec_pair(u) == i) m3_dec_unit<SCHEME>(dws[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
+            if (dec_pair(u) == i) m3_dec_unit<SCHEME>(dws[u >> 1], dws2[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
         /* granule q of the row is whole once unit 2q + 1 is decoded */
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -299,7 +348,7 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
     if constexpr (P == 0) {
 #pragma unroll
         for (int u = 0; u < 8; ++u)
-            m3_dec_unit<SCHEME>(dws[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
+            m3_dec_unit<SCHEME>(dws[u >> 1], dws2[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             *reinterpret_cast<r9vx_u32x4 *>(bdst + (((4u * hh + q) ^ bsw) << 4)) =
@@ -379,7 +428,7 @@ __device__ __forceinline__ void m3_mainloop_core(M3Lds &sm, const _Float16 *abas
     touch_pay(hnext);
     hcur = hnext;
     hook();
-    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], hcur, hh, lut, sm.b[0] + c * 128u,
+    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], pay[0], hcur, hh, lut, sm.b[0] + c * 128u,
                                  bsw);
     wait_vm<2>(); /* A0, P1 */
     touch_pay(pay[1]);
@@ -400,7 +449,7 @@ __device__ __forceinline__ void m3_mainloop_core(M3Lds &sm, const _Float16 *abas
             hcur = hnext;                                                                                    \
         }                                                                                                    \
         m3_compute<SCHEME, (J + 1) & 3, NR, TR, BS && (J & 1) == 0>(                                          \
-            sm.a[k & 1u], sm.b[k & 1u], lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3], hcur, hh, lut,           \
+            sm.a[k & 1u], sm.b[k & 1u], lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3], pay[(J + 1) & 3], hcur, hh, lut,           \
             sm.b[(k + 1) & 1u] + c * 128u, bsw, m3_bsd<BS && (J & 1) == 0>(bst, k, arow0, lane));              \
         __builtin_amdgcn_sched_barrier(0);                                                                   \
         wait_vm<(J == 1 ? 2 : 1)>(); /* A(k + 1) copied; payload k + 2 (and the header) arrived */           \
@@ -426,6 +475,80 @@ __device__ __forceinline__ void m3_mainloop(M3Lds &sm, const _Float16 *abase, co
     r9vx_u32x4 pay[4], hnext;
     m3_mainloop_core<SCHEME, NR, TR, BS, false>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst,
                                                 hook, pay, hnext);
+}
+
+/*
+ * The main loop for the m3_wide schemes (every tile size): a step's payload
+ * is the pair pay[2 (k & 1)], pay[2 (k & 1) + 1], loaded two steps ahead.
+ * Step k: barrier, the A(k + 1) copy and payload k + 2 (plus the next block's
+ * d values when J == 1) issued, the MFMAs of step k with the decode of
+ * B(k + 1), then a wait for A(k + 1) and payload k + 2 (the plain loop's
+ * wait for A(k + 1) already holds its payload loads to the same step and a
+ * half).
+ */
+template <int SCHEME, int NR, bool TR, bool BS, class Hook>
+__device__ __forceinline__ void m3_mainloop_wide(M3Lds &sm, const _Float16 *abase, const uint32_t (&aoff)[4],
+                                                 const M3WRow &w, uint32_t nk, uint32_t tid, uint32_t wave,
+                                                 const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
+                                                 r9vx_f32x16 (&acc)[4][2], const uint32_t *bst, Hook &hook) {
+    static_assert(m3_wide(SCHEME), "two-load payload schemes only");
+    const uint32_t lane = tid & 63, c = m3_brow(tid), hh = tid & 1, bsw = m2_swz(c);
+    const uint32_t a_lds = m3_lds_addr(&sm.a[0][0]);
+    r9vx_u32x4 pay[4], hnext, hcur;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pay[i] = r9vx_u32x4{0u, 0u, 0u, 0u};
+    hnext = r9vx_u32x4{0u, 0u, 0u, 0u};
+    /* prologue: P0 H0 | A0 | P1; B(0) decoded into B tile 0 */
+    m3_load_pay2(w, 0, hh, pay[0], pay[1]);
+    m3_load_hdr<SCHEME>(w, 0, hnext);
+    m3_dma_a(a_lds, abase, aoff, 0, wave);
+    m3_load_pay2(w, 1 < nk ? 1 : nk - 1, hh, pay[2], pay[3]);
+    wait_vm<6>(); /* P0, H0 (and the loads issued before) */
+    touch_pay(pay[0]);
+    touch_pay(pay[1]);
+    touch_pay(hnext);
+    hcur = hnext;
+    hook();
+    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], pay[1], hcur, hh, lut,
+                                 sm.b[0] + c * 128u, bsw);
+    wait_vm<0>(); /* A0, P1 */
+    touch_pay(pay[2]);
+    touch_pay(pay[3]);
+
+    for (uint32_t k0 = 0; k0 < nk; k0 += 4) {
+#define R9VX_M3W_STEP(J)                                                                                     \
+    {                                                                                                        \
+        const uint32_t k = k0 + J;                                                                           \
+        lds_barrier(); /* B(k), A(k) visible; step k - 1's tile and stage are free */                        \
+        m3_dma_a(a_lds + ((k + 1) & 1u) * kM3Stage, abase, aoff, k + 1 < nk ? k + 1 : nk - 1, wave);          \
+        m3_load_pay2(w, k + 2 < nk ? k + 2 : nk - 1, hh, pay[2 * (J & 1)], pay[2 * (J & 1) + 1]);             \
+        if (J == 1) {                                                                                        \
+            const uint32_t blk = (k + 3) / 4 < nk / 4 ? (k + 3) / 4 : nk / 4 - 1;                             \
+            m3_load_hdr<SCHEME>(w, blk, hnext);                                                              \
+        }                                                                                                    \
+        if (J == 3) {                                                                                        \
+            touch_pay(hnext);                                                                                \
+            hcur = hnext;                                                                                    \
+        }                                                                                                    \
+        m3_compute<SCHEME, (J + 1) & 3, NR, TR, BS && (J & 1) == 0>(                                          \
+            sm.a[k & 1u], sm.b[k & 1u], lane, arow0, bc0, bc1, acc, pay[2 * ((J + 1) & 1)],                   \
+            pay[2 * ((J + 1) & 1) + 1], hcur, hh, lut, sm.b[(k + 1) & 1u] + c * 128u, bsw,                    \
+            m3_bsd<BS && (J & 1) == 0>(bst, k, arow0, lane));                                                \
+        __builtin_amdgcn_sched_barrier(0);                                                                   \
+        wait_vm<(J == 1 ? 1 : 0)>(); /* A(k + 1) copied; payload k + 2 arrived */                            \
+        touch_pay(pay[2 * (J & 1)]);                                                                         \
+        touch_pay(pay[2 * (J & 1) + 1]);                                                                     \
+    }
+        R9VX_M3W_STEP(0)
+        R9VX_M3W_STEP(1)
+        R9VX_M3W_STEP(2)
+        R9VX_M3W_STEP(3)
+#undef R9VX_M3W_STEP
+    }
+    wait_vm<0>();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) touch_pay(pay[i]);
+    touch_pay(hnext);
 }
 
 /*
@@ -472,7 +595,7 @@ __device__ __forceinline__ void m3_mainloop_half(M3Lds &sm, const _Float16 *abas
     touch_pay(hnext);
     hcur = hnext;
     hook();
-    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], hcur, hh, lut, sm.b[0] + c * 128u,
+    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], pay[0], hcur, hh, lut, sm.b[0] + c * 128u,
                                  bsw);
     if (dma)
         wait_vm<10>(); /* A0, P1 */
@@ -496,7 +619,7 @@ __device__ __forceinline__ void m3_mainloop_half(M3Lds &sm, const _Float16 *abas
             hcur = hnext;                                                                                    \
         }                                                                                                    \
         m3_compute<SCHEME, (J + 1) & 3, NR, TR, BS && (J & 1) == 0>(                                          \
-            sm.a[0] + J * kSlot, sm.b[k & 1u], lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3], hcur, hh, lut,    \
+            sm.a[0] + J * kSlot, sm.b[k & 1u], lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3], pay[(J + 1) & 3], hcur, hh, lut,    \
             sm.b[(k + 1) & 1u] + c * 128u, bsw, m3_bsd<BS && (J & 1) == 0>(bst, k, arow0, lane));              \
         __builtin_amdgcn_sched_barrier(0);                                                                   \
         /* A(k + 1) and payload k + 2 (steps k - 1 and k may stay in flight) */                              \
@@ -548,22 +671,32 @@ __device__ __forceinline__ void m3_run(uint32_t nr, bool half, M3Lds &sm, const 
             for (int r = 0; r < 16; ++r) acc[t][j][r] = 0.f;
 #define R9VX_M3_CASE(LOOP, N) \
     case N: LOOP<SCHEME, N, TR, BS>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst, hook); break;
-    if (half) { /* the tile's rows fit waves 0-3 (uniform over the workgroup) */
+    if constexpr (m3_wide(SCHEME)) { /* one loop for every tile size */
         switch (nr) {
-            R9VX_M3_CASE(m3_mainloop_half, 4)
-            R9VX_M3_CASE(m3_mainloop_half, 3)
-            R9VX_M3_CASE(m3_mainloop_half, 2)
-            R9VX_M3_CASE(m3_mainloop_half, 1)
-        default: m3_mainloop_half<SCHEME, 0, TR, BS>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst, hook); break;
+            R9VX_M3_CASE(m3_mainloop_wide, 4)
+            R9VX_M3_CASE(m3_mainloop_wide, 3)
+            R9VX_M3_CASE(m3_mainloop_wide, 2)
+            R9VX_M3_CASE(m3_mainloop_wide, 1)
+        default: m3_mainloop_wide<SCHEME, 0, TR, BS>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst, hook); break;
         }
-        return;
-    }
-    switch (nr) {
-        R9VX_M3_CASE(m3_mainloop, 4)
-        R9VX_M3_CASE(m3_mainloop, 3)
-        R9VX_M3_CASE(m3_mainloop, 2)
-        R9VX_M3_CASE(m3_mainloop, 1)
-    default: m3_mainloop<SCHEME, 0, TR, BS>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst, hook); break;
+    } else {
+        if (half) { /* the tile's rows fit waves 0-3 (uniform over the workgroup) */
+            switch (nr) {
+                R9VX_M3_CASE(m3_mainloop_half, 4)
+                R9VX_M3_CASE(m3_mainloop_half, 3)
+                R9VX_M3_CASE(m3_mainloop_half, 2)
+                R9VX_M3_CASE(m3_mainloop_half, 1)
+            default: m3_mainloop_half<SCHEME, 0, TR, BS>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst, hook); break;
+            }
+            return;
+        }
+        switch (nr) {
+            R9VX_M3_CASE(m3_mainloop, 4)
+            R9VX_M3_CASE(m3_mainloop, 3)
+            R9VX_M3_CASE(m3_mainloop, 2)
+            R9VX_M3_CASE(m3_mainloop, 1)
+        default: m3_mainloop<SCHEME, 0, TR, BS>(sm, abase, aoff, w, nk, tid, wave, lut, arow0, bc0, bc1, acc, bst, hook); break;
+        }
     }
 #undef R9VX_M3_CASE
 }
