@@ -302,7 +302,7 @@ __global__ __launch_bounds__(512, 1) void gemm3_kernel(GemmArgs a) {
         aoff[i] = ((m0 + (r < rows ? r : 0)) * a.k + 8 * dma_group(r, lane)) * 2u;
     }
     M3WRow w{m3_uniform(a.w + (uint64_t)n0 * a.w_row_stride), m3_brow(tid) * (uint32_t)a.w_row_stride};
-    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+    if constexpr (SCHEME == R9VX_SCHEME_Q8_0 || SCHEME == R9VX_SCHEME_Q6_K) { /* the split layout's d row */
         w.sbase = m3_uniform(reinterpret_cast<const uint8_t *>(a.ws + (uint64_t)n0 * a.ws_row));
         w.soff = m3_brow(tid) * a.ws_row * 2u;
     }
@@ -434,6 +434,8 @@ int r9vx_launch_x_to_f16(const uint16_t *x, uint32_t m, uint32_t k, _Float16 *x1
         hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_Q4_K>, dim3((m + 3) / 4), dim3(256), 0, stream, x, m, k, x16, scale);
     else if (perm_scheme == R9VX_SCHEME_IQ4_XS)
         hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3((m + 3) / 4), dim3(256), 0, stream, x, m, k, x16, scale);
+    else if (perm_scheme == R9VX_SCHEME_Q6_K)
+        hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_Q6_K>, dim3((m + 3) / 4), dim3(256), 0, stream, x, m, k, x16, scale);
     else
         hipLaunchKernelGGL(x_to_f16_kernel<0>, dim3((m + 3) / 4), dim3(256), 0, stream, x, m, k, x16, scale);
     return (int)hipGetLastError();
@@ -469,19 +471,22 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
      * addressing bound -- never from the launch's row count: a row's outputs
      * are the same bits whatever rows share the launch, at whatever index,
      * and in every bucket above the decode GEMV's.  Q4_K / IQ4_XS run the
-     * 256 x 256 tiles (gemm3 for N % 256 == 0, gemm2 otherwise), Q8_0 gemm3
-     * for N % 256 == 0; Q6_K / IQ3_S, and Q8_0 otherwise, the 128-row
+     * 256 x 256 tiles (gemm3 for N % 256 == 0, gemm2 otherwise), Q8_0 / Q6_K
+     * gemm3 for N % 256 == 0; IQ3_S, and Q8_0 / Q6_K otherwise, the 128-row
      * LDS-decoded tile. */
     const bool split = p.scheme == R9VX_SCHEME_Q8_0 || p.scheme == R9VX_SCHEME_Q6_K || p.scheme == R9VX_SCHEME_IQ3_S;
     const bool m3_shape = p.n % kM3Cols == 0 && (uint64_t)p.m_bucket * p.k < (1ull << 31);
-    if (p.scheme == R9VX_SCHEME_Q8_0 && m3_shape) {
-        /* Q8_0's step halves are whole blocks: IQ4_XS's group order */
-        hipLaunchKernelGGL(x_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, dim3((p.m + 3) / 4), dim3(256), 0, stream, p.x, p.m, p.k,
-                           x16, scale);
+    if ((p.scheme == R9VX_SCHEME_Q8_0 || p.scheme == R9VX_SCHEME_Q6_K) && m3_shape) {
+        /* the split layouts on the 256 x 256 loop, x in their K order */
+        const int rc = r9vx_launch_x_to_f16(p.x, p.m, p.k, x16, scale, r9vx_group_order(p.scheme), stream);
+        if (rc) return rc;
         a.m_tiles = (p.m + kM2Rows - 1) / kM2Rows;
         a.n_tiles = (p.n + kM2Cols - 1) / kM2Cols;
         const dim3 grid3(plan_chunks(a, r9vx_device_cus()));
-        hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_Q8_0>), grid3, dim3(512), 0, stream, a);
+        if (p.scheme == R9VX_SCHEME_Q8_0)
+            hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_Q8_0>), grid3, dim3(512), 0, stream, a);
+        else
+            hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_Q6_K>), grid3, dim3(512), 0, stream, a);
         return (int)hipGetLastError();
     }
     if (!split) {
@@ -512,7 +517,7 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     a.m_tiles = (p.m + 127) / 128;
     a.n_tiles = (p.n + 255) / 256;
     dim3 grid(a.m_tiles * a.n_tiles);
-    /* Q6_K / IQ3_S (and Q8_0 at N % 256 != 0) take this LDS-decoded tile (their steps do not
+    /* IQ3_S (and Q8_0 / Q6_K at N % 256 != 0) take this LDS-decoded tile (their steps do not
      * fit the register-decoded core's 16-byte lane payload). */
     switch (p.scheme) {
     case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q6_K, 128, 1>), grid, dim3(256), 0, stream, a); break;

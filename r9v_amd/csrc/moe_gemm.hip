@@ -92,8 +92,8 @@ constexpr int kStage = 32 * kMT * 128;       /* 16 KiB per A stage */
     __shared__ __attribute__((aligned(16))) float lutf[512];          \
     uint8_t *const stages[4] = {st0, st1, st2, st3};
 
-/* Gate/up experts the r9vx_mma3.h loop does not decode (IQ3_S, and Q6_K in
- * the split layout): the LDS-decoded main loop of r9vx_mma.h (a 128 x
+/* Gate/up experts the r9vx_mma3.h loop does not decode (IQ3_S): the
+ * LDS-decoded main loop of r9vx_mma.h (a 128 x
  * 256 tile; thread t decodes weight row t of the tile into LDS: threads
  * 0..127 the gate rows j0..j0+127, threads 128..255 the up rows of the same
  * columns, so tile column c pairs with column c + 128), with the activations
@@ -164,15 +164,12 @@ __global__ __launch_bounds__(256, 2) void moe_gu_lds_kernel(GroupedArgs a) {
  * hexp and hbe for the down GEMMs), then lane l writes group l % 8 of K
  * step l / 8 (+ 8 per pass) as 8 fp16 in the down scheme's group order,
  * scaled by 2^-e. */
-/* K position of element i of group q in a 64-wide step of the h16 rows;
- * DN: the rows' order (r9vx_group_order of the down scheme: the group order
- * of the r9vx_mma3.h loop, 0 natural). */
+/* Row element of elements i .. i + 3 of the group stored at position c of
+ * an h16 row; DN: the rows' order (r9vx_group_order of the down scheme: the
+ * group order of the r9vx_mma3.h loop, 0 natural). */
 template <int DN>
-__device__ __forceinline__ uint32_t h_group_k(uint32_t q, uint32_t i) {
-    if constexpr (DN == R9VX_SCHEME_Q4_K || DN == R9VX_SCHEME_IQ4_XS)
-        return group_k<DN>(q, i);
-    else
-        return 8 * q + i;
+__device__ __forceinline__ uint32_t h_pos(uint32_t c, uint32_t i) {
+    return order_pos<DN>(c, i);
 }
 
 /* A row converted at one scale 2^-e: e goes to hexp and to each of its
@@ -201,9 +198,8 @@ __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t n
         for (int i = 0; i < 2; ++i) {
             const uint32_t c = lane + 64 * i;
             const uint32_t cc = c < a.dff / 8 ? c : 0u;
-            const uint32_t base = (cc >> 3) * 64, q = cc & 7;
-            lo[i] = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + h_group_k<DN>(q, 0));
-            hi[i] = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + h_group_k<DN>(q, 4));
+            lo[i] = *reinterpret_cast<const r9vx_f32x4 *>(hr + h_pos<DN>(8 * cc, 0));
+            hi[i] = *reinterpret_cast<const r9vx_f32x4 *>(hr + h_pos<DN>(8 * cc, 4));
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -233,9 +229,8 @@ __global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t n
     put_row_exp(a, row, row_shift(mx), lane);
     const float inv = ldexpf(1.0f, -row_shift(mx));
     for (uint32_t c = lane; c < a.dff / 8; c += 64) {
-        const uint32_t base = (c >> 3) * 64, q = c & 7;
-        const r9vx_f32x4 lo = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + h_group_k<DN>(q, 0));
-        const r9vx_f32x4 hi = *reinterpret_cast<const r9vx_f32x4 *>(hr + base + h_group_k<DN>(q, 4));
+        const r9vx_f32x4 lo = *reinterpret_cast<const r9vx_f32x4 *>(hr + h_pos<DN>(8 * c, 0));
+        const r9vx_f32x4 hi = *reinterpret_cast<const r9vx_f32x4 *>(hr + h_pos<DN>(8 * c, 4));
         *reinterpret_cast<r9vx_u32x4 *>(orow + 8 * c) =
             r9vx_u32x4{pack_h2(lo.x * inv, lo.y * inv), pack_h2(lo.z * inv, lo.w * inv), pack_h2(hi.x * inv, hi.y * inv),
                        pack_h2(hi.z * inv, hi.w * inv)};
@@ -255,13 +250,15 @@ __device__ __forceinline__ float dpp_f32(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
 }
 
-/* The 4-element chunk (K offset / 4 within a 64-wide step) that holds
- * elements i .. i + 3 (i = 0 or 4) of group q of an h16 row in order
- * `order` (h_group_k's orders, chosen at run time). */
-__device__ __forceinline__ uint32_t h_chunk(uint32_t order, uint32_t q, uint32_t i) {
-    if (order == R9VX_SCHEME_Q4_K) return group_k<R9VX_SCHEME_Q4_K>(q, i) / 4;
-    if (order == R9VX_SCHEME_IQ4_XS) return group_k<R9VX_SCHEME_IQ4_XS>(q, i) / 4;
-    return (8 * q + i) / 4;
+/* The 4-element chunk (column / 4 within a 128-column block) that holds
+ * elements i .. i + 3 (i = 0 or 4) of the group stored at position c (< 128)
+ * of the block in an h16 row of order `order` (h_pos's orders, chosen at
+ * run time). */
+__device__ __forceinline__ uint32_t h_chunk(uint32_t order, uint32_t c, uint32_t i) {
+    if (order == R9VX_SCHEME_Q4_K) return order_pos<R9VX_SCHEME_Q4_K>(c, i) / 4;
+    if (order == R9VX_SCHEME_IQ4_XS) return order_pos<R9VX_SCHEME_IQ4_XS>(c, i) / 4;
+    if (order == R9VX_SCHEME_Q6_K) return order_pos<R9VX_SCHEME_Q6_K>(c, i) / 4;
+    return order_pos<0>(c, i) / 4;
 }
 
 /* After the 256-row gate/up GEMM, for the down kernels that undo one
@@ -304,8 +301,8 @@ __global__ __launch_bounds__(256) void h_fix_kernel(GroupedArgs a, uint32_t nrow
 
 /* ---------------------------------------------------------------- down, LDS-decoded */
 
-/* Down experts the r9vx_mma3.h loop does not decode (IQ3_S, and Q6_K in the
- * split layout): the LDS-decoded main loop of r9vx_mma.h over a
+/* Down experts the r9vx_mma3.h loop does not decode (IQ3_S): the
+ * LDS-decoded main loop of r9vx_mma.h over a
  * 128-row tile of h16 rows (natural K order) and output columns n0 .. n0 +
  * 255 (thread t decodes weight row n0 + t).  The accumulators pass through
  * a 32 x 256 f32 LDS stage, 32 rows at a time; thread t then owns 32
@@ -430,7 +427,7 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     const uint32_t c = m3_brow(tid);
     const uint32_t wr = c < 128 ? j0 + c : a.dff + j0 + (c - 128);
     M3WRow w{m3_uniform(a.w_gu + (uint64_t)expert * 2 * a.dff * a.gu_row_bytes), wr * (uint32_t)a.gu_row_bytes};
-    if constexpr (GU == R9VX_SCHEME_Q8_0) {
+    if constexpr (GU == R9VX_SCHEME_Q8_0 || GU == R9VX_SCHEME_Q6_K) { /* the split layout's d rows */
         w.sbase = m3_uniform(reinterpret_cast<const uint8_t *>(a.s_gu + (uint64_t)expert * 2 * a.dff * a.gu_srow));
         w.soff = wr * a.gu_srow * 2u;
     }
@@ -473,7 +470,7 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
      * g >> 3, whose elements 0-3 and 4-7 are two 16-byte chunks of the staged
      * f32 row. */
     const uint32_t g = lane & 15, hs = g >> 3, hq = g & 7;
-    const uint32_t c_lo = 16 * hs + h_chunk(a.h_order, hq, 0), c_hi = 16 * hs + h_chunk(a.h_order, hq, 4);
+    const uint32_t c_lo = h_chunk(a.h_order, 64 * hs + 8 * hq, 0), c_hi = h_chunk(a.h_order, 64 * hs + 8 * hq, 4);
     int8_t *const hbe = reinterpret_cast<int8_t *>(a.ws + a.L.hbe);
     const uint32_t hstride = r9vx_moe_hbe_stride(a.dff);
     /* every row of the stage is converted (rows past the tile's hold stale
@@ -578,7 +575,7 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     auto weights = [&](uint32_t n0) {
         M3WRow w{m3_uniform(a.w_dn + ((uint64_t)expert * a.dm + n0) * a.dn_row_bytes),
                  m3_brow(tid) * (uint32_t)a.dn_row_bytes};
-        if constexpr (DN == R9VX_SCHEME_Q8_0) {
+        if constexpr (DN == R9VX_SCHEME_Q8_0 || DN == R9VX_SCHEME_Q6_K) {
             w.sbase = m3_uniform(reinterpret_cast<const uint8_t *>(a.s_dn + ((uint64_t)expert * a.dm + n0) * a.dn_srow));
             w.soff = m3_brow(tid) * a.dn_srow * 2u;
         }
@@ -722,8 +719,8 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
         case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_IQ4_XS>, ggu3, dim3(512), 0, s, a); break;
         case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q4_K>, ggu3, dim3(512), 0, s, a); break;
         case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q8_0>, ggu3, dim3(512), 0, s, a); break;
-        case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_IQ3_S>, ggu, dim3(256), 0, s, a); break;
-        default: hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_Q6_K>, ggu, dim3(256), 0, s, a); break;
+        case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q6_K>, ggu3, dim3(512), 0, s, a); break;
+        default: hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_IQ3_S>, ggu, dim3(256), 0, s, a); break;
         }
     }
     const uint32_t nrows = a.p + p.shared * p.t;
@@ -738,6 +735,7 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
         switch (a.h_order) {
         case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q4_K>, gh, dim3(256), 0, s, a, nrows); break;
         case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, gh, dim3(256), 0, s, a, nrows); break;
+        case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q6_K>, gh, dim3(256), 0, s, a, nrows); break;
         default: hipLaunchKernelGGL(h_to_f16_kernel<0>, gh, dim3(256), 0, s, a, nrows); break; /* natural */
         }
     }
@@ -756,8 +754,8 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
             hipLaunchKernelGGL((moe_dn_m3_kernel<R9VX_SCHEME_IQ4_XS, 1>), gdn3, dim3(512), 0, s, a);
             break;
         case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL((moe_dn_m3_kernel<R9VX_SCHEME_Q8_0, 1>), gdn3, dim3(512), 0, s, a); break;
-        case R9VX_SCHEME_IQ3_S: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_IQ3_S>, gdn, dim3(256), 0, s, a); break;
-        default: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_Q6_K>, gdn, dim3(256), 0, s, a); break;
+        case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL((moe_dn_m3_kernel<R9VX_SCHEME_Q6_K, 1>), gdn3, dim3(512), 0, s, a); break;
+        default: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_IQ3_S>, gdn, dim3(256), 0, s, a); break;
         }
     }
     return (int)hipGetLastError();

@@ -140,8 +140,23 @@ struct BScale {
 };
 
 template <int SCHEME, int KS>
-__device__ __forceinline__ BScale bscale(const r9vx_u32x4 &hd, uint32_t h) {
+__device__ __forceinline__ BScale bscale(const r9vx_u32x4 &hd, uint32_t h, uint32_t hd2 = 0u) {
     BScale s;
+    if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
+        /* hd: the block's 16 int8 scales, hd2: its f16 d.  Step KS (span n =
+         * KS / 2, part j = KS % 2), half h: the low nibbles' columns take
+         * scale 8 n + 2 j + h, the high nibbles' 8 n + 4 + 2 j + h (one per
+         * 16 columns, crates/r9v-format/src/ggml.rs:817-850) */
+        const uint32_t lw = (KS >> 1) == 0 ? hd.x : hd.z, hw = (KS >> 1) == 0 ? hd.y : hd.w;
+        const uint32_t sh = 8 * (2 * (KS & 1) + h);
+        const float d = r9vx_f16_to_f32((uint16_t)hd2);
+        s.dl0 = d * (float)(int8_t)(lw >> sh);
+        s.dl1 = d * (float)(int8_t)(hw >> sh);
+        s.c0 = -1056.f * s.dl0; /* exact: dl has at most 18 significant bits, 1056 = 33 * 2^5 */
+        s.c1 = -1056.f * s.dl1;
+        s.nml0 = s.nml1 = 0.f;
+        return s;
+    }
     if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
         /* hd: the f16 d of the eight 32-weight blocks of a 256-weight block;
          * step KS, half h is block 2 KS + h */

@@ -77,10 +77,11 @@ struct M3WRow {
     uint32_t soff = 0;
 };
 
-/* Q8_0: a thread's half of a K step is one whole block, 32 int8 quants (two
- * 16-byte loads), so its payload ring holds two steps in the registers the
- * 4-bit schemes use for four. */
-constexpr bool m3_wide(int s) { return s == R9VX_SCHEME_Q8_0; }
+/* Q8_0: a thread's half of a K step is one whole block, 32 int8 quants;
+ * Q6_K: 16 ql bytes and the 16 qh bytes holding their high bit pairs.  Two
+ * 16-byte loads either way, so the payload ring holds two steps in the
+ * registers the 4-bit schemes use for four. */
+constexpr bool m3_wide(int s) { return s == R9VX_SCHEME_Q8_0 || s == R9VX_SCHEME_Q6_K; }
 
 /* A pointer the caller knows to be wave-uniform, moved to scalar registers
  * (the loads take it as their SGPR base whatever the compiler's divergence
@@ -100,29 +101,59 @@ __device__ __forceinline__ void m3_load_pay(const M3WRow &w, uint32_t kt, uint32
     asm volatile("global_load_dwordx4 %0, %1, %2" : "+v"(p) : "v"(off), "s"(w.base) : "memory");
 }
 
-/* Q8_0 (m3_wide): step kt's block 2 kt + hh, quants 0-15 into p0 and 16-31
- * into p1. */
+/* The m3_wide payload of step kt.  Q8_0: block 2 kt + hh, quants 0-15 into
+ * p0 and 16-31 into p1.  Q6_K (208-byte body blocks: ql 0-127, qh 128-191,
+ * scales 192-207): step s = kt % 4 of block kt / 4 is span n = s / 2, part
+ * j = s % 2; p0 = ql bytes 64 n + 32 j + 16 hh .. + 15 (low nibbles: columns
+ * 128 n + 32 j + 16 hh + i, high: the same + 64), p1 = qh bytes 32 n + 16 hh
+ * .. + 15 (bit pairs j and 2 + j of those columns;
+ * crates/r9v-format/src/ggml.rs:817-850). */
+template <int SCHEME>
 __device__ __forceinline__ void m3_load_pay2(const M3WRow &w, uint32_t kt, uint32_t hh, r9vx_u32x4 &p0,
                                              r9vx_u32x4 &p1) {
-    const uint32_t off = w.off + 64 * kt + 32 * hh;
-    asm volatile("global_load_dwordx4 %0, %2, %3\n\tglobal_load_dwordx4 %1, %2, %3 offset:16"
-                 : "+v"(p0), "+v"(p1)
-                 : "v"(off), "s"(w.base)
-                 : "memory");
+    if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
+        const uint32_t s = kt & 3, b = w.off + (kt >> 2) * R9VX_Q6K_BODY + 16 * hh;
+        const uint32_t ql = b + 64 * (s >> 1) + 32 * (s & 1), qh = b + 128 + 32 * (s >> 1);
+        asm volatile("global_load_dwordx4 %0, %2, %4\n\tglobal_load_dwordx4 %1, %3, %4"
+                     : "+v"(p0), "+v"(p1)
+                     : "v"(ql), "v"(qh), "s"(w.base)
+                     : "memory");
+    } else {
+        const uint32_t off = w.off + 64 * kt + 32 * hh;
+        asm volatile("global_load_dwordx4 %0, %2, %3\n\tglobal_load_dwordx4 %1, %2, %3 offset:16"
+                     : "+v"(p0), "+v"(p1)
+                     : "v"(off), "s"(w.base)
+                     : "memory");
+    }
 }
 
 /* Q4_K: the 16-byte header; IQ4_XS: the block's first 16 bytes (its 8-byte
  * header and 8 payload bytes, inside the 136-byte block), of which .x/.y are
  * used; Q8_0: the f16 d values of the eight 32-weight blocks of 256-weight
- * block blk. */
+ * block blk; Q6_K: the block's 16 int8 scales (its d: m3_load_hdr2). */
 template <int SCHEME>
 __device__ __forceinline__ void m3_load_hdr(const M3WRow &w, uint32_t blk, r9vx_u32x4 &hd) {
     if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
         const uint32_t off = w.soff + 16 * blk;
         asm volatile("global_load_dwordx4 %0, %1, %2" : "+v"(hd) : "v"(off), "s"(w.sbase) : "memory");
+    } else if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
+        const uint32_t off = w.off + blk * R9VX_Q6K_BODY + 192;
+        asm volatile("global_load_dwordx4 %0, %1, %2" : "+v"(hd) : "v"(off), "s"(w.base) : "memory");
     } else {
         const uint32_t off = w.off + blk * (SCHEME == R9VX_SCHEME_Q4_K ? R9VX_Q4K_BYTES : R9VX_IQ4XS_BYTES);
         asm volatile("global_load_dwordx4 %0, %1, %2" : "+v"(hd) : "v"(off), "s"(w.base) : "memory");
+    }
+}
+
+/* Header loads per block (m3_load_hdr, and m3_load_hdr2 for Q6_K). */
+constexpr int m3_hdr_loads(int s) { return s == R9VX_SCHEME_Q6_K ? 2 : 1; }
+
+/* Q6_K: block blk's f16 d from the split layout's d row (zero-extended). */
+template <int SCHEME>
+__device__ __forceinline__ void m3_load_hdr2(const M3WRow &w, uint32_t blk, uint32_t &d) {
+    if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
+        const uint32_t off = w.soff + 2 * blk;
+        asm volatile("global_load_ushort %0, %1, %2" : "+v"(d) : "v"(off), "s"(w.sbase) : "memory");
     }
 }
 
@@ -170,11 +201,33 @@ __device__ __forceinline__ void m3_init_iq4_lut(uint32_t *lut, uint32_t tid, uin
  * Returns the two packed dwords {low pair, high pair}.  IQ4_XS: kv0 / kv1
  * are the bytes' codebook pairs {kv[low], kv[high]}.  Q8_0: the low pair is
  * quants 4q + 2m, +1 (bytes 2m, 2m + 1 of dword q of the first 16 quants,
- * dw), the high pair the same bytes of the second 16 (dw2). */
-template <int SCHEME>
+ * dw), the high pair the same bytes of the second 16 (dw2).  Q6_K: dw the
+ * ql dword, dw2 the qh dword; low pair = columns of the low nibbles (bit
+ * pair j = KS % 2), high pair = the high nibbles' (bit pair 2 + j). */
+template <int SCHEME, int KS = 0>
 __device__ __forceinline__ void m3_dec_unit(uint32_t dw, uint32_t dw2, int m, const BScale &sc, uint32_t kv0,
                                             uint32_t kv1, uint32_t &lo2, uint32_t &hi2) {
-    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+    if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
+        /* the 6-bit values q (nibble | bit pair << 4) under a 0x64 byte read
+         * as the fp16 1024 + q; w = dl (1024 + q) - 1056 dl, fused: dl q -
+         * 32 dl with dl = d sc (exact in f32, as is 1056 dl), rounded once */
+        constexpr uint32_t j = KS & 1;
+        const uint32_t lowq = r9vx_and_or(dw, 0x0F0F0F0Fu, (dw2 << (4 - 2 * j)) & 0x30303030u);
+        const uint32_t highq = r9vx_and_or(dw >> 4, 0x0F0F0F0Fu, (dw2 >> (2 * j)) & 0x30303030u);
+        const uint32_t sel = m ? 0x04030402u : 0x04010400u;
+        const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, lowq, sel);
+        const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, highq, sel);
+        uint32_t a, b;
+        asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(a) : "v"(sc.dl0), "v"(lo), "v"(sc.c0));
+        asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+            : "+v"(a) : "v"(sc.dl0), "v"(lo), "v"(sc.c0));
+        asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(b) : "v"(sc.dl1), "v"(hi), "v"(sc.c1));
+        asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+            : "+v"(b) : "v"(sc.dl1), "v"(hi), "v"(sc.c1));
+        lo2 = a;
+        hi2 = b;
+        asm volatile("" : "+v"(lo2), "+v"(hi2));
+    } else if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
         /* q + 128 (the byte XOR 0x80) under a 0x64 byte reads as the fp16
          * 1152 + q; w = d (1152 + q) - 1152 d, fused: d q is exact in f32
          * (11 + 8 significant bits) and -1152 d too, so the one rounding is
@@ -243,8 +296,8 @@ template <int SCHEME, int KS, int NR, bool TR, bool BSTEP = false>
 __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bsm, uint32_t lane, uint32_t arow0,
                                            uint32_t bc0, uint32_t bc1, r9vx_f32x16 (&acc)[4][2],
                                            const r9vx_u32x4 &pay, const r9vx_u32x4 &pay2, const r9vx_u32x4 &hd,
-                                           uint32_t hh, const uint32_t *lut, uint8_t *bdst, uint32_t bsw,
-                                           uint32_t bsd = 0u) {
+                                           uint32_t hd2, uint32_t hh, const uint32_t *lut, uint8_t *bdst,
+                                           uint32_t bsw, uint32_t bsd = 0u) {
     constexpr bool kIq4 = SCHEME == R9VX_SCHEME_IQ4_XS;
     constexpr int P = 4 * NR; /* MFMA pairs */
     const uint32_t h = lane >> 5, r32 = lane & 31, sw = m2_swz(r32);
@@ -285,7 +338,7 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
         for (int u = 0; u < 8; ++u)
             if (P == 0 || dec_pair(u) - kLead < 0) read_kv(u);
     }
-    const BScale sc = bscale<SCHEME, KS>(hd, hh);
+    const BScale sc = bscale<SCHEME, KS>(hd, hh, hd2);
     uint32_t o[4][4]; /* granule q of the decoded half row */
     /* Fragments are read kAhead pairs before their MFMAs (two when the
      * wave has several row tiles: B of a slice then lands after the slice
@@ -336,7 +389,7 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u)
-            if (dec_pair(u) == i) m3_dec_unit<SCHEME>(dws[u >> 1], dws2[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
+            if (dec_pair(u) == i) m3_dec_unit<SCHEME, KS>(dws[u >> 1], dws2[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
         /* granule q of the row is whole once unit 2q + 1 is decoded */
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -348,7 +401,7 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
     if constexpr (P == 0) {
 #pragma unroll
         for (int u = 0; u < 8; ++u)
-            m3_dec_unit<SCHEME>(dws[u >> 1], dws2[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
+            m3_dec_unit<SCHEME, KS>(dws[u >> 1], dws2[u >> 1], u & 1, sc, kv[2 * u], kv[2 * u + 1], o[u >> 1][u & 1], o[u >> 1][2 + (u & 1)]);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             *reinterpret_cast<r9vx_u32x4 *>(bdst + (((4u * hh + q) ^ bsw) << 4)) =
@@ -428,7 +481,7 @@ __device__ __forceinline__ void m3_mainloop_core(M3Lds &sm, const _Float16 *abas
     touch_pay(hnext);
     hcur = hnext;
     hook();
-    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], pay[0], hcur, hh, lut, sm.b[0] + c * 128u,
+    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], pay[0], hcur, 0u, hh, lut, sm.b[0] + c * 128u,
                                  bsw);
     wait_vm<2>(); /* A0, P1 */
     touch_pay(pay[1]);
@@ -449,7 +502,7 @@ __device__ __forceinline__ void m3_mainloop_core(M3Lds &sm, const _Float16 *abas
             hcur = hnext;                                                                                    \
         }                                                                                                    \
         m3_compute<SCHEME, (J + 1) & 3, NR, TR, BS && (J & 1) == 0>(                                          \
-            sm.a[k & 1u], sm.b[k & 1u], lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3], pay[(J + 1) & 3], hcur, hh, lut,           \
+            sm.a[k & 1u], sm.b[k & 1u], lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3], pay[(J + 1) & 3], hcur, 0u, hh, lut,           \
             sm.b[(k + 1) & 1u] + c * 128u, bsw, m3_bsd<BS && (J & 1) == 0>(bst, k, arow0, lane));              \
         __builtin_amdgcn_sched_barrier(0);                                                                   \
         wait_vm<(J == 1 ? 2 : 1)>(); /* A(k + 1) copied; payload k + 2 (and the header) arrived */           \
@@ -492,24 +545,29 @@ __device__ __forceinline__ void m3_mainloop_wide(M3Lds &sm, const _Float16 *abas
                                                  const uint32_t *lut, uint32_t arow0, uint32_t bc0, uint32_t bc1,
                                                  r9vx_f32x16 (&acc)[4][2], const uint32_t *bst, Hook &hook) {
     static_assert(m3_wide(SCHEME), "two-load payload schemes only");
+    constexpr int kH = m3_hdr_loads(SCHEME);
     const uint32_t lane = tid & 63, c = m3_brow(tid), hh = tid & 1, bsw = m2_swz(c);
     const uint32_t a_lds = m3_lds_addr(&sm.a[0][0]);
     r9vx_u32x4 pay[4], hnext, hcur;
+    uint32_t h2next = 0u, h2cur; /* Q6_K: the block's d */
 #pragma unroll
     for (int i = 0; i < 4; ++i) pay[i] = r9vx_u32x4{0u, 0u, 0u, 0u};
     hnext = r9vx_u32x4{0u, 0u, 0u, 0u};
     /* prologue: P0 H0 | A0 | P1; B(0) decoded into B tile 0 */
-    m3_load_pay2(w, 0, hh, pay[0], pay[1]);
+    m3_load_pay2<SCHEME>(w, 0, hh, pay[0], pay[1]);
     m3_load_hdr<SCHEME>(w, 0, hnext);
+    m3_load_hdr2<SCHEME>(w, 0, h2next);
     m3_dma_a(a_lds, abase, aoff, 0, wave);
-    m3_load_pay2(w, 1 < nk ? 1 : nk - 1, hh, pay[2], pay[3]);
+    m3_load_pay2<SCHEME>(w, 1 < nk ? 1 : nk - 1, hh, pay[2], pay[3]);
     wait_vm<6>(); /* P0, H0 (and the loads issued before) */
     touch_pay(pay[0]);
     touch_pay(pay[1]);
     touch_pay(hnext);
+    asm volatile("" : "+v"(h2next));
     hcur = hnext;
+    h2cur = h2next;
     hook();
-    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], pay[1], hcur, hh, lut,
+    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], pay[1], hcur, h2cur, hh, lut,
                                  sm.b[0] + c * 128u, bsw);
     wait_vm<0>(); /* A0, P1 */
     touch_pay(pay[2]);
@@ -521,21 +579,24 @@ __device__ __forceinline__ void m3_mainloop_wide(M3Lds &sm, const _Float16 *abas
         const uint32_t k = k0 + J;                                                                           \
         lds_barrier(); /* B(k), A(k) visible; step k - 1's tile and stage are free */                        \
         m3_dma_a(a_lds + ((k + 1) & 1u) * kM3Stage, abase, aoff, k + 1 < nk ? k + 1 : nk - 1, wave);          \
-        m3_load_pay2(w, k + 2 < nk ? k + 2 : nk - 1, hh, pay[2 * (J & 1)], pay[2 * (J & 1) + 1]);             \
+        m3_load_pay2<SCHEME>(w, k + 2 < nk ? k + 2 : nk - 1, hh, pay[2 * (J & 1)], pay[2 * (J & 1) + 1]);     \
         if (J == 1) {                                                                                        \
             const uint32_t blk = (k + 3) / 4 < nk / 4 ? (k + 3) / 4 : nk / 4 - 1;                             \
             m3_load_hdr<SCHEME>(w, blk, hnext);                                                              \
+            m3_load_hdr2<SCHEME>(w, blk, h2next);                                                            \
         }                                                                                                    \
         if (J == 3) {                                                                                        \
             touch_pay(hnext);                                                                                \
+            asm volatile("" : "+v"(h2next));                                                                 \
             hcur = hnext;                                                                                    \
+            h2cur = h2next;                                                                                  \
         }                                                                                                    \
         m3_compute<SCHEME, (J + 1) & 3, NR, TR, BS && (J & 1) == 0>(                                          \
             sm.a[k & 1u], sm.b[k & 1u], lane, arow0, bc0, bc1, acc, pay[2 * ((J + 1) & 1)],                   \
-            pay[2 * ((J + 1) & 1) + 1], hcur, hh, lut, sm.b[(k + 1) & 1u] + c * 128u, bsw,                    \
+            pay[2 * ((J + 1) & 1) + 1], hcur, h2cur, hh, lut, sm.b[(k + 1) & 1u] + c * 128u, bsw,             \
             m3_bsd<BS && (J & 1) == 0>(bst, k, arow0, lane));                                                \
         __builtin_amdgcn_sched_barrier(0);                                                                   \
-        wait_vm<(J == 1 ? 1 : 0)>(); /* A(k + 1) copied; payload k + 2 arrived */                            \
+        wait_vm<(J == 1 ? kH : 0)>(); /* A(k + 1) copied; payload k + 2 arrived */                           \
         touch_pay(pay[2 * (J & 1)]);                                                                         \
         touch_pay(pay[2 * (J & 1) + 1]);                                                                     \
     }
@@ -549,6 +610,7 @@ __device__ __forceinline__ void m3_mainloop_wide(M3Lds &sm, const _Float16 *abas
 #pragma unroll
     for (int i = 0; i < 4; ++i) touch_pay(pay[i]);
     touch_pay(hnext);
+    asm volatile("" : "+v"(h2next));
 }
 
 /*
@@ -595,7 +657,7 @@ __device__ __forceinline__ void m3_mainloop_half(M3Lds &sm, const _Float16 *abas
     touch_pay(hnext);
     hcur = hnext;
     hook();
-    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], pay[0], hcur, hh, lut, sm.b[0] + c * 128u,
+    m3_compute<SCHEME, 0, 0, TR>(nullptr, nullptr, lane, 0, 0, 0, acc, pay[0], pay[0], hcur, 0u, hh, lut, sm.b[0] + c * 128u,
                                  bsw);
     if (dma)
         wait_vm<10>(); /* A0, P1 */
@@ -619,7 +681,7 @@ __device__ __forceinline__ void m3_mainloop_half(M3Lds &sm, const _Float16 *abas
             hcur = hnext;                                                                                    \
         }                                                                                                    \
         m3_compute<SCHEME, (J + 1) & 3, NR, TR, BS && (J & 1) == 0>(                                          \
-            sm.a[0] + J * kSlot, sm.b[k & 1u], lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3], pay[(J + 1) & 3], hcur, hh, lut,    \
+            sm.a[0] + J * kSlot, sm.b[k & 1u], lane, arow0, bc0, bc1, acc, pay[(J + 1) & 3], pay[(J + 1) & 3], hcur, 0u, hh, lut,    \
             sm.b[(k + 1) & 1u] + c * 128u, bsw, m3_bsd<BS && (J & 1) == 0>(bst, k, arow0, lane));              \
         __builtin_amdgcn_sched_barrier(0);                                                                   \
         /* A(k + 1) and payload k + 2 (steps k - 1 and k may stay in flight) */                              \

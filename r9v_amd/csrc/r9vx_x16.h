@@ -3,7 +3,7 @@
  * max |x| picks the power-of-two scale 2^e that keeps it below 2^15 (e = 0
  * for any ordinary activation; bf16 values are exact in fp16 inside that
  * range), written beside the row, and each 64-column step is stored in the
- * weight scheme's K group order (group_k) or in natural order (PERM = 0).
+ * weight scheme's K group order (order_pos) or in natural order (PERM = 0).
  * One wave converts one row.
  */
 #ifndef R9VX_X16_H
@@ -23,6 +23,24 @@ __host__ __device__ constexpr uint32_t group_k(uint32_t q, uint32_t i) {
     }
 }
 
+/* Row element of elements i .. i + 3 (i = 0 or 4) of the 8-element group
+ * stored at position c (a multiple of 8) of a row in order PERM: 0 natural;
+ * Q4_K / IQ4_XS: each 64-column step in group_k's order; Q6_K: the two
+ * 64-position steps of each 128-column span j = 0, 1 hold columns
+ * 32 j + [0, 32) (group elements 0-3) and 64 + 32 j + [0, 32) (elements 4-7),
+ * group q at 4 q (a Q6_K thread's half step: 16 ql bytes, whose low and
+ * high nibbles are those two column ranges). */
+template <int PERM>
+__host__ __device__ constexpr uint32_t order_pos(uint32_t c, uint32_t i) {
+    if constexpr (PERM == 0) {
+        return c + i;
+    } else if constexpr (PERM == R9VX_SCHEME_Q6_K) {
+        return (c & ~127u) + 32 * ((c >> 6) & 1u) + 4 * ((c & 63u) >> 3) + (i ? 64u : 0u);
+    } else {
+        return (c & ~63u) + group_k<PERM>((c & 63u) >> 3, i);
+    }
+}
+
 template <int PERM>
 __device__ __forceinline__ void x16_row(const uint16_t *__restrict__ x, uint32_t k, _Float16 *__restrict__ x16,
                                         float *__restrict__ scale, uint32_t row, uint32_t lane) {
@@ -33,9 +51,8 @@ __device__ __forceinline__ void x16_row(const uint16_t *__restrict__ x, uint32_t
             const r9vx_u32x4 v = *reinterpret_cast<const r9vx_u32x4 *>(xr + c);
             w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
         } else {
-            const uint32_t base = c & ~63u, q = (c & 63u) >> 3;
-            const r9vx_u32x2 lo = *reinterpret_cast<const r9vx_u32x2 *>(xr + base + group_k<PERM>(q, 0));
-            const r9vx_u32x2 hi = *reinterpret_cast<const r9vx_u32x2 *>(xr + base + group_k<PERM>(q, 4));
+            const r9vx_u32x2 lo = *reinterpret_cast<const r9vx_u32x2 *>(xr + order_pos<PERM>(c, 0));
+            const r9vx_u32x2 hi = *reinterpret_cast<const r9vx_u32x2 *>(xr + order_pos<PERM>(c, 4));
             w[0] = lo.x, w[1] = lo.y, w[2] = hi.x, w[3] = hi.y;
         }
     };
@@ -111,6 +128,8 @@ __device__ __forceinline__ void x16_row_scheme(uint32_t perm, const uint16_t *__
         x16_row<R9VX_SCHEME_Q4_K>(x, k, x16, scale, row, lane);
     else if (perm == R9VX_SCHEME_IQ4_XS)
         x16_row<R9VX_SCHEME_IQ4_XS>(x, k, x16, scale, row, lane);
+    else if (perm == R9VX_SCHEME_Q6_K)
+        x16_row<R9VX_SCHEME_Q6_K>(x, k, x16, scale, row, lane);
     else
         x16_row<0>(x, k, x16, scale, row, lane);
 }

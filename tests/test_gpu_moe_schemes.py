@@ -56,7 +56,8 @@ def test_moe_ffn_expert_schemes(gu_s, dn_s, t):
     check_close(y.cpu().numpy(), ref, f"{NAMES[gu_s]}/{NAMES[dn_s]} t={t}")
 
 
-BIG_PAIRS = [(ffi.IQ3_S, ffi.Q4_K), (ffi.IQ3_S, ffi.IQ4_XS), (ffi.Q6_K, ffi.Q8_0), (ffi.Q8_0, ffi.Q8_0)]
+BIG_PAIRS = [(ffi.IQ3_S, ffi.Q4_K), (ffi.IQ3_S, ffi.IQ4_XS), (ffi.Q6_K, ffi.Q8_0), (ffi.Q8_0, ffi.Q8_0),
+             (ffi.Q8_0, ffi.Q6_K), (ffi.IQ3_S, ffi.Q6_K)]
 
 
 @pytest.mark.parametrize("t", [4, 200])

@@ -163,9 +163,8 @@ PREFILL = [(9, 320, 2048), (40, 1000, 4096), (300, 512, 2048), (129, 2304, 1024)
 @pytest.mark.parametrize("scheme", SCHEMES)
 @pytest.mark.parametrize("m,n,k", PREFILL)
 def test_prefill_gemm_split_layout_parity(scheme, m, n, k):
-    """m > 8: the MFMA GEMM on the split layout (Q6_K, and Q8_0 at n % 256 !=
-    0: the LDS-decoded 128 x 256 tile; Q8_0 at n % 256 == 0: the 256 x 256
-    loop)."""
+    """m > 8: the MFMA GEMM on the split layout (n % 256 != 0: the
+    LDS-decoded 128 x 256 tile; n % 256 == 0: the 256 x 256 loop)."""
     w = synth.quant_weights(scheme, 3000 + m + n, n, k)
     x = synth.normal_bf16(4000 + m + k, (m, k))
     body, scales = ffi.repack(dev(w), scheme, n, k)
@@ -173,21 +172,23 @@ def test_prefill_gemm_split_layout_parity(scheme, m, n, k):
     check_close(y, O.matmul(scheme, w, n, k, x, O.BF16, threads=8), f"scheme={scheme} m={m} n={n} k={k}")
 
 
-# Q8_0 with n % 256 == 0 runs the 256 x 256 loop that decodes each weight
-# tile once into LDS (two threads per weight row, one whole block each per K
-# step, loaded two steps ahead); these shapes reach its row-chunk plans (one
-# block, uniform chunks in the XCD band order, two chunk counts, several
-# rounds) with ragged last row tiles and the bias epilogue.
+# Q8_0 / Q6_K with n % 256 == 0 run the 256 x 256 loop that decodes each
+# weight tile once into LDS (two threads per weight row; a thread's half K
+# step is one Q8_0 block, or 16 Q6_K ql bytes and their 16 qh bytes, loaded
+# two steps ahead); these shapes reach its row-chunk plans (one block,
+# uniform chunks in the XCD band order, two chunk counts, several rounds)
+# with ragged last row tiles and the bias epilogue.
+@pytest.mark.parametrize("scheme", SCHEMES)
 @pytest.mark.parametrize("m,n,k", [(9, 256, 512), (700, 2560, 512), (1100, 5376, 512), (2048, 4096, 1024)])
-def test_prefill_gemm_q8_0_256_tile(m, n, k):
-    w = synth.quant_weights(ffi.Q8_0, 3100 + m, n, k)
+def test_prefill_gemm_split_256_tile(scheme, m, n, k):
+    w = synth.quant_weights(scheme, 3100 + m + scheme, n, k)
     x = synth.normal_bf16(3200 + m, (m, k))
     b = synth.normal_f32(3300 + m, (n,))
-    body, scales = ffi.repack(dev(w), ffi.Q8_0, n, k)
-    y = host(ffi.matmul(body, ffi.Q8_0, n, k, bf16_dev(x), bias=dev(b), w_scales=scales))
+    body, scales = ffi.repack(dev(w), scheme, n, k)
+    y = host(ffi.matmul(body, scheme, n, k, bf16_dev(x), bias=dev(b), w_scales=scales))
     rows = np.arange(m) if m * n <= 4_000_000 else np.unique(np.concatenate([np.arange(0, m, 7), [m - 1]]))
-    ref = O.matmul(ffi.Q8_0, w, n, k, np.ascontiguousarray(x[rows]), O.BF16, bias=b, threads=8)
-    check_close(y[rows], ref, f"m={m} n={n} k={k}")
+    ref = O.matmul(scheme, w, n, k, np.ascontiguousarray(x[rows]), O.BF16, bias=b, threads=8)
+    check_close(y[rows], ref, f"scheme={scheme} m={m} n={n} k={k}")
 
 
 @pytest.mark.parametrize("scheme", SCHEMES)
