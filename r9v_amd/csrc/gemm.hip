@@ -291,7 +291,13 @@ __global__ __launch_bounds__(512, 1) void gemm3_kernel(GemmArgs a) {
     const uint32_t span = 32u * (per + (ch < rem ? 1u : 0u));
     const uint32_t rows = a.m - m0 < span ? a.m - m0 : span;
     const float rsc = tid < rows ? a.scale[m0 + tid] : 0.f;
-    if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) m3_init_iq4_lut(sm.lut, tid, 512);
+    uint32_t *lut = sm.lut;
+    if constexpr (SCHEME == R9VX_SCHEME_IQ4_XS) m3_init_iq4_lut(lut, tid, 512);
+    if constexpr (SCHEME == R9VX_SCHEME_IQ3_S) {
+        __shared__ __attribute__((aligned(16))) uint32_t lut3[kM3Iq3Words];
+        lut = lut3;
+        m3_init_iq3s_lut(lut, tid, 512);
+    }
     __syncthreads();
 
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
@@ -309,7 +315,7 @@ __global__ __launch_bounds__(512, 1) void gemm3_kernel(GemmArgs a) {
     const uint32_t rh = wv >> 2, cq = wv & 3;
     const uint32_t nr = m3_active_tiles(rows, 128 * rh);
     r9vx_f32x16 acc[4][2];
-    m3_run<SCHEME, true>(nr, rows <= 128, sm, a.x16, aoff, w, a.k / kTileK, tid, wv, sm.lut, 128 * rh, 64 * cq, 64 * cq + 32, acc);
+    m3_run<SCHEME, true>(nr, rows <= 128, sm, a.x16, aoff, w, a.k / kTileK, tid, wv, lut, 128 * rh, 64 * cq, 64 * cq + 32, acc);
     if (tid < kM3Rows) rowsc[tid] = rsc;
     __syncthreads();
 
@@ -471,13 +477,13 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
      * addressing bound -- never from the launch's row count: a row's outputs
      * are the same bits whatever rows share the launch, at whatever index,
      * and in every bucket above the decode GEMV's.  Q4_K / IQ4_XS run the
-     * 256 x 256 tiles (gemm3 for N % 256 == 0, gemm2 otherwise), Q8_0 / Q6_K
-     * gemm3 for N % 256 == 0; IQ3_S, and Q8_0 / Q6_K otherwise, the 128-row
-     * LDS-decoded tile. */
+     * 256 x 256 tiles (gemm3 for N % 256 == 0, gemm2 otherwise), Q8_0 / Q6_K /
+     * IQ3_S gemm3 for N % 256 == 0 and the 128-row LDS-decoded tile
+     * otherwise. */
     const bool split = p.scheme == R9VX_SCHEME_Q8_0 || p.scheme == R9VX_SCHEME_Q6_K || p.scheme == R9VX_SCHEME_IQ3_S;
     const bool m3_shape = p.n % kM3Cols == 0 && (uint64_t)p.m_bucket * p.k < (1ull << 31);
-    if ((p.scheme == R9VX_SCHEME_Q8_0 || p.scheme == R9VX_SCHEME_Q6_K) && m3_shape) {
-        /* the split layouts on the 256 x 256 loop, x in their K order */
+    if (split && m3_shape) {
+        /* the split and IQ3_S layouts on the 256 x 256 loop, x in their K order */
         const int rc = r9vx_launch_x_to_f16(p.x, p.m, p.k, x16, scale, r9vx_group_order(p.scheme), stream);
         if (rc) return rc;
         a.m_tiles = (p.m + kM2Rows - 1) / kM2Rows;
@@ -485,8 +491,10 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
         const dim3 grid3(plan_chunks(a, r9vx_device_cus()));
         if (p.scheme == R9VX_SCHEME_Q8_0)
             hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_Q8_0>), grid3, dim3(512), 0, stream, a);
-        else
+        else if (p.scheme == R9VX_SCHEME_Q6_K)
             hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_Q6_K>), grid3, dim3(512), 0, stream, a);
+        else
+            hipLaunchKernelGGL((gemm3_kernel<R9VX_SCHEME_IQ3_S>), grid3, dim3(512), 0, stream, a);
         return (int)hipGetLastError();
     }
     if (!split) {
@@ -517,7 +525,7 @@ int r9vx_launch_gemm(const r9vx_gemm_problem &p, hipStream_t stream) {
     a.m_tiles = (p.m + 127) / 128;
     a.n_tiles = (p.n + 255) / 256;
     dim3 grid(a.m_tiles * a.n_tiles);
-    /* IQ3_S (and Q8_0 / Q6_K at N % 256 != 0) take this LDS-decoded tile (their steps do not
+    /* Q8_0 / Q6_K / IQ3_S at N % 256 != 0 take this LDS-decoded tile (their steps do not
      * fit the register-decoded core's 16-byte lane payload). */
     switch (p.scheme) {
     case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL((gemm_kernel<R9VX_SCHEME_Q6_K, 128, 1>), grid, dim3(256), 0, stream, a); break;

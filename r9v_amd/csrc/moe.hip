@@ -112,43 +112,28 @@ __device__ __forceinline__ bool sort_x16_part(const SortArgs &a, uint32_t b0, ui
 }
 
 /* The grouped GEMMs' row tiles (moe_gemm.hip): expert x with n pairs from
- * sorted position `off` becomes ceil(n / 128) entries (expert, first
- * position, rows, 0) of `tiles` and ceil(n / 256) of `tiles3`, experts in
- * ascending id, then the shared experts (t rows each, after the P pair
- * rows); status[3] / status[4] = the counts.  Thread x < E passes expert
- * x's count and offset (blockDim.x >= E). */
+ * sorted position `off` becomes ceil(n / 256) entries (expert, first
+ * position, rows, 0) of `tiles3`, experts in ascending id, then the shared
+ * experts (t rows each, after the P pair rows); status[4] = the count.
+ * Thread x < E passes expert x's count and offset (blockDim.x >= E). */
 __device__ void put_tile_lists(const SortArgs &a, uint32_t tot, uint32_t off, uint32_t *sh) {
     const MoeLayout &L = a.L;
-    r9vx_u32x4 *t1 = reinterpret_cast<r9vx_u32x4 *>(a.ws + L.tiles);
     r9vx_u32x4 *t3 = reinterpret_cast<r9vx_u32x4 *>(a.ws + L.tiles3);
     const uint32_t tid = threadIdx.x;
     const bool mine = tid < a.e;
-    const uint32_t n1 = mine ? (tot + kMoeTileM - 1) / kMoeTileM : 0u, n3 = mine ? (tot + kMoeTileM3 - 1) / kMoeTileM3 : 0u;
-    uint32_t all1, all3;
-    const uint32_t b1 = block_excl_scan(n1, sh, all1);
+    const uint32_t n3 = mine ? (tot + kMoeTileM3 - 1) / kMoeTileM3 : 0u;
+    uint32_t all3;
     const uint32_t b3 = block_excl_scan(n3, sh, all3);
-    for (uint32_t j = 0; j < n1; ++j) {
-        const uint32_t r = tot - j * kMoeTileM;
-        t1[b1 + j] = r9vx_u32x4{tid, off + j * kMoeTileM, r < kMoeTileM ? r : kMoeTileM, 0u};
-    }
     for (uint32_t j = 0; j < n3; ++j) {
         const uint32_t r = tot - j * kMoeTileM3;
         t3[b3 + j] = r9vx_u32x4{tid, off + j * kMoeTileM3, r < kMoeTileM3 ? r : kMoeTileM3, 0u};
     }
-    const uint32_t s1 = (a.t + kMoeTileM - 1) / kMoeTileM, s3 = (a.t + kMoeTileM3 - 1) / kMoeTileM3;
-    for (uint32_t i = tid; i < a.shared * s1; i += blockDim.x) {
-        const uint32_t sx = i / s1, j = i % s1, r = a.t - j * kMoeTileM;
-        t1[all1 + i] = r9vx_u32x4{a.e + sx, a.p + sx * a.t + j * kMoeTileM, r < kMoeTileM ? r : kMoeTileM, 0u};
-    }
+    const uint32_t s3 = (a.t + kMoeTileM3 - 1) / kMoeTileM3;
     for (uint32_t i = tid; i < a.shared * s3; i += blockDim.x) {
         const uint32_t sx = i / s3, j = i % s3, r = a.t - j * kMoeTileM3;
         t3[all3 + i] = r9vx_u32x4{a.e + sx, a.p + sx * a.t + j * kMoeTileM3, r < kMoeTileM3 ? r : kMoeTileM3, 0u};
     }
-    if (tid == 0) {
-        uint32_t *status = reinterpret_cast<uint32_t *>(a.ws + L.status);
-        status[3] = all1 + a.shared * s1;
-        status[4] = all3 + a.shared * s3;
-    }
+    if (tid == 0) reinterpret_cast<uint32_t *>(a.ws + L.status)[4] = all3 + a.shared * s3;
 }
 
 /* P <= 1024 pairs: everything in one workgroup of 1024 threads. */

@@ -6,8 +6,7 @@
  * gate/up Branch-D GEMM, act_mul SiLU, down GEMM); the combine is moe.hip's.
  *
  *  tiles : each expert with n pairs (or shared expert with t rows) is
- *          ceil(n / 256) row tiles (ceil(n / 128) for the LDS-decoded
- *          kernels), listed by the sort (moe.hip).
+ *          ceil(n / 256) row tiles, listed by the sort (moe.hip).
  *  gate/up: a workgroup owns 256 permuted rows x 128 columns j of h; its
  *          weight tile is gate rows j0.. and the matching up rows Dff+j0..,
  *          and a wave's two column tiles are a gate tile and its up tile, so
@@ -20,19 +19,16 @@
  *          256-row gate/up writes it directly, each 128-column block at its
  *          own scale (max|block| below 2^15), and the 256-row down GEMM
  *          rescales its f32 accumulators by the exponent step at each block
- *          boundary; for the LDS-decoded down kernels h_fix_kernel first
- *          brings a row's blocks to the row's scale.  The 128-row
- *          LDS-decoded gate/up writes f32 h, which h_to_f16_kernel converts
- *          at one scale per row.
+ *          boundary (past kM3MaxBlk blocks h_fix_kernel first brings a row's
+ *          blocks to the row's scale).
  *  down  : a workgroup owns 256 rows x 256 output columns of o; the scale is
  *          undone on the f32 accumulators.
- * Both GEMMs run the main loop of r9vx_mma3.h (weights decoded once per
- * workgroup into LDS, 8 waves, one workgroup per CU); a wave whose 128 rows
+ * Both GEMMs run the main loop of r9vx_mma3.h for every weight scheme
+ * (weights decoded once per workgroup into LDS, 8 waves, one workgroup per
+ * CU); a wave whose 128 rows
  * hold fewer than 4 row tiles of the tile runs only the MFMAs of those.
  * Tiles past the scanned count exit.
  */
-#include "r9vx_mma.h"
-#include "r9vx_mma2.h"
 #include "r9vx_mma3.h"
 #include "r9vx_moe.h"
 
@@ -40,7 +36,6 @@ using namespace r9vx;
 
 namespace {
 
-constexpr uint32_t kBM = kMoeTileM; /* 128 rows per tile */
 
 struct GroupedArgs {
     const _Float16 *x16;
@@ -79,163 +74,7 @@ __device__ __forceinline__ uint32_t row_token(const GroupedArgs &a, uint32_t exp
     return ws_u32(a, a.L.sorted)[pos] / a.k;
 }
 
-/* ---------------------------------------------------------------- gate/up */
-
-constexpr int kMT = 4;                       /* waves = 32-row tiles per workgroup */
-constexpr int kStage = 32 * kMT * 128;       /* 16 KiB per A stage */
-
-#define R9VX_MOE_STAGES                                                \
-    __shared__ __attribute__((aligned(16))) uint8_t st0[kStage];      \
-    __shared__ __attribute__((aligned(16))) uint8_t st1[kStage];      \
-    __shared__ __attribute__((aligned(16))) uint8_t st2[kStage];      \
-    __shared__ __attribute__((aligned(16))) uint8_t st3[kStage];      \
-    __shared__ __attribute__((aligned(16))) float lutf[512];          \
-    uint8_t *const stages[4] = {st0, st1, st2, st3};
-
-/* Gate/up experts the r9vx_mma3.h loop does not decode (IQ3_S): the
- * LDS-decoded main loop of r9vx_mma.h (a 128 x
- * 256 tile; thread t decodes weight row t of the tile into LDS: threads
- * 0..127 the gate rows j0..j0+127, threads 128..255 the up rows of the same
- * columns, so tile column c pairs with column c + 128), with the activations
- * in natural K order.  The accumulators pass through a 32 x 256 f32 LDS
- * stage, 32 rows at a time, and each thread writes silu(g) * u for 4
- * columns of 4 rows. */
-template <int GU>
-__global__ __launch_bounds__(256, 2) void moe_gu_lds_kernel(GroupedArgs a) {
-    using S = MmaShape<kBM, 1>;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
-    __shared__ float rowsc[kBM];
-    const uint32_t *status = ws_u32(a, a.L.status);
-    uint32_t tix, nt;
-    xcd_tile(a.dff / 128, tix, nt);
-    if (status[0] != 0u || tix >= status[3]) return;
-    const r9vx_u32x4 tile = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles)[tix];
-    const uint32_t expert = tile.x, pos0 = tile.y, rows = tile.z;
-    const uint32_t j0 = nt * 128;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid < kBM) rowsc[tid] = tid < rows ? a.xscale[row_token(a, expert, pos0 + tid)] : 0.f;
-
-    AF16Rows<kBM> as;
-    as.chunk = tid & 7;
-    as.row0 = tid >> 3;
-#pragma unroll
-    for (int i = 0; i < (int)kBM / 32; ++i) {
-        const uint32_t r = as.row0 + 32 * i;
-        as.row[i] = a.x16 + (uint64_t)row_token(a, expert, pos0 + (r < rows ? r : 0)) * a.dm + 8 * as.chunk;
-    }
-    const uint64_t wr = (uint64_t)expert * 2 * a.dff + (tid < 128 ? j0 + tid : (uint64_t)a.dff + j0 + (tid - 128));
-    const uint8_t *wrow = a.w_gu + wr * a.gu_row_bytes;
-    const uint16_t *srow = a.s_gu ? a.s_gu + wr * a.gu_srow : nullptr;
-    r9vx_f32x16 acc[kBM / 32][2];
-    mma_mainloop<GU, kBM, 1>(lds, as, wrow, a.dm / kTileK, acc, srow);
-
-    constexpr uint32_t kSRow = 260;
-    float *stage = reinterpret_cast<float *>(lds);
-    float *h = reinterpret_cast<float *>(a.ws + a.L.h);
-    const uint32_t c4 = 4 * (tid & 31);
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < (int)kBM / 32; ++i) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) stage[acc_row(0, r, lane) * kSRow + acc_col(wave, j, lane)] = acc[i][j][r];
-        __syncthreads();
-        for (uint32_t q = 0; q < 4; ++q) {
-            const uint32_t rl = (tid >> 5) + 8 * q, row = 32 * i + rl;
-            if (row >= rows) continue;
-            const float sc = rowsc[row];
-            const r9vx_f32x4 g4 = *reinterpret_cast<const r9vx_f32x4 *>(stage + rl * kSRow + c4);
-            const r9vx_f32x4 u4 = *reinterpret_cast<const r9vx_f32x4 *>(stage + rl * kSRow + 128 + c4);
-            const float gv[4] = {g4.x * sc, g4.y * sc, g4.z * sc, g4.w * sc};
-            const float uv[4] = {u4.x * sc, u4.y * sc, u4.z * sc, u4.w * sc};
-            float v[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) v[c] = swiglu_fast(gv[c], uv[c]);
-            *reinterpret_cast<r9vx_f32x4 *>(h + (uint64_t)(pos0 + row) * a.dff + j0 + c4) = r9vx_f32x4{v[0], v[1], v[2], v[3]};
-        }
-        __syncthreads();
-    }
-}
-
-/* ---------------------------------------------------------------- h -> fp16 */
-
-/* One wave per h row: max|h| over the row, e = row_shift(max|h|) (kept in
- * hexp and hbe for the down GEMMs), then lane l writes group l % 8 of K
- * step l / 8 (+ 8 per pass) as 8 fp16 in the down scheme's group order,
- * scaled by 2^-e. */
-/* Row element of elements i .. i + 3 of the group stored at position c of
- * an h16 row; DN: the rows' order (r9vx_group_order of the down scheme: the
- * group order of the r9vx_mma3.h loop, 0 natural). */
-template <int DN>
-__device__ __forceinline__ uint32_t h_pos(uint32_t c, uint32_t i) {
-    return order_pos<DN>(c, i);
-}
-
-/* A row converted at one scale 2^-e: e goes to hexp and to each of its
- * blocks' hbe entries (the 256-row down GEMM reads those). */
-__device__ __forceinline__ void put_row_exp(const GroupedArgs &a, uint32_t row, int e, uint32_t lane) {
-    const uint32_t nb = a.dff / 128, stride = r9vx_moe_hbe_stride(a.dff);
-    if (lane == 0) reinterpret_cast<int32_t *>(a.ws + a.L.hexp)[row] = e;
-    for (uint32_t b = lane; b < nb; b += 64) reinterpret_cast<int8_t *>(a.ws + a.L.hbe)[(uint64_t)row * stride + b] = (int8_t)e;
-}
-
-template <int DN>
-__global__ __launch_bounds__(256) void h_to_f16_kernel(GroupedArgs a, uint32_t nrows) {
-    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (row >= nrows) return;
-    const uint32_t *status = ws_u32(a, a.L.status);
-    if (status[0] != 0u) return;
-    const float *hr = reinterpret_cast<const float *>(a.ws + a.L.h) + (uint64_t)row * a.dff;
-    _Float16 *orow = a.h16 + (uint64_t)row * a.dff;
-    if (a.dff <= 1024) {
-        /* one pass: the lane loads the values it writes (all of the row
-         * between the wave's lanes), takes the row max from them and
-         * converts from registers */
-        r9vx_f32x4 lo[2], hi[2];
-        float mx = 0.f;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t c = lane + 64 * i;
-            const uint32_t cc = c < a.dff / 8 ? c : 0u;
-            lo[i] = *reinterpret_cast<const r9vx_f32x4 *>(hr + h_pos<DN>(8 * cc, 0));
-            hi[i] = *reinterpret_cast<const r9vx_f32x4 *>(hr + h_pos<DN>(8 * cc, 4));
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(fabsf(lo[i].x), fabsf(lo[i].y)), fmaxf(fabsf(lo[i].z), fabsf(lo[i].w))),
-                                 fmaxf(fmaxf(fabsf(hi[i].x), fabsf(hi[i].y)), fmaxf(fabsf(hi[i].z), fabsf(hi[i].w)))));
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-        put_row_exp(a, row, row_shift(mx), lane);
-        const float inv = ldexpf(1.0f, -row_shift(mx));
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t c = lane + 64 * i;
-            if (c >= a.dff / 8) break;
-            *reinterpret_cast<r9vx_u32x4 *>(orow + 8 * c) = r9vx_u32x4{
-                pack_h2(lo[i].x * inv, lo[i].y * inv), pack_h2(lo[i].z * inv, lo[i].w * inv),
-                pack_h2(hi[i].x * inv, hi[i].y * inv), pack_h2(hi[i].z * inv, hi[i].w * inv)};
-        }
-        return;
-    }
-    float mx = 0.f;
-    for (uint32_t c = lane; c < a.dff / 4; c += 64) {
-        const r9vx_f32x4 v = *reinterpret_cast<const r9vx_f32x4 *>(hr + 4 * c);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    put_row_exp(a, row, row_shift(mx), lane);
-    const float inv = ldexpf(1.0f, -row_shift(mx));
-    for (uint32_t c = lane; c < a.dff / 8; c += 64) {
-        const r9vx_f32x4 lo = *reinterpret_cast<const r9vx_f32x4 *>(hr + h_pos<DN>(8 * c, 0));
-        const r9vx_f32x4 hi = *reinterpret_cast<const r9vx_f32x4 *>(hr + h_pos<DN>(8 * c, 4));
-        *reinterpret_cast<r9vx_u32x4 *>(orow + 8 * c) =
-            r9vx_u32x4{pack_h2(lo.x * inv, lo.y * inv), pack_h2(lo.z * inv, lo.w * inv), pack_h2(hi.x * inv, hi.y * inv),
-                       pack_h2(hi.z * inv, hi.w * inv)};
-    }
-}
+/* ---------------------------------------------------------------- helpers */
 
 /* 4-byte load into a register that a later main loop's counted wait
  * covers (it is issued before that loop's loads); the destination is tied
@@ -261,9 +100,8 @@ __device__ __forceinline__ uint32_t h_chunk(uint32_t order, uint32_t c, uint32_t
     return order_pos<0>(c, i) / 4;
 }
 
-/* After the 256-row gate/up GEMM, for the down kernels that undo one
- * power-of-two scale per h16 row (the LDS-decoded ones, and the 256-row one
- * past kM3MaxBlk blocks): gives each row that scale.  The row's e is the
+/* After the gate/up GEMM, for a down GEMM past kM3MaxBlk blocks (which then
+ * undoes one power-of-two scale per h16 row): gives each row that scale.  The row's e is the
  * largest of its blocks' (hbe; row_shift is monotonic, so it is row_shift of
  * the row's max|h|) and goes to hexp.  Each block at a smaller e is
  * multiplied by 2^(e_block - e_row), a power of two below 1 -- exact unless
@@ -299,92 +137,6 @@ __global__ __launch_bounds__(256) void h_fix_kernel(GroupedArgs a, uint32_t nrow
     }
 }
 
-/* ---------------------------------------------------------------- down, LDS-decoded */
-
-/* Down experts the r9vx_mma3.h loop does not decode (IQ3_S): the
- * LDS-decoded main loop of r9vx_mma.h over a
- * 128-row tile of h16 rows (natural K order) and output columns n0 .. n0 +
- * 255 (thread t decodes weight row n0 + t).  The accumulators pass through
- * a 32 x 256 f32 LDS stage, 32 rows at a time; thread t then owns 32
- * consecutive columns of row t / 8 and writes them as the fp16 rows and
- * per-(row, 64-column) power-of-two scales the grouped combine reads (the
- * block's max: this thread's and its neighbour's). */
-template <int DN>
-__global__ __launch_bounds__(256, 2) void moe_dn_lds_kernel(GroupedArgs a) {
-    using S = MmaShape<kBM, 1>;
-    __shared__ __attribute__((aligned(16))) uint8_t lds[S::kLds];
-    __shared__ float rowsc[kBM]; /* 2^e that undoes each h row's fp16 scale */
-    const uint32_t *status = ws_u32(a, a.L.status);
-    uint32_t tix, nt;
-    xcd_tile(a.dm / 256, tix, nt);
-    if (status[0] != 0u || tix >= status[3]) return;
-    const r9vx_u32x4 tile = reinterpret_cast<const r9vx_u32x4 *>(a.ws + a.L.tiles)[tix];
-    const uint32_t pos0 = tile.y, rows = tile.z, expert = tile.x;
-    const uint32_t n0 = nt * 256;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid < kBM)
-        rowsc[tid] = tid < rows ? ldexpf(1.0f, reinterpret_cast<const int32_t *>(a.ws + a.L.hexp)[pos0 + tid]) : 0.f;
-    AF16Rows<kBM> as;
-    as.chunk = tid & 7;
-    as.row0 = tid >> 3;
-#pragma unroll
-    for (int i = 0; i < (int)kBM / 32; ++i) {
-        const uint32_t r = as.row0 + 32 * i;
-        as.row[i] = a.h16 + (uint64_t)(pos0 + (r < rows ? r : 0)) * a.dff + 8 * as.chunk;
-    }
-    const uint64_t wr = (uint64_t)expert * a.dm + n0 + tid;
-    const uint8_t *wrow = a.w_dn + wr * a.dn_row_bytes;
-    const uint16_t *srow = a.s_dn ? a.s_dn + wr * a.dn_srow : nullptr;
-    r9vx_f32x16 acc[kBM / 32][2];
-    mma_mainloop<DN, kBM, 1>(lds, as, wrow, a.dff / kTileK, acc, srow);
-
-    constexpr uint32_t kSRow = 260;
-    float *stage = reinterpret_cast<float *>(lds);
-    const uint64_t nrows_all = (uint64_t)a.p + (uint64_t)a.shared * a.t;
-    _Float16 *o16 = reinterpret_cast<_Float16 *>(a.ws + a.L.o);
-    float *oscale = reinterpret_cast<float *>(a.ws + a.L.o + r9vx_moe_oscale_offset(nrows_all, a.dm));
-    const uint32_t rl = tid >> 3, c0 = 32 * (tid & 7), nblk = a.dm / 64;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < (int)kBM / 32; ++i) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) stage[acc_row(0, r, lane) * kSRow + acc_col(wave, j, lane)] = acc[i][j][r];
-        __syncthreads();
-        const uint32_t row = 32 * i + rl;
-        const float sc = row < rows ? rowsc[row] : 0.f;
-        float v[32];
-        float m = 0.f;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const r9vx_f32x4 q = *reinterpret_cast<const r9vx_f32x4 *>(stage + rl * kSRow + c0 + 4 * c);
-            v[4 * c] = q.x * sc;
-            v[4 * c + 1] = q.y * sc;
-            v[4 * c + 2] = q.z * sc;
-            v[4 * c + 3] = q.w * sc;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) m = fmaxf(m, fabsf(v[4 * c + u]));
-        }
-        m = fmaxf(m, __shfl_xor(m, 1, 64)); /* the 64-column block: threads 2b, 2b + 1 */
-        int e = 0;
-        (void)frexpf(m, &e); /* m = f 2^e, f in [0.5, 1) */
-        if (row < rows) {
-            const float f = ldexpf(1.0f, 15 - e);
-            _Float16 *orow = o16 + (uint64_t)(pos0 + row) * a.dm + n0 + c0;
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-                *reinterpret_cast<r9vx_u32x4 *>(orow + 8 * c) =
-                    r9vx_u32x4{pack_h2h((_Float16)(v[8 * c] * f), (_Float16)(v[8 * c + 1] * f)),
-                               pack_h2h((_Float16)(v[8 * c + 2] * f), (_Float16)(v[8 * c + 3] * f)),
-                               pack_h2h((_Float16)(v[8 * c + 4] * f), (_Float16)(v[8 * c + 5] * f)),
-                               pack_h2h((_Float16)(v[8 * c + 6] * f), (_Float16)(v[8 * c + 7] * f))};
-            if ((tid & 1) == 0) oscale[(uint64_t)(pos0 + row) * nblk + (n0 + c0) / 64] = ldexpf(1.0f, e - 15);
-        }
-        __syncthreads();
-    }
-}
-
 /* ---------------------------------------------------------------- 256-row tiles */
 
 /* Gate/up on the r9vx_mma3.h loop: a workgroup owns a 256-row tile of one
@@ -395,7 +147,7 @@ __global__ __launch_bounds__(256, 2) void moe_dn_lds_kernel(GroupedArgs a) {
 template <int GU>
 __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
     __shared__ __attribute__((aligned(16))) M3Lds sm;
-    uint32_t *const lut = sm.lut;
+    uint32_t *lut = sm.lut;
     __shared__ float rowsc[kMoeTileM3];
     const uint32_t *status = ws_u32(a, a.L.status);
     uint32_t tix, nt;
@@ -414,6 +166,11 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
      * loop (the epilogue is its only reader) */
     const float rsc = tid < rows ? a.xscale[row_token(a, expert, pos0 + (tid < kMoeTileM3 ? tid : 0))] : 0.f;
     if constexpr (GU == R9VX_SCHEME_IQ4_XS) m3_init_iq4_lut(lut, tid, 512);
+    if constexpr (GU == R9VX_SCHEME_IQ3_S) {
+        __shared__ __attribute__((aligned(16))) uint32_t lut3[kM3Iq3Words];
+        lut = lut3;
+        m3_init_iq3s_lut(lut, tid, 512);
+    }
     __syncthreads();
 
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
@@ -503,7 +260,7 @@ __global__ __launch_bounds__(512, 1) void moe_gu_m3_kernel(GroupedArgs a) {
 template <int DN, int PASSES>
 __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
     __shared__ __attribute__((aligned(16))) M3Lds sm;
-    uint32_t *const lut = sm.lut;
+    uint32_t *lut = sm.lut;
     __shared__ float rowsc[kMoeTileM3]; /* 2^e that undoes each h row's last block's fp16 scale */
     __shared__ uint32_t bst[kM3MaxBlk * 64]; /* the rows' exponent steps per 128-K block (m3_bsd) */
     const uint32_t *status = ws_u32(a, a.L.status);
@@ -556,6 +313,11 @@ __global__ __launch_bounds__(512, 1) void moe_dn_m3_kernel(GroupedArgs a) {
         rowsc[tid] = tid < rows ? ldexpf(1.0f, eprev) : 0.f;
     };
     if constexpr (DN == R9VX_SCHEME_IQ4_XS) m3_init_iq4_lut(lut, tid, 512);
+    if constexpr (DN == R9VX_SCHEME_IQ3_S) {
+        __shared__ __attribute__((aligned(16))) uint32_t lut3[kM3Iq3Words];
+        lut = lut3;
+        m3_init_iq3s_lut(lut, tid, 512);
+    }
     __syncthreads();
 
     const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
@@ -706,39 +468,26 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
                                       reinterpret_cast<float *>(p.ws + L.xscale), r9vx_group_order(p.scheme_gu), s);
         if (rc) return rc;
     }
-    /* upper bounds on row tiles: ceil(P/TM) + one partial tile per work item */
-    const uint32_t max_tiles = (a.p + kBM - 1) / kBM + (a.p < p.e ? a.p : p.e) +
-                               (p.shared ? p.shared * ((p.t + kBM - 1) / kBM) : 0);
+    /* upper bound on row tiles: ceil(P/TM) + one partial tile per work item */
     const uint32_t max_tiles3 = (a.p + kMoeTileM3 - 1) / kMoeTileM3 + (a.p < p.e ? a.p : p.e) +
                                 (p.shared ? p.shared * ((p.t + kMoeTileM3 - 1) / kMoeTileM3) : 0);
-    const uint32_t tiles8 = (max_tiles + 7) / 8 * 8, tiles3_8 = (max_tiles3 + 7) / 8 * 8; /* xcd_tile's grids */
-    const dim3 ggu(tiles8 * (p.dff / 128)), ggu3(tiles3_8 * (p.dff / 128)), gdn(tiles8 * (p.dm / 256)),
-        gdn3(tiles3_8 * (p.dm / 256));
+    const uint32_t tiles3_8 = (max_tiles3 + 7) / 8 * 8; /* xcd_tile's grids */
+    const dim3 ggu3(tiles3_8 * (p.dff / 128)), gdn3(tiles3_8 * (p.dm / 256));
     if (part == 0 || part == 1) {
         switch (p.scheme_gu) {
         case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_IQ4_XS>, ggu3, dim3(512), 0, s, a); break;
         case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q4_K>, ggu3, dim3(512), 0, s, a); break;
         case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q8_0>, ggu3, dim3(512), 0, s, a); break;
         case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_Q6_K>, ggu3, dim3(512), 0, s, a); break;
-        default: hipLaunchKernelGGL(moe_gu_lds_kernel<R9VX_SCHEME_IQ3_S>, ggu, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL(moe_gu_m3_kernel<R9VX_SCHEME_IQ3_S>, ggu3, dim3(512), 0, s, a); break;
         }
     }
     const uint32_t nrows = a.p + p.shared * p.t;
-    const dim3 gh((nrows + 3) / 4);
-    /* the 256-row gate/up writes h16 at a scale per 128-column block, which
-     * the 256-row down GEMM takes as it is (up to kM3MaxBlk blocks); the
-     * LDS-decoded down kernels take one scale per row */
-    const bool gu_m3 = r9vx_m3_scheme(p.scheme_gu), dn_m3 = r9vx_m3_scheme(p.scheme_dn);
-    if (gu_m3 && (!dn_m3 || p.dff / 128 > kM3MaxBlk) && (part == 0 || part == 1))
+    /* the gate/up GEMM writes h16 at a scale per 128-column block, which the
+     * down GEMM takes as it is up to kM3MaxBlk blocks; past that every row
+     * is brought to one scale first */
+    if (p.dff / 128 > kM3MaxBlk && (part == 0 || part == 1))
         hipLaunchKernelGGL(h_fix_kernel, dim3((nrows + 255) / 256), dim3(256), 0, s, a, nrows);
-    if (!gu_m3 && part == 0) {
-        switch (a.h_order) {
-        case R9VX_SCHEME_Q4_K: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q4_K>, gh, dim3(256), 0, s, a, nrows); break;
-        case R9VX_SCHEME_IQ4_XS: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_IQ4_XS>, gh, dim3(256), 0, s, a, nrows); break;
-        case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL(h_to_f16_kernel<R9VX_SCHEME_Q6_K>, gh, dim3(256), 0, s, a, nrows); break;
-        default: hipLaunchKernelGGL(h_to_f16_kernel<0>, gh, dim3(256), 0, s, a, nrows); break; /* natural */
-        }
-    }
     if (part == 0 || part == 2) {
         /* the 256-row Q4_K down GEMM takes two column blocks per workgroup when Dm / 256 is even */
         const bool two = (p.dm / 256) % 2 == 0;
@@ -755,7 +504,7 @@ int r9vx_moe_grouped_part(const r9vx_moe_problem &p, const MoeLayout &L, uint32_
             break;
         case R9VX_SCHEME_Q8_0: hipLaunchKernelGGL((moe_dn_m3_kernel<R9VX_SCHEME_Q8_0, 1>), gdn3, dim3(512), 0, s, a); break;
         case R9VX_SCHEME_Q6_K: hipLaunchKernelGGL((moe_dn_m3_kernel<R9VX_SCHEME_Q6_K, 1>), gdn3, dim3(512), 0, s, a); break;
-        default: hipLaunchKernelGGL(moe_dn_lds_kernel<R9VX_SCHEME_IQ3_S>, gdn, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL((moe_dn_m3_kernel<R9VX_SCHEME_IQ3_S, 1>), gdn3, dim3(512), 0, s, a); break;
         }
     }
     return (int)hipGetLastError();

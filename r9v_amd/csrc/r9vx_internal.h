@@ -165,20 +165,21 @@ __host__ __device__ inline uint32_t r9vx_row_scales(uint32_t scheme, uint32_t k)
     return scheme == R9VX_SCHEME_Q8_0 ? k / 32 : scheme == R9VX_SCHEME_Q6_K ? k / 256 : 0u;
 }
 
-/* Weight schemes the 256 x 256 loop of r9vx_mma3.h decodes (IQ3_S runs the
- * 128-row LDS-decoded tile of r9vx_mma.h). */
+/* Weight schemes the 256 x 256 loop of r9vx_mma3.h decodes: all five (the
+ * grouped MoE GEMMs take it for every scheme; the dense GEMM for N % 256 ==
+ * 0). */
 __host__ __device__ inline bool r9vx_m3_scheme(uint32_t scheme) {
     return scheme == R9VX_SCHEME_Q4_K || scheme == R9VX_SCHEME_IQ4_XS || scheme == R9VX_SCHEME_Q8_0 ||
-           scheme == R9VX_SCHEME_Q6_K;
+           scheme == R9VX_SCHEME_Q6_K || scheme == R9VX_SCHEME_IQ3_S;
 }
 /* The K order (r9vx_x16.h order_pos) that activation rows take for a weight
  * scheme on that loop: Q4_K's and Q6_K's own; IQ4_XS's for IQ4_XS and Q8_0
  * (in both, group s of a thread's half step is elements 4s .. 4s + 3 and
  * 16 + 4s .. 16 + 4s + 3 of one 32-weight sub-block or block); 0 (natural)
- * for the others. */
+ * for IQ3_S (a thread's half step is one 32-weight group in column order). */
 __host__ __device__ inline uint32_t r9vx_group_order(uint32_t scheme) {
     if (scheme == R9VX_SCHEME_Q4_K || scheme == R9VX_SCHEME_Q6_K) return scheme;
-    return r9vx_m3_scheme(scheme) ? (uint32_t)R9VX_SCHEME_IQ4_XS : 0u;
+    return scheme == R9VX_SCHEME_IQ4_XS || scheme == R9VX_SCHEME_Q8_0 ? (uint32_t)R9VX_SCHEME_IQ4_XS : 0u;
 }
 
 struct r9vx_moe_problem {

@@ -1,6 +1,6 @@
 /*
- * r9vx_mma.h -- the shared main loop of the dequant-to-LDS MFMA GEMMs (dense
- * prefill matmul, grouped MoE gate/up and down).
+ * r9vx_mma.h -- the main loop of the dequant-to-LDS MFMA GEMM that the dense
+ * prefill matmul runs for Q8_0 / Q6_K / IQ3_S weights when N % 256 != 0.
  *
  * Workgroup: 256 threads = 4 waves, output tile BM x 256.  Wave w owns the
  * 64 output columns [64w, 64w+64) and all BM rows: (BM/32) x 2 tiles of

@@ -142,6 +142,15 @@ struct BScale {
 template <int SCHEME, int KS>
 __device__ __forceinline__ BScale bscale(const r9vx_u32x4 &hd, uint32_t h, uint32_t hd2 = 0u) {
     BScale s;
+    if constexpr (SCHEME == R9VX_SCHEME_IQ3_S) {
+        /* hd: the block's side word; group 2 KS + h: db = d (1 + 2 s) with
+         * s its scale nibble (crates/r9v-format/src/iq.rs:698-722) */
+        const float d = r9vx_f16_to_f32((uint16_t)(hd.w & 0xFFFF));
+        s.dl0 = d * (float)(1u + 2u * ((hd.z >> (4 * (2 * KS + h))) & 0xFu));
+        s.c0 = -1152.f * s.dl0; /* exact: db has at most 16 significant bits */
+        s.nml0 = s.dl1 = s.nml1 = s.c1 = 0.f;
+        return s;
+    }
     if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
         /* hd: the block's 16 int8 scales, hd2: its f16 d.  Step KS (span n =
          * KS / 2, part j = KS % 2), half h: the low nibbles' columns take

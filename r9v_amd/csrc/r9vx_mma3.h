@@ -81,7 +81,12 @@ struct M3WRow {
  * Q6_K: 16 ql bytes and the 16 qh bytes holding their high bit pairs.  Two
  * 16-byte loads either way, so the payload ring holds two steps in the
  * registers the 4-bit schemes use for four. */
-constexpr bool m3_wide(int s) { return s == R9VX_SCHEME_Q8_0 || s == R9VX_SCHEME_Q6_K; }
+constexpr bool m3_wide(int s) {
+    return s == R9VX_SCHEME_Q8_0 || s == R9VX_SCHEME_Q6_K || s == R9VX_SCHEME_IQ3_S;
+}
+/* Schemes whose decode reads an LDS table (IQ4_XS: codebook pairs; IQ3_S:
+ * the signed grid, m3_init_iq3s_lut), ahead of the MFMA pair that uses it. */
+constexpr bool m3_table(int s) { return s == R9VX_SCHEME_IQ4_XS || s == R9VX_SCHEME_IQ3_S; }
 
 /* A pointer the caller knows to be wave-uniform, moved to scalar registers
  * (the loads take it as their SGPR base whatever the compiler's divergence
@@ -107,11 +112,22 @@ __device__ __forceinline__ void m3_load_pay(const M3WRow &w, uint32_t kt, uint32
  * j = s % 2; p0 = ql bytes 64 n + 32 j + 16 hh .. + 15 (low nibbles: columns
  * 128 n + 32 j + 16 hh + i, high: the same + 64), p1 = qh bytes 32 n + 16 hh
  * .. + 15 (bit pairs j and 2 + j of those columns;
- * crates/r9v-format/src/ggml.rs:817-850). */
+ * crates/r9v-format/src/ggml.rs:817-850).  IQ3_S (112-byte device blocks:
+ * grid index bytes 0-63, sign words 64-95, side word 96-111): step s is
+ * groups 2 s (hh = 0) and 2 s + 1 (hh = 1) of 32 columns; p0 = their index
+ * bytes 16 s .. + 15 (8 per group), p1 = bytes 64 + 8 s .. + 15 (their sign
+ * words in .x / .y; .z / .w unused). */
 template <int SCHEME>
 __device__ __forceinline__ void m3_load_pay2(const M3WRow &w, uint32_t kt, uint32_t hh, r9vx_u32x4 &p0,
                                              r9vx_u32x4 &p1) {
-    if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
+    if constexpr (SCHEME == R9VX_SCHEME_IQ3_S) {
+        const uint32_t b = w.off + (kt >> 2) * R9VX_IQ3S_DEV_BYTES, s = kt & 3;
+        const uint32_t qs = b + 16 * s, sg = b + 64 + 8 * s;
+        asm volatile("global_load_dwordx4 %0, %2, %4\n\tglobal_load_dwordx4 %1, %3, %4"
+                     : "+v"(p0), "+v"(p1)
+                     : "v"(qs), "v"(sg), "s"(w.base)
+                     : "memory");
+    } else if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
         const uint32_t s = kt & 3, b = w.off + (kt >> 2) * R9VX_Q6K_BODY + 16 * hh;
         const uint32_t ql = b + 64 * (s >> 1) + 32 * (s & 1), qh = b + 128 + 32 * (s >> 1);
         asm volatile("global_load_dwordx4 %0, %2, %4\n\tglobal_load_dwordx4 %1, %3, %4"
@@ -130,10 +146,15 @@ __device__ __forceinline__ void m3_load_pay2(const M3WRow &w, uint32_t kt, uint3
 /* Q4_K: the 16-byte header; IQ4_XS: the block's first 16 bytes (its 8-byte
  * header and 8 payload bytes, inside the 136-byte block), of which .x/.y are
  * used; Q8_0: the f16 d values of the eight 32-weight blocks of 256-weight
- * block blk; Q6_K: the block's 16 int8 scales (its d: m3_load_hdr2). */
+ * block blk; Q6_K: the block's 16 int8 scales (its d: m3_load_hdr2); IQ3_S:
+ * the block's side word (qh bytes of groups 0-3 in .x, 4-7 in .y, the
+ * groups' scale nibbles in .z, d in the low half of .w). */
 template <int SCHEME>
 __device__ __forceinline__ void m3_load_hdr(const M3WRow &w, uint32_t blk, r9vx_u32x4 &hd) {
-    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+    if constexpr (SCHEME == R9VX_SCHEME_IQ3_S) {
+        const uint32_t off = w.off + blk * R9VX_IQ3S_DEV_BYTES + 96;
+        asm volatile("global_load_dwordx4 %0, %1, %2" : "+v"(hd) : "v"(off), "s"(w.base) : "memory");
+    } else if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
         const uint32_t off = w.soff + 16 * blk;
         asm volatile("global_load_dwordx4 %0, %1, %2" : "+v"(hd) : "v"(off), "s"(w.sbase) : "memory");
     } else if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
@@ -192,6 +213,22 @@ __device__ __forceinline__ void m3_init_iq4_lut(uint32_t *lut, uint32_t tid, uin
     }
 }
 
+/* IQ3_S: the signed grid as fp16 pairs.  Word (e << 3) | (h << 2) | s (e the
+ * 9-bit grid index, h a half of the entry, s two sign bits) holds the fp16
+ * 1152 + v0 and 1152 + v1 for values 2h and 2h + 1 of entry e (odd, 1..15),
+ * each negated first when its sign bit is set (crates/r9v-format/src/
+ * iq.rs:698-722): 16 KiB, so that a lookup of two signed weights is one LDS
+ * read. */
+constexpr uint32_t kM3Iq3Words = 512 * 8;
+__device__ __forceinline__ void m3_init_iq3s_lut(uint32_t *lut, uint32_t tid, uint32_t nthreads) {
+    for (uint32_t i = tid; i < kM3Iq3Words; i += nthreads) {
+        const uint32_t gw = kIq3sGrid[i >> 3], h = (i >> 2) & 1u, s = i & 3u;
+        const uint32_t v0 = (gw >> (16 * h)) & 0xFFu, v1 = (gw >> (16 * h + 8)) & 0xFFu;
+        const uint32_t b0 = (s & 1u) ? 128u - v0 : 128u + v0, b1 = (s & 2u) ? 128u - v1 : 128u + v1;
+        lut[i] = (0x6400u | b0) | ((0x6400u | b1) << 16);
+    }
+}
+
 /* Decode unit u (0..7) of a step: payload bytes 2u, 2u + 1 (bytes 4q + 2m,
  * 4q + 2m + 1 of dword q = u / 2, m = u % 2), whose low nibbles are elements
  * 2m, 2m + 1 and high nibbles elements 4 + 2m, 4 + 2m + 1 of group q.  Each
@@ -203,11 +240,26 @@ __device__ __forceinline__ void m3_init_iq4_lut(uint32_t *lut, uint32_t tid, uin
  * quants 4q + 2m, +1 (bytes 2m, 2m + 1 of dword q of the first 16 quants,
  * dw), the high pair the same bytes of the second 16 (dw2).  Q6_K: dw the
  * ql dword, dw2 the qh dword; low pair = columns of the low nibbles (bit
- * pair j = KS % 2), high pair = the high nibbles' (bit pair 2 + j). */
+ * pair j = KS % 2), high pair = the high nibbles' (bit pair 2 + j).  IQ3_S:
+ * kv0 / kv1 are the signed grid pairs (m3_init_iq3s_lut) of the low and high
+ * pair. */
 template <int SCHEME, int KS = 0>
 __device__ __forceinline__ void m3_dec_unit(uint32_t dw, uint32_t dw2, int m, const BScale &sc, uint32_t kv0,
                                             uint32_t kv1, uint32_t &lo2, uint32_t &hi2) {
-    if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
+    if constexpr (SCHEME == R9VX_SCHEME_IQ3_S) {
+        /* w = db (1152 +- v) - 1152 db, fused: db v is exact in f32 (db = d
+         * (1 + 2 s) has at most 16 significant bits, v 4), as is 1152 db */
+        uint32_t a, b;
+        asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(a) : "v"(sc.dl0), "v"(kv0), "v"(sc.c0));
+        asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+            : "+v"(a) : "v"(sc.dl0), "v"(kv0), "v"(sc.c0));
+        asm("v_fma_mixlo_f16 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(b) : "v"(sc.dl0), "v"(kv1), "v"(sc.c0));
+        asm("v_fma_mixhi_f16 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+            : "+v"(b) : "v"(sc.dl0), "v"(kv1), "v"(sc.c0));
+        lo2 = a;
+        hi2 = b;
+        asm volatile("" : "+v"(lo2), "+v"(hi2));
+    } else if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
         /* the 6-bit values q (nibble | bit pair << 4) under a 0x64 byte read
          * as the fp16 1024 + q; w = dl (1024 + q) - 1056 dl, fused: dl q -
          * 32 dl with dl = d sc (exact in f32, as is 1056 dl), rounded once */
@@ -298,7 +350,7 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
                                            const r9vx_u32x4 &pay, const r9vx_u32x4 &pay2, const r9vx_u32x4 &hd,
                                            uint32_t hd2, uint32_t hh, const uint32_t *lut, uint8_t *bdst,
                                            uint32_t bsw, uint32_t bsd = 0u) {
-    constexpr bool kIq4 = SCHEME == R9VX_SCHEME_IQ4_XS;
+    constexpr bool kIq4 = SCHEME == R9VX_SCHEME_IQ4_XS, kIq3 = SCHEME == R9VX_SCHEME_IQ3_S;
     constexpr int P = 4 * NR; /* MFMA pairs */
     const uint32_t h = lane >> 5, r32 = lane & 31, sw = m2_swz(r32);
     const uint8_t *arow = ast + (arow0 + r32) * 128u;
@@ -315,7 +367,54 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
     auto dec_pair = [](int u) { return ((u + 1) * P + 7) / 8 - 1; };
     uint32_t kv[16];
     const uint8_t *lutb = reinterpret_cast<const uint8_t *>(lut);
+    /* IQ3_S: the thread's group 2 KS + hh -- its 8 index bytes (payload
+     * dwords 2 hh, 2 hh + 1), sign word and qh byte */
+    uint32_t i3d0 = 0u, i3d1 = 0u, i3sg = 0u, i3qh = 0u;
+    if constexpr (kIq3) {
+        i3d0 = hh ? pay.z : pay.x;
+        i3d1 = hh ? pay.w : pay.y;
+        i3sg = hh ? pay2.y : pay2.x;
+        i3qh = ((KS < 2 ? hd.x : hd.y) >> (8 * (2 * (KS & 1) + hh))) & 0xFFu;
+    }
+    /* byte address of the grid entry of index i of the group in the signed
+     * table: (9-bit entry << 5) = index byte << 5 (one SDWA shift) | qh bit
+     * i << 13 */
+    auto i3_base = [&](int i) {
+        const uint32_t dw = i < 4 ? i3d0 : i3d1;
+        uint32_t b5;
+        switch (i & 3) {
+        case 0:
+            asm("v_lshlrev_b32_sdwa %0, 5, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+                : "=v"(b5) : "v"(dw));
+            break;
+        case 1:
+            asm("v_lshlrev_b32_sdwa %0, 5, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+                : "=v"(b5) : "v"(dw));
+            break;
+        case 2:
+            asm("v_lshlrev_b32_sdwa %0, 5, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+                : "=v"(b5) : "v"(dw));
+            break;
+        default:
+            asm("v_lshlrev_b32_sdwa %0, 5, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+                : "=v"(b5) : "v"(dw));
+            break;
+        }
+        return r9vx_and_or(i3qh << (13 - i), 0x2000u, b5);
+    };
+    /* sign bits p, p + 1 of the group as the table word's s, times 4 */
+    auto i3_sgn = [&](int p) { return p >= 2 ? (i3sg >> (p - 2)) & 0xCu : (i3sg << 2) & 0xCu; };
     auto read_kv = [&](int u) {
+        if constexpr (kIq3) {
+            /* unit (q, m): values 2m, 2m + 1 of indices 2q (low pair) and
+             * 2q + 1 (high pair), signs 8q + 2m and 8q + 4 + 2m */
+            const int q = u >> 1, m = u & 1;
+            const uint32_t a0 = i3_base(2 * q) | (uint32_t)(16 * m) | i3_sgn(8 * q + 2 * m);
+            const uint32_t a1 = i3_base(2 * q + 1) | (uint32_t)(16 * m) | i3_sgn(8 * q + 4 + 2 * m);
+            kv[2 * u] = *reinterpret_cast<const uint32_t *>(lutb + a0);
+            kv[2 * u + 1] = *reinterpret_cast<const uint32_t *>(lutb + a1);
+            return;
+        }
         uint32_t o0, o1; /* 4 x bytes 2m, 2m + 1 of the dword, one SDWA shift each */
         if (u & 1) {
             asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
@@ -333,7 +432,7 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
     };
 #pragma unroll
     for (int b = 0; b < 16; ++b) kv[b] = 0u;
-    if constexpr (kIq4) {
+    if constexpr (kIq4 || kIq3) {
 #pragma unroll
         for (int u = 0; u < 8; ++u)
             if (P == 0 || dec_pair(u) - kLead < 0) read_kv(u);
@@ -362,7 +461,7 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
     for (int i = 0; i < P; ++i) {
         const int s = i / NR, t = i % NR;
         if (i + kAhead < P) read_frags(i + kAhead);
-        if constexpr (kIq4) {
+        if constexpr (kIq4 || kIq3) {
 #pragma unroll
             for (int u = 0; u < 8; ++u)
                 if (dec_pair(u) - kLead == i) read_kv(u);

@@ -3,7 +3,7 @@
  * crates/r9v-kgen/src/abi/workspace.rs:13-40) and the stage launchers.
  *
  * Workspace regions (each 256-byte aligned), sized for t_bucket tokens:
- *   status  u32[16]  [0] status bits, [3] 128-row tiles, [4] 256-row tiles
+ *   status  u32[16]  [0] status bits, [4] 256-row tiles
  *   counts  u32[E]   pairs per expert
  *   offsets u32[E+1] exclusive scan of counts
  *   sorted  u32[P]   pair index (token*K + slot) at each sorted position
@@ -12,18 +12,18 @@
  *   ccount  u32[E*C] per-expert counts of each 256-pair chunk
  *   cbase   u32[E*C] exclusive scan of ccount over chunks
  *   cbad    u32[C]   1 where the chunk holds an id >= E
- *   tiles   u32x4[...] grouped-GEMM tile schedule (expert, first position,
- *                      rows, 0), 128-row tiles
- *   tiles3  u32x4[...] the same work in 256-row tiles (the r9vx_mma3.h kernels)
- *   h       f32[(P + S*T) * Dff]  SwiGLU rows in sorted order (decode path: pair
- *                                 order), shared rows after
+ *   tiles3  u32x4[...] grouped-GEMM tile schedule (expert, first position,
+ *                      rows, 0), 256-row tiles (the r9vx_mma3.h kernels)
+ *   h       f32[(P + S*T) * Dff]  SwiGLU rows of the decode form (t_bucket <= 8)
+ *                                 in pair order, shared rows after; empty for
+ *                                 the grouped form (h16 only)
  *   o       f32[(P + S*T) * Dm]   expert output rows (decode path: in pair
  *                                 order, no sort); the grouped path stores them in the
  *                                 same region as fp16 [(P + S*T) * Dm] scaled
  *                                 per (row, 64-column block), followed by the
  *                                 f32 scales [(P + S*T) * Dm/64]
  *   hexp    i32[P + S*T]          e of an h16 row's one scale 2^-e (grouped
- *                                 GEMM's LDS-decoded down kernels)
+ *                                 down GEMM past kM3MaxBlk blocks)
  *   h16     fp16[(P + S*T) * Dff] h rows scaled by a power of two, in the down
  *                                 weights' K group order (grouped GEMM)
  *   hbe     i8[(P + S*T) * NB4]   e of each (row, 128-column block)'s h16
@@ -42,13 +42,12 @@
 
 constexpr uint32_t kMoeMaxE = 1024;
 constexpr uint32_t kMoeMaxK = 32;
-constexpr uint32_t kMoeTileM = 128;  /* grouped-GEMM rows per tile */
 constexpr uint32_t kMoeTileM3 = 256; /* rows per tile of the r9vx_mma3.h grouped GEMMs */
 
 struct MoeLayout {
-    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, cbad, tiles, tiles3, h, o, hexp, h16, hbe, x16,
-        xscale, total;
-    uint32_t max_tiles, max_tiles3;
+    uint64_t status, counts, offsets, sorted, inv, rank, ccount, cbase, cbad, tiles3, h, o, hexp, h16, hbe, x16, xscale,
+        total;
+    uint32_t max_tiles3;
 };
 
 /* bytes per row of the hbe exponents: one per 128-column block of h,
@@ -67,7 +66,6 @@ inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint
         off += (bytes + 255) & ~255ull;
         return at;
     };
-    L.max_tiles = (uint32_t)((p + (uint64_t)shared * t_bucket) / kMoeTileM + e + shared + 1);
     L.max_tiles3 = (uint32_t)((p + (uint64_t)shared * t_bucket) / kMoeTileM3 + e + shared + 1);
     L.status = take(64);
     L.counts = take(4ull * e);
@@ -78,9 +76,8 @@ inline MoeLayout r9vx_moe_layout(uint32_t t_bucket, uint32_t e, uint32_t k, uint
     L.ccount = take(4ull * e * nchunk);
     L.cbase = take(4ull * e * nchunk);
     L.cbad = take(4 * nchunk);
-    L.tiles = take(16ull * L.max_tiles + 16);
     L.tiles3 = take(16ull * L.max_tiles3 + 16);
-    L.h = take(4ull * rows * dff);
+    L.h = take(t_bucket <= 8 ? 4ull * rows * dff : 0); /* the decode form (r9vx_moe_decode_form) */
     L.o = take(4ull * rows * dm);
     L.hexp = take(4ull * rows);
     L.h16 = take(2ull * rows * dff);

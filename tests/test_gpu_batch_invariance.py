@@ -140,10 +140,11 @@ def test_matmul_prefill_ragged_n(scheme):
     check_close(want.view(np.float32)[None], ref, "pinned row vs oracle")
 
 
-@pytest.mark.parametrize("scheme,n", [(O.Q8_0, 300), (O.Q8_0, 512), (O.Q6_K, 300), (O.Q6_K, 512), (O.IQ3_S, 300)])
+@pytest.mark.parametrize("scheme,n", [(O.Q8_0, 300), (O.Q8_0, 512), (O.Q6_K, 300), (O.Q6_K, 512), (O.IQ3_S, 300),
+                                      (O.IQ3_S, 512)])
 def test_matmul_prefill_repacked_schemes(scheme, n):
     """Q8_0 / Q6_K / IQ3_S at m_bucket 64: the 128-row LDS-decoded tile, and
-    for Q8_0 / Q6_K at n % 256 == 0 the 256 x 256 register-decoded loop."""
+    at n % 256 == 0 the 256 x 256 register-decoded loop."""
     k = 1024
     wire = synth.quant_weights(scheme, 8600 + scheme + n, n, k)
     w, sc = ffi.repack(dev(wire), scheme, n, k)
@@ -270,8 +271,7 @@ def test_moe_ffn_prefill_buckets_shared_and_q4k_gate_up():
 @pytest.mark.parametrize("t_bucket", [8, 64])
 def test_moe_ffn_buckets_repacked_schemes(gu_s, dn_s, t_bucket):
     """Experts in the split and IQ3_S layouts, decode (t_bucket 8) and grouped
-    (t_bucket 64: the 256-row loop for Q8_0 / Q6_K, the LDS-decoded kernels
-    for IQ3_S)."""
+    (t_bucket 64: the 256-row loop)."""
     e, k, dm, dff, s = 16, 4, 512, 256, 1
     gu_w = synth.quant_weights(gu_s, 9000 + gu_s, (e + s) * 2 * dff, dm)
     dn_w = synth.quant_weights(dn_s, 9001 + dn_s, (e + s) * dm, dff)

@@ -137,6 +137,23 @@ def test_prefill_gemm_parity(m, n, k):
     check_close(y, O.matmul(IQ3_S, w, n, k, x, O.BF16, threads=8), f"m={m} n={n} k={k}")
 
 
+# n % 256 == 0 runs the 256 x 256 loop (two threads per weight row, a
+# thread's half K step one 32-weight group: its 8 grid indices, sign word and
+# the block's side word, decoded through the signed grid table in LDS); these
+# shapes reach its row-chunk plans with ragged row tiles and the bias
+# epilogue.
+@pytest.mark.parametrize("m,n,k", [(9, 256, 512), (700, 2560, 512), (1100, 5376, 512), (2048, 4096, 1024)])
+def test_prefill_gemm_256_tile(m, n, k):
+    w = synth.quant_weights(IQ3_S, 3400 + m, n, k)
+    x = synth.normal_bf16(3500 + m, (m, k))
+    b = synth.normal_f32(3600 + m, (n,))
+    body, _ = ffi.repack(dev(w), IQ3_S, n, k)
+    y = host(ffi.matmul(body, IQ3_S, n, k, bf16_dev(x), bias=dev(b)))
+    rows = np.arange(m) if m * n <= 4_000_000 else np.unique(np.concatenate([np.arange(0, m, 7), [m - 1]]))
+    ref = O.matmul(IQ3_S, w, n, k, np.ascontiguousarray(x[rows]), O.BF16, bias=b, threads=8)
+    check_close(y[rows], ref, f"m={m} n={n} k={k}")
+
+
 def test_prefill_gemm_large_sampled():
     m, n, k = 1024, 4096, 4096
     w = synth.quant_weights(IQ3_S, 5151, n, k)
