@@ -45,11 +45,10 @@ FLAGS = [
 
 
 # Kernels whose main loops issue loads as inline assembly and wait for them by
-# count (r9vx_mma2.h, r9vx_mma3.h): a register the compiler spills between a
+# count (r9vx_mma3.h): a register the compiler spills between a
 # load and its wait would be saved before the data arrives, so these must be
 # spill-free (no scratch at all).
-SPILL_FREE = ("gemm2_kernel", "moe_gu_mfma_kernel", "moe_dn_mfma_kernel", "moe_gu_m3_kernel",
-              "moe_dn_m3_kernel", "gemm3_kernel")
+SPILL_FREE = ("moe_gu_m3_kernel", "moe_dn_m3_kernel", "gemm3_kernel")
 RESOURCES = BUILD / "kernel_resources.txt"
 
 _FIELDS = {"VGPRs": "vgpr", "AGPRs": "agpr", "ScratchSize [bytes/lane]": "scratch", "VGPRs Spill": "vgpr_spill",

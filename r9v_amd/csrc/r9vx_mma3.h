@@ -6,8 +6,8 @@
  * SIMD, one workgroup per CU).  LDS: two A stages and two B tiles (128 KiB).
  *   B (weights): thread t decodes half hh = t & 1 of weight row m3_brow(t)
  *     for the next K step while the MFMAs of the current one run: its 16
- *     payload bytes (groups 4hh .. 4hh+3 of the step, r9vx_mma2.h's K group
- *     order; Q8_0: the 32 quant bytes of one block) become 32 fp16 by the
+ *     payload bytes (groups 4hh .. 4hh+3 of the step in the scheme's K
+ *     order, r9vx_x16.h order_pos; Q8_0 / Q6_K / IQ3_S: two loads) become 32 fp16 by the
  *     exact f32 formula and one rounding, and each 16-byte granule goes to
  *     the other B tile as soon as it is whole.  Every weight is decoded once
  *     per 256 output rows.
@@ -24,19 +24,125 @@
  * then the MFMAs of step k interleaved with the decode and writes of
  * B(k + 1), then a wait for the A(k + 1) copy.
  *
- * Loads are inline assembly waited by count, as in r9vx_mma2.h; their
- * registers are tied in and out of the load ("+v") so that a value crossing
- * the loop back-edge keeps one register, and the kernels that use this loop
- * are checked spill-free at build time.
+ * Loads are inline assembly waited by count (wait_vm); their registers are
+ * tied in and out of the load ("+v") so that a value crossing the loop
+ * back-edge keeps one register, and the kernels that use this loop are
+ * checked spill-free at build time.
  */
 #ifndef R9VX_MMA3_H
 #define R9VX_MMA3_H
 
 #include <stddef.h>
 
-#include "r9vx_mma2.h"
+#include "r9vx_mfma.h"
+#include "r9vx_x16.h"
 
 namespace r9vx {
+
+/* LDS rows are 128 bytes of eight 16-byte groups, group q of row r stored at
+ * slot q ^ m2_swz(r): with 64 four-byte LDS banks a 128-byte row covers half
+ * the banks, so the 16 rows one LDS read cycle serves (8 even, 8 odd) use 8
+ * distinct slots per parity: conflict-free. */
+__host__ __device__ constexpr uint32_t m2_swz(uint32_t row) { return (row >> 1) & 7u; }
+
+/*
+ * The main loop issues its loads as inline assembly and waits for them itself
+ * (wait_vm before each step's barrier).  The compiler's automatic waits cannot
+ * tell a copy into one LDS stage from reads of another and count only the
+ * loads they know of, so with compiler-visible loads every step would stall
+ * on the prefetches of later steps.  touch_pay() marks the point after that
+ * wait from which the registers hold the loaded data.  Each load's
+ * destination is tied in and out ("+v") and nothing is built from it before
+ * the wait, so the register the load writes is the one later read, also for
+ * a value carried across the loop back-edge.
+ */
+__device__ __forceinline__ void touch_pay(r9vx_u32x4 &p) { asm volatile("" : "+v"(p)); }
+
+
+/* The A row (0..255) that instruction i of wave `wave` copies for this lane
+ * (m3_dma_a), and the group of that row the lane copies. */
+__device__ __forceinline__ uint32_t dma_row(uint32_t wave, int i, uint32_t lane) {
+    return (wave * 4 + (uint32_t)i) * 8 + (lane >> 3);
+}
+__device__ __forceinline__ uint32_t dma_group(uint32_t row, uint32_t lane) { return (lane & 7u) ^ m2_swz(row); }
+
+/* Workgroup barrier that the compiler does not move memory operations across.
+ * It first waits for this wave's own LDS reads: the compiler is free to sink
+ * the last MFMAs of a step (and the waits for their operands) below the
+ * barrier, and a read still in flight there would race with the copy that
+ * another wave starts into the same stage once the barrier opens.  The
+ * caller has already waited for the loads that other waves will read. */
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+/* Waits until at most N vector-memory loads of this wave are outstanding
+ * (loads complete in order), leaving LDS and scalar counters alone.  Written
+ * as inline assembly so that it stays ordered with the loads and touch()es
+ * around it. */
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N < 64, "vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+/* Per-step scale terms of one column. */
+struct BScale {
+    float dl0, nml0, dl1, nml1; /* Q4_K: low nibbles (sub-block 2ks), high (2ks+1); IQ4_XS: dl0 */
+    float c0, c1;               /* Q4_K: nml - 1024 dl, the addend for fp16 operands 1024 + q */
+};
+
+template <int SCHEME, int KS>
+__device__ __forceinline__ BScale bscale(const r9vx_u32x4 &hd, uint32_t h, uint32_t hd2 = 0u) {
+    BScale s;
+    if constexpr (SCHEME == R9VX_SCHEME_IQ3_S) {
+        /* hd: the block's side word; group 2 KS + h: db = d (1 + 2 s) with
+         * s its scale nibble (crates/r9v-format/src/iq.rs:698-722) */
+        const float d = r9vx_f16_to_f32((uint16_t)(hd.w & 0xFFFF));
+        s.dl0 = d * (float)(1u + 2u * ((hd.z >> (4 * (2 * KS + h))) & 0xFu));
+        s.c0 = -1152.f * s.dl0; /* exact: db has at most 16 significant bits */
+        s.nml0 = s.dl1 = s.nml1 = s.c1 = 0.f;
+        return s;
+    }
+    if constexpr (SCHEME == R9VX_SCHEME_Q6_K) {
+        /* hd: the block's 16 int8 scales, hd2: its f16 d.  Step KS (span n =
+         * KS / 2, part j = KS % 2), half h: the low nibbles' columns take
+         * scale 8 n + 2 j + h, the high nibbles' 8 n + 4 + 2 j + h (one per
+         * 16 columns, crates/r9v-format/src/ggml.rs:817-850) */
+        const uint32_t lw = (KS >> 1) == 0 ? hd.x : hd.z, hw = (KS >> 1) == 0 ? hd.y : hd.w;
+        const uint32_t sh = 8 * (2 * (KS & 1) + h);
+        const float d = r9vx_f16_to_f32((uint16_t)hd2);
+        s.dl0 = d * (float)(int8_t)(lw >> sh);
+        s.dl1 = d * (float)(int8_t)(hw >> sh);
+        s.c0 = -1056.f * s.dl0; /* exact: dl has at most 18 significant bits, 1056 = 33 * 2^5 */
+        s.c1 = -1056.f * s.dl1;
+        s.nml0 = s.nml1 = 0.f;
+        return s;
+    }
+    if constexpr (SCHEME == R9VX_SCHEME_Q8_0) {
+        /* hd: the f16 d of the eight 32-weight blocks of a 256-weight block;
+         * step KS, half h is block 2 KS + h */
+        const uint32_t dw = KS == 0 ? hd.x : KS == 1 ? hd.y : KS == 2 ? hd.z : hd.w;
+        s.dl0 = r9vx_f16_to_f32((uint16_t)(dw >> (16 * h)));
+        s.c0 = -1152.f * s.dl0; /* exact: 1152 = 9 * 2^7 */
+        s.nml0 = s.dl1 = s.nml1 = s.c1 = 0.f;
+        return s;
+    }
+    const float d = r9vx_f16_to_f32((uint16_t)(hd.x & 0xFFFF));
+    if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
+        const float dmin = r9vx_f16_to_f32((uint16_t)(hd.x >> 16));
+        uint32_t sc[2], mn[2];
+        r9vx_q4k_scale_pair(hd, KS, sc, mn); /* KS constant: no branches */
+        s.dl0 = d * (float)sc[0];
+        s.nml0 = -(dmin * (float)mn[0]);
+        s.dl1 = d * (float)sc[1];
+        s.nml1 = -(dmin * (float)mn[1]);
+        s.c0 = fmaf(-1024.f, s.dl0, s.nml0);
+        s.c1 = fmaf(-1024.f, s.dl1, s.nml1);
+    } else {
+        s.dl0 = d * r9vx_iq4xs_scale(r9vx_u32x2{hd.x, hd.y}, 2 * KS + h);
+        s.nml0 = s.dl1 = s.nml1 = s.c0 = s.c1 = 0.f;
+    }
+    return s;
+}
 
 constexpr uint32_t kM3Rows = 256;          /* output rows per tile */
 constexpr uint32_t kM3Cols = 256;          /* output columns per tile */
@@ -181,7 +287,7 @@ __device__ __forceinline__ void m3_load_hdr2(const M3WRow &w, uint32_t blk, uint
 /* Direct global->LDS copy of one K step of A (256 rows x 64 fp16, group
  * order): instruction i of wave w fills LDS rows 8(4w + i) .. +8 (1 KiB, lane
  * l at row 8(4w+i) + l/8, slot l%8); aoff[i] is the lane's byte offset from
- * the uniform base `abase` at step 0 (r9vx_mma2.h dma_row / dma_group). */
+ * the uniform base `abase` at step 0 (dma_row / dma_group). */
 __device__ __forceinline__ void m3_dma_a(uint32_t stage_lds, const _Float16 *abase, const uint32_t (&aoff)[4],
                                          uint32_t kt, uint32_t wave) {
 #pragma unroll

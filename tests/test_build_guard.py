@@ -10,7 +10,7 @@ import pytest
 
 from r9v_amd import build as B
 
-GUARDED = {"gemm.hip": ["gemm2_kernel", "gemm3_kernel"], "moe_gemm.hip": ["moe_gu_m3_kernel", "moe_dn_m3_kernel"]}
+GUARDED = {"gemm.hip": ["gemm3_kernel"], "moe_gemm.hip": ["moe_gu_m3_kernel", "moe_dn_m3_kernel"]}
 
 
 def _resources(src: str) -> dict:

@@ -251,22 +251,22 @@ def test_gemm_shapes(scheme, m, n, k):
     check_close(got, ref, f"m={m} n={n} k={k}")
 
 
-# Launches with >= 256 output tiles of 256 x 256 take the 8-wave paths: with
-# n % 256 == 0 the loop that decodes each weight tile once into LDS
-# (gemm3_kernel), otherwise the one that decodes the weights straight into
-# MFMA operands (gemm2_kernel); these shapes reach both with ragged M and N
-# tails and the smallest K (one super-block).
+# Launches of many 256 x 256 tiles (gemm3_kernel, every n): ragged M and N
+# tails (the last weight block past n decodes row n - 1 again and stores
+# nothing past n) and the smallest K (one super-block).
 @pytest.mark.parametrize("scheme", [O.Q4_K, O.IQ4_XS])
 @pytest.mark.parametrize("m,n,k", [(1000, 16400, 256), (1024, 16384, 512), (770, 21760, 1280), (300, 65536, 256)])
-def test_gemm_register_decoded_path(scheme, m, n, k):
+def test_gemm_large_ragged_shapes(scheme, m, n, k):
     rows = np.unique(np.concatenate([np.arange(0, m, 37), [0, 255, 256, m - 1]]))
     cols = np.unique(np.concatenate([np.arange(0, n, 29), [0, 31, 32, 255, 256, n - 17, n - 1]]))
     got, ref = _gemm_case(scheme, n, k, m, 7300 + m + k, rows=rows, cols=cols)
     check_close(got, ref, f"m={m} n={n} k={k}")
 
 
-@pytest.mark.parametrize("n", [28000, 28160])
-def test_gemm_register_decoded_epilogues(n):
+# Epilogues and bf16 output with n a multiple of 256, with a ragged last
+# block (n % 8 == 0: 16-byte rows), and with n % 8 != 0 (element stores).
+@pytest.mark.parametrize("n", [28000, 28160, 1001])
+def test_gemm_epilogues_ragged_n(n):
     m, k = 600, 256
     rows = np.arange(0, m, 7)
     cols = np.unique(np.concatenate([np.arange(0, n, 41), [n - 1]]))
