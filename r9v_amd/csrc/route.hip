@@ -122,25 +122,27 @@ __device__ __forceinline__ uint32_t check_row(const RouteArgs &a, uint32_t row, 
  * reference's loop. */
 template <int PER>
 __device__ __forceinline__ float ordered_sum(const float (&v)[PER], uint32_t e, uint32_t lane, float *buf) {
+    /* columns past E hold +0.0, which leaves a sum of values >= 0 bit for
+     * bit unchanged, so the chain has a compile-time length and its LDS reads
+     * can run ahead of the adds (eight quads per unrolled group) */
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const uint32_t c = lane + 64 * i;
-        if (c < e) buf[c] = v[i];
+        buf[c] = c < e ? v[i] : 0.0f;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const r9vx_f32x4 *b4 = reinterpret_cast<const r9vx_f32x4 *>(buf);
     float sum = 0.0f;
-    uint32_t c = 0;
-    for (; c + 16 <= e; c += 16) {
-        const r9vx_f32x4 q0 = b4[c / 4], q1 = b4[c / 4 + 1], q2 = b4[c / 4 + 2], q3 = b4[c / 4 + 3];
-        sum = sum + q0.x; sum = sum + q0.y; sum = sum + q0.z; sum = sum + q0.w;
-        sum = sum + q1.x; sum = sum + q1.y; sum = sum + q1.z; sum = sum + q1.w;
-        sum = sum + q2.x; sum = sum + q2.y; sum = sum + q2.z; sum = sum + q2.w;
-        sum = sum + q3.x; sum = sum + q3.y; sum = sum + q3.z; sum = sum + q3.w;
+#pragma unroll 8
+    for (int q = 0; q < PER * 16; ++q) {
+        const r9vx_f32x4 x = b4[q];
+        sum = sum + x.x;
+        sum = sum + x.y;
+        sum = sum + x.z;
+        sum = sum + x.w;
     }
-    for (; c < e; ++c) sum = sum + buf[c];
     return sum;
 }
 
@@ -221,10 +223,12 @@ __device__ __forceinline__ uint32_t check_loaded(const RouteArgs &a, uint32_t la
  * reference's order: descending score, ties to the smaller column.  Lane
  * j < n returns the j-th (column, score).  The composite key (score order,
  * ~column) makes every candidate distinct, so a wave max picks exactly the
- * reference's next element.  Keys are built once; a taken key or a padding
- * slot is 0, below every valid key (scores are >= 0, whose order keys are
- * >= 0x80000000).  The wave max runs on the score half; the column half is
- * needed only when several lanes tie on it.  n <= E. */
+ * reference's next element.  Each lane sorts its PER keys once (descending,
+ * Batcher's odd-even merge network); a round takes the wave max of the lanes'
+ * first keys and the winning lane drops its first key.  A padding slot or an
+ * exhausted lane holds 0, below every valid key (scores are >= 0, whose
+ * order keys are >= 0x80000000).  The wave max runs on the score half; the
+ * column half is needed only when several lanes tie on it.  n <= E. */
 template <int PER>
 __device__ __forceinline__ void select_top(const float (&v)[PER], uint32_t e, uint32_t n, uint32_t lane,
                                            uint32_t &my_col, float &my_v) {
@@ -234,18 +238,23 @@ __device__ __forceinline__ void select_top(const float (&v)[PER], uint32_t e, ui
         const uint32_t c = lane + 64 * i;
         key[i] = c < e ? ((uint64_t)total_order(v[i]) << 32) | (uint64_t)(0xFFFFFFFFu - c) : 0;
     }
+#pragma unroll
+    for (int p = 1; p < PER; p *= 2)
+#pragma unroll
+        for (int k = p; k >= 1; k /= 2)
+#pragma unroll
+            for (int j = k % p; j + k < PER; j += 2 * k)
+#pragma unroll
+                for (int i = 0; i < k && i + j + k < PER; ++i)
+                    if ((i + j) / (2 * p) == (i + j + k) / (2 * p)) {
+                        const uint64_t x = key[i + j], y = key[i + j + k];
+                        key[i + j] = x > y ? x : y;
+                        key[i + j + k] = x > y ? y : x;
+                    }
     my_col = 0;
     my_v = 0.0f;
     for (uint32_t j = 0; j < n; ++j) {
-        uint64_t m[PER];
-#pragma unroll
-        for (int i = 0; i < PER; ++i) m[i] = key[i];
-#pragma unroll
-        for (int w = 1; w < PER; w *= 2)
-#pragma unroll
-            for (int i = 0; i + w < PER; i += 2 * w) m[i] = m[i + w] > m[i] ? m[i + w] : m[i];
-        const uint64_t best = m[0];
-        const uint32_t bh = (uint32_t)(best >> 32), bl = (uint32_t)best;
+        const uint32_t bh = (uint32_t)(key[0] >> 32), bl = (uint32_t)key[0];
         const uint32_t mh = wave_max_u32(bh);
         const uint64_t tied = __ballot(bh == mh);
         uint32_t ml;
@@ -253,14 +262,13 @@ __device__ __forceinline__ void select_top(const float (&v)[PER], uint32_t e, ui
             ml = (uint32_t)__builtin_amdgcn_readlane((int)bl, (int)__builtin_ctzll(tied));
         else
             ml = wave_max_u32(bh == mh ? bl : 0u);
-        const uint32_t col = 0xFFFFFFFFu - ml;
-        if ((col & 63u) == lane) {
+        if (bh == mh && bl == ml) { /* the winning lane */
 #pragma unroll
-            for (int i = 0; i < PER; ++i)
-                if ((uint32_t)i == (col >> 6)) key[i] = 0;
+            for (int i = 0; i + 1 < PER; ++i) key[i] = key[i + 1];
+            key[PER - 1] = 0;
         }
         if (lane == j) {
-            my_col = col;
+            my_col = 0xFFFFFFFFu - ml;
             my_v = __builtin_bit_cast(float, (mh & 0x80000000u) ? (mh & 0x7FFFFFFFu) : ~mh);
         }
     }
@@ -340,8 +348,8 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
     }
 }
 
-/* Small-T form: one workgroup of two waves per row.  Softmax: both waves
- * compute the row's exp(s - max); wave 0 takes the ordered sum while wave 1
+/* Small-T form: one workgroup of four waves per row.  Softmax: waves 0 and
+ * 1 compute the row's exp(s - max); wave 0 takes the ordered sum while wave 1
  * selects the K + 1 largest numerators (the quotients p = e / sum have the
  * same order unless two of them round to the same p), then wave 1 divides
  * its K + 1 selections by the sum: if the K + 1 quotients strictly
@@ -349,10 +357,10 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
  * stand; otherwise (equal or one-ulp-apart numerators whose quotients round
  * equal) wave 1 divides every value and selects on the quotients.  Sigmoid
  * scores need no sum: wave 1 routes alone.  The batch-level refusal (no row
- * is written if any row is bad): every workgroup checks every row, its two
- * waves taking alternate rows with all their loads in flight at once, so the
- * rows' workgroups run on separate CUs without talking to each other;
- * workgroup 0 writes the status word. */
+ * is written if any row is bad): every workgroup checks every row, on its
+ * waves 2 and 3 (alternate rows, all their loads in flight at once) while
+ * waves 0 and 1 route, so the rows' workgroups run on separate CUs without
+ * talking to each other; workgroup 0 writes the status word. */
 constexpr uint32_t kRouteSmallT = 8;
 
 template <int PER>
@@ -400,7 +408,7 @@ struct CheckRows {
 };
 
 template <int PER>
-__global__ __launch_bounds__(128) void route_small_kernel(RouteArgs a) {
+__global__ __launch_bounds__(256) void route_small_kernel(RouteArgs a) {
     __shared__ uint32_t bad_all;
     __shared__ uint64_t etab[R9VX_EXP2F_N];
     __shared__ __attribute__((aligned(16))) float sbuf[PER * 64];
@@ -409,12 +417,18 @@ __global__ __launch_bounds__(128) void route_small_kernel(RouteArgs a) {
     r9vx_exp2_fill(etab, threadIdx.x, blockDim.x);
     if (threadIdx.x == 0) bad_all = 0;
     float sc[PER], lg[PER], bs[PER];
-    load_row<PER>(a, row, lane, sc, lg, bs);
     CheckRows<PER> cr;
-    cr.load(a, role, lane);
+    if (role < 2)
+        load_row<PER>(a, row, lane, sc, lg, bs);
+    else
+        cr.load(a, role - 2, lane);
     __syncthreads();
-    const uint32_t bad = cr.check(a, role, lane, etab);
-    if (bad && lane == 0) atomicOr(&bad_all, bad);
+    if (role >= 2) { /* the checking waves */
+        const uint32_t bad = cr.check(a, role - 2, lane, etab);
+        if (bad && lane == 0) atomicOr(&bad_all, bad);
+        __syncthreads();
+        return;
+    }
     const bool softmax = a.scoring == R9VX_SCORING_SOFTMAX;
     uint32_t id = 0, col = 0;
     float w = 0.0f, ev = 0.0f;
@@ -636,7 +650,7 @@ int r9vx_launch_route_hidden(const r9vx_route_hidden_problem &p, hipStream_t str
 template <int PER>
 static int launch_route_per(const RouteArgs &a, hipStream_t stream) {
     if (a.t <= kRouteSmallT) {
-        hipLaunchKernelGGL((route_small_kernel<PER>), dim3(a.t), dim3(128), 0, stream, a);
+        hipLaunchKernelGGL((route_small_kernel<PER>), dim3(a.t), dim3(256), 0, stream, a);
         return (int)hipGetLastError();
     }
     hipLaunchKernelGGL(clear_status_kernel, dim3(1), dim3(1), 0, stream, a.status);
