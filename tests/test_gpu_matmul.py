@@ -293,6 +293,28 @@ def test_gemm_row_chunk_plans(scheme, m, n):
     check_close(got, ref, f"m={m} n={n}")
 
 
+def test_gemm_rows_past_32_bit_activation_offsets():
+    """m * k >= 2^31 (x16 past 4 GiB): the rows go in several launches (at
+    most 149,792 rows at k = 14336); rows on both sides of the cut meet the
+    oracle and equal, bit for bit, the same rows launched alone."""
+    m, n, k = 150000, 256, 14336
+    w_h = synth.quant_weights(O.Q4_K, 7701, n, k)
+    w = dev(w_h)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7702)
+    x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+    y = ffi.matmul(w, O.Q4_K, n, k, x)
+    rows = [0, 149791, 149792, 149999]
+    got = host(y[rows])
+    del y
+    alone = host(ffi.matmul(w, O.Q4_K, n, k, x[rows].contiguous(), m_bucket=16))
+    assert np.array_equal(got.view(np.uint32), alone.view(np.uint32))
+    xr = host(x[rows].view(torch.int16)).view(np.uint16)
+    del x
+    torch.cuda.empty_cache()
+    check_close(got, O.matmul(O.Q4_K, w_h, n, k, xr, O.BF16, threads=8), "rows around the launch cut")
+
+
 def test_gemm_row_chunk_plans_keep_row_bits():
     """The same rows under two chunk plans of one static (m = 1100 and 2600 at
     m_bucket 4096, n = 14336: one round of uniform chunks, three rounds of two
