@@ -91,8 +91,8 @@ __device__ __forceinline__ float dpp_f32(float x) {
 
 /* The 4-element chunk (column / 4 within a 128-column block) that holds
  * elements i .. i + 3 (i = 0 or 4) of the group stored at position c (< 128)
- * of the block in an h16 row of order `order` (h_pos's orders, chosen at
- * run time). */
+ * of the block in an h16 row of order `order` (r9vx_x16.h order_pos's orders,
+ * chosen at run time). */
 __device__ __forceinline__ uint32_t h_chunk(uint32_t order, uint32_t c, uint32_t i) {
     if (order == R9VX_SCHEME_Q4_K) return order_pos<R9VX_SCHEME_Q4_K>(c, i) / 4;
     if (order == R9VX_SCHEME_IQ4_XS) return order_pos<R9VX_SCHEME_IQ4_XS>(c, i) / 4;

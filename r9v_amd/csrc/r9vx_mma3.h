@@ -456,7 +456,7 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
                                            const r9vx_u32x4 &pay, const r9vx_u32x4 &pay2, const r9vx_u32x4 &hd,
                                            uint32_t hd2, uint32_t hh, const uint32_t *lut, uint8_t *bdst,
                                            uint32_t bsw, uint32_t bsd = 0u) {
-    constexpr bool kIq4 = SCHEME == R9VX_SCHEME_IQ4_XS, kIq3 = SCHEME == R9VX_SCHEME_IQ3_S;
+    constexpr bool kIq3 = SCHEME == R9VX_SCHEME_IQ3_S;
     constexpr int P = 4 * NR; /* MFMA pairs */
     const uint32_t h = lane >> 5, r32 = lane & 31, sw = m2_swz(r32);
     const uint8_t *arow = ast + (arow0 + r32) * 128u;
@@ -538,7 +538,7 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
     };
 #pragma unroll
     for (int b = 0; b < 16; ++b) kv[b] = 0u;
-    if constexpr (kIq4 || kIq3) {
+    if constexpr (m3_table(SCHEME)) {
 #pragma unroll
         for (int u = 0; u < 8; ++u)
             if (P == 0 || dec_pair(u) - kLead < 0) read_kv(u);
@@ -567,7 +567,7 @@ __device__ __forceinline__ void m3_compute(const uint8_t *ast, const uint8_t *bs
     for (int i = 0; i < P; ++i) {
         const int s = i / NR, t = i % NR;
         if (i + kAhead < P) read_frags(i + kAhead);
-        if constexpr (kIq4 || kIq3) {
+        if constexpr (m3_table(SCHEME)) {
 #pragma unroll
             for (int u = 0; u < 8; ++u)
                 if (dec_pair(u) - kLead == i) read_kv(u);
