@@ -1013,7 +1013,9 @@ __global__ __launch_bounds__(256) void r9vx_moe_combine_kernel(MoeCombineArgs a)
 
 /* The same combine over the grouped path's fp16 rows: row value = o16 *
  * oscale[row, d / 64] (exact: the scale is a power of two), summed in the
- * same order. */
+ * same order.  The o rows are read once and y is written once, both with
+ * non-temporal accesses so the stream does not evict what the GEMMs keep in
+ * the caches (configs[4]: 79 -> 69 us). */
 __global__ __launch_bounds__(256) void r9vx_moe_combine16_kernel(MoeCombineArgs a) {
     __shared__ uint32_t spos[kMoeMaxK], opos[kMoeMaxK];
     __shared__ float sw[kMoeMaxK], ow[kMoeMaxK];
@@ -1059,7 +1061,7 @@ __global__ __launch_bounds__(256) void r9vx_moe_combine16_kernel(MoeCombineArgs 
         for (uint32_t j = 0; j < 8; ++j)
             if (jb + j < kk) {
                 const uint64_t row = opos[jb + j];
-                rows[j] = *reinterpret_cast<const h4 *>(o16 + row * a.dm + d0);
+                rows[j] = __builtin_nontemporal_load(reinterpret_cast<const h4 *>(o16 + row * a.dm + d0));
                 scs[j] = oscale[row * nblk + blk];
             }
 #pragma unroll
@@ -1082,7 +1084,7 @@ __global__ __launch_bounds__(256) void r9vx_moe_combine16_kernel(MoeCombineArgs 
         acc.z = acc.z + (float)v.z * sc;
         acc.w = acc.w + (float)v.w * sc;
     }
-    *reinterpret_cast<r9vx_f32x4 *>(a.y + (uint64_t)t * a.dm + d0) = acc;
+    __builtin_nontemporal_store(acc, reinterpret_cast<r9vx_f32x4 *>(a.y + (uint64_t)t * a.dm + d0));
 }
 
 /* ---------------------------------------------------------------- host side */
