@@ -158,7 +158,7 @@ __global__ __launch_bounds__(XS ? 256 : waves_for(M) * 64) void gemv_kernel(Gemv
                 else if constexpr (split_scheme(SCHEME))
                     load_chunk_split<SCHEME>(wrow, a.ws + (uint64_t)rr * a.ws_row, cis[s], qs[r][s], hd[r][s]);
                 else
-                    load_chunk<SCHEME>(wrow, cis[s], qs[r][s], hd[r][s]);
+                    load_chunk<SCHEME, true>(wrow, cis[s], qs[r][s], hd[r][s]); /* read once: non-temporal */
             }
         }
         /* 2. the codebook table is built (and the activation copy stored)

@@ -167,22 +167,28 @@ struct Hdr {
     uint32_t e;
 };
 
-/* The payload and the header of a block share cache lines, so both go
- * through the caches: a non-temporal payload load beside a cached header load
- * of the same line measured 4.0 TB/s on the configs[3] expert set against
- * 5.2 TB/s for cached loads (a plain 16-byte stream: 5.6). */
-template <int SCHEME>
+/* The payload and the header of a block share cache lines, so both take the
+ * same path: a non-temporal payload load beside a cached header load of the
+ * same line measured 4.0 TB/s on the configs[3] expert set against 5.2 TB/s
+ * for cached loads (a plain 16-byte stream: 5.6).  NT: both non-temporal --
+ * the one-shot GEMV's form (configs[1] M = 1: 4.14 -> 3.55 us, M = 5: 5.26 ->
+ * 4.75, configs[0] 5.24 -> 4.89, same box); the streaming form and the MoE
+ * decode GEMVs keep cached loads (streaming Q4_K 32768 x 4096: 16.0 -> 17.5
+ * us with NT; configs[3] unchanged). */
+template <int SCHEME, bool NT = false>
 __device__ __forceinline__ void load_chunk(const uint8_t *row, uint32_t ci, r9vx_u32x4 &qs, Hdr &h) {
     uint32_t b = ci >> 3, c = ci & 7;
     if constexpr (SCHEME == R9VX_SCHEME_Q4_K) {
         const uint8_t *blk = row + (uint64_t)b * R9VX_Q4K_BYTES;
-        h.v = r9vx_ld128(blk);
-        qs = r9vx_ld128(blk + 16 + 16 * c);
+        h.v = NT ? r9vx_ld128_nt(blk) : r9vx_ld128(blk);
+        qs = NT ? r9vx_ld128_nt(blk + 16 + 16 * c) : r9vx_ld128(blk + 16 + 16 * c);
     } else {
         const uint8_t *blk = row + (uint64_t)b * R9VX_IQ4XS_BYTES;
-        r9vx_u32x2 hh = *reinterpret_cast<const r9vx_u32x2 *>(blk);
+        typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
+        const u32x2a4 hh = NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x2a4 *>(blk))
+                              : *reinterpret_cast<const u32x2a4 *>(blk);
         h.v = r9vx_u32x4{hh.x, hh.y, 0u, 0u};
-        qs = r9vx_ld128(blk + 8 + 16 * c);
+        qs = NT ? r9vx_ld128_nt(blk + 8 + 16 * c) : r9vx_ld128(blk + 8 + 16 * c);
     }
 }
 
