@@ -166,8 +166,7 @@ __host__ __device__ inline uint32_t r9vx_row_scales(uint32_t scheme, uint32_t k)
 }
 
 /* Weight schemes the 256 x 256 loop of r9vx_mma3.h decodes: all five (the
- * grouped MoE GEMMs take it for every scheme; the dense GEMM for N % 256 ==
- * 0). */
+ * grouped MoE GEMMs and the dense GEMM take it for every scheme and N). */
 __host__ __device__ inline bool r9vx_m3_scheme(uint32_t scheme) {
     return scheme == R9VX_SCHEME_Q4_K || scheme == R9VX_SCHEME_IQ4_XS || scheme == R9VX_SCHEME_Q8_0 ||
            scheme == R9VX_SCHEME_Q6_K || scheme == R9VX_SCHEME_IQ3_S;
