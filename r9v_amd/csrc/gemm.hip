@@ -69,8 +69,10 @@ __global__ __launch_bounds__(256) void x_to_f16_kernel(const uint16_t *__restric
  * every wave reads its B fragments from there, and the accumulators are the
  * transposed tile, so lane l holds output row 128 rh + 32 t + (l & 31) and
  * columns 64 cq + 32 j + 8 (r >> 2) + 4 (l >> 5) + (r & 3) of acc[t][j][r].
- * A workgroup takes the chunk of rows plan_chunks gave its index.  The
- * launcher takes it for n % 256 == 0 and m k < 2^31 (the A copy offsets are
+ * A workgroup takes the chunk of rows plan_chunks gave its index.  Every n:
+ * in a ragged last weight block the threads of rows past n decode row n - 1
+ * again and the epilogue stores no column past n.  The launcher runs a
+ * bucket as row launches of m k < 2^31 each (the A copy offsets are
  * 32-bit). */
 template <int SCHEME>
 __global__ __launch_bounds__(512, 1) void gemm3_kernel(GemmArgs a) {

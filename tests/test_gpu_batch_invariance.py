@@ -143,8 +143,8 @@ def test_matmul_prefill_ragged_n(scheme):
 @pytest.mark.parametrize("scheme,n", [(O.Q8_0, 300), (O.Q8_0, 512), (O.Q6_K, 300), (O.Q6_K, 512), (O.IQ3_S, 300),
                                       (O.IQ3_S, 512)])
 def test_matmul_prefill_repacked_schemes(scheme, n):
-    """Q8_0 / Q6_K / IQ3_S at m_bucket 64: the 128-row LDS-decoded tile, and
-    at n % 256 == 0 the 256 x 256 register-decoded loop."""
+    """Q8_0 / Q6_K / IQ3_S at m_bucket 64 on the 256 x 256 loop, with a
+    ragged last weight block (n = 300) and whole blocks (n = 512)."""
     k = 1024
     wire = synth.quant_weights(scheme, 8600 + scheme + n, n, k)
     w, sc = ffi.repack(dev(wire), scheme, n, k)

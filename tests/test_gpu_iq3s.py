@@ -137,7 +137,7 @@ def test_prefill_gemm_parity(m, n, k):
     check_close(y, O.matmul(IQ3_S, w, n, k, x, O.BF16, threads=8), f"m={m} n={n} k={k}")
 
 
-# n % 256 == 0 runs the 256 x 256 loop (two threads per weight row, a
+# m > 8 runs the 256 x 256 loop for every n (two threads per weight row, a
 # thread's half K step one 32-weight group: its 8 grid indices, sign word and
 # the block's side word, decoded through the signed grid table in LDS); these
 # shapes reach its row-chunk plans with ragged row tiles and the bias

@@ -163,8 +163,8 @@ PREFILL = [(9, 320, 2048), (40, 1000, 4096), (300, 512, 2048), (129, 2304, 1024)
 @pytest.mark.parametrize("scheme", SCHEMES)
 @pytest.mark.parametrize("m,n,k", PREFILL)
 def test_prefill_gemm_split_layout_parity(scheme, m, n, k):
-    """m > 8: the MFMA GEMM on the split layout (n % 256 != 0: the
-    LDS-decoded 128 x 256 tile; n % 256 == 0: the 256 x 256 loop)."""
+    """m > 8: the MFMA GEMM on the split layout (the 256 x 256 loop; a
+    ragged n repeats row n - 1 in its last weight block)."""
     w = synth.quant_weights(scheme, 3000 + m + n, n, k)
     x = synth.normal_bf16(4000 + m + k, (m, k))
     body, scales = ffi.repack(dev(w), scheme, n, k)
@@ -172,7 +172,7 @@ def test_prefill_gemm_split_layout_parity(scheme, m, n, k):
     check_close(y, O.matmul(scheme, w, n, k, x, O.BF16, threads=8), f"scheme={scheme} m={m} n={n} k={k}")
 
 
-# Q8_0 / Q6_K with n % 256 == 0 run the 256 x 256 loop that decodes each
+# Q8_0 / Q6_K run the 256 x 256 loop (every n) that decodes each
 # weight tile once into LDS (two threads per weight row; a thread's half K
 # step is one Q8_0 block, or 16 Q6_K ql bytes and their 16 qh bytes, loaded
 # two steps ahead); these shapes reach its row-chunk plans (one block,
