@@ -326,9 +326,8 @@ def c2_extra(torch, ffi, synth, gsynth, steps, cpu_s, steps_only=False):
 def schemes_extra(torch, ffi, synth, gsynth, steps):
     """The other weight types at the headline shapes (measurement only; all
     three run the headline kernels' 256-row loop): the configs[2] dense GEMM
-    and the configs[4] moe_ffn
-    step with Q8_0, Q6_K and IQ3_S weights in their device layouts (split
-    body + f16 d array; 112-byte IQ3_S blocks)."""
+    and the configs[4] moe_ffn step with Q8_0, Q6_K and IQ3_S weights in
+    their device layouts (split body + f16 d array; 112-byte IQ3_S blocks)."""
     out = {"gemm_c2_shape": {}, "moe_ffn_c4_shape": {}}
     m, n, k = 2048, 14336, 4096
     x_host = synth.normal_bf16(synth.seed_for("c2", "x"), (m, k))
